@@ -1,0 +1,386 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 geometry kernels on the reference's headline workloads.
+
+Headline (``value``): wall time per batch of farthest point sampling + radius graph on
+configuration C2 — 16 clouds x 4096 points on unit spheres with 0.01 jitter, FPS to 1024 per
+cloud, radius graph r = 0.1 with at most 32 neighbours over all 65,536 points — including each
+op's single output-size host sync (as the reference's examples/registration/diagnose_perf.py
+times ops: perf_counter around synchronize).
+
+Roofline (``roofline``): segment-reduce forward sum on configuration C3 (E = 4,194,304 edges
+sorted by destination over S = 262,144 Zipf(1.2) segments capped at 64, C = 128 fp32), kernel
+time from HIP events on the launch stream, algorithmic bytes E*C*4 + S*C*4 + (S+1)*4.
+
+CPU baseline (``cpu_baseline``): the reference's CPU path (oracle/ref_cpu_path.py, same torch op
+sequences) on the same C2 batch, on this host's cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
+One JSON line goes to stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+METRIC = "ms/batch FPS+radius_graph (B=16,N=4096); segment_reduce GB/s vs HBM peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Synthetic configurations (deterministic, CPU generators)
+# ═══════════════════════════════════════════════════════════════════
+
+
+def make_c1():
+    """C1: 2048 points uniform in [-1, 1]^3, FPS 512 from index 0, radius r = 0.2 / K = 32 over
+    the 512 centres, C = 32 N(0, 1) features summed over that graph."""
+    g = torch.Generator().manual_seed(0)
+    pos = torch.rand(2048, 3, generator=g) * 2 - 1
+    feat = torch.randn(512, 32, generator=g)
+    return dict(pos=pos, M=512, r=0.2, K=32, feat=feat)
+
+
+def make_c2(B: int = 16, N: int = 4096):
+    """C2: B clouds of N points on the unit sphere + N(0, 0.01) jitter; FPS 1024 per cloud;
+    radius r = 0.1, K = 32; KNN k = 16 from the centres."""
+    g = torch.Generator().manual_seed(0)
+    clouds = []
+    for _ in range(B):
+        d = torch.randn(N, 3, generator=g)
+        clouds.append(d / d.norm(dim=1, keepdim=True) + 0.01 * torch.randn(N, 3, generator=g))
+    pos = torch.cat(clouds)
+    batch = torch.arange(B).repeat_interleave(N)
+    ptr = torch.arange(B + 1, dtype=torch.int64) * N
+    return dict(pos=pos, batch=batch, ptr=ptr, B=B, N=N, M=1024, r=0.1, K=32, k=16)
+
+
+def make_c3_offsets(S: int = 262144, E: int = 4194304):
+    """C3 segment sizes: min(zipf(1.2), 64) drawn with default_rng(0), accumulated until the sum
+    reaches E (the last one truncated, the rest empty), then permuted with default_rng(1)."""
+    rng = np.random.default_rng(0)
+    raw = np.minimum(rng.zipf(1.2, S), 64).astype(np.int64)
+    cs = np.cumsum(raw)
+    cut = int(np.searchsorted(cs, E))
+    sizes = raw.copy()
+    sizes[cut] = E - (cs[cut - 1] if cut > 0 else 0)
+    sizes[cut + 1:] = 0
+    sizes = sizes[np.random.default_rng(1).permutation(S)]
+    off = np.zeros(S + 1, dtype=np.int64)
+    off[1:] = np.cumsum(sizes)
+    assert off[-1] == E
+    return off
+
+
+def make_c4(B: int = 32, n: int = 2048):
+    """C4: B random superquadrics (exponents U(0.3, 3), random SO(3) rotation), n samples each."""
+    g = torch.Generator().manual_seed(0)
+
+    def spow(v, e):
+        return torch.sign(v) * v.abs().pow(e)
+
+    shapes = []
+    for _ in range(B):
+        e1, e2 = (torch.rand(2, generator=g) * 2.7 + 0.3).tolist()
+        eta = (torch.rand(n, generator=g) - 0.5) * math.pi
+        om = (torch.rand(n, generator=g) * 2 - 1) * math.pi
+        ce = spow(torch.cos(eta), e1)
+        p = torch.stack([ce * spow(torch.cos(om), e2), ce * spow(torch.sin(om), e2),
+                         spow(torch.sin(eta), e1)], dim=1)
+        q = torch.randn(4, generator=g)
+        w, x, y, z = (q / q.norm()).tolist()
+        R = torch.tensor([[1 - 2 * (y * y + z * z), 2 * (x * y - z * w), 2 * (x * z + y * w)],
+                          [2 * (x * y + z * w), 1 - 2 * (x * x + z * z), 2 * (y * z - x * w)],
+                          [2 * (x * z - y * w), 2 * (y * z + x * w), 1 - 2 * (x * x + y * y)]])
+        shapes.append(p @ R.T)
+    pos = torch.cat(shapes).float()
+    ptr = torch.arange(B + 1, dtype=torch.int64) * n
+    return dict(pos=pos, ptr=ptr, B=B, n=n, levels=(512, 128), radii=(0.2, 0.4), K=64,
+                channels=(64, 128))
+
+
+def make_c5():
+    """C5: one 64-ring spinning-lidar frame, 131,072 points: elevations linspace(-24.8, 2) deg,
+    2048 azimuths, range U(1, 80) m + N(0, 0.02), rays clipped to the ground plane z = -1.7."""
+    g = torch.Generator().manual_seed(0)
+    el = torch.deg2rad(torch.linspace(-24.8, 2.0, 64, dtype=torch.float64))
+    az = torch.arange(2048, dtype=torch.float64) * (2 * math.pi / 2048)
+    E_, A_ = torch.meshgrid(el, az, indexing="ij")
+    rng = torch.rand(64, 2048, generator=g, dtype=torch.float64) * 79 + 1
+    rng = rng + 0.02 * torch.randn(64, 2048, generator=g, dtype=torch.float64)
+    down = E_ < 0
+    t_hit = torch.where(down, 1.7 / torch.sin(-E_).clamp(min=1e-12), torch.full_like(E_, math.inf))
+    rng = torch.minimum(rng, t_hit)
+    pts = torch.stack([rng * torch.cos(E_) * torch.cos(A_), rng * torch.cos(E_) * torch.sin(A_),
+                       rng * torch.sin(E_)], dim=-1).reshape(-1, 3).float()
+    return dict(pos=pts, M=16384, r=0.5, K=64, k=8, C=32)
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Timing helpers
+# ═══════════════════════════════════════════════════════════════════
+
+
+def wall_ms(fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1000.0 / steps
+
+
+def event_ms(fn, iters: int, warmup: int) -> float:
+    """Average GPU time per call between HIP events recorded on the current stream (the stream
+    every op of this library launches on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--all", action="store_true", help="also time C1, C4, C5 and KNN legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run one leg: c2 | c3 | c3bf16 | c3bwd")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py measures one GPU: this build has no multi-GPU path (each op's work is a "
+            "single-GPU kernel; see DESIGN.md for how it would shard). Run with --gpus 1.")
+        return 2
+    if not torch.cuda.is_available():
+        log("bench.py needs a GPU")
+        return 2
+
+    import geoembodied  # noqa: F401  (registers the drop-in module paths)
+    from geoembodied.functional.fps import farthest_point_sampling
+    from geoembodied.functional.knn import knn
+    from geoembodied.functional.radius_graph import radius_graph
+    from geoembodied.functional.segment_reduce import segment_reduce, sort_and_build_csr
+    from gdl_amd import _native
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    result: dict = {}
+    legs: dict = {}
+
+    # ---------------------------------------------------------------- C2 headline ---
+    c2 = make_c2()
+    pos = c2["pos"].to(dev)
+    batch = c2["batch"].to(dev)
+    ptr = c2["ptr"].to(dev)
+
+    def step():
+        idx = farthest_point_sampling(pos, c2["M"], ptr=ptr)
+        row, col = radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                num_batch_elements=c2["B"])
+        return idx, row, col
+
+    ms_step = None
+    if args.only in (None, "c2"):
+        log("C2: FPS + radius_graph ...")
+        ms_step = wall_ms(step, args.steps, args.warmup)
+        idx, row, col = step()
+        legs["c2_fps_ms"] = wall_ms(lambda: farthest_point_sampling(pos, c2["M"], ptr=ptr),
+                                    args.steps, 3)
+        legs["c2_radius_ms"] = wall_ms(lambda: radius_graph(pos, c2["r"], max_num_neighbors=c2["K"],
+                                                            batch=batch, num_batch_elements=c2["B"]),
+                                       args.steps, 3)
+        legs["c2_edges"] = int(row.numel())
+        legs["c2_points_per_s"] = pos.shape[0] / (ms_step / 1e3)
+        legs["c2_edges_per_s"] = row.numel() / (legs["c2_radius_ms"] / 1e3)
+        legs["c2_fps_point_updates_per_s"] = c2["B"] * c2["N"] * c2["M"] / (legs["c2_fps_ms"] / 1e3)
+        cent = pos[idx]
+        ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
+        legs["c2_knn_ms"] = wall_ms(lambda: knn(cent, pos, ptr_q, ptr, c2["k"]), args.steps, 3)
+        legs["c2_radius_centres_ms"] = wall_ms(
+            lambda: radius_graph(cent, c2["r"], max_num_neighbors=c2["K"],
+                                 num_batch_elements=c2["B"]), args.steps, 3)
+        log(f"  step {ms_step:.3f} ms  fps {legs['c2_fps_ms']:.3f}  radius {legs['c2_radius_ms']:.3f}"
+            f"  knn {legs['c2_knn_ms']:.3f}  edges {legs['c2_edges']}")
+
+    # ---------------------------------------------------------------- C3 roofline ---
+    roof = None
+    if args.only in (None, "c3", "c3bf16", "c3bwd"):
+        log("C3: segment reduce ...")
+        off = make_c3_offsets()
+        S, E, C = off.shape[0] - 1, int(off[-1]), 128
+        ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
+        ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
+        col_sorted = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32),
+                                             (ne - ns).long())
+        perm = torch.arange(E, device=dev, dtype=torch.int32)
+        gen = torch.Generator(device=dev).manual_seed(0)
+        msg = torch.randn(E, C, device=dev, generator=gen)
+        bytes_fwd = E * C * 4 + S * C * 4 + (S + 1) * 4
+        iters = 50
+        if args.only in (None, "c3"):
+            ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
+            gbs = bytes_fwd / (ms * 1e-3) / 1e9
+            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": "seg_fwd_kernel<float,16,SUM>", "ms_per_launch": round(ms, 4),
+                    "algorithmic_bytes": bytes_fwd}
+            log(f"  fwd sum fp32: {ms:.4f} ms  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+            for red in ("mean", "max"):
+                extra = S * C * 4 if red == "max" else 0
+                msr = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S, reduce=red),
+                               iters, 5)
+                legs[f"c3_{red}_fp32_gbs"] = round((bytes_fwd + extra) / (msr * 1e-3) / 1e9, 1)
+        if args.only in (None, "c3bf16"):
+            mb = msg.bfloat16()
+            bytes_b = E * C * 2 + S * C * 2 + (S + 1) * 4
+            msb = event_ms(lambda: segment_reduce(mb, col_sorted, perm, ns, ne, S), iters, 5)
+            legs["c3_sum_bf16_ms"] = round(msb, 4)
+            legs["c3_sum_bf16_gbs"] = round(bytes_b / (msb * 1e-3) / 1e9, 1)
+            log(f"  fwd sum bf16: {msb:.4f} ms  {legs['c3_sum_bf16_gbs']} GB/s")
+            del mb
+        if args.only in (None, "c3bwd"):
+            from gdl_amd.csrc import segment_reduce_backward_hip
+            grad = torch.randn(S, C, device=dev, generator=gen)
+            bytes_bwd = S * C * 4 + E * C * 4 + (S + 1) * 4
+            msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, "sum"),
+                           iters, 5)
+            legs["c3_bwd_sum_fp32_gbs"] = round(bytes_bwd / (msb * 1e-3) / 1e9, 1)
+            log(f"  bwd sum fp32: {msb:.4f} ms  {legs['c3_bwd_sum_fp32_gbs']} GB/s")
+        col64 = col_sorted.long()
+        legs["c3_csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col64, S), 10, 2), 4)
+        del msg
+
+    # ---------------------------------------------------------------- extra legs ---
+    if args.all:
+        c1 = make_c1()
+        p1 = c1["pos"].to(dev)
+
+        def c1_step():
+            i = farthest_point_sampling(p1, c1["M"])
+            cen = p1[i]
+            row, col = radius_graph(cen, c1["r"], max_num_neighbors=c1["K"])
+            cs, pm, a, b = sort_and_build_csr(col, c1["M"])
+            return segment_reduce(c1["feat"].to(dev)[row], cs, pm, a, b, c1["M"])
+        legs["c1_ms"] = wall_ms(c1_step, 20, 3)
+        c4 = make_c4()
+        p4, ptr4 = c4["pos"].to(dev), c4["ptr"].to(dev)
+
+        def c4_step():
+            i1 = farthest_point_sampling(p4, 512, ptr=ptr4)
+            q1 = p4[i1]
+            ptr1 = torch.arange(c4["B"] + 1, device=dev, dtype=torch.int64) * 512
+            i2 = farthest_point_sampling(q1, 128, ptr=ptr1)
+            q2 = q1[i2]
+            outs = []
+            for pts, r, n, C in ((q1, 0.2, 512, 64), (q2, 0.4, 128, 128)):
+                row, col = radius_graph(pts, r, max_num_neighbors=64, num_batch_elements=c4["B"])
+                cs, pm, a, b = sort_and_build_csr(col, pts.shape[0])
+                f = torch.ones(pts.shape[0], C, device=dev)[row]
+                outs.append(segment_reduce(f, cs, pm, a, b, pts.shape[0], reduce="max"))
+                outs.append(segment_reduce(f, cs, pm, a, b, pts.shape[0], reduce="mean"))
+            return outs
+        legs["c4_ms"] = wall_ms(c4_step, 10, 2)
+        c5 = make_c5()
+        p5 = c5["pos"].to(dev)
+        t0 = time.perf_counter()
+        i5 = farthest_point_sampling(p5, c5["M"])
+        torch.cuda.synchronize()
+        legs["c5_fps_ms"] = (time.perf_counter() - t0) * 1e3
+        cen5 = p5[i5]
+        legs["c5_radius_ms"] = wall_ms(lambda: radius_graph(cen5, c5["r"], max_num_neighbors=64), 10, 2)
+        pq = torch.tensor([0, c5["M"]], device=dev, dtype=torch.int64)
+        ps = torch.tensor([0, p5.shape[0]], device=dev, dtype=torch.int64)
+        legs["c5_knn_ms"] = wall_ms(lambda: knn(cen5, p5, pq, ps, c5["k"]), 5, 1)
+        log(f"  extra legs: {legs}")
+
+    # ---------------------------------------------------------------- CPU baseline ---
+    cpu = None
+    if not args.no_cpu and args.only in (None, "c2"):
+        from oracle import ref_cpu_path
+        threads = torch.get_num_threads()
+        log(f"CPU baseline (reference CPU path, {threads} threads) ...")
+        pc, ptrc = c2["pos"], c2["ptr"]
+        kc = torch.full((c2["B"],), c2["M"], dtype=torch.int64)
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ref_cpu_path.fps(pc, ptrc, kc)
+            t1 = time.perf_counter()
+            ref_cpu_path.radius_graph(pc, c2["r"], c2["B"], c2["K"])
+            t2 = time.perf_counter()
+            runs.append((t2 - t0, t1 - t0, t2 - t1))
+        tot, t_fps, t_rad = sorted(runs)[1]
+        per_batch_ms = tot * 1e3
+        cpu = {"value": round(per_batch_ms, 1), "unit": "ms/batch", "cores": threads,
+               "kind": "port",
+               "sample": f"reference CPU path (iterative FPS + batched cdist/topk radius graph, "
+                         f"oracle/ref_cpu_path.py) on the full C2 batch, median of 3; fps "
+                         f"{t_fps:.2f} s, radius {t_rad:.2f} s",
+               "cpu_model": _cpu_model()}
+        log(f"  CPU: {per_batch_ms:.0f} ms/batch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(ms_step, 4) if ms_step is not None else None,
+        "unit": "ms/batch",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4) if ms_step is not None else None,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded generators of the five BASELINE configs, see bench.py)",
+        "config": {
+            "workload": "C2: FPS 4096->1024 per cloud + radius_graph(r=0.1, K=32) over 16x4096 "
+                        "unit-sphere points (step); roofline leg: C3 segment_reduce sum fp32, "
+                        "E=4194304, S=262144, C=128",
+            "global_batch": 16, "points_per_cloud": 4096, "fps_samples": 1024,
+            "radius": 0.1, "max_num_neighbors": 32, "parallelism": "single GPU",
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "legs": legs,
+        "library": _native.build_info(),
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,400 @@
+"""Backend dispatcher — gfx950 HIP kernels for radius graph, segment reduce, KNN and FPS.
+
+Same public names as the reference dispatcher (geoembodied/csrc/__init__.py): the
+``*_available`` probes, ``get_radius_graph_backend``, ``radius_graph_cuda``,
+``sort_and_build_csr_cuda``, ``segment_reduce_sum_cuda``, ``knn_cuda``, ``knn_self_cuda`` and
+``fps_cuda``.  On ROCm PyTorch the GPU device type is ``cuda``, so "cuda" names the HIP path.
+
+Differences from the reference, by design:
+
+* Kernels come from the prebuilt ``libgeoembodied_hip.so`` (no JIT compilation at first call).
+* There is no CPU path.  CPU tensors raise ``RuntimeError``; the reference's CPU fallbacks
+  ``_fps_iterative_fallback`` and ``_knn_bruteforce`` keep their names so that importing callers
+  (nn/modules/equivariant_pool.py:261) still import, and raise when called.
+* Each op performs at most one device-to-host synchronisation, to size its output
+  (``fps_cuda``: sample count; radius graph: edge count; plus ``batch.max()`` when the caller
+  does not give ``num_batch_elements``, as the reference does).
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from gdl_amd import _native as _nat
+
+logger = logging.getLogger(__name__)
+
+_NO_CPU = (
+    "{name}: this MI355X build of geoembodied runs its geometry kernels on the GPU only; "
+    "got a tensor on {device}. Move the inputs to a 'cuda' (HIP) device."
+)
+
+
+def _require_gpu(name: str, *tensors: Optional[Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(_NO_CPU.format(name=name, device=t.device))
+
+
+def _hip_ready() -> bool:
+    return torch.cuda.is_available() and _nat.loaded()
+
+
+def _i64(t: Tensor, device: torch.device) -> Tensor:
+    return t.to(device=device, dtype=torch.int64).contiguous()
+
+
+def _positions(name: str, x: Tensor) -> Tensor:
+    if x.dim() != 2 or x.shape[1] != 3:
+        raise ValueError(f"{name}: positions must have shape [N, 3], got {tuple(x.shape)}")
+    return x.contiguous().float()
+
+
+def fp32_radius_sq(r: float) -> float:
+    """fl32(fl64(r) * fl64(r)): the threshold the reference's CPU path compares against."""
+    return float(np.float32(float(r) * float(r)))
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Radius graph
+# ═══════════════════════════════════════════════════════════════════
+
+
+def get_radius_graph_backend() -> str:
+    """'cuda' when the HIP library is loaded and a GPU is visible, else 'unavailable'."""
+    return "cuda" if _hip_ready() else "unavailable"
+
+
+def radius_graph_hip(
+    x: Tensor,
+    r: float,
+    *,
+    max_num_neighbors: int = 32,
+    loop: bool = False,
+    mask: Optional[Tensor] = None,
+    batch: Optional[Tensor] = None,
+    num_batch_elements: Optional[int] = None,
+) -> Tuple[Tensor, Tensor]:
+    """Radius graph on the GPU; returns (row=source, col=target) int64, sorted by target then
+    source.  Cloud membership comes from ``batch`` when given, otherwise from
+    ``num_batch_elements`` contiguous equal chunks (one cloud when neither is given)."""
+    _require_gpu("radius_graph", x, mask, batch)
+    x = _positions("radius_graph", x)
+    dev = x.device
+    N = x.shape[0]
+    K = int(max_num_neighbors)
+    if K < 0:
+        raise ValueError(f"radius_graph: max_num_neighbors must be >= 0, got {K}")
+    r = float(r)
+    empty = torch.empty(0, dtype=torch.int64, device=dev)
+    if N == 0 or K == 0 or not (r > 0.0):
+        return empty, empty.clone()
+    r2 = fp32_radius_sq(r)
+    if batch is not None:
+        if batch.numel() != N:
+            raise ValueError(f"radius_graph: batch has {batch.numel()} entries for {N} points")
+        batch = _i64(batch.reshape(-1), dev)
+        B = int(num_batch_elements) if num_batch_elements is not None else int(batch.max().item()) + 1
+        ppc = 0
+    else:
+        B = int(num_batch_elements) if num_batch_elements is not None else 1
+        if B < 1:
+            raise ValueError(f"radius_graph: num_batch_elements must be >= 1, got {B}")
+        if N % B != 0:
+            raise ValueError(f"radius_graph: {N} points do not split into {B} equal clouds")
+        ppc = N // B
+    if B < 1:
+        return empty, empty.clone()
+    mask_u8 = None
+    if mask is not None:
+        if mask.numel() != N:
+            raise ValueError(f"radius_graph: mask has {mask.numel()} entries for {N} points")
+        mask_u8 = mask.to(device=dev, dtype=torch.bool).reshape(-1).contiguous().view(torch.uint8)
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        s = _nat.stream_of(dev)
+        ws_bytes = L.geo_radius_workspace_bytes(N, B)
+        ws = _nat.workspace(ws_bytes, dev)
+        row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
+        args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K, int(bool(loop)))
+        _nat.check(L.geo_radius_count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s),
+                   "geo_radius_count")
+        E = int(row_ptr[N].item())
+        row = torch.empty(E, dtype=torch.int64, device=dev)
+        col = torch.empty(E, dtype=torch.int64, device=dev)
+        if E > 0:
+            _nat.check(L.geo_radius_emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col),
+                                         _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
+    return row, col
+
+
+def radius_graph_cuda(
+    x: Tensor,
+    r: float,
+    *,
+    max_num_neighbors: int = 32,
+    loop: bool = False,
+    mask: Optional[Tensor] = None,
+    batch_size: Optional[int] = None,
+    points_per_batch: Optional[int] = None,
+) -> Tuple[Tensor, Tensor]:
+    """Reference-compatible entry (geoembodied/csrc/__init__.py:130-186): one cloud, or
+    ``batch_size`` contiguous clouds of ``points_per_batch`` points."""
+    if batch_size is not None and batch_size > 1:
+        if points_per_batch is None:
+            raise ValueError("points_per_batch required when batch_size > 1")
+        if int(batch_size) * int(points_per_batch) != x.shape[0]:
+            raise ValueError("radius_graph_cuda: batch_size * points_per_batch != N")
+        nb = int(batch_size)
+    else:
+        nb = None
+    return radius_graph_hip(x, r, max_num_neighbors=max_num_neighbors, loop=loop, mask=mask,
+                            num_batch_elements=nb)
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Segment reduce + CSR build
+# ═══════════════════════════════════════════════════════════════════
+
+
+def segment_reduce_available() -> bool:
+    return _hip_ready()
+
+
+def sort_and_build_csr_cuda(col: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Stable sort of targets + CSR offsets: (col_sorted, perm, node_start, node_end), int32."""
+    _require_gpu("sort_and_build_csr", col)
+    if col.dim() != 1:
+        raise ValueError(f"sort_and_build_csr: col must be 1-D, got {tuple(col.shape)}")
+    N = int(N)
+    if N < 0:
+        raise ValueError(f"sort_and_build_csr: N must be >= 0, got {N}")
+    dev = col.device
+    col = _i64(col, dev)
+    E = col.shape[0]
+    i32 = dict(dtype=torch.int32, device=dev)
+    col_sorted = torch.empty(E, **i32)
+    perm = torch.empty(E, **i32)
+    node_start = torch.empty(N, **i32)
+    node_end = torch.empty(N, **i32)
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        ws_bytes = L.geo_csr_workspace_bytes(E, N)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_csr_build(_nat.ptr(col), E, N, _nat.ptr(col_sorted), _nat.ptr(perm),
+                                   _nat.ptr(node_start), _nat.ptr(node_end), _nat.ptr(ws),
+                                   ws_bytes, _nat.stream_of(dev)), "geo_csr_build")
+    return col_sorted, perm, node_start, node_end
+
+
+def _dtype_code(name: str, t: Tensor) -> int:
+    code = _nat.DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"{name}: unsupported dtype {t.dtype} (float32, bfloat16, float64)")
+    return code
+
+
+def _i32(t: Optional[Tensor], device: torch.device) -> Optional[Tensor]:
+    return None if t is None else t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def segment_reduce_forward_hip(
+    msg: Tensor,
+    perm: Optional[Tensor],
+    node_start: Tensor,
+    node_end: Tensor,
+    N: int,
+    reduce: str = "sum",
+    tie_mode: int = 0,
+) -> Tuple[Tensor, Optional[Tensor]]:
+    """out[N, C] (and the int32 argmax record for 'max')."""
+    _require_gpu("segment_reduce", msg, perm, node_start, node_end)
+    if reduce not in _nat.REDUCE_CODES:
+        raise ValueError(f"segment_reduce: reduce must be sum, mean or max, got {reduce!r}")
+    if msg.dim() != 2:
+        raise ValueError(f"segment_reduce: msg must be [E, C], got {tuple(msg.shape)}")
+    N = int(N)
+    if node_start.numel() < N or node_end.numel() < N:
+        raise ValueError("segment_reduce: node_start/node_end shorter than N")
+    code = _dtype_code("segment_reduce", msg)
+    dev = msg.device
+    msg = msg.contiguous()
+    E, C = msg.shape
+    perm = _i32(perm, dev)
+    if perm is not None and perm.numel() != E:
+        raise ValueError(f"segment_reduce: perm has {perm.numel()} entries for E={E}")
+    ns, ne = _i32(node_start, dev), _i32(node_end, dev)
+    out = torch.empty(N, C, dtype=msg.dtype, device=dev)
+    arg = torch.empty(N, C, dtype=torch.int32, device=dev) if reduce == "max" else None
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_segment_reduce_fwd(
+            _nat.REDUCE_CODES[reduce], code, _nat.ptr(msg), _nat.ptr(perm), _nat.ptr(ns),
+            _nat.ptr(ne), E, N, C, _nat.ptr(out), _nat.ptr(arg), int(tie_mode),
+            _nat.stream_of(dev)), "geo_segment_reduce_fwd")
+    return out, arg
+
+
+def segment_reduce_backward_hip(
+    grad_out: Tensor,
+    col_sorted: Tensor,
+    perm: Optional[Tensor],
+    node_start: Optional[Tensor],
+    node_end: Optional[Tensor],
+    E: int,
+    reduce: str = "sum",
+    msg: Optional[Tensor] = None,
+    out: Optional[Tensor] = None,
+    arg: Optional[Tensor] = None,
+) -> Tensor:
+    """grad_msg[E, C] for the given reduction."""
+    _require_gpu("segment_reduce backward", grad_out, col_sorted, perm, msg, out, arg)
+    code = _dtype_code("segment_reduce backward", grad_out)
+    dev = grad_out.device
+    grad_out = grad_out.contiguous()
+    S, C = grad_out.shape
+    grad_msg = torch.empty(int(E), C, dtype=grad_out.dtype, device=dev)
+    cs = _i32(col_sorted, dev)
+    pm = _i32(perm, dev)
+    ns, ne = _i32(node_start, dev), _i32(node_end, dev)
+    if msg is not None:
+        msg = msg.to(grad_out.dtype).contiguous()
+    if out is not None:
+        out = out.to(grad_out.dtype).contiguous()
+    if arg is not None:
+        arg = arg.contiguous()
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_segment_reduce_bwd(
+            _nat.REDUCE_CODES[reduce], code, _nat.ptr(grad_out), _nat.ptr(msg), _nat.ptr(out),
+            _nat.ptr(arg), _nat.ptr(cs), _nat.ptr(pm), _nat.ptr(ns), _nat.ptr(ne), int(E), S, C,
+            _nat.ptr(grad_msg), _nat.stream_of(dev)), "geo_segment_reduce_bwd")
+    return grad_msg
+
+
+def segment_reduce_sum_cuda(
+    msg: Tensor,
+    perm: Tensor,
+    node_start: Tensor,
+    node_end: Tensor,
+    N: int,
+) -> Tensor:
+    """Deterministic segment sum (reference name; geoembodied/csrc/__init__.py:280-302)."""
+    return segment_reduce_forward_hip(msg, perm, node_start, node_end, N, "sum")[0]
+
+
+# ═══════════════════════════════════════════════════════════════════
+# KNN
+# ═══════════════════════════════════════════════════════════════════
+
+
+def knn_available() -> bool:
+    return _hip_ready()
+
+
+def knn_cuda(
+    query: Tensor,
+    source: Tensor,
+    ptr_q: Tensor,
+    ptr_s: Tensor,
+    k: int,
+) -> Tuple[Tensor, Tensor]:
+    """k nearest sources of each query within its cloud: (indices int64 [N_q, k] global source
+    indices or -1, squared distances float32 [N_q, k] or 1e30), ascending by (distance, index)."""
+    _require_gpu("knn", query, source)
+    q = _positions("knn", query)
+    s = _positions("knn", source)
+    dev = q.device
+    if ptr_q.numel() != ptr_s.numel():
+        raise ValueError("ptr_q and ptr_s must have same length (B+1)")
+    k = int(k)
+    if k < 0:
+        raise ValueError(f"knn: k must be >= 0, got {k}")
+    pq, ps = _i64(ptr_q, dev), _i64(ptr_s, dev)
+    B = pq.numel() - 1
+    Nq, Ns = q.shape[0], s.shape[0]
+    out_idx = torch.empty(Nq, k, dtype=torch.int64, device=dev)
+    out_d = torch.empty(Nq, k, dtype=torch.float32, device=dev)
+    if Nq == 0 or k == 0:
+        return out_idx, out_d
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        ws_bytes = L.geo_knn_workspace_bytes(Nq, Ns, max(B, 0), k)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_knn(_nat.ptr(q), Nq, _nat.ptr(s), Ns, _nat.ptr(pq), _nat.ptr(ps),
+                             max(B, 0), k, _nat.ptr(out_idx), _nat.ptr(out_d), _nat.ptr(ws),
+                             ws_bytes, _nat.stream_of(dev)), "geo_knn")
+    return out_idx, out_d
+
+
+def knn_self_cuda(points: Tensor, ptr: Tensor, k: int) -> Tuple[Tensor, Tensor]:
+    """Self-KNN within each cloud; self (distance 0) is included."""
+    return knn_cuda(points, points, ptr, ptr, k)
+
+
+def _knn_bruteforce(query, source, ptr_q, ptr_s, k):
+    """Name kept from the reference CPU fallback; this build has no CPU path."""
+    raise RuntimeError(_NO_CPU.format(name="_knn_bruteforce", device=query.device))
+
+
+# ═══════════════════════════════════════════════════════════════════
+# FPS
+# ═══════════════════════════════════════════════════════════════════
+
+
+def fps_available() -> bool:
+    return _hip_ready()
+
+
+def fps_cuda(pos: Tensor, ptr: Tensor, k_per_batch: Tensor) -> Tensor:
+    """Farthest point sampling per cloud; int64 global indices concatenated by cloud.
+
+    k is clamped to [0, cloud size]; a cloud sampled completely returns its indices in order.
+    One host sync (the output size)."""
+    _require_gpu("fps", pos)
+    pos = _positions("fps", pos)
+    dev = pos.device
+    p = _i64(ptr, dev)
+    kk = _i64(k_per_batch, dev)
+    B = p.numel() - 1
+    if B < 0:
+        raise ValueError("fps: ptr must have at least one entry")
+    if kk.numel() != B:
+        raise ValueError(f"fps: k_per_batch has {kk.numel()} entries for {B} clouds")
+    N = pos.shape[0]
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        s = _nat.stream_of(dev)
+        out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
+        info = torch.empty(3, dtype=torch.int64, device=dev)
+        _nat.check(L.geo_fps_prepare(_nat.ptr(p), _nat.ptr(kk), B, N, _nat.ptr(out_ptr),
+                                     _nat.ptr(info), s), "geo_fps_prepare")
+        total, max_n, bad = info.tolist()
+        if bad:
+            raise ValueError(f"fps: ptr is not a non-decreasing offset array within [0, {N}] "
+                             f"(first bad entry: ptr[{bad - 1}])")
+        out = torch.empty(total, dtype=torch.int64, device=dev)
+        if total == 0:
+            return out
+        ws_bytes = L.geo_fps_workspace_bytes(B, N, max_n)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_fps(_nat.ptr(pos), N, _nat.ptr(p), _nat.ptr(out_ptr), B, max_n,
+                             _nat.ptr(out), _nat.ptr(ws), ws_bytes, s), "geo_fps")
+    return out
+
+
+def _fps_iterative_fallback(pos, ptr, k_per_batch):
+    """Name kept from the reference CPU fallback; this build has no CPU path."""
+    raise RuntimeError(_NO_CPU.format(name="_fps_iterative_fallback", device=pos.device))
+
+
+__all__ = [
+    "get_radius_graph_backend", "radius_graph_cuda", "radius_graph_hip", "fp32_radius_sq",
+    "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
+    "segment_reduce_forward_hip", "segment_reduce_backward_hip",
+    "knn_available", "knn_cuda", "knn_self_cuda",
+    "fps_available", "fps_cuda",
+]

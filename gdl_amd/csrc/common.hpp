@@ -1,0 +1,169 @@
+// common.hpp — shared host/device helpers for the gfx950 geometry kernels.
+//
+// gfx950 (CDNA4) runs 64-lane wavefronts only; every cross-lane helper below assumes that.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/geo_api.h"
+
+namespace geo {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- host errors ---
+
+// Records a message for geo_last_error() on the calling thread; returns `code`.
+int set_error(int code, const char* fmt, ...);
+
+#define GEO_REQUIRE(cond, ...)                                  \
+  do {                                                          \
+    if (!(cond)) return ::geo::set_error(GEO_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define GEO_HIP_CHECK(expr)                                                        \
+  do {                                                                             \
+    hipError_t _e = (expr);                                                        \
+    if (_e != hipSuccess)                                                          \
+      return ::geo::set_error(GEO_ERR_HIP, "%s failed: %s (%s:%d)", #expr,         \
+                              hipGetErrorString(_e), __FILE__, __LINE__);          \
+  } while (0)
+
+// Checks the launch status of the kernels enqueued just before.
+#define GEO_LAUNCH_CHECK(what)                                                     \
+  do {                                                                             \
+    hipError_t _e = hipGetLastError();                                             \
+    if (_e != hipSuccess)                                                          \
+      return ::geo::set_error(GEO_ERR_HIP, "launch of %s failed: %s", what,        \
+                              hipGetErrorString(_e));                              \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves aligned sub-buffers out of one caller-provided workspace.
+struct Carver {
+  char* base;
+  size_t used = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    used = align_up(used, 256);
+    T* p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+    used += count * sizeof(T);
+    return p;
+  }
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------- lane primitives ---
+
+__device__ __forceinline__ int lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// DPP control codes (GFX9 encoding).
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;       // lane i <-> 15-i within 16
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// Every lane receives the max / min of its 16-lane row.
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+  v = min(v, dpp_u32<kDppXor1>(v));
+  v = min(v, dpp_u32<kDppXor2>(v));
+  v = min(v, dpp_u32<kDppHalfMirror>(v));
+  v = min(v, dpp_u32<kDppMirror>(v));
+  return v;
+}
+
+// Wave-uniform max / min over all 64 lanes (every lane must be active).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = row_max_u32(v);
+  uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = row_min_u32(v);
+  uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return min(min(a, b), min(c, d));
+}
+
+// Wave-wide inclusive prefix sum (all lanes active).
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_sum(T v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    T o = __shfl_up(v, d, kWave);
+    if (l >= d) v += o;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------- exact distance ---
+// Squared distance with the reference's operation order, (dx*dx + dy*dy) + dz*dz, each
+// operation rounded to fp32.  The library is compiled with -ffp-contract=off; the pragma keeps
+// the multiply-adds unfused here even if that flag is dropped.
+__device__ __forceinline__ float sqdist(float ax, float ay, float az, float bx, float by,
+                                        float bz) {
+#pragma clang fp contract(off)
+  const float dx = ax - bx, dy = ay - by, dz = az - bz;
+  return (dx * dx + dy * dy) + dz * dz;
+}
+
+// ---------------------------------------------------------------- bfloat16 ---
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round to nearest even; NaN -> canonical quiet NaN (matches PyTorch's conversion).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Float -> uint32 key that orders like the float (for atomic min / max on floats).
+__device__ __forceinline__ uint32_t float_order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float float_from_order_key(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+}  // namespace geo

@@ -1,0 +1,443 @@
+// radius_graph.hip — batched fixed-radius neighbour graph on gfx950.
+//
+// Replaces compute_cell_indices_kernel / CUB sort / compute_cell_offsets_kernel /
+// find_neighbors_kernel and the host loop over clouds (geoembodied/csrc/radius_graph_kernel.cu:
+// 91-467) with one device pipeline for all clouds and exact semantics (edge j -> i iff same
+// cloud, both valid, loop or i != j, d < r2; per target the K smallest (d, j)).
+//
+// geo_radius_count:
+//   rg_init     zero counters, reset bounding boxes
+//   rg_bbox     per-cloud point count and bounding box (wave-reduced atomics)
+//   rg_setup    per cloud: cell edge h >= r*(1+1/32), grid dims (capped at 4*n+64 cells and
+//               16384 per axis so that the 3x3x3 stencil stays exact), cell base offsets
+//   rg_cell     cell id per point, rank inside the cell (atomic counter)
+//   scan        cell offsets
+//   rg_scatter  points in cell order as float4 (x, y, z, index bits)
+//   rg_query<0> one thread per point in cell order (neighbouring threads share cells): count
+//               of in-radius sources over the 9 z-contiguous runs of the 27-cell stencil
+//   scan        row_ptr = exclusive scan of min(count, K) over target index
+// geo_radius_emit:
+//   rg_query<1> re-scans, keeps all accepted sources when count <= K, otherwise the K smallest
+//               (d, j) found by a bitwise threshold search; sources are kept sorted by index
+//               in an LDS list (K <= 256) or directly in the output row, then written.
+// Traversal order inside a cell is not deterministic (atomic ranks) and does not matter: the
+// accepted set is defined by a total order and the output is sorted.
+#include "scan.hpp"
+
+namespace geo {
+namespace {
+
+constexpr int kRgThreads = 256;
+constexpr int kRgEmitThreads = 64;
+constexpr int kRgMaxAxis = 16384;
+constexpr int kRgLdsK = 256;
+
+struct Grid {
+  float ox, oy, oz, inv_h;
+  int dx, dy, dz, base;
+};
+
+struct RgWs {
+  int32_t* cloud_n;
+  uint32_t* bbox;  // [B][6]: min x,y,z keys then max x,y,z keys
+  Grid* grid;
+  int32_t* pt_cell;
+  int32_t* pt_rank;
+  int32_t* cell_cnt;
+  int32_t* cell_start;
+  int32_t* cell_tiles;
+  float4* spos;
+  int32_t* cnt;
+  int32_t* deg;
+  int64_t* deg_tiles;
+  int64_t cells_max;
+  size_t bytes;
+};
+
+int64_t cells_cap(int64_t N, int64_t B) { return 4 * N + 64 * B; }
+
+RgWs carve_rg(void* base, int64_t N, int64_t B) {
+  Carver c(base);
+  RgWs w;
+  const int64_t nn = N > 0 ? N : 1, bb = B > 0 ? B : 1;
+  w.cells_max = cells_cap(N, B);
+  w.cloud_n = c.take<int32_t>(bb);
+  w.bbox = c.take<uint32_t>(6 * bb);
+  w.grid = c.take<Grid>(bb);
+  w.pt_cell = c.take<int32_t>(nn);
+  w.pt_rank = c.take<int32_t>(nn);
+  w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
+  w.cell_start = c.take<int32_t>(w.cells_max + 1);
+  w.cell_tiles = c.take<int32_t>(scan_workspace_elems(w.cells_max));
+  w.spos = c.take<float4>(nn);
+  w.cnt = c.take<int32_t>(nn);
+  w.deg = c.take<int32_t>(nn);
+  w.deg_tiles = c.take<int64_t>(scan_workspace_elems(N));
+  w.bytes = c.used;
+  return w;
+}
+
+__device__ __forceinline__ int cloud_of(int64_t i, const int64_t* __restrict__ batch, int64_t B,
+                                        int64_t ppc) {
+  if (batch) {
+    const int64_t b = batch[i];
+    return (b >= 0 && b < B) ? static_cast<int>(b) : -1;
+  }
+  const int64_t b = ppc > 0 ? i / ppc : 0;
+  return b < B ? static_cast<int>(b) : -1;
+}
+
+__global__ void rg_init(RgWs w, int64_t N, int64_t B) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < w.cells_max + 1 || i < N || i < 6 * B; i += stride) {
+    if (i < w.cells_max + 1) w.cell_cnt[i] = 0;
+    if (i < N) { w.cnt[i] = 0; w.deg[i] = 0; }
+    if (i < B) w.cloud_n[i] = 0;
+    if (i < 6 * B) w.bbox[i] = (i % 6) < 3 ? 0xffffffffu : 0u;
+  }
+}
+
+__global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __restrict__ x, int64_t N,
+                                                      const int64_t* __restrict__ batch, int64_t B,
+                                                      int64_t ppc, const uint8_t* __restrict__ mask) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  int b = -1;
+  float px = 0.f, py = 0.f, pz = 0.f;
+  if (i < N) {
+    b = cloud_of(i, batch, B, ppc);
+    if (mask && !mask[i]) b = -1;
+    if (b >= 0) { px = x[3 * i]; py = x[3 * i + 1]; pz = x[3 * i + 2]; }
+  }
+  const int b0 = __builtin_amdgcn_readfirstlane(b);
+  const bool uniform = __ballot(b != b0) == 0ull;
+  if (uniform) {
+    if (b0 < 0) return;
+    const uint32_t kx = float_order_key(px), ky = float_order_key(py), kz = float_order_key(pz);
+    const uint32_t mnx = wave_min_u32(kx), mny = wave_min_u32(ky), mnz = wave_min_u32(kz);
+    const uint32_t mxx = wave_max_u32(kx), mxy = wave_max_u32(ky), mxz = wave_max_u32(kz);
+    if (lane_id() == 0) {
+      atomicAdd(&w.cloud_n[b0], kWave);
+      uint32_t* bb = w.bbox + 6 * b0;
+      atomicMin(&bb[0], mnx); atomicMin(&bb[1], mny); atomicMin(&bb[2], mnz);
+      atomicMax(&bb[3], mxx); atomicMax(&bb[4], mxy); atomicMax(&bb[5], mxz);
+    }
+  } else if (b >= 0) {
+    atomicAdd(&w.cloud_n[b], 1);
+    uint32_t* bb = w.bbox + 6 * b;
+    atomicMin(&bb[0], float_order_key(px)); atomicMin(&bb[1], float_order_key(py));
+    atomicMin(&bb[2], float_order_key(pz));
+    atomicMax(&bb[3], float_order_key(px)); atomicMax(&bb[4], float_order_key(py));
+    atomicMax(&bb[5], float_order_key(pz));
+  }
+}
+
+// Single workgroup: grid parameters and cell bases for every cloud.
+__global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, float r_cell) {
+  __shared__ int64_t lds[kScanThreads / kWave];
+  int64_t carry = 0;
+  for (int64_t base = 0; base < B; base += kScanThreads) {
+    const int64_t b = base + threadIdx.x;
+    int64_t cells = 0;
+    Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
+    if (b < B && w.cloud_n[b] > 0) {
+      const uint32_t* bb = w.bbox + 6 * b;
+      const float mn[3] = {float_from_order_key(bb[0]), float_from_order_key(bb[1]),
+                           float_from_order_key(bb[2])};
+      const float mx[3] = {float_from_order_key(bb[3]), float_from_order_key(bb[4]),
+                           float_from_order_key(bb[5])};
+      const double cap = 4.0 * w.cloud_n[b] + 64.0;
+      double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
+      double ext[3];
+      for (int a = 0; a < 3; ++a) {
+        const double e = static_cast<double>(mx[a]) - static_cast<double>(mn[a]);
+        ext[a] = (e >= 0.0 && e < 1e30) ? e : 0.0;  // non-finite input: one slab on that axis
+      }
+      int64_t d[3] = {1, 1, 1};
+      bool ok = false;
+      for (int iter = 0; iter < 64 && !ok; ++iter) {
+        double prod = 1.0, worst_axis = 0.0;
+        for (int a = 0; a < 3; ++a) {
+          const double q = floor(ext[a] / h) + 1.0;
+          d[a] = q < static_cast<double>(kRgMaxAxis) * 4 ? static_cast<int64_t>(q) : kRgMaxAxis * 4;
+          prod *= static_cast<double>(d[a]);
+          worst_axis = fmax(worst_axis, static_cast<double>(d[a]) / kRgMaxAxis);
+        }
+        ok = prod <= cap && worst_axis <= 1.0;
+        if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst_axis), 1.0) * 1.01;
+      }
+      g.ox = mn[0]; g.oy = mn[1]; g.oz = mn[2];
+      g.inv_h = static_cast<float>(1.0 / h);
+      if (!ok) {  // one cell holds the whole cloud
+        d[0] = d[1] = d[2] = 1;
+        g.inv_h = 0.f;
+      }
+      g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
+      cells = d[0] * d[1] * d[2];
+    }
+    int64_t total;
+    const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
+    if (b < B) {
+      g.base = static_cast<int>(carry + off);
+      w.grid[b] = g;
+    }
+    carry += total;
+  }
+}
+
+__device__ __forceinline__ int cell_coord(float p, float o, float inv_h, int dim) {
+#pragma clang fp contract(off)
+  const float u = (p - o) * inv_h;
+  int c = static_cast<int>(floorf(u));
+  return c < 0 ? 0 : (c >= dim ? dim - 1 : c);
+}
+
+__global__ __launch_bounds__(kRgThreads) void rg_cell(RgWs w, const float* __restrict__ x, int64_t N,
+                                                      const int64_t* __restrict__ batch, int64_t B,
+                                                      int64_t ppc, const uint8_t* __restrict__ mask) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  int b = cloud_of(i, batch, B, ppc);
+  if (mask && !mask[i]) b = -1;
+  if (b < 0) {
+    w.pt_cell[i] = -1;
+    return;
+  }
+  const Grid g = w.grid[b];
+  const int cx = cell_coord(x[3 * i], g.ox, g.inv_h, g.dx);
+  const int cy = cell_coord(x[3 * i + 1], g.oy, g.inv_h, g.dy);
+  const int cz = cell_coord(x[3 * i + 2], g.oz, g.inv_h, g.dz);
+  const int c = g.base + (cx * g.dy + cy) * g.dz + cz;
+  w.pt_cell[i] = c;
+  w.pt_rank[i] = atomicAdd(&w.cell_cnt[c], 1);
+}
+
+__global__ __launch_bounds__(kRgThreads) void rg_scatter(RgWs w, const float* __restrict__ x,
+                                                         int64_t N) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const int c = w.pt_cell[i];
+  if (c < 0) return;
+  const int p = w.cell_start[c] + w.pt_rank[i];
+  w.spos[p] = make_float4(x[3 * i], x[3 * i + 1], x[3 * i + 2], __int_as_float(static_cast<int>(i)));
+}
+
+// Visits every source of the 27-cell stencil around the query as (d, j).
+template <typename F>
+__device__ __forceinline__ void for_each_candidate(const RgWs& w, const Grid& g, float qx, float qy,
+                                                   float qz, int qi, bool loop, F&& f) {
+  const int cx = cell_coord(qx, g.ox, g.inv_h, g.dx);
+  const int cy = cell_coord(qy, g.oy, g.inv_h, g.dy);
+  const int cz = cell_coord(qz, g.oz, g.inv_h, g.dz);
+  const int z0 = cz > 0 ? cz - 1 : 0;
+  const int z1 = cz + 1 < g.dz ? cz + 1 : g.dz - 1;
+  for (int ix = cx - 1; ix <= cx + 1; ++ix) {
+    if (ix < 0 || ix >= g.dx) continue;
+    for (int iy = cy - 1; iy <= cy + 1; ++iy) {
+      if (iy < 0 || iy >= g.dy) continue;
+      const int c0 = g.base + (ix * g.dy + iy) * g.dz;
+      const int a = w.cell_start[c0 + z0];
+      const int e = w.cell_start[c0 + z1 + 1];
+      for (int p = a; p < e; ++p) {
+        const float4 s = w.spos[p];
+        const int j = __float_as_int(s.w);
+        if (!loop && j == qi) continue;
+        f(sqdist(qx, qy, qz, s.x, s.y, s.z), j);
+      }
+    }
+  }
+}
+
+// Accepted-source list for one query, kept sorted by index.
+struct RowList {
+  int32_t* lds;   // LDS column (stride kRgEmitThreads) or nullptr
+  int64_t* out;   // output row
+  int n = 0;
+  __device__ __forceinline__ int get(int m) const {
+    return lds ? lds[m * kRgEmitThreads] : static_cast<int>(out[m]);
+  }
+  __device__ __forceinline__ void set(int m, int v) {
+    if (lds) lds[m * kRgEmitThreads] = v; else out[m] = v;
+  }
+  __device__ __forceinline__ void insert(int j) {
+    int m = n;
+    while (m > 0) {
+      const int v = get(m - 1);
+      if (v < j) break;
+      set(m, v);
+      --m;
+    }
+    set(m, j);
+    ++n;
+  }
+};
+
+template <int MODE>  // 0 = count, 1 = emit
+__global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, int64_t ppc,
+                         float r2, int K, int loop, const int64_t* __restrict__ row_ptr,
+                         int64_t* __restrict__ row_out, int64_t* __restrict__ col_out,
+                         int use_lds) {
+  __shared__ int32_t lbuf[MODE == 1 ? kRgLdsK * kRgEmitThreads : 1];
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int total = w.cell_start[w.cells_max];
+  if (t >= total) return;
+  const float4 q = w.spos[t];
+  const int qi = __float_as_int(q.w);
+  const int b = cloud_of(qi, batch, B, ppc);
+  const Grid g = w.grid[b];
+  const bool lp = loop != 0;
+  if constexpr (MODE == 0) {
+    int c = 0;
+    for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) { c += d < r2; });
+    w.cnt[qi] = c;
+    w.deg[qi] = c < K ? c : K;
+  } else {
+    const int c = w.cnt[qi];
+    if (c == 0) return;
+    const int64_t o = row_ptr[qi];
+    RowList lst;
+    lst.lds = use_lds ? lbuf + threadIdx.x : nullptr;
+    lst.out = row_out + o;
+    if (c <= K) {
+      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
+        if (d < r2) lst.insert(j);
+      });
+    } else {
+      // K smallest (d, j): binary search the K-th distance bits, then the index among ties.
+      const uint32_t r2b = __float_as_uint(r2);
+      uint32_t lo = 0, hi = r2b > 0 ? r2b - 1 : 0;
+      while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        int n = 0;
+        for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) {
+          n += (d < r2) && (__float_as_uint(d) <= mid);
+        });
+        if (n >= K) hi = mid; else lo = mid + 1;
+      }
+      const uint32_t dstar = lo;
+      int less = 0;
+      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) {
+        less += (d < r2) && (__float_as_uint(d) < dstar);
+      });
+      const int need = K - less;
+      int jlo = 0, jhi = 0x7ffffffe;
+      while (jlo < jhi) {
+        const int mid = jlo + ((jhi - jlo) >> 1);
+        int n = 0;
+        for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
+          n += (d < r2) && (__float_as_uint(d) == dstar) && (j <= mid);
+        });
+        if (n >= need) jhi = mid; else jlo = mid + 1;
+      }
+      const int jstar = jlo;
+      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
+        if (d < r2) {
+          const uint32_t db = __float_as_uint(d);
+          if (db < dstar || (db == dstar && j <= jstar)) lst.insert(j);
+        }
+      });
+    }
+    for (int m = 0; m < lst.n; ++m) {
+      if (lst.lds) row_out[o + m] = lst.get(m);
+      col_out[o + m] = qi;
+    }
+  }
+}
+
+int check_common(const float* x, int64_t N, int64_t B, int64_t ppc, const int64_t* batch,
+                 float r2, int64_t K) {
+  GEO_REQUIRE(N >= 0 && B >= 1, "radius_graph: need N >= 0 and B >= 1 (N=%lld B=%lld)",
+              (long long)N, (long long)B);
+  GEO_REQUIRE(N < 0x7fffffffLL / 4, "radius_graph: N=%lld too large", (long long)N);
+  GEO_REQUIRE(batch != nullptr || ppc * B == N,
+              "radius_graph: without batch, B*points_per_cloud must equal N");
+  GEO_REQUIRE(K >= 1 && K < 0x7fffffffLL, "radius_graph: max_num_neighbors must be >= 1");
+  GEO_REQUIRE(r2 == r2 && r2 >= 0.f, "radius_graph: r2 must be a non-negative number");
+  GEO_REQUIRE(N == 0 || x != nullptr, "radius_graph: null x");
+  return GEO_OK;
+}
+
+}  // namespace
+}  // namespace geo
+
+using namespace geo;
+
+extern "C" size_t geo_radius_workspace_bytes(int64_t N, int64_t B) {
+  if (N < 0 || B < 0) return 0;
+  return carve_rg(nullptr, N, B).bytes;
+}
+
+extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                                int64_t points_per_cloud, const uint8_t* mask, float r2,
+                                float r_cell, int64_t max_num_neighbors, int loop,
+                                int64_t* row_ptr, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
+  if (rc) return rc;
+  GEO_REQUIRE(r_cell > 0.f, "radius_graph: r_cell must be positive");
+  GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
+  RgWs w = carve_rg(workspace, N, B);
+  if (workspace == nullptr || workspace_bytes < w.bytes)
+    return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
+                     workspace_bytes, w.bytes);
+  hipStream_t st = as_stream(stream);
+  const int K = static_cast<int>(max_num_neighbors);
+  {
+    int64_t span = w.cells_max + 1;
+    if (N > span) span = N;
+    if (6 * B > span) span = 6 * B;
+    int64_t blocks = ceil_div(span, 256);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(rg_init, dim3(blocks), dim3(256), 0, st, w, N, B);
+    GEO_LAUNCH_CHECK("rg_init");
+  }
+  if (N > 0) {
+    const int64_t blocks = ceil_div(N, kRgThreads);
+    hipLaunchKernelGGL(rg_bbox, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N, batch, B,
+                       points_per_cloud, mask);
+    GEO_LAUNCH_CHECK("rg_bbox");
+    hipLaunchKernelGGL(rg_setup, dim3(1), dim3(kScanThreads), 0, st, w, B, r_cell);
+    GEO_LAUNCH_CHECK("rg_setup");
+    hipLaunchKernelGGL(rg_cell, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N, batch, B,
+                       points_per_cloud, mask);
+    GEO_LAUNCH_CHECK("rg_cell");
+  }
+  rc = device_exclusive_scan<int32_t, int32_t>(w.cell_cnt, w.cells_max, w.cell_start, nullptr,
+                                               true, w.cell_tiles, st);
+  if (rc) return rc;
+  if (N > 0) {
+    const int64_t blocks = ceil_div(N, kRgThreads);
+    hipLaunchKernelGGL(rg_scatter, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N);
+    GEO_LAUNCH_CHECK("rg_scatter");
+    hipLaunchKernelGGL((rg_query<0>), dim3(blocks), dim3(kRgThreads), 0, st, w, batch, B,
+                       points_per_cloud, r2, K, loop, static_cast<const int64_t*>(nullptr),
+                       static_cast<int64_t*>(nullptr), static_cast<int64_t*>(nullptr), 0);
+    GEO_LAUNCH_CHECK("rg_query<count>");
+  }
+  return device_exclusive_scan<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true, w.deg_tiles, st);
+}
+
+extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                               int64_t points_per_cloud, const uint8_t* mask, float r2,
+                               float r_cell, int64_t max_num_neighbors, int loop,
+                               const int64_t* row_ptr, int64_t* row_out, int64_t* col_out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  (void)mask; (void)r_cell;
+  int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
+  if (rc) return rc;
+  GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
+  RgWs w = carve_rg(workspace, N, B);
+  if (workspace == nullptr || workspace_bytes < w.bytes)
+    return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
+                     workspace_bytes, w.bytes);
+  if (N == 0) return GEO_OK;
+  GEO_REQUIRE(row_out && col_out, "radius_graph: null outputs");
+  hipStream_t st = as_stream(stream);
+  const int K = static_cast<int>(max_num_neighbors);
+  const int use_lds = K <= kRgLdsK ? 1 : 0;
+  const int64_t blocks = ceil_div(N, kRgEmitThreads);
+  hipLaunchKernelGGL((rg_query<1>), dim3(blocks), dim3(kRgEmitThreads), 0, st, w, batch, B,
+                     points_per_cloud, r2, K, loop, row_ptr, row_out, col_out, use_lds);
+  GEO_LAUNCH_CHECK("rg_query<emit>");
+  return GEO_OK;
+}

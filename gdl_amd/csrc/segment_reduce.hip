@@ -1,0 +1,499 @@
+// segment_reduce.hip — sorted-segment sum / mean / max, forward and backward, for gfx950.
+//
+// Forward (replaces segment_reduce_sum_kernel, geoembodied/csrc/segment_reduce_kernel.cu:66-93):
+//   one wavefront owns `segs_per_wave` consecutive segments.  A row of C elements is read as
+//   16-byte (or narrower, when C or the pointers do not allow it) vectors; L lanes cover a row
+//   (L = next power of two >= vectors per row, at most 64) and the wave's R = 64/L lane groups
+//   take rows start+g, start+g+R, ... so one wave-wide load instruction moves R whole rows.
+//   Four such loads are issued before any accumulation to keep >= 4 KB per wave in flight.
+//   The R partial results are combined with a xor-butterfly; no atomics, no LDS.
+// Backward (replaces the ATen gather + un-permute of geoembodied/functional/segment_reduce.py:
+//   259-270): one lane group per sorted edge row e, grad_msg[perm[e]] = f(grad_out[col_sorted[e]]).
+//
+// Sum / mean accumulate in fp32 (fp64 for double) in ascending row order inside a lane group;
+// the butterfly order is fixed, so results are bitwise reproducible run to run.
+// Every index read from memory is range-checked, so inconsistent CSR arrays cannot make a
+// kernel access memory outside the given tensors.
+#include "common.hpp"
+
+namespace geo {
+namespace {
+
+constexpr int kSegThreads = 256;
+constexpr int kSegWaves = kSegThreads / kWave;
+constexpr int kUnroll = 4;
+
+template <typename T> struct AccT { using type = float; };
+template <> struct AccT<double> { using type = double; };
+
+__device__ __forceinline__ float to_acc(float x) { return x; }
+__device__ __forceinline__ float to_acc(uint16_t x) { return bf16_to_f32(x); }
+__device__ __forceinline__ double to_acc(double x) { return x; }
+
+template <typename T> __device__ __forceinline__ T from_acc(float x);
+template <> __device__ __forceinline__ float from_acc<float>(float x) { return x; }
+template <> __device__ __forceinline__ uint16_t from_acc<uint16_t>(float x) { return f32_to_bf16(x); }
+template <typename T> __device__ __forceinline__ T from_acc(double x);
+template <> __device__ __forceinline__ double from_acc<double>(double x) { return x; }
+
+template <int VB> struct Raw;
+template <> struct Raw<16> { using type = uint4; };
+template <> struct Raw<8> { using type = uint2; };
+template <> struct Raw<4> { using type = uint32_t; };
+template <> struct Raw<2> { using type = uint16_t; };
+
+// One lane's slice of a row: VB bytes = EPV elements.
+template <typename T, int VB>
+struct Vec {
+  static constexpr int EPV = VB / static_cast<int>(sizeof(T));
+  union {
+    typename Raw<VB>::type raw;
+    T e[EPV];
+  };
+  __device__ __forceinline__ void load(const T* p) {
+    raw = *reinterpret_cast<const typename Raw<VB>::type*>(p);
+  }
+  __device__ __forceinline__ void store(T* p) const {
+    *reinterpret_cast<typename Raw<VB>::type*>(p) = raw;
+  }
+};
+
+// EPV int32 argmax entries belonging to one vector slice (4..32 bytes).
+template <int N>
+struct IVec {
+  int32_t e[N];
+  __device__ __forceinline__ void load(const int32_t* p) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 4) {
+        int4 t = *reinterpret_cast<const int4*>(p + i);
+        e[i] = t.x; e[i + 1] = t.y; e[i + 2] = t.z; e[i + 3] = t.w;
+      }
+    } else if constexpr (N == 2) {
+      int2 t = *reinterpret_cast<const int2*>(p);
+      e[0] = t.x; e[1] = t.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) e[i] = p[i];
+    }
+  }
+  __device__ __forceinline__ void store(int32_t* p) const {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < N; i += 4)
+        *reinterpret_cast<int4*>(p + i) = make_int4(e[i], e[i + 1], e[i + 2], e[i + 3]);
+    } else if constexpr (N == 2) {
+      *reinterpret_cast<int2*>(p) = make_int2(e[0], e[1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) p[i] = e[i];
+    }
+  }
+};
+
+// Max ordering with NaN above every number (NaN propagates like torch.maximum).
+template <typename A>
+__device__ __forceinline__ bool max_gt(A a, A b) { return a != a ? (b == b) : (a > b); }
+template <typename A>
+__device__ __forceinline__ bool max_eq(A a, A b) { return a != a ? (b != b) : (a == b); }
+
+template <typename A>
+__device__ __forceinline__ A shfl_xor_acc(A v, int m) { return __shfl_xor(v, m, kWave); }
+
+__device__ __forceinline__ int clamp_i(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+template <typename T, int VB, int OP>
+__global__ __launch_bounds__(kSegThreads) void seg_fwd_kernel(
+    const T* __restrict__ msg, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_end, int32_t E,
+    int64_t S, int64_t C, int vpr, int log_l, int segs_per_wave, T* __restrict__ out,
+    int32_t* __restrict__ arg, int tie_mode) {
+  using A = typename AccT<T>::type;
+  using V = Vec<T, VB>;
+  constexpr int EPV = V::EPV;
+  const int lane = lane_id();
+  const int L = 1 << log_l;
+  const int R = kWave >> log_l;
+  const int g = lane >> log_l;
+  const int vl = lane & (L - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSegWaves + (threadIdx.x / kWave);
+  const int64_t s_begin = wave * segs_per_wave;
+  const int64_t s_stop = min(S, s_begin + segs_per_wave);
+  const int ncol_iter = (vpr + L - 1) >> log_l;
+
+  for (int64_t s = s_begin; s < s_stop; ++s) {
+    const int start = clamp_i(__builtin_amdgcn_readfirstlane(seg_start[s]), 0, E);
+    const int end = clamp_i(__builtin_amdgcn_readfirstlane(seg_end[s]), start, E);
+    for (int ci = 0; ci < ncol_iter; ++ci) {
+      const int vb = vl + ci * L;
+      const bool col_ok = vb < vpr;
+      const int64_t col_off = static_cast<int64_t>(vb) * EPV;
+      A acc[EPV];
+      int first[EPV];
+      int cnt[EPV];
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        acc[i] = OP == GEO_REDUCE_MAX ? -__builtin_inf() : A(0);
+        first[i] = 0x7fffffff;
+        cnt[i] = 0;
+      }
+      for (int e0 = start + g; e0 < end; e0 += R * kUnroll) {
+        V buf[kUnroll];
+        bool ok[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int e = e0 + u * R;
+          int row = e;
+          ok[u] = col_ok && e < end;
+          if (ok[u] && perm) {
+            row = perm[e];
+            ok[u] = static_cast<unsigned>(row) < static_cast<unsigned>(E);
+          }
+          if (ok[u]) buf[u].load(msg + static_cast<int64_t>(row) * C + col_off);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          if (!ok[u]) continue;
+          const int e = e0 + u * R;
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) {
+            const A v = to_acc(buf[u].e[i]);
+            if constexpr (OP == GEO_REDUCE_MAX) {
+              if (max_gt(v, acc[i])) {
+                acc[i] = v; first[i] = e; cnt[i] = 1;
+              } else if (max_eq(v, acc[i])) {
+                cnt[i] += 1;
+                if (cnt[i] == 1) first[i] = e;
+              }
+            } else {
+              acc[i] += v;
+            }
+          }
+        }
+      }
+      // Combine the R lane groups (xor over the lane bits above log_l).
+      for (int m = L; m < kWave; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          const A o = shfl_xor_acc(acc[i], m);
+          if constexpr (OP == GEO_REDUCE_MAX) {
+            const int of = __shfl_xor(first[i], m, kWave);
+            const int oc = __shfl_xor(cnt[i], m, kWave);
+            if (max_gt(o, acc[i])) {
+              acc[i] = o; first[i] = of; cnt[i] = oc;
+            } else if (max_eq(o, acc[i])) {
+              // equal maxima (+-0, NaN payloads): keep the value of the earlier position
+              if (of < first[i]) { acc[i] = o; first[i] = of; }
+              cnt[i] += oc;
+            }
+          } else {
+            acc[i] += o;
+          }
+        }
+      }
+      if (g == 0 && col_ok) {
+        V res;
+        const int n = end - start;
+        if constexpr (OP == GEO_REDUCE_MAX) {
+          IVec<EPV> a;
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) {
+            res.e[i] = cnt[i] == 0 ? from_acc<T>(A(0)) : from_acc<T>(acc[i]);
+            a.e[i] = cnt[i] == 0 ? -1 : ((cnt[i] == 1 || tie_mode == 1) ? first[i] : -cnt[i]);
+          }
+          a.store(arg + s * C + col_off);
+        } else if constexpr (OP == GEO_REDUCE_MEAN) {
+          const A denom = static_cast<A>(n > 1 ? n : 1);
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) res.e[i] = from_acc<T>(acc[i] / denom);
+        } else {
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) res.e[i] = from_acc<T>(acc[i]);
+        }
+        res.store(out + s * C + col_off);
+      }
+    }
+  }
+}
+
+template <typename T, int VB, int OP>
+__global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
+    const T* __restrict__ grad_out, const T* __restrict__ msg, const T* __restrict__ fwd_out,
+    const int32_t* __restrict__ arg, const int32_t* __restrict__ col_sorted,
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ seg_start,
+    const int32_t* __restrict__ seg_end, int32_t E, int64_t S, int64_t C, int vpr, int log_l,
+    int rows_per_wave, T* __restrict__ grad_msg) {
+  using A = typename AccT<T>::type;
+  using V = Vec<T, VB>;
+  constexpr int EPV = V::EPV;
+  const int lane = lane_id();
+  const int L = 1 << log_l;
+  const int R = kWave >> log_l;
+  const int g = lane >> log_l;
+  const int vl = lane & (L - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kSegWaves + (threadIdx.x / kWave);
+  const int64_t e_begin = wave * rows_per_wave;
+  const int64_t e_stop = min(static_cast<int64_t>(E), e_begin + rows_per_wave);
+  const int ncol_iter = (vpr + L - 1) >> log_l;
+
+  for (int64_t e = e_begin + g; e < e_stop; e += R) {
+    const int s = col_sorted[e];
+    int p = perm ? perm[e] : static_cast<int>(e);
+    if (static_cast<unsigned>(p) >= static_cast<unsigned>(E)) continue;  // not a permutation
+    const bool s_ok = static_cast<unsigned>(s) < static_cast<unsigned>(S);
+    A scale = A(1);
+    if constexpr (OP == GEO_REDUCE_MEAN) {
+      if (s_ok) {
+        const int n = seg_end[s] - seg_start[s];
+        scale = static_cast<A>(n > 1 ? n : 1);
+      }
+    }
+    for (int ci = 0; ci < ncol_iter; ++ci) {
+      const int vb = vl + ci * L;
+      if (vb >= vpr) continue;
+      const int64_t col_off = static_cast<int64_t>(vb) * EPV;
+      V gv, res;
+      if (s_ok) {
+        gv.load(grad_out + static_cast<int64_t>(s) * C + col_off);
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) gv.e[i] = from_acc<T>(A(0));
+      }
+      if constexpr (OP == GEO_REDUCE_SUM) {
+        res = gv;
+      } else if constexpr (OP == GEO_REDUCE_MEAN) {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) res.e[i] = from_acc<T>(to_acc(gv.e[i]) / scale);
+      } else {
+        IVec<EPV> a;
+        if (s_ok) {
+          a.load(arg + static_cast<int64_t>(s) * C + col_off);
+        } else {
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) a.e[i] = -1;
+        }
+        bool any_tie = false;
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) any_tie |= a.e[i] <= -2;
+        V mv, ov;
+        if (any_tie) {
+          mv.load(msg + static_cast<int64_t>(p) * C + col_off);
+          ov.load(fwd_out + static_cast<int64_t>(s) * C + col_off);
+        }
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          A r = A(0);
+          if (a.e[i] == static_cast<int>(e)) {
+            r = to_acc(gv.e[i]);
+          } else if (a.e[i] <= -2) {
+            if (max_eq(to_acc(mv.e[i]), to_acc(ov.e[i])))
+              r = to_acc(gv.e[i]) / static_cast<A>(-a.e[i]);
+          }
+          res.e[i] = from_acc<T>(r);
+        }
+      }
+      res.store(grad_msg + static_cast<int64_t>(p) * C + col_off);
+    }
+  }
+}
+
+struct Layout {
+  int vb;      // bytes per lane vector
+  int vpr;     // vectors per row
+  int log_l;   // log2 lanes per row group
+};
+
+Layout choose_layout(int64_t C, int esize, uintptr_t align_bits) {
+  const int64_t row_bytes = C * esize;
+  int vb = 16;
+  while (vb > esize && ((row_bytes % vb) != 0 || (align_bits % vb) != 0)) vb >>= 1;
+  Layout l;
+  l.vb = vb;
+  l.vpr = static_cast<int>(row_bytes / vb);
+  int lanes = 1, lg = 0;
+  while (lanes < l.vpr && lanes < kWave) { lanes <<= 1; ++lg; }
+  l.log_l = lg;
+  return l;
+}
+
+template <typename T, int OP>
+int launch_fwd(const Layout& lay, const T* msg, const int32_t* perm, const int32_t* ns,
+               const int32_t* ne, int32_t E, int64_t S, int64_t C, T* out, int32_t* arg,
+               int tie_mode, hipStream_t st) {
+  int spw = static_cast<int>(ceil_div(S, 32768));
+  if (spw > 64) spw = 64;
+  if (spw < 1) spw = 1;
+  const int64_t waves = ceil_div(S, spw);
+  const int64_t blocks = ceil_div(waves, kSegWaves);
+#define GEO_FWD_CASE(VBV)                                                                   \
+  case VBV:                                                                                 \
+    if constexpr (VBV >= static_cast<int>(sizeof(T))) {                                     \
+      hipLaunchKernelGGL((seg_fwd_kernel<T, VBV, OP>), dim3(blocks), dim3(kSegThreads), 0, st, \
+                         msg, perm, ns, ne, E, S, C, lay.vpr, lay.log_l, spw, out, arg,       \
+                         tie_mode);                                                         \
+    }                                                                                       \
+    break;
+  switch (lay.vb) {
+    GEO_FWD_CASE(16)
+    GEO_FWD_CASE(8)
+    GEO_FWD_CASE(4)
+    GEO_FWD_CASE(2)
+    default:
+      return set_error(GEO_ERR_INVALID, "segment_reduce: unsupported vector width %d", lay.vb);
+  }
+#undef GEO_FWD_CASE
+  GEO_LAUNCH_CHECK("seg_fwd_kernel");
+  return GEO_OK;
+}
+
+template <typename T, int OP>
+int launch_bwd(const Layout& lay, const T* grad_out, const T* msg, const T* fwd_out,
+               const int32_t* arg, const int32_t* cs, const int32_t* perm, const int32_t* ns,
+               const int32_t* ne, int32_t E, int64_t S, int64_t C, T* grad_msg, hipStream_t st) {
+  const int R = kWave >> lay.log_l;
+  int rpw = R * 16;
+  const int64_t waves = ceil_div(E, rpw);
+  const int64_t blocks = ceil_div(waves, kSegWaves);
+#define GEO_BWD_CASE(VBV)                                                                    \
+  case VBV:                                                                                  \
+    if constexpr (VBV >= static_cast<int>(sizeof(T))) {                                      \
+      hipLaunchKernelGGL((seg_bwd_kernel<T, VBV, OP>), dim3(blocks), dim3(kSegThreads), 0, st, \
+                         grad_out, msg, fwd_out, arg, cs, perm, ns, ne, E, S, C, lay.vpr,     \
+                         lay.log_l, rpw, grad_msg);                                          \
+    }                                                                                        \
+    break;
+  switch (lay.vb) {
+    GEO_BWD_CASE(16)
+    GEO_BWD_CASE(8)
+    GEO_BWD_CASE(4)
+    GEO_BWD_CASE(2)
+    default:
+      return set_error(GEO_ERR_INVALID, "segment_reduce: unsupported vector width %d", lay.vb);
+  }
+#undef GEO_BWD_CASE
+  GEO_LAUNCH_CHECK("seg_bwd_kernel");
+  return GEO_OK;
+}
+
+int esize_of(int dtype) { return dtype == GEO_F32 ? 4 : dtype == GEO_BF16 ? 2 : 8; }
+
+}  // namespace
+}  // namespace geo
+
+using namespace geo;
+
+extern "C" int geo_segment_reduce_fwd(int reduce, int dtype, const void* msg, const int32_t* perm,
+                                      const int32_t* node_start, const int32_t* node_end,
+                                      int64_t E, int64_t S, int64_t C, void* out, int32_t* arg,
+                                      int tie_mode, void* stream) {
+  GEO_REQUIRE(reduce >= GEO_REDUCE_SUM && reduce <= GEO_REDUCE_MAX,
+              "segment_reduce: unknown reduce code %d", reduce);
+  GEO_REQUIRE(dtype == GEO_F32 || dtype == GEO_BF16 || dtype == GEO_F64,
+              "segment_reduce: unknown dtype code %d", dtype);
+  GEO_REQUIRE(E >= 0 && S >= 0 && C >= 0, "segment_reduce: negative size (E=%lld S=%lld C=%lld)",
+              (long long)E, (long long)S, (long long)C);
+  GEO_REQUIRE(E < 0x7fffffffLL, "segment_reduce: E=%lld exceeds int32 indexing", (long long)E);
+  if (S == 0 || C == 0) return GEO_OK;
+  GEO_REQUIRE(out != nullptr && node_start != nullptr && node_end != nullptr,
+              "segment_reduce: null output or offsets");
+  GEO_REQUIRE(E == 0 || msg != nullptr, "segment_reduce: null msg with E=%lld", (long long)E);
+  GEO_REQUIRE(reduce != GEO_REDUCE_MAX || arg != nullptr, "segment_reduce: max needs arg");
+  const int es = esize_of(dtype);
+  uintptr_t bits = reinterpret_cast<uintptr_t>(msg) | reinterpret_cast<uintptr_t>(out);
+  Layout lay = choose_layout(C, es, bits);
+  if (reduce == GEO_REDUCE_MAX) {
+    // Narrow the vector until the matching int32 slice of arg is naturally aligned.
+    const uintptr_t abits = reinterpret_cast<uintptr_t>(arg);
+    GEO_REQUIRE(abits % 4 == 0, "segment_reduce: arg must be 4-byte aligned");
+    while (lay.vb > es) {
+      const int ibytes = (lay.vb / es) * 4;
+      const int need = ibytes >= 16 ? 16 : ibytes;
+      if (abits % need == 0) break;
+      lay = choose_layout(C, es, bits | uintptr_t(lay.vb / 2));
+    }
+  }
+  hipStream_t st = as_stream(stream);
+  const int32_t E32 = static_cast<int32_t>(E);
+#define GEO_DISPATCH_FWD(TT)                                                                   \
+  switch (reduce) {                                                                            \
+    case GEO_REDUCE_SUM:                                                                       \
+      return launch_fwd<TT, GEO_REDUCE_SUM>(lay, static_cast<const TT*>(msg), perm, node_start, \
+                                            node_end, E32, S, C, static_cast<TT*>(out), arg,   \
+                                            tie_mode, st);                                     \
+    case GEO_REDUCE_MEAN:                                                                      \
+      return launch_fwd<TT, GEO_REDUCE_MEAN>(lay, static_cast<const TT*>(msg), perm,           \
+                                             node_start, node_end, E32, S, C,                  \
+                                             static_cast<TT*>(out), arg, tie_mode, st);         \
+    default:                                                                                   \
+      return launch_fwd<TT, GEO_REDUCE_MAX>(lay, static_cast<const TT*>(msg), perm, node_start, \
+                                            node_end, E32, S, C, static_cast<TT*>(out), arg,   \
+                                            tie_mode, st);                                     \
+  }
+  if (dtype == GEO_F32) { GEO_DISPATCH_FWD(float) }
+  if (dtype == GEO_BF16) { GEO_DISPATCH_FWD(uint16_t) }
+  GEO_DISPATCH_FWD(double)
+#undef GEO_DISPATCH_FWD
+}
+
+extern "C" int geo_segment_reduce_bwd(int reduce, int dtype, const void* grad_out,
+                                      const void* msg, const void* out, const int32_t* arg,
+                                      const int32_t* col_sorted, const int32_t* perm,
+                                      const int32_t* node_start, const int32_t* node_end,
+                                      int64_t E, int64_t S, int64_t C, void* grad_msg,
+                                      void* stream) {
+  GEO_REQUIRE(reduce >= GEO_REDUCE_SUM && reduce <= GEO_REDUCE_MAX,
+              "segment_reduce_bwd: unknown reduce code %d", reduce);
+  GEO_REQUIRE(dtype == GEO_F32 || dtype == GEO_BF16 || dtype == GEO_F64,
+              "segment_reduce_bwd: unknown dtype code %d", dtype);
+  GEO_REQUIRE(E >= 0 && S >= 0 && C >= 0, "segment_reduce_bwd: negative size");
+  GEO_REQUIRE(E < 0x7fffffffLL, "segment_reduce_bwd: E=%lld exceeds int32 indexing", (long long)E);
+  if (E == 0 || C == 0) return GEO_OK;
+  GEO_REQUIRE(grad_msg != nullptr && col_sorted != nullptr, "segment_reduce_bwd: null pointer");
+  GEO_REQUIRE(S == 0 || grad_out != nullptr, "segment_reduce_bwd: null grad_out");
+  GEO_REQUIRE(reduce != GEO_REDUCE_MEAN || (node_start && node_end),
+              "segment_reduce_bwd: mean needs node_start/node_end");
+  GEO_REQUIRE(reduce != GEO_REDUCE_MAX || (arg && msg && out),
+              "segment_reduce_bwd: max needs arg, msg and out");
+  const int es = esize_of(dtype);
+  uintptr_t bits = reinterpret_cast<uintptr_t>(grad_out) | reinterpret_cast<uintptr_t>(grad_msg);
+  if (reduce == GEO_REDUCE_MAX)
+    bits |= reinterpret_cast<uintptr_t>(msg) | reinterpret_cast<uintptr_t>(out);
+  Layout lay = choose_layout(C, es, bits);
+  if (reduce == GEO_REDUCE_MAX) {
+    // Narrow the vector until the matching int32 slice of arg is naturally aligned.
+    const uintptr_t abits = reinterpret_cast<uintptr_t>(arg);
+    while (lay.vb > es) {
+      const int ibytes = (lay.vb / es) * 4;
+      const int need = ibytes >= 16 ? 16 : ibytes;
+      if (abits % need == 0) break;
+      lay = choose_layout(C, es, bits | uintptr_t(lay.vb / 2));
+    }
+  }
+  hipStream_t st = as_stream(stream);
+  const int32_t E32 = static_cast<int32_t>(E);
+#define GEO_DISPATCH_BWD(TT)                                                                    \
+  switch (reduce) {                                                                             \
+    case GEO_REDUCE_SUM:                                                                        \
+      return launch_bwd<TT, GEO_REDUCE_SUM>(lay, static_cast<const TT*>(grad_out),              \
+                                            static_cast<const TT*>(msg),                        \
+                                            static_cast<const TT*>(out), arg, col_sorted, perm, \
+                                            node_start, node_end, E32, S, C,                    \
+                                            static_cast<TT*>(grad_msg), st);                    \
+    case GEO_REDUCE_MEAN:                                                                       \
+      return launch_bwd<TT, GEO_REDUCE_MEAN>(lay, static_cast<const TT*>(grad_out),             \
+                                             static_cast<const TT*>(msg),                       \
+                                             static_cast<const TT*>(out), arg, col_sorted,      \
+                                             perm, node_start, node_end, E32, S, C,             \
+                                             static_cast<TT*>(grad_msg), st);                   \
+    default:                                                                                    \
+      return launch_bwd<TT, GEO_REDUCE_MAX>(lay, static_cast<const TT*>(grad_out),              \
+                                            static_cast<const TT*>(msg),                        \
+                                            static_cast<const TT*>(out), arg, col_sorted, perm, \
+                                            node_start, node_end, E32, S, C,                    \
+                                            static_cast<TT*>(grad_msg), st);                    \
+  }
+  if (dtype == GEO_F32) { GEO_DISPATCH_BWD(float) }
+  if (dtype == GEO_BF16) { GEO_DISPATCH_BWD(uint16_t) }
+  GEO_DISPATCH_BWD(double)
+#undef GEO_DISPATCH_BWD
+}

@@ -1,0 +1,183 @@
+/*
+ * geo_api.h — C ABI of libgeoembodied_hip.so, the gfx950 (MI355X) implementation of
+ * GeoEmbodied's point-cloud geometry kernels: farthest-point sampling, KNN, radius graph,
+ * CSR build and segment reduce (sum / mean / max, forward and backward).
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers unless the comment says "host".
+ *   - The caller allocates every output and workspace; the library never allocates or frees
+ *     device memory.  Workspace sizes come from the matching *_workspace_bytes() function.
+ *   - All work is enqueued asynchronously on `stream` (a hipStream_t passed as void*; NULL is
+ *     the legacy default stream).  No entry point synchronises the host.
+ *   - Return value: GEO_OK (0) or a GEO_ERR_* code.  geo_last_error() returns a message for the
+ *     last failure on the calling thread (thread-local; valid until the next failing call).
+ *   - No mutable global state: entry points are re-entrant and thread-safe.
+ *   - Index tensors: int64 where the reference's Python API exposes int64, int32 for the CSR
+ *     arrays (the reference's CSR is int32 as well).
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the reference
+ * repository root).
+ */
+#ifndef GEO_API_H
+#define GEO_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEO_OK 0
+#define GEO_ERR_INVALID 1   /* bad argument (shape, size, range, alignment) */
+#define GEO_ERR_HIP 2       /* a HIP runtime call or kernel launch failed */
+#define GEO_ERR_WORKSPACE 3 /* workspace pointer NULL or smaller than required */
+#define GEO_ERR_UNSUPPORTED 4
+
+/* dtype codes for segment reduce */
+#define GEO_F32 0
+#define GEO_BF16 1
+#define GEO_F64 2
+
+/* reduction codes for segment reduce */
+#define GEO_REDUCE_SUM 0
+#define GEO_REDUCE_MEAN 1
+#define GEO_REDUCE_MAX 2
+
+/* ---------------------------------------------------------------- library --- */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* geo_last_error(void);
+/* Build identification: target arch, compiler, flags. */
+const char* geo_build_info(void);
+/* ABI version, bumped on any signature change. */
+int geo_abi_version(void);
+
+/* -------------------------------------------------------------------- FPS --- */
+/*
+ * Replaces fps_cuda (geoembodied/csrc/fps_kernel.cu:160-209, bound at :216-229, dispatched from
+ * geoembodied/csrc/__init__.py:566-597).  Semantics follow the CPU path
+ * _fps_iterative_fallback (geoembodied/csrc/__init__.py:600-654): per cloud b with
+ * n = ptr[b+1]-ptr[b] and k = clamp(k_per_batch[b], 0, n): k == 0 -> nothing; k == n ->
+ * ptr[b] + arange(n); otherwise start at ptr[b] and repeatedly take the lowest index attaining
+ * the max over points of min squared distance to the selected set.  Squared distance is
+ * (fl(dx*dx) + fl(dy*dy)) + fl(dz*dz) in fp32 without contraction.
+ *
+ * Two phases, because the caller allocates the output:
+ *   geo_fps_prepare writes out_ptr[0..B] (exclusive offsets of the clamped k) and
+ *   info[0] = total samples, info[1] = largest cloud size, info[2] = 0 or, when ptr is not a
+ *   valid non-decreasing offset array inside [0, N_total], the 1-based index of the first bad
+ *   entry.  The caller copies info to the host (the one host sync of the op), allocates
+ *   out_idx[info[0]] and calls geo_fps with max_cloud = info[1].
+ */
+int geo_fps_prepare(const int64_t* ptr, const int64_t* k_per_batch, int64_t B, int64_t N_total,
+                    int64_t* out_ptr, int64_t* info, void* stream);
+size_t geo_fps_workspace_bytes(int64_t B, int64_t N_total, int64_t max_cloud);
+int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr, const int64_t* out_ptr,
+            int64_t B, int64_t max_cloud, int64_t* out_idx, void* workspace,
+            size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------------- KNN --- */
+/*
+ * Replaces knn_cuda / knn_self_cuda (geoembodied/csrc/knn_kernel.cu:200-308, bound at
+ * :315-327, dispatched from geoembodied/csrc/__init__.py:376-432).  Semantics follow
+ * _knn_bruteforce (geoembodied/csrc/__init__.py:435-492) with a total order on ties: for each
+ * query of cloud b, out_idx/out_dist[q, 0..k) are the first k sources of cloud b (global
+ * indices) sorted ascending by the key (d, j), d = squared distance with dx = q.x - s.x.
+ * Rows with fewer than k sources are padded with -1 / 1e30f.  ptr_q and ptr_s both have B+1
+ * entries.  query may alias source (knn_self).
+ */
+size_t geo_knn_workspace_bytes(int64_t Nq, int64_t Ns, int64_t B, int64_t k);
+int geo_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
+            const int64_t* ptr_q, const int64_t* ptr_s, int64_t B, int64_t k,
+            int64_t* out_idx, float* out_dist, void* workspace, size_t workspace_bytes,
+            void* stream);
+
+/* ----------------------------------------------------------- radius graph --- */
+/*
+ * Replaces radius_graph_cuda and radius_graph_cuda_batched
+ * (geoembodied/csrc/radius_graph_kernel.cu:253-467, bound at :474-490, dispatched from
+ * geoembodied/csrc/__init__.py:130-186 and geoembodied/functional/radius_graph.py:19-105).
+ * Semantics follow the CPU path _radius_graph_batched/_single
+ * (geoembodied/functional/radius_graph.py:204-335) with exact distances: edge j -> i exists iff
+ * i and j are in the same cloud, both unmasked, (loop or i != j) and d(i,j) < r2, keeping per
+ * target i the first K = max_num_neighbors sources by key (d, j).  r2 is the fp32 threshold the
+ * caller computed as fl32(fl64(r) * fl64(r)) and r_cell = r (the grid cell edge is derived from
+ * it).
+ *
+ * Cloud membership: batch[i] (values outside [0, B) are treated as masked) when batch != NULL,
+ * otherwise contiguous chunks of points_per_cloud points (B * points_per_cloud == N).
+ * mask may be NULL (all valid); nonzero bytes mark valid points.
+ *
+ * Two phases sharing one workspace:
+ *   geo_radius_count builds the per-cloud uniform grid and writes row_ptr[0..N] (CSR offsets of
+ *   the edges grouped by target, row_ptr[N] = E).  The caller reads E (the one host sync),
+ *   allocates row_out[E], col_out[E] and calls geo_radius_emit with the same arguments and
+ *   workspace.  Output order: targets ascending, sources ascending within a target.
+ */
+size_t geo_radius_workspace_bytes(int64_t N, int64_t B);
+int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                     int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
+                     int64_t max_num_neighbors, int loop, int64_t* row_ptr, void* workspace,
+                     size_t workspace_bytes, void* stream);
+int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                    int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
+                    int64_t max_num_neighbors, int loop, const int64_t* row_ptr,
+                    int64_t* row_out, int64_t* col_out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* -------------------------------------------------------------- CSR build --- */
+/*
+ * Replaces sort_and_build_csr (geoembodied/csrc/segment_reduce_kernel.cu:100-169, bound at
+ * :217-221, dispatched from geoembodied/csrc/__init__.py:261-277 and
+ * geoembodied/functional/segment_reduce.py:41-109).  Stable sort of col[E] (int64 targets)
+ * by target: col_sorted[e] = col[perm[e]], perm ascending within each target.  node_start /
+ * node_end[N] are the CSR ranges (empty targets get start == end).  Targets outside [0, N)
+ * sort after every valid target and belong to no segment.
+ */
+size_t geo_csr_workspace_bytes(int64_t E, int64_t N);
+int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
+                  int32_t* perm, int32_t* node_start, int32_t* node_end, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------- segment reduce --- */
+/*
+ * Forward.  Replaces segment_reduce_sum (geoembodied/csrc/segment_reduce_kernel.cu:176-210,
+ * bound at :222-228, dispatched from geoembodied/csrc/__init__.py:280-302 and the custom op
+ * geoembodied/functional/segment_reduce.py:223-238) and adds mean and max, whose semantics
+ * follow global_mean_pool (geoembodied/nn/modules/se3_net.py:226-270: sum / max(count, 1)) and
+ * scatter_reduce 'amax' with include_self=False on zeros
+ * (geoembodied/nn/modules/invariant_attention.py:212-219: empty segment -> 0).
+ *
+ *   out[s, c] = reduce over e in [node_start[s], node_end[s]) of msg[perm[e], c]
+ *
+ * msg is [E, C] row-major of `dtype`; perm may be NULL (identity).  Sum and mean accumulate in
+ * fp32 (fp64 for GEO_F64) and round once to dtype.  For GEO_REDUCE_MAX, arg[S, C] (int32) is
+ * required and receives the sorted position e of the lowest-position maximum when it is
+ * unique, -1 for an empty segment and -(tie count) when tie_mode == 0 and the maximum is
+ * attained more than once (tie_mode == 1 always stores the lowest position).
+ */
+int geo_segment_reduce_fwd(int reduce, int dtype, const void* msg, const int32_t* perm,
+                           const int32_t* node_start, const int32_t* node_end, int64_t E,
+                           int64_t S, int64_t C, void* out, int32_t* arg, int tie_mode,
+                           void* stream);
+
+/*
+ * Backward.  Replaces the autograd backward of the reference custom op
+ * (geoembodied/functional/segment_reduce.py:259-270: grad_msg[perm[e]] = grad_out[col_sorted[e]])
+ * and adds mean (grad / max(count, 1)) and max.  Max routes grad_out[s, c] to the recorded
+ * argmax; with tie_mode 0 and -(count) recorded it splits grad_out[s, c] evenly over every
+ * position whose msg value equals out[s, c] (PyTorch scatter_reduce 'amax' semantics), which
+ * needs msg and out; otherwise msg and out may be NULL.  Every row of grad_msg is written.
+ */
+int geo_segment_reduce_bwd(int reduce, int dtype, const void* grad_out, const void* msg,
+                           const void* out, const int32_t* arg, const int32_t* col_sorted,
+                           const int32_t* perm, const int32_t* node_start,
+                           const int32_t* node_end, int64_t E, int64_t S, int64_t C,
+                           void* grad_msg, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GEO_API_H */

@@ -1,0 +1,307 @@
+"""GPU parity: FPS, KNN and radius graph vs the oracle — bit-exact indices, distances and edge
+sets (ties toward the lower index) — at small sizes, on tie-heavy integer lattices and on the
+five BASELINE configurations.  Also restates the reference's own tests
+(tests/test_fps_cuda_remote.py:63-202, tests/test_radius_graph_cuda.py:69-232,
+tests/test_phase1.py:258-298).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _f():
+    import geoembodied  # noqa: F401
+    from geoembodied.functional import fps, knn, radius_graph
+    return fps.farthest_point_sampling, knn.knn, knn.knn_self, radius_graph.radius_graph
+
+
+def _lattice(n_side, seed=0, jitter=False):
+    g = np.stack(np.meshgrid(*[np.arange(n_side)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    rng = np.random.default_rng(seed)
+    g = g[rng.permutation(len(g))].astype(np.float32)
+    return torch.from_numpy(g)
+
+
+def _ptr(sizes):
+    p = np.zeros(len(sizes) + 1, dtype=np.int64)
+    p[1:] = np.cumsum(sizes)
+    return torch.from_numpy(p)
+
+
+# ----------------------------------------------------------------------------------- FPS ---
+
+def _fps_check(dev, pos, ptr, k):
+    from gdl_amd.csrc import fps_cuda
+    got = fps_cuda(pos.to(dev), ptr.to(dev), k.to(dev)).cpu().numpy()
+    want = oracle.fps(pos.numpy(), ptr.numpy(), k.numpy())
+    np.testing.assert_array_equal(got, want)
+    return got
+
+
+@pytest.mark.parametrize("sizes,ks,seed", [
+    ([100], [10], 0), ([60, 40], [15, 10], 1), ([1000, 1000], [250, 250], 42),
+    ([2048, 1024, 4096, 512], [512, 256, 1024, 128], 3), ([1, 2, 3, 300], [1, 2, 5, 0], 4),
+    ([257, 511, 1025, 3000], [257, 100, 1024, 2999], 5), ([9000], [300], 6),
+    ([16384, 100], [500, 50], 7), ([20000, 5000], [200, 100], 8),
+])
+def test_fps_vs_oracle(dev, sizes, ks, seed):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randn(sum(sizes), 3, generator=g)
+    _fps_check(dev, pos, _ptr(sizes), torch.tensor(ks))
+
+
+def test_fps_tie_lattice(dev):
+    pos = _lattice(8)  # 512 integer points: exact distances, many ties
+    _fps_check(dev, pos, _ptr([512]), torch.tensor([200]))
+    pos2 = torch.cat([_lattice(6, 1), _lattice(7, 2)])
+    _fps_check(dev, pos2, _ptr([216, 343]), torch.tensor([216, 100]))
+
+
+def test_fps_reference_kat(dev):
+    """tests/test_fps_cuda_remote.py:63-90: 25 int64 indices, batch isolation, no duplicates."""
+    from gdl_amd.csrc import fps_cuda
+    pos = torch.randn(100, 3, device=dev)
+    idx = fps_cuda(pos, torch.tensor([0, 60, 100], device=dev), torch.tensor([15, 10], device=dev))
+    assert idx.shape == (25,) and idx.dtype == torch.int64 and idx.is_cuda
+    assert (idx[:15] < 60).all() and (idx[15:] >= 60).all()
+    assert idx.unique().numel() == 25
+
+
+def test_fps_spread_beats_random(dev):
+    """tests/test_fps_cuda_remote.py:141-167."""
+    fps, *_ = _f()
+    torch.manual_seed(0)
+    pos = torch.randn(4096, 3, device=dev)
+    sel = pos[fps(pos, 256)]
+    rnd = np.mean([torch.cdist(p, p).mean().item()
+                   for p in (pos[torch.randperm(4096, device=dev)[:256]] for _ in range(10))])
+    assert torch.cdist(sel, sel).mean().item() > rnd
+
+
+def test_fps_api_variants(dev):
+    fps, *_ = _f()
+    g = torch.Generator().manual_seed(9)
+    pos = torch.randn(300, 3, generator=g)
+    d = pos.to(dev)
+    assert torch.equal(fps(d, 500).cpu(), torch.arange(300))
+    np.testing.assert_array_equal(fps(d, 40).cpu().numpy(), oracle.fps(pos.numpy(), [0, 300], [40]))
+    ptr = torch.tensor([0, 100, 300])
+    np.testing.assert_array_equal(fps(d, 30, ptr=ptr.to(dev)).cpu().numpy(),
+                                  oracle.fps(pos.numpy(), ptr.numpy(), [30, 30]))
+    # legacy batch vector, clouds interleaved: cloud b is the points with batch == b in order
+    batch = torch.from_numpy(np.random.default_rng(0).integers(0, 3, 300))
+    got = fps(d, 25, batch=batch.to(dev)).cpu().numpy()
+    want = []
+    for b in range(3):
+        members = np.nonzero(batch.numpy() == b)[0]
+        loc = oracle.fps(pos.numpy()[members], [0, len(members)], [min(25, len(members))])
+        want.append(members[loc])
+    np.testing.assert_array_equal(got, np.concatenate(want))
+
+
+def test_fps_invalid_ptr_raises(dev):
+    from gdl_amd.csrc import fps_cuda
+    pos = torch.randn(10, 3, device=dev)
+    with pytest.raises(ValueError):
+        fps_cuda(pos, torch.tensor([0, 8, 5], device=dev), torch.tensor([2, 2], device=dev))
+    with pytest.raises(ValueError):
+        fps_cuda(pos, torch.tensor([0, 11], device=dev), torch.tensor([2], device=dev))
+
+
+# ----------------------------------------------------------------------------------- KNN ---
+
+def _knn_check(dev, q, s, pq, ps, k):
+    _, knn, _, _ = _f()
+    gi, gd = knn(q.to(dev), s.to(dev), pq.to(dev), ps.to(dev), k)
+    wi, wd = oracle.knn(q.numpy(), s.numpy(), pq.numpy(), ps.numpy(), k)
+    np.testing.assert_array_equal(gi.cpu().numpy(), wi)
+    np.testing.assert_array_equal(gd.cpu().numpy().view(np.uint32), wd.view(np.uint32))
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 8, 9, 16, 17, 33, 64, 100, 128])
+def test_knn_vs_oracle(dev, k):
+    g = torch.Generator().manual_seed(k)
+    qs, ss = [30, 0, 200, 77, 5], [50, 10, 1500, 0, 3]
+    q = torch.randn(sum(qs), 3, generator=g)
+    s = torch.randn(sum(ss), 3, generator=g)
+    _knn_check(dev, q, s, _ptr(qs), _ptr(ss), k)
+
+
+def test_knn_lattice_ties(dev):
+    s = _lattice(7)
+    q = _lattice(4, 3) + 0.5 * (torch.arange(64).reshape(-1, 1) % 2)  # some half-integer queries
+    _knn_check(dev, q, s, _ptr([64]), _ptr([343]), 27)
+    _, _, knn_self, _ = _f()
+    idx, d = knn_self(s.to(dev), _ptr([343]).to(dev), 7)
+    assert torch.equal(idx[:, 0].cpu(), torch.arange(343)) and (d[:, 0] == 0).all()
+
+
+def test_knn_bad_args(dev):
+    _, knn, _, _ = _f()
+    x = torch.randn(5, 3, device=dev)
+    with pytest.raises(ValueError):
+        knn(x, x, torch.tensor([0, 5], device=dev), torch.tensor([0, 2, 5], device=dev), 2)
+    with pytest.raises(RuntimeError):
+        knn(x, x, torch.tensor([0, 5], device=dev), torch.tensor([0, 5], device=dev), 129)
+
+
+# -------------------------------------------------------------------------- radius graph ---
+
+def _rg_check(dev, x, r, K=32, loop=False, mask=None, batch=None, nb=None):
+    *_, rg = _f()
+    row, col = rg(x.to(dev), r, max_num_neighbors=K, loop=loop,
+                  mask=None if mask is None else mask.to(dev),
+                  batch=None if batch is None else batch.to(dev), num_batch_elements=nb)
+    wr, wc = oracle.radius_graph(x.numpy(), r, K, loop,
+                                 mask=None if mask is None else mask.numpy(),
+                                 batch=None if batch is None else batch.numpy(),
+                                 num_batch_elements=nb)
+    assert row.dtype == torch.int64 and col.dtype == torch.int64
+    np.testing.assert_array_equal(col.cpu().numpy(), wc)
+    np.testing.assert_array_equal(row.cpu().numpy(), wr)
+    return row, col
+
+
+@pytest.mark.parametrize("N,r", [(50, 0.5), (100, 0.3), (200, 0.2), (500, 0.15), (1000, 0.1)])
+@pytest.mark.parametrize("K", [4, 16, 300])
+def test_radius_vs_oracle(dev, N, r, K):
+    torch.manual_seed(42)
+    x = torch.randn(N, 3)
+    _rg_check(dev, x, r * 4, K)   # dense: K caps bind (selection path)
+    _rg_check(dev, x, r, K)
+
+
+def test_radius_lattice_boundary(dev):
+    """Integer lattice, r = 1: neighbours at distance exactly 1 are excluded (d < r2)."""
+    x = _lattice(6)
+    r, c = _rg_check(dev, x, 1.0, 32)
+    assert r.numel() == 0
+    r, c = _rg_check(dev, x, 1.5, 32)     # 6-neighbourhood
+    r, c = _rg_check(dev, x, 1.5, 3)      # ties at d = 1 broken toward lower index
+    r, c = _rg_check(dev, x, 2.0, 100, loop=True)
+
+
+def test_radius_masks_batches(dev):
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(600, 3, generator=g)
+    mask = torch.rand(600, generator=g) > 0.3
+    batch = torch.randint(0, 5, (600,), generator=g)          # unsorted cloud ids
+    _rg_check(dev, x, 0.6, 16, mask=mask)
+    _rg_check(dev, x, 0.6, 16, batch=batch)
+    _rg_check(dev, x, 0.6, 16, batch=batch, mask=mask, loop=True)
+    _rg_check(dev, x, 0.6, 16, nb=4)                          # contiguous equal chunks
+    _rg_check(dev, x, 0.6, 16, batch=batch.sort().values, nb=5)
+
+
+def test_radius_reference_kats(dev):
+    """tests/test_phase1.py:258-298 and tests/test_radius_graph_cuda.py:105-192."""
+    *_, rg = _f()
+    x = torch.tensor([[0.0, 0, 0], [0.1, 0, 0], [10.0, 0, 0]], device=dev)
+    row, col = rg(x, r=1.0)
+    assert row.numel() == 2 and 2 not in row.tolist() and 2 not in col.tolist()
+    xr = torch.randn(20, 3, device=dev)
+    row, col = rg(xr, r=100.0)
+    assert not (row == col).any() and row.numel() == 20 * 19
+    row, col = rg(torch.tensor([[0.0, 0, 0], [0.1, 0, 0]], device=dev), r=100.0,
+                  batch=torch.tensor([0, 1], device=dev))
+    assert row.numel() == 0
+    assert rg(torch.randn(20, 3, device=dev) * 10, r=0.001)[0].numel() == 0
+    m = torch.ones(200, dtype=torch.bool, device=dev)
+    m[150:] = False
+    row, col = rg(torch.randn(200, 3, device=dev), 0.4, max_num_neighbors=16, mask=m)
+    assert (row < 150).all() and (col < 150).all()
+    assert rg(torch.randn(100, 3, device=dev), 1.0, mask=torch.zeros(100, dtype=torch.bool,
+                                                                     device=dev))[0].numel() == 0
+    row, col = rg(torch.randn(50, 3, device=dev), 10.0, max_num_neighbors=64, loop=True)
+    assert (row == col).sum() == 50
+    assert rg(torch.randn(1, 3, device=dev), 1.0)[0].numel() == 0
+    assert rg(torch.tensor([[0.0, 0, 0], [100.0, 0, 0]], device=dev), 1.0)[0].numel() == 0
+    assert rg(torch.tensor([[0.0, 0, 0], [0.1, 0, 0]], device=dev), 0.5)[0].numel() == 2
+    assert rg(torch.randn(100, 3, device=dev), 0.0)[0].numel() == 0
+    from geoembodied.functional.radius_graph import compute_edge_vectors
+    diff, dist, direction = compute_edge_vectors(torch.tensor([[0.0, 0, 0], [3.0, 4, 0]], device=dev),
+                                                 torch.tensor([0], device=dev),
+                                                 torch.tensor([1], device=dev))
+    assert torch.allclose(dist.cpu(), torch.tensor([5.0]))
+    assert torch.allclose(direction.cpu(), torch.tensor([[0.6, 0.8, 0.0]]))
+    from geoembodied.csrc import get_radius_graph_backend
+    assert get_radius_graph_backend() == "cuda"
+
+
+@pytest.mark.parametrize("N", [10000, 50000])
+def test_radius_large(dev, N):
+    torch.manual_seed(N)
+    x = torch.randn(N, 3) * 0.5
+    _rg_check(dev, x, 0.05, 32)
+
+
+def test_radius_degenerate_extent(dev):
+    """All points on a line far longer than r: the per-axis cell cap grows the cells."""
+    t = torch.linspace(0, 1000, 5000)
+    x = torch.stack([t, torch.zeros_like(t), torch.zeros_like(t)], 1)
+    _rg_check(dev, x, 0.5, 8)
+    x2 = torch.zeros(300, 3)   # all coincident
+    _rg_check(dev, x2, 0.1, 7)
+    _rg_check(dev, x2, 0.1, 400, loop=True)
+
+
+# ------------------------------------------------------------------------ BASELINE configs ---
+
+def test_config_c1(dev):
+    import bench
+    fps, _, _, rg = _f()
+    c = bench.make_c1()
+    idx = fps(c["pos"].to(dev), c["M"]).cpu().numpy()
+    np.testing.assert_array_equal(idx, oracle.fps(c["pos"].numpy(), [0, 2048], [512]))
+    cen = c["pos"][torch.from_numpy(idx)]
+    _rg_check(dev, cen, c["r"], c["K"])
+
+
+def test_config_c2(dev):
+    import bench
+    fps, knn, _, rg = _f()
+    c = bench.make_c2()
+    pos, ptr = c["pos"], c["ptr"]
+    idx = fps(pos.to(dev), c["M"], ptr=ptr.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(idx, oracle.fps(pos.numpy(), ptr.numpy(), [c["M"]] * c["B"]))
+    row, col = _rg_check(dev, pos, c["r"], c["K"], batch=c["batch"], nb=c["B"])
+    assert row.numel() > 600000
+    cen = pos[torch.from_numpy(idx)]
+    pq = torch.arange(c["B"] + 1) * c["M"]
+    _knn_check(dev, cen, pos, pq, ptr, c["k"])
+    _rg_check(dev, cen, c["r"], c["K"], nb=c["B"])
+
+
+def test_config_c4(dev):
+    import bench
+    fps, _, _, rg = _f()
+    c = bench.make_c4()
+    pos, ptr = c["pos"], c["ptr"]
+    i1 = fps(pos.to(dev), 512, ptr=ptr.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(i1, oracle.fps(pos.numpy(), ptr.numpy(), [512] * c["B"]))
+    q1 = pos[torch.from_numpy(i1)]
+    p1 = torch.arange(c["B"] + 1) * 512
+    i2 = fps(q1.to(dev), 128, ptr=p1.to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(i2, oracle.fps(q1.numpy(), p1.numpy(), [128] * c["B"]))
+    q2 = q1[torch.from_numpy(i2)]
+    _rg_check(dev, q1, 0.2, 64, nb=c["B"])
+    _rg_check(dev, q2, 0.4, 64, nb=c["B"])
+
+
+def test_config_c5(dev):
+    import bench
+    fps, knn, _, rg = _f()
+    c = bench.make_c5()
+    pos = c["pos"]
+    N = pos.shape[0]
+    idx = fps(pos.to(dev), c["M"]).cpu().numpy()
+    np.testing.assert_array_equal(idx, oracle.fps(pos.numpy(), [0, N], [c["M"]]))
+    cen = pos[torch.from_numpy(idx)]
+    _rg_check(dev, cen, c["r"], c["K"])
+    sub = cen[:2048]   # oracle KNN on a 2048-query sample against all 131072 sources
+    _knn_check(dev, sub, pos, torch.tensor([0, 2048]), torch.tensor([0, N]), c["k"])

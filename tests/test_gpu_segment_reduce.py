@@ -1,0 +1,293 @@
+"""GPU parity: CSR build and segment sum / mean / max (forward and backward) vs the oracle.
+
+Bars: CSR arrays, segment max values + argmax records and every backward value bit-exact;
+sum / mean within 1e-5 * sum|msg| (fp32), 2e-2 * sum|msg| (bf16), 1e-12 * sum|msg| (fp64)
+per element.  Also restates the reference's own segment-reduce tests
+(tests/test_segment_reduce.py:34-159).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float64: 1e-12}
+NP_DT = {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float64: "float64"}
+
+
+def _ops():
+    import geoembodied  # noqa: F401
+    from geoembodied.functional.segment_reduce import segment_reduce, sort_and_build_csr
+    return segment_reduce, sort_and_build_csr
+
+
+def _problem(E, N, C, dtype, seed, ties=False, sorted_col=False):
+    g = torch.Generator().manual_seed(seed)
+    col = torch.randint(0, max(N, 1), (E,), generator=g)
+    if sorted_col:
+        col = col.sort().values
+    msg = torch.randn(E, C, generator=g, dtype=torch.float64)
+    if ties:
+        msg = (msg * 2).round() / 2  # few distinct values -> many tied maxima
+    return col, msg.to(dtype)
+
+
+def _np(t):
+    return t.detach().cpu().float().numpy() if t.dtype == torch.bfloat16 else t.detach().cpu().numpy()
+
+
+# ----------------------------------------------------------------------------- CSR build ---
+
+@pytest.mark.parametrize("E,N,seed", [(1, 1, 0), (1000, 10, 1), (5000, 300, 2), (70000, 70000, 3),
+                                      (200000, 5000, 4), (300000, 20_000_000, 5)])
+def test_csr_matches_oracle(dev, E, N, seed):
+    _, csr = _ops()
+    g = torch.Generator().manual_seed(seed)
+    col = torch.randint(0, N, (E,), generator=g)
+    if E > 10:
+        col[::97] = -3          # out-of-range targets sort last
+        col[5::101] = N + 7
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    r = oracle.sort_and_build_csr(col.numpy(), N)
+    for got, want, name in zip((cs, pm, ns, ne), r, ("col_sorted", "perm", "node_start", "node_end")):
+        assert got.dtype == torch.int32, name
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
+
+
+def test_csr_empty(dev):
+    _, csr = _ops()
+    cs, pm, ns, ne = csr(torch.empty(0, dtype=torch.long, device=dev), 7)
+    assert cs.numel() == 0 and pm.numel() == 0
+    assert ns.tolist() == [0] * 7 and ne.tolist() == [0] * 7
+
+
+# ------------------------------------------------------------------------- forward / bwd ---
+
+CASES = [
+    # E, N, C, dtype
+    (3000, 500, 32, torch.float32),
+    (4000, 300, 1, torch.float32),
+    (4000, 300, 3, torch.float32),
+    (5000, 700, 112, torch.float32),
+    (5000, 256, 128, torch.float32),
+    (3000, 200, 300, torch.float32),
+    (5000, 700, 128, torch.bfloat16),
+    (4000, 300, 7, torch.bfloat16),
+    (3000, 400, 64, torch.float64),
+    (2000, 100, 5, torch.float64),
+]
+
+
+@pytest.mark.parametrize("E,N,C,dtype", CASES)
+@pytest.mark.parametrize("reduce", ["sum", "mean", "max"])
+def test_forward_backward_vs_oracle(dev, E, N, C, dtype, reduce):
+    seg, csr = _ops()
+    col, msg = _problem(E, N, C, dtype, seed=E + C, ties=reduce == "max")
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    m = msg.to(dev).requires_grad_(True)
+    out = seg(m, cs, pm, ns, ne, N, reduce=reduce)
+    assert out.shape == (N, C) and out.dtype == dtype
+    ref, aux = oracle.segment_reduce_fwd(_np(msg), pm.cpu().numpy(), ns.cpu().numpy(),
+                                         ne.cpu().numpy(), N, reduce)
+    got = _np(out).astype(np.float64)
+    if reduce == "max":
+        np.testing.assert_array_equal(got, ref)
+    else:
+        bound = TOL[dtype] * aux + 1e-30
+        if dtype == torch.bfloat16:
+            bound = bound + np.abs(ref) * 2.0 ** -8  # final rounding to bf16
+        assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) - bound))
+    grad = torch.randn(N, C, generator=torch.Generator().manual_seed(7), dtype=torch.float64).to(dtype)
+    out.backward(grad.to(dev))
+    from gdl_amd.csrc import segment_reduce_forward_hip
+    arg = None
+    if reduce == "max":
+        _, arg_t = segment_reduce_forward_hip(msg.to(dev), pm, ns, ne, N, "max")
+        np.testing.assert_array_equal(arg_t.cpu().numpy(), aux)
+        arg = aux
+    want = oracle.segment_reduce_bwd(_np(grad), cs.cpu().numpy(), pm.cpu().numpy(),
+                                     ns.cpu().numpy(), ne.cpu().numpy(), E, reduce,
+                                     msg=_np(msg), out=ref, arg=arg, dtype=NP_DT[dtype])
+    np.testing.assert_array_equal(_np(m.grad).astype(np.float64), want)
+
+
+def test_max_first_mode_and_identity_perm(dev):
+    seg, _ = _ops()
+    from gdl_amd.csrc import segment_reduce_forward_hip
+    E, N, C = 3000, 200, 16
+    col, msg = _problem(E, N, C, torch.float32, 11, ties=True, sorted_col=True)
+    counts = torch.bincount(col, minlength=N)
+    ne = counts.cumsum(0).int()
+    ns = ne - counts.int()
+    perm = torch.arange(E, dtype=torch.int32)
+    out, arg = segment_reduce_forward_hip(msg.to(dev), None, ns.to(dev), ne.to(dev), N, "max", 1)
+    ref, aux = oracle.segment_reduce_fwd(msg.numpy(), perm.numpy(), ns.numpy(), ne.numpy(), N, "max",
+                                         tie_mode=1)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    np.testing.assert_array_equal(arg.cpu().numpy(), aux)
+    m = msg.to(dev).requires_grad_(True)
+    o = seg(m, col.int().to(dev), perm.to(dev), ns.to(dev), ne.to(dev), N, reduce="max", max_ties="first")
+    o.sum().backward()
+    g = m.grad.cpu()
+    # each non-empty (segment, channel) routes exactly one unit of gradient
+    assert g.sum().item() == float((counts > 0).sum().item() * C)
+
+
+def test_empty_segments_and_special_values(dev):
+    seg, csr = _ops()
+    N, C = 6, 4
+    col = torch.tensor([1, 1, 3, 3, 3])
+    msg = torch.tensor([[-0.0, 1.0, float("nan"), -float("inf")],
+                        [0.0, 1.0, 2.0, -float("inf")],
+                        [5.0, -1.0, 2.0, 3.0],
+                        [5.0, -2.0, float("nan"), 3.0],
+                        [4.0, -1.0, 1.0, 3.0]])
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    for red in ("sum", "mean", "max"):
+        out = seg(msg.to(dev), cs, pm, ns, ne, N, reduce=red).cpu()
+        assert torch.all(out[[0, 2, 4, 5]] == 0), red
+    out = seg(msg.to(dev), cs, pm, ns, ne, N, reduce="max").cpu()
+    ref, _ = oracle.segment_reduce_fwd(msg.numpy(), pm.cpu().numpy(), ns.cpu().numpy(),
+                                       ne.cpu().numpy(), N, "max")
+    np.testing.assert_array_equal(out.numpy().view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
+# ----------------------------------------------- reference tests restated (test_segment_reduce) ---
+
+def test_matches_scatter_add(dev):
+    seg, csr = _ops()
+    torch.manual_seed(42)
+    N, E, C = 500, 3000, 32
+    col = torch.randint(0, N, (E,), device=dev)
+    msg = torch.randn(E, C, device=dev)
+    ref = torch.zeros(N, C, device=dev).scatter_add_(0, col.unsqueeze(-1).expand(E, C), msg)
+    out = seg(msg, *csr(col, N), N)
+    assert torch.allclose(out, ref, atol=1e-5)
+
+
+def test_bit_exact_determinism(dev):
+    seg, csr = _ops()
+    torch.manual_seed(0)
+    N, E, C = 100, 500, 8
+    col = torch.randint(0, N, (E,), device=dev)
+    msg = torch.randn(E, C, device=dev)
+    args = csr(col, N)
+    ref = seg(msg, *args, N)
+    for _ in range(19):
+        assert torch.equal(seg(msg, *args, N), ref)
+
+
+def test_backward_ones(dev):
+    seg, csr = _ops()
+    torch.manual_seed(42)
+    N, E, C = 50, 200, 8
+    col = torch.randint(0, N, (E,), device=dev)
+    msg = torch.randn(E, C, device=dev, requires_grad=True)
+    seg(msg, *csr(col, N), N).sum().backward()
+    assert torch.equal(msg.grad, torch.ones_like(msg))
+
+
+@pytest.mark.parametrize("reduce", ["sum", "mean", "max"])
+def test_gradcheck_fp64(dev, reduce):
+    seg, csr = _ops()
+    torch.manual_seed(3)
+    N, E, C = 10, 30, 4
+    col = torch.randint(0, N, (E,), device=dev)
+    args = csr(col, N)
+    msg = torch.randn(E, C, device=dev, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda m: seg(m, *args, N, reduce=reduce), (msg,), atol=1e-6)
+
+
+def test_empty_edges(dev):
+    seg, csr = _ops()
+    N, C = 10, 8
+    out = seg(torch.empty(0, C, device=dev), *csr(torch.empty(0, dtype=torch.long, device=dev), N), N)
+    assert out.shape == (N, C) and out.abs().sum() == 0
+
+
+def test_single_node(dev):
+    seg, csr = _ops()
+    E, C = 10, 4
+    out = seg(torch.ones(E, C, device=dev), *csr(torch.zeros(E, dtype=torch.long, device=dev), 1), 1)
+    assert torch.equal(out, torch.full((1, C), float(E), device=dev))
+
+
+@pytest.mark.parametrize("C", [1, 16, 32, 64])
+def test_channel_widths(dev, C):
+    seg, csr = _ops()
+    torch.manual_seed(C)
+    N, E = 30, 150
+    col = torch.randint(0, N, (E,), device=dev)
+    msg = torch.randn(E, C, device=dev)
+    ref = torch.zeros(N, C, device=dev).scatter_add_(0, col.unsqueeze(-1).expand(E, C), msg)
+    assert torch.allclose(seg(msg, *csr(col, N), N), ref, atol=1e-4)
+
+
+def test_mean_and_max_match_reference_call_sites(dev):
+    """mean == global_mean_pool (scatter_add / bincount.clamp(1)); max == scatter_reduce amax
+    with include_self=False on zeros; both with fp32 inputs (nn/modules/se3_net.py:226-270,
+    nn/modules/invariant_attention.py:212-219)."""
+    seg, csr = _ops()
+    torch.manual_seed(5)
+    N, E, C = 64, 900, 24
+    col = torch.randint(0, N - 4, (E,), device=dev)  # last 4 targets empty
+    msg = torch.randn(E, C, device=dev)
+    args = csr(col, N)
+    s = torch.zeros(N, C, device=dev).scatter_add_(0, col.unsqueeze(1).expand(E, C), msg)
+    mean_ref = s / torch.bincount(col, minlength=N).clamp(min=1).unsqueeze(1)
+    assert torch.allclose(seg(msg, *args, N, reduce="mean"), mean_ref, atol=1e-5)
+    mx_ref = torch.zeros(N, C, device=dev).scatter_reduce_(0, col.unsqueeze(1).expand(E, C), msg,
+                                                           reduce="amax", include_self=False)
+    assert torch.equal(seg(msg, *args, N, reduce="max"), mx_ref)
+    # gradient of max with ties split evenly, as scatter_reduce's backward.  Values sit on a
+    # 0.5 grid offset by 0.25 so that no segment maximum is exactly 0: for such segments
+    # PyTorch's backward also counts the zero-initialised output as a tie (grad / (count + 1)),
+    # which this implementation deliberately does not reproduce.
+    mt = ((msg * 2).round() / 2 + 0.25).requires_grad_(True)
+    mr = mt.detach().clone().requires_grad_(True)
+    g = torch.randn(N, C, device=dev)
+    seg(mt, *args, N, reduce="max").backward(g)
+    torch.zeros(N, C, device=dev).scatter_reduce(0, col.unsqueeze(1).expand(E, C), mr,
+                                                 reduce="amax", include_self=False).backward(g)
+    assert torch.allclose(mt.grad, mr.grad, atol=1e-6)
+
+
+# ------------------------------------------------------------------- full-size C3 properties ---
+
+def test_c3_full_size(dev):
+    """C3 at full size: oracle on a sample of segments, linearity and total-sum checks on all."""
+    import bench
+    seg, _ = _ops()
+    off = bench.make_c3_offsets()
+    S, E, C = off.shape[0] - 1, int(off[-1]), 128
+    ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
+    ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
+    cs = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32), (ne - ns).long())
+    perm = torch.arange(E, device=dev, dtype=torch.int32)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    msg = torch.randn(E, C, device=dev, generator=gen)
+    out = seg(msg, cs, perm, ns, ne, S)
+    # sampled oracle comparison
+    sample = np.random.default_rng(3).choice(S, 2000, replace=False)
+    rows = np.concatenate([np.arange(off[s], off[s + 1]) for s in sample])
+    sub = msg[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    loc = np.zeros(len(sample) + 1, dtype=np.int64)
+    loc[1:] = np.cumsum(off[sample + 1] - off[sample])
+    ref, scale = oracle.segment_reduce_fwd(sub, None, loc[:-1], loc[1:], len(sample), "sum")
+    got = out[torch.from_numpy(sample).to(dev)].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-30)
+    # empty segments are exactly zero
+    empty = (ne - ns) == 0
+    assert torch.all(out[empty] == 0)
+    # column totals: sum over segments == sum over edges (fp64 on both sides)
+    tot_seg = out.double().sum(0)
+    tot_edge = msg.double().sum(0)
+    assert torch.allclose(tot_seg, tot_edge, rtol=0, atol=1e-5 * msg.abs().double().sum(0).max().item())
+    # bf16 and max at full size: max exact against torch's segment reduction on the sorted rows
+    mx = seg(msg, cs, perm, ns, ne, S, reduce="max")
+    ref_mx = torch.segment_reduce(msg, "max", lengths=(ne - ns).long(), unsafe=True)
+    ref_mx = torch.where((ne - ns).unsqueeze(1) > 0, ref_mx, torch.zeros_like(ref_mx))
+    assert torch.equal(mx, ref_mx)
