@@ -100,19 +100,39 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
   return v;
 }
 
-// Wave-uniform max / min over all 64 lanes (every lane must be active).
+// DPP move with bound_ctrl: lanes without a source read 0, which lets the compiler fuse the
+// move into the consuming v_max_u32 (one v_max_u32_dpp per step).  0 is the identity of an
+// unsigned max.
+constexpr int kDppBcast15 = 0x142;      // lane 15 of each row -> the next row
+constexpr int kDppBcast31 = 0x143;      // lane 31 -> rows 2 and 3
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp0_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+
+// Wave-uniform max over all 64 lanes (every lane must be active): four in-row steps, two row
+// broadcasts, lane 63 holds the result.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = row_max_u32(v);
-  uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return max(max(a, b), max(c, d));
+  v = max(v, dpp0_u32<kDppXor1>(v));
+  v = max(v, dpp0_u32<kDppXor2>(v));
+  v = max(v, dpp0_u32<kDppHalfMirror>(v));
+  v = max(v, dpp0_u32<kDppMirror>(v));
+  v = max(v, dpp0_u32<kDppBcast15>(v));
+  v = max(v, dpp0_u32<kDppBcast31>(v));
+  return __builtin_amdgcn_readlane(v, 63);
 }
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-  v = row_min_u32(v);
-  uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return min(min(a, b), min(c, d));
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
+
+// Max / min over lanes 0..15 only (row 0); other lanes' values are ignored.
+__device__ __forceinline__ uint32_t row0_max_u32(uint32_t v) {
+  v = max(v, dpp0_u32<kDppXor1>(v));
+  v = max(v, dpp0_u32<kDppXor2>(v));
+  v = max(v, dpp0_u32<kDppHalfMirror>(v));
+  v = max(v, dpp0_u32<kDppMirror>(v));
+  return __builtin_amdgcn_readlane(v, 0);
 }
+__device__ __forceinline__ uint32_t row0_min_u32(uint32_t v) { return ~row0_max_u32(~v); }
 
 // Wave-wide inclusive prefix sum (all lanes active).
 template <typename T>

@@ -4,18 +4,20 @@
 // CPU path _fps_iterative_fallback (geoembodied/csrc/__init__.py:600-654): start at the first
 // point of the cloud, each step take the LOWEST index attaining max(min squared distance).
 //
-// Register kernel (clouds of up to 16384 points): one 256-thread workgroup per cloud, thread t
-// owns local points t, t+256, t+512, ... (PTS of them) with x, y, z and the running min
-// distance in VGPRs, so an iteration touches no memory except the centroid lookup (an LDS
-// table for clouds of up to 8192 points, L2 otherwise).  The per-iteration argmax is
-//   thread: strict '>' over its slots in index order (lowest index on ties);
-//   wave:   DPP row max of the distance bits (non-negative floats order like their bits),
-//           readlane across the 4 rows, then the same for the lowest index among the lanes
-//           holding that max;
-//   block:  one LDS slot per wave, double-buffered by iteration parity so that a single
-//           barrier per iteration suffices.
-// Streaming kernel (larger clouds): same reduction, positions read from HBM/L2 each
-// iteration and the running min distance kept in the workspace.
+// Three kernels, chosen by the largest cloud of the batch:
+//   bucketed (clouds of up to 8192 points, the common case): one 512-thread workgroup per
+//     cloud, points ordered along a Morton cell grid so that each register slot of a wave holds
+//     a compact bucket of 64 points; a bucket is only updated when the new centroid can lower
+//     one of its distances (an exact test, see below), and the argmax is assembled from cached
+//     per-bucket maxima.
+//   register (up to 16384 points): thread t owns local points t, t+256, ... (PTS of them) with
+//     x, y, z and the running min distance in VGPRs; every point is updated every iteration.
+//   streaming (larger clouds): positions read from HBM/L2 each iteration, running min
+//     distance in the workspace.
+// All three reduce (distance bits, index) per iteration as: wave max of the bits (DPP), then
+// the lowest index among the lanes holding it, then one LDS record per wave, double-buffered
+// by iteration parity so that a single barrier per iteration suffices.  Squared distances are
+// non-negative floats, whose bit patterns order like the values.
 #include "scan.hpp"
 
 namespace geo {
@@ -23,7 +25,8 @@ namespace {
 
 constexpr int kFpsThreads = 256;
 constexpr int kFpsWaves = kFpsThreads / kWave;
-constexpr int kFpsLdsPoints = 8192;  // centroid table: 8192 * 16 B = 128 KB of LDS
+constexpr int kFpsLdsPoints = 8192;  // register kernel centroid table: 8192 * 16 B of LDS
+constexpr int kFpsBucketThreads = 512;
 constexpr int kFpsStreamThreads = 1024;
 constexpr int kFpsStreamWaves = kFpsStreamThreads / kWave;
 
@@ -158,6 +161,264 @@ __global__ __launch_bounds__(kFpsThreads) void fps_register_kernel(
   }
 }
 
+// ------------------------------------------------------------------ bucketed kernel ---
+//
+// Clouds of up to 8192 points.  The cloud is first ordered along a 16^3 Morton cell grid
+// (LDS counting sort), so the 64 points a wave holds in one register slot — a bucket — lie
+// close together.  Each bucket keeps its bounding box and (max min-distance, lowest index
+// attaining it) in lane s of three VGPRs.  Per iteration the wave tests all its buckets at once
+// (one lane per bucket): with
+//   g_a = max(lo_a - c_a, c_a - hi_a, 0),  lb = (g_x*g_x + g_y*g_y) + g_z*g_z
+// evaluated with the same fp32 operations as the distance, every rounded operation is monotone,
+// so lb <= d(p, c) holds exactly for every point p of the bucket; when lb >= the bucket's max
+// min-distance no point of the bucket can change and the bucket is skipped.  Skipping is
+// therefore exact; only buckets near the new centroid pay for the update.
+constexpr int kCellBits = 4;                  // 16 cells per axis
+constexpr int kCells = 1 << (3 * kCellBits);  // 4096
+
+__device__ __forceinline__ uint32_t spread4(uint32_t v) {  // 4 bits -> every third bit
+  v &= 0xf;
+  v = (v | (v << 4)) & 0x0c3;
+  v = (v | (v << 2)) & 0x249;
+  return v;
+}
+
+__device__ __forceinline__ int cell16(float p, float lo, float scale) {
+  int c = static_cast<int>((p - lo) * scale);
+  return c < 0 ? 0 : (c > 15 ? 15 : c);
+}
+
+// Exchange record of one wave: its best (max min-distance bits, lowest index) and the
+// coordinates of that point, so the winner's position needs no second LDS round trip.
+struct alignas(16) FpsBest {
+  uint32_t dist_bits;
+  uint32_t idx;
+  float x, y, z;
+  uint32_t pad[3];
+};
+
+template <int PTS, int THREADS>
+__global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
+    const float* __restrict__ pos, const int64_t* __restrict__ ptr,
+    const int64_t* __restrict__ out_ptr, int64_t* __restrict__ out_idx) {
+  constexpr int WAVES = THREADS / kWave;
+  static_assert(PTS <= kWave, "one lane per bucket");
+  __shared__ FpsBest slots[2][WAVES];
+  __shared__ int hist[kCells];
+  __shared__ uint32_t red[6][WAVES];
+  extern __shared__ float4 scratch[];  // 12 bytes per point of sort scratch
+
+  const int b = blockIdx.x;
+  const int64_t start = ptr[b];
+  const int n = static_cast<int>(ptr[b + 1] - start);
+  const int64_t o0 = out_ptr[b];
+  const int k = static_cast<int>(out_ptr[b + 1] - o0);
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = lane_id();
+  if (k <= 0 || n <= 0) return;
+  if (k >= n) {
+    for (int i = t; i < n; i += THREADS) out_idx[o0 + i] = start + i;
+    return;
+  }
+  const float* P = pos + start * 3;
+
+  // 1. bounding box of the cloud
+  {
+    uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
+    for (int i = t; i < n; i += THREADS) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const uint32_t kk = float_order_key(P[3 * i + a]);
+        mn[a] = min(mn[a], kk);
+        mx[a] = max(mx[a], kk);
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      mn[a] = wave_min_u32(mn[a]);
+      mx[a] = wave_max_u32(mx[a]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
+    }
+    for (int i = t; i < kCells; i += THREADS) hist[i] = 0;
+    __syncthreads();
+  }
+  float lo[3], scale[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    uint32_t m0 = red[a][0], m1 = red[3 + a][0];
+    for (int ww = 1; ww < WAVES; ++ww) { m0 = min(m0, red[a][ww]); m1 = max(m1, red[3 + a][ww]); }
+    lo[a] = float_from_order_key(m0);
+    const float ext = float_from_order_key(m1) - lo[a];
+    scale[a] = ext > 0.f ? 16.f / ext : 0.f;
+  }
+
+  // 2. counting sort by Morton cell: int2 (code, rank) at [0, 8n), order at [8n, 12n)
+  int2* code_rank = reinterpret_cast<int2*>(scratch);
+  int* order = reinterpret_cast<int*>(reinterpret_cast<char*>(scratch) + 8 * static_cast<size_t>(n));
+  for (int i = t; i < n; i += THREADS) {
+    const int cx = cell16(P[3 * i], lo[0], scale[0]);
+    const int cy = cell16(P[3 * i + 1], lo[1], scale[1]);
+    const int cz = cell16(P[3 * i + 2], lo[2], scale[2]);
+    const int code = static_cast<int>(spread4(cx) | (spread4(cy) << 1) | (spread4(cz) << 2));
+    code_rank[i] = make_int2(code, atomicAdd(&hist[code], 1));
+  }
+  __syncthreads();
+  {  // exclusive scan of hist in place: thread t owns kCells / THREADS consecutive cells
+    constexpr int PER = kCells / THREADS;
+    int v[PER], s = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { v[j] = hist[t * PER + j]; s += v[j]; }
+    const int incl = wave_inclusive_sum(s);
+    __syncthreads();
+    if (lane == kWave - 1) red[0][w] = static_cast<uint32_t>(incl);
+    __syncthreads();
+    int off = incl - s;
+    for (int ww = 0; ww < w; ++ww) off += static_cast<int>(red[0][ww]);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { hist[t * PER + j] = off; off += v[j]; }
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += THREADS) {
+    const int2 cr = code_rank[i];
+    order[hist[cr.x] + cr.y] = i;
+  }
+  __syncthreads();
+
+  // 3. registers.  Bucket j = 64 consecutive sorted points; wave w owns buckets w, w+WAVES, ...
+  //    (neighbouring buckets on different waves, so the buckets near a centroid spread over
+  //    the SIMDs); slot s of wave w holds bucket s*WAVES + w.
+  float px[PTS], py[PTS], pz[PTS], md[PTS];
+  uint32_t oi[PTS];
+#pragma unroll
+  for (int s = 0; s < PTS; ++s) {
+    const int q = (s * WAVES + w) * kWave + lane;
+    if (q < n) {
+      const int i = order[q];
+      oi[s] = static_cast<uint32_t>(i);
+      px[s] = P[3 * i]; py[s] = P[3 * i + 1]; pz[s] = P[3 * i + 2];
+      md[s] = __builtin_inff();
+    } else {
+      oi[s] = 0xffffffffu;
+      px[s] = py[s] = pz[s] = 0.f;
+      md[s] = 0.f;  // padding: never changes, never wins
+    }
+  }
+
+  // 4. bucket records, lane s = bucket of slot s: box, max min-distance bits, and a cached
+  //    (lowest index attaining the max, its position) that an update invalidates.
+  float blx = __builtin_inff(), bly = __builtin_inff(), blz = __builtin_inff();
+  float bhx = -__builtin_inff(), bhy = -__builtin_inff(), bhz = -__builtin_inff();
+  uint32_t bmax = 0u, bidx = 0xffffffffu;
+  float bx = 0.f, by = 0.f, bz = 0.f;
+  uint64_t stale = 0;  // buckets whose cached (bidx, position) is out of date
+#pragma unroll
+  for (int s = 0; s < PTS; ++s) {
+    const bool valid = oi[s] != 0xffffffffu;
+    const uint32_t l0 = wave_min_u32(valid ? float_order_key(px[s]) : ~0u);
+    const uint32_t l1 = wave_min_u32(valid ? float_order_key(py[s]) : ~0u);
+    const uint32_t l2 = wave_min_u32(valid ? float_order_key(pz[s]) : ~0u);
+    const uint32_t h0 = wave_max_u32(valid ? float_order_key(px[s]) : 0u);
+    const uint32_t h1 = wave_max_u32(valid ? float_order_key(py[s]) : 0u);
+    const uint32_t h2 = wave_max_u32(valid ? float_order_key(pz[s]) : 0u);
+    const uint32_t mi = wave_min_u32(oi[s]);
+    if (lane == s && mi != 0xffffffffu) {
+      blx = float_from_order_key(l0); bly = float_from_order_key(l1); blz = float_from_order_key(l2);
+      bhx = float_from_order_key(h0); bhy = float_from_order_key(h1); bhz = float_from_order_key(h2);
+      bmax = 0x7f800000u;  // +inf: every bucket takes part in the first update
+    }
+  }
+  float cx = P[0], cy = P[1], cz = P[2];
+  if (t == 0) out_idx[o0] = start;
+
+  for (int it = 1; it < k; ++it) {
+    float gx, gy, gz;
+    {
+#pragma clang fp contract(off)
+      gx = fmaxf(fmaxf(blx - cx, cx - bhx), 0.f);
+      gy = fmaxf(fmaxf(bly - cy, cy - bhy), 0.f);
+      gz = fmaxf(fmaxf(blz - cz, cz - bhz), 0.f);
+    }
+    const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
+    const uint64_t act = __ballot(lane < PTS && __float_as_uint(lb) < bmax);
+    stale |= act;
+#pragma unroll
+    for (int s = 0; s < PTS; ++s) {
+      if (act & (1ull << s)) {
+        const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
+        md[s] = __builtin_amdgcn_fmed3f(d, md[s], -__builtin_inff());
+        const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
+        if (lane == s) bmax = m;
+      }
+    }
+    // wave best: the largest bucket max, then the lowest index over the buckets holding it
+    const uint32_t wbits = PTS <= 16 ? row0_max_u32(bmax) : wave_max_u32(lane < PTS ? bmax : 0u);
+    const uint64_t tied = __ballot(lane < PTS && bmax == wbits);
+    const uint64_t need = tied & stale;
+    if (need) {
+#pragma unroll
+      for (int s = 0; s < PTS; ++s) {
+        if (need & (1ull << s)) {
+          const uint32_t mb = __float_as_uint(md[s]);
+          const uint32_t mi = wave_min_u32(mb == wbits ? oi[s] : 0xffffffffu);
+          const int ml = __builtin_ctzll(__ballot(oi[s] == mi));
+          const float X = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(px[s]), ml));
+          const float Y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(py[s]), ml));
+          const float Z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pz[s]), ml));
+          if (lane == s) { bidx = mi; bx = X; by = Y; bz = Z; }
+        }
+      }
+      stale &= ~need;
+    }
+    uint32_t widx;
+    int wl;
+    if ((tied & (tied - 1)) == 0) {  // a single bucket holds the max (the usual case)
+      wl = __builtin_ctzll(tied | (1ull << 63));
+      widx = __builtin_amdgcn_readlane(bidx, wl);
+    } else {
+      widx = PTS <= 16 ? row0_min_u32((tied >> lane) & 1 ? bidx : 0xffffffffu)
+                       : wave_min_u32(lane < PTS && ((tied >> lane) & 1) ? bidx : 0xffffffffu);
+      wl = __builtin_ctzll(__ballot(lane < PTS && ((tied >> lane) & 1) && bidx == widx) | (1ull << 63));
+    }
+    FpsBest* sl = slots[it & 1];
+    {
+      const float X = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx), wl));
+      const float Y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(by), wl));
+      const float Z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bz), wl));
+      if (lane == 0) sl[w] = FpsBest{wbits, widx, X, Y, Z, {0u, 0u, 0u}};
+    }
+    __syncthreads();
+    // every lane of the first WAVES lanes reads one record; lexicographic (max bits, min idx)
+    const int rl = lane < WAVES ? lane : 0;
+    const FpsBest mine = sl[rl];
+    const uint32_t gbits = PTS <= 16 && WAVES <= 16 ? row0_max_u32(mine.dist_bits)
+                                                    : wave_max_u32(mine.dist_bits);
+    const uint32_t gidx = WAVES <= 16 ? row0_min_u32(mine.dist_bits == gbits ? mine.idx : 0xffffffffu)
+                                      : wave_min_u32(mine.dist_bits == gbits ? mine.idx : 0xffffffffu);
+    const int gl = __builtin_ctzll(__ballot(lane < WAVES && mine.idx == gidx) | (1ull << 63));
+    cx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.x), gl));
+    cy = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.y), gl));
+    cz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.z), gl));
+    if (t == 0) out_idx[o0 + it] = start + gidx;
+  }
+}
+
+template <int PTS, int THREADS>
+int launch_bucket(const float* pos, const int64_t* ptr, const int64_t* out_ptr, int64_t B,
+                  int64_t max_cloud, int64_t* out, hipStream_t st) {
+  const size_t lds = align_up(static_cast<size_t>(max_cloud > 0 ? max_cloud : 1) * 12, 16);
+  GEO_HIP_CHECK(hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&fps_bucket_kernel<PTS, THREADS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFpsLdsPoints * 12)));
+  hipLaunchKernelGGL((fps_bucket_kernel<PTS, THREADS>), dim3(B), dim3(THREADS), lds, st, pos, ptr,
+                     out_ptr, out);
+  GEO_LAUNCH_CHECK("fps_bucket_kernel");
+  return GEO_OK;
+}
+
 // Streaming kernel for clouds larger than the register kernel holds.
 __global__ __launch_bounds__(kFpsStreamThreads) void fps_stream_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ ptr,
@@ -266,6 +527,15 @@ extern "C" int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr,
     return set_error(GEO_ERR_WORKSPACE, "fps: workspace %zu bytes, need %lld", workspace_bytes,
                      (long long)need);
   const int64_t per = ceil_div(max_cloud, kFpsThreads);
+  if (max_cloud <= kFpsLdsPoints) {
+    // 512 threads: two waves per SIMD hide part of the per-iteration dependency chain.
+    const int64_t p2 = ceil_div(max_cloud, kFpsBucketThreads);
+    if (p2 <= 1) return launch_bucket<1, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+    if (p2 <= 2) return launch_bucket<2, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+    if (p2 <= 4) return launch_bucket<4, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+    if (p2 <= 8) return launch_bucket<8, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+    return launch_bucket<16, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+  }
   if (per <= 1) return launch_register<1>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   if (per <= 2) return launch_register<2>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   if (per <= 4) return launch_register<4>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);

@@ -5,7 +5,9 @@
 //   16-byte (or narrower, when C or the pointers do not allow it) vectors; L lanes cover a row
 //   (L = next power of two >= vectors per row, at most 64) and the wave's R = 64/L lane groups
 //   take rows start+g, start+g+R, ... so one wave-wide load instruction moves R whole rows.
-//   Four such loads are issued before any accumulation to keep >= 4 KB per wave in flight.
+//   The row ids of kUnroll = 8 rows per lane group are read first, then all 8 row loads are
+//   issued unconditionally (invalid ones read a valid row and are masked), so 8 KB per wave
+//   are in flight.  The wave's segment offsets arrive in one vector load.
 //   The R partial results are combined with a xor-butterfly; no atomics, no LDS.
 // Backward (replaces the ATen gather + un-permute of geoembodied/functional/segment_reduce.py:
 //   259-270): one lane group per sorted edge row e, grad_msg[perm[e]] = f(grad_out[col_sorted[e]]).
@@ -21,7 +23,7 @@ namespace {
 
 constexpr int kSegThreads = 256;
 constexpr int kSegWaves = kSegThreads / kWave;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;
 
 template <typename T> struct AccT { using type = float; };
 template <> struct AccT<double> { using type = double; };
@@ -120,14 +122,21 @@ __global__ __launch_bounds__(kSegThreads) void seg_fwd_kernel(
   const int64_t s_begin = wave * segs_per_wave;
   const int64_t s_stop = min(S, s_begin + segs_per_wave);
   const int ncol_iter = (vpr + L - 1) >> log_l;
+  // All segment offsets of this wave in one vector load (segs_per_wave <= 64).
+  int my_start = 0, my_end = 0;
+  if (s_begin + lane < s_stop) {
+    my_start = seg_start[s_begin + lane];
+    my_end = seg_end[s_begin + lane];
+  }
 
   for (int64_t s = s_begin; s < s_stop; ++s) {
-    const int start = clamp_i(__builtin_amdgcn_readfirstlane(seg_start[s]), 0, E);
-    const int end = clamp_i(__builtin_amdgcn_readfirstlane(seg_end[s]), start, E);
+    const int j = static_cast<int>(s - s_begin);
+    const int start = clamp_i(__builtin_amdgcn_readlane(my_start, j), 0, E);
+    const int end = clamp_i(__builtin_amdgcn_readlane(my_end, j), start, E);
     for (int ci = 0; ci < ncol_iter; ++ci) {
       const int vb = vl + ci * L;
       const bool col_ok = vb < vpr;
-      const int64_t col_off = static_cast<int64_t>(vb) * EPV;
+      const int64_t col_off = col_ok ? static_cast<int64_t>(vb) * EPV : 0;
       A acc[EPV];
       int first[EPV];
       int cnt[EPV];
@@ -138,18 +147,23 @@ __global__ __launch_bounds__(kSegThreads) void seg_fwd_kernel(
         cnt[i] = 0;
       }
       for (int e0 = start + g; e0 < end; e0 += R * kUnroll) {
+        // Row ids first (independent loads), then every row load unconditionally from a
+        // valid row, so kUnroll row reads are in flight together; invalid ones are masked.
+        int rows[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const int ev = min(e0 + u * R, end - 1);
+          rows[u] = perm ? perm[ev] : ev;
+        }
         V buf[kUnroll];
         bool ok[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
           const int e = e0 + u * R;
-          int row = e;
-          ok[u] = col_ok && e < end;
-          if (ok[u] && perm) {
-            row = perm[e];
-            ok[u] = static_cast<unsigned>(row) < static_cast<unsigned>(E);
-          }
-          if (ok[u]) buf[u].load(msg + static_cast<int64_t>(row) * C + col_off);
+          const int ev = min(e, end - 1);
+          ok[u] = col_ok && e < end && static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E);
+          const int row = static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E) ? rows[u] : ev;
+          buf[u].load(msg + static_cast<int64_t>(row) * C + col_off);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -236,18 +250,36 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
   const int64_t e_stop = min(static_cast<int64_t>(E), e_begin + rows_per_wave);
   const int ncol_iter = (vpr + L - 1) >> log_l;
 
-  for (int64_t e = e_begin + g; e < e_stop; e += R) {
-    const int s = col_sorted[e];
-    int p = perm ? perm[e] : static_cast<int>(e);
-    if (static_cast<unsigned>(p) >= static_cast<unsigned>(E)) continue;  // not a permutation
-    const bool s_ok = static_cast<unsigned>(s) < static_cast<unsigned>(S);
-    A scale = A(1);
-    if constexpr (OP == GEO_REDUCE_MEAN) {
-      if (s_ok) {
-        const int n = seg_end[s] - seg_start[s];
-        scale = static_cast<A>(n > 1 ? n : 1);
+  constexpr int U = kUnroll / 2;
+  for (int64_t e0 = e_begin + g; e0 < e_stop; e0 += static_cast<int64_t>(R) * U) {
+    // U rows per lane group: targets and destinations first, then the gradient rows.
+    int ss[U], pp[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = min(e0 + static_cast<int64_t>(u) * R, e_stop - 1);
+      ss[u] = col_sorted[e];
+      pp[u] = perm ? perm[e] : static_cast<int>(e);
+    }
+    A scales[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      scales[u] = A(1);
+      if constexpr (OP == GEO_REDUCE_MEAN) {
+        if (static_cast<unsigned>(ss[u]) < static_cast<unsigned>(S)) {
+          const int n = seg_end[ss[u]] - seg_start[ss[u]];
+          scales[u] = static_cast<A>(n > 1 ? n : 1);
+        }
       }
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+    const int64_t e = e0 + static_cast<int64_t>(u) * R;
+    if (e >= e_stop) break;
+    const int s = ss[u];
+    const int p = pp[u];
+    if (static_cast<unsigned>(p) >= static_cast<unsigned>(E)) continue;  // not a permutation
+    const bool s_ok = static_cast<unsigned>(s) < static_cast<unsigned>(S);
+    const A scale = scales[u];
     for (int ci = 0; ci < ncol_iter; ++ci) {
       const int vb = vl + ci * L;
       if (vb >= vpr) continue;
@@ -293,6 +325,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
         }
       }
       res.store(grad_msg + static_cast<int64_t>(p) * C + col_off);
+    }
     }
   }
 }

@@ -1,0 +1,129 @@
+"""CPU tests of the Python host layer: module paths and names of the reference, custom-op
+registration and shape inference, loud failure on CPU tensors, threshold rounding, and the
+deterministic workload generators."""
+
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+import geoembodied  # noqa: F401
+
+
+REFERENCE_NAMES = {
+    "geoembodied.csrc": ["get_radius_graph_backend", "radius_graph_cuda", "segment_reduce_available",
+                         "sort_and_build_csr_cuda", "segment_reduce_sum_cuda", "knn_available",
+                         "knn_cuda", "knn_self_cuda", "_knn_bruteforce", "fps_available",
+                         "fps_cuda", "_fps_iterative_fallback"],
+    "geoembodied.functional.fps": ["farthest_point_sampling"],
+    "geoembodied.functional.knn": ["knn", "knn_self"],
+    "geoembodied.functional.radius_graph": ["radius_graph", "compute_edge_vectors"],
+    "geoembodied.functional.segment_reduce": ["sort_and_build_csr", "segment_reduce",
+                                              "SegmentReduceFunction"],
+    "geoembodied.kernels": ["farthest_point_sampling", "knn", "knn_self", "radius_graph",
+                            "segment_reduce", "sort_and_build_csr"],
+}
+
+
+@pytest.mark.parametrize("module", sorted(REFERENCE_NAMES))
+def test_reference_module_paths_and_names(module):
+    mod = importlib.import_module(module)
+    for name in REFERENCE_NAMES[module]:
+        assert hasattr(mod, name), f"{module}.{name}"
+    assert mod is importlib.import_module(module.replace("geoembodied", "gdl_amd"))
+
+
+def test_product_does_not_import_oracle():
+    import sys
+    import subprocess
+    code = ("import sys, geoembodied, gdl_amd.functional; "
+            "import geoembodied.functional.segment_reduce; "
+            "print(any(m == 'oracle' or m.startswith('oracle.') for m in sys.modules))")
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, check=True)
+    assert out.stdout.strip() == "False"
+
+
+def test_custom_ops_registered_with_fake_kernels():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    ops = torch.ops.geoembodied
+    for name in ("segment_reduce_sum", "segment_reduce_mean", "segment_reduce_max",
+                 "segment_reduce_backward"):
+        assert hasattr(ops, name), name
+    with FakeTensorMode():
+        msg = torch.empty(30, 7)
+        i32 = torch.empty(30, dtype=torch.int32)
+        ns = torch.empty(5, dtype=torch.int32)
+        out = ops.segment_reduce_sum(msg, i32, i32, ns, ns, 5)
+        assert out.shape == (5, 7) and out.dtype == torch.float32
+        out, arg = ops.segment_reduce_max(msg, i32, i32, ns, ns, 5, 0)
+        assert out.shape == (5, 7) and arg.dtype == torch.int32
+        g = ops.segment_reduce_backward(out, i32, i32, ns, ns, None, None, None, 30, 0)
+        assert g.shape == (30, 7)
+
+
+def test_cpu_tensors_raise_clear_errors():
+    from geoembodied.csrc import _fps_iterative_fallback, _knn_bruteforce
+    from geoembodied.functional.fps import farthest_point_sampling
+    from geoembodied.functional.knn import knn
+    from geoembodied.functional.radius_graph import radius_graph
+    from geoembodied.functional.segment_reduce import segment_reduce, sort_and_build_csr
+    x = torch.randn(10, 3)
+    ptr = torch.tensor([0, 10])
+    for call in (
+        lambda: farthest_point_sampling(x, 4, ptr=ptr),
+        lambda: farthest_point_sampling(x, 4),
+        lambda: knn(x, x, ptr, ptr, 3),
+        lambda: radius_graph(x, 0.5),
+        lambda: sort_and_build_csr(torch.tensor([0, 1, 1]), 2),
+        lambda: segment_reduce(torch.randn(3, 2), *[torch.zeros(3, dtype=torch.int32)] * 2,
+                               torch.zeros(2, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 2),
+        lambda: _fps_iterative_fallback(x, ptr, torch.tensor([2])),
+        lambda: _knn_bruteforce(x, x, ptr, ptr, 2),
+    ):
+        with pytest.raises(RuntimeError, match="GPU only"):
+            call()
+
+
+def test_backend_probe_without_gpu():
+    from geoembodied.csrc import fps_available, get_radius_graph_backend, knn_available
+    if not torch.cuda.is_available():
+        assert get_radius_graph_backend() == "unavailable"
+        assert not fps_available() and not knn_available()
+
+
+def test_fp32_radius_threshold():
+    from geoembodied.csrc import fp32_radius_sq
+    for r in (0.1, 0.2, 0.4, 0.5, 0.3, 0.15, 2.0, 2.5):
+        assert fp32_radius_sq(r) == float(np.float32(r * r))
+    # the CUDA path's fl32(r)^2 is one ulp above at 0.1, 0.2, 0.4 (probe in the survey)
+    for r in (0.1, 0.2, 0.4):
+        assert fp32_radius_sq(r) < float(np.float32(np.float32(r) * np.float32(r)))
+
+
+def test_empty_edge_csr_shortcut_any_device():
+    from geoembodied.functional.segment_reduce import sort_and_build_csr
+    cs, pm, ns, ne = sort_and_build_csr(torch.empty(0, dtype=torch.long), 4)
+    assert cs.numel() == 0 and ns.tolist() == [0] * 4 and ne.tolist() == [0] * 4
+
+
+def test_generators_are_deterministic():
+    import bench
+    off = bench.make_c3_offsets()
+    sizes = np.diff(off)
+    assert off[-1] == 4_194_304 and (sizes > 0).sum() == 135_587 and sizes.max() == 64
+    a, b = bench.make_c2(), bench.make_c2()
+    assert torch.equal(a["pos"], b["pos"]) and a["pos"].shape == (65536, 3)
+    assert torch.equal(a["batch"], torch.arange(16).repeat_interleave(4096))
+    c5 = bench.make_c5()["pos"]
+    assert c5.shape == (131072, 3) and float(c5[:, 2].min()) >= -1.7001
+    c4 = bench.make_c4()
+    assert c4["pos"].shape == (65536, 3)
+
+
+def test_bench_refuses_multi_gpu():
+    import subprocess
+    import sys
+    out = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], capture_output=True, text=True,
+                         cwd=str(__import__("pathlib").Path(__file__).resolve().parents[1]))
+    assert out.returncode == 2 and "one GPU" in out.stderr
