@@ -166,7 +166,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--all", action="store_true", help="also time C1, C4, C5 and KNN legs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None, help="run one leg: c2 | c3 | c3bf16 | c3bwd")
+    ap.add_argument("--only", default=None,
+                    help="run one leg: c2 | c3 | c3bf16 | c3bwd | copy (HBM counter calibration)")
+    ap.add_argument("--iters", type=int, default=50, help="timed launches per C3 leg")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -238,7 +240,7 @@ def main() -> int:
         gen = torch.Generator(device=dev).manual_seed(0)
         msg = torch.randn(E, C, device=dev, generator=gen)
         bytes_fwd = E * C * 4 + S * C * 4 + (S + 1) * 4
-        iters = 50
+        iters = args.iters
         if args.only in (None, "c3"):
             ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
             gbs = bytes_fwd / (ms * 1e-3) / 1e9
@@ -271,6 +273,17 @@ def main() -> int:
         col64 = col_sorted.long()
         legs["c3_csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col64, S), 10, 2), 4)
         del msg
+
+    # ------------------------------------------------------- HBM counter calibration ---
+    if args.only == "copy":
+        # A plain elementwise pass over 1 GiB (read 1 GiB, write 1 GiB with 16-byte vector
+        # accesses): the reference point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE.
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = event_ms(lambda: torch.add(src, 1.0, out=dst), args.iters, 3)
+        legs["copy_1gib_ms"] = round(ms, 4)
+        legs["copy_1gib_gbs"] = round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)
+        log(f"  copy 1 GiB: {ms:.4f} ms  {legs['copy_1gib_gbs']} GB/s")
 
     # ---------------------------------------------------------------- extra legs ---
     if args.all:

@@ -5,7 +5,7 @@
 // point of the cloud, each step take the LOWEST index attaining max(min squared distance).
 //
 // Three kernels, chosen by the largest cloud of the batch:
-//   bucketed (clouds of up to 8192 points, the common case): one 512-thread workgroup per
+//   bucketed (clouds of up to 8192 points, the common case): one 1024-thread workgroup per
 //     cloud, points ordered along a Morton cell grid so that each register slot of a wave holds
 //     a compact bucket of 64 points; a bucket is only updated when the new centroid can lower
 //     one of its distances (an exact test, see below), and the argmax is assembled from cached
@@ -26,7 +26,7 @@ namespace {
 constexpr int kFpsThreads = 256;
 constexpr int kFpsWaves = kFpsThreads / kWave;
 constexpr int kFpsLdsPoints = 8192;  // register kernel centroid table: 8192 * 16 B of LDS
-constexpr int kFpsBucketThreads = 512;
+constexpr int kFpsBucketThreads = 1024;
 constexpr int kFpsStreamThreads = 1024;
 constexpr int kFpsStreamWaves = kFpsStreamThreads / kWave;
 
@@ -188,14 +188,6 @@ __device__ __forceinline__ int cell16(float p, float lo, float scale) {
   return c < 0 ? 0 : (c > 15 ? 15 : c);
 }
 
-// Exchange record of one wave: its best (max min-distance bits, lowest index) and the
-// coordinates of that point, so the winner's position needs no second LDS round trip.
-struct alignas(16) FpsBest {
-  uint32_t dist_bits;
-  uint32_t idx;
-  float x, y, z;
-  uint32_t pad[3];
-};
 
 template <int PTS, int THREADS>
 __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
@@ -203,10 +195,14 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const int64_t* __restrict__ out_ptr, int64_t* __restrict__ out_idx) {
   constexpr int WAVES = THREADS / kWave;
   static_assert(PTS <= kWave, "one lane per bucket");
-  __shared__ FpsBest slots[2][WAVES];
+  // Cross-wave argmax: one 64-bit LDS atomic max per wave on key (bits << 32) | ~index, so the
+  // largest distance wins and, among equal distances, the lowest index.  Three slots rotate:
+  // iteration it uses slot it % 3 and clears slot (it + 1) % 3, whose last readers finished
+  // before the previous barrier and whose next writers start after this one.
+  __shared__ unsigned long long slots[3];
   __shared__ int hist[kCells];
   __shared__ uint32_t red[6][WAVES];
-  extern __shared__ float4 scratch[];  // 12 bytes per point of sort scratch
+  extern __shared__ float4 table[];  // sort scratch (12 B/point), then positions by index
 
   const int b = blockIdx.x;
   const int64_t start = ptr[b];
@@ -257,8 +253,8 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   }
 
   // 2. counting sort by Morton cell: int2 (code, rank) at [0, 8n), order at [8n, 12n)
-  int2* code_rank = reinterpret_cast<int2*>(scratch);
-  int* order = reinterpret_cast<int*>(reinterpret_cast<char*>(scratch) + 8 * static_cast<size_t>(n));
+  int2* code_rank = reinterpret_cast<int2*>(table);
+  int* order = reinterpret_cast<int*>(reinterpret_cast<char*>(table) + 8 * static_cast<size_t>(n));
   for (int i = t; i < n; i += THREADS) {
     const int cx = cell16(P[3 * i], lo[0], scale[0]);
     const int cy = cell16(P[3 * i + 1], lo[1], scale[1]);
@@ -307,13 +303,15 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
       md[s] = 0.f;  // padding: never changes, never wins
     }
   }
+  __syncthreads();  // order[] is dead: the scratch becomes the position table
+  for (int i = t; i < n; i += THREADS) table[i] = make_float4(P[3 * i], P[3 * i + 1], P[3 * i + 2], 0.f);
+  if (t < 3) slots[t] = 0ull;
 
   // 4. bucket records, lane s = bucket of slot s: box, max min-distance bits, and a cached
-  //    (lowest index attaining the max, its position) that an update invalidates.
+  //    lowest index attaining the max that an update invalidates.
   float blx = __builtin_inff(), bly = __builtin_inff(), blz = __builtin_inff();
   float bhx = -__builtin_inff(), bhy = -__builtin_inff(), bhz = -__builtin_inff();
   uint32_t bmax = 0u, bidx = 0xffffffffu;
-  float bx = 0.f, by = 0.f, bz = 0.f;
   uint64_t stale = 0;  // buckets whose cached (bidx, position) is out of date
 #pragma unroll
   for (int s = 0; s < PTS; ++s) {
@@ -333,6 +331,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   }
   float cx = P[0], cy = P[1], cz = P[2];
   if (t == 0) out_idx[o0] = start;
+  __syncthreads();
 
   for (int it = 1; it < k; ++it) {
     float gx, gy, gz;
@@ -364,44 +363,26 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
         if (need & (1ull << s)) {
           const uint32_t mb = __float_as_uint(md[s]);
           const uint32_t mi = wave_min_u32(mb == wbits ? oi[s] : 0xffffffffu);
-          const int ml = __builtin_ctzll(__ballot(oi[s] == mi));
-          const float X = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(px[s]), ml));
-          const float Y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(py[s]), ml));
-          const float Z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pz[s]), ml));
-          if (lane == s) { bidx = mi; bx = X; by = Y; bz = Z; }
+          if (lane == s) bidx = mi;
         }
       }
       stale &= ~need;
     }
     uint32_t widx;
-    int wl;
     if ((tied & (tied - 1)) == 0) {  // a single bucket holds the max (the usual case)
-      wl = __builtin_ctzll(tied | (1ull << 63));
-      widx = __builtin_amdgcn_readlane(bidx, wl);
+      widx = __builtin_amdgcn_readlane(bidx, __builtin_ctzll(tied | (1ull << 63)));
     } else {
       widx = PTS <= 16 ? row0_min_u32((tied >> lane) & 1 ? bidx : 0xffffffffu)
                        : wave_min_u32(lane < PTS && ((tied >> lane) & 1) ? bidx : 0xffffffffu);
-      wl = __builtin_ctzll(__ballot(lane < PTS && ((tied >> lane) & 1) && bidx == widx) | (1ull << 63));
     }
-    FpsBest* sl = slots[it & 1];
-    {
-      const float X = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx), wl));
-      const float Y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(by), wl));
-      const float Z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bz), wl));
-      if (lane == 0) sl[w] = FpsBest{wbits, widx, X, Y, Z, {0u, 0u, 0u}};
-    }
+    const int p = it % 3;
+    if (lane == 0)
+      atomicMax(&slots[p], (static_cast<unsigned long long>(wbits) << 32) | static_cast<uint32_t>(~widx));
+    if (t == 0) slots[p == 2 ? 0 : p + 1] = 0ull;
     __syncthreads();
-    // every lane of the first WAVES lanes reads one record; lexicographic (max bits, min idx)
-    const int rl = lane < WAVES ? lane : 0;
-    const FpsBest mine = sl[rl];
-    const uint32_t gbits = PTS <= 16 && WAVES <= 16 ? row0_max_u32(mine.dist_bits)
-                                                    : wave_max_u32(mine.dist_bits);
-    const uint32_t gidx = WAVES <= 16 ? row0_min_u32(mine.dist_bits == gbits ? mine.idx : 0xffffffffu)
-                                      : wave_min_u32(mine.dist_bits == gbits ? mine.idx : 0xffffffffu);
-    const int gl = __builtin_ctzll(__ballot(lane < WAVES && mine.idx == gidx) | (1ull << 63));
-    cx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.x), gl));
-    cy = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.y), gl));
-    cz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine.z), gl));
+    const uint32_t gidx = ~static_cast<uint32_t>(slots[p]);
+    const float4 c = table[gidx];
+    cx = c.x; cy = c.y; cz = c.z;
     if (t == 0) out_idx[o0 + it] = start + gidx;
   }
 }
@@ -409,10 +390,10 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
 template <int PTS, int THREADS>
 int launch_bucket(const float* pos, const int64_t* ptr, const int64_t* out_ptr, int64_t B,
                   int64_t max_cloud, int64_t* out, hipStream_t st) {
-  const size_t lds = align_up(static_cast<size_t>(max_cloud > 0 ? max_cloud : 1) * 12, 16);
+  const size_t lds = static_cast<size_t>(max_cloud > 0 ? max_cloud : 1) * sizeof(float4);
   GEO_HIP_CHECK(hipFuncSetAttribute(
       reinterpret_cast<const void*>(&fps_bucket_kernel<PTS, THREADS>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFpsLdsPoints * 12)));
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFpsLdsPoints * sizeof(float4))));
   hipLaunchKernelGGL((fps_bucket_kernel<PTS, THREADS>), dim3(B), dim3(THREADS), lds, st, pos, ptr,
                      out_ptr, out);
   GEO_LAUNCH_CHECK("fps_bucket_kernel");
@@ -528,7 +509,7 @@ extern "C" int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr,
                      (long long)need);
   const int64_t per = ceil_div(max_cloud, kFpsThreads);
   if (max_cloud <= kFpsLdsPoints) {
-    // 512 threads: two waves per SIMD hide part of the per-iteration dependency chain.
+    // 1024 threads: four waves per SIMD hide much of the per-iteration dependency chain.
     const int64_t p2 = ceil_div(max_cloud, kFpsBucketThreads);
     if (p2 <= 1) return launch_bucket<1, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
     if (p2 <= 2) return launch_bucket<2, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);

@@ -101,7 +101,13 @@ __global__ void rg_init(RgWs w, int64_t N, int64_t B) {
 __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __restrict__ x, int64_t N,
                                                       const int64_t* __restrict__ batch, int64_t B,
                                                       int64_t ppc, const uint8_t* __restrict__ mask) {
+  // Points of one workgroup usually belong to one cloud: reduce in the workgroup first and
+  // issue 7 atomics per workgroup; mixed workgroups fall back to per-wave / per-lane atomics.
+  constexpr int W = kRgThreads / kWave;
+  __shared__ int s_cloud[W];
+  __shared__ uint32_t s_red[7][W];
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int wv = threadIdx.x / kWave;
   int b = -1;
   float px = 0.f, py = 0.f, pz = 0.f;
   if (i < N) {
@@ -109,26 +115,49 @@ __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __res
     if (mask && !mask[i]) b = -1;
     if (b >= 0) { px = x[3 * i]; py = x[3 * i + 1]; pz = x[3 * i + 2]; }
   }
+  // wave-uniform cloud (or -1 for "mixed")
   const int b0 = __builtin_amdgcn_readfirstlane(b);
   const bool uniform = __ballot(b != b0) == 0ull;
-  if (uniform) {
-    if (b0 < 0) return;
-    const uint32_t kx = float_order_key(px), ky = float_order_key(py), kz = float_order_key(pz);
-    const uint32_t mnx = wave_min_u32(kx), mny = wave_min_u32(ky), mnz = wave_min_u32(kz);
-    const uint32_t mxx = wave_max_u32(kx), mxy = wave_max_u32(ky), mxz = wave_max_u32(kz);
-    if (lane_id() == 0) {
-      atomicAdd(&w.cloud_n[b0], kWave);
-      uint32_t* bb = w.bbox + 6 * b0;
-      atomicMin(&bb[0], mnx); atomicMin(&bb[1], mny); atomicMin(&bb[2], mnz);
-      atomicMax(&bb[3], mxx); atomicMax(&bb[4], mxy); atomicMax(&bb[5], mxz);
-    }
-  } else if (b >= 0) {
+  const uint32_t kx = float_order_key(px), ky = float_order_key(py), kz = float_order_key(pz);
+  const uint32_t v[7] = {wave_min_u32(kx), wave_min_u32(ky), wave_min_u32(kz), wave_max_u32(kx),
+                         wave_max_u32(ky), wave_max_u32(kz), 0u};
+  if (lane_id() == 0) {
+    s_cloud[wv] = uniform ? b0 : -2;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) s_red[q][wv] = v[q];
+  }
+  if (!uniform && b >= 0) {  // mixed wave: per-lane atomics
     atomicAdd(&w.cloud_n[b], 1);
     uint32_t* bb = w.bbox + 6 * b;
-    atomicMin(&bb[0], float_order_key(px)); atomicMin(&bb[1], float_order_key(py));
-    atomicMin(&bb[2], float_order_key(pz));
-    atomicMax(&bb[3], float_order_key(px)); atomicMax(&bb[4], float_order_key(py));
-    atomicMax(&bb[5], float_order_key(pz));
+    atomicMin(&bb[0], kx); atomicMin(&bb[1], ky); atomicMin(&bb[2], kz);
+    atomicMax(&bb[3], kx); atomicMax(&bb[4], ky); atomicMax(&bb[5], kz);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int c0 = s_cloud[0];
+    bool same = c0 >= 0;
+    for (int q = 1; q < W; ++q) same = same && s_cloud[q] == c0;
+    if (same) {  // whole workgroup in one cloud
+      uint32_t r[6];
+      for (int q = 0; q < 6; ++q) r[q] = s_red[q][0];
+      for (int ww = 1; ww < W; ++ww) {
+        for (int q = 0; q < 3; ++q) r[q] = min(r[q], s_red[q][ww]);
+        for (int q = 3; q < 6; ++q) r[q] = max(r[q], s_red[q][ww]);
+      }
+      atomicAdd(&w.cloud_n[c0], kRgThreads);
+      uint32_t* bb = w.bbox + 6 * c0;
+      atomicMin(&bb[0], r[0]); atomicMin(&bb[1], r[1]); atomicMin(&bb[2], r[2]);
+      atomicMax(&bb[3], r[3]); atomicMax(&bb[4], r[4]); atomicMax(&bb[5], r[5]);
+    } else {
+      for (int ww = 0; ww < W; ++ww) {
+        const int c = s_cloud[ww];
+        if (c < 0) continue;  // mixed (handled per lane) or masked
+        atomicAdd(&w.cloud_n[c], kWave);
+        uint32_t* bb = w.bbox + 6 * c;
+        atomicMin(&bb[0], s_red[0][ww]); atomicMin(&bb[1], s_red[1][ww]); atomicMin(&bb[2], s_red[2][ww]);
+        atomicMax(&bb[3], s_red[3][ww]); atomicMax(&bb[4], s_red[4][ww]); atomicMax(&bb[5], s_red[5][ww]);
+      }
+    }
   }
 }
 
@@ -277,7 +306,7 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
                          float r2, int K, int loop, const int64_t* __restrict__ row_ptr,
                          int64_t* __restrict__ row_out, int64_t* __restrict__ col_out,
                          int use_lds) {
-  __shared__ int32_t lbuf[MODE == 1 ? kRgLdsK * kRgEmitThreads : 1];
+  extern __shared__ int32_t lbuf[];  // emit: K entries per thread, column-major by thread
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int total = w.cell_start[w.cells_max];
   if (t >= total) return;
@@ -435,8 +464,9 @@ extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, 
   hipStream_t st = as_stream(stream);
   const int K = static_cast<int>(max_num_neighbors);
   const int use_lds = K <= kRgLdsK ? 1 : 0;
+  const size_t lds = use_lds ? static_cast<size_t>(K) * kRgEmitThreads * sizeof(int32_t) : 0;
   const int64_t blocks = ceil_div(N, kRgEmitThreads);
-  hipLaunchKernelGGL((rg_query<1>), dim3(blocks), dim3(kRgEmitThreads), 0, st, w, batch, B,
+  hipLaunchKernelGGL((rg_query<1>), dim3(blocks), dim3(kRgEmitThreads), lds, st, w, batch, B,
                      points_per_cloud, r2, K, loop, row_ptr, row_out, col_out, use_lds);
   GEO_LAUNCH_CHECK("rg_query<emit>");
   return GEO_OK;
