@@ -32,6 +32,10 @@ import torch
 
 METRIC = "ms/batch FPS+radius_graph (B=16,N=4096); segment_reduce GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of seg_fwd_kernel<float,16,SUM> on C3, from rocprofv3 FETCH_SIZE x 2.0 +
+# WRITE_SIZE x 1.0 (factors from a plain 1 GiB elementwise pass); the run and its arithmetic are
+# in profiles/seg_fwd_kernel_c3_fp32.md.
+C3_SUM_TRAFFIC_BYTES = 2_325_600_000
 
 
 def log(*a):
@@ -245,7 +249,7 @@ def main() -> int:
             ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
             gbs = bytes_fwd / (ms * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_SUM_TRAFFIC_BYTES,
                     "kernel": "seg_fwd_kernel<float,16,SUM>", "ms_per_launch": round(ms, 4),
                     "algorithmic_bytes": bytes_fwd}
             log(f"  fwd sum fp32: {ms:.4f} ms  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of peak)")

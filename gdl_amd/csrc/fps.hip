@@ -515,7 +515,7 @@ extern "C" int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr,
     if (p2 <= 2) return launch_bucket<2, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
     if (p2 <= 4) return launch_bucket<4, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
     if (p2 <= 8) return launch_bucket<8, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
-    return launch_bucket<16, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+    return launch_bucket<8, kFpsBucketThreads>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   }
   if (per <= 1) return launch_register<1>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   if (per <= 2) return launch_register<2>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
