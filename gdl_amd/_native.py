@@ -34,7 +34,7 @@ _SIGNATURES = {
     "geo_knn_workspace_bytes": (c_size, [c_i64, c_i64, c_i64, c_i64]),
     "geo_knn": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp,
                         c_size, c_vp]),
-    "geo_radius_workspace_bytes": (c_size, [c_i64, c_i64]),
+    "geo_radius_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "geo_radius_count": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_f32, c_f32, c_i64,
                                  c_int, c_vp, c_vp, c_size, c_vp]),
     "geo_radius_emit": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_f32, c_f32, c_i64,

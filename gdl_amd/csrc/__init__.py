@@ -118,7 +118,7 @@ def radius_graph_hip(
     L = _nat.lib()
     with torch.cuda.device(dev):
         s = _nat.stream_of(dev)
-        ws_bytes = L.geo_radius_workspace_bytes(N, B)
+        ws_bytes = L.geo_radius_workspace_bytes(N, B, K)
         ws = _nat.workspace(ws_bytes, dev)
         row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
         args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K, int(bool(loop)))

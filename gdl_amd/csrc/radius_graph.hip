@@ -31,6 +31,7 @@ constexpr int kRgThreads = 256;
 constexpr int kRgEmitThreads = 64;
 constexpr int kRgMaxAxis = 16384;
 constexpr int kRgLdsK = 256;
+constexpr int kRgStageK = 64;
 
 struct Grid {
   float ox, oy, oz, inv_h;
@@ -50,13 +51,18 @@ struct RgWs {
   int32_t* cnt;
   int32_t* deg;
   int64_t* deg_tiles;
+  int32_t* list;  // [N][K] accepted sources per target (unsorted), or null when too large
   int64_t cells_max;
   size_t bytes;
 };
 
 int64_t cells_cap(int64_t N, int64_t B) { return 4 * N + 64 * B; }
 
-RgWs carve_rg(void* base, int64_t N, int64_t B) {
+// The per-target source lists are kept when they fit in 1 GiB of workspace; beyond that the
+// emit pass re-scans the candidates instead.
+constexpr int64_t kRgListMaxEntries = int64_t(1) << 28;
+
+RgWs carve_rg(void* base, int64_t N, int64_t B, int64_t K) {
   Carver c(base);
   RgWs w;
   const int64_t nn = N > 0 ? N : 1, bb = B > 0 ? B : 1;
@@ -73,6 +79,9 @@ RgWs carve_rg(void* base, int64_t N, int64_t B) {
   w.cnt = c.take<int32_t>(nn);
   w.deg = c.take<int32_t>(nn);
   w.deg_tiles = c.take<int64_t>(scan_workspace_elems(N));
+  const bool lists = K > 0 && N <= kRgListMaxEntries / K;
+  w.list = lists ? c.take<int32_t>(N * K) : nullptr;
+  if (lists && !base) w.list = reinterpret_cast<int32_t*>(1);  // size query: mark "present"
   w.bytes = c.used;
   return w;
 }
@@ -301,6 +310,40 @@ struct RowList {
   }
 };
 
+// Exact K smallest (d, j) among the in-radius sources of one target (used when a target has
+// more than K of them): the K-th distance bits by binary search, then the index threshold among
+// the sources at that distance.  Returns (d*, j*): keep d < d*, or d == d* and j <= j*.
+__device__ __forceinline__ void threshold_select(const RgWs& w, const Grid& g, float qx, float qy,
+                                                 float qz, int qi, bool lp, float r2, int K,
+                                                 uint32_t& dstar, int& jstar) {
+  const uint32_t r2b = __float_as_uint(r2);
+  uint32_t lo = 0, hi = r2b > 0 ? r2b - 1 : 0;
+  while (lo < hi) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    int n = 0;
+    for_each_candidate(w, g, qx, qy, qz, qi, lp, [&](float d, int) {
+      n += (d < r2) && (__float_as_uint(d) <= mid);
+    });
+    if (n >= K) hi = mid; else lo = mid + 1;
+  }
+  dstar = lo;
+  int less = 0;
+  for_each_candidate(w, g, qx, qy, qz, qi, lp, [&](float d, int) {
+    less += (d < r2) && (__float_as_uint(d) < dstar);
+  });
+  const int need = K - less;
+  int jlo = 0, jhi = 0x7ffffffe;
+  while (jlo < jhi) {
+    const int mid = jlo + ((jhi - jlo) >> 1);
+    int n = 0;
+    for_each_candidate(w, g, qx, qy, qz, qi, lp, [&](float d, int j) {
+      n += (d < r2) && (__float_as_uint(d) == dstar) && (j <= mid);
+    });
+    if (n >= need) jhi = mid; else jlo = mid + 1;
+  }
+  jstar = jlo;
+}
+
 template <int MODE>  // 0 = count, 1 = emit
 __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, int64_t ppc,
                          float r2, int K, int loop, const int64_t* __restrict__ row_ptr,
@@ -317,7 +360,13 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
   const bool lp = loop != 0;
   if constexpr (MODE == 0) {
     int c = 0;
-    for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) { c += d < r2; });
+    int32_t* L = w.list ? w.list + static_cast<int64_t>(qi) * K : nullptr;
+    for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
+      if (d < r2) {
+        if (L && c < K) L[c] = j;
+        ++c;
+      }
+    });
     w.cnt[qi] = c;
     w.deg[qi] = c < K ? c : K;
   } else {
@@ -332,33 +381,9 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
         if (d < r2) lst.insert(j);
       });
     } else {
-      // K smallest (d, j): binary search the K-th distance bits, then the index among ties.
-      const uint32_t r2b = __float_as_uint(r2);
-      uint32_t lo = 0, hi = r2b > 0 ? r2b - 1 : 0;
-      while (lo < hi) {
-        const uint32_t mid = lo + ((hi - lo) >> 1);
-        int n = 0;
-        for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) {
-          n += (d < r2) && (__float_as_uint(d) <= mid);
-        });
-        if (n >= K) hi = mid; else lo = mid + 1;
-      }
-      const uint32_t dstar = lo;
-      int less = 0;
-      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int) {
-        less += (d < r2) && (__float_as_uint(d) < dstar);
-      });
-      const int need = K - less;
-      int jlo = 0, jhi = 0x7ffffffe;
-      while (jlo < jhi) {
-        const int mid = jlo + ((jhi - jlo) >> 1);
-        int n = 0;
-        for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
-          n += (d < r2) && (__float_as_uint(d) == dstar) && (j <= mid);
-        });
-        if (n >= need) jhi = mid; else jlo = mid + 1;
-      }
-      const int jstar = jlo;
+      uint32_t dstar;
+      int jstar;
+      threshold_select(w, g, q.x, q.y, q.z, qi, lp, r2, K, dstar, jstar);
       for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
         if (d < r2) {
           const uint32_t db = __float_as_uint(d);
@@ -369,6 +394,59 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
     for (int m = 0; m < lst.n; ++m) {
       if (lst.lds) row_out[o + m] = lst.get(m);
       col_out[o + m] = qi;
+    }
+  }
+}
+
+// After the edge count is known: one thread per target writes its row, sources ascending.  The
+// collected list is unsorted (cell traversal order); each source goes to position
+// row_ptr[i] + (number of smaller sources in the list).  Targets with more than K sources
+// rebuild their list with the exact (d, j) threshold first.
+__global__ void rg_compact(RgWs w, const float* __restrict__ x, int64_t N,
+                           const int64_t* __restrict__ batch, int64_t B, int64_t ppc, float r2,
+                           int K, int loop, const int64_t* __restrict__ row_ptr,
+                           int64_t* __restrict__ row_out, int64_t* __restrict__ col_out) {
+  extern __shared__ int32_t stage[];  // K entries per thread when K <= kRgStageK
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const int c = w.cnt[i];
+  if (c == 0) return;
+  int32_t* L = w.list + i * K;
+  int m = c;
+  if (c > K) {
+    const int b = cloud_of(i, batch, B, ppc);
+    const Grid g = w.grid[b];
+    const float qx = x[3 * i], qy = x[3 * i + 1], qz = x[3 * i + 2];
+    uint32_t dstar;
+    int jstar;
+    threshold_select(w, g, qx, qy, qz, static_cast<int>(i), loop != 0, r2, K, dstar, jstar);
+    int n = 0;
+    for_each_candidate(w, g, qx, qy, qz, static_cast<int>(i), loop != 0, [&](float d, int j) {
+      if (d < r2) {
+        const uint32_t db = __float_as_uint(d);
+        if (db < dstar || (db == dstar && j <= jstar)) L[n++] = j;
+      }
+    });
+    m = K;
+  }
+  const int64_t o = row_ptr[i];
+  if (K <= kRgStageK) {
+    int32_t* S = stage + threadIdx.x;
+    for (int a = 0; a < m; ++a) S[a * kRgEmitThreads] = L[a];
+    for (int a = 0; a < m; ++a) {
+      const int v = S[a * kRgEmitThreads];
+      int r = 0;
+      for (int q = 0; q < m; ++q) r += S[q * kRgEmitThreads] < v;
+      row_out[o + r] = v;
+      col_out[o + a] = i;
+    }
+  } else {
+    for (int a = 0; a < m; ++a) {
+      const int v = L[a];
+      int r = 0;
+      for (int q = 0; q < m; ++q) r += L[q] < v;
+      row_out[o + r] = v;
+      col_out[o + a] = i;
     }
   }
 }
@@ -391,9 +469,9 @@ int check_common(const float* x, int64_t N, int64_t B, int64_t ppc, const int64_
 
 using namespace geo;
 
-extern "C" size_t geo_radius_workspace_bytes(int64_t N, int64_t B) {
-  if (N < 0 || B < 0) return 0;
-  return carve_rg(nullptr, N, B).bytes;
+extern "C" size_t geo_radius_workspace_bytes(int64_t N, int64_t B, int64_t max_num_neighbors) {
+  if (N < 0 || B < 0 || max_num_neighbors < 0) return 0;
+  return carve_rg(nullptr, N, B, max_num_neighbors).bytes;
 }
 
 extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
@@ -405,7 +483,7 @@ extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch,
   if (rc) return rc;
   GEO_REQUIRE(r_cell > 0.f, "radius_graph: r_cell must be positive");
   GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
-  RgWs w = carve_rg(workspace, N, B);
+  RgWs w = carve_rg(workspace, N, B, max_num_neighbors);
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
                      workspace_bytes, w.bytes);
@@ -455,7 +533,7 @@ extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, 
   int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
   if (rc) return rc;
   GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
-  RgWs w = carve_rg(workspace, N, B);
+  RgWs w = carve_rg(workspace, N, B, max_num_neighbors);
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
                      workspace_bytes, w.bytes);
@@ -463,9 +541,16 @@ extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, 
   GEO_REQUIRE(row_out && col_out, "radius_graph: null outputs");
   hipStream_t st = as_stream(stream);
   const int K = static_cast<int>(max_num_neighbors);
+  const int64_t blocks = ceil_div(N, kRgEmitThreads);
+  if (w.list) {
+    const size_t lds = K <= kRgStageK ? static_cast<size_t>(K) * kRgEmitThreads * sizeof(int32_t) : 0;
+    hipLaunchKernelGGL(rg_compact, dim3(blocks), dim3(kRgEmitThreads), lds, st, w, x, N, batch, B,
+                       points_per_cloud, r2, K, loop, row_ptr, row_out, col_out);
+    GEO_LAUNCH_CHECK("rg_compact");
+    return GEO_OK;
+  }
   const int use_lds = K <= kRgLdsK ? 1 : 0;
   const size_t lds = use_lds ? static_cast<size_t>(K) * kRgEmitThreads * sizeof(int32_t) : 0;
-  const int64_t blocks = ceil_div(N, kRgEmitThreads);
   hipLaunchKernelGGL((rg_query<1>), dim3(blocks), dim3(kRgEmitThreads), lds, st, w, batch, B,
                      points_per_cloud, r2, K, loop, row_ptr, row_out, col_out, use_lds);
   GEO_LAUNCH_CHECK("rg_query<emit>");

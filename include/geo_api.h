@@ -110,12 +110,14 @@ int geo_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
  * mask may be NULL (all valid); nonzero bytes mark valid points.
  *
  * Two phases sharing one workspace:
- *   geo_radius_count builds the per-cloud uniform grid and writes row_ptr[0..N] (CSR offsets of
- *   the edges grouped by target, row_ptr[N] = E).  The caller reads E (the one host sync),
- *   allocates row_out[E], col_out[E] and calls geo_radius_emit with the same arguments and
- *   workspace.  Output order: targets ascending, sources ascending within a target.
+ *   geo_radius_count builds the per-cloud uniform grid, counts (and, when N * max_num_neighbors
+ *   fits the workspace bound, collects) the in-radius sources of every target and writes
+ *   row_ptr[0..N] (CSR offsets of the edges grouped by target, row_ptr[N] = E).  The caller
+ *   reads E (the one host sync), allocates row_out[E], col_out[E] and calls geo_radius_emit
+ *   with the same arguments and workspace.  Output order: targets ascending, sources ascending
+ *   within a target.
  */
-size_t geo_radius_workspace_bytes(int64_t N, int64_t B);
+size_t geo_radius_workspace_bytes(int64_t N, int64_t B, int64_t max_num_neighbors);
 int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
                      int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
                      int64_t max_num_neighbors, int loop, int64_t* row_ptr, void* workspace,
