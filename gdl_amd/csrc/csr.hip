@@ -10,7 +10,8 @@
 //                  peers with the same digit are found with 8 ballots, per-wave LDS counters
 //                  give the running count, a cross-wave prefix finishes the tile rank.
 // Targets outside [0, N) get key N and sort after all valid targets.  node_start/node_end come
-// from an atomic count per target and a scan (empty targets: start == end == prefix).
+// from binary searches in the sorted keys (node_start[n] = first position with key >= n), so
+// empty targets get start == end and no atomics are involved.
 #include "scan.hpp"
 
 namespace geo {
@@ -44,7 +45,17 @@ __global__ __launch_bounds__(kRxThreads) void radix_hist(const void* __restrict_
 #pragma unroll
   for (int i = 0; i < kRxItems; ++i) {
     const int64_t idx = base + static_cast<int64_t>(i) * kRxThreads + threadIdx.x;
-    if (idx < n) atomicAdd(&h[(fetch_key<FIRST>(keys, idx, N) >> shift) & 255u], 1u);
+    const bool valid = idx < n;
+    const uint32_t d = valid ? (fetch_key<FIRST>(keys, idx, N) >> shift) & 255u : 0u;
+    // lanes with the same digit add once (sorted input would otherwise serialise 64 atomics)
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    if (valid && __popcll(peers & lanemask_lt()) == 0) atomicAdd(&h[d], static_cast<uint32_t>(__popcll(peers)));
   }
   __syncthreads();
   hist[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x] = h[threadIdx.x];
@@ -116,13 +127,19 @@ __global__ __launch_bounds__(kRxThreads) void radix_scatter(
   }
 }
 
-__global__ void csr_count(const int64_t* __restrict__ col, int64_t E, int64_t N,
-                          int32_t* __restrict__ counts) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < E;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t c = col[e];
-    if (c >= 0 && c < N) atomicAdd(&counts[c], 1);
+// Thread n in [0, N] computes lb(n) = first sorted position with key >= n; that is
+// node_start[n] (n < N) and node_end[n - 1] (n > 0).
+__global__ void csr_bounds(const uint32_t* __restrict__ sorted_keys, int64_t E, int64_t N,
+                           int32_t* __restrict__ node_start, int32_t* __restrict__ node_end) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (n > N) return;
+  int64_t lo = 0, hi = E;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (sorted_keys[mid] < static_cast<uint32_t>(n)) lo = mid + 1; else hi = mid;
   }
+  if (n < N) node_start[n] = static_cast<int32_t>(lo);
+  if (n > 0) node_end[n - 1] = static_cast<int32_t>(lo);
 }
 
 int radix_passes(int64_t N) {
@@ -133,7 +150,6 @@ int radix_passes(int64_t N) {
 
 struct CsrWs {
   uint32_t *ka, *va, *kb, *vb, *hist, *hist_tiles;
-  int32_t *counts, *count_tiles;
   size_t bytes;
 };
 
@@ -147,8 +163,6 @@ CsrWs carve_csr(void* base, int64_t E, int64_t N) {
   w.vb = c.take<uint32_t>(E);
   w.hist = c.take<uint32_t>(256 * ntiles);
   w.hist_tiles = c.take<uint32_t>(scan_workspace_elems(256 * ntiles));
-  w.counts = c.take<int32_t>(N > 0 ? N : 1);
-  w.count_tiles = c.take<int32_t>(scan_workspace_elems(N));
   w.bytes = c.used;
   return w;
 }
@@ -177,21 +191,12 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
   GEO_REQUIRE(N == 0 || (node_start && node_end), "csr_build: null node_start/node_end");
   GEO_REQUIRE(E == 0 || (col && col_sorted && perm), "csr_build: null edge arrays");
 
-  // Offsets: count + scan.
-  if (N > 0) {
-    int rc = device_fill<int32_t>(w.counts, N, 0, st);
+  if (E == 0) {
+    if (N == 0) return GEO_OK;
+    int rc = device_fill<int32_t>(node_start, N, 0, st);
     if (rc) return rc;
-    if (E > 0) {
-      int64_t blocks = ceil_div(E, 256);
-      if (blocks > 8192) blocks = 8192;
-      hipLaunchKernelGGL(csr_count, dim3(blocks), dim3(256), 0, st, col, E, N, w.counts);
-      GEO_LAUNCH_CHECK("csr_count");
-    }
-    rc = device_exclusive_scan<int32_t, int32_t>(w.counts, N, node_start, node_end, false,
-                                                 w.count_tiles, st);
-    if (rc) return rc;
+    return device_fill<int32_t>(node_end, N, 0, st);
   }
-  if (E == 0) return GEO_OK;
 
   // Stable radix sort.
   const int passes = radix_passes(N);
@@ -222,6 +227,11 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
     GEO_LAUNCH_CHECK("radix_scatter");
     kin = kout;
     vin = vout;
+  }
+  if (N > 0) {
+    hipLaunchKernelGGL(csr_bounds, dim3(ceil_div(N + 1, 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint32_t*>(col_sorted), E, N, node_start, node_end);
+    GEO_LAUNCH_CHECK("csr_bounds");
   }
   return GEO_OK;
 }
