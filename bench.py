@@ -250,7 +250,7 @@ def main() -> int:
             gbs = bytes_fwd / (ms * 1e-3) / 1e9
             roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_SUM_TRAFFIC_BYTES,
-                    "kernel": "seg_fwd_kernel<float,16,SUM>", "ms_per_launch": round(ms, 4),
+                    "kernel": "seg_fwd_merge_kernel<float,16,SUM,perm>", "ms_per_launch": round(ms, 4),
                     "algorithmic_bytes": bytes_fwd}
             log(f"  fwd sum fp32: {ms:.4f} ms  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of peak)")
             for red in ("mean", "max"):
@@ -258,6 +258,7 @@ def main() -> int:
                 msr = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S, reduce=red),
                                iters, 5)
                 legs[f"c3_{red}_fp32_gbs"] = round((bytes_fwd + extra) / (msr * 1e-3) / 1e9, 1)
+                log(f"  fwd {red} fp32: {msr:.4f} ms  {legs[f'c3_{red}_fp32_gbs']} GB/s")
         if args.only in (None, "c3bf16"):
             mb = msg.bfloat16()
             bytes_b = E * C * 2 + S * C * 2 + (S + 1) * 4

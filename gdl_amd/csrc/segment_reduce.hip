@@ -1,19 +1,21 @@
 // segment_reduce.hip — sorted-segment sum / mean / max, forward and backward, for gfx950.
 //
-// Forward (replaces segment_reduce_sum_kernel, geoembodied/csrc/segment_reduce_kernel.cu:66-93):
-//   one wavefront owns `segs_per_wave` consecutive segments.  A row of C elements is read as
-//   16-byte (or narrower, when C or the pointers do not allow it) vectors; L lanes cover a row
-//   (L = next power of two >= vectors per row, at most 64) and the wave's R = 64/L lane groups
-//   take rows start+g, start+g+R, ... so one wave-wide load instruction moves R whole rows.
-//   The row ids of kUnroll = 8 rows per lane group are read first, then all 8 row loads are
-//   issued unconditionally (invalid ones read a valid row and are masked), so 8 KB per wave
-//   are in flight.  The wave's segment offsets arrive in one vector load.
-//   The R partial results are combined with a xor-butterfly; no atomics, no LDS.
+// Forward (replaces segment_reduce_sum_kernel, geoembodied/csrc/segment_reduce_kernel.cu:66-93).
+//   A row of C elements is read as 16-byte (or narrower, when C or the pointers do not allow
+//   it) vectors; L lanes cover a row (L = next power of two >= vectors per row, at most 64), so
+//   a wave has R = 64/L lane groups and one wave-wide load instruction moves R whole rows.
+//   Two kernels:
+//   * seg_fwd_merge_kernel (many short segments, the graph-aggregation case): a wave takes up
+//     to L consecutive segments and splits their rows evenly over its lane groups (merge path);
+//     see the comment above the kernel.
+//   * seg_fwd_kernel (few long segments, the pooling case): a wave walks its segments one at a
+//     time; the lane groups take rows start+g, start+g+R, ..., 8 rows per group in flight, and
+//     the R partial results are combined with a xor-butterfly.
 // Backward (replaces the ATen gather + un-permute of geoembodied/functional/segment_reduce.py:
 //   259-270): one lane group per sorted edge row e, grad_msg[perm[e]] = f(grad_out[col_sorted[e]]).
 //
 // Sum / mean accumulate in fp32 (fp64 for double) in ascending row order inside a lane group;
-// the butterfly order is fixed, so results are bitwise reproducible run to run.
+// partial results are combined in a fixed order, so results are bitwise reproducible run to run.
 // Every index read from memory is range-checked, so inconsistent CSR arrays cannot make a
 // kernel access memory outside the given tensors.
 #include "common.hpp"
@@ -230,6 +232,281 @@ __global__ __launch_bounds__(kSegThreads) void seg_fwd_kernel(
   }
 }
 
+// Forward for many short segments: merge-path split of a wave's rows over its lane groups.
+//
+// A wave owns n <= L consecutive segments (L = lanes per row); every lane group holds the whole
+// segment table (lane vl <-> segment vl) and the inclusive prefix of the segment lengths, so the
+// wave's rows form one "flat" range [0, T).  Group g streams the flat positions
+// [g*c, min((g+1)*c, T)), c = ceil(T / R): every group has the same amount of work whatever the
+// segment sizes are.  The segment of a flat position f is the number of prefixes <= f (one
+// ballot) and its row is base[j] + f (one lane permute).  merge_unroll() rows per group are
+// loaded per step, and the row ids of the next step are fetched while those rows are in flight.
+// A segment is written by the group holding its first row; a segment that continues past the
+// end of a group's range is completed with the partial results of the following groups, which
+// park them in LDS (in group order, so the result does not depend on timing).
+//
+// Tuning (measured on MI355X, C3 shapes): one wave per workgroup schedules best; 8 rows per
+// group per step for 4/8-byte types, 4 for bf16 (more accumulators) and for max (more state);
+// about 16 KB of rows per wave (kMergeWaveBytes) balances per-wave overhead against tail effects.
+constexpr int kMergeThreads = kWave;
+constexpr int64_t kMergeWaveBytes = 16384;
+template <typename T, int OP>
+constexpr int merge_unroll() { return (OP == GEO_REDUCE_MAX || sizeof(T) == 2) ? 4 : 8; }
+
+template <typename T, int VB, int OP>
+struct MergeSlot {
+  using A = typename AccT<T>::type;
+  static constexpr int EPV = VB / static_cast<int>(sizeof(T));
+  A acc[EPV];
+  int first[OP == GEO_REDUCE_MAX ? EPV : 1];
+  int cnt[OP == GEO_REDUCE_MAX ? EPV : 1];
+};
+
+template <typename T, int VB, int OP, bool PERM>
+__global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
+    const T* __restrict__ msg, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_end, int32_t E,
+    int64_t S, int64_t C, int vpr, int log_l, int segs_per_wave, T* __restrict__ out,
+    int32_t* __restrict__ arg, int tie_mode) {
+  using A = typename AccT<T>::type;
+  using V = Vec<T, VB>;
+  constexpr int EPV = V::EPV;
+  constexpr bool MAX = OP == GEO_REDUCE_MAX;
+  constexpr int U = merge_unroll<T, OP>();
+  __shared__ MergeSlot<T, VB, OP> park[kWave];
+
+  const int lane = lane_id();
+  const int L = 1 << log_l;
+  const int log_r = 6 - log_l;
+  const int R = 1 << log_r;
+  const int g = lane >> log_l;
+  const int vl = lane & (L - 1);
+  const int gbase = g << log_l;
+  const uint64_t gmask = log_l == 6 ? ~0ull : ((1ull << L) - 1);
+  const int64_t s_begin = static_cast<int64_t>(blockIdx.x) * segs_per_wave;
+  if (s_begin >= S) return;
+  const int nseg = static_cast<int>(min(S - s_begin, static_cast<int64_t>(segs_per_wave)));
+
+  // Segment table, replicated in every group: lane vl <-> segment s_begin + vl.
+  const bool has = vl < nseg;
+  int st = 0, n = 0;
+  if (has) {
+    st = clamp_i(seg_start[s_begin + vl], 0, E);
+    n = clamp_i(seg_end[s_begin + vl], st, E) - st;
+  }
+  int incl = n;
+  for (int d = 1; d < L; d <<= 1) {
+    const int o = __shfl_up(incl, d, kWave);
+    if (vl >= d) incl += o;
+  }
+  const int excl = incl - n;
+  const int T_rows = __shfl(incl, L - 1, kWave);
+  const int base = st - excl;
+  const int key = has ? incl : 0x7fffffff;
+  const int chunk = (T_rows + R - 1) >> log_r;
+  const int lo = min(g * chunk, T_rows);
+  const int hi = min(lo + chunk, T_rows);
+  const int ncol_iter = (vpr + L - 1) >> log_l;
+
+  // Local segment of flat position f for this group (group-uniform result).
+  auto seg_of = [&](int f) -> int {
+    return static_cast<int>(__popcll((__ballot(key <= f) >> gbase) & gmask));
+  };
+  auto lane_of = [&](int j) { return gbase + (j < L ? j : L - 1); };
+
+  // Empty segments: zeros (and arg -1 for max); segment j is written by group j mod R.
+  {
+    uint64_t mine = (__ballot(has && n == 0) >> gbase) & gmask;
+    uint64_t sel = 0;
+    for (int j = g; j < L; j += R) sel |= 1ull << j;
+    mine &= sel;
+    while (__ballot(mine != 0)) {
+      if (mine != 0) {
+        const int64_t s = s_begin + __builtin_ctzll(mine);
+        mine &= mine - 1;
+        for (int ci = 0; ci < ncol_iter; ++ci) {
+          const int vb = vl + ci * L;
+          if (vb >= vpr) continue;
+          V z;
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) z.e[i] = from_acc<T>(A(0));
+          z.store(out + s * C + static_cast<int64_t>(vb) * EPV);
+          if constexpr (MAX) {
+            IVec<EPV> a;
+#pragma unroll
+            for (int i = 0; i < EPV; ++i) a.e[i] = -1;
+            a.store(arg + s * C + static_cast<int64_t>(vb) * EPV);
+          }
+        }
+      }
+    }
+  }
+  if (T_rows == 0) return;
+  const int steps = (chunk + U - 1) / U;
+
+  for (int ci = 0; ci < ncol_iter; ++ci) {
+    const int vb = vl + ci * L;
+    const bool col_ok = vb < vpr;
+    const int64_t col_off = col_ok ? static_cast<int64_t>(vb) * EPV : 0;
+    A acc[EPV];
+    int first[EPV];
+    int cnt[EPV];
+    int jcur = -1;
+    auto reset = [&]() {
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        acc[i] = MAX ? -__builtin_inf() : A(0);
+        first[i] = 0x7fffffff;
+        cnt[i] = 0;
+      }
+    };
+    auto write_out = [&](int j) {
+      // every lane of the group takes part in the permute, including lanes without a column
+      const int nj = OP == GEO_REDUCE_MEAN ? __shfl(n, lane_of(j), kWave) : 0;
+      if (!col_ok) return;
+      const int64_t s = s_begin + j;
+      V res;
+      if constexpr (MAX) {
+        IVec<EPV> a;
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          res.e[i] = cnt[i] == 0 ? from_acc<T>(A(0)) : from_acc<T>(acc[i]);
+          a.e[i] = cnt[i] == 0 ? -1 : ((cnt[i] == 1 || tie_mode == 1) ? first[i] : -cnt[i]);
+        }
+        a.store(arg + s * C + col_off);
+      } else if constexpr (OP == GEO_REDUCE_MEAN) {
+        const A denom = static_cast<A>(nj > 1 ? nj : 1);
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) res.e[i] = from_acc<T>(acc[i] / denom);
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) res.e[i] = from_acc<T>(acc[i]);
+      }
+      res.store(out + s * C + col_off);
+    };
+    // Park this group's partial of a segment that began in an earlier group's range.
+    auto park_partial = [&]() {
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        park[lane].acc[i] = acc[i];
+        if constexpr (MAX) {
+          park[lane].first[i] = first[i];
+          park[lane].cnt[i] = cnt[i];
+        }
+      }
+    };
+    // Segment jcur is finished inside this range: write it, or park it if it began earlier.
+    auto finish = [&]() {
+      const int ex = __shfl(excl, lane_of(jcur), kWave);
+      if (ex >= lo) write_out(jcur);
+      else park_partial();
+    };
+
+    auto locate = [&](int f0, int* e, int* rows) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int f = f0 + u;
+        const int b = __shfl(base, lane_of(seg_of(f)), kWave);
+        e[u] = f < hi ? b + f : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) rows[u] = PERM ? perm[e[u]] : e[u];
+    };
+
+    reset();
+    int e[U], rows[U];
+    locate(lo, e, rows);
+    for (int k = 0; k < steps; ++k) {
+      const int f0 = lo + k * U;
+      V buf[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool ok = f0 + u < hi && static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E);
+        buf[u].load(msg + static_cast<int64_t>(ok ? rows[u] : 0) * C + col_off);
+      }
+      int ecur[MAX ? U : 1];
+      uint32_t rok = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if constexpr (MAX) ecur[u] = e[u];
+        rok |= static_cast<uint32_t>(static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E)) << u;
+      }
+      locate(f0 + U, e, rows);
+      // Row values are consumed through selects only, so all U loads stay ahead of first use.
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int f = f0 + u;
+        const bool live = f < hi;
+        const int j = seg_of(f);
+        if (live && j != jcur) {
+          if (jcur >= 0) finish();
+          reset();
+          jcur = j;
+        }
+        const bool take = live && ((rok >> u) & 1u);
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          const A v = to_acc(buf[u].e[i]);
+          if constexpr (MAX) {
+            const bool gt = take && max_gt(v, acc[i]);
+            const bool eq = take && !gt && max_eq(v, acc[i]);
+            const int pos = ecur[MAX ? u : 0];
+            first[i] = (gt || (eq && cnt[i] == 0)) ? pos : first[i];
+            cnt[i] = gt ? 1 : cnt[i] + (eq ? 1 : 0);
+            acc[i] = gt ? v : acc[i];
+          } else {
+            acc[i] += take ? v : A(0);
+          }
+        }
+      }
+    }
+
+    // Last segment of the range.  If it began earlier, park it; if it ends here, write it;
+    // otherwise it continues into the following groups, whose parked partials complete it.
+    bool open = false;
+    if (jcur >= 0) {
+      const int ex = __shfl(excl, lane_of(jcur), kWave);
+      const int in = __shfl(incl, lane_of(jcur), kWave);
+      if (ex < lo) park_partial();
+      else if (in <= hi) write_out(jcur);
+      else open = true;
+    }
+    if (R > 1) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (open) {
+        const int in = __shfl(incl, lane_of(jcur), kWave);
+        for (int k = g + 1; k < R; ++k) {
+          const int lo_k = min(k * chunk, T_rows);
+          if (lo_k >= in) break;                       // segment ended before group k
+          const MergeSlot<T, VB, OP>& p = park[(k << log_l) + vl];
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) {
+            if constexpr (MAX) {
+              const A o = p.acc[i];
+              if (p.cnt[i] > 0) {
+                if (cnt[i] == 0 || max_gt(o, acc[i])) {
+                  acc[i] = o; first[i] = p.first[i]; cnt[i] = p.cnt[i];
+                } else if (max_eq(o, acc[i])) {
+                  cnt[i] += p.cnt[i];
+                }
+              }
+            } else {
+              acc[i] += p.acc[i];
+            }
+          }
+        }
+        write_out(jcur);
+      }
+      if (ci + 1 < ncol_iter) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+  }
+}
+
 template <typename T, int VB, int OP>
 __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
     const T* __restrict__ grad_out, const T* __restrict__ msg, const T* __restrict__ fwd_out,
@@ -353,17 +630,39 @@ template <typename T, int OP>
 int launch_fwd(const Layout& lay, const T* msg, const int32_t* perm, const int32_t* ns,
                const int32_t* ne, int32_t E, int64_t S, int64_t C, T* out, int32_t* arg,
                int tie_mode, hipStream_t st) {
-  int spw = static_cast<int>(ceil_div(S, 32768));
-  if (spw > 64) spw = 64;
-  if (spw < 1) spw = 1;
-  const int64_t waves = ceil_div(S, spw);
-  const int64_t blocks = ceil_div(waves, kSegWaves);
+  // Many short segments (the common case: graph aggregation) -> merge-path waves of at most L
+  // segments; few long segments (pooling) -> whole waves cooperating on one segment at a time.
+  const bool merge = S >= 4096 && E <= 128 * S;
+  int spw;
+  int64_t blocks;
+  if (merge) {
+    const int L = 1 << lay.log_l;
+    const double wave_bytes = (E > S ? static_cast<double>(E) / S : 1.0) * C * sizeof(T);
+    spw = static_cast<int>(static_cast<double>(kMergeWaveBytes) / wave_bytes + 0.5);
+    if (spw > L) spw = L;
+    if (spw < 1) spw = 1;
+    blocks = ceil_div(S, spw);
+  } else {
+    spw = static_cast<int>(ceil_div(S, 32768));
+    if (spw > 64) spw = 64;
+    if (spw < 1) spw = 1;
+    blocks = ceil_div(ceil_div(S, spw), kSegWaves);
+  }
 #define GEO_FWD_CASE(VBV)                                                                   \
   case VBV:                                                                                 \
     if constexpr (VBV >= static_cast<int>(sizeof(T))) {                                     \
-      hipLaunchKernelGGL((seg_fwd_kernel<T, VBV, OP>), dim3(blocks), dim3(kSegThreads), 0, st, \
-                         msg, perm, ns, ne, E, S, C, lay.vpr, lay.log_l, spw, out, arg,       \
-                         tie_mode);                                                         \
+      if (merge && perm)                                                                    \
+        hipLaunchKernelGGL((seg_fwd_merge_kernel<T, VBV, OP, true>), dim3(blocks),           \
+                           dim3(kMergeThreads), 0, st, msg, perm, ns, ne, E, S, C, lay.vpr,   \
+                           lay.log_l, spw, out, arg, tie_mode);                             \
+      else if (merge)                                                                       \
+        hipLaunchKernelGGL((seg_fwd_merge_kernel<T, VBV, OP, false>), dim3(blocks),          \
+                           dim3(kMergeThreads), 0, st, msg, perm, ns, ne, E, S, C, lay.vpr,   \
+                           lay.log_l, spw, out, arg, tie_mode);                             \
+      else                                                                                  \
+        hipLaunchKernelGGL((seg_fwd_kernel<T, VBV, OP>), dim3(blocks), dim3(kSegThreads), 0,  \
+                           st, msg, perm, ns, ne, E, S, C, lay.vpr, lay.log_l, spw, out, arg, \
+                           tie_mode);                                                       \
     }                                                                                       \
     break;
   switch (lay.vb) {

@@ -255,6 +255,69 @@ def test_mean_and_max_match_reference_call_sites(dev):
     assert torch.allclose(mt.grad, mr.grad, atol=1e-6)
 
 
+# ------------------------------------------------------------- many-segment forward path ---
+# S >= 4096 segments of average length <= 128 take the merge-path kernel: a wave's rows are
+# split evenly over its lane groups, so segments cross group boundaries and are completed from
+# partial results.  Layouts cover every group count R = 64 / L from 1 to 64.
+
+MERGE_LAYOUTS = [  # C, dtype  (lanes per row L)
+    (1, torch.float32),      # L = 1, R = 64
+    (3, torch.float32),      # L = 4
+    (32, torch.float32),     # L = 8
+    (128, torch.float32),    # L = 32
+    (300, torch.float32),    # L = 64, two column passes
+    (128, torch.bfloat16),   # L = 16
+    (7, torch.bfloat16),     # L = 8, 2-byte vectors
+    (64, torch.float64),     # L = 32
+]
+
+
+def _merge_sizes(kind, S, rng):
+    if kind == "zipf":
+        sz = np.minimum(rng.zipf(1.3, S), 64)
+        sz[rng.random(S) < 0.4] = 0
+    elif kind == "long":   # a few segments spanning many groups and waves' worth of rows
+        sz = rng.integers(0, 6, S)
+        sz[rng.choice(S, 8, replace=False)] = rng.integers(300, 3000, 8)
+    else:                  # "ones": every segment a single row
+        sz = np.ones(S, dtype=np.int64)
+    return sz.astype(np.int64)
+
+
+@pytest.mark.parametrize("C,dtype", MERGE_LAYOUTS)
+@pytest.mark.parametrize("kind", ["zipf", "long", "ones"])
+@pytest.mark.parametrize("reduce", ["sum", "mean", "max"])
+def test_merge_path_vs_oracle(dev, C, dtype, kind, reduce):
+    from gdl_amd.csrc import segment_reduce_forward_hip
+    rng = np.random.default_rng(C * 7 + len(kind))
+    S = 6000
+    sz = _merge_sizes(kind, S, rng)
+    ne = np.cumsum(sz)
+    ns = ne - sz
+    E = int(ne[-1])
+    assert E <= 128 * S
+    perm = rng.permutation(E).astype(np.int32)
+    msg = torch.from_numpy(rng.standard_normal((E, C)))
+    if reduce == "max":
+        msg = (msg * 2).round() / 2
+    msg = msg.to(dtype)
+    for p in (perm, None):
+        out, arg = segment_reduce_forward_hip(
+            msg.to(dev), None if p is None else torch.from_numpy(p).to(dev),
+            torch.from_numpy(ns.astype(np.int32)).to(dev),
+            torch.from_numpy(ne.astype(np.int32)).to(dev), S, reduce)
+        ref, aux = oracle.segment_reduce_fwd(_np(msg), p, ns, ne, S, reduce)
+        got = _np(out).astype(np.float64)
+        if reduce == "max":
+            np.testing.assert_array_equal(got, ref)
+            np.testing.assert_array_equal(arg.cpu().numpy(), aux)
+        else:
+            bound = TOL[dtype] * aux + 1e-30
+            if dtype == torch.bfloat16:
+                bound = bound + np.abs(ref) * 2.0 ** -8
+            assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) - bound))
+
+
 # ------------------------------------------------------------------- full-size C3 properties ---
 
 def test_c3_full_size(dev):
