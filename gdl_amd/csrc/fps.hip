@@ -18,7 +18,7 @@
 // the lowest index among the lanes holding it, then one LDS record per wave, double-buffered
 // by iteration parity so that a single barrier per iteration suffices.  Squared distances are
 // non-negative floats, whose bit patterns order like the values.
-#include "scan.hpp"
+#include "radix.hpp"
 
 namespace geo {
 namespace {
@@ -454,6 +454,320 @@ __global__ __launch_bounds__(kFpsStreamThreads) void fps_stream_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------- large clouds ---
+// Clouds larger than the register kernel holds (up to kFpsLargeMaxPoints).  The batch is
+// reordered by a device radix sort on (cloud + 1, Morton code of the point in its cloud's box),
+// which keeps every cloud on its own index range, and each cloud is cut into buckets of 64
+// consecutive sorted points.  Positions (with the original index) and running min distances
+// stay in the workspace, 20 bytes per point, which for one cloud fits the L2 of the XCD that
+// runs it.  One 1024-thread workgroup per cloud; lane l of wave w holds the records of buckets
+// w + 16 (l + 64 r), r < kFpsLargeSlots: box, max min-distance, lowest index attaining it and
+// that point's position.  Per iteration each wave tests its buckets with the exact lower bound
+// above, reloads and updates only the buckets the new centroid can change (four at a time, so
+// their loads overlap), recomputes its best (distance, index) only when one of its buckets
+// changed, and the workgroup agrees on the winner with one LDS 64-bit atomic max per wave on
+// (bits << 32) | (index complement << 4 | wave) and one barrier.
+constexpr int kFpsLargeThreads = 1024;
+constexpr int kFpsLargeWaves = kFpsLargeThreads / kWave;
+constexpr int kFpsLargeSlots = 3;
+constexpr int64_t kFpsLargeMaxPoints =
+    static_cast<int64_t>(kFpsLargeSlots) * kFpsLargeThreads * kWave;  // 196,608
+constexpr uint32_t kFpsLargeIdxMask = (1u << 18) - 1;                  // local index < 2^18
+constexpr int64_t kFpsLargeMaxClouds = (1 << 11) - 2;                  // cloud id + 1 in 11 bits
+
+__device__ __forceinline__ uint32_t spread10(uint32_t v) {  // 10 bits -> every third bit
+  v &= 0x3ffu;
+  v = (v | (v << 16)) & 0x030000ffu;
+  v = (v | (v << 8)) & 0x0300f00fu;
+  v = (v | (v << 4)) & 0x030c30c3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+
+// bbox[6 b .. 6 b + 5] = (lo x, lo y, lo z, hi x, hi y, hi z) of cloud b; one block per cloud.
+__global__ __launch_bounds__(kFpsLargeThreads) void fps_large_bbox_kernel(
+    const float* __restrict__ pos, const int64_t* __restrict__ ptr, float* __restrict__ bbox) {
+  __shared__ uint32_t red[6][kFpsLargeWaves];
+  const int b = blockIdx.x;
+  const int64_t s = ptr[b], e = ptr[b + 1];
+  const int t = threadIdx.x, w = t / kWave;
+  uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
+  for (int64_t i = s + t; i < e; i += kFpsLargeThreads) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const uint32_t kk = float_order_key(pos[3 * i + a]);
+      mn[a] = min(mn[a], kk);
+      mx[a] = max(mx[a], kk);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    mn[a] = wave_min_u32(mn[a]);
+    mx[a] = wave_max_u32(mx[a]);
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
+  }
+  __syncthreads();
+  if (t < 6) {
+    uint32_t v = red[t][0];
+    for (int ww = 1; ww < kFpsLargeWaves; ++ww) v = t < 3 ? min(v, red[t][ww]) : max(v, red[t][ww]);
+    bbox[6 * b + t] = (e > s) ? float_from_order_key(v) : 0.f;
+  }
+}
+
+// keys[i] = (cloud + 1) << 3 mbits | Morton code (mbits per axis) of point i in its cloud's
+// box; points before the first cloud get cloud field 0, points after the last B + 1.
+__global__ void fps_large_keys_kernel(const float* __restrict__ pos, const int64_t* __restrict__ ptr,
+                                      int64_t B, int64_t N, const float* __restrict__ bbox,
+                                      int mbits, uint32_t* __restrict__ keys) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  int64_t lo = 0, hi = B + 1;  // number of ptr entries <= i
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ptr[mid] <= i) lo = mid + 1; else hi = mid;
+  }
+  uint32_t code = 0;
+  if (lo >= 1 && lo <= B) {
+    const float* bb = bbox + 6 * (lo - 1);
+    const float cells = static_cast<float>(1 << mbits);
+    uint32_t c[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const float ext = bb[3 + a] - bb[a];
+      const float q = ext > 0.f ? (pos[3 * i + a] - bb[a]) * (cells / ext) : 0.f;
+      const int ci = static_cast<int>(q);
+      c[a] = static_cast<uint32_t>(ci < 0 ? 0 : (ci >= (1 << mbits) ? (1 << mbits) - 1 : ci));
+    }
+    code = spread10(c[0]) | (spread10(c[1]) << 1) | (spread10(c[2]) << 2);
+  }
+  keys[i] = (static_cast<uint32_t>(lo) << (3 * mbits)) | code;
+}
+
+// Sorted position j <- original point order[j]: (x, y, z, original index bits); md = +inf.
+__global__ void fps_large_gather_kernel(const float* __restrict__ pos,
+                                        const uint32_t* __restrict__ order, int64_t N,
+                                        float4* __restrict__ q, float* __restrict__ md) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  const uint32_t i = order[j];
+  q[j] = make_float4(pos[3 * static_cast<int64_t>(i)], pos[3 * static_cast<int64_t>(i) + 1],
+                     pos[3 * static_cast<int64_t>(i) + 2], __uint_as_float(i));
+  md[j] = __builtin_inff();
+}
+
+__global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
+    const float* __restrict__ pos, const float4* __restrict__ Qall, float* __restrict__ Mall,
+    const int64_t* __restrict__ ptr, const int64_t* __restrict__ out_ptr,
+    int64_t* __restrict__ out_idx) {
+  constexpr int S = kFpsLargeSlots;
+  __shared__ unsigned long long slots[3];
+  __shared__ float4 cand[2][kFpsLargeWaves];
+  const int b = blockIdx.x;
+  const int64_t start = ptr[b];
+  const int n = static_cast<int>(ptr[b + 1] - start);
+  const int64_t o0 = out_ptr[b];
+  const int k = static_cast<int>(out_ptr[b + 1] - o0);
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = lane_id();
+  if (k <= 0 || n <= 0) return;
+  if (k >= n) {
+    for (int i = t; i < n; i += kFpsLargeThreads) out_idx[o0 + i] = start + i;
+    return;
+  }
+  const float4* Q = Qall + start;
+  float* M = Mall + start;
+  const int nb = (n + kWave - 1) / kWave;
+  const uint32_t ustart = static_cast<uint32_t>(start);
+
+  // Bucket records of this lane (empty buckets: +inf box, max 0, never tested or chosen).
+  float blx[S], bly[S], blz[S], bhx[S], bhy[S], bhz[S], bcx[S], bcy[S], bcz[S];
+  uint32_t bmax[S], bidx[S];
+#pragma unroll
+  for (int r = 0; r < S; ++r) {
+    blx[r] = bly[r] = blz[r] = __builtin_inff();
+    bhx[r] = bhy[r] = bhz[r] = -__builtin_inff();
+    bcx[r] = bcy[r] = bcz[r] = 0.f;
+    bmax[r] = 0u;
+    bidx[r] = 0xffffffffu;
+    const int bk = w + kFpsLargeWaves * (lane + kWave * r);
+    if (bk < nb) {
+      const int q0 = bk * kWave;
+      const int q1 = min(q0 + kWave, n);
+#pragma unroll 8
+      for (int q = q0; q < q1; ++q) {
+        const float4 p = Q[q];
+        blx[r] = fminf(blx[r], p.x); bly[r] = fminf(bly[r], p.y); blz[r] = fminf(blz[r], p.z);
+        bhx[r] = fmaxf(bhx[r], p.x); bhy[r] = fmaxf(bhy[r], p.y); bhz[r] = fmaxf(bhz[r], p.z);
+        const uint32_t li = __float_as_uint(p.w) - ustart;
+        if (li < bidx[r]) { bidx[r] = li; bcx[r] = p.x; bcy[r] = p.y; bcz[r] = p.z; }
+      }
+      bmax[r] = 0x7f800000u;  // +inf: every bucket takes part in the first update
+    }
+  }
+  float cx = pos[3 * start], cy = pos[3 * start + 1], cz = pos[3 * start + 2];
+  if (t == 0) {
+    out_idx[o0] = start;
+    slots[0] = slots[1] = slots[2] = 0ull;
+  }
+  unsigned long long best_key = 0ull;
+  float4 best_c = make_float4(0.f, 0.f, 0.f, 0.f);
+  bool dirty = true;
+  __syncthreads();
+
+  for (int it = 1; it < k; ++it) {
+    uint64_t act[S];
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+      float gx, gy, gz;
+      {
+#pragma clang fp contract(off)
+        gx = fmaxf(fmaxf(blx[r] - cx, cx - bhx[r]), 0.f);
+        gy = fmaxf(fmaxf(bly[r] - cy, cy - bhy[r]), 0.f);
+        gz = fmaxf(fmaxf(blz[r] - cz, cz - bhz[r]), 0.f);
+      }
+      const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
+      act[r] = __ballot(__float_as_uint(lb) < bmax[r]);
+    }
+    while (act[0] | act[1] | act[2]) {
+      // up to four affected buckets of this wave per round, their loads issued together
+      constexpr int G = 4;
+      int rr[G], ll[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        rr[j] = act[0] ? 0 : (act[1] ? 1 : (act[2] ? 2 : -1));
+        ll[j] = 0;
+        if (rr[j] >= 0) {
+          const uint64_t m = rr[j] == 0 ? act[0] : (rr[j] == 1 ? act[1] : act[2]);
+          ll[j] = __builtin_ctzll(m);
+          const uint64_t cleared = m & (m - 1);
+          if (rr[j] == 0) act[0] = cleared; else if (rr[j] == 1) act[1] = cleared; else act[2] = cleared;
+        }
+      }
+      float4 p[G];
+      float mo[G];
+      bool v[G];
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        const int q = (w + kFpsLargeWaves * (ll[j] + kWave * (rr[j] < 0 ? 0 : rr[j]))) * kWave + lane;
+        v[j] = rr[j] >= 0 && q < n;
+        p[j] = Q[v[j] ? q : 0];
+        mo[j] = M[v[j] ? q : 0];
+      }
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (rr[j] < 0) continue;  // wave-uniform
+        const int q = (w + kFpsLargeWaves * (ll[j] + kWave * rr[j])) * kWave + lane;
+        const float d = sqdist(p[j].x, p[j].y, p[j].z, cx, cy, cz);
+        const float m = __builtin_amdgcn_fmed3f(d, mo[j], -__builtin_inff());
+        if (v[j] && m < mo[j]) M[q] = m;
+        const uint32_t bits = v[j] ? __float_as_uint(m) : 0u;
+        const uint32_t bm = wave_max_u32(bits);
+        const uint32_t li = __float_as_uint(p[j].w) - ustart;
+        const uint32_t ii = wave_min_u32(v[j] && bits == bm ? li : 0xffffffffu);
+        const uint64_t src = __ballot(v[j] && bits == bm && li == ii);
+        const int sl = __builtin_ctzll(src | (1ull << 63));
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].x), sl));
+        const float y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].y), sl));
+        const float z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].z), sl));
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+          if (r == rr[j] && lane == ll[j]) {
+            bmax[r] = bm; bidx[r] = ii; bcx[r] = x; bcy[r] = y; bcz[r] = z;
+          }
+        }
+      }
+      dirty = true;
+    }
+    if (dirty) {  // the wave's best record: largest max, then lowest index
+      uint32_t lh = 0u, llo = 0u;
+      float ex = 0.f, ey = 0.f, ez = 0.f;
+#pragma unroll
+      for (int r = 0; r < S; ++r) {
+        const uint32_t h = bmax[r];
+        const uint32_t l = bidx[r] <= kFpsLargeIdxMask
+                               ? ((kFpsLargeIdxMask - bidx[r]) << 4) | static_cast<uint32_t>(w)
+                               : 0u;
+        if (h > lh || (h == lh && l > llo)) { lh = h; llo = l; ex = bcx[r]; ey = bcy[r]; ez = bcz[r]; }
+      }
+      const uint32_t wh = wave_max_u32(lh);
+      const uint32_t wl = wave_max_u32(lh == wh ? llo : 0u);
+      const int sl = __builtin_ctzll(__ballot(lh == wh && llo == wl) | (1ull << 63));
+      best_key = (static_cast<unsigned long long>(wh) << 32) | wl;
+      best_c = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), sl)),
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ey), sl)),
+                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ez), sl)), 0.f);
+      dirty = false;
+    }
+    const int ps = it % 3;
+    if (lane == 0) {
+      cand[it & 1][w] = best_c;
+      atomicMax(&slots[ps], best_key);
+    }
+    if (t == 0) slots[ps == 2 ? 0 : ps + 1] = 0ull;
+    __syncthreads();
+    const unsigned long long key = slots[ps];
+    const uint32_t low = static_cast<uint32_t>(key);
+    const float4 c = cand[it & 1][low & 15u];
+    cx = c.x; cy = c.y; cz = c.z;
+    if (t == 0) out_idx[o0 + it] = start + (kFpsLargeIdxMask - ((low >> 4) & kFpsLargeIdxMask));
+  }
+}
+
+struct FpsLargeWs {
+  float4* q;
+  float* md;
+  float* bbox;
+  uint32_t *keys, *skeys, *order;
+  RadixBuffers rx;
+};
+
+FpsLargeWs carve_fps_large(void* base, int64_t B, int64_t N, size_t* bytes) {
+  Carver c(base);
+  FpsLargeWs w;
+  w.q = c.take<float4>(N);
+  w.md = c.take<float>(N);
+  w.bbox = c.take<float>(6 * (B > 0 ? B : 1));
+  w.keys = c.take<uint32_t>(N);
+  w.skeys = c.take<uint32_t>(N);
+  w.order = c.take<uint32_t>(N);
+  w.rx = carve_radix(c, N);
+  *bytes = c.used;
+  return w;
+}
+
+bool fps_use_large(int64_t B, int64_t max_cloud) {
+  return max_cloud > 64 * kFpsThreads && max_cloud <= kFpsLargeMaxPoints && B <= kFpsLargeMaxClouds;
+}
+
+int launch_large(const float* pos, int64_t N, const int64_t* ptr, const int64_t* out_ptr,
+                 int64_t B, int64_t* out, void* workspace, hipStream_t st) {
+  size_t bytes = 0;
+  const FpsLargeWs w = carve_fps_large(workspace, B, N, &bytes);
+  hipLaunchKernelGGL(fps_large_bbox_kernel, dim3(B), dim3(kFpsLargeThreads), 0, st, pos, ptr, w.bbox);
+  GEO_LAUNCH_CHECK("fps_large_bbox_kernel");
+  int cbits = 0;
+  while ((static_cast<uint64_t>(B + 1) >> cbits) != 0) ++cbits;  // holds cloud field 0 .. B + 1
+  int mbits = (32 - cbits) / 3;
+  if (mbits > 10) mbits = 10;
+  const int bits = cbits + 3 * mbits;
+  const unsigned grid = static_cast<unsigned>(ceil_div(N, 256));
+  hipLaunchKernelGGL(fps_large_keys_kernel, dim3(grid), dim3(256), 0, st, pos, ptr, B, N, w.bbox,
+                     mbits, w.keys);
+  GEO_LAUNCH_CHECK("fps_large_keys_kernel");
+  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, (bits + 7) / 8, w.skeys, w.order, w.rx, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(fps_large_gather_kernel, dim3(grid), dim3(256), 0, st, pos, w.order, N, w.q, w.md);
+  GEO_LAUNCH_CHECK("fps_large_gather_kernel");
+  hipLaunchKernelGGL(fps_large_kernel, dim3(B), dim3(kFpsLargeThreads), 0, st, pos, w.q, w.md, ptr,
+                     out_ptr, out);
+  GEO_LAUNCH_CHECK("fps_large_kernel");
+  return GEO_OK;
+}
+
 template <int PTS>
 int launch_register(const float* pos, const int64_t* ptr, const int64_t* out_ptr, int64_t B,
                     int64_t max_cloud, int64_t* out, hipStream_t st) {
@@ -488,7 +802,12 @@ extern "C" int geo_fps_prepare(const int64_t* ptr, const int64_t* k_per_batch, i
 }
 
 extern "C" size_t geo_fps_workspace_bytes(int64_t B, int64_t N_total, int64_t max_cloud) {
-  (void)B;
+  if (B < 0 || N_total < 0 || max_cloud < 0) return 0;
+  if (fps_use_large(B, max_cloud)) {
+    size_t bytes = 0;
+    carve_fps_large(nullptr, B, N_total, &bytes);
+    return bytes;
+  }
   if (max_cloud > 64 * kFpsThreads) return static_cast<size_t>(N_total > 0 ? N_total : 1) * 4;
   return 0;
 }
@@ -524,6 +843,8 @@ extern "C" int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr,
   if (per <= 16) return launch_register<16>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   if (per <= 32) return launch_register<32>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
   if (per <= 64) return launch_register<64>(pos, ptr, out_ptr, B, max_cloud, out_idx, st);
+  if (fps_use_large(B, max_cloud))
+    return launch_large(pos, N_total, ptr, out_ptr, B, out_idx, workspace, st);
   hipLaunchKernelGGL(fps_stream_kernel, dim3(B), dim3(kFpsStreamThreads), 0, st, pos, ptr,
                      out_ptr, out_idx, static_cast<float*>(workspace));
   GEO_LAUNCH_CHECK("fps_stream_kernel");

@@ -55,6 +55,22 @@ def test_fps_vs_oracle(dev, sizes, ks, seed):
     _fps_check(dev, pos, _ptr(sizes), torch.tensor(ks))
 
 
+def test_fps_large_clouds(dev):
+    """Clouds above 16384 points take the Morton-bucket path with points in the workspace:
+    several clouds, empty and tiny clouds, points outside every cloud, k = n and k = 0."""
+    g = torch.Generator().manual_seed(11)
+    pos = torch.randn(47100, 3, generator=g) * torch.tensor([30.0, 5.0, 1.0])
+    ptr = torch.tensor([50, 50, 30050, 30060, 47000])  # first 50 / last 100 points in no cloud
+    _fps_check(dev, pos, ptr, torch.tensor([5, 1000, 10, 500]))
+    _fps_check(dev, pos, ptr, torch.tensor([0, 20, 10, 16940]))     # k = 0 and k = n
+    _fps_check(dev, pos[:20000], _ptr([20000]), torch.tensor([4000]))
+
+
+def test_fps_large_tie_lattice(dev):
+    pos = _lattice(30, 3)  # 27,000 integer points: exact distances, ties at every step
+    _fps_check(dev, pos, _ptr([27000]), torch.tensor([3000]))
+
+
 def test_fps_tie_lattice(dev):
     pos = _lattice(8)  # 512 integer points: exact distances, many ties
     _fps_check(dev, pos, _ptr([512]), torch.tensor([200]))
