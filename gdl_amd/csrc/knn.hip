@@ -132,14 +132,387 @@ int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
   return GEO_OK;
 }
 
+// --------------------------------------------------------------------------- grid search ---
+// Clouds of many sources and k <= 32: each source cloud is binned into a uniform grid (cell
+// edge chosen so a cell holds about k/2 points at the cloud's mean density, at most 1024 cells
+// per axis and 2n + 64 cells), sources are counting-sorted by cell, and each query visits the
+// cells in shells of growing Chebyshev radius around its own cell.  After a shell it stops when
+// its k-th distance is below a bound that every unvisited source provably exceeds: the query's
+// distance to the faces of the visited block, measured in cell units minus 1e-3 of a cell (the
+// cell coordinates are rounded fp32 values below 1024, accurate to ~1e-4 cells), scaled by the
+// cell edge and shrunk by 1e-5 relative (the fp32 distance of a farther point can round down
+// by less than that).  The stop test is strict, so a source at exactly the k-th distance with a
+// smaller index cannot be missed.  Candidates arrive in cell order, so the register list keeps
+// the total order (d, j) explicitly.
+constexpr int kKnnGridThreads = 256;
+constexpr int kKnnGridMaxAxis = 1024;
+constexpr int kKnnGridMaxK = 32;
+
+struct KnnGrid {
+  float ox, oy, oz, inv_h, h;
+  int dx, dy, dz, base, ncells;
+};
+
+struct KnnGridWs {
+  KnnGrid* grid;
+  int32_t* cell_cnt;
+  int32_t* cell_start;
+  int32_t* cell_tiles;
+  int32_t* pt_cell;
+  int32_t* pt_rank;
+  float4* spos;
+  int64_t cells_max;
+};
+
+KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
+  Carver c(base);
+  KnnGridWs w;
+  const int64_t nn = Ns > 0 ? Ns : 1, bb = B > 0 ? B : 1;
+  w.cells_max = 2 * Ns + 64 * bb;
+  w.grid = c.take<KnnGrid>(bb);
+  w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
+  w.cell_start = c.take<int32_t>(w.cells_max + 1);
+  w.cell_tiles = c.take<int32_t>(scan_workspace_elems(w.cells_max + 1));
+  w.pt_cell = c.take<int32_t>(nn);
+  w.pt_rank = c.take<int32_t>(nn);
+  w.spos = c.take<float4>(nn);
+  *bytes = c.used;
+  return w;
+}
+
+__device__ __forceinline__ int64_t clamp_range(int64_t v, int64_t n) { return v < 0 ? 0 : (v > n ? n : v); }
+
+// One block per source cloud: bounding box, then (thread 0) the grid of that cloud.
+__global__ __launch_bounds__(kKnnGridThreads) void knn_grid_setup(
+    const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int k,
+    KnnGrid* __restrict__ grid) {
+  constexpr int W = kKnnGridThreads / kWave;
+  __shared__ uint32_t red[6][W];
+  const int b = blockIdx.x;
+  const int64_t sa = clamp_range(ptr_s[b], Ns);
+  const int64_t sc = sa > clamp_range(ptr_s[b + 1], Ns) ? sa : clamp_range(ptr_s[b + 1], Ns);
+  const int t = threadIdx.x, w = t / kWave;
+  uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
+  for (int64_t i = sa + t; i < sc; i += kKnnGridThreads) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const uint32_t kk = float_order_key(source[3 * i + a]);
+      mn[a] = min(mn[a], kk);
+      mx[a] = max(mx[a], kk);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    mn[a] = wave_min_u32(mn[a]);
+    mx[a] = wave_max_u32(mx[a]);
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
+  }
+  __syncthreads();
+  if (t != 0) return;
+  float lo[3], hi[3];
+  for (int a = 0; a < 3; ++a) {
+    uint32_t m0 = red[a][0], m1 = red[3 + a][0];
+    for (int ww = 1; ww < W; ++ww) { m0 = min(m0, red[a][ww]); m1 = max(m1, red[3 + a][ww]); }
+    lo[a] = float_from_order_key(m0);
+    hi[a] = float_from_order_key(m1);
+  }
+  const int64_t n = sc - sa;
+  KnnGrid g{0.f, 0.f, 0.f, 0.f, 0.f, 1, 1, 1, 0, 1};
+  double ext[3];
+  bool finite = n > 0;
+  for (int a = 0; a < 3; ++a) {
+    ext[a] = static_cast<double>(hi[a]) - static_cast<double>(lo[a]);
+    finite = finite && ext[a] >= 0.0 && ext[a] < 1e30;
+  }
+  if (finite) {
+    const double emax = fmax(fmax(ext[0], ext[1]), ext[2]);
+    const double target = fmax(0.5 * k, 1.0);
+    double h = emax;  // fixed point of h = cbrt(prod max(ext, h) * target / n)
+    for (int it = 0; it < 12 && h > 0.0; ++it)
+      h = cbrt(fmax(ext[0], h) * fmax(ext[1], h) * fmax(ext[2], h) * target / static_cast<double>(n));
+    if (h > 0.0) {
+      const double cap = 2.0 * static_cast<double>(n) + 64.0;
+      int64_t d[3] = {1, 1, 1};
+      bool ok = false;
+      for (int it = 0; it < 64 && !ok; ++it) {
+        double prod = 1.0, worst = 0.0;
+        for (int a = 0; a < 3; ++a) {
+          const double q = floor(ext[a] / h) + 1.0;
+          d[a] = q < 4.0 * kKnnGridMaxAxis ? static_cast<int64_t>(q) : 4 * kKnnGridMaxAxis;
+          prod *= static_cast<double>(d[a]);
+          worst = fmax(worst, static_cast<double>(d[a]) / kKnnGridMaxAxis);
+        }
+        ok = prod <= cap && worst <= 1.0;
+        if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst), 1.0) * 1.01;
+      }
+      if (ok) {
+        g.ox = lo[0]; g.oy = lo[1]; g.oz = lo[2];
+        g.inv_h = static_cast<float>(1.0 / h);
+        g.h = static_cast<float>(h * (1.0 - 1e-6));
+        g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
+      }
+    }
+  }
+  g.ncells = n > 0 ? g.dx * g.dy * g.dz : 0;
+  grid[b] = g;
+}
+
+// Single block: cell bases (exclusive scan of the cells per cloud).
+__global__ __launch_bounds__(kScanThreads) void knn_grid_base(KnnGrid* __restrict__ grid, int64_t B) {
+  __shared__ int64_t lds[kScanThreads / kWave];
+  int64_t carry = 0;
+  for (int64_t base = 0; base < B; base += kScanThreads) {
+    const int64_t b = base + threadIdx.x;
+    const int64_t cells = b < B ? grid[b].ncells : 0;
+    int64_t total;
+    const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
+    if (b < B) grid[b].base = static_cast<int>(carry + off);
+    carry += total;
+  }
+}
+
+__device__ __forceinline__ int knn_cell_coord(float p, float o, float inv_h, int dim, float* u_out) {
+#pragma clang fp contract(off)
+  const float u = (p - o) * inv_h;
+  *u_out = u;
+  const int c = static_cast<int>(floorf(u));
+  return c < 0 ? 0 : (c >= dim ? dim - 1 : c);
+}
+
+// Last b in [0, B) with ptr[b] <= i (the cloud holding index i, if any).
+__device__ __forceinline__ int64_t cloud_of_index(const int64_t* __restrict__ ptr, int64_t B, int64_t i) {
+  int64_t lo = 0, hi = B;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (ptr[mid + 1] <= i) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kKnnGridThreads) void knn_grid_cell(
+    const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int64_t B,
+    KnnGridWs w) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= Ns) return;
+  const int64_t b = cloud_of_index(ptr_s, B, i);
+  if (b >= B || i < ptr_s[b] || i >= ptr_s[b + 1]) {
+    w.pt_cell[i] = -1;
+    return;
+  }
+  const KnnGrid g = w.grid[b];
+  float u;
+  const int cx = knn_cell_coord(source[3 * i], g.ox, g.inv_h, g.dx, &u);
+  const int cy = knn_cell_coord(source[3 * i + 1], g.oy, g.inv_h, g.dy, &u);
+  const int cz = knn_cell_coord(source[3 * i + 2], g.oz, g.inv_h, g.dz, &u);
+  const int c = g.base + (cx * g.dy + cy) * g.dz + cz;
+  w.pt_cell[i] = c;
+  w.pt_rank[i] = atomicAdd(&w.cell_cnt[c], 1);
+}
+
+__global__ __launch_bounds__(kKnnGridThreads) void knn_grid_scatter(const float* __restrict__ source,
+                                                                    int64_t Ns, KnnGridWs w) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= Ns) return;
+  const int c = w.pt_cell[i];
+  if (c < 0) return;
+  w.spos[w.cell_start[c] + w.pt_rank[i]] =
+      make_float4(source[3 * i], source[3 * i + 1], source[3 * i + 2], __int_as_float(static_cast<int>(i)));
+}
+
+// (d, j) < (e, i) in the total order used throughout: distance, then source index.
+__device__ __forceinline__ bool knn_less(float d, int j, float e, int i) {
+  return d < e || (d == e && j < i);
+}
+
+// Sorted top-KMAX list of one lane; inserts (d, j) if it is among the KMAX smallest.
+template <int KMAX>
+__device__ __forceinline__ void knn_insert(float (&D)[KMAX], int (&J)[KMAX], float d, int j) {
+  if (d < __builtin_inff() && knn_less(d, j, D[KMAX - 1], J[KMAX - 1])) {
+#pragma unroll
+    for (int m = KMAX - 1; m > 0; --m) {
+      const bool shift = knn_less(d, j, D[m - 1], J[m - 1]);
+      const bool here = !shift && knn_less(d, j, D[m], J[m]);
+      D[m] = shift ? D[m - 1] : (here ? d : D[m]);
+      J[m] = shift ? J[m - 1] : (here ? j : J[m]);
+    }
+    if (knn_less(d, j, D[0], J[0])) { D[0] = d; J[0] = j; }
+  }
+}
+
+// Merge with the list of the lane `mask` away: keep the KMAX smallest of both, sorted.  The
+// element-wise minimum of one list and the other reversed is bitonic and holds exactly the KMAX
+// smallest; half-cleaners sort it.  Both lanes end with the same list.
+template <int KMAX>
+__device__ __forceinline__ void knn_merge_xor(float (&D)[KMAX], int (&J)[KMAX], int mask) {
+  float PD[KMAX];
+  int PJ[KMAX];
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    PD[i] = __shfl_xor(D[i], mask, kWave);
+    PJ[i] = __shfl_xor(J[i], mask, kWave);
+  }
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    const float od = PD[KMAX - 1 - i];
+    const int oj = PJ[KMAX - 1 - i];
+    const bool take = knn_less(od, oj, D[i], J[i]);
+    D[i] = take ? od : D[i];
+    J[i] = take ? oj : J[i];
+  }
+#pragma unroll
+  for (int sd = KMAX / 2; sd > 0; sd >>= 1) {
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      if ((i & sd) == 0) {
+        const bool sw = knn_less(D[i + sd], J[i + sd], D[i], J[i]);
+        const float d0 = D[i];
+        const int j0 = J[i];
+        D[i] = sw ? D[i + sd] : d0;
+        J[i] = sw ? J[i + sd] : j0;
+        D[i + sd] = sw ? d0 : D[i + sd];
+        J[i + sd] = sw ? j0 : J[i + sd];
+      }
+    }
+  }
+}
+
+// G lanes per query: the lanes of a group split every visited cell range (consecutive sources,
+// so the group's loads are contiguous), each keeps its own sorted top-KMAX, the stop test counts
+// the group's candidates below the bound (exact: a lane that dropped a candidate below the bound
+// already holds KMAX >= k of them), and the lists are merged pairwise at the end.
+template <int KMAX, int G>
+__global__ __launch_bounds__(kKnnGridThreads) void knn_grid_query(
+    const float* __restrict__ query, int64_t Nq, const int64_t* __restrict__ ptr_q, int64_t B,
+    KnnGridWs w, int k, int64_t* __restrict__ out_idx, float* __restrict__ out_dist) {
+  const int64_t gt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t q = gt / G;
+  const int gl = static_cast<int>(gt % G);
+  if (q >= Nq) return;  // whole groups leave together (G divides the block)
+  const int64_t b = cloud_of_index(ptr_q, B, q);
+  if (b >= B || q < ptr_q[b] || q >= ptr_q[b + 1]) return;  // no cloud: padding stays
+  const KnnGrid g = w.grid[b];
+  if (g.ncells == 0) return;                                  // empty source cloud
+  const float qx = query[3 * q], qy = query[3 * q + 1], qz = query[3 * q + 2];
+  float ux, uy, uz;
+  const int cx = knn_cell_coord(qx, g.ox, g.inv_h, g.dx, &ux);
+  const int cy = knn_cell_coord(qy, g.oy, g.inv_h, g.dy, &uy);
+  const int cz = knn_cell_coord(qz, g.oz, g.inv_h, g.dz, &uz);
+  constexpr int kNone = 0x7fffffff;
+  float D[KMAX];
+  int J[KMAX];
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) { D[i] = __builtin_inff(); J[i] = kNone; }
+
+  auto visit = [&](int a, int e) {
+    for (int p = a + gl; p < e; p += G) {
+      const float4 s = w.spos[p];
+      knn_insert<KMAX>(D, J, sqdist(qx, qy, qz, s.x, s.y, s.z), __float_as_int(s.w));
+    }
+  };
+  const int maxr = max(max(g.dx, g.dy), g.dz);
+  for (int r = 0; r <= maxr; ++r) {
+    const int x0 = max(cx - r, 0), x1 = min(cx + r, g.dx - 1);
+    const int y0 = max(cy - r, 0), y1 = min(cy + r, g.dy - 1);
+    const int z0 = max(cz - r, 0), z1 = min(cz + r, g.dz - 1);
+    for (int ix = x0; ix <= x1; ++ix) {
+      const bool xface = ix == cx - r || ix == cx + r;
+      for (int iy = y0; iy <= y1; ++iy) {
+        const int c0 = g.base + (ix * g.dy + iy) * g.dz;
+        if (xface || iy == cy - r || iy == cy + r) {
+          visit(w.cell_start[c0 + z0], w.cell_start[c0 + z1 + 1]);
+        } else {
+          if (cz - r >= 0) visit(w.cell_start[c0 + cz - r], w.cell_start[c0 + cz - r + 1]);
+          if (cz + r < g.dz) visit(w.cell_start[c0 + cz + r], w.cell_start[c0 + cz + r + 1]);
+        }
+      }
+    }
+    // distance (cell units) from the query to the faces of the visited block that still have
+    // cells beyond them
+    float gap = __builtin_inff();
+    if (cx - r > 0) gap = fminf(gap, ux - static_cast<float>(cx - r));
+    if (cx + r < g.dx - 1) gap = fminf(gap, static_cast<float>(cx + r + 1) - ux);
+    if (cy - r > 0) gap = fminf(gap, uy - static_cast<float>(cy - r));
+    if (cy + r < g.dy - 1) gap = fminf(gap, static_cast<float>(cy + r + 1) - uy);
+    if (cz - r > 0) gap = fminf(gap, uz - static_cast<float>(cz - r));
+    if (cz + r < g.dz - 1) gap = fminf(gap, static_cast<float>(cz + r + 1) - uz);
+    if (gap == __builtin_inff()) break;  // every cell of the cloud visited
+    const float gr = (gap - 1e-3f) * g.h;
+    const float bound = gap > 1e-3f ? gr * gr * (1.0f - 1e-5f) : 0.0f;
+    int below = 0;
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) below += D[i] < bound ? 1 : 0;
+#pragma unroll
+    for (int m = 1; m < G; m <<= 1) below += __shfl_xor(below, m, kWave);
+    if (below >= k) break;
+  }
+#pragma unroll
+  for (int m = 1; m < G; m <<= 1) knn_merge_xor<KMAX>(D, J, m);
+  int64_t* oi = out_idx + q * k;
+  float* od = out_dist + q * k;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    if (i < k && i % G == gl) {
+      oi[i] = J[i] != kNone ? static_cast<int64_t>(J[i]) : -1;
+      od[i] = J[i] != kNone ? D[i] : 1e30f;
+    }
+  }
+}
+
+bool knn_use_grid(int64_t Ns, int64_t B, int64_t k) {
+  return k >= 1 && k <= kKnnGridMaxK && B >= 1 && Ns >= 1024 * B;
+}
+
+int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t Ns,
+                    const int64_t* ptr_q, const int64_t* ptr_s, int64_t B, int k, int64_t* out_idx,
+                    float* out_dist, void* workspace, hipStream_t st) {
+  size_t bytes = 0;
+  const KnnGridWs w = carve_knn_grid(workspace, Ns, B, &bytes);
+  hipLaunchKernelGGL(knn_grid_setup, dim3(B), dim3(kKnnGridThreads), 0, st, source, Ns, ptr_s, k,
+                     w.grid);
+  GEO_LAUNCH_CHECK("knn_grid_setup");
+  hipLaunchKernelGGL(knn_grid_base, dim3(1), dim3(kScanThreads), 0, st, w.grid, B);
+  GEO_LAUNCH_CHECK("knn_grid_base");
+  int rc = device_fill<int32_t>(w.cell_cnt, w.cells_max + 1, 0, st);
+  if (rc) return rc;
+  const unsigned gs = static_cast<unsigned>(ceil_div(Ns, kKnnGridThreads));
+  hipLaunchKernelGGL(knn_grid_cell, dim3(gs), dim3(kKnnGridThreads), 0, st, source, Ns, ptr_s, B, w);
+  GEO_LAUNCH_CHECK("knn_grid_cell");
+  rc = device_exclusive_scan<int32_t, int32_t>(w.cell_cnt, w.cells_max + 1, w.cell_start, nullptr,
+                                               false, w.cell_tiles, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(knn_grid_scatter, dim3(gs), dim3(kKnnGridThreads), 0, st, source, Ns, w);
+  GEO_LAUNCH_CHECK("knn_grid_scatter");
+#define GEO_KNN_GRID_CASE(KV, GV)                                                               \
+  if (k <= KV) {                                                                                \
+    const unsigned gq = static_cast<unsigned>(ceil_div(Nq * GV, kKnnGridThreads));             \
+    hipLaunchKernelGGL((knn_grid_query<KV, GV>), dim3(gq), dim3(kKnnGridThreads), 0, st, query, \
+                       Nq, ptr_q, B, w, k, out_idx, out_dist);                                  \
+    GEO_LAUNCH_CHECK("knn_grid_query");                                                         \
+    return GEO_OK;                                                                              \
+  }
+  GEO_KNN_GRID_CASE(1, 8) GEO_KNN_GRID_CASE(2, 8) GEO_KNN_GRID_CASE(4, 8)
+  GEO_KNN_GRID_CASE(8, 8) GEO_KNN_GRID_CASE(16, 16) GEO_KNN_GRID_CASE(32, 16)
+#undef GEO_KNN_GRID_CASE
+  return set_error(GEO_ERR_UNSUPPORTED, "knn: k=%d unsupported by the grid search", k);
+}
+
 }  // namespace
 }  // namespace geo
 
 using namespace geo;
 
 extern "C" size_t geo_knn_workspace_bytes(int64_t Nq, int64_t Ns, int64_t B, int64_t k) {
-  (void)Nq; (void)Ns; (void)k;
-  return static_cast<size_t>((B > 0 ? B : 0) + 1) * sizeof(int64_t);
+  (void)Nq;
+  if (Ns < 0 || B < 0) return 0;
+  if (knn_use_grid(Ns, B, k)) {
+    size_t bytes = 0;
+    carve_knn_grid(nullptr, Ns, B, &bytes);
+    return bytes;
+  }
+  return static_cast<size_t>(B + 1) * sizeof(int64_t);
 }
 
 extern "C" int geo_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
@@ -169,10 +542,13 @@ extern "C" int geo_knn(const float* query, int64_t Nq, const float* source, int6
   if (rc) return rc;
   rc = device_fill<float>(out_dist, Nq * k, 1e30f, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(knn_prepare_kernel, dim3(1), dim3(kScanThreads), 0, st, ptr_q, B, Nq, tiles);
-  GEO_LAUNCH_CHECK("knn_prepare_kernel");
   GEO_REQUIRE(Ns == 0 || source != nullptr, "knn: null source");
   const int kk = static_cast<int>(k);
+  if (knn_use_grid(Ns, B, k))
+    return launch_knn_grid(query, Nq, source, Ns, ptr_q, ptr_s, B, kk, out_idx, out_dist,
+                           workspace, st);
+  hipLaunchKernelGGL(knn_prepare_kernel, dim3(1), dim3(kScanThreads), 0, st, ptr_q, B, Nq, tiles);
+  GEO_LAUNCH_CHECK("knn_prepare_kernel");
 #define GEO_KNN_CASE(KV) \
   if (kk <= KV) return launch_knn<KV>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx, out_dist, st);
   GEO_KNN_CASE(1) GEO_KNN_CASE(2) GEO_KNN_CASE(3) GEO_KNN_CASE(4) GEO_KNN_CASE(5)

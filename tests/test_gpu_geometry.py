@@ -148,6 +148,45 @@ def test_knn_vs_oracle(dev, k):
     _knn_check(dev, q, s, _ptr(qs), _ptr(ss), k)
 
 
+def _knn_grid_problem(kind, g):
+    """Source clouds of >= 1024 points on average (the grid search); queries in and around them."""
+    if kind == "cube":
+        ss, qs = [5000, 3000, 8000], [700, 0, 900]
+        s = torch.rand(sum(ss), 3, generator=g) * torch.tensor([4.0, 1.0, 0.25])
+        q = (torch.rand(sum(qs), 3, generator=g) * 3 - 1) * torch.tensor([4.0, 1.0, 0.25])
+    elif kind == "lattice":  # integer points: exact distances, ties everywhere
+        s = _lattice(20, 1)
+        q = _lattice(8, 2) * 2.5 - 1.0
+        ss, qs = [8000], [512]
+    elif kind == "sphere":
+        d = torch.randn(12000, 3, generator=g)
+        s = d / d.norm(dim=1, keepdim=True)
+        q = s[torch.randperm(12000, generator=g)[:1500]] * 1.01
+        ss, qs = [4000, 4000, 4000], [500, 500, 500]
+    elif kind == "plane":    # zero extent in z: one cell layer
+        s = torch.cat([torch.rand(6000, 2, generator=g), torch.zeros(6000, 1)], 1)
+        q = torch.rand(800, 3, generator=g) - 0.25
+        ss, qs = [6000], [800]
+    elif kind == "small_cloud":  # a cloud with fewer sources than k, an empty one
+        s = torch.randn(6005, 3, generator=g)
+        q = torch.randn(600, 3, generator=g)
+        ss, qs = [6000, 5, 0], [300, 200, 100]
+    else:                    # "nonfinite": one source at inf -> the cloud falls back to one cell
+        s = torch.randn(5000, 3, generator=g)
+        s[17] = float("inf")
+        q = torch.randn(300, 3, generator=g)
+        ss, qs = [5000], [300]
+    return q, s, _ptr(qs), _ptr(ss)
+
+
+@pytest.mark.parametrize("kind", ["cube", "lattice", "sphere", "plane", "small_cloud", "nonfinite"])
+@pytest.mark.parametrize("k", [1, 3, 8, 16, 17, 32])
+def test_knn_grid_vs_oracle(dev, kind, k):
+    g = torch.Generator().manual_seed(k * 31 + len(kind))
+    q, s, pq, ps = _knn_grid_problem(kind, g)
+    _knn_check(dev, q, s, pq, ps, k)
+
+
 def test_knn_lattice_ties(dev):
     s = _lattice(7)
     q = _lattice(4, 3) + 0.5 * (torch.arange(64).reshape(-1, 1) % 2)  # some half-integer queries
