@@ -331,6 +331,9 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   }
   float cx = P[0], cy = P[1], cz = P[2];
   if (t == 0) out_idx[o0] = start;
+  // The wave's best (bits, index), recomputed only after one of its buckets changed.
+  uint32_t wbits = 0u, widx = 0xffffffffu;
+  bool dirty = true;
   __syncthreads();
 
   for (int it = 1; it < k; ++it) {
@@ -343,37 +346,42 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     }
     const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
     const uint64_t act = __ballot(lane < PTS && __float_as_uint(lb) < bmax);
-    stale |= act;
-#pragma unroll
-    for (int s = 0; s < PTS; ++s) {
-      if (act & (1ull << s)) {
-        const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
-        md[s] = __builtin_amdgcn_fmed3f(d, md[s], -__builtin_inff());
-        const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
-        if (lane == s) bmax = m;
-      }
-    }
-    // wave best: the largest bucket max, then the lowest index over the buckets holding it
-    const uint32_t wbits = PTS <= 16 ? row0_max_u32(bmax) : wave_max_u32(lane < PTS ? bmax : 0u);
-    const uint64_t tied = __ballot(lane < PTS && bmax == wbits);
-    const uint64_t need = tied & stale;
-    if (need) {
+    if (act) {
+      stale |= act;
+      dirty = true;
 #pragma unroll
       for (int s = 0; s < PTS; ++s) {
-        if (need & (1ull << s)) {
-          const uint32_t mb = __float_as_uint(md[s]);
-          const uint32_t mi = wave_min_u32(mb == wbits ? oi[s] : 0xffffffffu);
-          if (lane == s) bidx = mi;
+        if (act & (1ull << s)) {
+          const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
+          md[s] = __builtin_amdgcn_fmed3f(d, md[s], -__builtin_inff());
+          const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
+          if (lane == s) bmax = m;
         }
       }
-      stale &= ~need;
     }
-    uint32_t widx;
-    if ((tied & (tied - 1)) == 0) {  // a single bucket holds the max (the usual case)
-      widx = __builtin_amdgcn_readlane(bidx, __builtin_ctzll(tied | (1ull << 63)));
-    } else {
-      widx = PTS <= 16 ? row0_min_u32((tied >> lane) & 1 ? bidx : 0xffffffffu)
-                       : wave_min_u32(lane < PTS && ((tied >> lane) & 1) ? bidx : 0xffffffffu);
+    if (dirty) {
+      // wave best: the largest bucket max, then the lowest index over the buckets holding it
+      wbits = PTS <= 16 ? row0_max_u32(bmax) : wave_max_u32(lane < PTS ? bmax : 0u);
+      const uint64_t tied = __ballot(lane < PTS && bmax == wbits);
+      const uint64_t need = tied & stale;
+      if (need) {
+#pragma unroll
+        for (int s = 0; s < PTS; ++s) {
+          if (need & (1ull << s)) {
+            const uint32_t mb = __float_as_uint(md[s]);
+            const uint32_t mi = wave_min_u32(mb == wbits ? oi[s] : 0xffffffffu);
+            if (lane == s) bidx = mi;
+          }
+        }
+        stale &= ~need;
+      }
+      if ((tied & (tied - 1)) == 0) {  // a single bucket holds the max (the usual case)
+        widx = __builtin_amdgcn_readlane(bidx, __builtin_ctzll(tied | (1ull << 63)));
+      } else {
+        widx = PTS <= 16 ? row0_min_u32((tied >> lane) & 1 ? bidx : 0xffffffffu)
+                         : wave_min_u32(lane < PTS && ((tied >> lane) & 1) ? bidx : 0xffffffffu);
+      }
+      dirty = false;
     }
     const int p = it % 3;
     if (lane == 0)
