@@ -134,6 +134,28 @@ __device__ __forceinline__ uint32_t row0_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t row0_min_u32(uint32_t v) { return ~row0_max_u32(~v); }
 
+// Slot of this lane among the increments of counter[key] made by the active lanes: lanes with
+// the same key share one atomic add (issued by the lowest of them), so a counter that many
+// lanes hit at once is not serialised.  The adds are issued back to back and their results
+// gathered once at the end.  `counter` must be the same address for equal keys.
+__device__ __forceinline__ int wave_aggregated_rank(int* counter, int key) {
+  const int lane = lane_id();
+  uint64_t todo = __ballot(true);
+  int base = 0, my_leader = lane, my_rank = 0;
+  while (todo) {
+    const int leader = __builtin_ctzll(todo);
+    const int lk = __builtin_amdgcn_readlane(key, leader);
+    const uint64_t peers = __ballot(key == lk) & todo;
+    if (lane == leader) base = atomicAdd(counter, static_cast<int>(__popcll(peers)));
+    if ((peers >> lane) & 1ull) {
+      my_leader = leader;
+      my_rank = static_cast<int>(__popcll(peers & lanemask_lt()));
+    }
+    todo &= ~peers;
+  }
+  return __shfl(base, my_leader, kWave) + my_rank;
+}
+
 // Wave-wide inclusive prefix sum (all lanes active).
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_sum(T v) {

@@ -134,7 +134,7 @@ int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
 
 // --------------------------------------------------------------------------- grid search ---
 // Clouds of many sources and k <= 32: each source cloud is binned into a uniform grid (cell
-// edge chosen so a cell holds about k/2 points at the cloud's mean density, at most 1024 cells
+// edge chosen so a cell holds about k/4 points at the cloud's mean density, at most 1024 cells
 // per axis and 2n + 64 cells), sources are counting-sorted by cell, and each query visits the
 // cells in shells of growing Chebyshev radius around its own cell.  After a shell it stops when
 // its k-th distance is below a bound that every unvisited source provably exceeds: the query's
@@ -145,8 +145,11 @@ int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
 // smaller index cannot be missed.  Candidates arrive in cell order, so the register list keeps
 // the total order (d, j) explicitly.
 constexpr int kKnnGridThreads = 256;
+constexpr int kKnnSetupThreads = 1024;
 constexpr int kKnnGridMaxAxis = 1024;
 constexpr int kKnnGridMaxK = 32;
+constexpr double kKnnCellTarget = 0.25;  // points per cell per neighbour (measured best)
+constexpr int kKnnCellCap = 2;            // cells per point
 
 struct KnnGrid {
   float ox, oy, oz, inv_h, h;
@@ -168,7 +171,7 @@ KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
   Carver c(base);
   KnnGridWs w;
   const int64_t nn = Ns > 0 ? Ns : 1, bb = B > 0 ? B : 1;
-  w.cells_max = 2 * Ns + 64 * bb;
+  w.cells_max = kKnnCellCap * Ns + 64 * bb;
   w.grid = c.take<KnnGrid>(bb);
   w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
   w.cell_start = c.take<int32_t>(w.cells_max + 1);
@@ -183,17 +186,18 @@ KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
 __device__ __forceinline__ int64_t clamp_range(int64_t v, int64_t n) { return v < 0 ? 0 : (v > n ? n : v); }
 
 // One block per source cloud: bounding box, then (thread 0) the grid of that cloud.
-__global__ __launch_bounds__(kKnnGridThreads) void knn_grid_setup(
+__global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_setup(
     const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int k,
     KnnGrid* __restrict__ grid) {
-  constexpr int W = kKnnGridThreads / kWave;
+  constexpr int W = kKnnSetupThreads / kWave;
   __shared__ uint32_t red[6][W];
   const int b = blockIdx.x;
   const int64_t sa = clamp_range(ptr_s[b], Ns);
   const int64_t sc = sa > clamp_range(ptr_s[b + 1], Ns) ? sa : clamp_range(ptr_s[b + 1], Ns);
   const int t = threadIdx.x, w = t / kWave;
   uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
-  for (int64_t i = sa + t; i < sc; i += kKnnGridThreads) {
+#pragma unroll 4
+  for (int64_t i = sa + t; i < sc; i += kKnnSetupThreads) {
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
       const uint32_t kk = float_order_key(source[3 * i + a]);
@@ -229,12 +233,12 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_setup(
   }
   if (finite) {
     const double emax = fmax(fmax(ext[0], ext[1]), ext[2]);
-    const double target = fmax(0.5 * k, 1.0);
+    const double target = fmax(kKnnCellTarget * k, 1.0);
     double h = emax;  // fixed point of h = cbrt(prod max(ext, h) * target / n)
     for (int it = 0; it < 12 && h > 0.0; ++it)
       h = cbrt(fmax(ext[0], h) * fmax(ext[1], h) * fmax(ext[2], h) * target / static_cast<double>(n));
     if (h > 0.0) {
-      const double cap = 2.0 * static_cast<double>(n) + 64.0;
+      const double cap = kKnnCellCap * static_cast<double>(n) + 64.0;
       int64_t d[3] = {1, 1, 1};
       bool ok = false;
       for (int it = 0; it < 64 && !ok; ++it) {
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_cell(
   const int cz = knn_cell_coord(source[3 * i + 2], g.oz, g.inv_h, g.dz, &u);
   const int c = g.base + (cx * g.dy + cy) * g.dz + cz;
   w.pt_cell[i] = c;
-  w.pt_rank[i] = atomicAdd(&w.cell_cnt[c], 1);
+  w.pt_rank[i] = wave_aggregated_rank(&w.cell_cnt[c], c);
 }
 
 __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_scatter(const float* __restrict__ source,
@@ -470,7 +474,7 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
                     float* out_dist, void* workspace, hipStream_t st) {
   size_t bytes = 0;
   const KnnGridWs w = carve_knn_grid(workspace, Ns, B, &bytes);
-  hipLaunchKernelGGL(knn_grid_setup, dim3(B), dim3(kKnnGridThreads), 0, st, source, Ns, ptr_s, k,
+  hipLaunchKernelGGL(knn_grid_setup, dim3(B), dim3(kKnnSetupThreads), 0, st, source, Ns, ptr_s, k,
                      w.grid);
   GEO_LAUNCH_CHECK("knn_grid_setup");
   hipLaunchKernelGGL(knn_grid_base, dim3(1), dim3(kScanThreads), 0, st, w.grid, B);
