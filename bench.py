@@ -229,6 +229,16 @@ def main() -> int:
                                  num_batch_elements=c2["B"]), args.steps, 3)
         log(f"  step {ms_step:.3f} ms  fps {legs['c2_fps_ms']:.3f}  radius {legs['c2_radius_ms']:.3f}"
             f"  knn {legs['c2_knn_ms']:.3f}  edges {legs['c2_edges']}")
+        # attention softmax over the C2 graph (4 heads): CSR from the radius graph's target order
+        from gdl_amd.functional.segment_softmax import segment_softmax, sparse_softmax
+        cs, pm, ns, ne = sort_and_build_csr(col, pos.shape[0])
+        scores = torch.randn(row.numel(), 4, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+        legs["c2_softmax_fwd_us"] = round(1e3 * event_ms(
+            lambda: segment_softmax(scores, pm, ns, ne, pos.shape[0]), args.iters, 5), 2)
+        legs["c2_sparse_softmax_us"] = round(1e3 * wall_ms(
+            lambda: sparse_softmax(scores, col, pos.shape[0]), args.steps, 3), 2)
+        log(f"  segment softmax (E={row.numel()}, H=4): {legs['c2_softmax_fwd_us']} us on the CSR, "
+            f"{legs['c2_sparse_softmax_us']} us from the target index")
 
     # ---------------------------------------------------------------- C3 roofline ---
     roof = None

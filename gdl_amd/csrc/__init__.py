@@ -286,6 +286,62 @@ def segment_reduce_sum_cuda(
     return segment_reduce_forward_hip(msg, perm, node_start, node_end, N, "sum")[0]
 
 
+def segment_softmax_forward_hip(
+    scores: Tensor,
+    perm: Optional[Tensor],
+    node_start: Tensor,
+    node_end: Tensor,
+    N: int,
+) -> Tensor:
+    """Softmax of scores[E, H] over each target segment of the CSR (rows in no segment -> 0)."""
+    _require_gpu("segment_softmax", scores, perm, node_start, node_end)
+    if scores.dim() != 2:
+        raise ValueError(f"segment_softmax: scores must be [E, H], got {tuple(scores.shape)}")
+    if scores.dtype not in (torch.float32, torch.float64):
+        raise TypeError(f"segment_softmax: scores must be float32 or float64, got {scores.dtype}")
+    N = int(N)
+    if node_start.numel() < N or node_end.numel() < N:
+        raise ValueError("segment_softmax: node_start/node_end shorter than N")
+    dev = scores.device
+    scores = scores.contiguous()
+    E, H = scores.shape
+    pm = _i32(perm, dev)
+    if pm is not None and pm.numel() != E:
+        raise ValueError(f"segment_softmax: perm has {pm.numel()} entries for E={E}")
+    ns, ne = _i32(node_start, dev), _i32(node_end, dev)
+    out = torch.zeros_like(scores)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_segment_softmax_fwd(
+            _nat.DTYPE_CODES[scores.dtype], _nat.ptr(scores), _nat.ptr(pm), _nat.ptr(ns),
+            _nat.ptr(ne), E, N, H, _nat.ptr(out), _nat.stream_of(dev)), "geo_segment_softmax_fwd")
+    return out
+
+
+def segment_softmax_backward_hip(
+    grad_out: Tensor,
+    out: Tensor,
+    perm: Optional[Tensor],
+    node_start: Tensor,
+    node_end: Tensor,
+    N: int,
+) -> Tensor:
+    """grad_scores = out * (grad_out - segment sum of grad_out * out)."""
+    _require_gpu("segment_softmax backward", grad_out, out, perm, node_start, node_end)
+    dev = out.device
+    grad_out = grad_out.to(out.dtype).contiguous()
+    out = out.contiguous()
+    E, H = out.shape
+    pm = _i32(perm, dev)
+    ns, ne = _i32(node_start, dev), _i32(node_end, dev)
+    grad = torch.zeros_like(out)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_segment_softmax_bwd(
+            _nat.DTYPE_CODES[out.dtype], _nat.ptr(grad_out), _nat.ptr(out), _nat.ptr(pm),
+            _nat.ptr(ns), _nat.ptr(ne), E, int(N), H, _nat.ptr(grad), _nat.stream_of(dev)),
+            "geo_segment_softmax_bwd")
+    return grad
+
+
 # ═══════════════════════════════════════════════════════════════════
 # KNN
 # ═══════════════════════════════════════════════════════════════════
@@ -394,6 +450,7 @@ def _fps_iterative_fallback(pos, ptr, k_per_batch):
 __all__ = [
     "get_radius_graph_backend", "radius_graph_cuda", "radius_graph_hip", "fp32_radius_sq",
     "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
+    "segment_softmax_forward_hip", "segment_softmax_backward_hip",
     "segment_reduce_forward_hip", "segment_reduce_backward_hip",
     "knn_available", "knn_cuda", "knn_self_cuda",
     "fps_available", "fps_cuda",

@@ -8,8 +8,10 @@ from gdl_amd.functional.segment_reduce import (
     segment_reduce,
     sort_and_build_csr,
 )
+from gdl_amd.functional.segment_softmax import segment_softmax, sparse_softmax
 
 __all__ = [
     "farthest_point_sampling", "knn", "knn_self", "radius_graph", "compute_edge_vectors",
-    "segment_reduce", "sort_and_build_csr", "SegmentReduceFunction",
+    "segment_reduce", "sort_and_build_csr", "SegmentReduceFunction", "segment_softmax",
+    "sparse_softmax",
 ]

@@ -17,6 +17,7 @@ _ALIASES = (
     "functional.knn",
     "functional.radius_graph",
     "functional.segment_reduce",
+    "functional.segment_softmax",
     "kernels",
 )
 

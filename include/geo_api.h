@@ -178,6 +178,28 @@ int geo_segment_reduce_bwd(int reduce, int dtype, const void* grad_out, const vo
                            const int32_t* node_end, int64_t E, int64_t S, int64_t C,
                            void* grad_msg, void* stream);
 
+/* -------------------------------------------------------- segment softmax --- */
+/*
+ * Replaces _sparse_softmax (geoembodied/nn/modules/invariant_attention.py:202-230: scatter
+ * 'amax' per target, exp(score - max), scatter_add, divide by the sum clamped at 1e-8) with one
+ * kernel over the CSR of the targets.  scores and out are [E, H] row-major of `dtype` (GEO_F32
+ * or GEO_F64); row perm[e] (e in [node_start[s], node_end[s])) belongs to segment s; perm may be
+ * NULL (identity).  Rows that belong to no segment are not written.  NaN scores make their
+ * segment NaN, as in the reference.
+ */
+int geo_segment_softmax_fwd(int dtype, const void* scores, const int32_t* perm,
+                            const int32_t* node_start, const int32_t* node_end, int64_t E,
+                            int64_t S, int64_t H, void* out, void* stream);
+/*
+ * Backward of the above (the gradient autograd forms for the reference's op sequence, whose
+ * max-shift term cancels analytically): grad_scores[e] = out[e] * (grad_out[e] - sum over the
+ * segment of grad_out * out).
+ */
+int geo_segment_softmax_bwd(int dtype, const void* grad_out, const void* out,
+                            const int32_t* perm, const int32_t* node_start,
+                            const int32_t* node_end, int64_t E, int64_t S, int64_t H,
+                            void* grad_scores, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

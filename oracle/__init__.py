@@ -11,6 +11,7 @@ Contents:
 * Segment sum / mean / max, forward and backward: numpy below.  Sum and mean are accumulated in
   float64 and returned with the per-element scale ``sum |msg|`` that the tolerance of the
   comparison multiplies; max, argmax and every backward value are exact.
+* Segment softmax (``sparse_softmax``) and its backward: numpy float64 below.
 
 Pinning (what checks each function independently of this restatement) is listed in
 ``tests/test_oracle.py``: reference KATs, closed forms on integer lattices where fp32 arithmetic
@@ -268,3 +269,37 @@ def segment_reduce_bwd(grad_out, col_sorted, perm, node_start, node_end, E: int,
         split = _div_in_dtype(gv, np.where(tie, -A, 1), dtype)
         res[p_idx] = np.where(first, gv, np.where(tie & eqv, split, 0.0))
     return res
+
+
+# ------------------------------------------------------------------------ segment softmax ---
+
+def sparse_softmax(scores, index, N: int) -> np.ndarray:
+    """Softmax of scores [E, H] over the edges of each target (float64), following
+    _sparse_softmax, geoembodied/nn/modules/invariant_attention.py:202-230: per-target max of the
+    edges' scores (NaN propagates), exp(score - max), per-target sum, divide by the sum clamped
+    at 1e-8."""
+    x = np.asarray(scores, dtype=np.float64)
+    squeeze = x.ndim == 1
+    if squeeze:
+        x = x[:, None]
+    idx = np.asarray(index, dtype=np.int64)
+    H = x.shape[1]
+    m = np.full((N, H), -np.inf)
+    np.maximum.at(m, idx, x)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ex = np.exp(x - m[idx])
+    z = np.zeros((N, H))
+    np.add.at(z, idx, ex)
+    with np.errstate(invalid="ignore"):
+        w = ex / np.maximum(z[idx], 1e-8)
+    return w[:, 0] if squeeze else w
+
+
+def sparse_softmax_bwd(grad, w, index, N: int) -> np.ndarray:
+    """Gradient of sparse_softmax with respect to the scores: w * (g - per-target sum of g * w)."""
+    g = np.asarray(grad, dtype=np.float64)
+    w = np.asarray(w, dtype=np.float64)
+    idx = np.asarray(index, dtype=np.int64)
+    dot = np.zeros((N,) + w.shape[1:])
+    np.add.at(dot, idx, g * w)
+    return w * (g - dot[idx])

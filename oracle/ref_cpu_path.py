@@ -13,6 +13,8 @@ is what a user of the reference pays on the CPU:
 * ``sort_and_build_csr`` / ``segment_sum`` — _sort_and_build_csr_pytorch and
                        _segment_reduce_pytorch, geoembodied/functional/segment_reduce.py:77-199:
                        argsort + bincount/cumsum, then a Python loop over segments.
+* ``sparse_softmax`` — _sparse_softmax, geoembodied/nn/modules/invariant_attention.py:202-230:
+                       scatter 'amax', exp, scatter_add, divide.
 
 Outputs follow those CPU semantics (cdist distances, topk tie order), which differ from the
 exact semantics of the GPU kernels at boundary pairs; they are timed, not used as the oracle.
@@ -100,3 +102,17 @@ def segment_sum(msg: Tensor, perm: Tensor, node_start: Tensor, node_end: Tensor,
         if a < b:
             out[n] = msg[perm[a:b].long()].sum(dim=0)
     return out
+
+
+def sparse_softmax(scores: Tensor, index: Tensor, num_nodes: int) -> Tensor:
+    """_sparse_softmax, geoembodied/nn/modules/invariant_attention.py:202-230: scatter 'amax'
+    into zeros with include_self=False, gather, exp, scatter_add, gather, divide by the sum
+    clamped at 1e-8 (the max buffers take the scores' dtype here so float64 runs stay float64)."""
+    max_scores = torch.zeros(num_nodes, scores.shape[-1], dtype=scores.dtype)
+    max_scores.scatter_reduce_(0, index.unsqueeze(-1).expand_as(scores), scores, reduce="amax",
+                               include_self=False)
+    shifted = scores - max_scores[index]
+    exp_scores = shifted.exp()
+    sum_exp = torch.zeros(num_nodes, scores.shape[-1], dtype=scores.dtype)
+    sum_exp.scatter_add_(0, index.unsqueeze(-1).expand_as(exp_scores), exp_scores)
+    return exp_scores / sum_exp[index].clamp(min=1e-8)

@@ -1,0 +1,97 @@
+"""GPU parity of the segment softmax (drop-in for _sparse_softmax,
+geoembodied/nn/modules/invariant_attention.py:202-230) against the float64 oracle.
+
+Bars: float32 |w - ref| <= 2e-6 + 1e-5 |ref| (exp and division are correctly rounded or within
+a few ulp; the segment sum adds deg roundings); float64 1e-12 relative; the backward likewise
+against the oracle's analytic gradient, which test_oracle.py pins to torch autograd of the
+reference's op sequence.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    import geoembodied  # noqa: F401
+    from geoembodied.functional.segment_softmax import segment_softmax, sparse_softmax
+    return segment_softmax, sparse_softmax
+
+
+def _check(got, ref, dtype):
+    got = got.detach().cpu().double().numpy()
+    if dtype == torch.float64:
+        np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-15)
+    else:
+        assert np.all(np.abs(got - ref) <= 2e-6 + 1e-5 * np.abs(ref)), float(np.max(np.abs(got - ref)))
+
+
+@pytest.mark.parametrize("E,N,H", [(1, 1, 1), (500, 40, 1), (3000, 200, 4), (20000, 3000, 8),
+                                   (70000, 4000, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_sparse_softmax_vs_oracle(dev, E, N, H, dtype):
+    _, sparse_softmax = _ops()
+    g = torch.Generator().manual_seed(E + H)
+    index = torch.randint(0, N, (E,), generator=g)
+    x = (torch.randn(E, H, generator=g, dtype=torch.float64) * 4).to(dtype)
+    xg = x.to(dev).requires_grad_(True)
+    w = sparse_softmax(xg, index.to(dev), N)
+    assert w.shape == (E, H) and w.dtype == dtype
+    ref = oracle.sparse_softmax(x.double().numpy(), index.numpy(), N)
+    _check(w, ref, dtype)
+    gr = torch.randn(E, H, generator=g, dtype=torch.float64).to(dtype)
+    w.backward(gr.to(dev))
+    want = oracle.sparse_softmax_bwd(gr.double().numpy(), w.detach().cpu().double().numpy(),
+                                     index.numpy(), N)
+    _check(xg.grad, want, dtype)
+
+
+def test_segment_softmax_csr_identity_perm_and_1d(dev):
+    segment_softmax, _ = _ops()
+    deg = torch.tensor([3, 0, 1, 5, 2])
+    ne = deg.cumsum(0).int()
+    ns = ne - deg.int()
+    E = int(deg.sum())
+    index = torch.repeat_interleave(torch.arange(5), deg)
+    x = torch.randn(E, dtype=torch.float64)
+    w = segment_softmax(x.to(dev), None, ns.to(dev), ne.to(dev), 5)
+    assert w.shape == (E,)
+    _check(w, oracle.sparse_softmax(x.numpy(), index.numpy(), 5), torch.float64)
+
+
+def test_softmax_special_values_and_unlisted_rows(dev):
+    _, sparse_softmax = _ops()
+    x = torch.tensor([[1.0], [float("nan")], [2.0], [float("-inf")], [0.5], [float("inf")], [3.0]])
+    index = torch.tensor([0, 0, 1, 1, 2, 3, 3])
+    w = sparse_softmax(x.to(dev), index.to(dev), 5).cpu().numpy()
+    ref = oracle.sparse_softmax(x.double().numpy(), index.numpy(), 5)
+    np.testing.assert_array_equal(np.isnan(w), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_allclose(w[ok], ref[ok], rtol=1e-6)
+    # rows of edges outside every segment are 0 (the CSR build sorts them last)
+    from gdl_amd.csrc import segment_softmax_forward_hip
+    ns = torch.tensor([0, 2], dtype=torch.int32, device=dev)
+    ne = torch.tensor([2, 3], dtype=torch.int32, device=dev)
+    out = segment_softmax_forward_hip(torch.ones(5, 2, device=dev), None, ns, ne, 2)
+    assert out.cpu().tolist() == [[0.5, 0.5], [0.5, 0.5], [1.0, 1.0], [0.0, 0.0], [0.0, 0.0]]
+
+
+def test_softmax_bf16_input_promoted(dev):
+    _, sparse_softmax = _ops()
+    x = torch.randn(1000, 2).bfloat16()
+    index = torch.randint(0, 50, (1000,))
+    w = sparse_softmax(x.to(dev), index.to(dev), 50)
+    assert w.dtype == torch.float32
+    _check(w, oracle.sparse_softmax(x.double().numpy(), index.numpy(), 50), torch.float32)
+
+
+def test_softmax_gradcheck_fp64(dev):
+    _, sparse_softmax = _ops()
+    g = torch.Generator().manual_seed(1)
+    index = torch.randint(0, 7, (40,), generator=g).to(dev)
+    x = torch.randn(40, 2, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda t: sparse_softmax(t, index, 7), (x,))

@@ -347,3 +347,43 @@ def test_bf16_round_matches_torch():
     np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
     ok = ~np.isnan(want)
     np.testing.assert_array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+
+
+# ----------------------------------------------------------------------- segment softmax ---
+
+def test_sparse_softmax_vs_reference_op_sequence_and_closed_forms():
+    """The oracle equals the reference's own torch op sequence (invariant_attention.py:202-230,
+    restated in ref_cpu_path.sparse_softmax) in float64, and the closed forms hold: equal scores
+    give 1/degree, a lone edge gives 1, every segment sums to 1, a constant shift changes
+    nothing."""
+    g = np.random.default_rng(4)
+    N, E, H = 40, 300, 3
+    index = g.integers(0, N, E)
+    x = g.standard_normal((E, H)) * 3
+    w = oracle.sparse_softmax(x, index, N)
+    ref = ref_cpu_path.sparse_softmax(torch.from_numpy(x), torch.from_numpy(index), N).numpy()
+    np.testing.assert_allclose(w, ref, rtol=1e-13, atol=1e-15)
+    sums = np.zeros((N, H))
+    np.add.at(sums, index, w)
+    deg = np.bincount(index, minlength=N)
+    np.testing.assert_allclose(sums[deg > 0], 1.0, rtol=1e-13)
+    np.testing.assert_allclose(oracle.sparse_softmax(x + 7.5, index, N), w, rtol=1e-12, atol=1e-15)
+    eq = oracle.sparse_softmax(np.ones((E, H)), index, N)
+    np.testing.assert_allclose(eq, (1.0 / deg[index])[:, None].repeat(H, 1), rtol=1e-15)
+    assert oracle.sparse_softmax(np.array([[-3.0]]), np.array([2]), 5).tolist() == [[1.0]]
+    # NaN makes its segment NaN, as torch's amax does
+    xn = np.array([[1.0], [np.nan], [2.0]])
+    wn = oracle.sparse_softmax(xn, np.array([0, 0, 1]), 2)
+    assert np.isnan(wn[:2]).all() and wn[2, 0] == 1.0
+
+
+def test_sparse_softmax_backward_vs_torch_autograd():
+    g = np.random.default_rng(5)
+    N, E, H = 25, 200, 2
+    index = g.integers(0, N, E)
+    x = torch.from_numpy(g.standard_normal((E, H))).requires_grad_(True)
+    gr = g.standard_normal((E, H))
+    ref_cpu_path.sparse_softmax(x, torch.from_numpy(index), N).backward(torch.from_numpy(gr))
+    w = oracle.sparse_softmax(x.detach().numpy(), index, N)
+    np.testing.assert_allclose(oracle.sparse_softmax_bwd(gr, w, index, N), x.grad.numpy(),
+                               rtol=1e-10, atol=1e-13)
