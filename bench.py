@@ -239,6 +239,14 @@ def main() -> int:
             lambda: sparse_softmax(scores, col, pos.shape[0]), args.steps, 3), 2)
         log(f"  segment softmax (E={row.numel()}, H=4): {legs['c2_softmax_fwd_us']} us on the CSR, "
             f"{legs['c2_sparse_softmax_us']} us from the target index")
+        # interpolation of 112-channel features (64 scalars + 16 vectors) from the centres back
+        # to every point with k = 3 IDW (the interpolation layer's shape)
+        from gdl_amd.functional.gather import knn_interpolate
+        ii, dd = knn(pos, cent, ptr, ptr_q, 3)
+        feats = torch.randn(cent.shape[0], 112, device=dev)
+        legs["c2_interp_k3_c112_us"] = round(1e3 * event_ms(lambda: knn_interpolate(feats, ii, dd),
+                                                            args.iters, 5), 2)
+        log(f"  knn_interpolate (65536 x k=3 x 112 ch): {legs['c2_interp_k3_c112_us']} us")
 
     # ---------------------------------------------------------------- C3 roofline ---
     roof = None

@@ -49,6 +49,11 @@ _SIGNATURES = {
                                         c_vp]),
     "geo_segment_softmax_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                         c_vp, c_vp]),
+    "geo_gather_weighted_sum": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
+                                        c_vp]),
+    "geo_gather_weighted_sum_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                                            c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "geo_idw_weights": (c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -342,6 +342,76 @@ def segment_softmax_backward_hip(
     return grad
 
 
+def gather_weighted_sum_forward_hip(feat: Tensor, idx: Tensor, w: Tensor) -> Tensor:
+    """out[n] = sum_k w[n, k] * feat[idx[n, k]] (idx < 0 or >= N_src contributes nothing)."""
+    _require_gpu("gather_weighted_sum", feat, idx, w)
+    if feat.dim() != 2 or idx.dim() != 2 or w.shape != idx.shape:
+        raise ValueError(f"gather_weighted_sum: feat [N_src, C], idx and w [N_out, K]; got "
+                         f"{tuple(feat.shape)}, {tuple(idx.shape)}, {tuple(w.shape)}")
+    code = _dtype_code("gather_weighted_sum", feat)
+    dev = feat.device
+    feat = feat.contiguous()
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    w = w.to(device=dev, dtype=feat.dtype).contiguous()
+    (N_src, C), (N_out, K) = feat.shape, idx.shape
+    out = torch.empty(N_out, C, dtype=feat.dtype, device=dev)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_gather_weighted_sum(
+            code, _nat.ptr(feat), N_src, C, _nat.ptr(idx), _nat.ptr(w), N_out, K, _nat.ptr(out),
+            _nat.stream_of(dev)), "geo_gather_weighted_sum")
+    return out
+
+
+def gather_weighted_sum_backward_hip(
+    grad_out: Tensor,
+    feat: Tensor,
+    idx: Tensor,
+    w: Tensor,
+    need_feat: bool = True,
+    need_w: bool = True,
+    csr: Optional[Tuple[Tensor, Tensor, Tensor, Tensor]] = None,
+) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+    """(grad_feat [N_src, C], grad_w [N_out, K]) of gather_weighted_sum; ``csr`` is the CSR of
+    the flattened idx over the sources (built here when not given)."""
+    _require_gpu("gather_weighted_sum backward", grad_out, feat, idx, w)
+    code = _dtype_code("gather_weighted_sum backward", feat)
+    dev = feat.device
+    grad_out = grad_out.to(feat.dtype).contiguous()
+    feat = feat.contiguous()
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    w = w.to(device=dev, dtype=feat.dtype).contiguous()
+    (N_src, C), (N_out, K) = feat.shape, idx.shape
+    grad_feat = torch.empty(N_src, C, dtype=feat.dtype, device=dev) if need_feat else None
+    grad_w = torch.empty(N_out, K, dtype=feat.dtype, device=dev) if need_w else None
+    pm = ns = ne = None
+    if need_feat:
+        if csr is None:
+            csr = sort_and_build_csr_cuda(idx.reshape(-1), N_src)
+        _, pm, ns, ne = csr
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_gather_weighted_sum_bwd(
+            code, _nat.ptr(grad_out), _nat.ptr(feat), _nat.ptr(w), _nat.ptr(idx), N_src, C,
+            N_out, K, _nat.ptr(pm), _nat.ptr(ns), _nat.ptr(ne), _nat.ptr(grad_feat),
+            _nat.ptr(grad_w), _nat.stream_of(dev)), "geo_gather_weighted_sum_bwd")
+    return grad_feat, grad_w
+
+
+def idw_weights_hip(idx: Tensor, dist: Tensor) -> Tensor:
+    """Inverse-distance weights of the interpolation layer (equivariant_interp.py:95-99)."""
+    _require_gpu("idw_weights", idx, dist)
+    dev = dist.device
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    dist = dist.to(torch.float32).contiguous()
+    if idx.shape != dist.shape or idx.dim() != 2:
+        raise ValueError("idw_weights: idx and dist must both be [N_out, K]")
+    N_out, K = idx.shape
+    w = torch.empty(N_out, K, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_idw_weights(_nat.ptr(idx), _nat.ptr(dist), N_out, K, _nat.ptr(w),
+                                              _nat.stream_of(dev)), "geo_idw_weights")
+    return w
+
+
 # ═══════════════════════════════════════════════════════════════════
 # KNN
 # ═══════════════════════════════════════════════════════════════════
@@ -451,6 +521,7 @@ __all__ = [
     "get_radius_graph_backend", "radius_graph_cuda", "radius_graph_hip", "fp32_radius_sq",
     "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
     "segment_softmax_forward_hip", "segment_softmax_backward_hip",
+    "gather_weighted_sum_forward_hip", "gather_weighted_sum_backward_hip", "idw_weights_hip",
     "segment_reduce_forward_hip", "segment_reduce_backward_hip",
     "knn_available", "knn_cuda", "knn_self_cuda",
     "fps_available", "fps_cuda",

@@ -14,6 +14,7 @@ _ALIASES = (
     "csrc",
     "functional",
     "functional.fps",
+    "functional.gather",
     "functional.knn",
     "functional.radius_graph",
     "functional.segment_reduce",

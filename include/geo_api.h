@@ -200,6 +200,42 @@ int geo_segment_softmax_bwd(int dtype, const void* grad_out, const void* out,
                             const int32_t* node_end, int64_t E, int64_t S, int64_t H,
                             void* grad_scores, void* stream);
 
+/* --------------------------------------------------- neighbourhood gather-sum --- */
+/*
+ * Fused weighted gather-sum over fixed-width neighbourhoods, replacing the gather + broadcast +
+ * sum over an [N_out, K, C] temporary of the interpolation, pooling and skip-fusion layers
+ * (geoembodied/nn/modules/equivariant_interp.py:95-125, equivariant_pool.py:412-471,
+ * equivariant_skip_fusion.py:304-320):
+ *
+ *   out[n, :] = sum_k w[n, k] * feat[idx[n, k], :]
+ *
+ * feat [N_src, C], w [N_out, K] and out [N_out, C] of `dtype` (accumulation in fp32, fp64 for
+ * GEO_F64); idx [N_out, K] int64 as KNN returns it: entries outside [0, N_src) (the -1 padding)
+ * contribute nothing, so a row without neighbours is 0.  K <= 32.
+ */
+int geo_gather_weighted_sum(int dtype, const void* feat, int64_t N_src, int64_t C,
+                            const int64_t* idx, const void* w, int64_t N_out, int64_t K,
+                            void* out, void* stream);
+/*
+ * Backward.  grad_w[n, k] = <grad_out[n], feat[idx[n, k]]> (0 for padding) when grad_w is
+ * non-NULL; grad_feat[j] = sum over the (n, k) with idx[n, k] = j of w[n, k] * grad_out[n] when
+ * grad_feat is non-NULL, which needs the CSR of idx over the sources: geo_csr_build of the
+ * flattened idx with N = N_src (perm, node_start, node_end).  Every row of each requested
+ * gradient is written.
+ */
+int geo_gather_weighted_sum_bwd(int dtype, const void* grad_out, const void* feat, const void* w,
+                                const int64_t* idx, int64_t N_src, int64_t C, int64_t N_out,
+                                int64_t K, const int32_t* perm, const int32_t* node_start,
+                                const int32_t* node_end, void* grad_feat, void* grad_w,
+                                void* stream);
+/*
+ * Inverse-distance weights of the interpolation layer (equivariant_interp.py:95-99): for each
+ * row, v_k = 1 / sqrt(max(dist[n, k], 1e-4)) where idx[n, k] >= 0 (else 0), w = v / max(sum v,
+ * 1e-8).  dist and w are fp32 [N_out, K]; K <= 32.
+ */
+int geo_idw_weights(const int64_t* idx, const float* dist, int64_t N_out, int64_t K, float* w,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

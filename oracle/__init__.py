@@ -12,6 +12,8 @@ Contents:
   float64 and returned with the per-element scale ``sum |msg|`` that the tolerance of the
   comparison multiplies; max, argmax and every backward value are exact.
 * Segment softmax (``sparse_softmax``) and its backward: numpy float64 below.
+* Neighbourhood gather-sum (``gather_weighted_sum``, ``idw_weights``) and its backward: numpy
+  float64 below.
 
 Pinning (what checks each function independently of this restatement) is listed in
 ``tests/test_oracle.py``: reference KATs, closed forms on integer lattices where fp32 arithmetic
@@ -303,3 +305,41 @@ def sparse_softmax_bwd(grad, w, index, N: int) -> np.ndarray:
     dot = np.zeros((N,) + w.shape[1:])
     np.add.at(dot, idx, g * w)
     return w * (g - dot[idx])
+
+
+# ------------------------------------------------------------- neighbourhood gather-sum ---
+
+def idw_weights(idx, dist) -> np.ndarray:
+    """Inverse-distance weights, float64: v = 1/sqrt(max(d, 1e-4)) for idx >= 0 else 0, divided
+    by max(sum v, 1e-8) (geoembodied/nn/modules/equivariant_interp.py:95-99)."""
+    i = np.asarray(idx, dtype=np.int64)
+    d = np.asarray(dist, dtype=np.float64)
+    v = np.where(i >= 0, 1.0 / np.sqrt(np.maximum(d, 1e-4)), 0.0)
+    return v / np.maximum(v.sum(-1, keepdims=True), 1e-8)
+
+
+def gather_weighted_sum(feat, idx, w):
+    """(out [N_out, C] float64, scale = sum_k |w| |feat| per element) of out[n] = sum_k w[n, k] *
+    feat[idx[n, k]], padding (idx outside [0, N_src)) skipped — the reference's
+    (w.unsqueeze(-1) * feat[idx.clamp(min=0)]).sum(1) with zero weights on padding
+    (equivariant_interp.py:104-125)."""
+    f = np.asarray(feat, dtype=np.float64)
+    i = np.asarray(idx, dtype=np.int64)
+    wt = np.asarray(w, dtype=np.float64)
+    ok = (i >= 0) & (i < f.shape[0])
+    g = f[np.where(ok, i, 0)] * ok[..., None]
+    return (wt[..., None] * g).sum(1), (np.abs(wt)[..., None] * np.abs(g)).sum(1)
+
+
+def gather_weighted_sum_bwd(grad_out, feat, idx, w):
+    """(grad_feat, grad_w) of gather_weighted_sum, float64."""
+    go = np.asarray(grad_out, dtype=np.float64)
+    f = np.asarray(feat, dtype=np.float64)
+    i = np.asarray(idx, dtype=np.int64)
+    wt = np.asarray(w, dtype=np.float64)
+    ok = (i >= 0) & (i < f.shape[0])
+    gf = np.zeros_like(f)
+    n_idx, k_idx = np.nonzero(ok)
+    np.add.at(gf, i[n_idx, k_idx], wt[n_idx, k_idx][:, None] * go[n_idx])
+    gw = np.where(ok, np.einsum("nc,nkc->nk", go, f[np.where(ok, i, 0)]), 0.0)
+    return gf, gw

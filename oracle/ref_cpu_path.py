@@ -13,6 +13,8 @@ is what a user of the reference pays on the CPU:
 * ``sort_and_build_csr`` / ``segment_sum`` — _sort_and_build_csr_pytorch and
                        _segment_reduce_pytorch, geoembodied/functional/segment_reduce.py:77-199:
                        argsort + bincount/cumsum, then a Python loop over segments.
+* ``idw_interpolate`` — the interpolation layer's IDW weights and neighbourhood sum,
+                       geoembodied/nn/modules/equivariant_interp.py:95-125.
 * ``sparse_softmax`` — _sparse_softmax, geoembodied/nn/modules/invariant_attention.py:202-230:
                        scatter 'amax', exp, scatter_add, divide.
 
@@ -116,3 +118,19 @@ def sparse_softmax(scores: Tensor, index: Tensor, num_nodes: int) -> Tensor:
     sum_exp = torch.zeros(num_nodes, scores.shape[-1], dtype=scores.dtype)
     sum_exp.scatter_add_(0, index.unsqueeze(-1).expand_as(exp_scores), exp_scores)
     return exp_scores / sum_exp[index].clamp(min=1e-8)
+
+
+def idw_interpolate(feat: Tensor, knn_idx: Tensor, knn_dists: Tensor) -> Tensor:
+    """The interpolation layer's weights and aggregation, geoembodied/nn/modules/
+    equivariant_interp.py:95-125: IDW weights, gather with idx.clamp(min=0), weighted sum over
+    the neighbours, rows without a valid neighbour set to 0."""
+    valid_mask = knn_idx >= 0
+    inv_dist = 1.0 / knn_dists.clamp(min=1e-4).sqrt()
+    inv_dist = inv_dist.masked_fill(~valid_mask, 0.0)
+    weight_sum = inv_dist.sum(dim=-1, keepdim=True).clamp(min=1e-8)
+    weights = inv_dist / weight_sum
+    safe_idx = knn_idx.clamp(min=0)
+    out = (weights.unsqueeze(-1) * feat[safe_idx]).sum(dim=1)
+    all_invalid = ~valid_mask.any(dim=1)
+    out[all_invalid] = 0.0
+    return out

@@ -387,3 +387,45 @@ def test_sparse_softmax_backward_vs_torch_autograd():
     w = oracle.sparse_softmax(x.detach().numpy(), index, N)
     np.testing.assert_allclose(oracle.sparse_softmax_bwd(gr, w, index, N), x.grad.numpy(),
                                rtol=1e-10, atol=1e-13)
+
+
+# ----------------------------------------------------------- neighbourhood gather-sum ---
+
+def test_idw_interpolation_vs_reference_op_sequence_and_closed_forms():
+    """oracle idw_weights + gather_weighted_sum equal the reference's interpolation op sequence
+    (equivariant_interp.py:95-125, restated in ref_cpu_path.idw_interpolate) in float64; equal
+    distances give 1/(valid neighbours); a lone valid neighbour gets weight 1; all-padding rows
+    are 0; the sum is linear in the features."""
+    g = np.random.default_rng(7)
+    Ns, No, K, C = 50, 30, 4, 6
+    idx = g.integers(0, Ns, (No, K))
+    idx[3, 1:] = -1
+    idx[4] = -1
+    dist = g.random((No, K)) * 2
+    dist[5] = 0.7
+    feat = g.standard_normal((Ns, C))
+    w = oracle.idw_weights(idx, dist)
+    out, _ = oracle.gather_weighted_sum(feat, idx, w)
+    ref = ref_cpu_path.idw_interpolate(torch.from_numpy(feat), torch.from_numpy(idx),
+                                       torch.from_numpy(dist)).numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(w[5], 0.25, rtol=1e-15)
+    assert w[3].tolist() == [1.0, 0.0, 0.0, 0.0] and (out[4] == 0).all()
+    out2, _ = oracle.gather_weighted_sum(2 * feat + 1, idx, w)
+    np.testing.assert_allclose(out2, 2 * out + w.sum(1, keepdims=True) * (idx >= 0).any(1, keepdims=True),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_gather_weighted_sum_backward_vs_torch_autograd():
+    g = np.random.default_rng(8)
+    Ns, No, K, C = 40, 25, 5, 3
+    idx = g.integers(-1, Ns, (No, K))
+    f = torch.from_numpy(g.standard_normal((Ns, C))).requires_grad_(True)
+    w = torch.from_numpy(g.standard_normal((No, K))).requires_grad_(True)
+    ok = torch.from_numpy(idx >= 0)
+    out = ((w * ok).unsqueeze(-1) * f[torch.from_numpy(idx).clamp(min=0)]).sum(1)
+    go = g.standard_normal((No, C))
+    out.backward(torch.from_numpy(go))
+    gf, gw = oracle.gather_weighted_sum_bwd(go, f.detach().numpy(), idx, w.detach().numpy())
+    np.testing.assert_allclose(gf, f.grad.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(gw, w.grad.numpy(), rtol=1e-12, atol=1e-14)
