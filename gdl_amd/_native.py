@@ -54,6 +54,13 @@ _SIGNATURES = {
     "geo_gather_weighted_sum_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                             c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_idw_weights": (c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "geo_radius_count_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
+                                     c_vp, c_vp, c_size, c_vp]),
+    "geo_radius_emit_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
+                                    c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
+    "geo_knn_radius_stat_workspace_bytes": (c_size, [c_i64]),
+    "geo_knn_radius_stat": (c_int, [c_vp, c_i64, c_i64, c_i64, c_int, ctypes.c_double, c_vp, c_vp,
+                                    c_size, c_vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -72,7 +72,7 @@ def get_radius_graph_backend() -> str:
 
 def radius_graph_hip(
     x: Tensor,
-    r: float,
+    r,
     *,
     max_num_neighbors: int = 32,
     loop: bool = False,
@@ -82,7 +82,9 @@ def radius_graph_hip(
 ) -> Tuple[Tensor, Tensor]:
     """Radius graph on the GPU; returns (row=source, col=target) int64, sorted by target then
     source.  Cloud membership comes from ``batch`` when given, otherwise from
-    ``num_batch_elements`` contiguous equal chunks (one cloud when neither is given)."""
+    ``num_batch_elements`` contiguous equal chunks (one cloud when neither is given).  ``r`` is a
+    Python number or a one-element device tensor (e.g. an adaptive radius computed on the GPU),
+    which the kernels read directly: no host round trip for the radius."""
     _require_gpu("radius_graph", x, mask, batch)
     x = _positions("radius_graph", x)
     dev = x.device
@@ -90,6 +92,12 @@ def radius_graph_hip(
     K = int(max_num_neighbors)
     if K < 0:
         raise ValueError(f"radius_graph: max_num_neighbors must be >= 0, got {K}")
+    r_dev = None
+    if isinstance(r, Tensor):
+        if r.numel() != 1:
+            raise ValueError(f"radius_graph: a tensor radius must have one element, got {r.numel()}")
+        r_dev = r.reshape(()).to(device=dev, dtype=torch.float64).contiguous()
+        r = 1.0
     r = float(r)
     empty = torch.empty(0, dtype=torch.int64, device=dev)
     if N == 0 or K == 0 or not (r > 0.0):
@@ -121,15 +129,21 @@ def radius_graph_hip(
         ws_bytes = L.geo_radius_workspace_bytes(N, B, K)
         ws = _nat.workspace(ws_bytes, dev)
         row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
-        args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K, int(bool(loop)))
-        _nat.check(L.geo_radius_count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s),
-                   "geo_radius_count")
+        if r_dev is None:
+            count, emit = L.geo_radius_count, L.geo_radius_emit
+            args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K,
+                    int(bool(loop)))
+        else:
+            count, emit = L.geo_radius_count_dev, L.geo_radius_emit_dev
+            args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), _nat.ptr(r_dev), K,
+                    int(bool(loop)))
+        _nat.check(count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s), "geo_radius_count")
         E = int(row_ptr[N].item())
         row = torch.empty(E, dtype=torch.int64, device=dev)
         col = torch.empty(E, dtype=torch.int64, device=dev)
         if E > 0:
-            _nat.check(L.geo_radius_emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col),
-                                         _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
+            _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col), _nat.ptr(ws),
+                            ws_bytes, s), "geo_radius_emit")
     return row, col
 
 
@@ -412,6 +426,29 @@ def idw_weights_hip(idx: Tensor, dist: Tensor) -> Tensor:
     return w
 
 
+def knn_radius_stat_hip(dist: Tensor, col: int, mode: str, multiplier: float) -> Tensor:
+    """multiplier * (mean of sqrt(clamp(d, 1e-8, 1e20)) | lower median of sqrt(max(d, 1e-12)))
+    over column ``col`` of a KNN distance matrix, as a float64 device scalar (no host sync)."""
+    _require_gpu("knn_radius_stat", dist)
+    if dist.dim() != 2 or dist.shape[0] == 0:
+        raise ValueError(f"knn_radius_stat: dist must be a non-empty [N, k], got {tuple(dist.shape)}")
+    codes = {"mean": 0, "median": 1}
+    if mode not in codes:
+        raise ValueError(f"knn_radius_stat: mode must be 'mean' or 'median', got {mode!r}")
+    dev = dist.device
+    d = dist.to(torch.float32).contiguous()
+    N, k = d.shape
+    out = torch.empty((), dtype=torch.float64, device=dev)
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        ws_bytes = L.geo_knn_radius_stat_workspace_bytes(N)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_knn_radius_stat(_nat.ptr(d), N, k, int(col) % k, codes[mode],
+                                         float(multiplier), _nat.ptr(out), _nat.ptr(ws), ws_bytes,
+                                         _nat.stream_of(dev)), "geo_knn_radius_stat")
+    return out
+
+
 # ═══════════════════════════════════════════════════════════════════
 # KNN
 # ═══════════════════════════════════════════════════════════════════
@@ -522,6 +559,7 @@ __all__ = [
     "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
     "segment_softmax_forward_hip", "segment_softmax_backward_hip",
     "gather_weighted_sum_forward_hip", "gather_weighted_sum_backward_hip", "idw_weights_hip",
+    "knn_radius_stat_hip",
     "segment_reduce_forward_hip", "segment_reduce_backward_hip",
     "knn_available", "knn_cuda", "knn_self_cuda",
     "fps_available", "fps_cuda",

@@ -54,7 +54,21 @@ struct RgWs {
   int32_t* list;  // [N][K] accepted sources per target (unsorted), or null when too large
   int64_t cells_max;
   size_t bytes;
+  const double* r_dev = nullptr;  // radius on the device (geo_radius_*_dev), else null
 };
+
+// Threshold and cell edge: the host values, or those of the device radius r (fl32(r * r) with the
+// product in float64, as the host computes it; r <= 0 or NaN gives no edges).
+__device__ __forceinline__ float rg_r2(const RgWs& w, float r2) {
+  if (!w.r_dev) return r2;
+  const double r = *w.r_dev;
+  return r > 0.0 ? static_cast<float>(r * r) : 0.0f;
+}
+__device__ __forceinline__ float rg_rcell(const RgWs& w, float r_cell) {
+  if (!w.r_dev) return r_cell;
+  const double r = *w.r_dev;
+  return r > 0.0 ? static_cast<float>(r) : 1.0f;
+}
 
 int64_t cells_cap(int64_t N, int64_t B) { return 4 * N + 64 * B; }
 
@@ -173,6 +187,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __res
 // Single workgroup: grid parameters and cell bases for every cloud.
 __global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, float r_cell) {
   __shared__ int64_t lds[kScanThreads / kWave];
+  r_cell = rg_rcell(w, r_cell);
   int64_t carry = 0;
   for (int64_t base = 0; base < B; base += kScanThreads) {
     const int64_t b = base + threadIdx.x;
@@ -350,6 +365,7 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
                          int64_t* __restrict__ row_out, int64_t* __restrict__ col_out,
                          int use_lds) {
   extern __shared__ int32_t lbuf[];  // emit: K entries per thread, column-major by thread
+  r2 = rg_r2(w, r2);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int total = w.cell_start[w.cells_max];
   if (t >= total) return;
@@ -407,6 +423,7 @@ __global__ void rg_compact(RgWs w, const float* __restrict__ x, int64_t N,
                            int K, int loop, const int64_t* __restrict__ row_ptr,
                            int64_t* __restrict__ row_out, int64_t* __restrict__ col_out) {
   extern __shared__ int32_t stage[];  // K entries per thread when K <= kRgStageK
+  r2 = rg_r2(w, r2);
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= N) return;
   const int c = w.cnt[i];
@@ -474,16 +491,17 @@ extern "C" size_t geo_radius_workspace_bytes(int64_t N, int64_t B, int64_t max_n
   return carve_rg(nullptr, N, B, max_num_neighbors).bytes;
 }
 
-extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
-                                int64_t points_per_cloud, const uint8_t* mask, float r2,
-                                float r_cell, int64_t max_num_neighbors, int loop,
-                                int64_t* row_ptr, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                             int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
+                             const double* r_dev, int64_t max_num_neighbors, int loop,
+                             int64_t* row_ptr, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
   if (rc) return rc;
   GEO_REQUIRE(r_cell > 0.f, "radius_graph: r_cell must be positive");
   GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
   RgWs w = carve_rg(workspace, N, B, max_num_neighbors);
+  w.r_dev = r_dev;
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
                      workspace_bytes, w.bytes);
@@ -524,16 +542,16 @@ extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch,
   return device_exclusive_scan<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true, w.deg_tiles, st);
 }
 
-extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, int64_t B,
-                               int64_t points_per_cloud, const uint8_t* mask, float r2,
-                               float r_cell, int64_t max_num_neighbors, int loop,
-                               const int64_t* row_ptr, int64_t* row_out, int64_t* col_out,
-                               void* workspace, size_t workspace_bytes, void* stream) {
-  (void)mask; (void)r_cell;
+static int radius_emit_impl(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                            int64_t points_per_cloud, float r2, const double* r_dev,
+                            int64_t max_num_neighbors, int loop, const int64_t* row_ptr,
+                            int64_t* row_out, int64_t* col_out, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
   if (rc) return rc;
   GEO_REQUIRE(row_ptr != nullptr, "radius_graph: null row_ptr");
   RgWs w = carve_rg(workspace, N, B, max_num_neighbors);
+  w.r_dev = r_dev;
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(GEO_ERR_WORKSPACE, "radius_graph: workspace %zu bytes, need %zu",
                      workspace_bytes, w.bytes);
@@ -555,4 +573,44 @@ extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, 
                      points_per_cloud, r2, K, loop, row_ptr, row_out, col_out, use_lds);
   GEO_LAUNCH_CHECK("rg_query<emit>");
   return GEO_OK;
+}
+
+extern "C" int geo_radius_count(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                                int64_t points_per_cloud, const uint8_t* mask, float r2,
+                                float r_cell, int64_t max_num_neighbors, int loop,
+                                int64_t* row_ptr, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  return radius_count_impl(x, N, batch, B, points_per_cloud, mask, r2, r_cell, nullptr,
+                           max_num_neighbors, loop, row_ptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                               int64_t points_per_cloud, const uint8_t* mask, float r2,
+                               float r_cell, int64_t max_num_neighbors, int loop,
+                               const int64_t* row_ptr, int64_t* row_out, int64_t* col_out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  (void)mask; (void)r_cell;
+  return radius_emit_impl(x, N, batch, B, points_per_cloud, r2, nullptr, max_num_neighbors, loop,
+                          row_ptr, row_out, col_out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int geo_radius_count_dev(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                                    int64_t points_per_cloud, const uint8_t* mask,
+                                    const double* radius, int64_t max_num_neighbors, int loop,
+                                    int64_t* row_ptr, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  GEO_REQUIRE(radius != nullptr, "radius_graph: null device radius");
+  return radius_count_impl(x, N, batch, B, points_per_cloud, mask, 0.f, 1.f, radius,
+                           max_num_neighbors, loop, row_ptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int geo_radius_emit_dev(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                                   int64_t points_per_cloud, const uint8_t* mask,
+                                   const double* radius, int64_t max_num_neighbors, int loop,
+                                   const int64_t* row_ptr, int64_t* row_out, int64_t* col_out,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  (void)mask;
+  GEO_REQUIRE(radius != nullptr, "radius_graph: null device radius");
+  return radius_emit_impl(x, N, batch, B, points_per_cloud, 0.f, radius, max_num_neighbors, loop,
+                          row_ptr, row_out, col_out, workspace, workspace_bytes, stream);
 }

@@ -29,7 +29,8 @@ def radius_graph(
 
     Args:
         x: [N, 3] positions (GPU).
-        r: radius (strict: ``|xi - xj| < r``).
+        r: radius (strict: ``|xi - xj| < r``): a number, or a one-element device tensor such
+            as ``adaptive_radius(...)`` returns (read by the kernels, no host sync).
         max_num_neighbors: cap on sources per target.
         batch: optional [N] cloud id per point (any order).
         loop: include self edges.

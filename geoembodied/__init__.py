@@ -13,6 +13,7 @@ import sys
 _ALIASES = (
     "csrc",
     "functional",
+    "functional.adaptive",
     "functional.fps",
     "functional.gather",
     "functional.knn",

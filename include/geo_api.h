@@ -128,6 +128,37 @@ int geo_radius_emit(const float* x, int64_t N, const int64_t* batch, int64_t B,
                     int64_t* row_out, int64_t* col_out, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/*
+ * The same two phases with the radius read from device memory (`radius`: one float64), so a
+ * radius computed on the GPU (geo_knn_radius_stat) needs no host round trip: the threshold is
+ * fl32(radius * radius) with the product in float64 — what the host computes for a Python
+ * float — and radius <= 0 or NaN gives no edges.  Replaces the .item() of the adaptive radius
+ * (geoembodied/nn/modules/multi_scale_se3_net.py:99-124) feeding radius_graph.
+ */
+int geo_radius_count_dev(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                         int64_t points_per_cloud, const uint8_t* mask, const double* radius,
+                         int64_t max_num_neighbors, int loop, int64_t* row_ptr, void* workspace,
+                         size_t workspace_bytes, void* stream);
+int geo_radius_emit_dev(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                        int64_t points_per_cloud, const uint8_t* mask, const double* radius,
+                        int64_t max_num_neighbors, int loop, const int64_t* row_ptr,
+                        int64_t* row_out, int64_t* col_out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------- adaptive radius statistic --- */
+/*
+ * Device-side statistic of column `col` of a KNN distance matrix dist [N, k] (fp32 squared
+ * distances), written as one float64 to `out` (device):
+ *   mode 0: multiplier * mean of sqrt(clamp(d, 1e-8, 1e20)) with the mean rounded to fp32
+ *           (geoembodied/nn/modules/multi_scale_se3_net.py:118-123, without the .item());
+ *   mode 1: multiplier * sqrt(lower median of max(d, 1e-12)), NaN if any d is NaN
+ *           (geoembodied/nn/modules/equivariant_skip_fusion.py:243-248, without the .item()).
+ */
+size_t geo_knn_radius_stat_workspace_bytes(int64_t N);
+int geo_knn_radius_stat(const float* dist, int64_t N, int64_t k, int64_t col, int mode,
+                        double multiplier, double* out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* -------------------------------------------------------------- CSR build --- */
 /*
  * Replaces sort_and_build_csr (geoembodied/csrc/segment_reduce_kernel.cu:100-169, bound at

@@ -343,3 +343,20 @@ def gather_weighted_sum_bwd(grad_out, feat, idx, w):
     np.add.at(gf, i[n_idx, k_idx], wt[n_idx, k_idx][:, None] * go[n_idx])
     gw = np.where(ok, np.einsum("nc,nkc->nk", go, f[np.where(ok, i, 0)]), 0.0)
     return gf, gw
+
+
+# ------------------------------------------------------------- adaptive radius statistic ---
+
+def knn_radius_stat(dist, col: int, mode: str, multiplier: float) -> float:
+    """mode "mean": multiplier * float32 mean of sqrt(clamp(d, 1e-8, 1e20)) (values in float32,
+    summed in float64, rounded once) — geoembodied/nn/modules/multi_scale_se3_net.py:118-123;
+    mode "median": multiplier * sqrt(lower median of max(d, 1e-12)), NaN if any d is NaN —
+    equivariant_skip_fusion.py:243-248."""
+    d = np.asarray(dist, dtype=np.float32)[:, col]
+    if mode == "mean":
+        v = np.sqrt(np.maximum(np.minimum(d, np.float32(1e20)), np.float32(1e-8)))
+        return float(np.float32(v.astype(np.float64).sum() / d.size)) * multiplier
+    c = np.maximum(d, np.float32(1e-12))
+    if np.isnan(c).any():
+        return float("nan")
+    return float(np.sqrt(np.sort(c)[(c.size - 1) // 2])) * multiplier

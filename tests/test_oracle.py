@@ -429,3 +429,25 @@ def test_gather_weighted_sum_backward_vs_torch_autograd():
     gf, gw = oracle.gather_weighted_sum_bwd(go, f.detach().numpy(), idx, w.detach().numpy())
     np.testing.assert_allclose(gf, f.grad.numpy(), rtol=1e-12, atol=1e-14)
     np.testing.assert_allclose(gw, w.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+# ------------------------------------------------------------ adaptive radius statistic ---
+
+def test_knn_radius_stat_vs_reference_expressions():
+    """The oracle statistic equals the reference's expressions evaluated by torch on the same
+    KNN distances: the mean up to float32 summation order, the median exactly."""
+    g = np.random.default_rng(11)
+    d = (g.random((5001, 2)) ** 2).astype(np.float32)
+    d[:, 0] = 0.0
+    d[7, 1] = 1e30   # padding distance: clamped at 1e20
+    d[9, 1] = 0.0    # duplicate point: clamped at 1e-8 / 1e-12
+    t = torch.from_numpy(d)
+    ref_mean = t[:, 1].clamp(max=1e20).clamp(min=1e-8).sqrt().mean().item() * 4.0
+    assert oracle.knn_radius_stat(d, 1, "mean", 4.0) == pytest.approx(ref_mean, rel=1e-6)
+    ref_med = t[:, -1].clamp(min=1e-12).sqrt().median().item() * 2.5
+    assert oracle.knn_radius_stat(d, 1, "median", 2.5) == ref_med
+    even = d[:5000]
+    assert oracle.knn_radius_stat(even, 1, "median", 1.0) == \
+        torch.from_numpy(even)[:, -1].clamp(min=1e-12).sqrt().median().item()
+    d[3, 1] = np.nan
+    assert np.isnan(oracle.knn_radius_stat(d, 1, "median", 1.0))
