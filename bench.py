@@ -247,6 +247,14 @@ def main() -> int:
         legs["c2_interp_k3_c112_us"] = round(1e3 * event_ms(lambda: knn_interpolate(feats, ii, dd),
                                                             args.iters, 5), 2)
         log(f"  knn_interpolate (65536 x k=3 x 112 ch): {legs['c2_interp_k3_c112_us']} us")
+        # the whole spatial graph: radius graph + CSR + directions, distances, SH (l <= 2) and
+        # average degrees, as one call
+        from gdl_amd.graph import SpatialGraph
+        legs["c2_spatial_graph_ms"] = wall_ms(
+            lambda: SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                       num_batch_elements=c2["B"]), args.steps, 3)
+        log(f"  SpatialGraph.build: {legs['c2_spatial_graph_ms']:.3f} ms "
+            f"(radius graph alone {legs['c2_radius_ms']:.3f} ms)")
 
     # ---------------------------------------------------------------- C3 roofline ---
     roof = None

@@ -59,6 +59,12 @@ _SIGNATURES = {
     "geo_radius_emit_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
                                     c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_knn_radius_stat_workspace_bytes": (c_size, [c_i64]),
+    "geo_edge_geometry": (c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_int, c_vp, c_vp, c_vp, c_vp]),
+    "geo_edge_geometry_bwd": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_vp]),
+    "geo_spherical_harmonics": (c_int, [c_vp, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp]),
+    "geo_spherical_harmonics_bwd": (c_int, [c_vp, c_vp, c_i64, c_int, c_vp, c_vp]),
+    "geo_graph_avg_degree_workspace_bytes": (c_size, [c_i64]),
+    "geo_graph_avg_degree": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_size, c_vp]),
     "geo_knn_radius_stat": (c_int, [c_vp, c_i64, c_i64, c_i64, c_int, ctypes.c_double, c_vp, c_vp,
                                     c_size, c_vp]),
 }

@@ -80,6 +80,21 @@ def radius_graph_hip(
     batch: Optional[Tensor] = None,
     num_batch_elements: Optional[int] = None,
 ) -> Tuple[Tensor, Tensor]:
+    row, col, _ = radius_graph_csr_hip(x, r, max_num_neighbors=max_num_neighbors, loop=loop,
+                                       mask=mask, batch=batch, num_batch_elements=num_batch_elements)
+    return row, col
+
+
+def radius_graph_csr_hip(
+    x: Tensor,
+    r,
+    *,
+    max_num_neighbors: int = 32,
+    loop: bool = False,
+    mask: Optional[Tensor] = None,
+    batch: Optional[Tensor] = None,
+    num_batch_elements: Optional[int] = None,
+) -> Tuple[Tensor, Tensor, Tensor]:
     """Radius graph on the GPU; returns (row=source, col=target) int64, sorted by target then
     source.  Cloud membership comes from ``batch`` when given, otherwise from
     ``num_batch_elements`` contiguous equal chunks (one cloud when neither is given).  ``r`` is a
@@ -101,7 +116,7 @@ def radius_graph_hip(
     r = float(r)
     empty = torch.empty(0, dtype=torch.int64, device=dev)
     if N == 0 or K == 0 or not (r > 0.0):
-        return empty, empty.clone()
+        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev)
     r2 = fp32_radius_sq(r)
     if batch is not None:
         if batch.numel() != N:
@@ -117,7 +132,7 @@ def radius_graph_hip(
             raise ValueError(f"radius_graph: {N} points do not split into {B} equal clouds")
         ppc = N // B
     if B < 1:
-        return empty, empty.clone()
+        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev)
     mask_u8 = None
     if mask is not None:
         if mask.numel() != N:
@@ -144,7 +159,7 @@ def radius_graph_hip(
         if E > 0:
             _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col), _nat.ptr(ws),
                             ws_bytes, s), "geo_radius_emit")
-    return row, col
+    return row, col, row_ptr
 
 
 def radius_graph_cuda(
@@ -449,6 +464,89 @@ def knn_radius_stat_hip(dist: Tensor, col: int, mode: str, multiplier: float) ->
     return out
 
 
+def edge_geometry_hip(pos: Tensor, row: Tensor, col: Tensor, max_l: int = 2,
+                      with_sh: bool = True) -> Tuple[Tensor, Tensor, Optional[Tensor]]:
+    """(direction [E, 3], dist [E], Y [E, (max_l+1)^2] or None) of the edges row -> col."""
+    _require_gpu("edge_geometry", pos, row, col)
+    pos = _positions("edge_geometry", pos)
+    dev = pos.device
+    row, col = _i64(row.reshape(-1), dev), _i64(col.reshape(-1), dev)
+    E = row.numel()
+    direction = torch.empty(E, 3, dtype=torch.float32, device=dev)
+    dist = torch.empty(E, dtype=torch.float32, device=dev)
+    Y = torch.empty(E, (max_l + 1) ** 2, dtype=torch.float32, device=dev) if with_sh else None
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_edge_geometry(
+            _nat.ptr(pos), pos.shape[0], _nat.ptr(row), _nat.ptr(col), E, int(max_l),
+            _nat.ptr(direction), _nat.ptr(dist), _nat.ptr(Y), _nat.stream_of(dev)), "geo_edge_geometry")
+    return direction, dist, Y
+
+
+def edge_geometry_backward_hip(direction: Tensor, dist: Tensor, grad_direction: Optional[Tensor],
+                               grad_dist: Optional[Tensor], grad_Y: Optional[Tensor],
+                               max_l: int = 2) -> Tensor:
+    """d loss / d diff [E, 3] from the gradients of direction, dist and Y."""
+    dev = direction.device
+    E = direction.shape[0]
+    out = torch.empty(E, 3, dtype=torch.float32, device=dev)
+
+    def f32(t):
+        return None if t is None else t.to(torch.float32).contiguous()
+
+    gd, gl, gy = f32(grad_direction), f32(grad_dist), f32(grad_Y)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_edge_geometry_bwd(
+            _nat.ptr(direction), _nat.ptr(dist), _nat.ptr(gd), _nat.ptr(gl), _nat.ptr(gy), E,
+            int(max_l), _nat.ptr(out), _nat.stream_of(dev)), "geo_edge_geometry_bwd")
+    return out
+
+
+def spherical_harmonics_hip(xyz: Tensor, max_l: int, normalize: bool):
+    """(Y [N, (max_l+1)^2], unit [N, 3] or None, norm [N] or None) of xyz [N, 3] (fp32)."""
+    _require_gpu("spherical_harmonics", xyz)
+    dev = xyz.device
+    xyz = xyz.to(torch.float32).contiguous()
+    N = xyz.shape[0]
+    Y = torch.empty(N, (max_l + 1) ** 2, dtype=torch.float32, device=dev)
+    unit = torch.empty(N, 3, dtype=torch.float32, device=dev) if normalize else None
+    norm = torch.empty(N, dtype=torch.float32, device=dev) if normalize else None
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_spherical_harmonics(
+            _nat.ptr(xyz), N, int(max_l), int(bool(normalize)), _nat.ptr(Y), _nat.ptr(unit),
+            _nat.ptr(norm), _nat.stream_of(dev)), "geo_spherical_harmonics")
+    return Y, unit, norm
+
+
+def spherical_harmonics_backward_hip(xyz: Tensor, grad_Y: Tensor, max_l: int) -> Tensor:
+    dev = xyz.device
+    N = xyz.shape[0]
+    out = torch.empty(N, 3, dtype=torch.float32, device=dev)
+    gY = grad_Y.to(torch.float32).contiguous()
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_spherical_harmonics_bwd(
+            _nat.ptr(xyz), _nat.ptr(gY), N, int(max_l), _nat.ptr(out), _nat.stream_of(dev)),
+            "geo_spherical_harmonics_bwd")
+    return out
+
+
+def graph_avg_degree_hip(row_ptr: Tensor, N: int, batch: Optional[Tensor], B: int) -> Tensor:
+    """Per-node average degree of its cloud from the CSR row pointer, clamped below at 1."""
+    dev = row_ptr.device
+    out = torch.empty(N, dtype=torch.float32, device=dev)
+    if N == 0:
+        return out
+    ppc = 0 if batch is not None else N // max(B, 1)
+    b = None if batch is None else _i64(batch.reshape(-1), dev)
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        ws_bytes = L.geo_graph_avg_degree_workspace_bytes(B)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_graph_avg_degree(_nat.ptr(row_ptr.contiguous()), N, _nat.ptr(b), B, ppc,
+                                          _nat.ptr(out), _nat.ptr(ws), ws_bytes, _nat.stream_of(dev)),
+                   "geo_graph_avg_degree")
+    return out
+
+
 # ═══════════════════════════════════════════════════════════════════
 # KNN
 # ═══════════════════════════════════════════════════════════════════
@@ -559,7 +657,9 @@ __all__ = [
     "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
     "segment_softmax_forward_hip", "segment_softmax_backward_hip",
     "gather_weighted_sum_forward_hip", "gather_weighted_sum_backward_hip", "idw_weights_hip",
-    "knn_radius_stat_hip",
+    "knn_radius_stat_hip", "radius_graph_csr_hip", "edge_geometry_hip",
+    "edge_geometry_backward_hip", "spherical_harmonics_hip", "spherical_harmonics_backward_hip",
+    "graph_avg_degree_hip",
     "segment_reduce_forward_hip", "segment_reduce_backward_hip",
     "knn_available", "knn_cuda", "knn_self_cuda",
     "fps_available", "fps_cuda",

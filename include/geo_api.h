@@ -267,6 +267,50 @@ int geo_gather_weighted_sum_bwd(int dtype, const void* grad_out, const void* fea
 int geo_idw_weights(const int64_t* idx, const float* dist, int64_t N_out, int64_t K, float* w,
                     void* stream);
 
+/* ----------------------------------------------- spatial-graph edge epilogue --- */
+/*
+ * The per-edge geometry SpatialGraph.build computes after the radius graph
+ * (geoembodied/nn/modules/spatial_graph.py:126-153: compute_edge_vectors,
+ * geoembodied/functional/radius_graph.py:336-358, then spherical_harmonics,
+ * geoembodied/kernels/triton_sph_harm.py:61-198) in one pass per edge:
+ *   diff = pos[col] - pos[row], dist[e] = max(|diff|, 1e-8), direction[e] = diff / dist[e],
+ *   Y[e] = real spherical harmonics of direction up to max_l <= 2 ((max_l+1)^2 values, order
+ *   Y_0^0 | Y_1^{-1,0,1} | Y_2^{-2..2}, orthonormal on the sphere; Y may be NULL).
+ * Edges whose endpoints lie outside [0, N) get the geometry of point 0 to itself.
+ */
+int geo_edge_geometry(const float* pos, int64_t N, const int64_t* row, const int64_t* col,
+                      int64_t E, int max_l, float* direction, float* dist, float* Y, void* stream);
+/*
+ * Gradient of the loss with respect to diff from the gradients of direction, dist and Y (any
+ * of them NULL = zero): through the spherical harmonics, then the normalisation (constant
+ * dist where the 1e-8 clamp is active).  The caller adds grad_diff to pos[col] and subtracts it
+ * from pos[row] (segment sums over the two CSRs).
+ */
+int geo_edge_geometry_bwd(const float* direction, const float* dist, const float* grad_direction,
+                          const float* grad_dist, const float* grad_Y, int64_t E, int max_l,
+                          float* grad_diff, void* stream);
+/*
+ * spherical_harmonics(xyz, max_l, normalize) of geoembodied/kernels/triton_sph_harm.py:322-372:
+ * Y [N, (max_l+1)^2] of the rows of xyz [N, 3], normalised first (xyz / max(|xyz|, 1e-8)) when
+ * `normalize`; `unit` [N, 3] and `norm` [N] (may be NULL) receive the normalised vectors and
+ * clamped norms for the backward.  The backward (not normalised) writes d loss / d xyz from
+ * grad_Y; the normalised backward is geo_edge_geometry_bwd with direction = unit, dist = norm.
+ */
+int geo_spherical_harmonics(const float* xyz, int64_t N, int max_l, int normalize, float* Y,
+                            float* unit, float* norm, void* stream);
+int geo_spherical_harmonics_bwd(const float* xyz, const float* grad_Y, int64_t N, int max_l,
+                                float* grad_xyz, void* stream);
+/*
+ * Per-node average degree of its cloud (spatial_graph.py:137-152): from the CSR row pointer
+ * row_ptr[N+1], integer degree sums and node counts per cloud, avg = sum / max(count, 1) in fp32,
+ * clamped below at 1.  Clouds by batch[N] (values outside [0, B) give 1), or contiguous chunks
+ * of points_per_cloud when batch is NULL.  out is fp32 [N].
+ */
+size_t geo_graph_avg_degree_workspace_bytes(int64_t B);
+int geo_graph_avg_degree(const int64_t* row_ptr, int64_t N, const int64_t* batch, int64_t B,
+                         int64_t points_per_cloud, float* out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

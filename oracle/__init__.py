@@ -360,3 +360,48 @@ def knn_radius_stat(dist, col: int, mode: str, multiplier: float) -> float:
     if np.isnan(c).any():
         return float("nan")
     return float(np.sqrt(np.sort(c)[(c.size - 1) // 2])) * multiplier
+
+
+# ---------------------------------------------------- spatial-graph edge geometry + SH ---
+
+def spherical_harmonics(xyz, max_l: int = 2, normalize: bool = False) -> np.ndarray:
+    """Real spherical harmonics, float64, order Y_0^0 | Y_1^{-1,0,1} | Y_2^{-2..2}
+    (geoembodied/kernels/triton_sph_harm.py:177-220 formulas; normalisation xyz / max(|xyz|,
+    1e-8) when asked, triton_sph_harm.py:361-362)."""
+    v = np.asarray(xyz, dtype=np.float64).reshape(-1, 3)
+    if normalize:
+        v = v / np.maximum(np.linalg.norm(v, axis=1, keepdims=True), 1e-8)
+    x, y, z = v[:, 0], v[:, 1], v[:, 2]
+    cols = [np.full_like(x, np.sqrt(1.0 / (4.0 * np.pi)))]
+    if max_l >= 1:
+        c1 = np.sqrt(3.0 / (4.0 * np.pi))
+        cols += [c1 * y, c1 * z, c1 * x]
+    if max_l >= 2:
+        c20, c21, c22 = np.sqrt(5.0 / (16.0 * np.pi)), np.sqrt(15.0 / (4.0 * np.pi)), np.sqrt(15.0 / (16.0 * np.pi))
+        cols += [c21 * x * y, c21 * y * z, c20 * (3.0 * z * z - 1.0), c21 * x * z, c22 * (x * x - y * y)]
+    return np.stack(cols, axis=1)
+
+
+def edge_geometry(pos, row, col, max_l: int = 2):
+    """(direction, dist, Y) float64 of the edges row -> col: diff = pos[col] - pos[row],
+    dist = max(|diff|, 1e-8), direction = diff / dist, Y of direction
+    (geoembodied/functional/radius_graph.py:336-358, nn/modules/spatial_graph.py:125-129)."""
+    p = np.asarray(pos, dtype=np.float64)
+    diff = p[np.asarray(col)] - p[np.asarray(row)]
+    dist = np.maximum(np.linalg.norm(diff, axis=1), 1e-8)
+    direction = diff / dist[:, None]
+    return direction, dist, spherical_harmonics(direction, max_l)
+
+
+def graph_avg_degree(node_start, node_end, batch=None, B: int = 1) -> np.ndarray:
+    """Per-node average degree of its cloud, clamped below at 1 (spatial_graph.py:137-152)."""
+    deg = np.asarray(node_end, np.float64) - np.asarray(node_start, np.float64)
+    N = deg.size
+    if batch is None:
+        avg = np.full(N, deg.mean() if N else 0.0)
+    else:
+        b = np.asarray(batch, np.int64)
+        s = np.bincount(b, weights=deg, minlength=B)
+        c = np.bincount(b, minlength=B)
+        avg = (s / np.maximum(c, 1))[b]
+    return np.maximum(avg, 1.0)

@@ -1,0 +1,139 @@
+"""GPU: spherical harmonics, the fused spatial-graph edge epilogue and SpatialGraph against the
+float64 oracle (pinned by quadrature and closed forms in test_oracle.py).
+
+Bars: fp32 values within 2e-6 absolute (directions and SH of unit vectors are O(1); the kernel
+rounds each operation once) and distances within 1e-6 relative; topology, CSR arrays and average
+degrees exact; gradients with respect to positions within 1e-4 relative of float64 autograd of
+the reference's op sequence (fp32 chains through a normalisation).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _f():
+    import geoembodied  # noqa: F401
+    from geoembodied.kernels.triton_sph_harm import spherical_harmonics
+    from geoembodied.nn.modules.spatial_graph import SpatialGraph
+    return spherical_harmonics, SpatialGraph
+
+
+def _sh_torch(v, max_l):
+    """The reference's PyTorch formula (triton_sph_harm.py:177-220) in float64, for autograd."""
+    import math
+    x, y, z = v[..., 0], v[..., 1], v[..., 2]
+    out = [torch.full_like(x, math.sqrt(1 / (4 * math.pi)))]
+    if max_l >= 1:
+        c1 = math.sqrt(3 / (4 * math.pi))
+        out += [c1 * y, c1 * z, c1 * x]
+    if max_l >= 2:
+        c20, c21, c22 = math.sqrt(5 / (16 * math.pi)), math.sqrt(15 / (4 * math.pi)), math.sqrt(15 / (16 * math.pi))
+        out += [c21 * x * y, c21 * y * z, c20 * (3 * z * z - 1), c21 * x * z, c22 * (x * x - y * y)]
+    return torch.stack(out, -1)
+
+
+@pytest.mark.parametrize("max_l", [0, 1, 2])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_spherical_harmonics_vs_oracle_and_grad(dev, max_l, normalize):
+    sh, _ = _f()
+    g = torch.Generator().manual_seed(max_l * 2 + normalize)
+    v = torch.randn(5000, 3, generator=g)
+    if not normalize:
+        v = v / v.norm(dim=1, keepdim=True)
+    v[0] = 0.0                                             # zero vector (normalised: clamp)
+    vd = v.to(dev).requires_grad_(True)
+    Y = sh(vd, max_l=max_l, normalize=normalize)
+    assert Y.shape == (5000, (max_l + 1) ** 2)
+    np.testing.assert_allclose(Y.detach().cpu().numpy(), oracle.spherical_harmonics(v.numpy(), max_l, normalize),
+                               atol=2e-6, rtol=0)
+    gY = torch.randn(5000, (max_l + 1) ** 2, generator=g)
+    Y.backward(gY.to(dev))
+    v64 = v.double().requires_grad_(True)
+    u = v64 / v64.norm(dim=-1, keepdim=True).clamp(min=1e-8) if normalize else v64
+    if max_l == 0:                                         # Y_0^0 is constant
+        want = np.zeros((5000, 3))
+    else:
+        _sh_torch(u, max_l).backward(gY.double())
+        want = v64.grad.numpy()
+    got = vd.grad.cpu().numpy()
+    ok = np.abs(v.numpy()).sum(1) > 0
+    np.testing.assert_allclose(got[ok], want[ok], rtol=1e-4, atol=1e-5)
+
+
+def _cloud(N, B, seed):
+    g = torch.Generator().manual_seed(seed)
+    d = torch.randn(N * B, 3, generator=g)
+    pos = d / d.norm(dim=1, keepdim=True) + 0.01 * torch.randn(N * B, 3, generator=g)
+    return pos, torch.arange(B).repeat_interleave(N)
+
+
+@pytest.mark.parametrize("B,N,r,K", [(1, 500, 0.3, 16), (4, 1000, 0.15, 32), (16, 4096, 0.1, 32)])
+def test_spatial_graph_build_vs_oracle(dev, B, N, r, K):
+    _, SpatialGraph = _f()
+    pos, batch = _cloud(N, B, N + B)
+    graph = SpatialGraph.build(pos.to(dev), r, max_num_neighbors=K, batch=batch.to(dev),
+                               num_batch_elements=B)
+    wr, wc = oracle.radius_graph(pos.numpy(), r, K, batch=batch.numpy(), num_batch_elements=B)
+    np.testing.assert_array_equal(graph.row.cpu().numpy(), wr)
+    np.testing.assert_array_equal(graph.col.cpu().numpy(), wc)
+    assert graph.E == len(wr) and graph.N == N * B
+    cs, pm, ns, ne = oracle.sort_and_build_csr(wc, N * B)
+    for got, want in ((graph.col_sorted, cs), (graph.perm, pm), (graph.node_start, ns), (graph.node_end, ne)):
+        assert got.dtype == torch.int32
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+    d, dist, Y = oracle.edge_geometry(pos.numpy(), wr, wc)
+    np.testing.assert_allclose(graph.direction.cpu().numpy(), d, atol=2e-6, rtol=0)
+    np.testing.assert_allclose(graph.dist.cpu().numpy(), dist, rtol=1e-6)
+    np.testing.assert_allclose(graph.Y.cpu().numpy(), Y, atol=2e-6, rtol=0)
+    np.testing.assert_allclose(graph.avg_degree.cpu().numpy(),
+                               oracle.graph_avg_degree(ns, ne, batch.numpy(), B), rtol=1e-7)
+
+
+def test_spatial_graph_gradient_and_from_edge_index(dev):
+    _, SpatialGraph = _f()
+    pos, batch = _cloud(600, 2, 9)
+    p = pos.to(dev).requires_grad_(True)
+    graph = SpatialGraph.build(p, 0.25, max_num_neighbors=24, batch=batch.to(dev), num_batch_elements=2)
+    g = torch.Generator().manual_seed(1)
+    w_dir = torch.randn(graph.E, 3, generator=g)
+    w_dist = torch.randn(graph.E, generator=g)
+    w_Y = torch.randn(graph.E, 9, generator=g)
+    loss = (graph.direction * w_dir.to(dev)).sum() + (graph.dist * w_dist.to(dev)).sum() + \
+        (graph.Y * w_Y.to(dev)).sum()
+    loss.backward()
+    p64 = pos.double().requires_grad_(True)
+    row, col = graph.row.cpu(), graph.col.cpu()
+    diff = p64[col] - p64[row]
+    dist = diff.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+    direction = diff / dist
+    ref = (direction * w_dir.double()).sum() + (dist.squeeze(-1) * w_dist.double()).sum() + \
+        (_sh_torch(direction, 2) * w_Y.double()).sum()
+    ref.backward()
+    np.testing.assert_allclose(p.grad.cpu().numpy(), p64.grad.numpy(), rtol=1e-4, atol=2e-4)
+    # the same edges given in shuffled order: identical per-edge geometry and the stable CSR
+    sh = torch.randperm(graph.E, generator=g)
+    g2 = SpatialGraph.from_edge_index(graph.row[sh.to(dev)], graph.col[sh.to(dev)], pos.to(dev),
+                                      graph.N, batch=batch.to(dev), num_batch_elements=2)
+    np.testing.assert_array_equal(g2.direction.cpu().numpy(), graph.direction[sh.to(dev)].detach().cpu().numpy())
+    np.testing.assert_array_equal(g2.Y.cpu().numpy(), graph.Y[sh.to(dev)].detach().cpu().numpy())
+    cs, pm, ns, ne = oracle.sort_and_build_csr(graph.col[sh.to(dev)].cpu().numpy(), graph.N)
+    np.testing.assert_array_equal(g2.perm.cpu().numpy(), pm)
+    np.testing.assert_array_equal(g2.avg_degree.cpu().numpy(), graph.avg_degree.cpu().numpy())
+
+
+def test_spatial_graph_empty_and_device_radius(dev):
+    _, SpatialGraph = _f()
+    pos = torch.randn(100, 3, device=dev) * 100
+    g0 = SpatialGraph.build(pos, 1e-3)
+    assert g0.E == 0 and g0.Y.shape == (0, 9) and (g0.avg_degree == 1).all()
+    from geoembodied.functional.adaptive import adaptive_radius
+    p2, _ = _cloud(800, 1, 3)
+    r = adaptive_radius(p2.to(dev), torch.tensor([0, 800], device=dev), 3.0)
+    ga = SpatialGraph.build(p2.to(dev), r, max_num_neighbors=16)
+    gb = SpatialGraph.build(p2.to(dev), float(r), max_num_neighbors=16)
+    assert torch.equal(ga.row, gb.row) and torch.equal(ga.Y, gb.Y)

@@ -451,3 +451,42 @@ def test_knn_radius_stat_vs_reference_expressions():
         torch.from_numpy(even)[:, -1].clamp(min=1e-12).sqrt().median().item()
     d[3, 1] = np.nan
     assert np.isnan(oracle.knn_radius_stat(d, 1, "median", 1.0))
+
+
+# -------------------------------------------------- spherical harmonics / edge geometry ---
+
+def test_spherical_harmonics_orthonormal_and_addition_theorem():
+    """Gauss-Legendre x uniform-phi quadrature (exact for these degrees) gives the identity Gram
+    matrix, and sum_m Y_lm(u)^2 = (2l+1)/(4 pi) on unit vectors: both pin every constant and
+    formula independently of how the oracle writes them."""
+    t, wt = np.polynomial.legendre.leggauss(12)
+    phi = np.arange(24) * (2 * np.pi / 24)
+    ct, P = np.meshgrid(t, phi, indexing="ij")
+    st = np.sqrt(1 - ct ** 2)
+    u = np.stack([st * np.cos(P), st * np.sin(P), ct], -1).reshape(-1, 3)
+    w = (wt[:, None] * np.full(24, 2 * np.pi / 24)[None, :]).reshape(-1)
+    Y = oracle.spherical_harmonics(u, 2)
+    np.testing.assert_allclose((Y * w[:, None]).T @ Y, np.eye(9), atol=1e-12)
+    g = np.random.default_rng(0).standard_normal((100, 3))
+    Yn = oracle.spherical_harmonics(g, 2, normalize=True)
+    for l, sl in ((0, slice(0, 1)), (1, slice(1, 4)), (2, slice(4, 9))):
+        np.testing.assert_allclose((Yn[:, sl] ** 2).sum(1), (2 * l + 1) / (4 * np.pi), rtol=1e-12)
+    assert oracle.spherical_harmonics(g, 1).shape == (100, 4)
+
+
+def test_edge_geometry_and_avg_degree_closed_forms():
+    g = np.random.default_rng(1)
+    pos = g.standard_normal((30, 3))
+    row, col = g.integers(0, 30, 80), g.integers(0, 30, 80)
+    row[0] = col[0]                       # zero-length edge: dist clamps to 1e-8
+    d, dist, Y = oracle.edge_geometry(pos, row, col)
+    ref = pos[col] - pos[row]
+    loops = row == col
+    np.testing.assert_allclose(dist, np.maximum(np.sqrt((ref ** 2).sum(1)), 1e-8), rtol=1e-14)
+    assert (dist[loops] == 1e-8).all() and (d[loops] == 0).all()
+    np.testing.assert_allclose(np.linalg.norm(d[~loops], axis=1), 1.0, rtol=1e-14)
+    ns = np.array([0, 2, 2, 5, 9])
+    ne = np.array([2, 2, 5, 9, 9])
+    np.testing.assert_allclose(oracle.graph_avg_degree(ns, ne, [0, 0, 1, 1, 1], 2),
+                               [1.0, 1.0, 7 / 3, 7 / 3, 7 / 3])
+    np.testing.assert_allclose(oracle.graph_avg_degree(ns, ne), 1.8)
