@@ -22,6 +22,7 @@ c_int = ctypes.c_int
 c_vp = ctypes.c_void_p
 c_size = ctypes.c_size_t
 c_f32 = ctypes.c_float
+c_i32 = ctypes.c_int32
 
 # name -> (restype, argtypes)
 _SIGNATURES = {
@@ -67,6 +68,23 @@ _SIGNATURES = {
     "geo_graph_avg_degree": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_size, c_vp]),
     "geo_knn_radius_stat": (c_int, [c_vp, c_i64, c_i64, c_i64, c_int, ctypes.c_double, c_vp, c_vp,
                                     c_size, c_vp]),
+    "geo_se3_aggregate_fwd": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
+                                      c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp,
+                                      c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "geo_se3_gemm": (c_int, [c_vp, c_i64, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp,
+                             c_vp, c_vp]),
+    "geo_se3_grad_prep": (c_int, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "geo_se3_bwd_edge": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
+                                 c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp, c_i32, c_vp,
+                                 c_i32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    "geo_radial_mlp_fwd": (c_int, [c_vp, c_i64, c_vp, c_i32, c_f32, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
+                                   c_vp, c_vp]),
+    "geo_radial_mlp_bwd_workspace_bytes": (c_size, [c_i64]),
+    "geo_radial_mlp_bwd": (c_int, [c_vp, c_i64, c_vp, c_i32, c_f32, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
+                                   c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
+    "geo_se3_bwd_src": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64,
+                                c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp,
+                                c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

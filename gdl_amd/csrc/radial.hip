@@ -1,0 +1,364 @@
+// radial.hip — the radial basis MLP of SE3Conv, forward and backward, on the matrix cores.
+//
+// Reference: RadialBasis.forward (geoembodied/nn/modules/se3_conv.py:238-282), per edge e with
+// length d:
+//   x_i = sin(f_i d) / max(d, 1e-8) * env(d),  env(d) = max(0.5 (1 + cos((pi d) / cutoff)), 0)
+//   z_j = b1_j + sum_i W1[j][i] x_i,  h_j = silu(z_j) = z_j / (1 + exp(-z_j))
+//   R_p = b2_p + sum_j W2[p][j] h_j
+// with i < NB <= 16 basis functions, j < H <= 64 hidden units and p < P <= 16 outputs.  PyTorch
+// runs this as a dozen kernels with [E, 64] intermediates, and its weight gradients as GEMMs
+// whose reduction dimension is E.  Here one wave takes 16 edges at a time through fp32 MFMA
+// (v_mfma_f32_16x16x4_f32) tiles, nothing per edge but d, R and dR touches memory, and the weight
+// gradients accumulate in MFMA accumulators across all of a wave's edges.
+//
+// MFMA operand convention (as in se3_message.hip): in MFMA number q (q < 4) of a 16-wide k chunk,
+// lane l supplies A[row = l % 16][k = 4 (l / 16) + q] and B[k = 4 (l / 16) + q][col = l % 16];
+// the result D[row = 4 (l / 16) + q][col = l % 16] sits in element q of lane l.  So the result of
+// one GEMM is directly the B operand of the next along the same k chunk.
+//
+// Forward:  Z^T = W1 X^T (A = W1, B = X^T), H^T = silu(Z^T + b1), R^T = W2 H^T (B = H^T as is).
+// Backward (per 16 edges):  Z = X W1^T and dH = dR W2 in the edge-major layout, dZ = dH silu'(Z);
+//   dW2 += dR^T H,  dW1^T += X^T dZ,  db1 += colsum dZ,  db2 += colsum dR  (accumulators);
+//   dX^T = W1^T dZ^T (dZ transposed through LDS), d(dist) = sum_i dX_i dx_i/dd.
+// Per-block partial sums of the weight gradients are combined by one more kernel in block order,
+// so results are deterministic.
+#include "scan.hpp"
+
+namespace geo {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRbThreads = 256;
+constexpr int kRbWaves = kRbThreads / kWave;
+constexpr int kRbMaxBasis = 16;
+constexpr int kRbMaxHidden = 64;
+constexpr int kRbMaxOut = 16;
+constexpr int kRbPart = 16 * 64 + 16 * 64 + 64 + 16;  // dW1^T | dW2 | db1 | db2 per block
+constexpr int kRbMaxBlocks = 1024;
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+struct RbParams {
+  const float* dist;
+  int64_t E;
+  const float* freqs;
+  int NB;
+  float cutoff;
+  const float* W1;  // [H][NB]
+  const float* b1;  // [H]
+  int H;
+  const float* W2;  // [P][H]
+  const float* b2;  // [P]
+  int P;
+};
+
+// Envelope and its derivative with respect to d (the clamp at 0 never bites: 0.5 (1 + cos) >= 0).
+__device__ __forceinline__ void envelope(float d, float cutoff, float& env, float& denv) {
+#pragma clang fp contract(off)
+  const float t = (3.14159265358979323846f * d) / cutoff;
+  const float c = cosf(t);
+  const float e = 0.5f * (1.0f + c);
+  env = e < 0.f ? 0.f : e;
+  denv = -0.5f * sinf(t) * (3.14159265358979323846f / cutoff);
+}
+
+// x_i(d) and, when asked, dx_i/dd.
+__device__ __forceinline__ float basis(float f, float d, float env, float denv, float* dx) {
+#pragma clang fp contract(off)
+  const float dc = d < 1e-8f ? 1e-8f : d;
+  const float s = sinf(f * d);
+  const float b = s / dc;
+  if (dx) {
+    // d/dd [sin(f d) / dc] = f cos(f d) / dc - [d >= 1e-8] sin(f d) / dc^2
+    const float db = f * cosf(f * d) / dc - (d >= 1e-8f ? s / (dc * dc) : 0.f);
+    *dx = db * env + b * denv;
+  }
+  return b * env;
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
+
+__global__ __launch_bounds__(kRbThreads) void radial_fwd_kernel(RbParams p, float* __restrict__ R) {
+  const int lane = lane_id();
+  const int g = lane >> 4, li = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  float w1[4][4], b1r[4][4], w2[4][4], fr[4], b2r[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 4 * g + q;
+    fr[q] = i < p.NB ? p.freqs[i] : 0.f;
+    b2r[q] = i < p.P ? p.b2[i] : 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const int j = 16 * jb + li;
+      w1[jb][q] = (j < p.H && i < p.NB) ? p.W1[j * p.NB + i] : 0.f;      // A of Z^T: W1[j][i]
+      const int jj = 16 * jb + 4 * g + q;
+      b1r[jb][q] = jj < p.H ? p.b1[jj] : 0.f;                              // rows of Z^T
+      w2[jb][q] = (li < p.P && jj < p.H) ? p.W2[li * p.H + jj] : 0.f;      // A of R^T: W2[p][j]
+    }
+  }
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRbWaves * 16;
+  for (int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kRbWaves + wave) * 16; e0 < p.E; e0 += stride) {
+    const int64_t e = e0 + li;
+    const bool ok = e < p.E;
+    const float d = ok ? p.dist[e] : 1.f;
+    float env, denv;
+    envelope(d, p.cutoff, env, denv);
+    float x[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = 4 * g + q < p.NB ? basis(fr[q], d, env, denv, nullptr) : 0.f;
+    floatx4 h[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      floatx4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) z = mfma4(w1[jb][q], x[q], z);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[jb][q] = silu(z[q] + b1r[jb][q]);
+    }
+    floatx4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r = mfma4(w2[c][q], h[c][q], r);
+    if (ok) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (4 * g + q < p.P) R[e * p.P + 4 * g + q] = r[q] + b2r[q];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, const float* __restrict__ dR,
+                                                               float* __restrict__ ddist,
+                                                               float* __restrict__ part) {
+  __shared__ float tz[kRbWaves][16][kRbMaxHidden + 1];   // dZ of 16 edges, per wave
+  __shared__ float red[kRbWaves][kRbPart];
+  const int lane = lane_id();
+  const int g = lane >> 4, li = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  float fr[4], frl;
+  float w1[4][4], w2b[4][4], w1t[4][4], b1z[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 4 * g + q;
+    fr[q] = i < p.NB ? p.freqs[i] : 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const int j = 16 * jb + li;
+      w1[jb][q] = (j < p.H && i < p.NB) ? p.W1[j * p.NB + i] : 0.f;   // B of Z = X W1^T
+      w2b[jb][q] = (i < p.P && j < p.H) ? p.W2[i * p.H + j] : 0.f;    // B of dH = dR W2
+      const int jj = 16 * jb + 4 * g + q;
+      w1t[jb][q] = (jj < p.H && li < p.NB) ? p.W1[jj * p.NB + li] : 0.f;  // A of dX^T = W1^T dZ^T
+    }
+  }
+  frl = li < p.NB ? p.freqs[li] : 0.f;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) b1z[jb] = 16 * jb + li < p.H ? p.b1[16 * jb + li] : 0.f;
+  floatx4 aw1[4], aw2[4];
+  float db1p[4] = {0.f, 0.f, 0.f, 0.f}, db2p = 0.f;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    aw1[jb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    aw2[jb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kRbWaves * 16;
+  for (int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kRbWaves + wave) * 16; e0 < p.E; e0 += stride) {
+    // edge li: x_i, i = 4g + q (A of Z; also the layout of dX^T) and dR[e][4g + q] (A of dH)
+    const int64_t ea = e0 + li;
+    const bool oka = ea < p.E;
+    const float da = oka ? p.dist[ea] : 1.f;
+    float enva, denva;
+    envelope(da, p.cutoff, enva, denva);
+    float xa[4], dxa[4], dra[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = 4 * g + q;
+      xa[q] = i < p.NB ? basis(fr[q], da, enva, denva, &dxa[q]) : 0.f;
+      if (i >= p.NB) dxa[q] = 0.f;
+      dra[q] = (oka && i < p.P) ? dR[ea * p.P + i] : 0.f;
+    }
+    // edges 4g + q: x_li (A of dW1^T) and dR[e][li] (A of dW2)
+    float xb[4], drb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t eb = e0 + 4 * g + q;
+      const bool okb = eb < p.E;
+      const float db = okb ? p.dist[eb] : 1.f;
+      float envb, denvb;
+      envelope(db, p.cutoff, envb, denvb);
+      xb[q] = (okb && li < p.NB) ? basis(frl, db, envb, denvb, nullptr) : 0.f;
+      drb[q] = (okb && li < p.P) ? dR[eb * p.P + li] : 0.f;
+      db2p += drb[q];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      floatx4 z = {0.f, 0.f, 0.f, 0.f}, dh = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        z = mfma4(xa[q], w1[jb][q], z);     // Z[e = 4g + q'][j = 16 jb + li]
+        dh = mfma4(dra[q], w2b[jb][q], dh);  // dH, same layout
+      }
+      floatx4 h, dz;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float zz = z[q] + b1z[jb];
+        const float sg = 1.0f / (1.0f + expf(-zz));
+        h[q] = zz * sg;
+        dz[q] = dh[q] * (sg * (1.0f + zz * (1.0f - sg)));  // silu'(z) = s (1 + z (1 - s))
+        db1p[jb] += dz[q];
+        tz[wave][4 * g + q][16 * jb + li] = dz[q];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        aw2[jb] = mfma4(drb[q], h[q], aw2[jb]);   // dW2[p = 4g + q'][j]   (k = edges)
+        aw1[jb] = mfma4(xb[q], dz[q], aw1[jb]);   // dW1^T[i = 4g + q'][j]
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (ddist) {
+      floatx4 dx = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dx = mfma4(w1t[c][q], tz[wave][li][16 * c + 4 * g + q], dx);
+      // dX^T[i = 4g + q][e = li]
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s += dx[q] * dxa[q];
+      s += __shfl_xor(s, 16, kWave);
+      s += __shfl_xor(s, 32, kWave);
+      if (g == 0 && oka) ddist[ea] = s;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // db1 / db2: sum over the four lane groups
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    db1p[jb] += __shfl_xor(db1p[jb], 16, kWave);
+    db1p[jb] += __shfl_xor(db1p[jb], 32, kWave);
+  }
+  db2p += __shfl_xor(db2p, 16, kWave);
+  db2p += __shfl_xor(db2p, 32, kWave);
+  float* my = red[wave];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      my[(4 * g + q) * 64 + 16 * jb + li] = aw1[jb][q];
+      my[1024 + (4 * g + q) * 64 + 16 * jb + li] = aw2[jb][q];
+    }
+  if (g == 0) {
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) my[2048 + 16 * jb + li] = db1p[jb];
+    my[2112 + li] = db2p;
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < kRbPart; k += kRbThreads) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRbWaves; ++w) s += red[w][k];
+    part[static_cast<int64_t>(blockIdx.x) * kRbPart + k] = s;
+  }
+}
+
+__global__ __launch_bounds__(kRbThreads) void radial_bwd_final(const float* __restrict__ part, int nblk,
+                                                              int NB, int H, int P,
+                                                              float* __restrict__ dW1,
+                                                              float* __restrict__ db1,
+                                                              float* __restrict__ dW2,
+                                                              float* __restrict__ db2) {
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= kRbPart) return;
+  float s = 0.f;
+  for (int b = 0; b < nblk; ++b) s += part[static_cast<int64_t>(b) * kRbPart + k];
+  if (k < 1024) {
+    const int i = k / 64, j = k % 64;
+    if (i < NB && j < H && dW1) dW1[j * NB + i] = s;
+  } else if (k < 2048) {
+    const int pp = (k - 1024) / 64, j = (k - 1024) % 64;
+    if (pp < P && j < H && dW2) dW2[pp * H + j] = s;
+  } else if (k < 2112) {
+    const int j = k - 2048;
+    if (j < H && db1) db1[j] = s;
+  } else {
+    const int pp = k - 2112;
+    if (pp < P && db2) db2[pp] = s;
+  }
+}
+
+int rb_check(const char* who, int64_t E, int NB, int H, int P, float cutoff) {
+  GEO_REQUIRE(E >= 0, "%s: negative E", who);
+  GEO_REQUIRE(NB >= 1 && NB <= kRbMaxBasis, "%s: num_basis=%d outside [1, %d]", who, NB, kRbMaxBasis);
+  GEO_REQUIRE(H >= 1 && H <= kRbMaxHidden, "%s: hidden=%d outside [1, %d]", who, H, kRbMaxHidden);
+  GEO_REQUIRE(P >= 1 && P <= kRbMaxOut, "%s: outputs=%d outside [1, %d]", who, P, kRbMaxOut);
+  GEO_REQUIRE(cutoff > 0.f, "%s: cutoff must be positive", who);
+  return GEO_OK;
+}
+
+unsigned rb_blocks(int64_t E) {
+  const int64_t b = ceil_div(E, 16 * kRbWaves * 4);  // about four 16-edge tiles per wave
+  return static_cast<unsigned>(b < 1 ? 1 : (b > kRbMaxBlocks ? kRbMaxBlocks : b));
+}
+
+}  // namespace
+}  // namespace geo
+
+using namespace geo;
+
+extern "C" int geo_radial_mlp_fwd(const float* dist, int64_t E, const float* freqs, int32_t NB,
+                                  float cutoff, const float* W1, const float* b1, int32_t H,
+                                  const float* W2, const float* b2, int32_t P, float* R,
+                                  void* stream) {
+  int rc = rb_check("radial_mlp_fwd", E, NB, H, P, cutoff);
+  if (rc) return rc;
+  if (E == 0) return GEO_OK;
+  GEO_REQUIRE(dist && freqs && W1 && b1 && W2 && b2 && R, "radial_mlp_fwd: null pointer");
+  RbParams p{dist, E, freqs, NB, cutoff, W1, b1, H, W2, b2, P};
+  hipLaunchKernelGGL(radial_fwd_kernel, dim3(rb_blocks(E)), dim3(kRbThreads), 0, as_stream(stream), p, R);
+  GEO_LAUNCH_CHECK("radial_fwd_kernel");
+  return GEO_OK;
+}
+
+extern "C" size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E) {
+  if (E < 0) return 0;
+  return static_cast<size_t>(rb_blocks(E)) * kRbPart * sizeof(float);
+}
+
+extern "C" int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* freqs, int32_t NB,
+                                  float cutoff, const float* W1, const float* b1, int32_t H,
+                                  const float* W2, const float* b2, int32_t P, const float* dR,
+                                  float* d_dist, float* dW1, float* db1, float* dW2, float* db2,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = rb_check("radial_mlp_bwd", E, NB, H, P, cutoff);
+  if (rc) return rc;
+  GEO_REQUIRE(freqs && W1 && b1 && W2 && b2, "radial_mlp_bwd: null weight pointer");
+  hipStream_t st = as_stream(stream);
+  if (E == 0) {  // weight gradients of an empty batch are zero
+    if (dW1) { rc = device_fill<float>(dW1, static_cast<int64_t>(H) * NB, 0.f, st); if (rc) return rc; }
+    if (db1) { rc = device_fill<float>(db1, H, 0.f, st); if (rc) return rc; }
+    if (dW2) { rc = device_fill<float>(dW2, static_cast<int64_t>(P) * H, 0.f, st); if (rc) return rc; }
+    if (db2) { rc = device_fill<float>(db2, P, 0.f, st); if (rc) return rc; }
+    return GEO_OK;
+  }
+  GEO_REQUIRE(dist && dR, "radial_mlp_bwd: null pointer");
+  const size_t need = geo_radial_mlp_bwd_workspace_bytes(E);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(GEO_ERR_WORKSPACE, "radial_mlp_bwd: workspace %zu bytes, need %zu",
+                     workspace_bytes, need);
+  RbParams p{dist, E, freqs, NB, cutoff, W1, b1, H, W2, b2, P};
+  const unsigned nblk = rb_blocks(E);
+  float* part = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(radial_bwd_kernel, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part);
+  GEO_LAUNCH_CHECK("radial_bwd_kernel");
+  hipLaunchKernelGGL(radial_bwd_final, dim3(static_cast<unsigned>(ceil_div(kRbPart, kRbThreads))),
+                     dim3(kRbThreads), 0, st, part, static_cast<int>(nblk), NB, H, P, dW1, db1, dW2, db2);
+  GEO_LAUNCH_CHECK("radial_bwd_final");
+  return GEO_OK;
+}

@@ -1,0 +1,885 @@
+// se3_message.hip — SE(3)-equivariant message passing with the aggregation folded in front of
+// the channel mixing.
+//
+// The reference (geoembodied/nn/modules/se3_conv.py:61-235 `_compute_messages`, :516-545) builds
+// one message per edge e = (m -> n) for up to nine tensor-product paths, each of the form
+//     msg_e = r_e,p * W_p * x_e,p        (r_e,p: a per-edge scalar, x_e,p: a per-edge feature)
+// with a weight matrix W_p shared by all edges, concatenates the messages into an [E, C] tensor
+// and sums it over the edges of each target.  Because W_p is shared,
+//     sum_e r_e,p W_p x_e,p = W_p (sum_e r_e,p x_e,p),
+// so this library sums the r-weighted source features per target first (se3_fwd_aggregate: one
+// wave per target node, lanes over input channels, no per-edge tensor) and applies the weights
+// once per node with an fp32 MFMA GEMM whose epilogue divides by the node's average degree, adds
+// the scalar bias and applies the mask (se3_gemm).  The per-edge GEMM work of the reference
+// becomes per-node work (E/N times fewer flops) and the [E, C] message tensor never exists.
+//
+// Paths (source features s [N,Cs], v [N,Cv,3], t [N,Ct,5]; d = unit direction, y0 = Y_0^0,
+// y2 = Y_2 of the edge; r_p = R[e, col_p]; cg = the Cartesian CG(1,1->2) table [3][3][5]):
+//   0  s -> s    r0 y0 s               3  v -> s    r3 (d . v)           6  t -> t   r6 y0 t
+//   1  s -> v    r1 d_k s              4  v -> v    r4 (d x v)_k         7  v -> t   r7 sum_ij d_i v_j cg_ijm
+//   2  v -> v    r2 y0 v_k             5  s -> t    r5 y2_m s            8  t -> s   r8 sum_m t_m^2
+//
+// Per-node aggregate layout (rows zero-padded to a multiple of 16 floats):
+//   Xs[n]    = [A0 (Cs) | A3 (Cv) | A8 (Ct)]                    -> s_out = Xs Ws^T, Ws = [W0|W3|W8]
+//   Xv[n][k] = [A1_k (Cs) | A2_k (Cv) | A4_k (Cv)]   k = x,y,z  -> v_out = Xv Wv^T, Wv = [W1|W2|W4]
+//   Xt[n][m] = [A5_m (Cs) | A6_m (Ct) | A7_m (Cv)]   m = 0..4   -> t_out = Xt Wt^T, Wt = [W5|W6|W7]
+//
+// The backward is the same structure transposed: se3_bwd_edge forms the per-edge gradients of
+// R, the direction and Y from the per-node gradient rows gX = g W (one wave per target node) and
+// se3_bwd_src sums the gradient rows of each source's targets with the per-edge weights (one wave
+// per source node over the CSR of the sources), after which GEMMs with the transposed weights
+// give the feature gradients.
+#include "common.hpp"
+
+namespace geo {
+namespace {
+
+constexpr int kSeThreads = 256;
+constexpr int kSeWaves = kSeThreads / kWave;
+constexpr int kSePaths = 9;
+
+struct SeEdges {
+  const int64_t* other;   // source of each edge (forward, edge grads) or target (source pass)
+  const int32_t* perm;    // CSR position -> edge id
+  const int32_t* ns;
+  const int32_t* ne;
+  int32_t E;
+  int64_t N;
+  const float* dir;       // [E, 3]
+  const float* Y;         // [E, ysh]
+  int32_t ysh;
+  const float* R;         // [E, P]
+  int32_t P;
+  int32_t pc[kSePaths];   // column of R for each path, -1 when the path is off
+  float cg[45];           // [3][3][5]
+};
+
+struct SeFeat {
+  const float* s;
+  const float* v;
+  const float* t;
+  int32_t Cs, Cv, Ct;
+};
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float rlane(float x, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j));
+}
+
+// The scalars of one edge: the other endpoint, R of every path (0 for paths that are off), the
+// direction and Y_0^0 / Y_2.
+struct EdgeScalars {
+  int32_t other;
+  int32_t e;
+  int32_t ok;
+  float r[kSePaths];
+  float d[3];
+  float y0;
+  float y2[5];
+};
+
+// Lane j of the wave loads the scalars of the edge at CSR position base + j (j < cnt), so the
+// edges of a node are fetched in one round of parallel loads; the edge loops then read them
+// from lane j with v_readlane (uniform j) or a lane shuffle (per-row j).
+__device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, int cnt, int lane) {
+  EdgeScalars q;
+  q.other = 0;
+  q.e = 0;
+  q.ok = 0;
+#pragma unroll
+  for (int i = 0; i < kSePaths; ++i) q.r[i] = 0.f;
+  q.d[0] = q.d[1] = q.d[2] = 0.f;
+  q.y0 = 0.f;
+#pragma unroll
+  for (int m = 0; m < 5; ++m) q.y2[m] = 0.f;
+  if (lane < cnt) {
+    const int e = g.perm ? g.perm[base + lane] : base + lane;
+    if (static_cast<unsigned>(e) < static_cast<unsigned>(g.E)) {
+      const int64_t o = g.other[e];
+      if (o >= 0 && o < g.N) {
+        q.ok = 1;
+        q.other = static_cast<int32_t>(o);
+        q.e = e;
+        const float* rr = g.R + static_cast<int64_t>(e) * g.P;
+#pragma unroll
+        for (int i = 0; i < kSePaths; ++i) q.r[i] = g.pc[i] >= 0 ? rr[g.pc[i]] : 0.f;
+        const float* dd = g.dir + 3 * static_cast<int64_t>(e);
+        q.d[0] = dd[0];
+        q.d[1] = dd[1];
+        q.d[2] = dd[2];
+        const float* y = g.Y + static_cast<int64_t>(e) * g.ysh;
+        q.y0 = y[0];
+        if (g.ysh >= 9) {
+#pragma unroll
+          for (int m = 0; m < 5; ++m) q.y2[m] = y[4 + m];
+        }
+      }
+    }
+  }
+  return q;
+}
+
+// The staged scalars of lane j (j wave-uniform).
+__device__ __forceinline__ EdgeScalars edge_at(const EdgeScalars& st, int j) {
+  EdgeScalars q;
+  q.other = __builtin_amdgcn_readlane(st.other, j);
+  q.e = __builtin_amdgcn_readlane(st.e, j);
+  q.ok = __builtin_amdgcn_readlane(st.ok, j);
+#pragma unroll
+  for (int i = 0; i < kSePaths; ++i) q.r[i] = rlane(st.r[i], j);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) q.d[k] = rlane(st.d[k], j);
+  q.y0 = rlane(st.y0, j);
+#pragma unroll
+  for (int m = 0; m < 5; ++m) q.y2[m] = rlane(st.y2[m], j);
+  return q;
+}
+
+// The staged scalars of lane j (j may differ between lanes).
+__device__ __forceinline__ EdgeScalars edge_from(const EdgeScalars& st, int j) {
+  EdgeScalars q;
+  q.other = __shfl(st.other, j, kWave);
+  q.e = __shfl(st.e, j, kWave);
+  q.ok = __shfl(st.ok, j, kWave);
+#pragma unroll
+  for (int i = 0; i < kSePaths; ++i) q.r[i] = __shfl(st.r[i], j, kWave);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) q.d[k] = __shfl(st.d[k], j, kWave);
+  q.y0 = __shfl(st.y0, j, kWave);
+#pragma unroll
+  for (int m = 0; m < 5; ++m) q.y2[m] = __shfl(st.y2[m], j, kWave);
+  return q;
+}
+
+// sum_ij d_i v_j cg[i][j][m]
+__device__ __forceinline__ void cg_dv(const float* cg, const float d[3], const float v[3],
+                                      float out[5]) {
+#pragma unroll
+  for (int m = 0; m < 5; ++m) {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j) a += d[i] * v[j] * cg[(i * 3 + j) * 5 + m];
+    out[m] = a;
+  }
+}
+
+__device__ __forceinline__ void zero_pad(float* row, int used, int K) {
+  for (int q = used + lane_id(); q < K; q += kWave) row[q] = 0.f;
+}
+
+__device__ __forceinline__ void node_range(const SeEdges& g, int64_t n, int& a, int& b) {
+  a = g.ns[n];
+  b = g.ne[n];
+  a = a < 0 ? 0 : (a > g.E ? g.E : a);
+  b = b < a ? a : (b > g.E ? g.E : b);
+}
+
+constexpr int kSeUnroll = 4;  // edges whose source rows are in flight together
+
+// ------------------------------------------------------------------ forward aggregate ---
+// One wave per target node, lanes over input channels (chunks of 64).  The node's edges are
+// staged in lanes, then walked four at a time: the four source rows are loaded first, then
+// accumulated in CSR order.
+__global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFeat f,
+                                                               float* __restrict__ Xs, int Ks,
+                                                               float* __restrict__ Xv, int Kv,
+                                                               float* __restrict__ Xt, int Kt) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  if (n >= g.N) return;
+  const int lane = lane_id();
+  int a, b;
+  node_range(g, n, a, b);
+  const int cmax = max(f.Cs, max(f.Cv, f.Ct));
+  for (int c0 = 0; c0 < cmax; c0 += kWave) {
+    const int c = c0 + lane;
+    const bool hs = c < f.Cs, hv = c < f.Cv, ht = c < f.Ct;
+    float A0 = 0.f, A1[3] = {0.f, 0.f, 0.f}, A5[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    float A2[3] = {0.f, 0.f, 0.f}, A3 = 0.f, A4[3] = {0.f, 0.f, 0.f};
+    float A7[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A6[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A8 = 0.f;
+    for (int base = a; base < b; base += kWave) {
+      const int cnt = min(kWave, b - base);
+      const EdgeScalars st = stage_edges(g, base, cnt, lane);
+      for (int j0 = 0; j0 < cnt; j0 += kSeUnroll) {
+        float sv[kSeUnroll], vv[kSeUnroll][3], tt[kSeUnroll][5];
+#pragma unroll
+        for (int u = 0; u < kSeUnroll; ++u) {
+          const int j = min(j0 + u, kWave - 1);
+          const int64_t m = __builtin_amdgcn_readlane(st.other, j);  // 0 past cnt: in bounds
+          if (hs) sv[u] = f.s[m * f.Cs + c];
+          if (hv) {
+            const float* vp = f.v + (m * f.Cv + c) * 3;
+            vv[u][0] = vp[0]; vv[u][1] = vp[1]; vv[u][2] = vp[2];
+          }
+          if (ht) {
+            const float* tp = f.t + (m * f.Ct + c) * 5;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) tt[u][k] = tp[k];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kSeUnroll; ++u) {
+          if (j0 + u >= cnt) break;
+          const EdgeScalars q = edge_at(st, j0 + u);
+          if (!q.ok) continue;
+          if (hs) {
+            const float x = sv[u];
+            if (g.pc[0] >= 0) A0 += q.r[0] * q.y0 * x;
+            if (g.pc[1] >= 0) {
+#pragma unroll
+              for (int k = 0; k < 3; ++k) A1[k] += q.r[1] * q.d[k] * x;
+            }
+            if (g.pc[5] >= 0) {
+#pragma unroll
+              for (int k = 0; k < 5; ++k) A5[k] += q.r[5] * q.y2[k] * x;
+            }
+          }
+          if (hv) {
+            const float* v = vv[u];
+            if (g.pc[2] >= 0) {
+#pragma unroll
+              for (int k = 0; k < 3; ++k) A2[k] += q.r[2] * q.y0 * v[k];
+            }
+            if (g.pc[3] >= 0) A3 += q.r[3] * ((q.d[0] * v[0] + q.d[1] * v[1]) + q.d[2] * v[2]);
+            if (g.pc[4] >= 0) {
+              A4[0] += q.r[4] * (q.d[1] * v[2] - q.d[2] * v[1]);
+              A4[1] += q.r[4] * (q.d[2] * v[0] - q.d[0] * v[2]);
+              A4[2] += q.r[4] * (q.d[0] * v[1] - q.d[1] * v[0]);
+            }
+            if (g.pc[7] >= 0 && Xt) {
+              float tp[5];
+              cg_dv(g.cg, q.d, v, tp);
+#pragma unroll
+              for (int k = 0; k < 5; ++k) A7[k] += q.r[7] * tp[k];
+            }
+          }
+          if (ht) {
+            const float* t = tt[u];
+            if (g.pc[6] >= 0) {
+#pragma unroll
+              for (int k = 0; k < 5; ++k) A6[k] += q.r[6] * q.y0 * t[k];
+            }
+            if (g.pc[8] >= 0)
+              A8 += q.r[8] * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
+          }
+        }
+      }
+    }
+    if (Xs) {
+      float* row = Xs + n * Ks;
+      if (hs) row[c] = A0;
+      if (hv) row[f.Cs + c] = A3;
+      if (ht) row[f.Cs + f.Cv + c] = A8;
+    }
+    if (Xv) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        float* row = Xv + (n * 3 + k) * Kv;
+        if (hs) row[c] = A1[k];
+        if (hv) row[f.Cs + c] = A2[k];
+        if (hv) row[f.Cs + f.Cv + c] = A4[k];
+      }
+    }
+    if (Xt) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k) {
+        float* row = Xt + (n * 5 + k) * Kt;
+        if (hs) row[c] = A5[k];
+        if (ht) row[f.Cs + c] = A6[k];
+        if (hv) row[f.Cs + f.Ct + c] = A7[k];
+      }
+    }
+  }
+  if (Xs) zero_pad(Xs + n * Ks, f.Cs + f.Cv + f.Ct, Ks);
+  if (Xv)
+    for (int k = 0; k < 3; ++k) zero_pad(Xv + (n * 3 + k) * Kv, f.Cs + 2 * f.Cv, Kv);
+  if (Xt)
+    for (int k = 0; k < 5; ++k) zero_pad(Xt + (n * 5 + k) * Kt, f.Cs + f.Ct + f.Cv, Kt);
+}
+
+// ------------------------------------------------------------------------ MFMA GEMM ---
+// out(r, o) = epilogue(sum_k A[r, k] B[o, k]) for r < M, o < O, with A [M, K] and B [>= grid
+// columns, K] row-major, K a multiple of 16 and both 16-byte aligned.  Row r is node n = r / G,
+// component g = r % G, stored at out[n * ostride + o * G + g] (G = 1 scalars, 3 vectors, 5
+// type-2 features).  Epilogue: divide by avg[n], add bias[o], zero where mask[n] == 0 (each
+// optional).
+//
+// v_mfma_f32_16x16x4_f32: lane l supplies A[i = l % 16][k = l / 16] and B[k = l / 16][j = l % 16]
+// and holds D[i = 4 (l / 16) + q][j = l % 16] in element q.  Each lane loads four consecutive k
+// of a 16-wide chunk as one float4 (k = 4 (l / 16) + q for the q-th MFMA); A and B use the same
+// assignment, so the four MFMAs cover the chunk's 16 k exactly once.  A wave computes 32 rows x
+// 16 NB columns; a block is four waves stacked along the rows.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int NB>
+__global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__ A, int64_t M, int K,
+                                                      const float* __restrict__ B, int O, int G,
+                                                      float* __restrict__ out, int64_t ostride,
+                                                      const float* __restrict__ avg,
+                                                      const float* __restrict__ bias,
+                                                      const uint8_t* __restrict__ mask) {
+  const int lane = lane_id();
+  const int li = lane & 15, lk = lane >> 4;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave)) * 32;
+  if (row0 >= M) return;
+  const int col0 = blockIdx.y * 16 * NB;
+  const float* ap[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    int64_t r = row0 + rb * 16 + li;
+    r = r < M ? r : M - 1;
+    ap[rb] = A + r * K + 4 * lk;
+  }
+  const float* bp[NB];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) bp[cb] = B + static_cast<int64_t>(col0 + cb * 16 + li) * K + 4 * lk;
+  floatx4 acc[2][NB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) acc[rb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 a[2], b[NB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) a[rb] = *reinterpret_cast<const floatx4*>(ap[rb]);
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) b[cb] = *reinterpret_cast<const floatx4*>(bp[cb]);
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    floatx4 an[2], bn[NB];
+    const int kn = k0 + 16 < K ? k0 + 16 : k0;  // last chunk reloads itself (in bounds)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) an[rb] = *reinterpret_cast<const floatx4*>(ap[rb] + kn);
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) bn[cb] = *reinterpret_cast<const floatx4*>(bp[cb] + kn);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[rb][q], b[cb][q], acc[rb][cb], 0, 0, 0);
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) a[rb] = an[rb];
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) b[cb] = bn[cb];
+  }
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t r = row0 + rb * 16 + 4 * lk + q;
+      if (r >= M) continue;
+      const int64_t n = r / G;
+      const int gc = static_cast<int>(r - n * G);
+      const bool keep = mask == nullptr || mask[n] != 0;
+      const float den = avg ? avg[n] : 1.f;
+#pragma unroll
+      for (int cb = 0; cb < NB; ++cb) {
+        const int o = col0 + cb * 16 + li;
+        if (o >= O) continue;
+        float val = acc[rb][cb][q];
+        if (avg) val = val / den;
+        if (bias) val += bias[o];
+        out[n * ostride + static_cast<int64_t>(o) * G + gc] = keep ? val : 0.f;
+      }
+    }
+}
+
+// ------------------------------------------------------------------ backward helpers ---
+// out[n][g][o] (row length Opad, zero padded) = in[n][o][g] / avg[n], zero where mask[n] == 0.
+__global__ __launch_bounds__(kSeThreads) void se3_grad_prep(const float* __restrict__ gin, int64_t N,
+                                                           int O, int G, int Opad,
+                                                           const float* __restrict__ avg,
+                                                           const uint8_t* __restrict__ mask,
+                                                           float* __restrict__ out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * G * Opad) return;
+  const int o = static_cast<int>(t % Opad);
+  const int64_t ng = t / Opad;
+  const int64_t n = ng / G;
+  const int gc = static_cast<int>(ng - n * G);
+  float val = 0.f;
+  if (o < O && (mask == nullptr || mask[n] != 0)) {
+    val = gin[(n * O + o) * G + gc];
+    if (avg) val = val / avg[n];
+  }
+  out[t] = val;
+}
+
+// v + (v of the DPP source lane); lanes without a source, or outside ROWS, add 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true);
+  return v + __int_as_float(s);
+}
+
+// Lane 0 of a row turns the 21 per-edge sums into the edge's gradients of R, the direction and Y.
+__device__ __forceinline__ void write_edge_grads(const SeEdges& g, const EdgeScalars& q,
+                                                 const float S[21], float* dR, float* ddir,
+                                                 float* dY) {
+  const int64_t e = q.e;
+  const float* d = q.d;
+  if (dR) {
+    float* o = dR + e * g.P;
+    float val[kSePaths];
+    val[0] = q.y0 * S[0];
+    val[1] = (d[0] * S[1] + d[1] * S[2]) + d[2] * S[3];
+    val[5] = (((q.y2[0] * S[4] + q.y2[1] * S[5]) + q.y2[2] * S[6]) + q.y2[3] * S[7]) + q.y2[4] * S[8];
+    val[2] = q.y0 * S[9];
+    val[3] = (d[0] * S[10] + d[1] * S[11]) + d[2] * S[12];
+    val[4] = (d[0] * S[13] + d[1] * S[14]) + d[2] * S[15];
+    val[7] = (d[0] * S[16] + d[1] * S[17]) + d[2] * S[18];
+    val[6] = q.y0 * S[19];
+    val[8] = S[20];
+#pragma unroll
+    for (int i = 0; i < kSePaths; ++i)
+      if (g.pc[i] >= 0) o[g.pc[i]] = val[i];
+  }
+  if (ddir) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      ddir[3 * e + k] = q.r[1] * S[1 + k] + q.r[3] * S[10 + k] + q.r[4] * S[13 + k] + q.r[7] * S[16 + k];
+  }
+  if (dY) {
+    float* o = dY + e * g.ysh;
+    o[0] = q.r[0] * S[0] + q.r[2] * S[9] + q.r[6] * S[19];
+    if (g.ysh >= 9) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k) o[4 + k] = q.r[5] * S[4 + k];
+    }
+  }
+}
+
+// Sum over the 16 lanes of each row; every lane of the row receives its row's total.
+__device__ __forceinline__ float row_total(float v) {
+  v = dpp_add<kDppXor1, 0xF>(v);
+  v = dpp_add<kDppXor2, 0xF>(v);
+  v = dpp_add<kDppHalfMirror, 0xF>(v);
+  v = dpp_add<kDppMirror, 0xF>(v);
+  return v;
+}
+
+// The target's gradient row for one channel chunk, as held by one lane: scalar-input channels
+// c = cs0 + 4 li + u (u < 4), vector and type-2 input channels c = cv0 + li.
+struct GRow {
+  float s0[4], s1[3][4], s5[5][4];
+  float v2[3], v3, v4[3], v7[5];
+  float t6[5], t8;
+};
+
+__device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, int64_t n, int h, int li,
+                                          const float* Gs, int Ks, const float* Gv, int Kv,
+                                          const float* Gt, int Kt) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = 64 * h + 4 * li + u;
+    const bool ok = c < f.Cs;
+    G.s0[u] = ok && Gs ? Gs[n * Ks + c] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) G.s1[k][u] = ok && Gv ? Gv[(n * 3 + k) * Kv + c] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) G.s5[k][u] = ok && Gt ? Gt[(n * 5 + k) * Kt + c] : 0.f;
+  }
+  const int c = 16 * h + li;
+  const bool okv = c < f.Cv, okt = c < f.Ct;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    G.v2[k] = okv && Gv ? Gv[(n * 3 + k) * Kv + f.Cs + c] : 0.f;
+    G.v4[k] = okv && Gv ? Gv[(n * 3 + k) * Kv + f.Cs + f.Cv + c] : 0.f;
+  }
+  G.v3 = okv && Gs ? Gs[n * Ks + f.Cs + c] : 0.f;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    G.v7[k] = okv && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + f.Ct + c] : 0.f;
+    G.t6[k] = okt && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + c] : 0.f;
+  }
+  G.t8 = okt && Gs ? Gs[n * Ks + f.Cs + f.Cv + c] : 0.f;
+}
+
+// Per-edge gradients of R, the direction and Y.  One wave per target node n; its four 16-lane
+// rows take four edges at a time (row r: edge j0 + r), the lanes of a row split the channels
+// (64 scalar channels as 4 per lane, 16 vector / type-2 channels as 1 per lane, per chunk), and
+// the 21 per-edge sums are reduced within the row.  With one chunk (ONE) the target's gradient
+// row stays in registers for all of its edges.
+template <bool ONE>
+__global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
+                                                          const float* __restrict__ Gs, int Ks,
+                                                          const float* __restrict__ Gv, int Kv,
+                                                          const float* __restrict__ Gt, int Kt,
+                                                          float* __restrict__ dR,
+                                                          float* __restrict__ ddir,
+                                                          float* __restrict__ dY) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  if (n >= g.N) return;
+  const int lane = lane_id();
+  const int row = lane >> 4, li = lane & 15;
+  int a, b;
+  node_range(g, n, a, b);
+  const int nch = ONE ? 1 : max((f.Cs + 63) / 64, max((f.Cv + 15) / 16, (f.Ct + 15) / 16));
+  GRow G;
+  if (ONE) load_grow(G, f, n, 0, li, Gs, Ks, Gv, Kv, Gt, Kt);
+  for (int base = a; base < b; base += kWave) {
+    const int cnt = min(kWave, b - base);
+    const EdgeScalars st = stage_edges(g, base, cnt, lane);
+    for (int j0 = 0; j0 < cnt; j0 += 4) {
+      const int j = j0 + row;
+      const EdgeScalars q = edge_from(st, min(j, kWave - 1));
+      const bool ok = j < cnt && q.ok;
+      const int64_t m = ok ? q.other : 0;
+      float S[21];
+#pragma unroll
+      for (int i = 0; i < 21; ++i) S[i] = 0.f;
+      for (int h = 0; h < nch; ++h) {
+        if (!ONE) load_grow(G, f, n, h, li, Gs, Ks, Gv, Kv, Gt, Kt);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = 64 * h + 4 * li + u;
+          if (c < f.Cs) {
+            const float x = f.s[m * f.Cs + c];
+            S[0] += G.s0[u] * x;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) S[1 + k] += G.s1[k][u] * x;
+#pragma unroll
+            for (int k = 0; k < 5; ++k) S[4 + k] += G.s5[k][u] * x;
+          }
+        }
+        const int c = 16 * h + li;
+        if (c < f.Cv) {
+          const float* vp = f.v + (m * f.Cv + c) * 3;
+          const float v[3] = {vp[0], vp[1], vp[2]};
+          S[9] += (G.v2[0] * v[0] + G.v2[1] * v[1]) + G.v2[2] * v[2];
+#pragma unroll
+          for (int k = 0; k < 3; ++k) S[10 + k] += G.v3 * v[k];
+          S[13] += v[1] * G.v4[2] - v[2] * G.v4[1];  // v x G4
+          S[14] += v[2] * G.v4[0] - v[0] * G.v4[2];
+          S[15] += v[0] * G.v4[1] - v[1] * G.v4[0];
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < 3; ++jj)
+#pragma unroll
+              for (int k = 0; k < 5; ++k) acc += v[jj] * g.cg[(i * 3 + jj) * 5 + k] * G.v7[k];
+            S[16 + i] += acc;
+          }
+        }
+        if (c < f.Ct) {
+          const float* tp = f.t + (m * f.Ct + c) * 5;
+          const float t[5] = {tp[0], tp[1], tp[2], tp[3], tp[4]};
+          S[19] += (((G.t6[0] * t[0] + G.t6[1] * t[1]) + G.t6[2] * t[2]) + G.t6[3] * t[3]) + G.t6[4] * t[4];
+          S[20] += G.t8 * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 21; ++i) S[i] = row_total(S[i]);
+      if (li == 0 && ok) write_edge_grads(g, q, S, dR, ddir, dY);
+    }
+  }
+}
+
+// Source-side sums of the output-gradient rows (edges grouped by source m; the wave's lanes
+// run over output channels, the target's rows are gathered per edge, four edges in flight):
+//   Zs[m]    = [Z0 (Os) | Z1 (Ov) | Z5 (Ot)]                 -> ds = Zs [W0|W1|W5]
+//   Zv[m][k] = [Z2_k (Ov) | Z3_k (Os) | Z4_k (Ov) | Z7_k (Ot)] -> dv = Zv [W2|W3|W4|W7]
+//   Zt[m][j] = [Z6_j (Ot)]                                   -> dt = Zt W6 + 2 t (Z8 W8)
+//   Z8[m]    = [Z8 (Os)]
+// with gs [N, Os], gv [N][3][Ov], gt [N][5][Ot] the prepared output gradients.
+__global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float* __restrict__ gs,
+                                                         int Os, int OsP,
+                                                         const float* __restrict__ gv, int Ov,
+                                                         int OvP, const float* __restrict__ gt,
+                                                         int Ot, int OtP, float* __restrict__ Zs,
+                                                         int KZs, float* __restrict__ Zv, int KZv,
+                                                         float* __restrict__ Zt, int KZt,
+                                                         float* __restrict__ Z8, int KZ8) {
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  if (m >= g.N) return;
+  const int lane = lane_id();
+  int a, b;
+  node_range(g, m, a, b);
+  const int omax = max(Os, max(Ov, Ot));
+  for (int o0 = 0; o0 < omax; o0 += kWave) {
+    const int o = o0 + lane;
+    const bool hs = o < Os && gs, hv = o < Ov && gv, ht = o < Ot && gt;
+    float z0 = 0.f, z1 = 0.f, z5 = 0.f, z8 = 0.f;
+    float z2[3] = {0.f, 0.f, 0.f}, z3[3] = {0.f, 0.f, 0.f}, z4[3] = {0.f, 0.f, 0.f};
+    float z7[3] = {0.f, 0.f, 0.f}, z6[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int base = a; base < b; base += kWave) {
+      const int cnt = min(kWave, b - base);
+      const EdgeScalars st = stage_edges(g, base, cnt, lane);
+      for (int j0 = 0; j0 < cnt; j0 += kSeUnroll) {
+        float ws[kSeUnroll], wv[kSeUnroll][3], wt[kSeUnroll][5];
+#pragma unroll
+        for (int u = 0; u < kSeUnroll; ++u) {
+          const int j = min(j0 + u, kWave - 1);
+          const int64_t n = __builtin_amdgcn_readlane(st.other, j);  // 0 past cnt: in bounds
+          if (hs) ws[u] = gs[n * OsP + o];
+          if (hv) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) wv[u][k] = gv[(n * 3 + k) * OvP + o];
+          }
+          if (ht) {
+#pragma unroll
+            for (int k = 0; k < 5; ++k) wt[u][k] = gt[(n * 5 + k) * OtP + o];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kSeUnroll; ++u) {
+          if (j0 + u >= cnt) break;
+          const EdgeScalars q = edge_at(st, j0 + u);
+          if (!q.ok) continue;
+          if (hs) {
+            const float gsv = ws[u];
+            z0 += q.r[0] * q.y0 * gsv;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) z3[k] += q.r[3] * q.d[k] * gsv;
+            z8 += q.r[8] * gsv;
+          }
+          if (hv) {
+            const float* w = wv[u];
+            z1 += q.r[1] * ((q.d[0] * w[0] + q.d[1] * w[1]) + q.d[2] * w[2]);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) z2[k] += q.r[2] * q.y0 * w[k];
+            z4[0] += q.r[4] * (w[1] * q.d[2] - w[2] * q.d[1]);  // w x d
+            z4[1] += q.r[4] * (w[2] * q.d[0] - w[0] * q.d[2]);
+            z4[2] += q.r[4] * (w[0] * q.d[1] - w[1] * q.d[0]);
+          }
+          if (ht) {
+            const float* w = wt[u];
+            z5 += q.r[5] * ((((q.y2[0] * w[0] + q.y2[1] * w[1]) + q.y2[2] * w[2]) + q.y2[3] * w[3]) +
+                            q.y2[4] * w[4]);
+#pragma unroll
+            for (int k = 0; k < 5; ++k) z6[k] += q.r[6] * q.y0 * w[k];
+#pragma unroll
+            for (int jj = 0; jj < 3; ++jj) {
+              float acc = 0.f;
+#pragma unroll
+              for (int i = 0; i < 3; ++i)
+#pragma unroll
+                for (int k = 0; k < 5; ++k) acc += q.d[i] * g.cg[(i * 3 + jj) * 5 + k] * w[k];
+              z7[jj] += q.r[7] * acc;
+            }
+          }
+        }
+      }
+    }
+    if (Zs) {
+      float* row = Zs + m * KZs;
+      if (hs) row[o] = z0;
+      if (hv) row[Os + o] = z1;
+      if (ht) row[Os + Ov + o] = z5;
+    }
+    if (Zv) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        float* row = Zv + (m * 3 + k) * KZv;
+        if (hv) row[o] = z2[k];
+        if (hs) row[Ov + o] = z3[k];
+        if (hv) row[Ov + Os + o] = z4[k];
+        if (ht) row[2 * Ov + Os + o] = z7[k];
+      }
+    }
+    if (Zt) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k)
+        if (ht) Zt[(m * 5 + k) * KZt + o] = z6[k];
+    }
+    if (Z8 && hs) Z8[m * KZ8 + o] = z8;
+  }
+  // lanes whose group is absent wrote nothing: clear those slots and the padding
+  if (Zs) {
+    float* row = Zs + m * KZs;
+    for (int q = lane; q < KZs; q += kWave) {
+      const bool written = (q < Os && gs) || (q >= Os && q < Os + Ov && gv) ||
+                           (q >= Os + Ov && q < Os + Ov + Ot && gt);
+      if (!written) row[q] = 0.f;
+    }
+  }
+  if (Zv) {
+    for (int k = 0; k < 3; ++k) {
+      float* row = Zv + (m * 3 + k) * KZv;
+      for (int q = lane; q < KZv; q += kWave) {
+        const bool written = (q < Ov && gv) || (q >= Ov && q < Ov + Os && gs) ||
+                             (q >= Ov + Os && q < 2 * Ov + Os && gv) ||
+                             (q >= 2 * Ov + Os && q < 2 * Ov + Os + Ot && gt);
+        if (!written) row[q] = 0.f;
+      }
+    }
+  }
+  if (Zt)
+    for (int k = 0; k < 5; ++k) {
+      float* row = Zt + (m * 5 + k) * KZt;
+      for (int q = lane; q < KZt; q += kWave)
+        if (!(q < Ot && gt)) row[q] = 0.f;
+    }
+  if (Z8)
+    for (int q = lane; q < KZ8; q += kWave)
+      if (!(q < Os && gs)) Z8[m * KZ8 + q] = 0.f;
+}
+
+
+SeEdges make_edges(const int64_t* other, const int32_t* perm, const int32_t* ns, const int32_t* ne,
+                   int64_t N, int64_t E, const float* dir, const float* Y, int ysh, const float* R,
+                   int P, const int32_t* path_cols, const float* cg) {
+  SeEdges g;
+  g.other = other;
+  g.perm = perm;
+  g.ns = ns;
+  g.ne = ne;
+  g.E = static_cast<int32_t>(E);
+  g.N = N;
+  g.dir = dir;
+  g.Y = Y;
+  g.ysh = ysh;
+  g.R = R;
+  g.P = P;
+  for (int i = 0; i < kSePaths; ++i) g.pc[i] = path_cols[i];
+  for (int i = 0; i < 45; ++i) g.cg[i] = cg[i];
+  return g;
+}
+
+int check_edges(const char* who, int64_t N, int64_t E, int ysh, int P, const int32_t* path_cols,
+                const float* cg) {
+  GEO_REQUIRE(N >= 0 && E >= 0, "%s: negative size", who);
+  GEO_REQUIRE(N < 0x7fffffffLL && E < 0x7fffffffLL, "%s: sizes exceed int32 indexing", who);
+  GEO_REQUIRE(path_cols && cg, "%s: null path table or CG table", who);
+  GEO_REQUIRE(ysh >= 1, "%s: Y needs at least one channel", who);
+  for (int i = 0; i < kSePaths; ++i)
+    GEO_REQUIRE(path_cols[i] >= -1 && path_cols[i] < P, "%s: path %d uses column %d of R (P=%d)",
+                who, i, path_cols[i], P);
+  GEO_REQUIRE(path_cols[5] < 0 || ysh >= 9, "%s: path 5 needs Y with 9 channels", who);
+  return GEO_OK;
+}
+
+}  // namespace
+}  // namespace geo
+
+using namespace geo;
+
+extern "C" int geo_se3_aggregate_fwd(const float* s, const float* v, const float* t, int64_t N,
+                                     int32_t Cs, int32_t Cv, int32_t Ct, const int64_t* row,
+                                     const int32_t* perm, const int32_t* node_start,
+                                     const int32_t* node_end, int64_t E, const float* dir,
+                                     const float* Y, int32_t ysh, const float* R, int32_t P,
+                                     const int32_t* path_cols, const float* cg, float* Xs,
+                                     int32_t Ks, float* Xv, int32_t Kv, float* Xt, int32_t Kt,
+                                     void* stream) {
+  int rc = check_edges("se3_aggregate_fwd", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(Cs >= 0 && Cv >= 0 && Ct >= 0, "se3_aggregate_fwd: negative channel count");
+  GEO_REQUIRE(!Xs || Ks >= Cs + Cv + Ct, "se3_aggregate_fwd: Ks=%d < Cs+Cv+Ct", Ks);
+  GEO_REQUIRE(!Xv || Kv >= Cs + 2 * Cv, "se3_aggregate_fwd: Kv=%d < Cs+2Cv", Kv);
+  GEO_REQUIRE(!Xt || Kt >= Cs + Ct + Cv, "se3_aggregate_fwd: Kt=%d < Cs+Ct+Cv", Kt);
+  GEO_REQUIRE((Cs == 0 || s) && (Cv == 0 || v) && (Ct == 0 || t), "se3_aggregate_fwd: null features");
+  GEO_REQUIRE(path_cols[6] < 0 || Ct > 0, "se3_aggregate_fwd: path 6 without type-2 input");
+  GEO_REQUIRE(path_cols[8] < 0 || Ct > 0, "se3_aggregate_fwd: path 8 without type-2 input");
+  if (N == 0 || (!Xs && !Xv && !Xt)) return GEO_OK;
+  GEO_REQUIRE(node_start && node_end && (E == 0 || (row && dir && Y && R)),
+              "se3_aggregate_fwd: null graph array");
+  SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  SeFeat f{s, v, t, Cs, Cv, Ct};
+  hipLaunchKernelGGL(se3_fwd_aggregate, dim3(static_cast<unsigned>(ceil_div(N, kSeWaves))),
+                     dim3(kSeThreads), 0, as_stream(stream), g, f, Xs, Ks, Xv, Kv, Xt, Kt);
+  GEO_LAUNCH_CHECK("se3_fwd_aggregate");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B, int32_t B_rows,
+                            int32_t O, int32_t G, float* out, int64_t out_stride, const float* avg,
+                            const float* bias, const uint8_t* mask, void* stream) {
+  GEO_REQUIRE(M >= 0 && K > 0 && O >= 0 && G >= 1, "se3_gemm: bad sizes");
+  GEO_REQUIRE(K % 16 == 0, "se3_gemm: K=%d must be a multiple of 16", K);
+  if (M == 0 || O == 0) return GEO_OK;
+  GEO_REQUIRE(M % G == 0, "se3_gemm: M=%lld is not a multiple of G=%d", (long long)M, G);
+  GEO_REQUIRE(A && B && out, "se3_gemm: null pointer");
+  GEO_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0,
+              "se3_gemm: A and B must be 16-byte aligned");
+  GEO_REQUIRE(out_stride >= static_cast<int64_t>(O) * G, "se3_gemm: out_stride too small");
+  const int nb = O > 32 ? 4 : (O > 16 ? 2 : 1);
+  const int cols = 16 * nb;
+  const int64_t gy = ceil_div(O, cols);
+  GEO_REQUIRE(B_rows >= gy * cols, "se3_gemm: B has %d rows, the launch reads %lld", B_rows,
+              (long long)(gy * cols));
+  const dim3 grid(static_cast<unsigned>(ceil_div(M, 32 * kSeWaves)), static_cast<unsigned>(gy));
+  hipStream_t st = as_stream(stream);
+  if (nb == 4)
+    hipLaunchKernelGGL(se3_gemm<4>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
+                       avg, bias, mask);
+  else if (nb == 2)
+    hipLaunchKernelGGL(se3_gemm<2>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
+                       avg, bias, mask);
+  else
+    hipLaunchKernelGGL(se3_gemm<1>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
+                       avg, bias, mask);
+  GEO_LAUNCH_CHECK("se3_gemm");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_grad_prep(const float* grad, int64_t N, int32_t O, int32_t G, int32_t Opad,
+                                 const float* avg, const uint8_t* mask, float* out, void* stream) {
+  GEO_REQUIRE(N >= 0 && O >= 0 && G >= 1 && Opad >= O, "se3_grad_prep: bad sizes");
+  const int64_t total = N * G * Opad;
+  if (total == 0) return GEO_OK;
+  GEO_REQUIRE(out && (O == 0 || grad), "se3_grad_prep: null pointer");
+  hipLaunchKernelGGL(se3_grad_prep, dim3(static_cast<unsigned>(ceil_div(total, kSeThreads))),
+                     dim3(kSeThreads), 0, as_stream(stream), grad, N, O, G, Opad, avg, mask, out);
+  GEO_LAUNCH_CHECK("se3_grad_prep");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_bwd_edge(const float* s, const float* v, const float* t, int64_t N,
+                                int32_t Cs, int32_t Cv, int32_t Ct, const int64_t* row,
+                                const int32_t* perm, const int32_t* node_start,
+                                const int32_t* node_end, int64_t E, const float* dir, const float* Y,
+                                int32_t ysh, const float* R, int32_t P, const int32_t* path_cols,
+                                const float* cg, const float* gXs, int32_t Ks, const float* gXv,
+                                int32_t Kv, const float* gXt, int32_t Kt, float* dR, float* ddir,
+                                float* dY, void* stream) {
+  int rc = check_edges("se3_bwd_edge", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(!gXs || Ks >= Cs + Cv + Ct, "se3_bwd_edge: Ks too small");
+  GEO_REQUIRE(!gXv || Kv >= Cs + 2 * Cv, "se3_bwd_edge: Kv too small");
+  GEO_REQUIRE(!gXt || Kt >= Cs + Ct + Cv, "se3_bwd_edge: Kt too small");
+  GEO_REQUIRE((Cs == 0 || s) && (Cv == 0 || v) && (Ct == 0 || t), "se3_bwd_edge: null features");
+  if (N == 0 || E == 0 || (!dR && !ddir && !dY)) return GEO_OK;
+  GEO_REQUIRE(row && node_start && node_end && dir && Y && R, "se3_bwd_edge: null graph array");
+  SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  SeFeat f{s, v, t, Cs, Cv, Ct};
+  const bool one = Cs <= 64 && Cv <= 16 && Ct <= 16;
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kSeWaves)));
+  if (one)
+    hipLaunchKernelGGL(se3_bwd_edge<true>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f, gXs,
+                       Ks, gXv, Kv, gXt, Kt, dR, ddir, dY);
+  else
+    hipLaunchKernelGGL(se3_bwd_edge<false>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f, gXs,
+                       Ks, gXv, Kv, gXt, Kt, dR, ddir, dY);
+  GEO_LAUNCH_CHECK("se3_bwd_edge");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const float* gv, int32_t Ov,
+                               int32_t OvP, const float* gt, int32_t Ot, int32_t OtP, int64_t N,
+                               const int64_t* col, const int32_t* perm, const int32_t* node_start,
+                               const int32_t* node_end, int64_t E, const float* dir, const float* Y,
+                               int32_t ysh, const float* R, int32_t P, const int32_t* path_cols,
+                               const float* cg, float* Zs, int32_t KZs, float* Zv, int32_t KZv,
+                               float* Zt, int32_t KZt, float* Z8, int32_t KZ8, void* stream) {
+  int rc = check_edges("se3_bwd_src", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(Os >= 0 && Ov >= 0 && Ot >= 0, "se3_bwd_src: negative channel count");
+  GEO_REQUIRE((!gs || OsP >= Os) && (!gv || OvP >= Ov) && (!gt || OtP >= Ot),
+              "se3_bwd_src: padded widths too small");
+  GEO_REQUIRE(!Zs || KZs >= Os + Ov + Ot, "se3_bwd_src: KZs too small");
+  GEO_REQUIRE(!Zv || KZv >= 2 * Ov + Os + Ot, "se3_bwd_src: KZv too small");
+  GEO_REQUIRE(!Zt || KZt >= Ot, "se3_bwd_src: KZt too small");
+  GEO_REQUIRE(!Z8 || KZ8 >= Os, "se3_bwd_src: KZ8 too small");
+  if (N == 0 || (!Zs && !Zv && !Zt && !Z8)) return GEO_OK;
+  GEO_REQUIRE(node_start && node_end && (E == 0 || (col && dir && Y && R)),
+              "se3_bwd_src: null graph array");
+  SeEdges g = make_edges(col, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  hipLaunchKernelGGL(se3_bwd_src, dim3(static_cast<unsigned>(ceil_div(N, kSeWaves))),
+                     dim3(kSeThreads), 0, as_stream(stream), g, gs, Os, OsP, gv, Ov, OvP, gt, Ot,
+                     OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
+  GEO_LAUNCH_CHECK("se3_bwd_src");
+  return GEO_OK;
+}

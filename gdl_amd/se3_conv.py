@@ -1,0 +1,529 @@
+"""SE(3)-equivariant convolution with fused message passing (drop-in for
+geoembodied/nn/modules/se3_conv.py: ``SE3Conv``, ``RadialBasis``).
+
+The reference forms one message per edge for up to nine tensor-product paths, concatenates them
+into an ``[E, Cs + 3 Cv + 5 Ct]`` tensor and segment-sums it over targets (se3_conv.py:61-235,
+:516-545).  Every path is ``r_p(e) * W_p * x_p(e)`` with ``W_p`` shared by all edges, so here the
+r-weighted source features are summed per target node first (one kernel pass over the target
+CSR, no per-edge tensor) and the weights applied once per node by an fp32 MFMA GEMM whose
+epilogue divides by the average degree, adds the scalar bias and applies the mask.  The
+backward is the transposed structure: per-edge gradients of R, the direction and Y from
+per-node gradient rows, and source-side sums over the CSR of the sources followed by GEMMs
+with the transposed weights.  Weight gradients are plain GEMMs over nodes (torch.matmul).
+
+Arithmetic is fp32 (inputs of lower precision are computed in fp32, as the reference does;
+float64 inputs are computed in fp32 and returned as float64).  Results equal the reference's
+up to the order of the sums.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from gdl_amd import _native as _nat
+from gdl_amd.csrc import _require_gpu, sort_and_build_csr_cuda
+
+PATH_NAMES = ("w_ss", "w_sv", "w_vv_scalar", "w_vs", "w_vv_cross", "w_st2", "w_t2t2", "w_vt2", "w_t2s")
+
+
+def _pad16(x: int) -> int:
+    return (int(x) + 15) // 16 * 16
+
+
+def _pad64(x: int) -> int:
+    return max((int(x) + 63) // 64 * 64, 64)
+
+
+def cg_11_2_cartesian(dtype=torch.float32, device=None) -> Tensor:
+    """CG(1, 1 -> 2) as [3, 3, 5] in Cartesian (x, y, z) order: the symmetric traceless products
+    (xy, yz, (2zz - xx - yy)/sqrt3, xz, xx - yy) / sqrt2 in the basis order of Y_2
+    (the reference's table, functional/tensor_product.py:104-126, permuted from the (y, z, x)
+    order as se3_conv.py:384-390 does)."""
+    c = torch.zeros(3, 3, 5, dtype=torch.float64)
+    h = math.sqrt(0.5)
+    c[0, 1, 0] = c[1, 0, 0] = h
+    c[1, 2, 1] = c[2, 1, 1] = h
+    c[2, 2, 2] = 2.0 / math.sqrt(6.0)
+    c[0, 0, 2] = c[1, 1, 2] = -1.0 / math.sqrt(6.0)
+    c[0, 2, 3] = c[2, 0, 3] = h
+    c[0, 0, 4] = 1.0 / math.sqrt(2.0)
+    c[1, 1, 4] = -1.0 / math.sqrt(2.0)
+    return c.to(dtype=dtype, device=device)
+
+
+def path_columns(weights: Dict[str, Optional[Tensor]], has_t2_src: bool, has_y2: bool,
+                 Ct2_out: int) -> list:
+    """Column of R of each path, -1 where it does not run.  A path runs when its weight exists
+    and, for the type-2 paths, its inputs do; columns are numbered in the order the paths run
+    (se3_conv.py:149-233)."""
+    run = [
+        weights.get("w_ss") is not None,
+        weights.get("w_sv") is not None,
+        weights.get("w_vv_scalar") is not None,
+        weights.get("w_vs") is not None,
+        weights.get("w_vv_cross") is not None,
+        weights.get("w_st2") is not None and has_y2 and Ct2_out > 0,
+        weights.get("w_t2t2") is not None and has_t2_src and Ct2_out > 0,
+        weights.get("w_vt2") is not None and Ct2_out > 0,
+        weights.get("w_t2s") is not None and has_t2_src,
+    ]
+    cols, k = [], 0
+    for r in run:
+        cols.append(k if r else -1)
+        k += int(r)
+    return cols
+
+
+class _Plan:
+    """Sizes, padded row widths and the path table of one call."""
+
+    def __init__(self, Cs, Cv, Ct, Os, Ov, Ot, pc, P, ysh, t_out):
+        self.Cs, self.Cv, self.Ct = Cs, Cv, Ct
+        self.Os, self.Ov, self.Ot = Os, Ov, (Ot if t_out else 0)
+        self.pc, self.P, self.ysh = pc, P, ysh
+        self.Ks = _pad16(Cs + Cv + Ct)
+        self.Kv = _pad16(Cs + 2 * Cv)
+        self.Kt = _pad16(Cs + Ct + Cv)
+        self.OsP, self.OvP, self.OtP = _pad16(self.Os), _pad16(self.Ov), _pad16(self.Ot)
+        self.KZs = _pad16(self.Os + self.Ov + self.Ot)
+        self.KZv = _pad16(2 * self.Ov + self.Os + self.Ot)
+        self.KZt = _pad16(self.Ot)
+        self.KZ8 = _pad16(self.Os)
+        self.pc_c = (ctypes.c_int32 * 9)(*pc)
+
+    def w(self, W, i):
+        return W[i] if self.pc[i] >= 0 else None
+
+
+def _block(rows: int, K: int, parts, device) -> Tensor:
+    """[pad64(rows), K] fp32 with the given [rows, width] blocks side by side (None = zeros)."""
+    out = torch.zeros(_pad64(rows), K, dtype=torch.float32, device=device)
+    c = 0
+    for width, w in parts:
+        if w is not None and rows > 0 and width > 0:
+            out[:rows, c:c + width] = w
+        c += width
+    return out
+
+
+def _transpose_block(Wb: Tensor, OP: int, K: int) -> Tensor:
+    """[pad64(K), OP] with rows k < K equal to column k of the first OP rows of the block."""
+    out = torch.zeros(_pad64(K), OP, dtype=torch.float32, device=Wb.device)
+    out[:K] = Wb[:OP, :K].t()
+    return out
+
+
+def _gemm(A: Tensor, M: int, K: int, B: Tensor, O: int, G: int, out: Tensor, ostride: int,
+          avg=None, bias=None, mask=None) -> None:
+    if M == 0 or O == 0:
+        return
+    _nat.check(_nat.lib().geo_se3_gemm(
+        _nat.ptr(A), M, K, _nat.ptr(B), B.shape[0], O, G, _nat.ptr(out), ostride, _nat.ptr(avg),
+        _nat.ptr(bias), _nat.ptr(mask), _nat.stream_of(A.device)), "geo_se3_gemm")
+
+
+class _SE3MessageAggregate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, plan: _Plan, graph_arrays, cg_c, avg, mask_u8, s, v, t, direction, Y, R,
+                bias, *W):
+        row, col, perm, ns, ne, src_csr = graph_arrays
+        p = plan
+        dev = s.device
+        N, E = s.shape[0], row.shape[0]
+        f32 = dict(dtype=torch.float32, device=dev)
+        Xs = torch.empty(N, p.Ks, **f32) if p.Os > 0 else None
+        Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 else None
+        Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 else None
+        L = _nat.lib()
+        st = _nat.stream_of(dev)
+        _nat.check(L.geo_se3_aggregate_fwd(
+            _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, p.Cs, p.Cv, p.Ct, _nat.ptr(row), _nat.ptr(perm),
+            _nat.ptr(ns), _nat.ptr(ne), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P,
+            p.pc_c, cg_c, _nat.ptr(Xs), p.Ks, _nat.ptr(Xv), p.Kv, _nat.ptr(Xt), p.Kt, st),
+            "geo_se3_aggregate_fwd")
+        Cs, Cv, Ct = p.Cs, p.Cv, p.Ct
+        Ws = _block(p.Os, p.Ks, [(Cs, p.w(W, 0)), (Cv, p.w(W, 3)), (Ct, p.w(W, 8))], dev)
+        Wv = _block(p.Ov, p.Kv, [(Cs, p.w(W, 1)), (Cv, p.w(W, 2)), (Cv, p.w(W, 4))], dev)
+        Wt = _block(p.Ot, p.Kt, [(Cs, p.w(W, 5)), (Ct, p.w(W, 6)), (Cv, p.w(W, 7))], dev)
+        s_out = torch.empty(N, p.Os, **f32)
+        v_out = torch.empty(N, p.Ov, 3, **f32)
+        t_out = torch.empty(N, p.Ot, 5, **f32)
+        _gemm(Xs, N, p.Ks, Ws, p.Os, 1, s_out, p.Os, avg, bias, mask_u8)
+        _gemm(Xv, 3 * N, p.Kv, Wv, p.Ov, 3, v_out, 3 * p.Ov, avg, None, mask_u8)
+        _gemm(Xt, 5 * N, p.Kt, Wt, p.Ot, 5, t_out, 5 * p.Ot, avg, None, mask_u8)
+        ctx.plan, ctx.graph_arrays, ctx.cg_c = plan, graph_arrays, cg_c
+        ctx.wblocks = (Ws, Wv, Wt)
+        ctx.has_bias = bias is not None
+        ctx.save_for_backward(s, v, t, direction, Y, R, avg, mask_u8, Xs, Xv, Xt, *W)
+        return s_out, v_out, t_out
+
+    @staticmethod
+    def backward(ctx, g_s, g_v, g_t):
+        p = ctx.plan
+        s, v, t, direction, Y, R, avg, mask_u8, Xs, Xv, Xt, *W = ctx.saved_tensors
+        row, col, perm, ns, ne, src_csr = ctx.graph_arrays
+        dev = s.device
+        N, E = s.shape[0], row.shape[0]
+        f32 = dict(dtype=torch.float32, device=dev)
+        L = _nat.lib()
+        st = _nat.stream_of(dev)
+        need = ctx.needs_input_grad  # (plan, graph, cg, avg, mask, s, v, t, dir, Y, R, bias, *W)
+
+        def prep(g, O, G, OP):
+            if O == 0:
+                return None
+            out = torch.empty(N, G, OP, **f32)
+            gc = (g if g is not None else torch.zeros(N, O, G, **f32)).to(torch.float32).contiguous()
+            _nat.check(L.geo_se3_grad_prep(_nat.ptr(gc), N, O, G, OP, _nat.ptr(avg), _nat.ptr(mask_u8),
+                                           _nat.ptr(out), st), "geo_se3_grad_prep")
+            return out
+
+        Gs = prep(g_s, p.Os, 1, p.OsP)
+        Gv = prep(g_v, p.Ov, 3, p.OvP)
+        Gt = prep(g_t, p.Ot, 5, p.OtP)
+        Cs, Cv, Ct, Os, Ov, Ot = p.Cs, p.Cv, p.Ct, p.Os, p.Ov, p.Ot
+
+        # per-edge gradients of R, direction and Y from gX = G W (per target node)
+        dR = ddir = dY = None
+        if (need[8] or need[9] or need[10]) and E > 0:
+            gXs = gXv = gXt = None
+            Ws, Wv, Wt = ctx.wblocks
+            if Gs is not None:
+                gXs = torch.empty(N, p.Ks, **f32)
+                _gemm(Gs, N, p.OsP, _transpose_block(Ws, p.OsP, p.Ks), p.Ks, 1, gXs, p.Ks)
+            if Gv is not None:
+                gXv = torch.empty(N, 3, p.Kv, **f32)
+                _gemm(Gv, 3 * N, p.OvP, _transpose_block(Wv, p.OvP, p.Kv), p.Kv, 1, gXv, p.Kv)
+            if Gt is not None:
+                gXt = torch.empty(N, 5, p.Kt, **f32)
+                _gemm(Gt, 5 * N, p.OtP, _transpose_block(Wt, p.OtP, p.Kt), p.Kt, 1, gXt, p.Kt)
+            dR = torch.zeros(E, p.P, **f32) if need[10] else None
+            ddir = torch.zeros(E, 3, **f32) if need[8] else None
+            dY = torch.zeros(E, p.ysh, **f32) if need[9] else None
+            _nat.check(L.geo_se3_bwd_edge(
+                _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, Cs, Cv, Ct, _nat.ptr(row), _nat.ptr(perm),
+                _nat.ptr(ns), _nat.ptr(ne), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R),
+                p.P, p.pc_c, ctx.cg_c, _nat.ptr(gXs), p.Ks, _nat.ptr(gXv), p.Kv, _nat.ptr(gXt), p.Kt,
+                _nat.ptr(dR), _nat.ptr(ddir), _nat.ptr(dY), st), "geo_se3_bwd_edge")
+
+        # feature gradients: source-side sums over the CSR of the sources, then GEMMs with W^T
+        ds = dv = dt = None
+        want_s, want_v, want_t = need[5] and Cs > 0, need[6] and Cv > 0, need[7] and Ct > 0
+        if want_s or want_v or want_t:
+            perm_r, ns_r, ne_r = src_csr()
+            Zs = torch.empty(N, p.KZs, **f32) if want_s else None
+            Zv = torch.empty(N, 3, p.KZv, **f32) if want_v else None
+            Zt = torch.empty(N, 5, p.KZt, **f32) if want_t and Ot > 0 else None
+            Z8 = torch.empty(N, p.KZ8, **f32) if want_t and p.pc[8] >= 0 else None
+            _nat.check(L.geo_se3_bwd_src(
+                _nat.ptr(Gs), Os, p.OsP, _nat.ptr(Gv), Ov, p.OvP, _nat.ptr(Gt), Ot, p.OtP, N,
+                _nat.ptr(col), _nat.ptr(perm_r), _nat.ptr(ns_r), _nat.ptr(ne_r), E, _nat.ptr(direction),
+                _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, ctx.cg_c, _nat.ptr(Zs), p.KZs, _nat.ptr(Zv),
+                p.KZv, _nat.ptr(Zt), p.KZt, _nat.ptr(Z8), p.KZ8, st), "geo_se3_bwd_src")
+
+            def wt(i, _rows):  # W_i^T [in, out] or None
+                return W[i].t() if p.pc[i] >= 0 else None
+
+            if want_s:
+                Bs = _block(Cs, p.KZs, [(Os, wt(0, Cs)), (Ov, wt(1, Cs)), (Ot, wt(5, Cs))], dev)
+                ds = torch.empty(N, Cs, **f32)
+                _gemm(Zs, N, p.KZs, Bs, Cs, 1, ds, Cs)
+            if want_v:
+                Bv = _block(Cv, p.KZv, [(Ov, wt(2, Cv)), (Os, wt(3, Cv)), (Ov, wt(4, Cv)), (Ot, wt(7, Cv))], dev)
+                dv = torch.empty(N, Cv, 3, **f32)
+                _gemm(Zv, 3 * N, p.KZv, Bv, Cv, 3, dv, 3 * Cv)
+            if want_t:
+                dt = torch.zeros(N, Ct, 5, **f32)
+                if Zt is not None and p.pc[6] >= 0:
+                    Bt = _block(Ct, p.KZt, [(Ot, wt(6, Ct))], dev)
+                    _gemm(Zt, 5 * N, p.KZt, Bt, Ct, 5, dt, 5 * Ct)
+                if Z8 is not None:
+                    B8 = _block(Ct, p.KZ8, [(Os, wt(8, Ct))], dev)
+                    u = torch.empty(N, Ct, **f32)
+                    _gemm(Z8, N, p.KZ8, B8, Ct, 1, u, Ct)
+                    dt = dt + 2.0 * t * u.unsqueeze(-1)
+
+        # weight gradients: sums over nodes of (prepared output gradient) x (per-node aggregate)
+        dW = [None] * 9
+        if Gs is not None and any(need[12 + i] for i in (0, 3, 8)):
+            m = Gs.view(N, p.OsP)[:, :Os].t() @ Xs[:, :Cs + Cv + Ct]
+            for i, a, b in ((0, 0, Cs), (3, Cs, Cs + Cv), (8, Cs + Cv, Cs + Cv + Ct)):
+                if p.pc[i] >= 0:
+                    dW[i] = m[:, a:b]
+        if Gv is not None and any(need[12 + i] for i in (1, 2, 4)):
+            m = Gv.view(3 * N, p.OvP)[:, :Ov].t() @ Xv.view(3 * N, p.Kv)[:, :Cs + 2 * Cv]
+            for i, a, b in ((1, 0, Cs), (2, Cs, Cs + Cv), (4, Cs + Cv, Cs + 2 * Cv)):
+                if p.pc[i] >= 0:
+                    dW[i] = m[:, a:b]
+        if Gt is not None and any(need[12 + i] for i in (5, 6, 7)):
+            m = Gt.view(5 * N, p.OtP)[:, :Ot].t() @ Xt.view(5 * N, p.Kt)[:, :Cs + Ct + Cv]
+            for i, a, b in ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)):
+                if p.pc[i] >= 0:
+                    dW[i] = m[:, a:b]
+        dbias = None
+        if ctx.has_bias and need[11] and g_s is not None:
+            gm = g_s if mask_u8 is None else g_s * mask_u8.view(N, 1).to(g_s.dtype)
+            dbias = gm.sum(0)
+        dW = [dW[i] if (dW[i] is not None and need[12 + i]) else None for i in range(9)]
+        return (None, None, None, None, None, ds, dv, dt, ddir, dY, dR, dbias, *dW)
+
+
+def _source_csr_getter(graph, row: Tensor, N: int):
+    def get():
+        cached = getattr(graph, "_source_csr", None)
+        if cached is not None:
+            return cached
+        _, perm_r, ns_r, ne_r = sort_and_build_csr_cuda(row, N)
+        out = (perm_r, ns_r, ne_r)
+        try:
+            object.__setattr__(graph, "_source_csr", out)
+        except (AttributeError, TypeError):
+            pass
+        return out
+    return get
+
+
+def se3_message_aggregate(
+    scalars: Tensor,
+    vectors: Tensor,
+    graph,
+    R: Tensor,
+    weights: Dict[str, Optional[Tensor]],
+    Cs_out: int,
+    Cv_out: int,
+    Ct2_out: int = 0,
+    type2: Optional[Tensor] = None,
+    cg_11_2: Optional[Tensor] = None,
+    bias: Optional[Tensor] = None,
+    mask: Optional[Tensor] = None,
+    return_type2: bool = False,
+):
+    """Messages of the nine tensor-product paths summed over each target's edges, divided by the
+    per-node average degree, plus the scalar bias, masked (se3_conv.py:61-235 and :482-579 from
+    the radial weights R on).  ``graph`` provides row, col, perm, node_start, node_end (CSR of the
+    targets), direction, Y, avg_degree and N.  Returns (s [N, Cs_out], v [N, Cv_out, 3]) or with
+    ``return_type2`` also t [N, Ct2_out, 5]; differentiable with respect to the features, the
+    graph's direction and Y, R, the weights and the bias."""
+    _require_gpu("se3_message_aggregate", scalars, vectors, R)
+    dev = scalars.device
+    N = int(graph.N)
+    f32 = torch.float32
+    s = scalars.to(f32).contiguous()
+    v = vectors.to(f32).contiguous()
+    Cs, Cv = s.shape[1], v.shape[1]
+    if s.shape[0] != N or v.shape[0] != N or v.shape[2] != 3:
+        raise ValueError(f"se3_message_aggregate: features {tuple(s.shape)}, {tuple(v.shape)} for N={N}")
+    t = type2.to(f32).contiguous() if type2 is not None else None
+    Ct = t.shape[1] if t is not None else 0
+    Y = graph.Y.to(f32).contiguous()
+    ysh = Y.shape[1]
+    has_y2 = ysh >= 9
+    pc = path_columns(weights, t is not None and Ct > 0, has_y2, Ct2_out)
+    if t is not None and Ct == 0:
+        t = None
+    R = R.to(f32).contiguous()
+    P = R.shape[1]
+    if max(pc) >= P:
+        raise ValueError(f"se3_message_aggregate: {max(pc) + 1} paths run but R has {P} columns")
+    plan = _Plan(Cs, Cv, Ct, Cs_out, Cv_out, Ct2_out, pc, P, ysh, return_type2 and Ct2_out > 0)
+    cg = cg_11_2 if cg_11_2 is not None else cg_11_2_cartesian()
+    cg_c = (ctypes.c_float * 45)(*[float(x) for x in cg.detach().reshape(-1).cpu().tolist()])
+    row = graph.row.to(device=dev, dtype=torch.int64).contiguous()
+    col = graph.col.to(device=dev, dtype=torch.int64).contiguous()
+    arrays = (row, col, graph.perm.to(device=dev, dtype=torch.int32).contiguous(),
+              graph.node_start.to(device=dev, dtype=torch.int32).contiguous(),
+              graph.node_end.to(device=dev, dtype=torch.int32).contiguous(),
+              _source_csr_getter(graph, row, N))
+    avg = graph.avg_degree
+    avg = (avg.to(device=dev, dtype=f32).contiguous() if avg is not None
+           else torch.ones(N, dtype=f32, device=dev))
+    mask_u8 = None
+    if mask is not None:
+        mask_u8 = mask.to(device=dev, dtype=torch.bool).reshape(-1).contiguous().view(torch.uint8)
+    b = bias.to(f32).contiguous() if bias is not None and Cs_out > 0 else None
+    Wl = [(weights.get(k).to(f32).contiguous() if weights.get(k) is not None else
+           torch.zeros(0, device=dev)) for k in PATH_NAMES]
+    direction = graph.direction.to(f32).contiguous()
+    with torch.cuda.device(dev):
+        s_out, v_out, t_out = _SE3MessageAggregate.apply(
+            plan, arrays, cg_c, avg, mask_u8, s, v, t, direction, Y, R, b, *Wl)
+    if return_type2:
+        return s_out, v_out, (t_out if Ct2_out > 0 else None)
+    return s_out, v_out
+
+
+class _RadialMLP(torch.autograd.Function):
+    """R = W2 silu(W1 (basis(dist) * envelope(dist)) + b1) + b2 in one kernel per direction."""
+
+    @staticmethod
+    def forward(ctx, dist, freqs, cutoff, W1, b1, W2, b2):
+        dev = dist.device
+        E = dist.shape[0]
+        H, NB = W1.shape
+        P = W2.shape[0]
+        d = dist.to(torch.float32).contiguous()
+        args = [x.to(torch.float32).contiguous() for x in (freqs, W1, b1, W2, b2)]
+        R = torch.empty(E, P, dtype=torch.float32, device=dev)
+        with torch.cuda.device(dev):
+            _nat.check(_nat.lib().geo_radial_mlp_fwd(
+                _nat.ptr(d), E, _nat.ptr(args[0]), NB, float(cutoff), _nat.ptr(args[1]),
+                _nat.ptr(args[2]), H, _nat.ptr(args[3]), _nat.ptr(args[4]), P, _nat.ptr(R),
+                _nat.stream_of(dev)), "geo_radial_mlp_fwd")
+        ctx.save_for_backward(d, *args)
+        ctx.cutoff, ctx.dims = float(cutoff), (E, NB, H, P)
+        return R
+
+    @staticmethod
+    def backward(ctx, dR):
+        d, freqs, W1, b1, W2, b2 = ctx.saved_tensors
+        E, NB, H, P = ctx.dims
+        dev = d.device
+        need = ctx.needs_input_grad
+        f32 = dict(dtype=torch.float32, device=dev)
+        dd = torch.empty(E, **f32) if need[0] else None
+        dW1 = torch.empty(H, NB, **f32) if need[3] else None
+        db1 = torch.empty(H, **f32) if need[4] else None
+        dW2 = torch.empty(P, H, **f32) if need[5] else None
+        db2 = torch.empty(P, **f32) if need[6] else None
+        g = dR.to(torch.float32).contiguous()
+        L = _nat.lib()
+        with torch.cuda.device(dev):
+            nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E)
+            ws = _nat.workspace(nbytes, dev)
+            _nat.check(L.geo_radial_mlp_bwd(
+                _nat.ptr(d), E, _nat.ptr(freqs), NB, ctx.cutoff, _nat.ptr(W1), _nat.ptr(b1), H,
+                _nat.ptr(W2), _nat.ptr(b2), P, _nat.ptr(g), _nat.ptr(dd), _nat.ptr(dW1), _nat.ptr(db1),
+                _nat.ptr(dW2), _nat.ptr(db2), _nat.ptr(ws), nbytes, _nat.stream_of(dev)),
+                "geo_radial_mlp_bwd")
+        return dd, None, None, dW1, db1, dW2, db2
+
+
+def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
+               b2: Tensor) -> Tensor:
+    """Radial weights [E, P] of edge lengths ``dist`` [E] (fp32, on the GPU; num_basis <= 16,
+    hidden <= 64, outputs <= 16), differentiable with respect to dist and the four weights."""
+    _require_gpu("radial_mlp", dist)
+    return _RadialMLP.apply(dist, freqs, cutoff, W1, b1, W2, b2)
+
+
+class RadialBasis(nn.Module):
+    """Radial weights of the edge lengths: sinusoidal basis sin(k pi d / cutoff) / d times the
+    cosine envelope 0.5 (1 + cos(pi d / cutoff)) clamped at 0, through a two-layer SiLU MLP
+    (se3_conv.py:238-282; same parameter names)."""
+
+    def __init__(self, num_basis: int = 16, cutoff: float = 5.0, num_hidden: int = 64,
+                 num_output: int = 1) -> None:
+        super().__init__()
+        self.cutoff = cutoff
+        self.num_basis = num_basis
+        freqs = torch.arange(1, num_basis + 1).float() * math.pi / cutoff
+        self.register_buffer("freqs", freqs)
+        self.mlp = nn.Sequential(nn.Linear(num_basis, num_hidden), nn.SiLU(),
+                                 nn.Linear(num_hidden, num_output))
+
+    def forward(self, dist: Tensor) -> Tensor:
+        """[E] edge lengths -> [E, num_output] radial weights (one fused kernel; fp32)."""
+        l1, l2 = self.mlp[0], self.mlp[2]
+        R = radial_mlp(dist.reshape(-1), self.freqs, self.cutoff, l1.weight, l1.bias, l2.weight,
+                       l2.bias)
+        return R.reshape(*dist.shape, l2.weight.shape[0])
+
+
+class SE3Conv(nn.Module):
+    """SE(3)-equivariant continuous convolution (se3_conv.py:285-602): the reference's
+    constructor, parameter names (``w_ss`` ... ``w_t2s`` as bias-free ``nn.Linear``,
+    ``radial_basis``, ``scalar_bias``, buffer ``cg_11_2``) and forward contract, with the
+    messages and their aggregation computed by the fused GPU kernels."""
+
+    def __init__(self, in_scalar_channels: int, in_vector_channels: int, out_scalar_channels: int,
+                 out_vector_channels: int, in_type2_channels: int = 0, out_type2_channels: int = 0,
+                 radius: float = 2.0, max_num_neighbors: int = 32,
+                 num_radial_basis: int = 16) -> None:
+        super().__init__()
+        self.in_scalar_channels = in_scalar_channels
+        self.in_vector_channels = in_vector_channels
+        self.out_scalar_channels = out_scalar_channels
+        self.out_vector_channels = out_vector_channels
+        self.in_type2_channels = in_type2_channels
+        self.out_type2_channels = out_type2_channels
+        self.radius = radius
+        self.max_num_neighbors = max_num_neighbors
+        cs, cv, ct = in_scalar_channels, in_vector_channels, in_type2_channels
+        os_, ov, ot = out_scalar_channels, out_vector_channels, out_type2_channels
+        spec = {
+            "w_ss": (cs, os_), "w_sv": (cs, ov), "w_vv_scalar": (cv, ov), "w_vs": (cv, os_),
+            "w_vv_cross": (cv, ov), "w_st2": (cs, ot), "w_t2t2": (ct, ot), "w_vt2": (cv, ot),
+            "w_t2s": (ct, os_),
+        }
+        self._num_paths = 0
+        for name in PATH_NAMES:
+            i, o = spec[name]
+            if i > 0 and o > 0:
+                setattr(self, name, nn.Linear(i, o, bias=False))
+                self._num_paths += 1
+            else:
+                setattr(self, name, None)
+        if self.w_vt2 is not None:
+            self.register_buffer("cg_11_2", cg_11_2_cartesian())
+        else:
+            self.register_buffer("cg_11_2", None)
+        self.radial_basis = RadialBasis(num_basis=num_radial_basis, cutoff=radius, num_hidden=64,
+                                        num_output=max(self._num_paths, 1))
+        self.scalar_bias = nn.Parameter(torch.zeros(os_)) if os_ > 0 else None
+
+    def forward(self, scalars: Tensor, vectors: Tensor, graph, mask: Optional[Tensor] = None,
+                type2: Optional[Tensor] = None):
+        """(s_out [N, Cs_out], v_out [N, Cv_out, 3]) or with type-2 input and output also
+        t_out [N, Ct2_out, 5], in the input dtype (se3_conv.py:429-566)."""
+        N = graph.N
+        input_dtype = scalars.dtype
+        has_type2 = type2 is not None and self.out_type2_channels > 0
+        if graph.E == 0:
+            s_out = scalars.new_zeros(N, self.out_scalar_channels)
+            v_out = vectors.new_zeros(N, self.out_vector_channels, 3)
+            s_out = s_out + (scalars.sum() * 0).unsqueeze(0)
+            v_out = v_out + (vectors.sum() * 0).unsqueeze(0).unsqueeze(0)
+            if self.scalar_bias is not None:
+                s_out = s_out + self.scalar_bias
+            if has_type2:
+                return s_out, v_out, scalars.new_zeros(N, self.out_type2_channels, 5)
+            return s_out, v_out
+        with torch.autocast(scalars.device.type, enabled=False):
+            R = self.radial_basis(graph.dist.to(torch.float32))
+            weights = {k: (getattr(self, k).weight if getattr(self, k) is not None else None)
+                       for k in PATH_NAMES}
+            t_in = type2 if (type2 is not None and self.in_type2_channels > 0) else None
+            out = se3_message_aggregate(
+                scalars, vectors, graph, R, weights, self.out_scalar_channels,
+                self.out_vector_channels, self.out_type2_channels, type2=t_in,
+                cg_11_2=self.cg_11_2, bias=self.scalar_bias, mask=mask, return_type2=has_type2)
+        if has_type2:
+            s_out, v_out, t_out = out
+            return s_out.to(input_dtype), v_out.to(input_dtype), t_out.to(input_dtype)
+        s_out, v_out = out
+        return s_out.to(input_dtype), v_out.to(input_dtype)
+
+    def forward_legacy(self, pos: Tensor, scalars: Tensor, vectors: Tensor,
+                       batch: Optional[Tensor] = None, mask: Optional[Tensor] = None,
+                       edge_index: Optional[Tuple[Tensor, Tensor]] = None):
+        """Builds the graph from ``pos`` (or ``edge_index``) first (se3_conv.py:581-596)."""
+        from gdl_amd.graph import SpatialGraph
+        if edge_index is not None:
+            row, col = edge_index
+            graph = SpatialGraph.from_edge_index(row, col, pos, pos.shape[0])
+        else:
+            graph = SpatialGraph.build(pos, self.radius, max_num_neighbors=self.max_num_neighbors,
+                                       batch=batch, mask=mask)
+        return self.forward(scalars, vectors, graph, mask=mask)
+
+    def extra_repr(self) -> str:
+        return (f"scalar: {self.in_scalar_channels}→{self.out_scalar_channels}, "
+                f"vector: {self.in_vector_channels}→{self.out_vector_channels}, "
+                f"type2: {self.in_type2_channels}→{self.out_type2_channels}, "
+                f"radius={self.radius}, paths={self._num_paths}")

@@ -311,6 +311,91 @@ int geo_graph_avg_degree(const int64_t* row_ptr, int64_t N, const int64_t* batch
                          int64_t points_per_cloud, float* out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------ SE(3) message passing (fused aggregate) --- */
+/*
+ * The message computation and aggregation of SE3Conv.forward
+ * (geoembodied/nn/modules/se3_conv.py:61-235 `_compute_messages`, :482-566), reordered: each of
+ * the nine tensor-product paths is r_p(e) * W_p * x_p(e) with W_p shared by all edges, so the
+ * r-weighted source features are summed per target node first and the weights applied per node.
+ *
+ * geo_se3_aggregate_fwd: for each target n (edges p in [node_start[n], node_end[n]) of the CSR,
+ * edge perm[p], source row[edge]) writes the per-node sums (rows zero-padded to Ks / Kv / Kt):
+ *   Xs[n]    = [A0 (Cs) | A3 (Cv) | A8 (Ct)]
+ *   Xv[n][k] = [A1_k (Cs) | A2_k (Cv) | A4_k (Cv)]       k = x, y, z
+ *   Xt[n][m] = [A5_m (Cs) | A6_m (Ct) | A7_m (Cv)]       m = 0..4
+ * with A0 = sum r0 y0 s, A1_k = sum r1 d_k s, A2_k = sum r2 y0 v_k, A3 = sum r3 (d . v),
+ * A4 = sum r4 (d x v), A5_m = sum r5 y2_m s, A6_m = sum r6 y0 t_m,
+ * A7_m = sum r7 sum_ij d_i v_j cg[i][j][m], A8 = sum r8 |t|^2.  s [N, Cs], v [N, Cv, 3],
+ * t [N, Ct, 5] fp32; dir [E, 3]; Y [E, ysh] (y0 = Y[:, 0], y2 = Y[:, 4:9]); R [E, P];
+ * path_cols[9] (host array) = column of R of each path or -1 when the path is off (the
+ * reference's runtime path numbering); cg[45] (host array) = CG(1,1->2) in Cartesian order
+ * [3][3][5].  Xs / Xv / Xt may be NULL.
+ */
+int geo_se3_aggregate_fwd(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
+                          int32_t Cv, int32_t Ct, const int64_t* row, const int32_t* perm,
+                          const int32_t* node_start, const int32_t* node_end, int64_t E,
+                          const float* dir, const float* Y, int32_t ysh, const float* R, int32_t P,
+                          const int32_t* path_cols, const float* cg, float* Xs, int32_t Ks,
+                          float* Xv, int32_t Kv, float* Xt, int32_t Kt, void* stream);
+/*
+ * fp32 MFMA GEMM with the SE3Conv output epilogue (se3_conv.py:547-566): for r < M, o < O,
+ *   v = sum_k A[r, k] B[o, k];  v = v / avg[n] (avg may be NULL);  v += bias[o] (may be NULL);
+ *   v = 0 where mask[n] == 0 (mask may be NULL);  out[n * out_stride + o * G + g] = v,
+ * with n = r / G, g = r % G.  A [M, K] and B [B_rows, K] row-major, 16-byte aligned, K a multiple
+ * of 16; B_rows >= O rounded up to the launch's column tile (16, 32 or 64; zero rows past O).
+ */
+int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B, int32_t B_rows, int32_t O,
+                 int32_t G, float* out, int64_t out_stride, const float* avg, const float* bias,
+                 const uint8_t* mask, void* stream);
+/*
+ * Backward helpers.  geo_se3_grad_prep: out[n][g][o] (rows of Opad, zero padded) =
+ * grad[n][o][g] / avg[n], zero where mask[n] == 0.
+ * geo_se3_bwd_edge: per-edge gradients of R (dR [E, P], only the active paths' columns are
+ * written), of the direction (ddir [E, 3]) and of Y (dY [E, ysh]: columns 0 and 4..8) from the
+ * per-node gradient rows gX (same layouts as Xs / Xv / Xt) and the source features; each may be
+ * NULL.  geo_se3_bwd_src: for each source m over the CSR of the sources (col = target of each
+ * edge), sums of the prepared output gradients gs [N, OsP], gv [N][3][OvP], gt [N][5][OtP]:
+ *   Zs[m] = [Z0 (Os) | Z1 (Ov) | Z5 (Ot)], Zv[m][k] = [Z2_k (Ov) | Z3_k (Os) | Z4_k (Ov) | Z7_k (Ot)],
+ *   Zt[m][j] = Z6_j (Ot), Z8[m] (Os)
+ * (Z0 = sum r0 y0 gs, Z1 = sum r1 d . gv, Z5 = sum r5 y2 . gt, Z2_k = sum r2 y0 gv_k,
+ * Z3_k = sum r3 d_k gs, Z4 = sum r4 gv x d, Z7_j = sum r7 sum_im d_i cg[i][j][m] gt_m,
+ * Z6_j = sum r6 y0 gt_j, Z8 = sum r8 gs), from which the feature gradients are GEMMs with the
+ * transposed weights.
+ */
+int geo_se3_grad_prep(const float* grad, int64_t N, int32_t O, int32_t G, int32_t Opad,
+                      const float* avg, const uint8_t* mask, float* out, void* stream);
+int geo_se3_bwd_edge(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
+                     int32_t Cv, int32_t Ct, const int64_t* row, const int32_t* perm,
+                     const int32_t* node_start, const int32_t* node_end, int64_t E,
+                     const float* dir, const float* Y, int32_t ysh, const float* R, int32_t P,
+                     const int32_t* path_cols, const float* cg, const float* gXs, int32_t Ks,
+                     const float* gXv, int32_t Kv, const float* gXt, int32_t Kt, float* dR,
+                     float* ddir, float* dY, void* stream);
+int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const float* gv, int32_t Ov,
+                    int32_t OvP, const float* gt, int32_t Ot, int32_t OtP, int64_t N,
+                    const int64_t* col, const int32_t* perm, const int32_t* node_start,
+                    const int32_t* node_end, int64_t E, const float* dir, const float* Y,
+                    int32_t ysh, const float* R, int32_t P, const int32_t* path_cols,
+                    const float* cg, float* Zs, int32_t KZs, float* Zv, int32_t KZv, float* Zt,
+                    int32_t KZt, float* Z8, int32_t KZ8, void* stream);
+
+/*
+ * Radial basis MLP of SE3Conv (geoembodied/nn/modules/se3_conv.py:238-282), per edge length d:
+ *   x_i = sin(freqs[i] d) / max(d, 1e-8) * max(0.5 (1 + cos((pi d) / cutoff)), 0)   (i < NB)
+ *   R[e][p] = b2[p] + sum_j W2[p][j] silu(b1[j] + sum_i W1[j][i] x_i)          (j < H, p < P)
+ * fp32, NB <= 16, H <= 64, P <= 16; W1 [H][NB], W2 [P][H] row-major.  The backward writes
+ * d loss / d dist (d_dist, may be NULL) and the weight gradients (each may be NULL; written,
+ * not accumulated) from dR [E, P]; its workspace holds per-block partial sums.
+ */
+int geo_radial_mlp_fwd(const float* dist, int64_t E, const float* freqs, int32_t NB, float cutoff,
+                       const float* W1, const float* b1, int32_t H, const float* W2, const float* b2,
+                       int32_t P, float* R, void* stream);
+size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E);
+int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* freqs, int32_t NB, float cutoff,
+                       const float* W1, const float* b1, int32_t H, const float* W2, const float* b2,
+                       int32_t P, const float* dR, float* d_dist, float* dW1, float* db1, float* dW2,
+                       float* db2, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

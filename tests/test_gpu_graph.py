@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import oracle
+from sh_torch import sh_torch as _sh_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -21,20 +22,6 @@ def _f():
     from geoembodied.kernels.triton_sph_harm import spherical_harmonics
     from geoembodied.nn.modules.spatial_graph import SpatialGraph
     return spherical_harmonics, SpatialGraph
-
-
-def _sh_torch(v, max_l):
-    """The reference's PyTorch formula (triton_sph_harm.py:177-220) in float64, for autograd."""
-    import math
-    x, y, z = v[..., 0], v[..., 1], v[..., 2]
-    out = [torch.full_like(x, math.sqrt(1 / (4 * math.pi)))]
-    if max_l >= 1:
-        c1 = math.sqrt(3 / (4 * math.pi))
-        out += [c1 * y, c1 * z, c1 * x]
-    if max_l >= 2:
-        c20, c21, c22 = math.sqrt(5 / (16 * math.pi)), math.sqrt(15 / (4 * math.pi)), math.sqrt(15 / (16 * math.pi))
-        out += [c21 * x * y, c21 * y * z, c20 * (3 * z * z - 1), c21 * x * z, c22 * (x * x - y * y)]
-    return torch.stack(out, -1)
 
 
 @pytest.mark.parametrize("max_l", [0, 1, 2])

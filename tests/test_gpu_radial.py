@@ -1,0 +1,62 @@
+"""GPU: the fused radial basis MLP (forward and backward) against the float64 oracle
+(oracle/se3.py radial_basis, pinned by closed forms in test_oracle_se3.py).
+
+Bars: R within 1e-5 |R| + 1e-5 max|R|; gradients within 1e-4 relative + 1e-5 of the tensor's
+max (fp32 with sums over up to E edges for the weight gradients)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import se3 as ose3
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, want, rtol, arel):
+    got = got.detach().double().cpu().numpy()
+    want = want.detach().double().cpu().numpy()
+    scale = max(float(np.abs(want).max()) if want.size else 0.0, 1e-30)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=arel * scale)
+
+
+@pytest.mark.parametrize("E,NB,H,P", [(1000, 16, 64, 5), (70001, 16, 64, 9), (333, 8, 32, 1),
+                                      (16, 16, 64, 16), (5, 3, 7, 2)])
+def test_radial_mlp_vs_oracle(dev, E, NB, H, P):
+    from gdl_amd.se3_conv import radial_mlp
+    g = torch.Generator().manual_seed(E + P)
+    cutoff = 0.3
+    dist = torch.rand(E, generator=g) * cutoff * 1.1
+    dist[0] = 0.0
+    freqs = torch.arange(1, NB + 1, dtype=torch.float32) * math.pi / cutoff
+    W1 = torch.randn(H, NB, generator=g) / NB ** 0.5
+    b1 = torch.randn(H, generator=g) * 0.1
+    W2 = torch.randn(P, H, generator=g) / H ** 0.5
+    b2 = torch.randn(P, generator=g) * 0.1
+    leaves = {"d": dist, "W1": W1, "b1": b1, "W2": W2, "b2": b2}
+    gp = {k: v.to(dev).requires_grad_(True) for k, v in leaves.items()}
+    cp = {k: v.double().requires_grad_(True) for k, v in leaves.items()}
+    R = radial_mlp(gp["d"], freqs.to(dev), cutoff, gp["W1"], gp["b1"], gp["W2"], gp["b2"])
+    Rw = ose3.radial_basis(cp["d"], freqs, cutoff, cp["W1"], cp["b1"], cp["W2"], cp["b2"])
+    assert R.shape == (E, P)
+    _close(R, Rw, 1e-5, 1e-5)
+    c = torch.randn(E, P, generator=g, dtype=torch.float64)
+    (R * c.to(dev).float()).sum().backward()
+    (Rw * c).sum().backward()
+    for k in leaves:
+        _close(gp[k].grad, cp[k].grad, 1e-4, 1e-5)
+
+
+def test_radial_basis_module_matches_reference_formula(dev):
+    from gdl_amd.se3_conv import RadialBasis
+    torch.manual_seed(0)
+    rb = RadialBasis(num_basis=16, cutoff=0.5, num_hidden=64, num_output=5).to(dev)
+    d = torch.rand(4000, device=dev) * 0.6
+    R = rb(d)
+    l1, l2 = rb.mlp[0], rb.mlp[2]
+    want = ose3.radial_basis(d.cpu(), rb.freqs.cpu(), 0.5, l1.weight.cpu(), l1.bias.cpu(),
+                             l2.weight.cpu(), l2.bias.cpu())
+    _close(R, want, 1e-5, 1e-5)
+    assert rb(torch.empty(0, device=dev)).shape == (0, 5)

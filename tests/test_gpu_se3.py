@@ -1,0 +1,210 @@
+"""GPU: fused SE3Conv message passing against the float64 oracle (oracle/se3.py, pinned by closed
+forms and rotation equivariance in test_oracle_se3.py).
+
+Bars (fp32 arithmetic with the sums reordered: aggregate first, then the weights):
+  outputs     |got - want| <= 2e-4 |want| + 2e-5 max|want|
+  gradients   |got - want| <= 5e-4 |want| + 5e-5 max|want|     (per tensor)
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import se3 as ose3
+
+pytestmark = pytest.mark.gpu
+
+SPEC = lambda Cs, Cv, Ct, Os, Ov, Ot: {  # noqa: E731
+    "w_ss": (Os, Cs), "w_sv": (Ov, Cs), "w_vv_scalar": (Ov, Cv), "w_vs": (Os, Cv),
+    "w_vv_cross": (Ov, Cv), "w_st2": (Ot, Cs), "w_t2t2": (Ot, Ct), "w_vt2": (Ot, Cv), "w_t2s": (Os, Ct)}
+
+
+def _close(got, want, rtol, arel):
+    got = got.detach().double().cpu().numpy()
+    want = want.detach().double().cpu().numpy()
+    scale = max(float(np.abs(want).max()) if want.size else 0.0, 1e-30)
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=arel * scale)
+
+
+def test_gemm_kernel_vs_torch(dev):
+    from gdl_amd.se3_conv import _gemm, _pad64
+    g = torch.Generator().manual_seed(0)
+    for (N, G, K, O) in [(1000, 1, 80, 64), (333, 3, 96, 16), (257, 5, 48, 23), (64, 1, 16, 100)]:
+        A = torch.randn(N * G, K, generator=g)
+        B = torch.zeros(_pad64(O), K)
+        B[:O] = torch.randn(O, K, generator=g)
+        avg = torch.rand(N, generator=g) + 0.5
+        bias = torch.randn(O, generator=g) if G == 1 else None
+        mask = torch.rand(N, generator=g) > 0.3
+        out = torch.full((N, O, G), float("nan"), device=dev)
+        _gemm(A.to(dev), N * G, K, B.to(dev), O, G, out, O * G, avg.to(dev),
+              None if bias is None else bias.to(dev), mask.to(dev).view(torch.uint8))
+        want = (A.double() @ B[:O].double().t()).view(N, G, O).permute(0, 2, 1) / avg.double().view(N, 1, 1)
+        if bias is not None:
+            want = want + bias.double().view(1, O, 1)
+        want = want * mask.double().view(N, 1, 1)
+        _close(out, want, 1e-5, 1e-6)
+
+
+def _graph(N, B, r, K, seed, shuffle):
+    from gdl_amd.graph import SpatialGraph
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand(N * B, 3, generator=g)
+    batch = torch.arange(B).repeat_interleave(N)
+    gr = SpatialGraph.build(pos.cuda(), r, max_num_neighbors=K, batch=batch.cuda(), num_batch_elements=B)
+    if shuffle:
+        p = torch.randperm(gr.E, generator=g).cuda()
+        gr = SpatialGraph.from_edge_index(gr.row[p], gr.col[p], pos.cuda(), gr.N, batch=batch.cuda(),
+                                          num_batch_elements=B)
+    return gr
+
+
+CONFIGS = [
+    # Cs, Cv, Ct, Os, Ov, Ot, type2-in, type2-out
+    (8, 4, 0, 8, 4, 0),
+    (64, 16, 0, 64, 16, 0),
+    (80, 20, 6, 70, 10, 4),
+    (0, 4, 0, 3, 2, 0),
+    (5, 0, 2, 4, 0, 3),
+    (12, 6, 0, 10, 5, 3),      # type-2 output from scalars and vectors only
+]
+
+
+def _inputs(cfg, gr, seed, dev):
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    g = torch.Generator().manual_seed(seed)
+    N, E = gr.N, gr.E
+    s = torch.randn(N, Cs, generator=g)
+    v = torch.randn(N, Cv, 3, generator=g)
+    t = torch.randn(N, Ct, 5, generator=g) if Ct > 0 else None
+    W = {k: (torch.randn(*sh, generator=g) / max(sh[1], 1) ** 0.5 if sh[0] > 0 and sh[1] > 0 else None)
+         for k, sh in SPEC(*cfg).items()}
+    pc = ose3.path_columns(W, t is not None, True, Ot)
+    P = max(sum(1 for x in pc if x >= 0), 1) + 1          # one spare column, as in the module
+    R = torch.randn(E, P, generator=g)
+    bias = torch.randn(Os, generator=g) if Os > 0 else None
+    mask = torch.rand(N, generator=g) > 0.2
+    return s, v, t, W, R, bias, mask
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=[str(c) for c in CONFIGS])
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_forward_and_gradients_vs_oracle(dev, cfg, shuffle):
+    from gdl_amd.se3_conv import se3_message_aggregate
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    gr = _graph(300, 2, 0.22, 24, sum(cfg) + shuffle, shuffle)
+    s, v, t, W, R, bias, mask = _inputs(cfg, gr, 1 + shuffle, dev)
+    d = gr.direction.detach()
+    Y = gr.Y.detach()
+    leaves = {"s": s, "v": v, "R": R, "d": d.cpu(), "Y": Y.cpu()}
+    if t is not None:
+        leaves["t"] = t
+    if bias is not None:
+        leaves["bias"] = bias
+    for k, w in W.items():
+        if w is not None:
+            leaves[k] = w
+    gpu = {k: x.detach().to(dev).requires_grad_(True) for k, x in leaves.items()}
+    cpu = {k: x.detach().double().requires_grad_(True) for k, x in leaves.items()}
+
+    class G:  # the graph with differentiable direction / Y
+        pass
+    gg = G()
+    for k in ("row", "col", "perm", "node_start", "node_end", "avg_degree", "N", "E"):
+        setattr(gg, k, getattr(gr, k))
+    gg.direction, gg.Y = gpu["d"], gpu["Y"]
+    Wg = {k: gpu.get(k) for k in W}
+    outs = se3_message_aggregate(gpu["s"], gpu["v"], gg, gpu["R"], Wg, Os, Ov, Ot, type2=gpu.get("t"),
+                                 bias=gpu.get("bias"), mask=mask.to(dev), return_type2=True)
+    Wc = {k: cpu.get(k) for k in W}
+    want = ose3.se3_conv(cpu["s"], cpu["v"], cpu.get("t"), gr.row.cpu(), gr.col.cpu(), cpu["d"], cpu["Y"],
+                         cpu["R"], Wc, ose3.cg_11_2_cartesian(), Os, Ov, Ot, gr.avg_degree.cpu(),
+                         bias=cpu.get("bias"), mask=mask)
+    for o, w in zip(outs, want):
+        if w is None:
+            assert o is None or o.numel() == 0
+            continue
+        _close(o, w, 2e-4, 2e-5)
+    gen = torch.Generator().manual_seed(5)
+    loss_g, loss_c = 0, 0
+    for o, w in zip(outs, want):
+        if w is None or w.numel() == 0:
+            continue
+        c = torch.randn(w.shape, generator=gen, dtype=torch.float64)
+        loss_g = loss_g + (o * c.to(dev).float()).sum()
+        loss_c = loss_c + (w * c).sum()
+    loss_g.backward()
+    loss_c.backward()
+    for k in leaves:
+        wg = cpu[k].grad
+        gg_ = gpu[k].grad
+        if wg is None:
+            assert gg_ is None or float(gg_.abs().max()) == 0.0, k
+            continue
+        assert gg_ is not None, k
+        _close(gg_, wg, 5e-4, 5e-5)
+
+
+def test_se3conv_module_end_to_end(dev):
+    """The module on a SpatialGraph: outputs and parameter / feature / position gradients vs the
+    oracle fed with the module's own radial weights (float64 on the CPU)."""
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv
+    torch.manual_seed(0)
+    conv = SE3Conv(16, 8, 12, 6, in_type2_channels=4, out_type2_channels=3, radius=0.3).to(dev)
+    with torch.no_grad():
+        conv.scalar_bias.normal_()
+    g = torch.Generator().manual_seed(3)
+    pos = torch.rand(500, 3, generator=g)
+    s = torch.randn(500, 16, generator=g)
+    v = torch.randn(500, 8, 3, generator=g)
+    t = torch.randn(500, 4, 5, generator=g)
+    p_gpu = pos.to(dev).requires_grad_(True)
+    gr = SpatialGraph.build(p_gpu, 0.3, max_num_neighbors=20)
+    sg, vg, tg = (x.to(dev).requires_grad_(True) for x in (s, v, t))
+    out = conv(sg, vg, gr, type2=tg)
+    assert len(out) == 3
+    gen = torch.Generator().manual_seed(1)
+    cs = [torch.randn(o.shape, generator=gen) for o in out]
+    sum((o * c.to(dev)).sum() for o, c in zip(out, cs)).backward()
+
+    import copy
+    from sh_torch import sh_torch
+    ref = copy.deepcopy(conv).cpu().double()
+    ref.zero_grad(set_to_none=True)
+    p64 = pos.double().requires_grad_(True)
+    row, col = gr.row.cpu(), gr.col.cpu()
+    diff = p64[col] - p64[row]
+    dist = diff.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+    direction = diff / dist
+    Y = sh_torch(direction, 2)
+    rb = ref.radial_basis
+    R = ose3.radial_basis(dist.squeeze(-1), rb.freqs, rb.cutoff, rb.mlp[0].weight, rb.mlp[0].bias,
+                          rb.mlp[2].weight, rb.mlp[2].bias)
+    W = {k: (getattr(ref, k).weight if getattr(ref, k) is not None else None) for k in ose3.PATH_NAMES}
+    s64, v64, t64 = (x.double().requires_grad_(True) for x in (s, v, t))
+    want = ose3.se3_conv(s64, v64, t64, row, col, direction, Y, R, W, ref.cg_11_2, 12, 6, 3,
+                         gr.avg_degree.cpu(), bias=ref.scalar_bias)
+    for o, w in zip(out, want):
+        _close(o, w, 2e-4, 2e-5)
+    sum((w * c.double()).sum() for w, c in zip(want, cs)).backward()
+    for got, wnt in ((sg.grad, s64.grad), (vg.grad, v64.grad), (tg.grad, t64.grad), (p_gpu.grad, p64.grad)):
+        _close(got, wnt, 1e-3, 1e-4)
+    for (name, pg), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
+        assert pg.grad is not None, name
+        _close(pg.grad, pr.grad, 1e-3, 1e-4)
+
+
+def test_se3conv_empty_graph(dev):
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv
+    conv = SE3Conv(4, 2, 3, 2).to(dev)
+    with torch.no_grad():
+        conv.scalar_bias.fill_(0.5)
+    pos = torch.randn(20, 3, device=dev) * 100
+    gr = SpatialGraph.build(pos, 1e-3)
+    s = torch.randn(20, 4, device=dev, requires_grad=True)
+    so, vo = conv(s, torch.randn(20, 2, 3, device=dev), gr)
+    assert torch.equal(so, torch.full((20, 3), 0.5, device=dev)) and not vo.any()
+    so.sum().backward()
+    assert s.grad is not None and not s.grad.any()
