@@ -268,16 +268,27 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
   }
 }
 
+// Sum of the per-block partials, then scattered into the gradient tensors.  Each block sums 64
+// entries over all partial blocks with four thread groups (group g takes blocks b = g mod 4 in
+// order), then adds the four group sums in order: a fixed order, so results are deterministic.
 __global__ __launch_bounds__(kRbThreads) void radial_bwd_final(const float* __restrict__ part, int nblk,
                                                               int NB, int H, int P,
                                                               float* __restrict__ dW1,
                                                               float* __restrict__ db1,
                                                               float* __restrict__ dW2,
                                                               float* __restrict__ db2) {
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= kRbPart) return;
+  __shared__ float red[4][64];
+  const int kl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + kl;
   float s = 0.f;
-  for (int b = 0; b < nblk; ++b) s += part[static_cast<int64_t>(b) * kRbPart + k];
+  if (k < kRbPart) {
+#pragma unroll 8
+    for (int b = grp; b < nblk; b += 4) s += part[static_cast<int64_t>(b) * kRbPart + k];
+  }
+  red[grp][kl] = s;
+  __syncthreads();
+  if (grp != 0 || k >= kRbPart) return;
+  s = ((red[0][kl] + red[1][kl]) + red[2][kl]) + red[3][kl];
   if (k < 1024) {
     const int i = k / 64, j = k % 64;
     if (i < NB && j < H && dW1) dW1[j * NB + i] = s;
@@ -357,7 +368,7 @@ extern "C" int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* fre
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL(radial_bwd_kernel, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part);
   GEO_LAUNCH_CHECK("radial_bwd_kernel");
-  hipLaunchKernelGGL(radial_bwd_final, dim3(static_cast<unsigned>(ceil_div(kRbPart, kRbThreads))),
+  hipLaunchKernelGGL(radial_bwd_final, dim3(static_cast<unsigned>(ceil_div(kRbPart, 64))),
                      dim3(kRbThreads), 0, st, part, static_cast<int>(nblk), NB, H, P, dW1, db1, dW2, db2);
   GEO_LAUNCH_CHECK("radial_bwd_final");
   return GEO_OK;

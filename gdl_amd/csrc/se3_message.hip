@@ -151,18 +151,14 @@ __device__ __forceinline__ EdgeScalars edge_from(const EdgeScalars& st, int j) {
   return q;
 }
 
-// sum_ij d_i v_j cg[i][j][m]
-__device__ __forceinline__ void cg_dv(const float* cg, const float d[3], const float v[3],
-                                      float out[5]) {
+// D[j][m] = r * sum_i d_i cg[i][j][m]: path 7's per-edge coefficients, so that a lane's share
+// is sum_j v_j D[j][m] (forward) or sum_m D[j][m] w_m (source-side backward).
+__device__ __forceinline__ void cg_coef(const float* cg, const float d[3], float r, float D[3][5]) {
 #pragma unroll
-  for (int m = 0; m < 5; ++m) {
-    float a = 0.f;
+  for (int j = 0; j < 3; ++j)
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-#pragma unroll
-      for (int j = 0; j < 3; ++j) a += d[i] * v[j] * cg[(i * 3 + j) * 5 + m];
-    out[m] = a;
-  }
+    for (int m = 0; m < 5; ++m)
+      D[j][m] = r * ((d[0] * cg[j * 5 + m] + d[1] * cg[(3 + j) * 5 + m]) + d[2] * cg[(6 + j) * 5 + m]);
 }
 
 __device__ __forceinline__ void zero_pad(float* row, int used, int K) {
@@ -248,10 +244,10 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
               A4[2] += q.r[4] * (q.d[0] * v[1] - q.d[1] * v[0]);
             }
             if (g.pc[7] >= 0 && Xt) {
-              float tp[5];
-              cg_dv(g.cg, q.d, v, tp);
+              float D[3][5];
+              cg_coef(g.cg, q.d, q.r[7], D);
 #pragma unroll
-              for (int k = 0; k < 5; ++k) A7[k] += q.r[7] * tp[k];
+              for (int k = 0; k < 5; ++k) A7[k] += (D[0][k] * v[0] + D[1][k] * v[1]) + D[2][k] * v[2];
             }
           }
           if (ht) {
@@ -385,6 +381,108 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__
     }
 }
 
+// ------------------------------------------------------------ split-K transposed GEMM ---
+// out[o][k] = sum_r A[r * lda + o] * B[r * ldb + k] over r < M (o < O, k < K): the weight
+// gradients (output gradients x per-node aggregates, summed over nodes).  The reduction
+// dimension M is long and O, K are small, so the rows are split over the waves of the grid;
+// each wave accumulates its OB x KB tiles of 16 x 16 in MFMA accumulators (A^T as the MFMA A
+// operand, B as the B operand, k = rows) and writes them as one partial; se3_gemm_tn_final adds
+// the partials in a fixed order.
+template <int OB, int KB>
+__global__ __launch_bounds__(kSeThreads) void se3_gemm_tn(const float* __restrict__ A, int64_t M,
+                                                         int lda, int O,
+                                                         const float* __restrict__ B, int ldb,
+                                                         int K, int64_t rows_per_wave, int kb_groups,
+                                                         float* __restrict__ part, int Opad,
+                                                         int Kpad) {
+  const int lane = lane_id();
+  const int g = lane >> 4, li = lane & 15;
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  const int ob0 = (blockIdx.y / kb_groups) * OB, kb0 = (blockIdx.y % kb_groups) * KB;
+  const int64_t r_begin = wid * rows_per_wave;
+  const int64_t r_end = min(M, r_begin + rows_per_wave);
+  floatx4 acc[OB][KB];
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc[ob][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t r0 = r_begin; r0 < r_end; r0 += 16) {
+    float a[OB][4], b[KB][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t r = r0 + 4 * g + q;
+      const bool ok = r < r_end;
+#pragma unroll
+      for (int ob = 0; ob < OB; ++ob) {
+        const int o = 16 * (ob0 + ob) + li;
+        a[ob][q] = ok && o < O ? A[r * lda + o] : 0.f;
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int k = 16 * (kb0 + kb) + li;
+        b[kb][q] = ok && k < K ? B[r * ldb + k] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+          acc[ob][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ob][q], b[kb][q], acc[ob][kb], 0, 0, 0);
+  }
+  float* my = part + wid * static_cast<int64_t>(Opad) * Kpad;
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int o = 16 * (ob0 + ob) + 4 * g + q, k = 16 * (kb0 + kb) + li;
+        if (o < Opad && k < Kpad) my[static_cast<int64_t>(o) * Kpad + k] = acc[ob][kb][q];
+      }
+}
+
+__global__ __launch_bounds__(kSeThreads) void se3_gemm_tn_final(const float* __restrict__ part,
+                                                               int nparts, int Opad, int Kpad,
+                                                               int O, int K,
+                                                               float* __restrict__ out, int ldo) {
+  __shared__ float red[4][64];
+  const int kl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 64 + kl;
+  const int64_t n = static_cast<int64_t>(Opad) * Kpad;
+  float s = 0.f;
+  if (idx < n) {
+#pragma unroll 8
+    for (int b = grp; b < nparts; b += 4) s += part[b * n + idx];
+  }
+  red[grp][kl] = s;
+  __syncthreads();
+  if (grp != 0 || idx >= n) return;
+  const int o = static_cast<int>(idx / Kpad), k = static_cast<int>(idx % Kpad);
+  if (o < O && k < K) out[static_cast<int64_t>(o) * ldo + k] = ((red[0][kl] + red[1][kl]) + red[2][kl]) + red[3][kl];
+}
+
+struct TnPlan {
+  int ob, kb, kb_groups, groups, nparts_x;
+  int64_t rows_per_wave;
+};
+
+TnPlan tn_plan(int64_t M, int O, int K) {
+  TnPlan t;
+  const int nob = (O + 15) / 16, nkb = (K + 15) / 16;
+  t.ob = nob <= 1 ? 1 : (nob <= 2 ? 2 : 4);
+  const int kb = nkb < 8 ? nkb : 8;
+  t.kb = kb <= 2 ? 2 : (kb <= 4 ? 4 : (kb <= 6 ? 6 : 8));
+  t.kb_groups = (nkb + t.kb - 1) / t.kb;
+  t.groups = ((nob + t.ob - 1) / t.ob) * t.kb_groups;
+  int64_t blocks = ceil_div(M, 1024);
+  blocks = blocks < 1 ? 1 : (blocks > 128 ? 128 : blocks);
+  t.nparts_x = static_cast<int>(blocks);
+  t.rows_per_wave = ceil_div(ceil_div(M, blocks * kSeWaves), 16) * 16;
+  return t;
+}
+
 // ------------------------------------------------------------------ backward helpers ---
 // out[n][g][o] (row length Opad, zero padded) = in[n][o][g] / avg[n], zero where mask[n] == 0.
 __global__ __launch_bounds__(kSeThreads) void se3_grad_prep(const float* __restrict__ gin, int64_t N,
@@ -463,13 +561,13 @@ __device__ __forceinline__ float row_total(float v) {
 // c = cs0 + 4 li + u (u < 4), vector and type-2 input channels c = cv0 + li.
 struct GRow {
   float s0[4], s1[3][4], s5[5][4];
-  float v2[3], v3, v4[3], v7[5];
+  float v2[3], v3, v4[3], v7c[3][3];  // v7c[i][j] = sum_m cg[i][j][m] G7_m
   float t6[5], t8;
 };
 
-__device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, int64_t n, int h, int li,
-                                          const float* Gs, int Ks, const float* Gv, int Kv,
-                                          const float* Gt, int Kt) {
+__device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float* cg, int64_t n,
+                                          int h, int li, const float* Gs, int Ks, const float* Gv,
+                                          int Kv, const float* Gt, int Kt) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int c = 64 * h + 4 * li + u;
@@ -488,11 +586,19 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, int64_t n, i
     G.v4[k] = okv && Gv ? Gv[(n * 3 + k) * Kv + f.Cs + f.Cv + c] : 0.f;
   }
   G.v3 = okv && Gs ? Gs[n * Ks + f.Cs + c] : 0.f;
+  float v7[5];
 #pragma unroll
   for (int k = 0; k < 5; ++k) {
-    G.v7[k] = okv && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + f.Ct + c] : 0.f;
+    v7[k] = okv && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + f.Ct + c] : 0.f;
     G.t6[k] = okt && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + c] : 0.f;
   }
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float* cc = cg + (i * 3 + j) * 5;
+      G.v7c[i][j] = (((cc[0] * v7[0] + cc[1] * v7[1]) + cc[2] * v7[2]) + cc[3] * v7[3]) + cc[4] * v7[4];
+    }
   G.t8 = okt && Gs ? Gs[n * Ks + f.Cs + f.Cv + c] : 0.f;
 }
 
@@ -517,7 +623,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
   node_range(g, n, a, b);
   const int nch = ONE ? 1 : max((f.Cs + 63) / 64, max((f.Cv + 15) / 16, (f.Ct + 15) / 16));
   GRow G;
-  if (ONE) load_grow(G, f, n, 0, li, Gs, Ks, Gv, Kv, Gt, Kt);
+  if (ONE) load_grow(G, f, g.cg, n, 0, li, Gs, Ks, Gv, Kv, Gt, Kt);
   for (int base = a; base < b; base += kWave) {
     const int cnt = min(kWave, b - base);
     const EdgeScalars st = stage_edges(g, base, cnt, lane);
@@ -530,7 +636,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
 #pragma unroll
       for (int i = 0; i < 21; ++i) S[i] = 0.f;
       for (int h = 0; h < nch; ++h) {
-        if (!ONE) load_grow(G, f, n, h, li, Gs, Ks, Gv, Kv, Gt, Kt);
+        if (!ONE) load_grow(G, f, g.cg, n, h, li, Gs, Ks, Gv, Kv, Gt, Kt);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int c = 64 * h + 4 * li + u;
@@ -554,14 +660,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
           S[14] += v[2] * G.v4[0] - v[0] * G.v4[2];
           S[15] += v[0] * G.v4[1] - v[1] * G.v4[0];
 #pragma unroll
-          for (int i = 0; i < 3; ++i) {
-            float acc = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < 3; ++jj)
-#pragma unroll
-              for (int k = 0; k < 5; ++k) acc += v[jj] * g.cg[(i * 3 + jj) * 5 + k] * G.v7[k];
-            S[16 + i] += acc;
-          }
+          for (int i = 0; i < 3; ++i)
+            S[16 + i] += (v[0] * G.v7c[i][0] + v[1] * G.v7c[i][1]) + v[2] * G.v7c[i][2];
         }
         if (c < f.Ct) {
           const float* tp = f.t + (m * f.Ct + c) * 5;
@@ -650,15 +750,12 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
                             q.y2[4] * w[4]);
 #pragma unroll
             for (int k = 0; k < 5; ++k) z6[k] += q.r[6] * q.y0 * w[k];
+            float D[3][5];
+            cg_coef(g.cg, q.d, q.r[7], D);
 #pragma unroll
-            for (int jj = 0; jj < 3; ++jj) {
-              float acc = 0.f;
-#pragma unroll
-              for (int i = 0; i < 3; ++i)
-#pragma unroll
-                for (int k = 0; k < 5; ++k) acc += q.d[i] * g.cg[(i * 3 + jj) * 5 + k] * w[k];
-              z7[jj] += q.r[7] * acc;
-            }
+            for (int jj = 0; jj < 3; ++jj)
+              z7[jj] += (((D[jj][0] * w[0] + D[jj][1] * w[1]) + D[jj][2] * w[2]) + D[jj][3] * w[3]) +
+                        D[jj][4] * w[4];
           }
         }
       }
@@ -881,5 +978,46 @@ extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const f
                      dim3(kSeThreads), 0, as_stream(stream), g, gs, Os, OsP, gv, Ov, OvP, gt, Ot,
                      OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
   GEO_LAUNCH_CHECK("se3_bwd_src");
+  return GEO_OK;
+}
+
+extern "C" size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t K) {
+  if (M < 0 || O < 0 || K < 0) return 0;
+  const TnPlan t = tn_plan(M, O, K);
+  const int64_t Opad = ((O + 15) / 16) * 16, Kpad = ((K + 15) / 16) * 16;
+  return static_cast<size_t>(t.nparts_x) * kSeWaves * Opad * Kpad * sizeof(float);
+}
+
+extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B,
+                               int32_t ldb, int32_t K, float* out, int32_t ldo, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  GEO_REQUIRE(M >= 0 && O >= 0 && K >= 0 && lda >= O && ldb >= K && ldo >= K,
+              "se3_gemm_tn: bad sizes (M=%lld O=%d K=%d lda=%d ldb=%d ldo=%d)", (long long)M, O, K,
+              lda, ldb, ldo);
+  if (O == 0 || K == 0) return GEO_OK;
+  GEO_REQUIRE(out && (M == 0 || (A && B)), "se3_gemm_tn: null pointer");
+  const size_t need = geo_se3_gemm_tn_workspace_bytes(M, O, K);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(GEO_ERR_WORKSPACE, "se3_gemm_tn: workspace %zu bytes, need %zu",
+                     workspace_bytes, need);
+  const TnPlan t = tn_plan(M, O, K);
+  const int Opad = ((O + 15) / 16) * 16, Kpad = ((K + 15) / 16) * 16;
+  float* part = static_cast<float*>(workspace);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(t.nparts_x), static_cast<unsigned>(t.groups));
+#define GEO_TN(OB_, KB_)                                                                         \
+  if (t.ob == OB_ && t.kb == KB_)                                                                \
+    hipLaunchKernelGGL((se3_gemm_tn<OB_, KB_>), grid, dim3(kSeThreads), 0, st, A, M, lda, O, B, ldb, \
+                       K, t.rows_per_wave, t.kb_groups, part, Opad, Kpad);
+  GEO_TN(1, 2) GEO_TN(1, 4) GEO_TN(1, 6) GEO_TN(1, 8)
+  GEO_TN(2, 2) GEO_TN(2, 4) GEO_TN(2, 6) GEO_TN(2, 8)
+  GEO_TN(4, 2) GEO_TN(4, 4) GEO_TN(4, 6) GEO_TN(4, 8)
+#undef GEO_TN
+  GEO_LAUNCH_CHECK("se3_gemm_tn");
+  const int nparts = t.nparts_x * kSeWaves;
+  hipLaunchKernelGGL(se3_gemm_tn_final,
+                     dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(Opad) * Kpad, 64))),
+                     dim3(kSeThreads), 0, st, part, nparts, Opad, Kpad, O, K, out, ldo);
+  GEO_LAUNCH_CHECK("se3_gemm_tn_final");
   return GEO_OK;
 }

@@ -251,19 +251,18 @@ class _SE3MessageAggregate(torch.autograd.Function):
 
         # weight gradients: sums over nodes of (prepared output gradient) x (per-node aggregate)
         dW = [None] * 9
-        if Gs is not None and any(need[12 + i] for i in (0, 3, 8)):
-            m = Gs.view(N, p.OsP)[:, :Os].t() @ Xs[:, :Cs + Cv + Ct]
-            for i, a, b in ((0, 0, Cs), (3, Cs, Cs + Cv), (8, Cs + Cv, Cs + Cv + Ct)):
-                if p.pc[i] >= 0:
-                    dW[i] = m[:, a:b]
-        if Gv is not None and any(need[12 + i] for i in (1, 2, 4)):
-            m = Gv.view(3 * N, p.OvP)[:, :Ov].t() @ Xv.view(3 * N, p.Kv)[:, :Cs + 2 * Cv]
-            for i, a, b in ((1, 0, Cs), (2, Cs, Cs + Cv), (4, Cs + Cv, Cs + 2 * Cv)):
-                if p.pc[i] >= 0:
-                    dW[i] = m[:, a:b]
-        if Gt is not None and any(need[12 + i] for i in (5, 6, 7)):
-            m = Gt.view(5 * N, p.OtP)[:, :Ot].t() @ Xt.view(5 * N, p.Kt)[:, :Cs + Ct + Cv]
-            for i, a, b in ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)):
+        for Gm, Xm, rows, OP, O_, KX, width, parts in (
+                (Gs, Xs, N, p.OsP, Os, p.Ks, Cs + Cv + Ct, ((0, 0, Cs), (3, Cs, Cs + Cv), (8, Cs + Cv, Cs + Cv + Ct))),
+                (Gv, Xv, 3 * N, p.OvP, Ov, p.Kv, Cs + 2 * Cv, ((1, 0, Cs), (2, Cs, Cs + Cv), (4, Cs + Cv, Cs + 2 * Cv))),
+                (Gt, Xt, 5 * N, p.OtP, Ot, p.Kt, Cs + Ct + Cv, ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)))):
+            if Gm is None or not any(need[12 + i] and p.pc[i] >= 0 for i, _, _ in parts) or width == 0:
+                continue
+            m = torch.empty(O_, width, **f32)
+            nbytes = L.geo_se3_gemm_tn_workspace_bytes(rows, O_, width)
+            ws = _nat.workspace(nbytes, dev)
+            _nat.check(L.geo_se3_gemm_tn(_nat.ptr(Gm), rows, OP, O_, _nat.ptr(Xm), KX, width, _nat.ptr(m),
+                                         width, _nat.ptr(ws), nbytes, st), "geo_se3_gemm_tn")
+            for i, a, b in parts:
                 if p.pc[i] >= 0:
                     dW[i] = m[:, a:b]
         dbias = None

@@ -362,6 +362,15 @@ int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B, int32_t B
  * Z6_j = sum r6 y0 gt_j, Z8 = sum r8 gs), from which the feature gradients are GEMMs with the
  * transposed weights.
  */
+/*
+ * Weight gradients as one long reduction: out[o * ldo + k] = sum_{r < M} A[r * lda + o] *
+ * B[r * ldb + k] for o < O, k < K (fp32 MFMA, rows split over the grid, per-wave partials in the
+ * workspace added in a fixed order).
+ */
+size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t K);
+int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B, int32_t ldb,
+                    int32_t K, float* out, int32_t ldo, void* workspace, size_t workspace_bytes,
+                    void* stream);
 int geo_se3_grad_prep(const float* grad, int64_t N, int32_t O, int32_t G, int32_t Opad,
                       const float* avg, const uint8_t* mask, float* out, void* stream);
 int geo_se3_bwd_edge(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
