@@ -136,6 +136,33 @@ def make_c5():
 # ═══════════════════════════════════════════════════════════════════
 
 
+def _se3_reference_torch(conv, s, v, gr):
+    """SE3Conv.forward as the reference computes it (se3_conv.py:61-235, :482-566: radial MLP
+    in PyTorch ops, per-edge messages of paths 0-4 from gathered source features, concatenation,
+    segment sum over the target CSR, division by the average degree, bias), on the same GPU;
+    the segment sum is this library's kernel, so the comparison isolates the fusion."""
+    from geoembodied.functional.segment_reduce import segment_reduce
+    rb = conv.radial_basis
+    d = gr.dist.unsqueeze(-1)
+    basis = torch.sin(rb.freqs * d) / d.clamp(min=1e-8)
+    env = (0.5 * (1.0 + torch.cos(math.pi * gr.dist / rb.cutoff))).clamp(min=0.0).unsqueeze(-1)
+    R = rb.mlp(basis * env)
+    s_src, v_src = s[gr.row], v[gr.row]
+    y0, dr = gr.Y[:, 0:1], gr.direction
+    sm = R[:, 0:1] * y0 * (s_src @ conv.w_ss.weight.t())
+    vm = (R[:, 1:2] * (s_src @ conv.w_sv.weight.t())).unsqueeze(-1) * dr.unsqueeze(-2)
+    mixed = (v_src.transpose(-1, -2) @ conv.w_vv_scalar.weight.t()).transpose(-1, -2)
+    vm = vm + R[:, 2:3].unsqueeze(-1) * y0.unsqueeze(-1) * mixed
+    dot = (dr.unsqueeze(-2) * v_src).sum(-1)
+    sm = sm + R[:, 3:4] * (dot @ conv.w_vs.weight.t())
+    cross = torch.linalg.cross(dr.unsqueeze(-2).expand_as(v_src), v_src, dim=-1)
+    vm = vm + R[:, 4:5].unsqueeze(-1) * (cross.transpose(-1, -2) @ conv.w_vv_cross.weight.t()).transpose(-1, -2)
+    msg = torch.cat([sm, vm.reshape(gr.E, -1)], dim=-1)
+    out = segment_reduce(msg, gr.col_sorted, gr.perm, gr.node_start, gr.node_end, gr.N)
+    out = out / gr.avg_degree.unsqueeze(1)
+    return out[:, :64] + conv.scalar_bias, out[:, 64:].reshape(gr.N, 16, 3)
+
+
 def wall_ms(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
@@ -255,6 +282,39 @@ def main() -> int:
                                        num_batch_elements=c2["B"]), args.steps, 3)
         log(f"  SpatialGraph.build: {legs['c2_spatial_graph_ms']:.3f} ms "
             f"(radius graph alone {legs['c2_radius_ms']:.3f} ms)")
+        # one SE3Conv layer (64 scalar + 16 vector channels in and out, paths 0-4) on the C2 graph:
+        # fused message passing vs the reference's op sequence in PyTorch on the same GPU
+        from gdl_amd.se3_conv import SE3Conv
+        gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                num_batch_elements=c2["B"])
+        torch.manual_seed(0)
+        conv = SE3Conv(64, 16, 64, 16, radius=c2["r"]).to(dev)
+        fs = torch.randn(gr.N, 64, device=dev, requires_grad=True)
+        fv = torch.randn(gr.N, 16, 3, device=dev, requires_grad=True)
+
+        def se3_fwd():
+            with torch.no_grad():
+                return conv(fs, fv, gr)
+
+        def se3_fb():
+            so, vo = conv(fs, fv, gr)
+            torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
+
+        def ref_fwd():
+            with torch.no_grad():
+                return _se3_reference_torch(conv, fs, fv, gr)
+
+        def ref_fb():
+            so, vo = _se3_reference_torch(conv, fs, fv, gr)
+            torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
+
+        legs["c2_se3conv_fwd_ms"] = wall_ms(se3_fwd, args.steps, 3)
+        legs["c2_se3conv_fwd_bwd_ms"] = wall_ms(se3_fb, args.steps, 3)
+        legs["c2_se3conv_torch_ref_fwd_ms"] = wall_ms(ref_fwd, args.steps, 3)
+        legs["c2_se3conv_torch_ref_fwd_bwd_ms"] = wall_ms(ref_fb, args.steps, 3)
+        log(f"  SE3Conv 64s+16v (E={gr.E}): fused {legs['c2_se3conv_fwd_ms']:.3f} ms fwd, "
+            f"{legs['c2_se3conv_fwd_bwd_ms']:.3f} ms fwd+bwd; reference op sequence in PyTorch "
+            f"{legs['c2_se3conv_torch_ref_fwd_ms']:.3f} / {legs['c2_se3conv_torch_ref_fwd_bwd_ms']:.3f} ms")
 
     # ---------------------------------------------------------------- C3 roofline ---
     roof = None
