@@ -7,9 +7,10 @@ names, so ``from geoembodied.functional.segment_reduce import segment_reduce``
 (nn/modules/se3_conv.py:39), ``from geoembodied.csrc import fps_cuda``
 (nn/modules/equivariant_pool.py:261) and ``from geoembodied.kernels.triton_sph_harm import
 spherical_harmonics`` (nn/modules/spatial_graph.py:37) resolve to the gfx950 implementation.
-``geoembodied.nn.modules.spatial_graph`` is the graph container of ``gdl_amd.graph``; the rest
-of the reference's ``nn`` package (the layers and models) is not part of this build, so
-``geoembodied.nn`` holds only that module.
+``geoembodied.nn.modules.spatial_graph`` is the graph container of ``gdl_amd.graph`` and
+``geoembodied.nn.modules.se3_conv`` the fused convolution of ``gdl_amd.se3_conv``; the rest of
+the reference's ``nn`` package (the other layers and the models) is not part of this build, so
+``geoembodied.nn`` holds only those two modules.
 """
 
 import importlib
@@ -39,6 +40,7 @@ for _name in _ALIASES:
 _RENAMED = (
     ("kernels.triton_sph_harm", "gdl_amd.kernels.sph_harm"),
     ("nn.modules.spatial_graph", "gdl_amd.graph"),
+    ("nn.modules.se3_conv", "gdl_amd.se3_conv"),
 )
 for _name, _target in _RENAMED:
     _parts = _name.split(".")
