@@ -79,7 +79,12 @@ __device__ __forceinline__ float basis(float f, float d, float env, float denv, 
   return b * env;
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
+// Logistic sigmoid 1 / (1 + e^-z) from the hardware exp2 and reciprocal (each within 1 ulp):
+// saturates to 0 / 1 for large |z| like the exact function.
+__device__ __forceinline__ float sigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * 1.4426950408889634f));
+}
+__device__ __forceinline__ float silu(float z) { return z * sigmoid(z); }
 
 __global__ __launch_bounds__(kRbThreads) void radial_fwd_kernel(RbParams p, float* __restrict__ R) {
   const int lane = lane_id();
@@ -136,11 +141,12 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
                                                                float* __restrict__ ddist,
                                                                float* __restrict__ part) {
   __shared__ float tz[kRbWaves][16][kRbMaxHidden + 1];   // dZ of 16 edges, per wave
+  __shared__ float tx[kRbWaves][16][17];                  // X of 16 edges x 16 basis, per wave
   __shared__ float red[kRbWaves][kRbPart];
   const int lane = lane_id();
   const int g = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  float fr[4], frl;
+  float fr[4];
   float w1[4][4], w2b[4][4], w1t[4][4], b1z[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -155,7 +161,6 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
       w1t[jb][q] = (jj < p.H && li < p.NB) ? p.W1[jj * p.NB + li] : 0.f;  // A of dX^T = W1^T dZ^T
     }
   }
-  frl = li < p.NB ? p.freqs[li] : 0.f;
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) b1z[jb] = 16 * jb + li < p.H ? p.b1[16 * jb + li] : 0.f;
   floatx4 aw1[4], aw2[4];
@@ -181,20 +186,22 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
       if (i >= p.NB) dxa[q] = 0.f;
       dra[q] = (oka && i < p.P) ? dR[ea * p.P + i] : 0.f;
     }
-    // edges 4g + q: x_li (A of dW1^T) and dR[e][li] (A of dW2)
+    // edges 4g + q: x_li (A of dW1^T, the transpose of xa through LDS) and dR[e][li] (A of dW2)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) tx[wave][li][4 * g + q] = oka ? xa[q] : 0.f;
     float xb[4], drb[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t eb = e0 + 4 * g + q;
       const bool okb = eb < p.E;
-      const float db = okb ? p.dist[eb] : 1.f;
-      float envb, denvb;
-      envelope(db, p.cutoff, envb, denvb);
-      xb[q] = (okb && li < p.NB) ? basis(frl, db, envb, denvb, nullptr) : 0.f;
       drb[q] = (okb && li < p.P) ? dR[eb * p.P + li] : 0.f;
       db2p += drb[q];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xb[q] = tx[wave][4 * g + q][li];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       floatx4 z = {0.f, 0.f, 0.f, 0.f}, dh = {0.f, 0.f, 0.f, 0.f};
@@ -207,7 +214,7 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const float zz = z[q] + b1z[jb];
-        const float sg = 1.0f / (1.0f + expf(-zz));
+        const float sg = sigmoid(zz);
         h[q] = zz * sg;
         dz[q] = dh[q] * (sg * (1.0f + zz * (1.0f - sg)));  // silu'(z) = s (1 + z (1 - s))
         db1p[jb] += dz[q];

@@ -31,6 +31,11 @@
 // give the feature gradients.
 #include "common.hpp"
 
+// The library is built with -ffp-contract=off because the geometry kernels must round like the
+// reference's distance expressions.  These sums are compared within a tolerance instead, so here
+// a multiply feeding an add may be fused (one rounding instead of two).
+#pragma clang fp contract(fast)
+
 namespace geo {
 namespace {
 
@@ -178,6 +183,7 @@ constexpr int kSeUnroll = 4;  // edges whose source rows are in flight together
 // One wave per target node, lanes over input channels (chunks of 64).  The node's edges are
 // staged in lanes, then walked four at a time: the four source rows are loaded first, then
 // accumulated in CSR order.
+template <bool T2>  // T2: type-2 features or outputs present (else their paths compile out)
 __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFeat f,
                                                                float* __restrict__ Xs, int Ks,
                                                                float* __restrict__ Xv, int Kv,
@@ -190,7 +196,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
   const int cmax = max(f.Cs, max(f.Cv, f.Ct));
   for (int c0 = 0; c0 < cmax; c0 += kWave) {
     const int c = c0 + lane;
-    const bool hs = c < f.Cs, hv = c < f.Cv, ht = c < f.Ct;
+    const bool hs = c < f.Cs, hv = c < f.Cv, ht = T2 && c < f.Ct;
     float A0 = 0.f, A1[3] = {0.f, 0.f, 0.f}, A5[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
     float A2[3] = {0.f, 0.f, 0.f}, A3 = 0.f, A4[3] = {0.f, 0.f, 0.f};
     float A7[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A6[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A8 = 0.f;
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
 #pragma unroll
               for (int k = 0; k < 3; ++k) A1[k] += q.r[1] * q.d[k] * x;
             }
-            if (g.pc[5] >= 0) {
+            if (T2 && g.pc[5] >= 0) {
 #pragma unroll
               for (int k = 0; k < 5; ++k) A5[k] += q.r[5] * q.y2[k] * x;
             }
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
               A4[1] += q.r[4] * (q.d[2] * v[0] - q.d[0] * v[2]);
               A4[2] += q.r[4] * (q.d[0] * v[1] - q.d[1] * v[0]);
             }
-            if (g.pc[7] >= 0 && Xt) {
+            if (T2 && g.pc[7] >= 0 && Xt) {
               float D[3][5];
               cg_coef(g.cg, q.d, q.r[7], D);
 #pragma unroll
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
         if (hv) row[f.Cs + f.Cv + c] = A4[k];
       }
     }
-    if (Xt) {
+    if (T2 && Xt) {
 #pragma unroll
       for (int k = 0; k < 5; ++k) {
         float* row = Xt + (n * 5 + k) * Kt;
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
   if (Xs) zero_pad(Xs + n * Ks, f.Cs + f.Cv + f.Ct, Ks);
   if (Xv)
     for (int k = 0; k < 3; ++k) zero_pad(Xv + (n * 3 + k) * Kv, f.Cs + 2 * f.Cv, Kv);
-  if (Xt)
+  if (T2 && Xt)
     for (int k = 0; k < 5; ++k) zero_pad(Xt + (n * 5 + k) * Kt, f.Cs + f.Ct + f.Cv, Kt);
 }
 
@@ -565,6 +571,7 @@ struct GRow {
   float t6[5], t8;
 };
 
+template <bool T2>
 __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float* cg, int64_t n,
                                           int h, int li, const float* Gs, int Ks, const float* Gv,
                                           int Kv, const float* Gt, int Kt) {
@@ -576,10 +583,10 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float*
 #pragma unroll
     for (int k = 0; k < 3; ++k) G.s1[k][u] = ok && Gv ? Gv[(n * 3 + k) * Kv + c] : 0.f;
 #pragma unroll
-    for (int k = 0; k < 5; ++k) G.s5[k][u] = ok && Gt ? Gt[(n * 5 + k) * Kt + c] : 0.f;
+    for (int k = 0; k < 5; ++k) G.s5[k][u] = T2 && ok && Gt ? Gt[(n * 5 + k) * Kt + c] : 0.f;
   }
   const int c = 16 * h + li;
-  const bool okv = c < f.Cv, okt = c < f.Ct;
+  const bool okv = c < f.Cv, okt = T2 && c < f.Ct;
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
     G.v2[k] = okv && Gv ? Gv[(n * 3 + k) * Kv + f.Cs + c] : 0.f;
@@ -589,7 +596,7 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float*
   float v7[5];
 #pragma unroll
   for (int k = 0; k < 5; ++k) {
-    v7[k] = okv && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + f.Ct + c] : 0.f;
+    v7[k] = T2 && okv && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + f.Ct + c] : 0.f;
     G.t6[k] = okt && Gt ? Gt[(n * 5 + k) * Kt + f.Cs + c] : 0.f;
   }
 #pragma unroll
@@ -607,7 +614,7 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float*
 // (64 scalar channels as 4 per lane, 16 vector / type-2 channels as 1 per lane, per chunk), and
 // the 21 per-edge sums are reduced within the row.  With one chunk (ONE) the target's gradient
 // row stays in registers for all of its edges.
-template <bool ONE>
+template <bool ONE, bool T2>
 __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
                                                           const float* __restrict__ Gs, int Ks,
                                                           const float* __restrict__ Gv, int Kv,
@@ -623,7 +630,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
   node_range(g, n, a, b);
   const int nch = ONE ? 1 : max((f.Cs + 63) / 64, max((f.Cv + 15) / 16, (f.Ct + 15) / 16));
   GRow G;
-  if (ONE) load_grow(G, f, g.cg, n, 0, li, Gs, Ks, Gv, Kv, Gt, Kt);
+  if (ONE) load_grow<T2>(G, f, g.cg, n, 0, li, Gs, Ks, Gv, Kv, Gt, Kt);
   for (int base = a; base < b; base += kWave) {
     const int cnt = min(kWave, b - base);
     const EdgeScalars st = stage_edges(g, base, cnt, lane);
@@ -636,7 +643,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
 #pragma unroll
       for (int i = 0; i < 21; ++i) S[i] = 0.f;
       for (int h = 0; h < nch; ++h) {
-        if (!ONE) load_grow(G, f, g.cg, n, h, li, Gs, Ks, Gv, Kv, Gt, Kt);
+        if (!ONE) load_grow<T2>(G, f, g.cg, n, h, li, Gs, Ks, Gv, Kv, Gt, Kt);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int c = 64 * h + 4 * li + u;
@@ -646,7 +653,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
 #pragma unroll
             for (int k = 0; k < 3; ++k) S[1 + k] += G.s1[k][u] * x;
 #pragma unroll
-            for (int k = 0; k < 5; ++k) S[4 + k] += G.s5[k][u] * x;
+            for (int k = 0; k < 5; ++k)
+              if (T2) S[4 + k] += G.s5[k][u] * x;
           }
         }
         const int c = 16 * h + li;
@@ -659,11 +667,13 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
           S[13] += v[1] * G.v4[2] - v[2] * G.v4[1];  // v x G4
           S[14] += v[2] * G.v4[0] - v[0] * G.v4[2];
           S[15] += v[0] * G.v4[1] - v[1] * G.v4[0];
+          if (T2) {
 #pragma unroll
-          for (int i = 0; i < 3; ++i)
-            S[16 + i] += (v[0] * G.v7c[i][0] + v[1] * G.v7c[i][1]) + v[2] * G.v7c[i][2];
+            for (int i = 0; i < 3; ++i)
+              S[16 + i] += (v[0] * G.v7c[i][0] + v[1] * G.v7c[i][1]) + v[2] * G.v7c[i][2];
+          }
         }
-        if (c < f.Ct) {
+        if (T2 && c < f.Ct) {
           const float* tp = f.t + (m * f.Ct + c) * 5;
           const float t[5] = {tp[0], tp[1], tp[2], tp[3], tp[4]};
           S[19] += (((G.t6[0] * t[0] + G.t6[1] * t[1]) + G.t6[2] * t[2]) + G.t6[3] * t[3]) + G.t6[4] * t[4];
@@ -671,7 +681,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
         }
       }
 #pragma unroll
-      for (int i = 0; i < 21; ++i) S[i] = row_total(S[i]);
+      for (int i = 0; i < 21; ++i)
+        if (T2 || i < 4 || (i >= 9 && i < 16)) S[i] = row_total(S[i]);
       if (li == 0 && ok) write_edge_grads(g, q, S, dR, ddir, dY);
     }
   }
@@ -684,6 +695,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
 //   Zt[m][j] = [Z6_j (Ot)]                                   -> dt = Zt W6 + 2 t (Z8 W8)
 //   Z8[m]    = [Z8 (Os)]
 // with gs [N, Os], gv [N][3][Ov], gt [N][5][Ot] the prepared output gradients.
+template <bool T2>
 __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float* __restrict__ gs,
                                                          int Os, int OsP,
                                                          const float* __restrict__ gv, int Ov,
@@ -700,7 +712,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
   const int omax = max(Os, max(Ov, Ot));
   for (int o0 = 0; o0 < omax; o0 += kWave) {
     const int o = o0 + lane;
-    const bool hs = o < Os && gs, hv = o < Ov && gv, ht = o < Ot && gt;
+    const bool hs = o < Os && gs, hv = o < Ov && gv, ht = T2 && o < Ot && gt;
     float z0 = 0.f, z1 = 0.f, z5 = 0.f, z8 = 0.f;
     float z2[3] = {0.f, 0.f, 0.f}, z3[3] = {0.f, 0.f, 0.f}, z4[3] = {0.f, 0.f, 0.f};
     float z7[3] = {0.f, 0.f, 0.f}, z6[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
@@ -875,8 +887,15 @@ extern "C" int geo_se3_aggregate_fwd(const float* s, const float* v, const float
               "se3_aggregate_fwd: null graph array");
   SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
   SeFeat f{s, v, t, Cs, Cv, Ct};
-  hipLaunchKernelGGL(se3_fwd_aggregate, dim3(static_cast<unsigned>(ceil_div(N, kSeWaves))),
-                     dim3(kSeThreads), 0, as_stream(stream), g, f, Xs, Ks, Xv, Kv, Xt, Kt);
+  const bool t2 = Ct > 0 || Xt != nullptr || path_cols[5] >= 0 || path_cols[6] >= 0 ||
+                  path_cols[7] >= 0 || path_cols[8] >= 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kSeWaves)));
+  if (t2)
+    hipLaunchKernelGGL(se3_fwd_aggregate<true>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f,
+                       Xs, Ks, Xv, Kv, Xt, Kt);
+  else
+    hipLaunchKernelGGL(se3_fwd_aggregate<false>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f,
+                       Xs, Ks, Xv, Kv, Xt, Kt);
   GEO_LAUNCH_CHECK("se3_fwd_aggregate");
   return GEO_OK;
 }
@@ -943,13 +962,18 @@ extern "C" int geo_se3_bwd_edge(const float* s, const float* v, const float* t, 
   SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
   SeFeat f{s, v, t, Cs, Cv, Ct};
   const bool one = Cs <= 64 && Cv <= 16 && Ct <= 16;
+  const bool t2 = Ct > 0 || gXt != nullptr || path_cols[5] >= 0 || path_cols[6] >= 0 ||
+                  path_cols[7] >= 0 || path_cols[8] >= 0;
   const dim3 grid(static_cast<unsigned>(ceil_div(N, kSeWaves)));
-  if (one)
-    hipLaunchKernelGGL(se3_bwd_edge<true>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f, gXs,
-                       Ks, gXv, Kv, gXt, Kt, dR, ddir, dY);
-  else
-    hipLaunchKernelGGL(se3_bwd_edge<false>, grid, dim3(kSeThreads), 0, as_stream(stream), g, f, gXs,
-                       Ks, gXv, Kv, gXt, Kt, dR, ddir, dY);
+  hipStream_t st = as_stream(stream);
+#define GEO_BWD_EDGE(ONE_, T2_)                                                                    \
+  hipLaunchKernelGGL((se3_bwd_edge<ONE_, T2_>), grid, dim3(kSeThreads), 0, st, g, f, gXs, Ks, gXv, Kv, \
+                     gXt, Kt, dR, ddir, dY)
+  if (one && t2) GEO_BWD_EDGE(true, true);
+  else if (one) GEO_BWD_EDGE(true, false);
+  else if (t2) GEO_BWD_EDGE(false, true);
+  else GEO_BWD_EDGE(false, false);
+#undef GEO_BWD_EDGE
   GEO_LAUNCH_CHECK("se3_bwd_edge");
   return GEO_OK;
 }
@@ -974,9 +998,13 @@ extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const f
   GEO_REQUIRE(node_start && node_end && (E == 0 || (col && dir && Y && R)),
               "se3_bwd_src: null graph array");
   SeEdges g = make_edges(col, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
-  hipLaunchKernelGGL(se3_bwd_src, dim3(static_cast<unsigned>(ceil_div(N, kSeWaves))),
-                     dim3(kSeThreads), 0, as_stream(stream), g, gs, Os, OsP, gv, Ov, OvP, gt, Ot,
-                     OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kSeWaves)));
+  if (gt != nullptr && Ot > 0)
+    hipLaunchKernelGGL(se3_bwd_src<true>, grid, dim3(kSeThreads), 0, as_stream(stream), g, gs, Os,
+                       OsP, gv, Ov, OvP, gt, Ot, OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
+  else
+    hipLaunchKernelGGL(se3_bwd_src<false>, grid, dim3(kSeThreads), 0, as_stream(stream), g, gs, Os,
+                       OsP, gv, Ov, OvP, gt, Ot, OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
   GEO_LAUNCH_CHECK("se3_bwd_src");
   return GEO_OK;
 }
