@@ -408,7 +408,8 @@ def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tenso
     """Radial weights [E, P] of edge lengths ``dist`` [E] (fp32, on the GPU; num_basis <= 16,
     hidden <= 64, outputs <= 16), differentiable with respect to dist and the four weights."""
     _require_gpu("radial_mlp", dist)
-    return _RadialMLP.apply(dist, freqs, cutoff, W1, b1, W2, b2)
+    f = torch.float32
+    return _RadialMLP.apply(dist.to(f), freqs.to(f), cutoff, W1.to(f), b1.to(f), W2.to(f), b2.to(f))
 
 
 class RadialBasis(nn.Module):

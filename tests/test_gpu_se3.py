@@ -208,3 +208,75 @@ def test_se3conv_empty_graph(dev):
     assert torch.equal(so, torch.full((20, 3), 0.5, device=dev)) and not vo.any()
     so.sum().backward()
     assert s.grad is not None and not s.grad.any()
+
+
+def _rot(seed):
+    q, _ = np.linalg.qr(np.random.default_rng(seed).normal(size=(3, 3)))
+    return q * np.sign(np.linalg.det(q))
+
+
+def _wigner_d2(Q):
+    import oracle
+    u = np.random.default_rng(7).normal(size=(64, 3))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    A = oracle.spherical_harmonics(u, 2, False)[:, 4:9]
+    B = oracle.spherical_harmonics(u @ Q.T, 2, False)[:, 4:9]
+    D, *_ = np.linalg.lstsq(A, B, rcond=None)
+    return D.T
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_se3conv_rotation_equivariance(dev, seed):
+    """f(R x) = R . f(x) for all three feature types (the reference's SE3Conv equivariance test,
+    tests/test_se3conv_equivariance.py:186-300, with type-2 features added): the same edge set is
+    used for both poses so that no edge flips at the radius boundary."""
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv
+    torch.manual_seed(seed)
+    conv = SE3Conv(8, 4, 6, 5, in_type2_channels=3, out_type2_channels=2, radius=0.4).to(dev)
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand(400, 3, generator=g)
+    s = torch.randn(400, 8, generator=g)
+    v = torch.randn(400, 4, 3, generator=g)
+    t = torch.randn(400, 3, 5, generator=g)
+    gr1 = SpatialGraph.build(pos.to(dev), 0.4, max_num_neighbors=24)
+    Q = torch.from_numpy(_rot(seed)).float()
+    D2 = torch.from_numpy(_wigner_d2(_rot(seed))).float()
+    pr = pos @ Q.T
+    gr2 = SpatialGraph.from_edge_index(gr1.row, gr1.col, pr.to(dev), 400)
+    s1, v1, t1 = conv(s.to(dev), v.to(dev), gr1, type2=t.to(dev))
+    s2, v2, t2 = conv(s.to(dev), (v @ Q.T).to(dev), gr2, type2=(t @ D2.T).to(dev))
+    _close(s2, s1, 1e-4, 1e-4)
+    _close(v2, v1 @ Q.T.to(dev), 1e-4, 1e-4)
+    _close(t2, t1 @ D2.T.to(dev), 1e-4, 1e-4)
+
+
+def test_se3conv_dtypes_and_autocast(dev):
+    """Outputs keep the input dtype (fp64 module and inputs, as tests/test_dtype_preservation.py:
+    10-30 asks; half inputs computed in fp32 and returned as half) and stay fp32 under autocast
+    (:74-103)."""
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv
+    torch.manual_seed(0)
+    pos = torch.rand(200, 3, device=dev)
+    gr = SpatialGraph.build(pos, 0.3, max_num_neighbors=32)
+    conv = SE3Conv(16, 4, 16, 4, radius=0.3).to(dev)
+    s = torch.randn(200, 16, device=dev)
+    v = torch.randn(200, 4, 3, device=dev)
+    s32, v32 = conv(s, v, gr)
+    c64 = SE3Conv(16, 4, 16, 4, radius=0.3).to(dev)
+    c64.load_state_dict(conv.state_dict())
+    c64 = c64.double()
+    sd = s.double().requires_grad_(True)
+    s64, v64 = c64(sd, v.double(), gr)
+    assert s64.dtype == torch.float64 and v64.dtype == torch.float64
+    _close(s64, s32, 1e-6, 1e-6)
+    (s64.sum() + v64.sum()).backward()
+    assert sd.grad.dtype == torch.float64
+    assert all(p.grad is not None and p.grad.dtype == torch.float64 for p in c64.parameters())
+    s16, v16 = conv(s.half(), v.half(), gr)
+    assert s16.dtype == torch.float16 and v16.dtype == torch.float16
+    with torch.autocast("cuda"):
+        sa, va = conv(s, v, gr)
+    assert sa.dtype == torch.float32 and va.dtype == torch.float32
+    _close(sa, s32, 0, 0)
