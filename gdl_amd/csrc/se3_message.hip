@@ -489,6 +489,86 @@ TnPlan tn_plan(int64_t M, int O, int K) {
   return t;
 }
 
+// ------------------------------------------------------------------- weight packing ---
+// The GEMMs read the nine path weights W_p [out][in] as zero-padded blocks (one launch builds
+// them all instead of a zeroing pass and a copy per block).  Block kinds (rows x cols):
+//   0 Ws  [Os][Cs|Cv|Ct]      = [W0 | W3 | W8]         forward, scalar outputs
+//   1 Wv  [Ov][Cs|Cv|Cv]      = [W1 | W2 | W4]         forward, vector outputs
+//   2 Wt  [Ot][Cs|Ct|Cv]      = [W5 | W6 | W7]         forward, type-2 outputs
+//   3-5   the transposes of 0-2 (rows = input slots, cols = outputs)     backward, gX = g W
+//   6 Bs  [Cs][Os|Ov|Ot]      = [W0^T | W1^T | W5^T]   backward, d scalars
+//   7 Bv  [Cv][Ov|Os|Ov|Ot]   = [W2^T | W3^T | W4^T | W7^T]
+//   8 Bt  [Ct][Ot]            = W6^T
+//   9 B8  [Ct][Os]            = W8^T
+struct SePackOut {
+  float* p;
+  int rows, cols, kind;  // rows / cols of the padded block; entries outside the real block are 0
+};
+struct SePack {
+  const float* W[kSePaths];
+  int Cs, Cv, Ct, Os, Ov, Ot;
+  int nout;
+  SePackOut out[10];
+  int64_t start[11];  // element offsets of the outputs in the flattened launch
+};
+
+__device__ __forceinline__ float w_at(const SePack& k, int path, int o, int i, int O, int I) {
+  return (k.W[path] && o < O && i < I) ? k.W[path][o * I + i] : 0.f;
+}
+
+__device__ float pack_elem(const SePack& k, int kind, int r, int c) {
+  const int Cs = k.Cs, Cv = k.Cv, Ct = k.Ct, Os = k.Os, Ov = k.Ov, Ot = k.Ot;
+  if (kind >= 3 && kind <= 5) {  // transpose of the forward block
+    const int t = r;
+    r = c;
+    c = t;
+    kind -= 3;
+  }
+  switch (kind) {
+    case 0:
+      if (r >= Os) return 0.f;
+      if (c < Cs) return w_at(k, 0, r, c, Os, Cs);
+      if (c < Cs + Cv) return w_at(k, 3, r, c - Cs, Os, Cv);
+      return w_at(k, 8, r, c - Cs - Cv, Os, Ct);
+    case 1:
+      if (r >= Ov) return 0.f;
+      if (c < Cs) return w_at(k, 1, r, c, Ov, Cs);
+      if (c < Cs + Cv) return w_at(k, 2, r, c - Cs, Ov, Cv);
+      return w_at(k, 4, r, c - Cs - Cv, Ov, Cv);
+    case 2:
+      if (r >= Ot) return 0.f;
+      if (c < Cs) return w_at(k, 5, r, c, Ot, Cs);
+      if (c < Cs + Ct) return w_at(k, 6, r, c - Cs, Ot, Ct);
+      return w_at(k, 7, r, c - Cs - Ct, Ot, Cv);
+    case 6:
+      if (r >= Cs) return 0.f;
+      if (c < Os) return w_at(k, 0, c, r, Os, Cs);
+      if (c < Os + Ov) return w_at(k, 1, c - Os, r, Ov, Cs);
+      return w_at(k, 5, c - Os - Ov, r, Ot, Cs);
+    case 7:
+      if (r >= Cv) return 0.f;
+      if (c < Ov) return w_at(k, 2, c, r, Ov, Cv);
+      if (c < Ov + Os) return w_at(k, 3, c - Ov, r, Os, Cv);
+      if (c < 2 * Ov + Os) return w_at(k, 4, c - Ov - Os, r, Ov, Cv);
+      return w_at(k, 7, c - 2 * Ov - Os, r, Ot, Cv);
+    case 8:
+      return r < Ct ? w_at(k, 6, c, r, Ot, Ct) : 0.f;
+    default:
+      return r < Ct ? w_at(k, 8, c, r, Os, Ct) : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(kSeThreads) void se3_pack_kernel(SePack k) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= k.start[k.nout]) return;
+  int j = 0;
+  while (j + 1 < k.nout && t >= k.start[j + 1]) ++j;
+  const SePackOut& o = k.out[j];
+  const int64_t local = t - k.start[j];
+  const int r = static_cast<int>(local / o.cols), c = static_cast<int>(local % o.cols);
+  o.p[local] = pack_elem(k, o.kind, r, c);
+}
+
 // ------------------------------------------------------------------ backward helpers ---
 // out[n][g][o] (row length Opad, zero padded) = in[n][o][g] / avg[n], zero where mask[n] == 0.
 __global__ __launch_bounds__(kSeThreads) void se3_grad_prep(const float* __restrict__ gin, int64_t N,
@@ -518,6 +598,7 @@ __device__ __forceinline__ float dpp_add(float v) {
 }
 
 // Lane 0 of a row turns the 21 per-edge sums into the edge's gradients of R, the direction and Y.
+template <bool T2>
 __device__ __forceinline__ void write_edge_grads(const SeEdges& g, const EdgeScalars& q,
                                                  const float S[21], float* dR, float* ddir,
                                                  float* dY) {
@@ -528,26 +609,33 @@ __device__ __forceinline__ void write_edge_grads(const SeEdges& g, const EdgeSca
     float val[kSePaths];
     val[0] = q.y0 * S[0];
     val[1] = (d[0] * S[1] + d[1] * S[2]) + d[2] * S[3];
-    val[5] = (((q.y2[0] * S[4] + q.y2[1] * S[5]) + q.y2[2] * S[6]) + q.y2[3] * S[7]) + q.y2[4] * S[8];
     val[2] = q.y0 * S[9];
     val[3] = (d[0] * S[10] + d[1] * S[11]) + d[2] * S[12];
     val[4] = (d[0] * S[13] + d[1] * S[14]) + d[2] * S[15];
-    val[7] = (d[0] * S[16] + d[1] * S[17]) + d[2] * S[18];
-    val[6] = q.y0 * S[19];
-    val[8] = S[20];
+    if (T2) {
+      val[5] = (((q.y2[0] * S[4] + q.y2[1] * S[5]) + q.y2[2] * S[6]) + q.y2[3] * S[7]) + q.y2[4] * S[8];
+      val[6] = q.y0 * S[19];
+      val[7] = (d[0] * S[16] + d[1] * S[17]) + d[2] * S[18];
+      val[8] = S[20];
+    }
 #pragma unroll
-    for (int i = 0; i < kSePaths; ++i)
+    for (int i = 0; i < (T2 ? kSePaths : 5); ++i)
       if (g.pc[i] >= 0) o[g.pc[i]] = val[i];
   }
   if (ddir) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
-      ddir[3 * e + k] = q.r[1] * S[1 + k] + q.r[3] * S[10 + k] + q.r[4] * S[13 + k] + q.r[7] * S[16 + k];
+    for (int k = 0; k < 3; ++k) {
+      float v = q.r[1] * S[1 + k] + q.r[3] * S[10 + k] + q.r[4] * S[13 + k];
+      if (T2) v += q.r[7] * S[16 + k];
+      ddir[3 * e + k] = v;
+    }
   }
   if (dY) {
     float* o = dY + e * g.ysh;
-    o[0] = q.r[0] * S[0] + q.r[2] * S[9] + q.r[6] * S[19];
-    if (g.ysh >= 9) {
+    float v0 = q.r[0] * S[0] + q.r[2] * S[9];
+    if (T2) v0 += q.r[6] * S[19];
+    o[0] = v0;
+    if (T2 && g.ysh >= 9) {
 #pragma unroll
       for (int k = 0; k < 5; ++k) o[4 + k] = q.r[5] * S[4 + k];
     }
@@ -683,7 +771,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
 #pragma unroll
       for (int i = 0; i < 21; ++i)
         if (T2 || i < 4 || (i >= 9 && i < 16)) S[i] = row_total(S[i]);
-      if (li == 0 && ok) write_edge_grads(g, q, S, dR, ddir, dY);
+      if (li == 0 && ok) write_edge_grads<T2>(g, q, S, dR, ddir, dY);
     }
   }
 }
@@ -1047,5 +1135,31 @@ extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O
                      dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(Opad) * Kpad, 64))),
                      dim3(kSeThreads), 0, st, part, nparts, Opad, Kpad, O, K, out, ldo);
   GEO_LAUNCH_CHECK("se3_gemm_tn_final");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_pack_weights(const float* const* W, int32_t Cs, int32_t Cv, int32_t Ct,
+                                    int32_t Os, int32_t Ov, int32_t Ot, int32_t nout,
+                                    float* const* out, const int32_t* rows, const int32_t* cols,
+                                    const int32_t* kinds, void* stream) {
+  GEO_REQUIRE(W && out && rows && cols && kinds, "se3_pack_weights: null table");
+  GEO_REQUIRE(nout >= 1 && nout <= 10, "se3_pack_weights: nout=%d outside [1, 10]", nout);
+  GEO_REQUIRE(Cs >= 0 && Cv >= 0 && Ct >= 0 && Os >= 0 && Ov >= 0 && Ot >= 0,
+              "se3_pack_weights: negative channel count");
+  SePack k;
+  for (int i = 0; i < kSePaths; ++i) k.W[i] = W[i];
+  k.Cs = Cs; k.Cv = Cv; k.Ct = Ct; k.Os = Os; k.Ov = Ov; k.Ot = Ot;
+  k.nout = nout;
+  k.start[0] = 0;
+  for (int j = 0; j < nout; ++j) {
+    GEO_REQUIRE(kinds[j] >= 0 && kinds[j] <= 9 && rows[j] >= 0 && cols[j] >= 0 && out[j],
+                "se3_pack_weights: bad output %d", j);
+    k.out[j] = SePackOut{out[j], rows[j], cols[j], kinds[j]};
+    k.start[j + 1] = k.start[j] + static_cast<int64_t>(rows[j]) * cols[j];
+  }
+  if (k.start[nout] == 0) return GEO_OK;
+  hipLaunchKernelGGL(se3_pack_kernel, dim3(static_cast<unsigned>(ceil_div(k.start[nout], kSeThreads))),
+                     dim3(kSeThreads), 0, as_stream(stream), k);
+  GEO_LAUNCH_CHECK("se3_pack_kernel");
   return GEO_OK;
 }

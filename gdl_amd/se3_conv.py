@@ -97,26 +97,23 @@ class _Plan:
         self.KZ8 = _pad16(self.Os)
         self.pc_c = (ctypes.c_int32 * 9)(*pc)
 
-    def w(self, W, i):
-        return W[i] if self.pc[i] >= 0 else None
 
-
-def _block(rows: int, K: int, parts, device) -> Tensor:
-    """[pad64(rows), K] fp32 with the given [rows, width] blocks side by side (None = zeros)."""
-    out = torch.zeros(_pad64(rows), K, dtype=torch.float32, device=device)
-    c = 0
-    for width, w in parts:
-        if w is not None and rows > 0 and width > 0:
-            out[:rows, c:c + width] = w
-        c += width
-    return out
-
-
-def _transpose_block(Wb: Tensor, OP: int, K: int) -> Tensor:
-    """[pad64(K), OP] with rows k < K equal to column k of the first OP rows of the block."""
-    out = torch.zeros(_pad64(K), OP, dtype=torch.float32, device=Wb.device)
-    out[:K] = Wb[:OP, :K].t()
-    return out
+def _pack(p: "_Plan", W, specs, device) -> list:
+    """Zero-padded weight blocks [(kind, rows, cols), ...] built by one kernel launch."""
+    specs = [sp for sp in specs]
+    outs = [torch.empty(r, c, dtype=torch.float32, device=device) for _, r, c in specs]
+    live = [(o, sp) for o, sp in zip(outs, specs) if o.numel() > 0]
+    if live:
+        n = len(live)
+        wp = (ctypes.c_void_p * 9)(*[(W[i].data_ptr() if p.pc[i] >= 0 else None) for i in range(9)])
+        op = (ctypes.c_void_p * n)(*[o.data_ptr() for o, _ in live])
+        rows = (ctypes.c_int32 * n)(*[sp[1] for _, sp in live])
+        cols = (ctypes.c_int32 * n)(*[sp[2] for _, sp in live])
+        kinds = (ctypes.c_int32 * n)(*[sp[0] for _, sp in live])
+        _nat.check(_nat.lib().geo_se3_pack_weights(wp, p.Cs, p.Cv, p.Ct, p.Os, p.Ov, p.Ot, n, op, rows,
+                                                   cols, kinds, _nat.stream_of(device)),
+                   "geo_se3_pack_weights")
+    return outs
 
 
 def _gemm(A: Tensor, M: int, K: int, B: Tensor, O: int, G: int, out: Tensor, ostride: int,
@@ -147,10 +144,8 @@ class _SE3MessageAggregate(torch.autograd.Function):
             _nat.ptr(ns), _nat.ptr(ne), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P,
             p.pc_c, cg_c, _nat.ptr(Xs), p.Ks, _nat.ptr(Xv), p.Kv, _nat.ptr(Xt), p.Kt, st),
             "geo_se3_aggregate_fwd")
-        Cs, Cv, Ct = p.Cs, p.Cv, p.Ct
-        Ws = _block(p.Os, p.Ks, [(Cs, p.w(W, 0)), (Cv, p.w(W, 3)), (Ct, p.w(W, 8))], dev)
-        Wv = _block(p.Ov, p.Kv, [(Cs, p.w(W, 1)), (Cv, p.w(W, 2)), (Cv, p.w(W, 4))], dev)
-        Wt = _block(p.Ot, p.Kt, [(Cs, p.w(W, 5)), (Ct, p.w(W, 6)), (Cv, p.w(W, 7))], dev)
+        Ws, Wv, Wt = _pack(p, W, [(0, _pad64(p.Os), p.Ks), (1, _pad64(p.Ov), p.Kv),
+                                  (2, _pad64(p.Ot), p.Kt)], dev)
         s_out = torch.empty(N, p.Os, **f32)
         v_out = torch.empty(N, p.Ov, 3, **f32)
         t_out = torch.empty(N, p.Ot, 5, **f32)
@@ -158,7 +153,6 @@ class _SE3MessageAggregate(torch.autograd.Function):
         _gemm(Xv, 3 * N, p.Kv, Wv, p.Ov, 3, v_out, 3 * p.Ov, avg, None, mask_u8)
         _gemm(Xt, 5 * N, p.Kt, Wt, p.Ot, 5, t_out, 5 * p.Ot, avg, None, mask_u8)
         ctx.plan, ctx.graph_arrays, ctx.cg_c = plan, graph_arrays, cg_c
-        ctx.wblocks = (Ws, Wv, Wt)
         ctx.has_bias = bias is not None
         ctx.save_for_backward(s, v, t, direction, Y, R, avg, mask_u8, Xs, Xv, Xt, *W)
         return s_out, v_out, t_out
@@ -193,16 +187,18 @@ class _SE3MessageAggregate(torch.autograd.Function):
         dR = ddir = dY = None
         if (need[8] or need[9] or need[10]) and E > 0:
             gXs = gXv = gXt = None
-            Ws, Wv, Wt = ctx.wblocks
+            WsT, WvT, WtT = _pack(p, W, [(3, _pad64(p.Ks), p.OsP if Gs is not None else 0),
+                                         (4, _pad64(p.Kv), p.OvP if Gv is not None else 0),
+                                         (5, _pad64(p.Kt), p.OtP if Gt is not None else 0)], dev)
             if Gs is not None:
                 gXs = torch.empty(N, p.Ks, **f32)
-                _gemm(Gs, N, p.OsP, _transpose_block(Ws, p.OsP, p.Ks), p.Ks, 1, gXs, p.Ks)
+                _gemm(Gs, N, p.OsP, WsT, p.Ks, 1, gXs, p.Ks)
             if Gv is not None:
                 gXv = torch.empty(N, 3, p.Kv, **f32)
-                _gemm(Gv, 3 * N, p.OvP, _transpose_block(Wv, p.OvP, p.Kv), p.Kv, 1, gXv, p.Kv)
+                _gemm(Gv, 3 * N, p.OvP, WvT, p.Kv, 1, gXv, p.Kv)
             if Gt is not None:
                 gXt = torch.empty(N, 5, p.Kt, **f32)
-                _gemm(Gt, 5 * N, p.OtP, _transpose_block(Wt, p.OtP, p.Kt), p.Kt, 1, gXt, p.Kt)
+                _gemm(Gt, 5 * N, p.OtP, WtT, p.Kt, 1, gXt, p.Kt)
             dR = torch.zeros(E, p.P, **f32) if need[10] else None
             ddir = torch.zeros(E, 3, **f32) if need[8] else None
             dY = torch.zeros(E, p.ysh, **f32) if need[9] else None
@@ -227,24 +223,22 @@ class _SE3MessageAggregate(torch.autograd.Function):
                 _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, ctx.cg_c, _nat.ptr(Zs), p.KZs, _nat.ptr(Zv),
                 p.KZv, _nat.ptr(Zt), p.KZt, _nat.ptr(Z8), p.KZ8, st), "geo_se3_bwd_src")
 
-            def wt(i, _rows):  # W_i^T [in, out] or None
-                return W[i].t() if p.pc[i] >= 0 else None
-
+            t6 = want_t and Zt is not None and p.pc[6] >= 0
+            Bs, Bv, Bt, B8 = _pack(p, W, [(6, _pad64(Cs), p.KZs if want_s else 0),
+                                          (7, _pad64(Cv), p.KZv if want_v else 0),
+                                          (8, _pad64(Ct), p.KZt if t6 else 0),
+                                          (9, _pad64(Ct), p.KZ8 if Z8 is not None else 0)], dev)
             if want_s:
-                Bs = _block(Cs, p.KZs, [(Os, wt(0, Cs)), (Ov, wt(1, Cs)), (Ot, wt(5, Cs))], dev)
                 ds = torch.empty(N, Cs, **f32)
                 _gemm(Zs, N, p.KZs, Bs, Cs, 1, ds, Cs)
             if want_v:
-                Bv = _block(Cv, p.KZv, [(Ov, wt(2, Cv)), (Os, wt(3, Cv)), (Ov, wt(4, Cv)), (Ot, wt(7, Cv))], dev)
                 dv = torch.empty(N, Cv, 3, **f32)
                 _gemm(Zv, 3 * N, p.KZv, Bv, Cv, 3, dv, 3 * Cv)
             if want_t:
                 dt = torch.zeros(N, Ct, 5, **f32)
-                if Zt is not None and p.pc[6] >= 0:
-                    Bt = _block(Ct, p.KZt, [(Ot, wt(6, Ct))], dev)
+                if t6:
                     _gemm(Zt, 5 * N, p.KZt, Bt, Ct, 5, dt, 5 * Ct)
                 if Z8 is not None:
-                    B8 = _block(Ct, p.KZ8, [(Os, wt(8, Ct))], dev)
                     u = torch.empty(N, Ct, **f32)
                     _gemm(Z8, N, p.KZ8, B8, Ct, 1, u, Ct)
                     dt = dt + 2.0 * t * u.unsqueeze(-1)

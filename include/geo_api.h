@@ -371,6 +371,18 @@ size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t K);
 int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B, int32_t ldb,
                     int32_t K, float* out, int32_t ldo, void* workspace, size_t workspace_bytes,
                     void* stream);
+/*
+ * Zero-padded weight blocks for geo_se3_gemm, built in one launch from the nine path weights
+ * W[p] ([out][in] row-major fp32 device pointers, NULL for absent paths; path order w_ss, w_sv,
+ * w_vv_scalar, w_vs, w_vv_cross, w_st2, w_t2t2, w_vt2, w_t2s).  Output j is a rows[j] x cols[j]
+ * block of kind kinds[j]: 0 [W0|W3|W8], 1 [W1|W2|W4], 2 [W5|W6|W7] (rows = outputs), 3-5 their
+ * transposes, 6 [W0^T|W1^T|W5^T], 7 [W2^T|W3^T|W4^T|W7^T], 8 W6^T, 9 W8^T (rows = inputs);
+ * entries outside the real block are 0.  Host arrays W, out, rows, cols, kinds; nout <= 10.
+ */
+int geo_se3_pack_weights(const float* const* W, int32_t Cs, int32_t Cv, int32_t Ct, int32_t Os,
+                         int32_t Ov, int32_t Ot, int32_t nout, float* const* out,
+                         const int32_t* rows, const int32_t* cols, const int32_t* kinds,
+                         void* stream);
 int geo_se3_grad_prep(const float* grad, int64_t N, int32_t O, int32_t G, int32_t Opad,
                       const float* avg, const uint8_t* mask, float* out, void* stream);
 int geo_se3_bwd_edge(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
