@@ -304,8 +304,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
 // out(r, o) = epilogue(sum_k A[r, k] B[o, k]) for r < M, o < O, with A [M, K] and B [>= grid
 // columns, K] row-major, K a multiple of 16 and both 16-byte aligned.  Row r is node n = r / G,
 // component g = r % G, stored at out[n * ostride + o * G + g] (G = 1 scalars, 3 vectors, 5
-// type-2 features).  Epilogue: divide by avg[n], add bias[o], zero where mask[n] == 0 (each
-// optional).
+// type-2 features; a template parameter).  Epilogue: scale by 1 / avg[n] (one reciprocal per
+// row), add bias[o], zero where mask[n] == 0 (each optional).
 //
 // v_mfma_f32_16x16x4_f32: lane l supplies A[i = l % 16][k = l / 16] and B[k = l / 16][j = l % 16]
 // and holds D[i = 4 (l / 16) + q][j = l % 16] in element q.  Each lane loads four consecutive k
@@ -314,9 +314,9 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
 // 16 NB columns; a block is four waves stacked along the rows.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int NB>
+template <int NB, int G>
 __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__ A, int64_t M, int K,
-                                                      const float* __restrict__ B, int O, int G,
+                                                      const float* __restrict__ B, int O,
                                                       float* __restrict__ out, int64_t ostride,
                                                       const float* __restrict__ avg,
                                                       const float* __restrict__ bias,
@@ -365,6 +365,15 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__
 #pragma unroll
     for (int cb = 0; cb < NB; ++cb) b[cb] = bn[cb];
   }
+  // epilogue: per-row scale (1 / avg, 0 where masked) and per-column bias, then strided stores
+  float bcol[NB];
+  bool ocol[NB];
+#pragma unroll
+  for (int cb = 0; cb < NB; ++cb) {
+    const int o = col0 + cb * 16 + li;
+    ocol[cb] = o < O;
+    bcol[cb] = (bias && ocol[cb]) ? bias[o] : 0.f;
+  }
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -374,15 +383,13 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__
       const int64_t n = r / G;
       const int gc = static_cast<int>(r - n * G);
       const bool keep = mask == nullptr || mask[n] != 0;
-      const float den = avg ? avg[n] : 1.f;
+      const float scale = avg ? 1.0f / avg[n] : 1.0f;
+      float* orow = out + n * ostride + gc;
 #pragma unroll
       for (int cb = 0; cb < NB; ++cb) {
-        const int o = col0 + cb * 16 + li;
-        if (o >= O) continue;
-        float val = acc[rb][cb][q];
-        if (avg) val = val / den;
-        if (bias) val += bias[o];
-        out[n * ostride + static_cast<int64_t>(o) * G + gc] = keep ? val : 0.f;
+        if (!ocol[cb]) continue;
+        const float val = acc[rb][cb][q] * scale + bcol[cb];
+        orow[static_cast<int64_t>(col0 + cb * 16 + li) * G] = keep ? val : 0.f;
       }
     }
 }
@@ -1004,17 +1011,17 @@ extern "C" int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B
   const int64_t gy = ceil_div(O, cols);
   GEO_REQUIRE(B_rows >= gy * cols, "se3_gemm: B has %d rows, the launch reads %lld", B_rows,
               (long long)(gy * cols));
+  GEO_REQUIRE(G == 1 || G == 3 || G == 5, "se3_gemm: G=%d must be 1, 3 or 5", G);
   const dim3 grid(static_cast<unsigned>(ceil_div(M, 32 * kSeWaves)), static_cast<unsigned>(gy));
   hipStream_t st = as_stream(stream);
-  if (nb == 4)
-    hipLaunchKernelGGL(se3_gemm<4>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
-                       avg, bias, mask);
-  else if (nb == 2)
-    hipLaunchKernelGGL(se3_gemm<2>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
-                       avg, bias, mask);
-  else
-    hipLaunchKernelGGL(se3_gemm<1>, grid, dim3(kSeThreads), 0, st, A, M, K, B, O, G, out, out_stride,
-                       avg, bias, mask);
+#define GEO_GEMM(NB_, G_)                                                                         \
+  if (nb == NB_ && G == G_)                                                                       \
+    hipLaunchKernelGGL((se3_gemm<NB_, G_>), grid, dim3(kSeThreads), 0, st, A, M, K, B, O, out,     \
+                       out_stride, avg, bias, mask);
+  GEO_GEMM(1, 1) GEO_GEMM(2, 1) GEO_GEMM(4, 1)
+  GEO_GEMM(1, 3) GEO_GEMM(2, 3) GEO_GEMM(4, 3)
+  GEO_GEMM(1, 5) GEO_GEMM(2, 5) GEO_GEMM(4, 5)
+#undef GEO_GEMM
   GEO_LAUNCH_CHECK("se3_gemm");
   return GEO_OK;
 }
