@@ -57,8 +57,20 @@ struct Vec {
   __device__ __forceinline__ void load(const T* p) {
     raw = *reinterpret_cast<const typename Raw<VB>::type*>(p);
   }
+  // Outputs are written once and not read back by this kernel: non-temporal (streaming) stores
+  // keep them from displacing the message rows in the caches.
   __device__ __forceinline__ void store(T* p) const {
-    *reinterpret_cast<typename Raw<VB>::type*>(p) = raw;
+    if constexpr (VB == 16) {
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = {raw.x, raw.y, raw.z, raw.w};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+    } else if constexpr (VB == 8) {
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 v = {raw.x, raw.y};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+    } else {
+      __builtin_nontemporal_store(raw, reinterpret_cast<typename Raw<VB>::type*>(p));
+    }
   }
 };
 
@@ -82,15 +94,20 @@ struct IVec {
     }
   }
   __device__ __forceinline__ void store(int32_t* p) const {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    typedef int i32x2 __attribute__((ext_vector_type(2)));
     if constexpr (N % 4 == 0) {
 #pragma unroll
-      for (int i = 0; i < N; i += 4)
-        *reinterpret_cast<int4*>(p + i) = make_int4(e[i], e[i + 1], e[i + 2], e[i + 3]);
+      for (int i = 0; i < N; i += 4) {
+        const i32x4 v = {e[i], e[i + 1], e[i + 2], e[i + 3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(p + i));
+      }
     } else if constexpr (N == 2) {
-      *reinterpret_cast<int2*>(p) = make_int2(e[0], e[1]);
+      const i32x2 v = {e[0], e[1]};
+      __builtin_nontemporal_store(v, reinterpret_cast<i32x2*>(p));
     } else {
 #pragma unroll
-      for (int i = 0; i < N; ++i) p[i] = e[i];
+      for (int i = 0; i < N; ++i) __builtin_nontemporal_store(e[i], p + i);
     }
   }
 };
