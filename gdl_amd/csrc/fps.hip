@@ -165,8 +165,9 @@ __global__ __launch_bounds__(kFpsThreads) void fps_register_kernel(
 //
 // Clouds of up to 8192 points.  The cloud is first ordered along a 16^3 Morton cell grid
 // (LDS counting sort), so the 64 points a wave holds in one register slot — a bucket — lie
-// close together.  Each bucket keeps its bounding box and (max min-distance, lowest index
-// attaining it) in lane s of three VGPRs.  Per iteration the wave tests all its buckets at once
+// close together.  Each bucket keeps its bounding box in lane s of six VGPRs and its (max
+// min-distance, lowest index attaining it) as wave-uniform scalars, so a wave's best is a few
+// scalar max / compare instructions after an update instead of another cross-lane reduction.  Per iteration the wave tests all its buckets at once
 // (one lane per bucket): with
 //   g_a = max(lo_a - c_a, c_a - hi_a, 0),  lb = (g_x*g_x + g_y*g_y) + g_z*g_z
 // evaluated with the same fp32 operations as the distance, every rounded operation is monotone,
@@ -307,12 +308,15 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   for (int i = t; i < n; i += THREADS) table[i] = make_float4(P[3 * i], P[3 * i + 1], P[3 * i + 2], 0.f);
   if (t < 3) slots[t] = 0ull;
 
-  // 4. bucket records, lane s = bucket of slot s: box, max min-distance bits, and a cached
-  //    lowest index attaining the max that an update invalidates.
+  // 4. bucket records: box in lane s (bucket of slot s); max min-distance bits and a cached
+  //    lowest index attaining the max (invalidated by an update) as scalars bm[s], bi[s].
   float blx = __builtin_inff(), bly = __builtin_inff(), blz = __builtin_inff();
   float bhx = -__builtin_inff(), bhy = -__builtin_inff(), bhz = -__builtin_inff();
-  uint32_t bmax = 0u, bidx = 0xffffffffu;
-  uint64_t stale = 0;  // buckets whose cached (bidx, position) is out of date
+  uint32_t bmax = 0u;
+  // Bucket maxima and cached lowest indices attaining them are wave-uniform: kept as scalars
+  // (bm, bi), with bmax (lane s = bucket s) the per-lane copy the skip test reads.
+  uint32_t bm[PTS], bi[PTS];
+  uint64_t stale = 0;  // buckets whose cached index is out of date
 #pragma unroll
   for (int s = 0; s < PTS; ++s) {
     const bool valid = oi[s] != 0xffffffffu;
@@ -323,6 +327,8 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const uint32_t h1 = wave_max_u32(valid ? float_order_key(py[s]) : 0u);
     const uint32_t h2 = wave_max_u32(valid ? float_order_key(pz[s]) : 0u);
     const uint32_t mi = wave_min_u32(oi[s]);
+    bm[s] = mi != 0xffffffffu ? 0x7f800000u : 0u;
+    bi[s] = 0xffffffffu;
     if (lane == s && mi != 0xffffffffu) {
       blx = float_from_order_key(l0); bly = float_from_order_key(l1); blz = float_from_order_key(l2);
       bhx = float_from_order_key(h0); bhy = float_from_order_key(h1); bhz = float_from_order_key(h2);
@@ -355,32 +361,31 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
           const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
           md[s] = __builtin_amdgcn_fmed3f(d, md[s], -__builtin_inff());
           const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
+          bm[s] = m;
           if (lane == s) bmax = m;
         }
       }
     }
     if (dirty) {
-      // wave best: the largest bucket max, then the lowest index over the buckets holding it
-      wbits = PTS <= 16 ? row0_max_u32(bmax) : wave_max_u32(lane < PTS ? bmax : 0u);
-      const uint64_t tied = __ballot(lane < PTS && bmax == wbits);
-      const uint64_t need = tied & stale;
-      if (need) {
+      // wave best: the largest bucket max (scalar), then the lowest index over the buckets
+      // holding it, refreshing the cached index of a tied bucket that changed
+      uint32_t wb = 0u;
 #pragma unroll
-        for (int s = 0; s < PTS; ++s) {
-          if (need & (1ull << s)) {
+      for (int s = 0; s < PTS; ++s) wb = bm[s] > wb ? bm[s] : wb;
+      wbits = wb;
+      uint32_t best = 0xffffffffu;
+#pragma unroll
+      for (int s = 0; s < PTS; ++s) {
+        if (bm[s] == wb) {
+          if ((stale >> s) & 1ull) {
             const uint32_t mb = __float_as_uint(md[s]);
-            const uint32_t mi = wave_min_u32(mb == wbits ? oi[s] : 0xffffffffu);
-            if (lane == s) bidx = mi;
+            bi[s] = wave_min_u32(mb == wb ? oi[s] : 0xffffffffu);
+            stale &= ~(1ull << s);
           }
+          best = bi[s] < best ? bi[s] : best;
         }
-        stale &= ~need;
       }
-      if ((tied & (tied - 1)) == 0) {  // a single bucket holds the max (the usual case)
-        widx = __builtin_amdgcn_readlane(bidx, __builtin_ctzll(tied | (1ull << 63)));
-      } else {
-        widx = PTS <= 16 ? row0_min_u32((tied >> lane) & 1 ? bidx : 0xffffffffu)
-                         : wave_min_u32(lane < PTS && ((tied >> lane) & 1) ? bidx : 0xffffffffu);
-      }
+      widx = best;
       dirty = false;
     }
     const int p = it % 3;
