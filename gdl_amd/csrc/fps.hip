@@ -342,7 +342,8 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   bool dirty = true;
   __syncthreads();
 
-  for (int it = 1; it < k; ++it) {
+  int p = 1;  // it % 3
+  for (int it = 1; it < k; ++it, p = p == 2 ? 0 : p + 1) {
     float gx, gy, gz;
     {
 #pragma clang fp contract(off)
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
       gz = fmaxf(fmaxf(blz - cz, cz - bhz), 0.f);
     }
     const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
-    const uint64_t act = __ballot(lane < PTS && __float_as_uint(lb) < bmax);
+    const uint64_t act = __ballot(__float_as_uint(lb) < bmax);  // bmax = 0 on lanes >= PTS
     if (act) {
       stale |= act;
       dirty = true;
@@ -388,7 +389,6 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
       widx = best;
       dirty = false;
     }
-    const int p = it % 3;
     if (lane == 0)
       atomicMax(&slots[p], (static_cast<unsigned long long>(wbits) << 32) | static_cast<uint32_t>(~widx));
     if (t == 0) slots[p == 2 ? 0 : p + 1] = 0ull;
