@@ -380,7 +380,12 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
         if (bm[s] == wb) {
           if ((stale >> s) & 1ull) {
             const uint32_t mb = __float_as_uint(md[s]);
-            bi[s] = wave_min_u32(mb == wb ? oi[s] : 0xffffffffu);
+            const uint64_t hit = __ballot(mb == wb);
+            // one lane holds the maximum (distance ties are rare): take its index directly
+            bi[s] = (hit & (hit - 1)) == 0
+                        ? static_cast<uint32_t>(__builtin_amdgcn_readlane(
+                              static_cast<int>(oi[s]), __builtin_ctzll(hit | (1ull << 63))))
+                        : wave_min_u32(mb == wb ? oi[s] : 0xffffffffu);
             stale &= ~(1ull << s);
           }
           best = bi[s] < best ? bi[s] : best;
