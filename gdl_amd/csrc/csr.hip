@@ -26,10 +26,10 @@ __global__ void csr_bounds(const uint32_t* __restrict__ sorted_keys, int64_t E, 
   if (n > 0) node_end[n - 1] = static_cast<int32_t>(lo);
 }
 
-int radix_passes(int64_t N) {
+int radix_key_bits(int64_t N) {
   int bits = 0;
   while (bits < 32 && (static_cast<uint64_t>(N) >> bits) != 0) ++bits;  // bits to hold key N
-  return bits == 0 ? 1 : (bits + 7) / 8;
+  return bits == 0 ? 1 : bits;
 }
 
 RadixBuffers carve_csr(void* base, int64_t E, size_t* bytes) {
@@ -73,7 +73,7 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
     return device_fill<int32_t>(node_end, N, 0, st);
   }
 
-  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_passes(N),
+  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),
                                 reinterpret_cast<uint32_t*>(col_sorted),
                                 reinterpret_cast<uint32_t*>(perm), w, st);
   if (rc) return rc;

@@ -776,7 +776,7 @@ int launch_large(const float* pos, int64_t N, const int64_t* ptr, const int64_t*
   hipLaunchKernelGGL(fps_large_keys_kernel, dim3(grid), dim3(256), 0, st, pos, ptr, B, N, w.bbox,
                      mbits, w.keys);
   GEO_LAUNCH_CHECK("fps_large_keys_kernel");
-  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, (bits + 7) / 8, w.skeys, w.order, w.rx, st);
+  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, bits, w.skeys, w.order, w.rx, st);
   if (rc) return rc;
   hipLaunchKernelGGL(fps_large_gather_kernel, dim3(grid), dim3(256), 0, st, pos, w.order, N, w.q, w.md);
   GEO_LAUNCH_CHECK("fps_large_gather_kernel");

@@ -1,11 +1,12 @@
-// radix.hpp — stable LSD radix sort of (uint32 key, uint32 value) pairs, 8-bit digits.
+// radix.hpp — stable LSD radix sort of (uint32 key, uint32 value) pairs, 8- to 11-bit digits.
 //
-// Three kernels per pass:
-//   radix_hist     one 2048-key tile per block, 256-bin LDS histogram -> hist[digit][tile]
+// A sort of b-bit keys takes ceil(b / 11) passes of near-equal digit width (17-bit CSR keys: two
+// passes of 9 and 8 bits instead of three of 8).  Three kernels per pass:
+//   radix_hist     one 2048-key tile per block, 2^BITS-bin LDS histogram -> hist[digit][tile]
 //                  (lanes holding the same digit add once: sorted input does not serialise)
 //   scan           device-wide exclusive scan of hist (digit-major) -> global offsets
 //   radix_scatter  stable rank inside the tile: each wave walks its 512 keys in index order,
-//                  peers with the same digit are found with 8 ballots, per-wave LDS counters
+//                  peers with the same digit are found with BITS ballots, per-wave LDS counters
 //                  give the running count, a cross-wave prefix finishes the tile rank.
 // The first pass reads the caller's keys in one of three forms (RxSource) and writes uint32
 // keys; the value of the first pass is the element index unless values are supplied.
@@ -20,6 +21,8 @@ constexpr int kRxItems = 8;
 constexpr int kRxTile = kRxThreads * kRxItems;
 constexpr int kRxWaves = kRxThreads / kWave;
 constexpr int kRxWaveSpan = kRxItems * kWave;  // keys per wave in a tile
+constexpr int kRxMaxBits = 11;                  // widest digit
+constexpr int kRxMaxBins = 1 << kRxMaxBits;
 
 enum RxSource {
   kRxCol64 = 0,     // int64 keys, values outside [0, N) become N; value = index
@@ -38,10 +41,11 @@ __device__ __forceinline__ uint32_t rx_fetch_key(const void* keys, int64_t i, in
 }
 
 // Lanes of the wave whose (valid) digit equals this lane's digit.
+template <int BITS>
 __device__ __forceinline__ uint64_t rx_peers(uint32_t d, bool valid) {
   uint64_t peers = __ballot(valid);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
+  for (int b = 0; b < BITS; ++b) {
     const bool bit = (d >> b) & 1u;
     const uint64_t bb = __ballot(bit);
     peers &= bit ? bb : ~bb;
@@ -49,41 +53,46 @@ __device__ __forceinline__ uint64_t rx_peers(uint32_t d, bool valid) {
   return peers;
 }
 
-template <int SRC>
+template <int SRC, int BITS>
 __global__ __launch_bounds__(kRxThreads) void radix_hist(const void* __restrict__ keys, int64_t n,
                                                          int64_t N, int shift,
                                                          uint32_t* __restrict__ hist,
                                                          int64_t ntiles) {
-  __shared__ uint32_t h[256];
-  h[threadIdx.x] = 0;
+  constexpr int BINS = 1 << BITS;
+  __shared__ uint32_t h[BINS];
+  for (int b = threadIdx.x; b < BINS; b += kRxThreads) h[b] = 0;
   __syncthreads();
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kRxTile;
 #pragma unroll
   for (int i = 0; i < kRxItems; ++i) {
     const int64_t idx = base + static_cast<int64_t>(i) * kRxThreads + threadIdx.x;
     const bool valid = idx < n;
-    const uint32_t d = valid ? (rx_fetch_key<SRC>(keys, idx, N) >> shift) & 255u : 0u;
-    const uint64_t peers = rx_peers(d, valid);
+    const uint32_t d = valid ? (rx_fetch_key<SRC>(keys, idx, N) >> shift) & (BINS - 1u) : 0u;
+    const uint64_t peers = rx_peers<BITS>(d, valid);
     if (valid && __popcll(peers & lanemask_lt()) == 0)
       atomicAdd(&h[d], static_cast<uint32_t>(__popcll(peers)));
   }
   __syncthreads();
-  hist[static_cast<int64_t>(threadIdx.x) * ntiles + blockIdx.x] = h[threadIdx.x];
+  for (int b = threadIdx.x; b < BINS; b += kRxThreads)
+    hist[static_cast<int64_t>(b) * ntiles + blockIdx.x] = h[b];
 }
 
-template <int SRC>
+template <int SRC, int BITS>
 __global__ __launch_bounds__(kRxThreads) void radix_scatter(
     const void* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n, int64_t N,
     int shift, const uint32_t* __restrict__ offsets, int64_t ntiles, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out) {
-  __shared__ uint32_t cnt[kRxWaves][256];
-  __shared__ uint32_t goff[256];
+  constexpr int BINS = 1 << BITS;
+  __shared__ uint32_t cnt[kRxWaves][BINS];
+  __shared__ uint32_t goff[BINS];
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int lane = lane_id();
+  for (int b = t; b < BINS; b += kRxThreads) {
 #pragma unroll
-  for (int ww = 0; ww < kRxWaves; ++ww) cnt[ww][t] = 0;
-  goff[t] = offsets[static_cast<int64_t>(t) * ntiles + blockIdx.x];
+    for (int ww = 0; ww < kRxWaves; ++ww) cnt[ww][b] = 0;
+    goff[b] = offsets[static_cast<int64_t>(b) * ntiles + blockIdx.x];
+  }
   __syncthreads();
 
   const uint64_t lt = lanemask_lt();
@@ -99,8 +108,8 @@ __global__ __launch_bounds__(kRxThreads) void radix_scatter(
     } else {
       val[i] = static_cast<uint32_t>(idx);
     }
-    const uint32_t d = (key[i] >> shift) & 255u;
-    const uint64_t peers = rx_peers(d, valid);
+    const uint32_t d = (key[i] >> shift) & (BINS - 1u);
+    const uint64_t peers = rx_peers<BITS>(d, valid);
     const uint32_t r = static_cast<uint32_t>(__popcll(peers & lt));
     const uint32_t before = cnt[w][d];
     __builtin_amdgcn_wave_barrier();
@@ -109,12 +118,12 @@ __global__ __launch_bounds__(kRxThreads) void radix_scatter(
     rank[i] = before + r;
   }
   __syncthreads();
-  {
+  for (int b = t; b < BINS; b += kRxThreads) {
     uint32_t run = 0;
 #pragma unroll
     for (int ww = 0; ww < kRxWaves; ++ww) {
-      const uint32_t c = cnt[ww][t];
-      cnt[ww][t] = run;
+      const uint32_t c = cnt[ww][b];
+      cnt[ww][b] = run;
       run += c;
     }
   }
@@ -123,7 +132,7 @@ __global__ __launch_bounds__(kRxThreads) void radix_scatter(
   for (int i = 0; i < kRxItems; ++i) {
     const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
     if (idx < n) {
-      const uint32_t d = (key[i] >> shift) & 255u;
+      const uint32_t d = (key[i] >> shift) & (BINS - 1u);
       const uint32_t pos = goff[d] + cnt[w][d] + rank[i];
       keys_out[pos] = key[i];
       vals_out[pos] = val[i];
@@ -143,41 +152,60 @@ inline RadixBuffers carve_radix(Carver& c, int64_t n) {
   r.va = c.take<uint32_t>(n);
   r.kb = c.take<uint32_t>(n);
   r.vb = c.take<uint32_t>(n);
-  r.hist = c.take<uint32_t>(256 * ntiles);
-  r.hist_tiles = c.take<uint32_t>(scan_workspace_elems(256 * ntiles));
+  r.hist = c.take<uint32_t>(static_cast<int64_t>(kRxMaxBins) * ntiles);
+  r.hist_tiles = c.take<uint32_t>(scan_workspace_elems(static_cast<int64_t>(kRxMaxBins) * ntiles));
   return r;
 }
 
-// Sorts n > 0 keys on digits 0 .. passes-1 (8 bits each); the last pass writes keys_out /
-// vals_out.  keys / vals are read as the first pass's source SRC.
-template <int SRC>
-int radix_sort(const void* keys, const uint32_t* vals, int64_t n, int64_t N, int passes,
-               uint32_t* keys_out, uint32_t* vals_out, const RadixBuffers& r, hipStream_t st) {
+template <int SRC, int BITS>
+int radix_pass(const void* kin, const uint32_t* vin, int64_t n, int64_t N, int shift,
+               uint32_t* kout, uint32_t* vout, const RadixBuffers& r, hipStream_t st) {
   const int64_t ntiles = ceil_div(n, kRxTile);
+  hipLaunchKernelGGL((radix_hist<SRC, BITS>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, n, N,
+                     shift, r.hist, ntiles);
+  GEO_LAUNCH_CHECK("radix_hist");
+  int rc = device_exclusive_scan<uint32_t, uint32_t>(r.hist, (int64_t{1} << BITS) * ntiles, r.hist,
+                                                     nullptr, false, r.hist_tiles, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL((radix_scatter<SRC, BITS>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, vin,
+                     n, N, shift, r.hist, ntiles, kout, vout);
+  GEO_LAUNCH_CHECK("radix_scatter");
+  return GEO_OK;
+}
+
+template <int SRC>
+int radix_pass_bits(int bits, const void* kin, const uint32_t* vin, int64_t n, int64_t N, int shift,
+                    uint32_t* kout, uint32_t* vout, const RadixBuffers& r, hipStream_t st) {
+  switch (bits) {
+    case 8: return radix_pass<SRC, 8>(kin, vin, n, N, shift, kout, vout, r, st);
+    case 9: return radix_pass<SRC, 9>(kin, vin, n, N, shift, kout, vout, r, st);
+    case 10: return radix_pass<SRC, 10>(kin, vin, n, N, shift, kout, vout, r, st);
+    default: return radix_pass<SRC, 11>(kin, vin, n, N, shift, kout, vout, r, st);
+  }
+}
+
+// Sorts n > 0 keys below 2^key_bits (stable); the last pass writes keys_out / vals_out.  keys /
+// vals are read as the first pass's source SRC.  Digit widths: ceil(key_bits / 11) passes of
+// near-equal width, at least 8 bits each.
+template <int SRC>
+int radix_sort(const void* keys, const uint32_t* vals, int64_t n, int64_t N, int key_bits,
+               uint32_t* keys_out, uint32_t* vals_out, const RadixBuffers& r, hipStream_t st) {
+  key_bits = key_bits < 1 ? 1 : (key_bits > 32 ? 32 : key_bits);
+  const int passes = (key_bits + kRxMaxBits - 1) / kRxMaxBits;
   const void* kin = keys;
   const uint32_t* vin = vals;
+  int shift = 0;
   for (int p = 0; p < passes; ++p) {
     const bool first = p == 0, last = p == passes - 1;
     uint32_t* kout = last ? keys_out : ((p % 2 == 0) ? r.ka : r.kb);
     uint32_t* vout = last ? vals_out : ((p % 2 == 0) ? r.va : r.vb);
-    const int shift = 8 * p;
-    if (first)
-      hipLaunchKernelGGL((radix_hist<SRC>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, n, N,
-                         shift, r.hist, ntiles);
-    else
-      hipLaunchKernelGGL((radix_hist<kRxPairs>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, n,
-                         N, shift, r.hist, ntiles);
-    GEO_LAUNCH_CHECK("radix_hist");
-    int rc = device_exclusive_scan<uint32_t, uint32_t>(r.hist, 256 * ntiles, r.hist, nullptr,
-                                                       false, r.hist_tiles, st);
+    const int left = key_bits - shift;
+    int bits = (left + (passes - p) - 1) / (passes - p);
+    bits = bits < 8 ? 8 : bits;
+    const int rc = first ? radix_pass_bits<SRC>(bits, kin, vin, n, N, shift, kout, vout, r, st)
+                         : radix_pass_bits<kRxPairs>(bits, kin, vin, n, N, shift, kout, vout, r, st);
     if (rc) return rc;
-    if (first)
-      hipLaunchKernelGGL((radix_scatter<SRC>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, vin,
-                         n, N, shift, r.hist, ntiles, kout, vout);
-    else
-      hipLaunchKernelGGL((radix_scatter<kRxPairs>), dim3(ntiles), dim3(kRxThreads), 0, st, kin,
-                         vin, n, N, shift, r.hist, ntiles, kout, vout);
-    GEO_LAUNCH_CHECK("radix_scatter");
+    shift += bits;
     kin = kout;
     vin = vout;
   }
