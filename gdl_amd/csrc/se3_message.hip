@@ -156,6 +156,73 @@ __device__ __forceinline__ EdgeScalars edge_from(const EdgeScalars& st, int j) {
   return q;
 }
 
+// Per-edge coefficients with the edge's scalars folded in, computed once by the lane that stages
+// the edge (instead of by every channel lane):
+//   c0 = r0 y0, c1 = r1 d, c2 = r2 y0, c3 = r3 d, c4 = r4 d, c5 = r5 y2, c6 = r6 y0, c8 = r8,
+//   d7[j][m] = r7 sum_i d_i cg[i][j][m]
+// (r_p = 0 for paths that are off).  The forward accumulates c0 s, c1 s, c2 v, c3 . v, c4 x v,
+// c5 s, c6 t, c8 |t|^2 and sum_j d7[j] v_j; the source-side backward the transposed products.
+template <bool T2>
+struct EdgeCoef {
+  int32_t other;
+  int32_t ok;
+  float c0, c1[3], c2, c3[3], c4[3];
+  float c5[5], c6, c8, d7[3][5];
+};
+
+__device__ __forceinline__ void cg_coef(const float* cg, const float d[3], float r, float D[3][5]);
+
+template <bool T2>
+__device__ __forceinline__ EdgeCoef<T2> stage_coef(const SeEdges& g, int base, int cnt, int lane) {
+  const EdgeScalars q = stage_edges(g, base, cnt, lane);
+  EdgeCoef<T2> c;
+  c.other = q.other;
+  c.ok = q.ok;
+  c.c0 = q.r[0] * q.y0;
+  c.c2 = q.r[2] * q.y0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    c.c1[k] = q.r[1] * q.d[k];
+    c.c3[k] = q.r[3] * q.d[k];
+    c.c4[k] = q.r[4] * q.d[k];
+  }
+  if (T2) {
+#pragma unroll
+    for (int m = 0; m < 5; ++m) c.c5[m] = q.r[5] * q.y2[m];
+    c.c6 = q.r[6] * q.y0;
+    c.c8 = q.r[8];
+    cg_coef(g.cg, q.d, q.r[7], c.d7);
+  }
+  return c;
+}
+
+// The staged coefficients of lane j (j wave-uniform).
+template <bool T2>
+__device__ __forceinline__ EdgeCoef<T2> coef_at(const EdgeCoef<T2>& st, int j) {
+  EdgeCoef<T2> c;
+  c.other = __builtin_amdgcn_readlane(st.other, j);
+  c.ok = __builtin_amdgcn_readlane(st.ok, j);
+  c.c0 = rlane(st.c0, j);
+  c.c2 = rlane(st.c2, j);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    c.c1[k] = rlane(st.c1[k], j);
+    c.c3[k] = rlane(st.c3[k], j);
+    c.c4[k] = rlane(st.c4[k], j);
+  }
+  if (T2) {
+#pragma unroll
+    for (int m = 0; m < 5; ++m) c.c5[m] = rlane(st.c5[m], j);
+    c.c6 = rlane(st.c6, j);
+    c.c8 = rlane(st.c8, j);
+#pragma unroll
+    for (int jj = 0; jj < 3; ++jj)
+#pragma unroll
+      for (int m = 0; m < 5; ++m) c.d7[jj][m] = rlane(st.d7[jj][m], j);
+  }
+  return c;
+}
+
 // D[j][m] = r * sum_i d_i cg[i][j][m]: path 7's per-edge coefficients, so that a lane's share
 // is sum_j v_j D[j][m] (forward) or sum_m D[j][m] w_m (source-side backward).
 __device__ __forceinline__ void cg_coef(const float* cg, const float d[3], float r, float D[3][5]) {
@@ -202,7 +269,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
     float A7[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A6[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A8 = 0.f;
     for (int base = a; base < b; base += kWave) {
       const int cnt = min(kWave, b - base);
-      const EdgeScalars st = stage_edges(g, base, cnt, lane);
+      const EdgeCoef<T2> st = stage_coef<T2>(g, base, cnt, lane);
       for (int j0 = 0; j0 < cnt; j0 += kSeUnroll) {
         float sv[kSeUnroll], vv[kSeUnroll][3], tt[kSeUnroll][5];
 #pragma unroll
@@ -223,47 +290,46 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
 #pragma unroll
         for (int u = 0; u < kSeUnroll; ++u) {
           if (j0 + u >= cnt) break;
-          const EdgeScalars q = edge_at(st, j0 + u);
+          const EdgeCoef<T2> q = coef_at<T2>(st, j0 + u);
           if (!q.ok) continue;
           if (hs) {
             const float x = sv[u];
-            if (g.pc[0] >= 0) A0 += q.r[0] * q.y0 * x;
+            if (g.pc[0] >= 0) A0 += q.c0 * x;
             if (g.pc[1] >= 0) {
 #pragma unroll
-              for (int k = 0; k < 3; ++k) A1[k] += q.r[1] * q.d[k] * x;
+              for (int k = 0; k < 3; ++k) A1[k] += q.c1[k] * x;
             }
             if (T2 && g.pc[5] >= 0) {
 #pragma unroll
-              for (int k = 0; k < 5; ++k) A5[k] += q.r[5] * q.y2[k] * x;
+              for (int k = 0; k < 5; ++k) A5[k] += q.c5[k] * x;
             }
           }
           if (hv) {
             const float* v = vv[u];
             if (g.pc[2] >= 0) {
 #pragma unroll
-              for (int k = 0; k < 3; ++k) A2[k] += q.r[2] * q.y0 * v[k];
+              for (int k = 0; k < 3; ++k) A2[k] += q.c2 * v[k];
             }
-            if (g.pc[3] >= 0) A3 += q.r[3] * ((q.d[0] * v[0] + q.d[1] * v[1]) + q.d[2] * v[2]);
+            if (g.pc[3] >= 0) A3 += (q.c3[0] * v[0] + q.c3[1] * v[1]) + q.c3[2] * v[2];
             if (g.pc[4] >= 0) {
-              A4[0] += q.r[4] * (q.d[1] * v[2] - q.d[2] * v[1]);
-              A4[1] += q.r[4] * (q.d[2] * v[0] - q.d[0] * v[2]);
-              A4[2] += q.r[4] * (q.d[0] * v[1] - q.d[1] * v[0]);
+              A4[0] += q.c4[1] * v[2] - q.c4[2] * v[1];
+              A4[1] += q.c4[2] * v[0] - q.c4[0] * v[2];
+              A4[2] += q.c4[0] * v[1] - q.c4[1] * v[0];
             }
             if (T2 && g.pc[7] >= 0 && Xt) {
-              float D[3][5];
-              cg_coef(g.cg, q.d, q.r[7], D);
 #pragma unroll
-              for (int k = 0; k < 5; ++k) A7[k] += (D[0][k] * v[0] + D[1][k] * v[1]) + D[2][k] * v[2];
+              for (int k = 0; k < 5; ++k)
+                A7[k] += (q.d7[0][k] * v[0] + q.d7[1][k] * v[1]) + q.d7[2][k] * v[2];
             }
           }
           if (ht) {
             const float* t = tt[u];
             if (g.pc[6] >= 0) {
 #pragma unroll
-              for (int k = 0; k < 5; ++k) A6[k] += q.r[6] * q.y0 * t[k];
+              for (int k = 0; k < 5; ++k) A6[k] += q.c6 * t[k];
             }
             if (g.pc[8] >= 0)
-              A8 += q.r[8] * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
+              A8 += q.c8 * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
           }
         }
       }
@@ -813,7 +879,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
     float z7[3] = {0.f, 0.f, 0.f}, z6[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
     for (int base = a; base < b; base += kWave) {
       const int cnt = min(kWave, b - base);
-      const EdgeScalars st = stage_edges(g, base, cnt, lane);
+      const EdgeCoef<T2> st = stage_coef<T2>(g, base, cnt, lane);
       for (int j0 = 0; j0 < cnt; j0 += kSeUnroll) {
         float ws[kSeUnroll], wv[kSeUnroll][3], wt[kSeUnroll][5];
 #pragma unroll
@@ -833,36 +899,33 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
 #pragma unroll
         for (int u = 0; u < kSeUnroll; ++u) {
           if (j0 + u >= cnt) break;
-          const EdgeScalars q = edge_at(st, j0 + u);
+          const EdgeCoef<T2> q = coef_at<T2>(st, j0 + u);
           if (!q.ok) continue;
           if (hs) {
             const float gsv = ws[u];
-            z0 += q.r[0] * q.y0 * gsv;
+            z0 += q.c0 * gsv;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) z3[k] += q.r[3] * q.d[k] * gsv;
-            z8 += q.r[8] * gsv;
+            for (int k = 0; k < 3; ++k) z3[k] += q.c3[k] * gsv;
+            if (T2) z8 += q.c8 * gsv;
           }
           if (hv) {
             const float* w = wv[u];
-            z1 += q.r[1] * ((q.d[0] * w[0] + q.d[1] * w[1]) + q.d[2] * w[2]);
+            z1 += (q.c1[0] * w[0] + q.c1[1] * w[1]) + q.c1[2] * w[2];
 #pragma unroll
-            for (int k = 0; k < 3; ++k) z2[k] += q.r[2] * q.y0 * w[k];
-            z4[0] += q.r[4] * (w[1] * q.d[2] - w[2] * q.d[1]);  // w x d
-            z4[1] += q.r[4] * (w[2] * q.d[0] - w[0] * q.d[2]);
-            z4[2] += q.r[4] * (w[0] * q.d[1] - w[1] * q.d[0]);
+            for (int k = 0; k < 3; ++k) z2[k] += q.c2 * w[k];
+            z4[0] += w[1] * q.c4[2] - w[2] * q.c4[1];  // w x (r4 d)
+            z4[1] += w[2] * q.c4[0] - w[0] * q.c4[2];
+            z4[2] += w[0] * q.c4[1] - w[1] * q.c4[0];
           }
           if (ht) {
             const float* w = wt[u];
-            z5 += q.r[5] * ((((q.y2[0] * w[0] + q.y2[1] * w[1]) + q.y2[2] * w[2]) + q.y2[3] * w[3]) +
-                            q.y2[4] * w[4]);
+            z5 += (((q.c5[0] * w[0] + q.c5[1] * w[1]) + q.c5[2] * w[2]) + q.c5[3] * w[3]) + q.c5[4] * w[4];
 #pragma unroll
-            for (int k = 0; k < 5; ++k) z6[k] += q.r[6] * q.y0 * w[k];
-            float D[3][5];
-            cg_coef(g.cg, q.d, q.r[7], D);
+            for (int k = 0; k < 5; ++k) z6[k] += q.c6 * w[k];
 #pragma unroll
             for (int jj = 0; jj < 3; ++jj)
-              z7[jj] += (((D[jj][0] * w[0] + D[jj][1] * w[1]) + D[jj][2] * w[2]) + D[jj][3] * w[3]) +
-                        D[jj][4] * w[4];
+              z7[jj] += (((q.d7[jj][0] * w[0] + q.d7[jj][1] * w[1]) + q.d7[jj][2] * w[2]) + q.d7[jj][3] * w[3]) +
+                        q.d7[jj][4] * w[4];
           }
         }
       }
