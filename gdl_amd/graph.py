@@ -107,9 +107,11 @@ class SpatialGraph:
         else:
             B = 1
         avg = graph_avg_degree_hip(row_ptr, N, batch, B)
-        return SpatialGraph(row=row, col=col, direction=direction, dist=dist,
-                            col_sorted=col.to(torch.int32), perm=perm, node_start=node_start,
-                            node_end=node_end, Y=Y, N=N, E=E, avg_degree=avg)
+        graph = SpatialGraph(row=row, col=col, direction=direction, dist=dist,
+                             col_sorted=col.to(torch.int32), perm=perm, node_start=node_start,
+                             node_end=node_end, Y=Y, N=N, E=E, avg_degree=avg)
+        object.__setattr__(graph, "_perm_identity", True)  # kernels may skip the perm lookup
+        return graph
 
     @staticmethod
     def _empty(N: int, device: torch.device, max_l: int = 2) -> "SpatialGraph":

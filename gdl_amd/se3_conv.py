@@ -329,7 +329,9 @@ def se3_message_aggregate(
     cg_c = (ctypes.c_float * 45)(*[float(x) for x in cg.detach().reshape(-1).cpu().tolist()])
     row = graph.row.to(device=dev, dtype=torch.int64).contiguous()
     col = graph.col.to(device=dev, dtype=torch.int64).contiguous()
-    arrays = (row, col, graph.perm.to(device=dev, dtype=torch.int32).contiguous(),
+    perm = None if getattr(graph, "_perm_identity", False) else \
+        graph.perm.to(device=dev, dtype=torch.int32).contiguous()
+    arrays = (row, col, perm,
               graph.node_start.to(device=dev, dtype=torch.int32).contiguous(),
               graph.node_end.to(device=dev, dtype=torch.int32).contiguous(),
               _source_csr_getter(graph, row, N))
