@@ -163,6 +163,62 @@ def _se3_reference_torch(conv, s, v, gr):
     return out[:, :64] + conv.scalar_bias, out[:, 64:].reshape(gr.N, 16, 3)
 
 
+def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx, dist, gr, conv,
+                     fs, fv) -> dict:
+    """HIP-event time of single kernels of the fused rows on the C2 graph, with their algorithmic
+    bytes (every access of the kernel's pattern counted once: gathered rows per gather) and the
+    fraction of the 8 TB/s HBM peak."""
+    import ctypes
+    from gdl_amd import _native as nat
+    from gdl_amd.csrc import edge_geometry_hip
+    from gdl_amd.functional.gather import gather_weighted_sum, idw_weights
+    from gdl_amd.functional.segment_softmax import segment_softmax
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pad16, cg_11_2_cartesian, path_columns
+
+    def entry(us, nbytes):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+                "frac": round(gbs / 8000.0, 4)}
+
+    out = {}
+    E, N, H = row.numel(), pos.shape[0], scores.shape[1]
+    us = 1e3 * event_ms(lambda: segment_softmax(scores, perm, ns, ne, N), args.iters, 5)
+    out["segment_softmax_fwd"] = entry(us, 2 * E * H * 4 + E * 4 + 2 * N * 4)
+    w = idw_weights(idx, dist)
+    n_out, K = idx.shape
+    C = feats.shape[1]
+    us = 1e3 * event_ms(lambda: gather_weighted_sum(feats, idx, w), args.iters, 5)
+    out["gather_weighted_sum_k3_c112"] = entry(us, n_out * K * (8 + 4 + C * 4) + n_out * C * 4)
+    with torch.no_grad():
+        us = 1e3 * event_ms(lambda: edge_geometry_hip(pos, row, col, 2), args.iters, 5)
+    out["edge_geometry_l2"] = entry(us, E * (16 + 24 + 52))
+    # the SE3 forward aggregate alone (sums of r-weighted source features per target)
+    Cs, Cv = fs.shape[1], fv.shape[1]
+    weights = {k: getattr(conv, k).weight if getattr(conv, k) is not None else None for k in PATH_NAMES}
+    pc = path_columns(weights, False, True, 0)
+    with torch.no_grad():
+        R = conv.radial_basis(gr.dist)
+    P = R.shape[1]
+    plan = _Plan(Cs, Cv, 0, conv.out_scalar_channels, conv.out_vector_channels, 0, pc, P, 9, False)
+    Xs = torch.empty(N, plan.Ks, device=dev)
+    Xv = torch.empty(N, 3, plan.Kv, device=dev)
+    cg = (ctypes.c_float * 45)(*cg_11_2_cartesian().reshape(-1).tolist())
+    s_, v_ = fs.detach().contiguous(), fv.detach().contiguous()
+    Y, d = gr.Y.detach().contiguous(), gr.direction.detach().contiguous()
+
+    def agg():
+        nat.check(nat.lib().geo_se3_aggregate_fwd(
+            nat.ptr(s_), nat.ptr(v_), None, N, Cs, Cv, 0, nat.ptr(gr.row), None, nat.ptr(gr.node_start),
+            nat.ptr(gr.node_end), E, nat.ptr(d), nat.ptr(Y), 9, nat.ptr(R), P, plan.pc_c, cg,
+            nat.ptr(Xs), plan.Ks, nat.ptr(Xv), plan.Kv, None, 0, nat.stream_of(dev)), "aggregate")
+
+    us = 1e3 * event_ms(agg, args.iters, 5)
+    out["se3_fwd_aggregate_64s16v"] = entry(
+        us, E * (Cs + 3 * Cv) * 4 + E * (8 + 4 * P + 12 + 4) + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4)
+    assert _pad16(Cs + 2 * Cv) == plan.Kv
+    return out
+
+
 def wall_ms(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
@@ -336,6 +392,11 @@ def main() -> int:
         log(f"  SE3Conv 64s+16v (E={gr.E}): fused {legs['c2_se3conv_fwd_ms']:.3f} ms fwd, "
             f"{legs['c2_se3conv_fwd_bwd_ms']:.3f} ms fwd+bwd; reference op sequence in PyTorch "
             f"{legs['c2_se3conv_torch_ref_fwd_ms']:.3f} / {legs['c2_se3conv_torch_ref_fwd_bwd_ms']:.3f} ms")
+        legs["c2_fused_rooflines"] = _fused_rooflines(args, dev, pos, row, col, pm, ns, ne, scores,
+                                                      feats, ii, dd, gr, conv, fs, fv)
+        for name, r in legs["c2_fused_rooflines"].items():
+            log(f"  {name}: {r['us']} us, {r['GB/s']} GB/s = {100 * r['frac']:.1f}% of 8 TB/s "
+                f"({r['bytes']} algorithmic bytes)")
 
     # ---------------------------------------------------------------- C3 roofline ---
     roof = None
