@@ -30,6 +30,8 @@ _SIGNATURES = {
     "geo_build_info": (ctypes.c_char_p, []),
     "geo_abi_version": (c_int, []),
     "geo_fps_prepare": (c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "geo_fps_prepare_uniform": (c_int, [c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
+    "geo_fps_guarded": (c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp]),
     "geo_fps_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "geo_fps": (c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_size, c_vp]),
     "geo_knn_workspace_bytes": (c_size, [c_i64, c_i64, c_i64, c_i64]),

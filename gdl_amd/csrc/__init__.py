@@ -18,6 +18,7 @@ Differences from the reference, by design:
 
 from __future__ import annotations
 
+import ctypes
 import logging
 from typing import Optional, Tuple
 
@@ -625,14 +626,73 @@ def fps_cuda(pos: Tensor, ptr: Tensor, k_per_batch: Tensor) -> Tensor:
         raise ValueError("fps: ptr must have at least one entry")
     if kk.numel() != B:
         raise ValueError(f"fps: k_per_batch has {kk.numel()} entries for {B} clouds")
+    return _fps_run(pos, p, B, lambda L, out_ptr, info, s: L.geo_fps_prepare(
+        _nat.ptr(p), _nat.ptr(kk), B, pos.shape[0], _nat.ptr(out_ptr), _nat.ptr(info), s))
+
+
+def fps_uniform_hip(pos: Tensor, ptr: Tensor, num_samples: int) -> Tensor:
+    """``fps_cuda(pos, ptr, (ptr[1:] - ptr[:-1]).clamp(max=num_samples))``, the ptr path of
+    ``farthest_point_sampling``, with the host sync taken off the GPU's critical path.
+
+    The prepare kernel forms the per-cloud k and writes its summary (total, largest cloud,
+    validity) to device memory and to a pinned host buffer.  The sampling kernel for clouds of
+    the average size is launched right behind it, before the host has read anything; it reads
+    the device summary itself and does nothing if ptr is invalid or a cloud is larger than it
+    holds.  The host waits only for the prepare kernel (an event), and launches the right kernel
+    itself in that case.  The output is allocated at its bound min(N, B * num_samples) and
+    returned as the prefix of length total."""
+    _require_gpu("fps", pos)
+    pos = _positions("fps", pos)
+    dev = pos.device
+    p = _i64(ptr, dev)
+    B = p.numel() - 1
+    if B < 0:
+        raise ValueError("fps: ptr must have at least one entry")
+    N = pos.shape[0]
+    k = max(int(num_samples), 0)
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        s = _nat.stream_of(dev)
+        out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
+        info = torch.empty(3, dtype=torch.int64, device=dev)
+        info_h = torch.empty(3, dtype=torch.int64, pin_memory=True)
+        out = torch.empty(min(N, B * k), dtype=torch.int64, device=dev)
+        _nat.check(L.geo_fps_prepare_uniform(_nat.ptr(p), k, B, N, _nat.ptr(out_ptr),
+                                             _nat.ptr(info), info_h.data_ptr(), s),
+                   "geo_fps_prepare_uniform")
+        prepared = torch.cuda.Event()
+        prepared.record(torch.cuda.current_stream(dev))
+        cap = ctypes.c_int64(0)
+        guess = -(-N // B) if B > 0 and out.numel() > 0 else 0
+        _nat.check(L.geo_fps_guarded(_nat.ptr(pos), N, _nat.ptr(p), _nat.ptr(out_ptr), B, guess,
+                                     _nat.ptr(out), _nat.ptr(info), ctypes.byref(cap), s),
+                   "geo_fps_guarded")
+        prepared.synchronize()
+        total, max_n, bad = info_h.tolist()
+        if bad:
+            raise ValueError(f"fps: ptr is not a non-decreasing offset array within [0, {N}] "
+                             f"(first bad entry: ptr[{bad - 1}])")
+        if total < out.numel():
+            out = out[:total]
+        if total == 0 or 0 < max_n <= cap.value:
+            return out
+        ws_bytes = L.geo_fps_workspace_bytes(B, N, max_n)
+        ws = _nat.workspace(ws_bytes, dev)
+        _nat.check(L.geo_fps(_nat.ptr(pos), N, _nat.ptr(p), _nat.ptr(out_ptr), B, max_n,
+                             _nat.ptr(out), _nat.ptr(ws), ws_bytes, s), "geo_fps")
+    return out
+
+
+def _fps_run(pos: Tensor, p: Tensor, B: int, prepare) -> Tensor:
+    """prepare (offsets, total, largest cloud, validity) -> one host sync -> geo_fps."""
+    dev = pos.device
     N = pos.shape[0]
     L = _nat.lib()
     with torch.cuda.device(dev):
         s = _nat.stream_of(dev)
         out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
         info = torch.empty(3, dtype=torch.int64, device=dev)
-        _nat.check(L.geo_fps_prepare(_nat.ptr(p), _nat.ptr(kk), B, N, _nat.ptr(out_ptr),
-                                     _nat.ptr(info), s), "geo_fps_prepare")
+        _nat.check(prepare(L, out_ptr, info, s), "geo_fps_prepare")
         total, max_n, bad = info.tolist()
         if bad:
             raise ValueError(f"fps: ptr is not a non-decreasing offset array within [0, {N}] "
@@ -662,5 +722,5 @@ __all__ = [
     "graph_avg_degree_hip",
     "segment_reduce_forward_hip", "segment_reduce_backward_hip",
     "knn_available", "knn_cuda", "knn_self_cuda",
-    "fps_available", "fps_cuda",
+    "fps_available", "fps_cuda", "fps_uniform_hip",
 ]

@@ -37,8 +37,9 @@ struct alignas(8) FpsSlot {
 
 // prepare: clamp k to [0, n], exclusive offsets, total, max cloud, ptr validation.
 __global__ __launch_bounds__(kScanThreads) void fps_prepare_kernel(
-    const int64_t* __restrict__ ptr, const int64_t* __restrict__ kpb, int64_t B, int64_t N_total,
-    int64_t* __restrict__ out_ptr, int64_t* __restrict__ info) {
+    const int64_t* __restrict__ ptr, const int64_t* __restrict__ kpb, int64_t k_all, int64_t B,
+    int64_t N_total, int64_t* __restrict__ out_ptr, int64_t* __restrict__ info,
+    int64_t* __restrict__ info_host) {
   __shared__ int64_t lds[kScanThreads / kWave];
   __shared__ unsigned long long s_max, s_bad;
   constexpr unsigned long long kNone = ~0ull;
@@ -56,7 +57,7 @@ __global__ __launch_bounds__(kScanThreads) void fps_prepare_kernel(
       const int64_t n = p1 - p0;
       if (n < 0 || p1 > N_total) atomicMin(&s_bad, static_cast<unsigned long long>(b + 2));
       const int64_t nn = n > 0 ? n : 0;
-      k = kpb[b];
+      k = kpb ? kpb[b] : k_all;  // one k for every cloud when no per-cloud array is given
       k = k < 0 ? 0 : (k > nn ? nn : k);
       atomicMax(&s_max, static_cast<unsigned long long>(nn));
     }
@@ -67,10 +68,17 @@ __global__ __launch_bounds__(kScanThreads) void fps_prepare_kernel(
   }
   __syncthreads();
   if (threadIdx.x == 0) {
+    const int64_t bad = s_bad == kNone ? 0 : static_cast<int64_t>(s_bad);
     out_ptr[B] = carry;
     info[0] = carry;
     info[1] = static_cast<int64_t>(s_max);
-    info[2] = s_bad == kNone ? 0 : static_cast<int64_t>(s_bad);
+    info[2] = bad;
+    if (info_host) {  // mapped pinned host copy, read by the host once this kernel has finished
+      info_host[0] = carry;
+      info_host[1] = static_cast<int64_t>(s_max);
+      info_host[2] = bad;
+      __threadfence_system();
+    }
   }
 }
 
@@ -193,9 +201,13 @@ __device__ __forceinline__ int cell16(float p, float lo, float scale) {
 template <int PTS, int THREADS>
 __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ ptr,
-    const int64_t* __restrict__ out_ptr, int64_t* __restrict__ out_idx) {
+    const int64_t* __restrict__ out_ptr, int64_t* __restrict__ out_idx,
+    const int64_t* __restrict__ guard) {
   constexpr int WAVES = THREADS / kWave;
   static_assert(PTS <= kWave, "one lane per bucket");
+  // Launched before the host has seen the prepare kernel's summary: do nothing unless ptr was
+  // valid and every cloud fits this variant (the host then launches the right one).
+  if (guard != nullptr && (guard[2] != 0 || guard[1] > PTS * THREADS)) return;
   // Cross-wave argmax: one 64-bit LDS atomic max per wave on key (bits << 32) | ~index, so the
   // largest distance wins and, among equal distances, the lowest index.  Three slots rotate:
   // iteration it uses slot it % 3 and clears slot (it + 1) % 3, whose last readers finished
@@ -407,13 +419,14 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
 
 template <int PTS, int THREADS>
 int launch_bucket(const float* pos, const int64_t* ptr, const int64_t* out_ptr, int64_t B,
-                  int64_t max_cloud, int64_t* out, hipStream_t st) {
+                  int64_t max_cloud, int64_t* out, hipStream_t st,
+                  const int64_t* guard = nullptr) {
   const size_t lds = static_cast<size_t>(max_cloud > 0 ? max_cloud : 1) * sizeof(float4);
   GEO_HIP_CHECK(hipFuncSetAttribute(
       reinterpret_cast<const void*>(&fps_bucket_kernel<PTS, THREADS>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFpsLdsPoints * sizeof(float4))));
   hipLaunchKernelGGL((fps_bucket_kernel<PTS, THREADS>), dim3(B), dim3(THREADS), lds, st, pos, ptr,
-                     out_ptr, out);
+                     out_ptr, out, guard);
   GEO_LAUNCH_CHECK("fps_bucket_kernel");
   return GEO_OK;
 }
@@ -814,9 +827,51 @@ extern "C" int geo_fps_prepare(const int64_t* ptr, const int64_t* k_per_batch, i
   GEO_REQUIRE(B >= 0 && N_total >= 0, "fps_prepare: negative size");
   GEO_REQUIRE(ptr && out_ptr && info && (B == 0 || k_per_batch), "fps_prepare: null pointer");
   hipLaunchKernelGGL(fps_prepare_kernel, dim3(1), dim3(kScanThreads), 0, as_stream(stream), ptr,
-                     k_per_batch, B, N_total, out_ptr, info);
+                     k_per_batch, int64_t{0}, B, N_total, out_ptr, info,
+                     static_cast<int64_t*>(nullptr));
   GEO_LAUNCH_CHECK("fps_prepare_kernel");
   return GEO_OK;
+}
+
+extern "C" int geo_fps_prepare_uniform(const int64_t* ptr, int64_t k, int64_t B, int64_t N_total,
+                                       int64_t* out_ptr, int64_t* info, int64_t* info_host,
+                                       void* stream) {
+  GEO_REQUIRE(B >= 0 && N_total >= 0, "fps_prepare: negative size");
+  GEO_REQUIRE(ptr && out_ptr && info, "fps_prepare: null pointer");
+  int64_t* host_dev = nullptr;
+  if (info_host) {
+    GEO_HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&host_dev), info_host, 0));
+    GEO_REQUIRE(host_dev != nullptr, "fps_prepare: info_host is not mapped pinned memory");
+  }
+  hipLaunchKernelGGL(fps_prepare_kernel, dim3(1), dim3(kScanThreads), 0, as_stream(stream), ptr,
+                     static_cast<const int64_t*>(nullptr), k, B, N_total, out_ptr, info, host_dev);
+  GEO_LAUNCH_CHECK("fps_prepare_kernel");
+  return GEO_OK;
+}
+
+extern "C" int geo_fps_guarded(const float* pos, int64_t N_total, const int64_t* ptr,
+                               const int64_t* out_ptr, int64_t B, int64_t max_cloud_guess,
+                               int64_t* out_idx, const int64_t* info, int64_t* capacity,
+                               void* stream) {
+  GEO_REQUIRE(capacity != nullptr, "fps_guarded: null capacity");
+  *capacity = 0;
+  GEO_REQUIRE(B >= 0 && N_total >= 0 && max_cloud_guess >= 0, "fps_guarded: negative size");
+  GEO_REQUIRE(N_total < 0x7fffffffLL, "fps: N_total exceeds int32 indexing");
+  if (B == 0 || max_cloud_guess == 0 || max_cloud_guess > kFpsLdsPoints) return GEO_OK;
+  GEO_REQUIRE(pos && ptr && out_ptr && out_idx && info, "fps_guarded: null pointer");
+  hipStream_t st = as_stream(stream);
+  const int64_t p2 = ceil_div(max_cloud_guess, kFpsBucketThreads);
+  const int pts = p2 <= 1 ? 1 : (p2 <= 2 ? 2 : (p2 <= 4 ? 4 : 8));
+  const int64_t cap = static_cast<int64_t>(pts) * kFpsBucketThreads;
+  int rc;
+  switch (pts) {
+    case 1: rc = launch_bucket<1, kFpsBucketThreads>(pos, ptr, out_ptr, B, cap, out_idx, st, info); break;
+    case 2: rc = launch_bucket<2, kFpsBucketThreads>(pos, ptr, out_ptr, B, cap, out_idx, st, info); break;
+    case 4: rc = launch_bucket<4, kFpsBucketThreads>(pos, ptr, out_ptr, B, cap, out_idx, st, info); break;
+    default: rc = launch_bucket<8, kFpsBucketThreads>(pos, ptr, out_ptr, B, cap, out_idx, st, info); break;
+  }
+  if (rc == GEO_OK) *capacity = cap;
+  return rc;
 }
 
 extern "C" size_t geo_fps_workspace_bytes(int64_t B, int64_t N_total, int64_t max_cloud) {

@@ -41,12 +41,11 @@ def farthest_point_sampling(
 
 
 def _fps_batched_ptr(pos: Tensor, num_samples: int, ptr: Tensor) -> Tensor:
-    from gdl_amd.csrc import fps_cuda
+    """k_per_batch = clamp(sizes, max=num_samples) (reference fps.py:108-109), formed on the
+    device by the prepare kernel."""
+    from gdl_amd.csrc import fps_uniform_hip
 
-    ptr = ptr.to(device=pos.device, dtype=torch.int64)
-    sizes = ptr[1:] - ptr[:-1]
-    k_per_batch = sizes.clamp(max=int(num_samples))
-    return fps_cuda(pos, ptr, k_per_batch)
+    return fps_uniform_hip(pos, ptr, num_samples)
 
 
 def _fps_single(pos: Tensor, num_samples: int) -> Tensor:

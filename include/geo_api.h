@@ -72,6 +72,22 @@ int geo_abi_version(void);
  */
 int geo_fps_prepare(const int64_t* ptr, const int64_t* k_per_batch, int64_t B, int64_t N_total,
                     int64_t* out_ptr, int64_t* info, void* stream);
+/* geo_fps_prepare with k_per_batch[b] = k for every cloud: the ptr path of the public op
+ * (geoembodied/functional/fps.py:84-118, `k_per_batch = sizes.clamp(max=num_samples)` at
+ * :108-109) without the two elementwise launches that form that array.  info_host (may be
+ * NULL) is pinned host memory of 3 int64 (hipHostMalloc'd, e.g. a torch pin_memory tensor) that
+ * also receives info, so the host can read it after an event recorded behind this launch
+ * instead of copying it behind later work on the stream. */
+int geo_fps_prepare_uniform(const int64_t* ptr, int64_t k, int64_t B, int64_t N_total,
+                            int64_t* out_ptr, int64_t* info, int64_t* info_host, void* stream);
+/* geo_fps for clouds of at most max_cloud_guess points, launched before the host has read
+ * info: the kernel reads info (device copy) and does nothing when ptr was invalid or the
+ * largest cloud exceeds the variant's capacity, which is returned in *capacity (0 = nothing
+ * launched, as for guesses above 8192 points).  The caller then checks info[1] <= *capacity
+ * and otherwise calls geo_fps.  Replaces the same kernel call as geo_fps. */
+int geo_fps_guarded(const float* pos, int64_t N_total, const int64_t* ptr, const int64_t* out_ptr,
+                    int64_t B, int64_t max_cloud_guess, int64_t* out_idx, const int64_t* info,
+                    int64_t* capacity, void* stream);
 size_t geo_fps_workspace_bytes(int64_t B, int64_t N_total, int64_t max_cloud);
 int geo_fps(const float* pos, int64_t N_total, const int64_t* ptr, const int64_t* out_ptr,
             int64_t B, int64_t max_cloud, int64_t* out_idx, void* workspace,

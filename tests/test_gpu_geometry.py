@@ -120,6 +120,44 @@ def test_fps_api_variants(dev):
     np.testing.assert_array_equal(got, np.concatenate(want))
 
 
+@pytest.mark.parametrize("sizes,k", [
+    ([4096] * 4, 1024),                 # every cloud the average size: the early launch is right
+    ([100, 3000], 700),                 # average 1550 -> 2048-point variant; 3000 needs the next
+    ([5000, 20, 0, 7], 9),              # empty and tiny clouds, k >= n for some
+    ([9000, 100], 64),                  # average above 8192 points: no early launch
+    ([12000, 3000, 3000], 100),         # average in range, largest cloud beyond the bucket kernels
+    ([300, 300], 0),                    # nothing selected
+    ([64, 64, 64], 64),                 # k == n everywhere
+])
+def test_fps_ptr_path_vs_oracle(dev, sizes, k):
+    """The ptr path launches the sampling kernel for the average cloud size before the host has
+    read the prepare summary; the kernel must do nothing when a cloud is larger, and the host then
+    runs the right variant."""
+    fps, *_ = _f()
+    g = torch.Generator().manual_seed(sum(sizes) + k)
+    pos = torch.randn(sum(sizes), 3, generator=g)
+    ptr = _ptr(sizes)
+    got = fps(pos.to(dev), k, ptr=ptr.to(dev))
+    want = oracle.fps(pos.numpy(), ptr.numpy(), np.minimum(np.diff(ptr.numpy()), k))
+    assert got.dtype == torch.int64 and got.is_contiguous()
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def test_fps_ptr_path_invalid_and_repeated(dev):
+    fps, *_ = _f()
+    pos = torch.randn(5000, 3, device=dev)
+    with pytest.raises(ValueError):
+        fps(pos, 4, ptr=torch.tensor([0, 4000, 3000, 5000], device=dev))
+    with pytest.raises(ValueError):
+        fps(pos, 4, ptr=torch.tensor([0, 2000, 5001], device=dev))
+    # valid calls right after, with a smaller problem second: nothing stale from the earlier ones
+    cpu = pos.cpu().numpy()
+    for ptr, k in (([0, 2500, 5000], 300), ([0, 10, 40], 5)):
+        got = fps(pos, k, ptr=torch.tensor(ptr, device=dev)).cpu().numpy()
+        want = oracle.fps(cpu, np.array(ptr), np.minimum(np.diff(ptr), k))
+        np.testing.assert_array_equal(got, want)
+
+
 def test_fps_invalid_ptr_raises(dev):
     from gdl_amd.csrc import fps_cuda
     pos = torch.randn(10, 3, device=dev)
