@@ -369,11 +369,14 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
     int first[EPV];
     int cnt[EPV];
     int jcur = -1;
-    auto reset = [&]() {
+    // `pos0` is the position of the segment's first row in this range: with a valid
+    // permutation that row is taken, so a first maximum of -inf (equal to the initial value)
+    // is recorded there without a separate "nothing seen yet" test per element.
+    auto reset = [&](int pos0) {
 #pragma unroll
       for (int i = 0; i < EPV; ++i) {
         acc[i] = MAX ? -__builtin_inf() : A(0);
-        first[i] = 0x7fffffff;
+        first[i] = pos0;
         cnt[i] = 0;
       }
     };
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
       for (int u = 0; u < U; ++u) rows[u] = PERM ? perm[e[u]] : e[u];
     };
 
-    reset();
+    reset(0x7fffffff);
     int e[U], rows[U];
     locate(lo, e, rows);
     for (int k = 0; k < steps; ++k) {
@@ -457,7 +460,7 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
         const int j = seg_of(f);
         if (live && j != jcur) {
           if (jcur >= 0) finish();
-          reset();
+          reset(MAX ? ecur[MAX ? u : 0] : 0);
           jcur = j;
         }
         const bool take = live && ((rok >> u) & 1u);
@@ -468,7 +471,7 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
             const bool gt = take && max_gt(v, acc[i]);
             const bool eq = take && !gt && max_eq(v, acc[i]);
             const int pos = ecur[MAX ? u : 0];
-            first[i] = (gt || (eq && cnt[i] == 0)) ? pos : first[i];
+            first[i] = gt ? pos : first[i];
             cnt[i] = gt ? 1 : cnt[i] + (eq ? 1 : 0);
             acc[i] = gt ? v : acc[i];
           } else {
