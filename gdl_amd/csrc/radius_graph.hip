@@ -13,13 +13,15 @@
 //   rg_cell     cell id per point, rank inside the cell (atomic counter)
 //   scan        cell offsets
 //   rg_scatter  points in cell order as float4 (x, y, z, index bits)
-//   rg_query<0> one thread per point in cell order (neighbouring threads share cells): count
-//               of in-radius sources over the 9 z-contiguous runs of the 27-cell stencil
+//   rg_count    kRgGroup lanes per point in cell order (neighbouring groups share cells): count
+//               of in-radius sources over the 9 z-contiguous runs of the 27-cell stencil, and
+//               the first K accepted sources in a per-target list
 //   scan        row_ptr = exclusive scan of min(count, K) over target index
 // geo_radius_emit:
-//   rg_query<1> re-scans, keeps all accepted sources when count <= K, otherwise the K smallest
-//               (d, j) found by a bitwise threshold search; sources are kept sorted by index
-//               in an LDS list (K <= 256) or directly in the output row, then written.
+//   rg_compact  kRgGroup lanes per target: the list sorted by source index into the CSR row;
+//               a target with more than K sources first rebuilds its list with the K smallest
+//               (d, j), found by a bitwise threshold search
+//   rg_emit     (lists too large for the workspace) re-scans the stencil per target instead
 // Traversal order inside a cell is not deterministic (atomic ranks) and does not matter: the
 // accepted set is defined by a total order and the output is sorted.
 #include "scan.hpp"
@@ -31,7 +33,6 @@ constexpr int kRgThreads = 256;
 constexpr int kRgEmitThreads = 64;
 constexpr int kRgMaxAxis = 16384;
 constexpr int kRgLdsK = 256;
-constexpr int kRgStageK = 64;
 
 struct Grid {
   float ox, oy, oz, inv_h;
@@ -121,6 +122,60 @@ __global__ void rg_init(RgWs w, int64_t N, int64_t B) {
   }
 }
 
+// Single workgroup: grid parameters and cell bases for every cloud.
+__global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, float r_cell) {
+  __shared__ int64_t lds[kScanThreads / kWave];
+  r_cell = rg_rcell(w, r_cell);
+  int64_t carry = 0;
+  for (int64_t base = 0; base < B; base += kScanThreads) {
+    const int64_t b = base + threadIdx.x;
+    int64_t cells = 0;
+    Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
+    if (b < B && w.cloud_n[b] > 0) {
+      const uint32_t* bb = w.bbox + 6 * b;
+      const float mn[3] = {float_from_order_key(bb[0]), float_from_order_key(bb[1]),
+                           float_from_order_key(bb[2])};
+      const float mx[3] = {float_from_order_key(bb[3]), float_from_order_key(bb[4]),
+                           float_from_order_key(bb[5])};
+      const double cap = 4.0 * w.cloud_n[b] + 64.0;
+      double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
+      double ext[3];
+      for (int a = 0; a < 3; ++a) {
+        const double e = static_cast<double>(mx[a]) - static_cast<double>(mn[a]);
+        ext[a] = (e >= 0.0 && e < 1e30) ? e : 0.0;  // non-finite input: one slab on that axis
+      }
+      int64_t d[3] = {1, 1, 1};
+      bool ok = false;
+      for (int iter = 0; iter < 64 && !ok; ++iter) {
+        double prod = 1.0, worst_axis = 0.0;
+        for (int a = 0; a < 3; ++a) {
+          const double q = floor(ext[a] / h) + 1.0;
+          d[a] = q < static_cast<double>(kRgMaxAxis) * 4 ? static_cast<int64_t>(q) : kRgMaxAxis * 4;
+          prod *= static_cast<double>(d[a]);
+          worst_axis = fmax(worst_axis, static_cast<double>(d[a]) / kRgMaxAxis);
+        }
+        ok = prod <= cap && worst_axis <= 1.0;
+        if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst_axis), 1.0) * 1.01;
+      }
+      g.ox = mn[0]; g.oy = mn[1]; g.oz = mn[2];
+      g.inv_h = static_cast<float>(1.0 / h);
+      if (!ok) {  // one cell holds the whole cloud
+        d[0] = d[1] = d[2] = 1;
+        g.inv_h = 0.f;
+      }
+      g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
+      cells = d[0] * d[1] * d[2];
+    }
+    int64_t total;
+    const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
+    if (b < B) {
+      g.base = static_cast<int>(carry + off);
+      w.grid[b] = g;
+    }
+    carry += total;
+  }
+}
+
 __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __restrict__ x, int64_t N,
                                                       const int64_t* __restrict__ batch, int64_t B,
                                                       int64_t ppc, const uint8_t* __restrict__ mask) {
@@ -181,60 +236,6 @@ __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __res
         atomicMax(&bb[3], s_red[3][ww]); atomicMax(&bb[4], s_red[4][ww]); atomicMax(&bb[5], s_red[5][ww]);
       }
     }
-  }
-}
-
-// Single workgroup: grid parameters and cell bases for every cloud.
-__global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, float r_cell) {
-  __shared__ int64_t lds[kScanThreads / kWave];
-  r_cell = rg_rcell(w, r_cell);
-  int64_t carry = 0;
-  for (int64_t base = 0; base < B; base += kScanThreads) {
-    const int64_t b = base + threadIdx.x;
-    int64_t cells = 0;
-    Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
-    if (b < B && w.cloud_n[b] > 0) {
-      const uint32_t* bb = w.bbox + 6 * b;
-      const float mn[3] = {float_from_order_key(bb[0]), float_from_order_key(bb[1]),
-                           float_from_order_key(bb[2])};
-      const float mx[3] = {float_from_order_key(bb[3]), float_from_order_key(bb[4]),
-                           float_from_order_key(bb[5])};
-      const double cap = 4.0 * w.cloud_n[b] + 64.0;
-      double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
-      double ext[3];
-      for (int a = 0; a < 3; ++a) {
-        const double e = static_cast<double>(mx[a]) - static_cast<double>(mn[a]);
-        ext[a] = (e >= 0.0 && e < 1e30) ? e : 0.0;  // non-finite input: one slab on that axis
-      }
-      int64_t d[3] = {1, 1, 1};
-      bool ok = false;
-      for (int iter = 0; iter < 64 && !ok; ++iter) {
-        double prod = 1.0, worst_axis = 0.0;
-        for (int a = 0; a < 3; ++a) {
-          const double q = floor(ext[a] / h) + 1.0;
-          d[a] = q < static_cast<double>(kRgMaxAxis) * 4 ? static_cast<int64_t>(q) : kRgMaxAxis * 4;
-          prod *= static_cast<double>(d[a]);
-          worst_axis = fmax(worst_axis, static_cast<double>(d[a]) / kRgMaxAxis);
-        }
-        ok = prod <= cap && worst_axis <= 1.0;
-        if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst_axis), 1.0) * 1.01;
-      }
-      g.ox = mn[0]; g.oy = mn[1]; g.oz = mn[2];
-      g.inv_h = static_cast<float>(1.0 / h);
-      if (!ok) {  // one cell holds the whole cloud
-        d[0] = d[1] = d[2] = 1;
-        g.inv_h = 0.f;
-      }
-      g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
-      cells = d[0] * d[1] * d[2];
-    }
-    int64_t total;
-    const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
-    if (b < B) {
-      g.base = static_cast<int>(carry + off);
-      w.grid[b] = g;
-    }
-    carry += total;
   }
 }
 
@@ -359,12 +360,14 @@ __device__ __forceinline__ void threshold_select(const RgWs& w, const Grid& g, f
   jstar = jlo;
 }
 
-template <int MODE>  // 0 = count, 1 = emit
-__global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, int64_t ppc,
-                         float r2, int K, int loop, const int64_t* __restrict__ row_ptr,
-                         int64_t* __restrict__ row_out, int64_t* __restrict__ col_out,
-                         int use_lds) {
-  extern __shared__ int32_t lbuf[];  // emit: K entries per thread, column-major by thread
+// Emit pass without the per-target lists (when they would not fit the workspace): one thread per
+// target re-scans the stencil, keeping all accepted sources (count <= K) or the K smallest (d, j)
+// found by the threshold search, sorted by index in an LDS column (K <= kRgLdsK) or directly in
+// the output row.
+__global__ void rg_emit(RgWs w, const int64_t* __restrict__ batch, int64_t B, int64_t ppc,
+                        float r2, int K, int loop, const int64_t* __restrict__ row_ptr,
+                        int64_t* __restrict__ row_out, int64_t* __restrict__ col_out, int use_lds) {
+  extern __shared__ int32_t lbuf[];  // K entries per thread, column-major by thread
   r2 = rg_r2(w, r2);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int total = w.cell_start[w.cells_max];
@@ -374,61 +377,154 @@ __global__ void rg_query(RgWs w, const int64_t* __restrict__ batch, int64_t B, i
   const int b = cloud_of(qi, batch, B, ppc);
   const Grid g = w.grid[b];
   const bool lp = loop != 0;
-  if constexpr (MODE == 0) {
-    int c = 0;
-    int32_t* L = w.list ? w.list + static_cast<int64_t>(qi) * K : nullptr;
+  const int c = w.cnt[qi];
+  if (c == 0) return;
+  const int64_t o = row_ptr[qi];
+  RowList lst;
+  lst.lds = use_lds ? lbuf + threadIdx.x : nullptr;
+  lst.out = row_out + o;
+  if (c <= K) {
+    for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
+      if (d < r2) lst.insert(j);
+    });
+  } else {
+    uint32_t dstar;
+    int jstar;
+    threshold_select(w, g, q.x, q.y, q.z, qi, lp, r2, K, dstar, jstar);
     for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
       if (d < r2) {
-        if (L && c < K) L[c] = j;
-        ++c;
+        const uint32_t db = __float_as_uint(d);
+        if (db < dstar || (db == dstar && j <= jstar)) lst.insert(j);
       }
     });
-    w.cnt[qi] = c;
-    w.deg[qi] = c < K ? c : K;
-  } else {
-    const int c = w.cnt[qi];
-    if (c == 0) return;
-    const int64_t o = row_ptr[qi];
-    RowList lst;
-    lst.lds = use_lds ? lbuf + threadIdx.x : nullptr;
-    lst.out = row_out + o;
-    if (c <= K) {
-      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
-        if (d < r2) lst.insert(j);
-      });
-    } else {
-      uint32_t dstar;
-      int jstar;
-      threshold_select(w, g, q.x, q.y, q.z, qi, lp, r2, K, dstar, jstar);
-      for_each_candidate(w, g, q.x, q.y, q.z, qi, lp, [&](float d, int j) {
-        if (d < r2) {
-          const uint32_t db = __float_as_uint(d);
-          if (db < dstar || (db == dstar && j <= jstar)) lst.insert(j);
-        }
-      });
-    }
-    for (int m = 0; m < lst.n; ++m) {
-      if (lst.lds) row_out[o + m] = lst.get(m);
-      col_out[o + m] = qi;
-    }
+  }
+  for (int m = 0; m < lst.n; ++m) {
+    if (lst.lds) row_out[o + m] = lst.get(m);
+    col_out[o + m] = qi;
   }
 }
 
-// After the edge count is known: one thread per target writes its row, sources ascending.  The
-// collected list is unsorted (cell traversal order); each source goes to position
-// row_ptr[i] + (number of smaller sources in the list).  Targets with more than K sources
-// rebuild their list with the exact (d, j) threshold first.
-__global__ void rg_compact(RgWs w, const float* __restrict__ x, int64_t N,
-                           const int64_t* __restrict__ batch, int64_t B, int64_t ppc, float r2,
-                           int K, int loop, const int64_t* __restrict__ row_ptr,
-                           int64_t* __restrict__ row_out, int64_t* __restrict__ col_out) {
-  extern __shared__ int32_t stage[];  // K entries per thread when K <= kRgStageK
+// Count pass with kRgGroup lanes per target (targets in cell order, so neighbouring groups
+// share cells).  The 18 run bounds of the 3x3 stencil columns are loaded at once, then the first
+// kRgGroup sources of all nine runs (one float4 per lane per run, all in flight together);
+// longer runs continue chunk by chunk.  Accepted sources are appended to the target's list in
+// ballot order (the list is unsorted; the compaction sorts it), the count is the group's total.
+constexpr int kRgGroup = 8;
+
+__global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __restrict__ batch,
+                                                       int64_t B, int64_t ppc, float r2, int K,
+                                                       int loop) {
   r2 = rg_r2(w, r2);
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t t = (static_cast<int64_t>(blockIdx.x) * kRgThreads + threadIdx.x) / kRgGroup;
+  const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
+  const int total = w.cell_start[w.cells_max];
+  if (t >= total) return;  // the whole group leaves together
+  const float4 q = w.spos[t];
+  const int qi = __float_as_int(q.w);
+  const int b = cloud_of(qi, batch, B, ppc);
+  const Grid g = w.grid[b];
+  const int cx = cell_coord(q.x, g.ox, g.inv_h, g.dx);
+  const int cy = cell_coord(q.y, g.oy, g.inv_h, g.dy);
+  const int cz = cell_coord(q.z, g.oz, g.inv_h, g.dz);
+  const int z0 = cz > 0 ? cz - 1 : 0;
+  const int z1 = cz + 1 < g.dz ? cz + 1 : g.dz - 1;
+  int ra[9], rn[9];
+#pragma unroll
+  for (int r = 0; r < 9; ++r) {
+    const int ix = cx - 1 + r / 3, iy = cy - 1 + r % 3;
+    const bool in = ix >= 0 && ix < g.dx && iy >= 0 && iy < g.dy;
+    const int c0 = g.base + (ix * g.dy + iy) * g.dz;
+    const int a = in ? w.cell_start[c0 + z0] : 0;
+    const int e = in ? w.cell_start[c0 + z1 + 1] : 0;
+    ra[r] = a;
+    rn[r] = e - a;
+  }
+  float4 sv[9];
+#pragma unroll
+  for (int r = 0; r < 9; ++r) sv[r] = sub < rn[r] ? w.spos[ra[r] + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+  int32_t* L = w.list ? w.list + static_cast<int64_t>(qi) * K : nullptr;
+  const int shift = lane_id() & ~(kRgGroup - 1);
+  const uint32_t below = (1u << sub) - 1u;
+  const bool lp = loop != 0;
+  int c = 0;  // accepted so far (group-uniform)
+  auto take = [&](const float4& s4, bool ok) {
+    const int j = __float_as_int(s4.w);
+    const bool acc = ok && (lp || j != qi) && sqdist(q.x, q.y, q.z, s4.x, s4.y, s4.z) < r2;
+    const uint32_t m = static_cast<uint32_t>(__ballot(acc) >> shift) & ((1u << kRgGroup) - 1u);
+    if (acc && L) {
+      const int slot = c + __popc(m & below);
+      if (slot < K) L[slot] = j;
+    }
+    c += __popc(m);
+  };
+#pragma unroll
+  for (int r = 0; r < 9; ++r) take(sv[r], sub < rn[r]);
+  for (int r = 0; r < 9; ++r) {
+    for (int m0 = kRgGroup; m0 < rn[r]; m0 += kRgGroup) {  // group-uniform trip count
+      const bool ok = m0 + sub < rn[r];
+      take(ok ? w.spos[ra[r] + m0 + sub] : make_float4(0.f, 0.f, 0.f, 0.f), ok);
+    }
+  }
+  if (sub == 0) {
+    w.cnt[qi] = c;
+    w.deg[qi] = c < K ? c : K;
+  }
+}
+
+// After the edge count is known: kRgGroup lanes per target write its row, sources ascending.
+// The collected list is unsorted (traversal order); each source goes to position
+// row_ptr[i] + (number of smaller sources in the list), with the list held in the group's
+// registers (kRgSlots entries per lane) and compared through lane shuffles.  Targets with more
+// than K sources (rebuilt with the exact (d, j) threshold) or lists longer than the registers
+// hold are done by the group's first lane from the list in memory.
+constexpr int kRgSlots = 8;
+
+__global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __restrict__ x,
+                                                         int64_t N, const int64_t* __restrict__ batch,
+                                                         int64_t B, int64_t ppc, float r2, int K,
+                                                         int loop, const int64_t* __restrict__ row_ptr,
+                                                         int64_t* __restrict__ row_out,
+                                                         int64_t* __restrict__ col_out) {
+  r2 = rg_r2(w, r2);
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * kRgThreads + threadIdx.x) / kRgGroup;
+  const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
   if (i >= N) return;
   const int c = w.cnt[i];
-  if (c == 0) return;
+  if (c == 0) return;  // group-uniform
   int32_t* L = w.list + i * K;
+  const int64_t o = row_ptr[i];
+  if (c <= K && c <= kRgGroup * kRgSlots) {
+    int v[kRgSlots];
+#pragma unroll
+    for (int k = 0; k < kRgSlots; ++k) {
+      const int a = k * kRgGroup + sub;
+      v[k] = a < c ? L[a] : 0x7fffffff;
+    }
+    const int gbase = lane_id() & ~(kRgGroup - 1);
+    int rank[kRgSlots];
+#pragma unroll
+    for (int k = 0; k < kRgSlots; ++k) rank[k] = 0;
+#pragma unroll
+    for (int k2 = 0; k2 < kRgSlots; ++k2) {
+      if (k2 * kRgGroup >= c) break;  // group-uniform
+#pragma unroll
+      for (int l = 0; l < kRgGroup; ++l) {
+        const int u = __shfl(v[k2], gbase + l, kWave);  // entry k2 * G + l (INT_MAX past the end)
+#pragma unroll
+        for (int k = 0; k < kRgSlots; ++k) rank[k] += u < v[k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kRgSlots; ++k) {
+      const int a = k * kRgGroup + sub;
+      if (a < c) {
+        row_out[o + rank[k]] = v[k];
+        col_out[o + a] = i;
+      }
+    }
+    return;
+  }
+  if (sub != 0) return;
   int m = c;
   if (c > K) {
     const int b = cloud_of(i, batch, B, ppc);
@@ -446,25 +542,12 @@ __global__ void rg_compact(RgWs w, const float* __restrict__ x, int64_t N,
     });
     m = K;
   }
-  const int64_t o = row_ptr[i];
-  if (K <= kRgStageK) {
-    int32_t* S = stage + threadIdx.x;
-    for (int a = 0; a < m; ++a) S[a * kRgEmitThreads] = L[a];
-    for (int a = 0; a < m; ++a) {
-      const int v = S[a * kRgEmitThreads];
-      int r = 0;
-      for (int q = 0; q < m; ++q) r += S[q * kRgEmitThreads] < v;
-      row_out[o + r] = v;
-      col_out[o + a] = i;
-    }
-  } else {
-    for (int a = 0; a < m; ++a) {
-      const int v = L[a];
-      int r = 0;
-      for (int q = 0; q < m; ++q) r += L[q] < v;
-      row_out[o + r] = v;
-      col_out[o + a] = i;
-    }
+  for (int a = 0; a < m; ++a) {
+    const int val = L[a];
+    int r = 0;
+    for (int q = 0; q < m; ++q) r += L[q] < val;
+    row_out[o + r] = val;
+    col_out[o + a] = i;
   }
 }
 
@@ -534,10 +617,10 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
     const int64_t blocks = ceil_div(N, kRgThreads);
     hipLaunchKernelGGL(rg_scatter, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N);
     GEO_LAUNCH_CHECK("rg_scatter");
-    hipLaunchKernelGGL((rg_query<0>), dim3(blocks), dim3(kRgThreads), 0, st, w, batch, B,
-                       points_per_cloud, r2, K, loop, static_cast<const int64_t*>(nullptr),
-                       static_cast<int64_t*>(nullptr), static_cast<int64_t*>(nullptr), 0);
-    GEO_LAUNCH_CHECK("rg_query<count>");
+    const int64_t gblocks = ceil_div(N * kRgGroup, kRgThreads);
+    hipLaunchKernelGGL(rg_count, dim3(gblocks), dim3(kRgThreads), 0, st, w, batch, B,
+                       points_per_cloud, r2, K, loop);
+    GEO_LAUNCH_CHECK("rg_count");
   }
   return device_exclusive_scan<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true, w.deg_tiles, st);
 }
@@ -561,17 +644,17 @@ static int radius_emit_impl(const float* x, int64_t N, const int64_t* batch, int
   const int K = static_cast<int>(max_num_neighbors);
   const int64_t blocks = ceil_div(N, kRgEmitThreads);
   if (w.list) {
-    const size_t lds = K <= kRgStageK ? static_cast<size_t>(K) * kRgEmitThreads * sizeof(int32_t) : 0;
-    hipLaunchKernelGGL(rg_compact, dim3(blocks), dim3(kRgEmitThreads), lds, st, w, x, N, batch, B,
-                       points_per_cloud, r2, K, loop, row_ptr, row_out, col_out);
+    hipLaunchKernelGGL(rg_compact, dim3(ceil_div(N * kRgGroup, kRgThreads)), dim3(kRgThreads), 0,
+                       st, w, x, N, batch, B, points_per_cloud, r2, K, loop, row_ptr, row_out,
+                       col_out);
     GEO_LAUNCH_CHECK("rg_compact");
     return GEO_OK;
   }
   const int use_lds = K <= kRgLdsK ? 1 : 0;
   const size_t lds = use_lds ? static_cast<size_t>(K) * kRgEmitThreads * sizeof(int32_t) : 0;
-  hipLaunchKernelGGL((rg_query<1>), dim3(blocks), dim3(kRgEmitThreads), lds, st, w, batch, B,
+  hipLaunchKernelGGL(rg_emit, dim3(blocks), dim3(kRgEmitThreads), lds, st, w, batch, B,
                      points_per_cloud, r2, K, loop, row_ptr, row_out, col_out, use_lds);
-  GEO_LAUNCH_CHECK("rg_query<emit>");
+  GEO_LAUNCH_CHECK("rg_emit");
   return GEO_OK;
 }
 
