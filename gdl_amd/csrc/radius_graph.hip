@@ -11,7 +11,7 @@
 //   rg_setup    per cloud: cell edge h >= r*(1+1/32), grid dims (capped at 4*n+64 cells and
 //               16384 per axis so that the 3x3x3 stencil stays exact), cell base offsets
 //   rg_cell     cell id per point, rank inside the cell (atomic counter)
-//   scan        cell offsets
+//   scan        cell offsets (single pass, decoupled look-back)
 //   rg_scatter  points in cell order as float4 (x, y, z, index bits)
 //   rg_count    kRgGroup lanes per point in cell order (neighbouring groups share cells): count
 //               of in-radius sources over the 9 z-contiguous runs of the 27-cell stencil, and
@@ -47,11 +47,11 @@ struct RgWs {
   int32_t* pt_rank;
   int32_t* cell_cnt;
   int32_t* cell_start;
-  int32_t* cell_tiles;
+  uint64_t* cell_scan;  // look-back status of the cell-offset scan (zeroed by rg_init)
   float4* spos;
   int32_t* cnt;
   int32_t* deg;
-  int64_t* deg_tiles;
+  uint64_t* deg_scan;   // look-back status of the row-pointer scan (zeroed by rg_init)
   int32_t* list;  // [N][K] accepted sources per target (unsorted), or null when too large
   int64_t cells_max;
   size_t bytes;
@@ -89,11 +89,11 @@ RgWs carve_rg(void* base, int64_t N, int64_t B, int64_t K) {
   w.pt_rank = c.take<int32_t>(nn);
   w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
   w.cell_start = c.take<int32_t>(w.cells_max + 1);
-  w.cell_tiles = c.take<int32_t>(scan_workspace_elems(w.cells_max));
+  w.cell_scan = c.take<uint64_t>(scan_lookback_elems(w.cells_max));
   w.spos = c.take<float4>(nn);
   w.cnt = c.take<int32_t>(nn);
   w.deg = c.take<int32_t>(nn);
-  w.deg_tiles = c.take<int64_t>(scan_workspace_elems(N));
+  w.deg_scan = c.take<uint64_t>(scan_lookback_elems(N));
   const bool lists = K > 0 && N <= kRgListMaxEntries / K;
   w.list = lists ? c.take<int32_t>(N * K) : nullptr;
   if (lists && !base) w.list = reinterpret_cast<int32_t*>(1);  // size query: mark "present"
@@ -118,6 +118,8 @@ __global__ void rg_init(RgWs w, int64_t N, int64_t B) {
     if (i < w.cells_max + 1) w.cell_cnt[i] = 0;
     if (i < N) { w.cnt[i] = 0; w.deg[i] = 0; }
     if (i < B) w.cloud_n[i] = 0;
+    if (i < scan_lookback_elems(w.cells_max)) w.cell_scan[i] = 0;
+    if (i < scan_lookback_elems(N)) w.deg_scan[i] = 0;
     if (i < 6 * B) w.bbox[i] = (i % 6) < 3 ? 0xffffffffu : 0u;
   }
 }
@@ -610,8 +612,8 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                        points_per_cloud, mask);
     GEO_LAUNCH_CHECK("rg_cell");
   }
-  rc = device_exclusive_scan<int32_t, int32_t>(w.cell_cnt, w.cells_max, w.cell_start, nullptr,
-                                               true, w.cell_tiles, st);
+  rc = device_exclusive_scan_lookback<int32_t, int32_t>(w.cell_cnt, w.cells_max, w.cell_start,
+                                                        nullptr, true, w.cell_scan, st);
   if (rc) return rc;
   if (N > 0) {
     const int64_t blocks = ceil_div(N, kRgThreads);
@@ -622,7 +624,8 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                        points_per_cloud, r2, K, loop);
     GEO_LAUNCH_CHECK("rg_count");
   }
-  return device_exclusive_scan<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true, w.deg_tiles, st);
+  return device_exclusive_scan_lookback<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true,
+                                                          w.deg_scan, st);
 }
 
 static int radius_emit_impl(const float* x, int64_t N, const int64_t* batch, int64_t B,
