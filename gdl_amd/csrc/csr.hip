@@ -84,3 +84,4 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
   }
   return GEO_OK;
 }
+

@@ -83,33 +83,45 @@ __device__ __forceinline__ void sh_grad(const ShConst& c, float x, float y, floa
   }
 }
 
+// One thread per edge; the block's direction and Y rows are staged in LDS and written back as
+// contiguous runs (a thread's own rows are 12 and 36 bytes apart from its neighbours').
 __global__ __launch_bounds__(kEgThreads) void edge_geom_kernel(
     const float* __restrict__ pos, int64_t N, const int64_t* __restrict__ row,
     const int64_t* __restrict__ col, int64_t E, int max_l, ShConst c, float* __restrict__ dir,
     float* __restrict__ dist, float* __restrict__ Y) {
 #pragma clang fp contract(off)
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= E) return;
-  int64_t i = col[e], j = row[e];
-  const bool ok = i >= 0 && i < N && j >= 0 && j < N;
-  i = ok ? i : 0;
-  j = ok ? j : 0;
-  const float dx = pos[3 * i] - pos[3 * j];
-  const float dy = pos[3 * i + 1] - pos[3 * j + 1];
-  const float dz = pos[3 * i + 2] - pos[3 * j + 2];
-  const float n = sqrtf((dx * dx + dy * dy) + dz * dz);
-  const float d = n < 1e-8f ? 1e-8f : n;
-  const float ux = dx / d, uy = dy / d, uz = dz / d;
-  dir[3 * e] = ux;
-  dir[3 * e + 1] = uy;
-  dir[3 * e + 2] = uz;
-  dist[e] = d;
-  if (Y) {
-    const int nsh = (max_l + 1) * (max_l + 1);
-    float y[9];
-    sh_eval(c, ux, uy, uz, max_l, y);
-    for (int k = 0; k < nsh; ++k) Y[e * nsh + k] = y[k];
+  __shared__ float s_dir[3 * kEgThreads];
+  __shared__ float s_y[9 * kEgThreads];
+  const int t = static_cast<int>(threadIdx.x);
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads;
+  const int64_t e = e0 + t;
+  const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
+  const int nsh = (max_l + 1) * (max_l + 1);
+  if (e < E) {
+    int64_t i = col[e], j = row[e];
+    const bool ok = i >= 0 && i < N && j >= 0 && j < N;
+    i = ok ? i : 0;
+    j = ok ? j : 0;
+    const float dx = pos[3 * i] - pos[3 * j];
+    const float dy = pos[3 * i + 1] - pos[3 * j + 1];
+    const float dz = pos[3 * i + 2] - pos[3 * j + 2];
+    const float n = sqrtf((dx * dx + dy * dy) + dz * dz);
+    const float d = n < 1e-8f ? 1e-8f : n;
+    const float ux = dx / d, uy = dy / d, uz = dz / d;
+    s_dir[3 * t] = ux;
+    s_dir[3 * t + 1] = uy;
+    s_dir[3 * t + 2] = uz;
+    dist[e] = d;
+    if (Y) {
+      float y[9];
+      sh_eval(c, ux, uy, uz, max_l, y);
+      for (int k = 0; k < nsh; ++k) s_y[nsh * t + k] = y[k];
+    }
   }
+  __syncthreads();
+  for (int q = t; q < 3 * cnt; q += kEgThreads) dir[3 * e0 + q] = s_dir[q];
+  if (Y)
+    for (int q = t; q < nsh * cnt; q += kEgThreads) Y[nsh * e0 + q] = s_y[q];
 }
 
 __global__ __launch_bounds__(kEgThreads) void edge_geom_bwd_kernel(
@@ -195,28 +207,96 @@ __global__ __launch_bounds__(kEgThreads) void sph_harm_bwd_kernel(const float* _
 // lanes cloud by cloud (one pass per distinct cloud among its lanes: one or two for clouds stored
 // contiguously) and issues one atomic pair per cloud, so the counters of a few clouds are not hit
 // once per node.
-__global__ __launch_bounds__(kEgThreads) void avg_degree_sums(
+// Degree sums and point counts per cloud.  Each thread takes kAdPer consecutive points; a wave
+// whose points all lie in one cloud sums them with shuffles, and the block adds runs of waves in
+// the same cloud with one atomic pair (a block of contiguous clouds: one pair per cloud it
+// touches).  Points of a thread that straddles clouds, and waves mixing clouds, add per point /
+// per cloud instead.
+constexpr int kAdThreads = 1024;
+constexpr int kAdPer = 4;
+
+__global__ __launch_bounds__(kAdThreads) void avg_degree_sums(
     const int64_t* __restrict__ row_ptr, int64_t N, const int64_t* __restrict__ batch, int64_t B,
     int64_t ppc, unsigned long long* __restrict__ sums, unsigned long long* __restrict__ cnts) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const bool in = i < N;
-  const int64_t b = !in ? -1 : (batch ? batch[i] : (ppc > 0 ? i / ppc : 0));
-  const bool valid = in && b >= 0 && b < B;
-  const unsigned long long deg =
-      valid ? static_cast<unsigned long long>(row_ptr[i + 1] - row_ptr[i]) : 0ull;
-  unsigned long long pending = __ballot(valid);
-  while (pending) {  // wave-uniform loop: every lane takes part in each shuffle
-    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-    const int64_t lb = __shfl(b, leader, kWave);
-    const bool mine = valid && b == lb;
-    const unsigned long long m = __ballot(mine);
-    unsigned long long v = mine ? deg : 0ull;
-    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    if (lane_id() == leader) {
-      atomicAdd(&sums[lb], v);
-      atomicAdd(&cnts[lb], static_cast<unsigned long long>(__popcll(m)));
+  constexpr int W = kAdThreads / kWave;
+  __shared__ int64_t s_b[W];
+  __shared__ unsigned long long s_s[W], s_c[W];
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kAdThreads + threadIdx.x) * kAdPer;
+  int64_t b = -1;
+  unsigned long long sv = 0, cv = 0;
+  bool mixed = false;
+#pragma unroll
+  for (int k = 0; k < kAdPer; ++k) {
+    const int64_t i = i0 + k;
+    if (i < N) {
+      const int64_t bk = batch ? batch[i] : (ppc > 0 ? i / ppc : 0);
+      if (bk >= 0 && bk < B) {
+        mixed = mixed || (b >= 0 && bk != b);
+        b = bk;
+        sv += static_cast<unsigned long long>(row_ptr[i + 1] - row_ptr[i]);
+        cv += 1;
+      }
     }
-    pending &= ~m;
+  }
+  if (mixed) {  // this thread's points straddle clouds: add them one by one
+#pragma unroll
+    for (int k = 0; k < kAdPer; ++k) {
+      const int64_t i = i0 + k;
+      if (i < N) {
+        const int64_t bk = batch ? batch[i] : (ppc > 0 ? i / ppc : 0);
+        if (bk >= 0 && bk < B) {
+          atomicAdd(&sums[bk], static_cast<unsigned long long>(row_ptr[i + 1] - row_ptr[i]));
+          atomicAdd(&cnts[bk], 1ull);
+        }
+      }
+    }
+    b = -1;
+    sv = cv = 0;
+  }
+  const int w = static_cast<int>(threadIdx.x) / kWave;
+  const uint64_t has = __ballot(b >= 0);
+  int64_t wb = -1;
+  if (has) {
+    const int64_t lb = __shfl(b, __builtin_ctzll(has), kWave);
+    if (__ballot(b >= 0 && b != lb) == 0) {  // one cloud in the whole wave
+      wb = lb;
+      sv = wave_sum<unsigned long long>(sv);
+      cv = wave_sum<unsigned long long>(cv);
+    } else {
+      uint64_t pending = has;
+      while (pending) {  // wave-uniform loop: every lane takes part in each shuffle
+        const int leader = __builtin_ctzll(pending);
+        const int64_t cb = __shfl(b, leader, kWave);
+        const bool mine = b >= 0 && b == cb;
+        const uint64_t m = __ballot(mine);
+        const unsigned long long s2 = wave_sum<unsigned long long>(mine ? sv : 0ull);
+        const unsigned long long c2 = wave_sum<unsigned long long>(mine ? cv : 0ull);
+        if (lane_id() == leader) {
+          atomicAdd(&sums[cb], s2);
+          atomicAdd(&cnts[cb], c2);
+        }
+        pending &= ~m;
+      }
+    }
+  }
+  if (lane_id() == 0) {
+    s_b[w] = wb;
+    s_s[w] = sv;
+    s_c[w] = cv;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t rb = -1;
+    unsigned long long rs = 0, rc = 0;
+    for (int q = 0; q < W; ++q) {
+      if (s_b[q] != rb) {
+        if (rb >= 0) { atomicAdd(&sums[rb], rs); atomicAdd(&cnts[rb], rc); }
+        rb = s_b[q];
+        rs = rc = 0;
+      }
+      if (rb >= 0) { rs += s_s[q]; rc += s_c[q]; }
+    }
+    if (rb >= 0) { atomicAdd(&sums[rb], rs); atomicAdd(&cnts[rb], rc); }
   }
 }
 
@@ -234,6 +314,26 @@ __global__ __launch_bounds__(kEgThreads) void avg_degree_write(
     a = s / n;
   }
   out[i] = a < 1.f ? 1.f : a;
+}
+
+// CSR arrays of edges that are already grouped by target with offsets row_ptr (the radius
+// graph's output): identity permutation, int32 targets, int32 ranges, in one pass.
+__global__ void csr_from_row_ptr(const int64_t* __restrict__ row_ptr, int64_t N,
+                                 const int64_t* __restrict__ col, int64_t E,
+                                 int32_t* __restrict__ col32, int32_t* __restrict__ perm,
+                                 int32_t* __restrict__ node_start, int32_t* __restrict__ node_end) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < E || q < N;
+       q += stride) {
+    if (q < E) {
+      perm[q] = static_cast<int32_t>(q);
+      col32[q] = static_cast<int32_t>(col[q]);
+    }
+    if (q < N) {
+      node_start[q] = static_cast<int32_t>(row_ptr[q]);
+      node_end[q] = static_cast<int32_t>(row_ptr[q + 1]);
+    }
+  }
 }
 
 }  // namespace
@@ -318,11 +418,45 @@ extern "C" int geo_graph_avg_degree(const int64_t* row_ptr, int64_t N, const int
   int rc = device_fill<unsigned long long>(sums, 2 * B, 0ull, st);
   if (rc) return rc;
   const unsigned grid = static_cast<unsigned>(ceil_div(N, kEgThreads));
-  hipLaunchKernelGGL(avg_degree_sums, dim3(grid), dim3(kEgThreads), 0, st, row_ptr, N, batch, B,
-                     points_per_cloud, sums, sums + B);
+  hipLaunchKernelGGL(avg_degree_sums, dim3(static_cast<unsigned>(ceil_div(N, kAdThreads * kAdPer))),
+                     dim3(kAdThreads), 0, st, row_ptr, N, batch, B, points_per_cloud, sums,
+                     sums + B);
   GEO_LAUNCH_CHECK("avg_degree_sums");
   hipLaunchKernelGGL(avg_degree_write, dim3(grid), dim3(kEgThreads), 0, st, batch, N, B,
                      points_per_cloud, sums, sums + B, out);
   GEO_LAUNCH_CHECK("avg_degree_write");
   return GEO_OK;
+}
+
+extern "C" int geo_csr_from_row_ptr(const int64_t* row_ptr, int64_t N, const int64_t* col,
+                                    int64_t E, int32_t* col32, int32_t* perm, int32_t* node_start,
+                                    int32_t* node_end, void* stream) {
+  GEO_REQUIRE(N >= 0 && E >= 0, "csr_from_row_ptr: negative size");
+  GEO_REQUIRE(E < 0x7fffffffLL && N < 0x7fffffffLL, "csr_from_row_ptr: sizes exceed int32");
+  if (N == 0 && E == 0) return GEO_OK;
+  GEO_REQUIRE(row_ptr && node_start && node_end && (E == 0 || (col && col32 && perm)),
+              "csr_from_row_ptr: null pointer");
+  const int64_t span = E > N ? E : N;
+  int64_t blocks = ceil_div(span, 256);
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(csr_from_row_ptr, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     as_stream(stream), row_ptr, N, col, E, col32, perm, node_start, node_end);
+  GEO_LAUNCH_CHECK("csr_from_row_ptr");
+  return GEO_OK;
+}
+
+extern "C" int geo_spatial_graph_epilogue(const float* pos, int64_t N, const int64_t* row,
+                                          const int64_t* col, const int64_t* row_ptr, int64_t E,
+                                          int max_l, const int64_t* batch, int64_t B,
+                                          int64_t points_per_cloud, float* direction,
+                                          float* dist, float* Y, int32_t* col_sorted,
+                                          int32_t* perm, int32_t* node_start, int32_t* node_end,
+                                          float* avg_degree, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  int rc = geo_csr_from_row_ptr(row_ptr, N, col, E, col_sorted, perm, node_start, node_end, stream);
+  if (rc) return rc;
+  rc = geo_edge_geometry(pos, N, row, col, E, max_l, direction, dist, Y, stream);
+  if (rc) return rc;
+  return geo_graph_avg_degree(row_ptr, N, batch, B, points_per_cloud, avg_degree, workspace,
+                              workspace_bytes, stream);
 }

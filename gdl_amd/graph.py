@@ -21,7 +21,9 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
+from gdl_amd import _native as _nat
 from gdl_amd.csrc import (
+    _positions,
     edge_geometry_backward_hip,
     edge_geometry_hip,
     graph_avg_degree_hip,
@@ -98,17 +100,45 @@ class SpatialGraph:
         E = row.shape[0]
         if E == 0:
             return SpatialGraph._empty(N, dev, max_l)
-        node_start = row_ptr[:-1].to(torch.int32)
-        node_end = row_ptr[1:].to(torch.int32)
-        perm = torch.arange(E, dtype=torch.int32, device=dev)
-        direction, dist, Y = edge_geometry(pos, row, col, max_l, (perm, node_start, node_end))
         if batch is not None:
             B = int(num_batch_elements) if num_batch_elements is not None else int(batch.max().item()) + 1
+            batch = batch.reshape(-1).to(device=dev, dtype=torch.int64)
+            ppc = 0
         else:
-            B = 1
-        avg = graph_avg_degree_hip(row_ptr, N, batch, B)
+            B, ppc = 1, N
+        nsh = (max_l + 1) ** 2
+        ibuf = torch.empty(2 * E + 2 * N, dtype=torch.int32, device=dev)
+        col_sorted, perm = ibuf[:E], ibuf[E:2 * E]
+        node_start, node_end = ibuf[2 * E:2 * E + N], ibuf[2 * E + N:]
+        L = _nat.lib()
+        if torch.is_grad_enabled() and pos.requires_grad:
+            # differentiable geometry (autograd function), CSR arrays and degrees separately
+            with torch.cuda.device(dev):
+                _nat.check(L.geo_csr_from_row_ptr(
+                    _nat.ptr(row_ptr), N, _nat.ptr(col), E, _nat.ptr(col_sorted), _nat.ptr(perm),
+                    _nat.ptr(node_start), _nat.ptr(node_end), _nat.stream_of(dev)),
+                    "geo_csr_from_row_ptr")
+            direction, dist, Y = edge_geometry(pos, row, col, max_l, (perm, node_start, node_end))
+            avg = graph_avg_degree_hip(row_ptr, N, batch, B)
+        else:
+            # one call for CSR arrays, geometry and degrees; one float allocation for the fields
+            p32 = _positions("spatial_graph", pos)
+            fbuf = torch.empty(E * (4 + nsh) + N, dtype=torch.float32, device=dev)
+            direction = fbuf[:3 * E].view(E, 3)
+            dist = fbuf[3 * E:4 * E]
+            Y = fbuf[4 * E:(4 + nsh) * E].view(E, nsh)
+            avg = fbuf[(4 + nsh) * E:]
+            with torch.cuda.device(dev):
+                ws_bytes = L.geo_graph_avg_degree_workspace_bytes(B)
+                ws = _nat.workspace(ws_bytes, dev)
+                _nat.check(L.geo_spatial_graph_epilogue(
+                    _nat.ptr(p32), N, _nat.ptr(row), _nat.ptr(col), _nat.ptr(row_ptr), E,
+                    int(max_l), _nat.ptr(batch), B, ppc, _nat.ptr(direction), _nat.ptr(dist),
+                    _nat.ptr(Y), _nat.ptr(col_sorted), _nat.ptr(perm), _nat.ptr(node_start),
+                    _nat.ptr(node_end), _nat.ptr(avg), _nat.ptr(ws), ws_bytes, _nat.stream_of(dev)),
+                    "geo_spatial_graph_epilogue")
         graph = SpatialGraph(row=row, col=col, direction=direction, dist=dist,
-                             col_sorted=col.to(torch.int32), perm=perm, node_start=node_start,
+                             col_sorted=col_sorted, perm=perm, node_start=node_start,
                              node_end=node_end, Y=Y, N=N, E=E, avg_degree=avg)
         object.__setattr__(graph, "_perm_identity", True)  # kernels may skip the perm lookup
         return graph

@@ -188,6 +188,13 @@ size_t geo_csr_workspace_bytes(int64_t E, int64_t N);
 int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
                   int32_t* perm, int32_t* node_start, int32_t* node_end, void* workspace,
                   size_t workspace_bytes, void* stream);
+/* The same four arrays for edges already grouped by target with int64 offsets row_ptr[N+1]
+ * (the radius graph's CSR output): perm = identity, col_sorted = int32(col), node_start =
+ * row_ptr[:-1], node_end = row_ptr[1:].  Replaces the casts and arange SpatialGraph.build
+ * performs on the radius graph's output (geoembodied/nn/modules/spatial_graph.py:126-153). */
+int geo_csr_from_row_ptr(const int64_t* row_ptr, int64_t N, const int64_t* col, int64_t E,
+                         int32_t* col_sorted, int32_t* perm, int32_t* node_start,
+                         int32_t* node_end, void* stream);
 
 /* --------------------------------------------------------- segment reduce --- */
 /*
@@ -326,6 +333,15 @@ size_t geo_graph_avg_degree_workspace_bytes(int64_t B);
 int geo_graph_avg_degree(const int64_t* row_ptr, int64_t N, const int64_t* batch, int64_t B,
                          int64_t points_per_cloud, float* out, void* workspace,
                          size_t workspace_bytes, void* stream);
+/* SpatialGraph.build after the radius graph (geoembodied/nn/modules/spatial_graph.py:126-153)
+ * in one call: geo_csr_from_row_ptr, geo_edge_geometry and geo_graph_avg_degree on the same
+ * stream (workspace: geo_graph_avg_degree_workspace_bytes(B)). */
+int geo_spatial_graph_epilogue(const float* pos, int64_t N, const int64_t* row, const int64_t* col,
+                               const int64_t* row_ptr, int64_t E, int max_l, const int64_t* batch,
+                               int64_t B, int64_t points_per_cloud, float* direction, float* dist,
+                               float* Y, int32_t* col_sorted, int32_t* perm, int32_t* node_start,
+                               int32_t* node_end, float* avg_degree, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------ SE(3) message passing (fused aggregate) --- */
 /*

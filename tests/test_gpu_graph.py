@@ -81,6 +81,43 @@ def test_spatial_graph_build_vs_oracle(dev, B, N, r, K):
                                oracle.graph_avg_degree(ns, ne, batch.numpy(), B), rtol=1e-7)
 
 
+def _avg_degree_np(row_ptr, batch, B):
+    deg = np.diff(row_ptr).astype(np.float64)
+    valid = (batch >= 0) & (batch < B)
+    s = np.bincount(batch[valid], weights=deg[valid], minlength=B)
+    c = np.bincount(batch[valid], minlength=B)
+    avg = np.ones(len(deg), np.float32)
+    a = (s[batch[valid]] / np.maximum(c[batch[valid]], 1)).astype(np.float32)
+    avg[valid] = np.maximum(a, 1.0)
+    return avg
+
+
+@pytest.mark.parametrize("N,B,kind", [
+    (10001, 3, "sorted"),      # uneven contiguous clouds, boundaries inside threads and waves
+    (9000, 7, "unsorted"),     # every wave mixes clouds
+    (5000, 4, "invalid"),      # ids outside [0, B) contribute nothing and get 1
+    (16384, 4, "ppc"),         # no batch vector: equal contiguous clouds
+    (3, 2, "sorted"),
+])
+def test_graph_avg_degree_vs_numpy(dev, N, B, kind):
+    from gdl_amd.csrc import graph_avg_degree_hip
+    rng = np.random.default_rng(N + B)
+    deg = rng.integers(0, 40, N)
+    row_ptr = np.zeros(N + 1, np.int64)
+    row_ptr[1:] = np.cumsum(deg)
+    if kind == "sorted":
+        batch = np.sort(rng.integers(0, B, N))
+    elif kind == "unsorted":
+        batch = rng.integers(0, B, N)
+    elif kind == "invalid":
+        batch = rng.integers(-1, B + 1, N)
+    else:
+        batch = np.repeat(np.arange(B), N // B)
+    got = graph_avg_degree_hip(torch.from_numpy(row_ptr).to(dev), N,
+                               None if kind == "ppc" else torch.from_numpy(batch).to(dev), B)
+    np.testing.assert_allclose(got.cpu().numpy(), _avg_degree_np(row_ptr, batch, B), rtol=1e-7)
+
+
 def test_spatial_graph_gradient_and_from_edge_index(dev):
     _, SpatialGraph = _f()
     pos, batch = _cloud(600, 2, 9)
