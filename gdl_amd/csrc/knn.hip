@@ -160,7 +160,7 @@ struct KnnGridWs {
   KnnGrid* grid;
   int32_t* cell_cnt;
   int32_t* cell_start;
-  int32_t* cell_tiles;
+  uint64_t* cell_scan;  // look-back status of the cell scan; zeroed with cell_cnt (carved next)
   int32_t* pt_cell;
   int32_t* pt_rank;
   float4* spos;
@@ -174,8 +174,8 @@ KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
   w.cells_max = kKnnCellCap * Ns + 64 * bb;
   w.grid = c.take<KnnGrid>(bb);
   w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
+  w.cell_scan = c.take<uint64_t>(scan_lookback_elems(w.cells_max + 1));
   w.cell_start = c.take<int32_t>(w.cells_max + 1);
-  w.cell_tiles = c.take<int32_t>(scan_workspace_elems(w.cells_max + 1));
   w.pt_cell = c.take<int32_t>(nn);
   w.pt_rank = c.take<int32_t>(nn);
   w.spos = c.take<float4>(nn);
@@ -296,6 +296,18 @@ __device__ __forceinline__ int64_t cloud_of_index(const int64_t* __restrict__ pt
   return lo;
 }
 
+// Rank of this point in its cell's counter.  Points in scan order (lidar) put long runs of a
+// wave into one cell: there one atomic per distinct cell (wave-aggregated) avoids serialising
+// 64 atomics on one address; scattered points take plain per-lane atomics, since aggregation
+// would loop over up to 64 distinct cells.  The run count comes from neighbouring-lane equality.
+__device__ __forceinline__ int cell_rank(int* counter, int key) {
+  const int lane = lane_id();
+  const int prev = __shfl_up(key, 1, kWave);
+  const int runs = __popcll(__ballot(lane == 0 || prev != key));
+  if (runs <= 16) return wave_aggregated_rank(counter, key);
+  return atomicAdd(counter, 1);
+}
+
 __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_cell(
     const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int64_t B,
     KnnGridWs w) {
@@ -313,7 +325,7 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_cell(
   const int cz = knn_cell_coord(source[3 * i + 2], g.oz, g.inv_h, g.dz, &u);
   const int c = g.base + (cx * g.dy + cy) * g.dz + cz;
   w.pt_cell[i] = c;
-  w.pt_rank[i] = wave_aggregated_rank(&w.cell_cnt[c], c);
+  w.pt_rank[i] = cell_rank(&w.cell_cnt[c], c);
 }
 
 __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_scatter(const float* __restrict__ source,
@@ -396,9 +408,15 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_query(
   const int gl = static_cast<int>(gt % G);
   if (q >= Nq) return;  // whole groups leave together (G divides the block)
   const int64_t b = cloud_of_index(ptr_q, B, q);
-  if (b >= B || q < ptr_q[b] || q >= ptr_q[b + 1]) return;  // no cloud: padding stays
+  const bool covered = b < B && q >= ptr_q[b] && q < ptr_q[b + 1];
+  if (!covered || w.grid[b].ncells == 0) {  // no cloud, or an empty source cloud: padding
+    for (int i = gl; i < k; i += G) {
+      out_idx[q * k + i] = -1;
+      out_dist[q * k + i] = 1e30f;
+    }
+    return;
+  }
   const KnnGrid g = w.grid[b];
-  if (g.ncells == 0) return;                                  // empty source cloud
   const float qx = query[3 * q], qy = query[3 * q + 1], qz = query[3 * q + 2];
   float ux, uy, uz;
   const int cx = knn_cell_coord(qx, g.ox, g.inv_h, g.dx, &ux);
@@ -479,13 +497,17 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
   GEO_LAUNCH_CHECK("knn_grid_setup");
   hipLaunchKernelGGL(knn_grid_base, dim3(1), dim3(kScanThreads), 0, st, w.grid, B);
   GEO_LAUNCH_CHECK("knn_grid_base");
-  int rc = device_fill<int32_t>(w.cell_cnt, w.cells_max + 1, 0, st);
+  // cell counts and the scan's look-back status are carved next to each other: one zero fill
+  const int64_t zero_words =
+      (reinterpret_cast<char*>(w.cell_scan + scan_lookback_elems(w.cells_max + 1)) -
+       reinterpret_cast<char*>(w.cell_cnt)) / static_cast<int64_t>(sizeof(int32_t));
+  int rc = device_fill<int32_t>(w.cell_cnt, zero_words, 0, st);
   if (rc) return rc;
   const unsigned gs = static_cast<unsigned>(ceil_div(Ns, kKnnGridThreads));
   hipLaunchKernelGGL(knn_grid_cell, dim3(gs), dim3(kKnnGridThreads), 0, st, source, Ns, ptr_s, B, w);
   GEO_LAUNCH_CHECK("knn_grid_cell");
-  rc = device_exclusive_scan<int32_t, int32_t>(w.cell_cnt, w.cells_max + 1, w.cell_start, nullptr,
-                                               false, w.cell_tiles, st);
+  rc = device_exclusive_scan_lookback<int32_t, int32_t>(w.cell_cnt, w.cells_max + 1, w.cell_start,
+                                                        nullptr, false, w.cell_scan, st);
   if (rc) return rc;
   hipLaunchKernelGGL(knn_grid_scatter, dim3(gs), dim3(kKnnGridThreads), 0, st, source, Ns, w);
   GEO_LAUNCH_CHECK("knn_grid_scatter");
@@ -541,16 +563,17 @@ extern "C" int geo_knn(const float* query, int64_t Nq, const float* source, int6
     if (rc) return rc;
     return device_fill<float>(out_dist, Nq * k, 1e30f, st);
   }
-  // Queries outside every cloud keep padding: pre-fill only when the clouds may not cover Nq.
+  GEO_REQUIRE(Ns == 0 || source != nullptr, "knn: null source");
+  const int kk = static_cast<int>(k);
+  // the grid search writes every output row itself (padding for queries outside every cloud)
+  if (knn_use_grid(Ns, B, k))
+    return launch_knn_grid(query, Nq, source, Ns, ptr_q, ptr_s, B, kk, out_idx, out_dist,
+                           workspace, st);
+  // Queries outside every cloud keep padding.
   int rc = device_fill<int64_t>(out_idx, Nq * k, -1, st);
   if (rc) return rc;
   rc = device_fill<float>(out_dist, Nq * k, 1e30f, st);
   if (rc) return rc;
-  GEO_REQUIRE(Ns == 0 || source != nullptr, "knn: null source");
-  const int kk = static_cast<int>(k);
-  if (knn_use_grid(Ns, B, k))
-    return launch_knn_grid(query, Nq, source, Ns, ptr_q, ptr_s, B, kk, out_idx, out_dist,
-                           workspace, st);
   hipLaunchKernelGGL(knn_prepare_kernel, dim3(1), dim3(kScanThreads), 0, st, ptr_q, B, Nq, tiles);
   GEO_LAUNCH_CHECK("knn_prepare_kernel");
 #define GEO_KNN_CASE(KV) \

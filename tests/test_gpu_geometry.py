@@ -209,6 +209,10 @@ def _knn_grid_problem(kind, g):
         s = torch.randn(6005, 3, generator=g)
         q = torch.randn(600, 3, generator=g)
         ss, qs = [6000, 5, 0], [300, 200, 100]
+    elif kind == "uncovered":  # queries before the first and after the last cloud: padding
+        s = torch.randn(9000, 3, generator=g)
+        q = torch.randn(800, 3, generator=g)
+        return q, s, torch.tensor([50, 300, 300, 700]), _ptr([4000, 3000, 2000])
     else:                    # "nonfinite": one source at inf -> the cloud falls back to one cell
         s = torch.randn(5000, 3, generator=g)
         s[17] = float("inf")
@@ -217,7 +221,8 @@ def _knn_grid_problem(kind, g):
     return q, s, _ptr(qs), _ptr(ss)
 
 
-@pytest.mark.parametrize("kind", ["cube", "lattice", "sphere", "plane", "small_cloud", "nonfinite"])
+@pytest.mark.parametrize("kind", ["cube", "lattice", "sphere", "plane", "small_cloud", "uncovered",
+                                  "nonfinite"])
 @pytest.mark.parametrize("k", [1, 3, 8, 16, 17, 32])
 def test_knn_grid_vs_oracle(dev, kind, k):
     g = torch.Generator().manual_seed(k * 31 + len(kind))
