@@ -3,7 +3,8 @@
 // A sort of b-bit keys takes ceil(b / 11) passes of near-equal digit width (17-bit CSR keys: two
 // passes of 9 and 8 bits instead of three of 8).  Three kernels per pass:
 //   radix_hist     one 2048-key tile per block, 2^BITS-bin LDS histogram -> hist[digit][tile]
-//                  (lanes holding the same digit add once: sorted input does not serialise)
+//                  (a run of equal digits in consecutive lanes adds once: sorted input does not
+//                  serialise on one counter)
 //   scan           device-wide exclusive scan of hist (digit-major) -> global offsets
 //   radix_scatter  stable rank inside the tile: each wave walks its 512 keys in index order,
 //                  peers with the same digit are found with BITS ballots, per-wave LDS counters
@@ -63,14 +64,21 @@ __global__ __launch_bounds__(kRxThreads) void radix_hist(const void* __restrict_
   for (int b = threadIdx.x; b < BINS; b += kRxThreads) h[b] = 0;
   __syncthreads();
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kRxTile;
+  const int lane = lane_id();
 #pragma unroll
   for (int i = 0; i < kRxItems; ++i) {
     const int64_t idx = base + static_cast<int64_t>(i) * kRxThreads + threadIdx.x;
     const bool valid = idx < n;
-    const uint32_t d = valid ? (rx_fetch_key<SRC>(keys, idx, N) >> shift) & (BINS - 1u) : 0u;
-    const uint64_t peers = rx_peers<BITS>(d, valid);
-    if (valid && __popcll(peers & lanemask_lt()) == 0)
-      atomicAdd(&h[d], static_cast<uint32_t>(__popcll(peers)));
+    // runs of equal digits in consecutive lanes add once (sorted input does not serialise on
+    // one counter); invalid lanes, at the end of the range, carry a digit no key has
+    const uint32_t d = valid ? (rx_fetch_key<SRC>(keys, idx, N) >> shift) & (BINS - 1u) : BINS;
+    const uint32_t prev = __shfl_up(d, 1, kWave);
+    const uint64_t starts = __ballot(lane == 0 || prev != d);
+    if (valid && (lane == 0 || prev != d)) {
+      const uint64_t later = lane == kWave - 1 ? 0ull : (starts & (~0ull << (lane + 1)));
+      const int next = later ? __builtin_ctzll(later) : kWave;
+      atomicAdd(&h[d], static_cast<uint32_t>(next - lane));
+    }
   }
   __syncthreads();
   for (int b = threadIdx.x; b < BINS; b += kRxThreads)
@@ -164,6 +172,7 @@ int radix_pass(const void* kin, const uint32_t* vin, int64_t n, int64_t N, int s
   hipLaunchKernelGGL((radix_hist<SRC, BITS>), dim3(ntiles), dim3(kRxThreads), 0, st, kin, n, N,
                      shift, r.hist, ntiles);
   GEO_LAUNCH_CHECK("radix_hist");
+  // three-kernel scan: with ~10^3 tiles of offsets the look-back chain is slower (measured)
   int rc = device_exclusive_scan<uint32_t, uint32_t>(r.hist, (int64_t{1} << BITS) * ntiles, r.hist,
                                                      nullptr, false, r.hist_tiles, st);
   if (rc) return rc;
