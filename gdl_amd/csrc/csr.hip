@@ -73,9 +73,10 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
     return device_fill<int32_t>(node_end, N, 0, st);
   }
 
+  // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one pass
   int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),
                                 reinterpret_cast<uint32_t*>(col_sorted),
-                                reinterpret_cast<uint32_t*>(perm), w, st);
+                                reinterpret_cast<uint32_t*>(perm), w, st, true);
   if (rc) return rc;
   if (N > 0) {
     hipLaunchKernelGGL(csr_bounds, dim3(ceil_div(N + 1, 256)), dim3(256), 0, st,

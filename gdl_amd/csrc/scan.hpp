@@ -34,7 +34,9 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* lds, T& total) {
 template <typename TIn, typename TOut>
 __global__ __launch_bounds__(kScanThreads) void scan_tile_reduce(const TIn* __restrict__ in,
                                                                    int64_t n,
-                                                                   TOut* __restrict__ tile_sums) {
+                                                                   TOut* __restrict__ tile_sums,
+                                                                   const uint32_t* __restrict__ active) {
+  if (active != nullptr && *active == 0u) return;
   __shared__ TOut lds[kScanThreads / kWave];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
   TOut s = 0;
@@ -51,7 +53,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_reduce(const TIn* __re
 // Single block: exclusive scan of tile_sums[0..ntiles) in place.
 template <typename TOut>
 __global__ __launch_bounds__(kScanThreads) void scan_tile_sums(TOut* __restrict__ tile_sums,
-                                                                 int64_t ntiles) {
+                                                                 int64_t ntiles,
+                                                                 const uint32_t* __restrict__ active) {
+  if (active != nullptr && *active == 0u) return;
   __shared__ TOut lds[kScanThreads / kWave];
   TOut carry = 0;
   for (int64_t base = 0; base < ntiles; base += kScanTile) {
@@ -81,7 +85,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_sums(TOut* __restrict_
 template <typename TIn, typename TOut>
 __global__ __launch_bounds__(kScanThreads) void scan_tile_apply(
     const TIn* __restrict__ in, int64_t n, const TOut* __restrict__ tile_offsets,
-    TOut* __restrict__ out_excl, TOut* __restrict__ out_incl, int write_total) {
+    TOut* __restrict__ out_excl, TOut* __restrict__ out_incl, int write_total,
+    const uint32_t* __restrict__ active = nullptr) {
+  if (active != nullptr && *active == 0u) return;
   __shared__ TOut lds[kScanThreads / kWave];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
   TOut v[kScanItems];
@@ -112,9 +118,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_apply(
 inline int64_t scan_workspace_elems(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
 
 // out_excl needs n+1 entries when write_total.  tile_ws needs scan_workspace_elems(n) entries.
+// With `active` (device word), the kernels do nothing when it reads 0.
 template <typename TIn, typename TOut>
 int device_exclusive_scan(const TIn* in, int64_t n, TOut* out_excl, TOut* out_incl,
-                          bool write_total, TOut* tile_ws, hipStream_t stream) {
+                          bool write_total, TOut* tile_ws, hipStream_t stream,
+                          const uint32_t* active = nullptr) {
   if (n <= 0) {
     if (write_total) {
       // total of an empty range is 0: use a one-element apply on a zero tile.
@@ -128,19 +136,19 @@ int device_exclusive_scan(const TIn* in, int64_t n, TOut* out_excl, TOut* out_in
   if (ntiles == 1) {
     hipLaunchKernelGGL((scan_tile_apply<TIn, TOut>), dim3(1), dim3(kScanThreads), 0, stream, in,
                        n, static_cast<const TOut*>(nullptr), out_excl, out_incl,
-                       write_total ? 1 : 0);
+                       write_total ? 1 : 0, active);
     GEO_LAUNCH_CHECK("scan_tile_apply");
     return GEO_OK;
   }
   hipLaunchKernelGGL((scan_tile_reduce<TIn, TOut>), dim3(ntiles), dim3(kScanThreads), 0, stream,
-                     in, n, tile_ws);
+                     in, n, tile_ws, active);
   GEO_LAUNCH_CHECK("scan_tile_reduce");
   hipLaunchKernelGGL((scan_tile_sums<TOut>), dim3(1), dim3(kScanThreads), 0, stream, tile_ws,
-                     ntiles);
+                     ntiles, active);
   GEO_LAUNCH_CHECK("scan_tile_sums");
   hipLaunchKernelGGL((scan_tile_apply<TIn, TOut>), dim3(ntiles), dim3(kScanThreads), 0, stream,
                      in, n, static_cast<const TOut*>(tile_ws), out_excl, out_incl,
-                     write_total ? 1 : 0);
+                     write_total ? 1 : 0, active);
   GEO_LAUNCH_CHECK("scan_tile_apply");
   return GEO_OK;
 }

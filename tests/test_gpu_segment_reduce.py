@@ -57,6 +57,33 @@ def test_csr_matches_oracle(dev, E, N, seed):
         np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
 
 
+@pytest.mark.parametrize("kind", ["sorted", "sorted_invalid_last", "invalid_first", "one_descent",
+                                  "constant", "reversed"])
+@pytest.mark.parametrize("E,N", [(3000, 500), (200000, 300000)])   # one and two radix passes
+def test_csr_sorted_input_detection(dev, kind, E, N):
+    """Targets that arrive sorted take the identity path (one pass); anything out of order, however
+    little, takes the full sort.  Both must give the oracle's stable CSR."""
+    _, csr = _ops()
+    g = torch.Generator().manual_seed(E + len(kind))
+    col = torch.sort(torch.randint(0, N, (E,), generator=g)).values
+    if kind == "sorted_invalid_last":
+        col[-7:] = N + 3               # clamped to N: still sorted
+    elif kind == "invalid_first":
+        col[0] = -1                    # clamped to N at the front: out of order
+    elif kind == "one_descent":
+        i = E // 2 + 5
+        col[i] = col[i - 1] - 1 if col[i - 1] > 0 else col[i]
+        col[i - 1] = col[i - 1] if col[i - 1] > 0 else N - 1
+    elif kind == "constant":
+        col[:] = N // 2
+    elif kind == "reversed":
+        col = col.flip(0)
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    r = oracle.sort_and_build_csr(col.numpy(), N)
+    for got, want, name in zip((cs, pm, ns, ne), r, ("col_sorted", "perm", "node_start", "node_end")):
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
+
+
 def test_csr_empty(dev):
     _, csr = _ops()
     cs, pm, ns, ne = csr(torch.empty(0, dtype=torch.long, device=dev), 7)
