@@ -445,6 +445,10 @@ def main() -> int:
             log(f"  bwd sum fp32: {msb:.4f} ms  {legs['c3_bwd_sum_fp32_gbs']} GB/s")
         col64 = col_sorted.long()
         legs["c3_csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col64, S), 10, 2), 4)
+        # the same targets in random order (the sorted-input identity path does not apply)
+        col_sh = col64[torch.randperm(E, device=dev, generator=gen)]
+        legs["c3_csr_build_shuffled_ms"] = round(wall_ms(lambda: sort_and_build_csr(col_sh, S), 10, 2), 4)
+        del col_sh
         del msg
 
     # ------------------------------------------------------- HBM counter calibration ---
