@@ -246,6 +246,15 @@ __device__ __forceinline__ void node_range(const SeEdges& g, int64_t n, int& a, 
 
 constexpr int kSeUnroll = 4;  // edges whose source rows are in flight together
 
+// The dispatcher hands workgroups to the 8 XCDs in turn (workgroup b to XCD b mod 8).  This
+// renumbering gives each XCD one contiguous range of the node space, so neighbouring nodes --
+// which share source rows -- are processed under the same L2.
+__device__ __forceinline__ int64_t xcd_block() {
+  const int64_t G = gridDim.x, b = blockIdx.x;
+  const int64_t q = G / 8, r = G % 8, x = b % 8, k = b / 8;
+  return x * q + (x < r ? x : r) + k;
+}
+
 // ------------------------------------------------------------------ forward aggregate ---
 // One wave per target node, lanes over input channels (chunks of 64).  The node's edges are
 // staged in lanes, then walked four at a time: the four source rows are loaded first, then
@@ -255,7 +264,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
                                                                float* __restrict__ Xs, int Ks,
                                                                float* __restrict__ Xv, int Kv,
                                                                float* __restrict__ Xt, int Kt) {
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  const int64_t n = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
   if (n >= g.N) return;
   const int lane = lane_id();
   int a, b;
@@ -783,7 +792,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
                                                           float* __restrict__ dR,
                                                           float* __restrict__ ddir,
                                                           float* __restrict__ dY) {
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  const int64_t n = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
   if (n >= g.N) return;
   const int lane = lane_id();
   const int row = lane >> 4, li = lane & 15;
@@ -865,7 +874,7 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
                                                          int KZs, float* __restrict__ Zv, int KZv,
                                                          float* __restrict__ Zt, int KZt,
                                                          float* __restrict__ Z8, int KZ8) {
-  const int64_t m = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  const int64_t m = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
   if (m >= g.N) return;
   const int lane = lane_id();
   int a, b;
