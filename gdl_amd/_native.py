@@ -63,6 +63,9 @@ _SIGNATURES = {
     "geo_idw_weights": (c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "geo_radius_count_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
                                      c_vp, c_vp, c_size, c_vp]),
+    "geo_radius_count_async": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_f32, c_f32, c_vp,
+                                       c_i64, c_int, c_vp, c_vp, c_vp, c_size, c_vp]),
+    "geo_radius_copy_edges": (c_int, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp]),
     "geo_radius_emit_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
                                     c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_knn_radius_stat_workspace_bytes": (c_size, [c_i64]),
@@ -168,3 +171,21 @@ def stream_of(device: torch.device) -> int:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+_tls = threading.local()
+
+
+def sync_slot(device: torch.device):
+    """(pinned int64[4] host tensor, event) kept per thread and device for an op's one size sync:
+    a kernel writes the sizes into the mapped pinned memory, the op records the event behind it,
+    waits for the event and reads the values before returning, so consecutive calls of a thread
+    never overlap on the slot and threads never share one."""
+    slots = getattr(_tls, "slots", None)
+    if slots is None:
+        slots = _tls.slots = {}
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    slot = slots.get(key)
+    if slot is None:
+        slot = slots[key] = (torch.empty(4, dtype=torch.int64, pin_memory=True), torch.cuda.Event())
+    return slot

@@ -71,6 +71,11 @@ def get_radius_graph_backend() -> str:
     return "cuda" if _hip_ready() else "unavailable"
 
 
+# Largest N * max_num_neighbors whose bound-sized emit scratch (16 bytes per entry) is allocated
+# to overlap the edge-count sync with the emit pass (2^26 entries = 1 GiB); larger graphs wait.
+_RADIUS_ASYNC_MAX_EDGES = 1 << 26
+
+
 def radius_graph_hip(
     x: Tensor,
     r,
@@ -146,20 +151,41 @@ def radius_graph_csr_hip(
         ws = _nat.workspace(ws_bytes, dev)
         row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
         if r_dev is None:
-            count, emit = L.geo_radius_count, L.geo_radius_emit
+            emit = L.geo_radius_emit
             args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K,
                     int(bool(loop)))
         else:
-            count, emit = L.geo_radius_count_dev, L.geo_radius_emit_dev
+            emit = L.geo_radius_emit_dev
             args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), _nat.ptr(r_dev), K,
                     int(bool(loop)))
-        _nat.check(count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s), "geo_radius_count")
-        E = int(row_ptr[N].item())
-        row = torch.empty(E, dtype=torch.int64, device=dev)
-        col = torch.empty(E, dtype=torch.int64, device=dev)
-        if E > 0:
-            _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col), _nat.ptr(ws),
-                            ws_bytes, s), "geo_radius_emit")
+        if N * K <= _RADIUS_ASYNC_MAX_EDGES:
+            # emit into bound-sized scratch right behind the count; the host waits only for the
+            # count (an event) to learn E, then one copy gives exact-sized outputs
+            edges_h, counted = _nat.sync_slot(dev)
+            _nat.check(L.geo_radius_count_async(
+                _nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, _nat.ptr(r_dev),
+                K, int(bool(loop)), _nat.ptr(row_ptr), edges_h.data_ptr(), _nat.ptr(ws), ws_bytes,
+                s), "geo_radius_count_async")
+            counted.record(torch.cuda.current_stream(dev))
+            scratch = torch.empty(2, N * K, dtype=torch.int64, device=dev)
+            _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(scratch[0]), _nat.ptr(scratch[1]),
+                            _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
+            counted.synchronize()
+            E = int(edges_h[0].item())
+            row = torch.empty(E, dtype=torch.int64, device=dev)
+            col = torch.empty(E, dtype=torch.int64, device=dev)
+            _nat.check(L.geo_radius_copy_edges(_nat.ptr(scratch[0]), _nat.ptr(scratch[1]), E,
+                                               _nat.ptr(row), _nat.ptr(col), s),
+                       "geo_radius_copy_edges")
+        else:
+            count = L.geo_radius_count if r_dev is None else L.geo_radius_count_dev
+            _nat.check(count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s), "geo_radius_count")
+            E = int(row_ptr[N].item())
+            row = torch.empty(E, dtype=torch.int64, device=dev)
+            col = torch.empty(E, dtype=torch.int64, device=dev)
+            if E > 0:
+                _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col), _nat.ptr(ws),
+                                ws_bytes, s), "geo_radius_emit")
     return row, col, row_ptr
 
 
@@ -655,12 +681,11 @@ def fps_uniform_hip(pos: Tensor, ptr: Tensor, num_samples: int) -> Tensor:
         s = _nat.stream_of(dev)
         out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
         info = torch.empty(3, dtype=torch.int64, device=dev)
-        info_h = torch.empty(3, dtype=torch.int64, pin_memory=True)
+        info_h, prepared = _nat.sync_slot(dev)
         out = torch.empty(min(N, B * k), dtype=torch.int64, device=dev)
         _nat.check(L.geo_fps_prepare_uniform(_nat.ptr(p), k, B, N, _nat.ptr(out_ptr),
                                              _nat.ptr(info), info_h.data_ptr(), s),
                    "geo_fps_prepare_uniform")
-        prepared = torch.cuda.Event()
         prepared.record(torch.cuda.current_stream(dev))
         cap = ctypes.c_int64(0)
         guess = -(-N // B) if B > 0 and out.numel() > 0 else 0
@@ -668,7 +693,7 @@ def fps_uniform_hip(pos: Tensor, ptr: Tensor, num_samples: int) -> Tensor:
                                      _nat.ptr(out), _nat.ptr(info), ctypes.byref(cap), s),
                    "geo_fps_guarded")
         prepared.synchronize()
-        total, max_n, bad = info_h.tolist()
+        total, max_n, bad = info_h[:3].tolist()
         if bad:
             raise ValueError(f"fps: ptr is not a non-decreasing offset array within [0, {N}] "
                              f"(first bad entry: ptr[{bad - 1}])")

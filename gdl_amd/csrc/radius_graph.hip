@@ -580,7 +580,7 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                              int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
                              const double* r_dev, int64_t max_num_neighbors, int loop,
                              int64_t* row_ptr, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             void* stream, int64_t* edges_host = nullptr) {
   int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
   if (rc) return rc;
   GEO_REQUIRE(r_cell > 0.f, "radius_graph: r_cell must be positive");
@@ -624,8 +624,12 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                        points_per_cloud, r2, K, loop);
     GEO_LAUNCH_CHECK("rg_count");
   }
+  if (N == 0 && edges_host) {  // no scan launch to carry the total: zero it from a fill
+    rc = device_fill<int64_t>(edges_host, 1, int64_t{0}, st);
+    if (rc) return rc;
+  }
   return device_exclusive_scan_lookback<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true,
-                                                          w.deg_scan, st);
+                                                          w.deg_scan, st, edges_host);
 }
 
 static int radius_emit_impl(const float* x, int64_t N, const int64_t* batch, int64_t B,
@@ -699,4 +703,51 @@ extern "C" int geo_radius_emit_dev(const float* x, int64_t N, const int64_t* bat
   GEO_REQUIRE(radius != nullptr, "radius_graph: null device radius");
   return radius_emit_impl(x, N, batch, B, points_per_cloud, 0.f, radius, max_num_neighbors, loop,
                           row_ptr, row_out, col_out, workspace, workspace_bytes, stream);
+}
+
+// Asynchronous form of the two phases: the count also writes E into mapped pinned host memory
+// (edges_host: a host pointer from hipHostMalloc, e.g. a pin_memory tensor), and the emit can be
+// issued at once into bound-sized buffers (N * max_num_neighbors entries) before the host has
+// read E; geo_radius_copy_edges then moves the first E entries into the exact-sized outputs.
+// radius_dev, when not NULL, replaces r2 / r_cell (as geo_radius_count_dev).
+extern "C" int geo_radius_count_async(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                                      int64_t points_per_cloud, const uint8_t* mask, float r2,
+                                      float r_cell, const double* radius_dev,
+                                      int64_t max_num_neighbors, int loop, int64_t* row_ptr,
+                                      int64_t* edges_host, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  GEO_REQUIRE(edges_host != nullptr, "radius_graph: null edges_host");
+  int64_t* host_dev = nullptr;
+  GEO_HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&host_dev), edges_host, 0));
+  GEO_REQUIRE(host_dev != nullptr, "radius_graph: edges_host is not mapped pinned memory");
+  if (radius_dev) { r2 = 0.f; r_cell = 1.f; }
+  return radius_count_impl(x, N, batch, B, points_per_cloud, mask, r2, r_cell, radius_dev,
+                           max_num_neighbors, loop, row_ptr, workspace, workspace_bytes, stream,
+                           host_dev);
+}
+
+namespace geo {
+namespace {
+__global__ void rg_copy_edges(const int64_t* __restrict__ src_row, const int64_t* __restrict__ src_col,
+                              int64_t E, int64_t* __restrict__ row, int64_t* __restrict__ col) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < E; q += stride) {
+    row[q] = src_row[q];
+    col[q] = src_col[q];
+  }
+}
+}  // namespace
+}  // namespace geo
+
+extern "C" int geo_radius_copy_edges(const int64_t* src_row, const int64_t* src_col, int64_t E,
+                                     int64_t* row, int64_t* col, void* stream) {
+  GEO_REQUIRE(E >= 0, "radius_graph: negative edge count");
+  if (E == 0) return GEO_OK;
+  GEO_REQUIRE(src_row && src_col && row && col, "radius_graph: null edge arrays");
+  int64_t blocks = ceil_div(E, 256);
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(rg_copy_edges, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     as_stream(stream), src_row, src_col, E, row, col);
+  GEO_LAUNCH_CHECK("rg_copy_edges");
+  return GEO_OK;
 }

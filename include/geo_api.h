@@ -161,6 +161,23 @@ int geo_radius_emit_dev(const float* x, int64_t N, const int64_t* batch, int64_t
                         int64_t* row_out, int64_t* col_out, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/*
+ * The two phases without a host wait between them.  geo_radius_count_async is geo_radius_count
+ * (or geo_radius_count_dev when radius_dev is not NULL) that also writes E into edges_host, one
+ * int64 of mapped pinned host memory (hipHostMalloc'd, e.g. a pin_memory tensor).  The caller
+ * records an event, calls geo_radius_emit[_dev] at once with outputs of the bound size
+ * N * max_num_neighbors, waits for the event, reads E, allocates row_out[E], col_out[E] and calls
+ * geo_radius_copy_edges to move the first E emitted entries there.  The same sync as the
+ * reference's (geoembodied/csrc/__init__.py:130-186), taken off the GPU's critical path.
+ */
+int geo_radius_count_async(const float* x, int64_t N, const int64_t* batch, int64_t B,
+                           int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,
+                           const double* radius_dev, int64_t max_num_neighbors, int loop,
+                           int64_t* row_ptr, int64_t* edges_host, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int geo_radius_copy_edges(const int64_t* src_row, const int64_t* src_col, int64_t E,
+                          int64_t* row_out, int64_t* col_out, void* stream);
+
 /* ---------------------------------------------------- adaptive radius statistic --- */
 /*
  * Device-side statistic of column `col` of a KNN distance matrix dist [N, k] (fp32 squared
