@@ -57,6 +57,20 @@ struct Vec {
   __device__ __forceinline__ void load(const T* p) {
     raw = *reinterpret_cast<const typename Raw<VB>::type*>(p);
   }
+  // Message rows are read once per reduction: non-temporal (streaming) loads.
+  __device__ __forceinline__ void load_stream(const T* p) {
+    if constexpr (VB == 16) {
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+      raw.x = v.x; raw.y = v.y; raw.z = v.z; raw.w = v.w;
+    } else if constexpr (VB == 8) {
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+      raw.x = v.x; raw.y = v.y;
+    } else {
+      raw = __builtin_nontemporal_load(reinterpret_cast<const typename Raw<VB>::type*>(p));
+    }
+  }
   // Outputs are written once and not read back by this kernel: non-temporal (streaming) stores
   // keep them from displacing the message rows in the caches.
   __device__ __forceinline__ void store(T* p) const {
@@ -442,7 +456,7 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool ok = f0 + u < hi && static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E);
-        buf[u].load(msg + static_cast<int64_t>(ok ? rows[u] : 0) * C + col_off);
+        buf[u].load_stream(msg + static_cast<int64_t>(ok ? rows[u] : 0) * C + col_off);
       }
       int ecur[MAX ? U : 1];
       uint32_t rok = 0;
