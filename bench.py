@@ -373,7 +373,15 @@ def main() -> int:
             with torch.no_grad():
                 return conv(fs, fv, gr)
 
+        # a training step's backward: gradients start empty (zero_grad(set_to_none=True)), so
+        # no accumulation adds enter either side's timing
+        def clear_grads():
+            conv.zero_grad(set_to_none=True)
+            fs.grad = None
+            fv.grad = None
+
         def se3_fb():
+            clear_grads()
             so, vo = conv(fs, fv, gr)
             torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
 
@@ -382,6 +390,7 @@ def main() -> int:
                 return _se3_reference_torch(conv, fs, fv, gr)
 
         def ref_fb():
+            clear_grads()
             so, vo = _se3_reference_torch(conv, fs, fv, gr)
             torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
 

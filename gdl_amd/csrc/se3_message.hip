@@ -784,8 +784,10 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float*
 // (64 scalar channels as 4 per lane, 16 vector / type-2 channels as 1 per lane, per chunk), and
 // the 21 per-edge sums are reduced within the row.  With one chunk (ONE) the target's gradient
 // row stays in registers for all of its edges.
+// Without the type-2 paths the kernel fits 75 registers: six waves per SIMD instead of four
+// (measured 207 -> 165 us at C2); with them the register file sets the occupancy.
 template <bool ONE, bool T2>
-__global__ __launch_bounds__(kSeThreads) void se3_bwd_edge(SeEdges g, SeFeat f,
+__global__ __launch_bounds__(kSeThreads, T2 ? 1 : 6) void se3_bwd_edge(SeEdges g, SeFeat f,
                                                           const float* __restrict__ Gs, int Ks,
                                                           const float* __restrict__ Gv, int Kv,
                                                           const float* __restrict__ Gt, int Kt,
