@@ -162,12 +162,18 @@ __global__ __launch_bounds__(kRbThreads) void radial_fwd_kernel(RbParams p, floa
   }
 }
 
-__global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, const float* __restrict__ dR,
+__global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, const float* __restrict__ dR,
                                                                float* __restrict__ ddist,
                                                                float* __restrict__ part) {
-  __shared__ float tz[kRbWaves][16][kRbMaxHidden + 1];   // dZ of 16 edges, per wave
-  __shared__ float tx[kRbWaves][16][17];                  // X of 16 edges x 16 basis, per wave
-  __shared__ float red[kRbWaves][kRbPart];
+  // The edge-loop transposes (tz, tx) and the final per-wave partials (red) share one LDS buffer
+  // (a barrier separates them): 34 KB per block instead of 55 KB, so LDS no longer caps the
+  // occupancy below what the registers allow.
+  constexpr int kTz = kRbWaves * 16 * (kRbMaxHidden + 1), kTx = kRbWaves * 16 * 17;
+  constexpr int kRed = kRbWaves * kRbPart;
+  __shared__ float smem[kTz + kTx > kRed ? kTz + kTx : kRed];
+  auto tz = reinterpret_cast<float (*)[16][kRbMaxHidden + 1]>(smem);  // dZ of 16 edges, per wave
+  auto tx = reinterpret_cast<float (*)[16][17]>(smem + kTz);          // X of 16 edges x 16 basis
+  auto red = reinterpret_cast<float (*)[kRbPart]>(smem);
   const float pic = 3.14159265358979323846f / p.cutoff;
   const int lane = lane_id();
   const int g = lane >> 4, li = lane & 15;
@@ -283,6 +289,7 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_kernel(RbParams p, cons
   }
   db2p += __shfl_xor(db2p, 16, kWave);
   db2p += __shfl_xor(db2p, 32, kWave);
+  __syncthreads();  // every wave is past its edge loop: tz / tx are dead, red may overwrite them
   float* my = red[wave];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb)
@@ -401,7 +408,8 @@ extern "C" int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* fre
     return set_error(GEO_ERR_WORKSPACE, "radial_mlp_bwd: workspace %zu bytes, need %zu",
                      workspace_bytes, need);
   RbParams p{dist, E, freqs, NB, cutoff, W1, b1, H, W2, b2, P};
-  const unsigned nblk = rb_blocks(E);
+  // three waves per SIMD fit the backward: one resident round of 768 blocks on 256 CUs
+  const unsigned nblk = rb_blocks(E) < 768u ? rb_blocks(E) : 768u;
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL(radial_bwd_kernel, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part);
   GEO_LAUNCH_CHECK("radial_bwd_kernel");
