@@ -12,6 +12,8 @@
 // is walked three times (max, sum, write), so the exponentials that are summed are exactly the
 // ones that are divided; the sum runs in ascending edge order.  Rows are H consecutive values,
 // so the H threads of a segment read one row together.
+#include <initializer_list>
+
 #include "common.hpp"
 
 namespace geo {
@@ -265,10 +267,300 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_bwd(
   }
 }
 
+
+// ------------------------------------------------------- fp32, H in {1, 2, 4, 8} ---
+// The same row layout with H a compile-time constant: a row of H scores is one 4/8/16-byte
+// vector access (two for H = 8), every exponential is computed once and kept for the division,
+// and a wave takes SQ groups of segments whose CSR bounds, permutation entries and rows are all
+// requested before the first is used, so the three dependent loads of one group overlap those
+// of the others.  Short segments (the host picks by average degree) take 8 lanes each, so
+// fewer lane slots idle; each lane sums its chunks in order, then the row is reduced.
+template <int HH>
+__device__ __forceinline__ void sm_load(const float* __restrict__ x, int r, float (&v)[HH]) {
+  const float* p = x + static_cast<int64_t>(r) * HH;
+  if constexpr (HH == 1) {
+    v[0] = p[0];
+  } else if constexpr (HH == 2) {
+    const float2 q = *reinterpret_cast<const float2*>(p);
+    v[0] = q.x; v[1] = q.y;
+  } else {
+#pragma unroll
+    for (int j = 0; j < HH / 4; ++j) {
+      const float4 q = *reinterpret_cast<const float4*>(p + 4 * j);
+      v[4 * j] = q.x; v[4 * j + 1] = q.y; v[4 * j + 2] = q.z; v[4 * j + 3] = q.w;
+    }
+  }
+}
+
+template <int HH>
+__device__ __forceinline__ void sm_store(float* __restrict__ y, int r, const float (&v)[HH]) {
+  float* p = y + static_cast<int64_t>(r) * HH;
+  if constexpr (HH == 1) {
+    p[0] = v[0];
+  } else if constexpr (HH == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < HH / 4; ++j)
+      *reinterpret_cast<float4*>(p + 4 * j) = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+  }
+}
+
+// Segments take LW = 8 or 16 lanes (one DPP half-row or row) and a lane keeps its first KC
+// chunks of LW edges (32 edges) in registers; a wave serves SQ groups of 64 / LW segments.
+template <int HH, int LW>
+constexpr int sm_quads() { return (LW == 8 || HH >= 8) ? 1 : 2; }
+
+template <int LW>
+__device__ __forceinline__ float grp_maxf(float v) {
+  v = fmaxf(v, sm_dpp<kDppXor1>(v));
+  v = fmaxf(v, sm_dpp<kDppXor2>(v));
+  v = fmaxf(v, sm_dpp<kDppHalfMirror>(v));
+  if constexpr (LW == 16) v = fmaxf(v, sm_dpp<kDppMirror>(v));
+  return v;
+}
+template <int LW>
+__device__ __forceinline__ float grp_sumf(float v) {
+  v += sm_dpp<kDppXor1>(v);
+  v += sm_dpp<kDppXor2>(v);
+  v += sm_dpp<kDppHalfMirror>(v);
+  if constexpr (LW == 16) v += sm_dpp<kDppMirror>(v);
+  return v;
+}
+
+// Bounds of the segment of group `quad` that this lane serves.
+template <int LW>
+__device__ __forceinline__ void sm_bounds(const int32_t* ns, const int32_t* ne, int32_t E, int64_t S,
+                                          int64_t quad, int& a, int& b) {
+  const int64_t s = quad * (kWave / LW) + lane_id() / LW;
+  a = 0;
+  b = 0;
+  if (s < S) {
+    a = clamp_idx(ns[s], 0, E);
+    b = clamp_idx(ne[s], a, E);
+  }
+}
+
+template <int HH, int LW>
+__global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
+    const float* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
+    const int32_t* __restrict__ ne, int32_t E, int64_t S, float* __restrict__ w) {
+  constexpr int SQ = sm_quads<HH, LW>();
+  constexpr int KC = 32 / LW;
+  const int li = lane_id() & (LW - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kSmThreads / kWave) + threadIdx.x / kWave;
+  int a[SQ], b[SQ], rk[SQ][KC];
+  float v[SQ][KC][HH];
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) sm_bounds<LW>(ns, ne, E, S, wave * SQ + q, a[q], b[q]);
+#pragma unroll
+  for (int q = 0; q < SQ; ++q)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int e = a[q] + LW * c + li;
+      rk[q][c] = e < b[q] ? sm_row(perm, E, e) : -1;
+    }
+#pragma unroll
+  for (int q = 0; q < SQ; ++q)
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      if (rk[q][c] >= 0) sm_load<HH>(x, rk[q][c], v[q][c]);
+      else
+#pragma unroll
+        for (int h = 0; h < HH; ++h) v[q][c][h] = 0.f;
+    }
+
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    const int nch = uniform_max((b[q] - a[q] + LW - 1) / LW);
+    auto row_of = [&](int c) -> int {
+      const int e = a[q] + LW * c + li;
+      return e < b[q] ? sm_row(perm, E, e) : -1;
+    };
+    // A NaN score is skipped by the max but makes the segment's sum, and with it every weight
+    // of the segment, NaN: the result torch's amax -> exp -> sum -> divide gives.
+    float m[HH], z[HH];
+#pragma unroll
+    for (int h = 0; h < HH; ++h) { m[h] = -__builtin_inff(); z[h] = 0.f; }
+    for (int c = 0; c < nch; ++c) {
+      float t[HH];
+      int r;
+      if (c < KC) {
+        r = rk[q][c];
+#pragma unroll
+        for (int h = 0; h < HH; ++h) t[h] = v[q][c][h];
+      } else {
+        r = row_of(c);
+        if (r >= 0) sm_load<HH>(x, r, t);
+      }
+      if (r >= 0)
+#pragma unroll
+        for (int h = 0; h < HH; ++h) m[h] = t[h] > m[h] ? t[h] : m[h];
+    }
+#pragma unroll
+    for (int h = 0; h < HH; ++h) m[h] = grp_maxf<LW>(m[h]);
+    // exponentials of the register-held chunks are computed once, summed and divided
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      if (c < nch)
+#pragma unroll
+        for (int h = 0; h < HH; ++h) v[q][c][h] = expf(v[q][c][h] - m[h]);
+    for (int c = 0; c < nch; ++c) {
+      if (c < KC) {
+        if (rk[q][c] >= 0)
+#pragma unroll
+          for (int h = 0; h < HH; ++h) z[h] += v[q][c][h];
+      } else {
+        const int r = row_of(c);
+        if (r >= 0) {
+          float t[HH];
+          sm_load<HH>(x, r, t);
+#pragma unroll
+          for (int h = 0; h < HH; ++h) z[h] += expf(t[h] - m[h]);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < HH; ++h) {
+      const float zz = grp_sumf<LW>(z[h]);
+      z[h] = zz < 1e-8f ? 1e-8f : zz;  // clamp(min=1e-8) keeps NaN, as torch's does
+    }
+    for (int c = 0; c < nch; ++c) {
+      float o[HH];
+      if (c < KC) {
+        if (rk[q][c] < 0) continue;
+#pragma unroll
+        for (int h = 0; h < HH; ++h) o[h] = v[q][c][h] / z[h];
+        sm_store<HH>(w, rk[q][c], o);
+      } else {
+        const int r = row_of(c);
+        if (r < 0) continue;
+        float t[HH];
+        sm_load<HH>(x, r, t);
+#pragma unroll
+        for (int h = 0; h < HH; ++h) o[h] = expf(t[h] - m[h]) / z[h];
+        sm_store<HH>(w, r, o);
+      }
+    }
+  }
+}
+
+template <int HH, int LW>
+__global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
+    const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S,
+    float* __restrict__ dx) {
+  constexpr int SQ = sm_quads<HH, LW>();
+  constexpr int KC = 32 / LW;
+  const int li = lane_id() & (LW - 1);
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kSmThreads / kWave) + threadIdx.x / kWave;
+  int a[SQ], b[SQ], r0[SQ];
+  float g0[SQ][HH], w0[SQ][HH];
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) sm_bounds<LW>(ns, ne, E, S, wave * SQ + q, a[q], b[q]);
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    const int e = a[q] + li;
+    r0[q] = e < b[q] ? sm_row(perm, E, e) : -1;
+  }
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    if (r0[q] >= 0) {
+      sm_load<HH>(g_, r0[q], g0[q]);
+      sm_load<HH>(w, r0[q], w0[q]);
+    } else {
+#pragma unroll
+      for (int h = 0; h < HH; ++h) { g0[q][h] = 0.f; w0[q][h] = 0.f; }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    const int nch = uniform_max((b[q] - a[q] + LW - 1) / LW);
+    auto row_of = [&](int c) -> int {
+      const int e = a[q] + LW * c + li;
+      return e < b[q] ? sm_row(perm, E, e) : -1;
+    };
+    float dot[HH];
+#pragma unroll
+    for (int h = 0; h < HH; ++h) {
+      dot[h] = 0.f;
+      if (r0[q] >= 0) dot[h] += g0[q][h] * w0[q][h];
+    }
+    for (int c = 1; c < nch; ++c) {
+      const int r = row_of(c);
+      if (r < 0) continue;
+      float gv[HH], wv[HH];
+      sm_load<HH>(g_, r, gv);
+      sm_load<HH>(w, r, wv);
+#pragma unroll
+      for (int h = 0; h < HH; ++h) dot[h] += gv[h] * wv[h];
+    }
+#pragma unroll
+    for (int h = 0; h < HH; ++h) dot[h] = grp_sumf<LW>(dot[h]);
+    for (int c = 0; c < nch; ++c) {
+      float o[HH];
+      if (c == 0) {
+        if (r0[q] < 0) continue;
+#pragma unroll
+        for (int h = 0; h < HH; ++h) o[h] = w0[q][h] * (g0[q][h] - dot[h]);
+        sm_store<HH>(dx, r0[q], o);
+      } else {
+        const int r = row_of(c);
+        if (r < 0) continue;
+        float gv[HH], wv[HH];
+        sm_load<HH>(g_, r, gv);
+        sm_load<HH>(w, r, wv);
+#pragma unroll
+        for (int h = 0; h < HH; ++h) o[h] = wv[h] * (gv[h] - dot[h]);
+        sm_store<HH>(dx, r, o);
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace geo
 
 using namespace geo;
+
+// Head counts with a vector-row kernel, when every row pointer is aligned to its vector width.
+static bool sm_vec_ok(int64_t H, std::initializer_list<const void*> ps) {
+  if (H != 1 && H != 2 && H != 4 && H != 8) return false;
+  const uintptr_t al = H >= 4 ? 16 : static_cast<uintptr_t>(4 * H);
+  for (const void* p : ps)
+    if (reinterpret_cast<uintptr_t>(p) % al != 0) return false;
+  return true;
+}
+
+// Lanes per segment: 8 when segments average at most 12 edges, else 16.
+static int sm_lanes(int64_t E, int64_t S) { return E <= 12 * S ? 8 : 16; }
+
+template <template <int, int> class L, int LW, typename... Args>
+static void sm_launch_heads(int64_t H, int64_t S, hipStream_t st, Args... args) {
+  const int64_t per_wave = (kWave / LW) * ((LW == 8 || H >= 8) ? 1 : 2);
+  const dim3 grid(static_cast<unsigned>(ceil_div(S, per_wave * (kSmThreads / kWave))));
+  switch (H) {
+    case 1: hipLaunchKernelGGL((L<1, LW>::kernel), grid, dim3(kSmThreads), 0, st, args...); break;
+    case 2: hipLaunchKernelGGL((L<2, LW>::kernel), grid, dim3(kSmThreads), 0, st, args...); break;
+    case 4: hipLaunchKernelGGL((L<4, LW>::kernel), grid, dim3(kSmThreads), 0, st, args...); break;
+    default: hipLaunchKernelGGL((L<8, LW>::kernel), grid, dim3(kSmThreads), 0, st, args...); break;
+  }
+}
+
+template <int HH, int LW>
+struct SmFwd {
+  static constexpr auto kernel = seg_softmax_vec_fwd<HH, LW>;
+};
+template <int HH, int LW>
+struct SmBwd {
+  static constexpr auto kernel = seg_softmax_vec_bwd<HH, LW>;
+};
+
+template <template <int, int> class L, typename... Args>
+static void sm_launch_vec(int64_t E, int64_t H, int64_t S, hipStream_t st, Args... args) {
+  if (sm_lanes(E, S) == 8) sm_launch_heads<L, 8>(H, S, st, args...);
+  else sm_launch_heads<L, 16>(H, S, st, args...);
+}
 
 static int sm_check(int dtype, int64_t E, int64_t S, int64_t H) {
   GEO_REQUIRE(dtype == GEO_F32 || dtype == GEO_F64, "segment_softmax: dtype must be f32 or f64 (got %d)",
@@ -287,7 +579,10 @@ extern "C" int geo_segment_softmax_fwd(int dtype, const void* scores, const int3
   GEO_REQUIRE(scores && out && node_start && node_end, "segment_softmax: null pointer");
   const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
   hipStream_t st = as_stream(stream);
-  if (dtype == GEO_F32 && H <= kSmRowHeads) {
+  if (dtype == GEO_F32 && sm_vec_ok(H, {scores, out})) {
+    sm_launch_vec<SmFwd>(E, H, S, st, static_cast<const float*>(scores), perm, node_start, node_end,
+                         static_cast<int32_t>(E), S, static_cast<float*>(out));
+  } else if (dtype == GEO_F32 && H <= kSmRowHeads) {
     const unsigned rgrid = static_cast<unsigned>(ceil_div(S, 4 * (kSmThreads / kWave)));
     hipLaunchKernelGGL(seg_softmax_rows_fwd, dim3(rgrid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(scores), perm, node_start, node_end,
@@ -315,7 +610,11 @@ extern "C" int geo_segment_softmax_bwd(int dtype, const void* grad_out, const vo
               "segment_softmax_bwd: null pointer");
   const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
   hipStream_t st = as_stream(stream);
-  if (dtype == GEO_F32 && H <= kSmRowHeads) {
+  if (dtype == GEO_F32 && sm_vec_ok(H, {grad_out, out, grad_scores})) {
+    sm_launch_vec<SmBwd>(E, H, S, st, static_cast<const float*>(grad_out), static_cast<const float*>(out),
+                         perm, node_start, node_end, static_cast<int32_t>(E), S,
+                         static_cast<float*>(grad_scores));
+  } else if (dtype == GEO_F32 && H <= kSmRowHeads) {
     const unsigned rgrid = static_cast<unsigned>(ceil_div(S, 4 * (kSmThreads / kWave)));
     hipLaunchKernelGGL(seg_softmax_rows_bwd, dim3(rgrid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(grad_out), static_cast<const float*>(out), perm,

@@ -95,3 +95,69 @@ def test_softmax_gradcheck_fp64(dev):
     index = torch.randint(0, 7, (40,), generator=g).to(dev)
     x = torch.randn(40, 2, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
     assert torch.autograd.gradcheck(lambda t: sparse_softmax(t, index, 7), (x,))
+
+
+@pytest.mark.parametrize("H", [1, 2, 4, 8])
+@pytest.mark.parametrize("short", [False, True])
+def test_segment_softmax_vector_rows_long_segments(dev, H, short):
+    """Head counts with vector-row kernels, forward and backward, shuffled permutation.
+    short=False: segments of 0..100 edges (average 50: 16 lanes per segment, chunks past the
+    second re-read from memory).  short=True: mostly 0..8 edges with every 25th segment 33..70
+    long (average <= 12: 8 lanes per segment, chunks past the fourth re-read)."""
+    from gdl_amd.csrc import segment_softmax_backward_hip, segment_softmax_forward_hip
+    g = torch.Generator().manual_seed(40 + H + 100 * short)
+    N = 700
+    if short:
+        deg = torch.randint(0, 9, (N,), generator=g)
+        deg[::25] = torch.randint(33, 71, (deg[::25].numel(),), generator=g)
+        assert int(deg.sum()) <= 12 * N
+    else:
+        deg = torch.randint(0, 101, (N,), generator=g)
+    deg[::7] = 0
+    index = torch.repeat_interleave(torch.arange(N), deg)
+    E = index.numel()
+    sh = torch.randperm(E, generator=g)
+    index = index[sh]
+    x = torch.randn(E, H, generator=g) * 3
+    x[5 % E, 0] = float("nan")
+    order = torch.sort(index, stable=True).indices
+    cnt = torch.bincount(index, minlength=N)
+    ne = cnt.cumsum(0).int()
+    ns = (ne - cnt.int())
+    pm = order.int().to(dev)
+    w = segment_softmax_forward_hip(x.to(dev), pm, ns.to(dev), ne.to(dev), N)
+    ref = oracle.sparse_softmax(x.double().numpy(), index.numpy(), N)
+    got = w.cpu().double().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.all(np.abs(got[ok] - ref[ok]) <= 2e-6 + 1e-5 * np.abs(ref[ok]))
+    gr = torch.randn(E, H, generator=g)
+    dx = segment_softmax_backward_hip(gr.to(dev), w, pm, ns.to(dev), ne.to(dev), N)
+    want = oracle.sparse_softmax_bwd(gr.double().numpy(), got, index.numpy(), N)
+    got_dx = dx.cpu().double().numpy()
+    fin = np.isfinite(want)
+    assert np.all(np.abs(got_dx[fin] - want[fin]) <= 2e-6 + 1e-5 * np.abs(want[fin]))
+
+
+def test_segment_softmax_misaligned_rows_match_aligned(dev):
+    """Rows not aligned to the vector width take the runtime-H kernel (16 lanes per segment;
+    the aligned rows here take 8): both within the oracle bar and within a few ulp of each
+    other."""
+    from gdl_amd.csrc import segment_softmax_forward_hip
+    g = torch.Generator().manual_seed(3)
+    E, N, H = 5000, 600, 4
+    index = torch.sort(torch.randint(0, N, (E,), generator=g)).values
+    cnt = torch.bincount(index, minlength=N)
+    ne = cnt.cumsum(0).int().to(dev)
+    ns = ne - cnt.int().to(dev)
+    x = torch.randn(E, H, generator=g).to(dev)
+    buf = torch.empty(E * H + 1, device=dev)
+    buf[1:] = x.reshape(-1)
+    xm = buf[1:].view(E, H)
+    assert xm.data_ptr() % 16 != 0
+    a = segment_softmax_forward_hip(x, None, ns, ne, N)
+    b = segment_softmax_forward_hip(xm, None, ns, ne, N)
+    ref = oracle.sparse_softmax(x.cpu().double().numpy(), index.numpy(), N)
+    _check(a, ref, torch.float32)
+    _check(b, ref, torch.float32)
+    torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-7)
