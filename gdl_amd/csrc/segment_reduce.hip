@@ -482,11 +482,14 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
         for (int i = 0; i < EPV; ++i) {
           const A v = to_acc(buf[u].e[i]);
           if constexpr (MAX) {
-            const bool gt = take && max_gt(v, acc[i]);
-            const bool eq = take && !gt && max_eq(v, acc[i]);
+            // max_gt / max_eq as mask logic (no short-circuit, so no branches): NaN above
+            // every number, all NaNs equal
+            const bool vn = v != v, an = acc[i] != acc[i];
+            const bool gt = take & ((v > acc[i]) | (vn & !an));
+            const bool eq = take & !gt & ((v == acc[i]) | (vn & an));
             const int pos = ecur[MAX ? u : 0];
             first[i] = gt ? pos : first[i];
-            cnt[i] = gt ? 1 : cnt[i] + (eq ? 1 : 0);
+            cnt[i] = (gt ? 0 : cnt[i]) + ((gt | eq) ? 1 : 0);
             acc[i] = gt ? v : acc[i];
           } else {
             acc[i] += take ? v : A(0);
