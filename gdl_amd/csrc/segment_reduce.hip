@@ -137,6 +137,12 @@ __device__ __forceinline__ A shfl_xor_acc(A v, int m) { return __shfl_xor(v, m, 
 
 __device__ __forceinline__ int clamp_i(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+// Element offset of row r (0 <= r < 2^31) in rows of c elements (c < 2^32, checked by the host):
+// one 32 x 32 -> 64-bit multiply instead of a signed 64-bit product.
+__device__ __forceinline__ int64_t row_off(int r, int64_t c) {
+  return static_cast<int64_t>(static_cast<uint64_t>(static_cast<uint32_t>(r)) * static_cast<uint32_t>(c));
+}
+
 template <typename T, int VB, int OP>
 __global__ __launch_bounds__(kSegThreads) void seg_fwd_kernel(
     const T* __restrict__ msg, const int32_t* __restrict__ perm,
@@ -456,7 +462,7 @@ __global__ __launch_bounds__(kMergeThreads) void seg_fwd_merge_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool ok = f0 + u < hi && static_cast<unsigned>(rows[u]) < static_cast<unsigned>(E);
-        buf[u].load_stream(msg + static_cast<int64_t>(ok ? rows[u] : 0) * C + col_off);
+        buf[u].load_stream(msg + row_off(ok ? rows[u] : 0, C) + col_off);
       }
       int ecur[MAX ? U : 1];
       uint32_t rok = 0;
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
       const int64_t col_off = static_cast<int64_t>(vb) * EPV;
       V gv, res;
       if (s_ok) {
-        gv.load(grad_out + static_cast<int64_t>(s) * C + col_off);
+        gv.load(grad_out + row_off(s, C) + col_off);
       } else {
 #pragma unroll
         for (int i = 0; i < EPV; ++i) gv.e[i] = from_acc<T>(A(0));
@@ -613,7 +619,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
       } else {
         IVec<EPV> a;
         if (s_ok) {
-          a.load(arg + static_cast<int64_t>(s) * C + col_off);
+          a.load(arg + row_off(s, C) + col_off);
         } else {
 #pragma unroll
           for (int i = 0; i < EPV; ++i) a.e[i] = -1;
@@ -623,8 +629,8 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
         for (int i = 0; i < EPV; ++i) any_tie |= a.e[i] <= -2;
         V mv, ov;
         if (any_tie) {
-          mv.load(msg + static_cast<int64_t>(p) * C + col_off);
-          ov.load(fwd_out + static_cast<int64_t>(s) * C + col_off);
+          mv.load(msg + row_off(p, C) + col_off);
+          ov.load(fwd_out + row_off(s, C) + col_off);
         }
 #pragma unroll
         for (int i = 0; i < EPV; ++i) {
@@ -638,7 +644,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_bwd_kernel(
           res.e[i] = from_acc<T>(r);
         }
       }
-      res.store(grad_msg + static_cast<int64_t>(p) * C + col_off);
+      res.store(grad_msg + row_off(p, C) + col_off);
     }
     }
   }
@@ -762,6 +768,7 @@ extern "C" int geo_segment_reduce_fwd(int reduce, int dtype, const void* msg, co
   GEO_REQUIRE(E >= 0 && S >= 0 && C >= 0, "segment_reduce: negative size (E=%lld S=%lld C=%lld)",
               (long long)E, (long long)S, (long long)C);
   GEO_REQUIRE(E < 0x7fffffffLL, "segment_reduce: E=%lld exceeds int32 indexing", (long long)E);
+  GEO_REQUIRE(C <= 0xffffffffLL, "segment_reduce: C=%lld exceeds 32 bits", (long long)C);
   if (S == 0 || C == 0) return GEO_OK;
   GEO_REQUIRE(out != nullptr && node_start != nullptr && node_end != nullptr,
               "segment_reduce: null output or offsets");
@@ -816,6 +823,7 @@ extern "C" int geo_segment_reduce_bwd(int reduce, int dtype, const void* grad_ou
               "segment_reduce_bwd: unknown dtype code %d", dtype);
   GEO_REQUIRE(E >= 0 && S >= 0 && C >= 0, "segment_reduce_bwd: negative size");
   GEO_REQUIRE(E < 0x7fffffffLL, "segment_reduce_bwd: E=%lld exceeds int32 indexing", (long long)E);
+  GEO_REQUIRE(C <= 0xffffffffLL, "segment_reduce_bwd: C=%lld exceeds 32 bits", (long long)C);
   if (E == 0 || C == 0) return GEO_OK;
   GEO_REQUIRE(grad_msg != nullptr && col_sorted != nullptr, "segment_reduce_bwd: null pointer");
   GEO_REQUIRE(S == 0 || grad_out != nullptr, "segment_reduce_bwd: null grad_out");
