@@ -474,8 +474,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__
 // gradients (output gradients x per-node aggregates, summed over nodes).  The reduction
 // dimension M is long and O, K are small, so the rows are split over the waves of the grid;
 // each wave accumulates its OB x KB tiles of 16 x 16 in MFMA accumulators (A^T as the MFMA A
-// operand, B as the B operand, k = rows) and writes them as one partial; se3_gemm_tn_final adds
-// the partials in a fixed order.
+// operand, B as the B operand, k = rows), the block's waves are added in LDS and the block
+// writes one partial; se3_gemm_tn_final adds the partials in a fixed order.
 template <int OB, int KB>
 __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn(const float* __restrict__ A, int64_t M,
                                                          int lda, int O,
@@ -485,7 +485,8 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn(const float* __restric
                                                          int Kpad) {
   const int lane = lane_id();
   const int g = lane >> 4, li = lane & 15;
-  const int64_t wid = static_cast<int64_t>(blockIdx.x) * kSeWaves + uniform(threadIdx.x / kWave);
+  const int w = uniform(threadIdx.x / kWave);
+  const int64_t wid = static_cast<int64_t>(blockIdx.x) * kSeWaves + w;
   const int ob0 = (blockIdx.y / kb_groups) * OB, kb0 = (blockIdx.y % kb_groups) * KB;
   const int64_t r_begin = wid * rows_per_wave;
   const int64_t r_end = min(M, r_begin + rows_per_wave);
@@ -519,7 +520,34 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn(const float* __restric
         for (int kb = 0; kb < KB; ++kb)
           acc[ob][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ob][q], b[kb][q], acc[ob][kb], 0, 0, 0);
   }
-  float* my = part + wid * static_cast<int64_t>(Opad) * Kpad;
+  // The block's four waves add their tiles in LDS, (w0 + w2) + (w1 + w3), so one partial per
+  // block reaches memory and the grid can hold many more waves for the same partial traffic.
+  static_assert(kSeWaves == 4, "two reduction rounds");
+  __shared__ floatx4 red[2][OB * KB][kWave];
+  if (w >= 2)
+#pragma unroll
+    for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) red[w - 2][ob * KB + kb][lane] = acc[ob][kb];
+  __syncthreads();
+  if (w < 2)
+#pragma unroll
+    for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) acc[ob][kb] += red[w][ob * KB + kb][lane];
+  __syncthreads();
+  if (w == 1)
+#pragma unroll
+    for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) red[0][ob * KB + kb][lane] = acc[ob][kb];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int ob = 0; ob < OB; ++ob)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) acc[ob][kb] += red[0][ob * KB + kb][lane];
+  float* my = part + static_cast<int64_t>(blockIdx.x) * Opad * Kpad;
 #pragma unroll
   for (int ob = 0; ob < OB; ++ob)
 #pragma unroll
@@ -559,13 +587,14 @@ struct TnPlan {
 TnPlan tn_plan(int64_t M, int O, int K) {
   TnPlan t;
   const int nob = (O + 15) / 16, nkb = (K + 15) / 16;
-  t.ob = nob <= 1 ? 1 : (nob <= 2 ? 2 : 4);
+  t.ob = nob <= 1 ? 1 : 2;  // wider O tiles spill accumulators in the LDS reduction
   const int kb = nkb < 8 ? nkb : 8;
   t.kb = kb <= 2 ? 2 : (kb <= 4 ? 4 : (kb <= 6 ? 6 : 8));
   t.kb_groups = (nkb + t.kb - 1) / t.kb;
   t.groups = ((nob + t.ob - 1) / t.ob) * t.kb_groups;
-  int64_t blocks = ceil_div(M, 1024);
-  blocks = blocks < 1 ? 1 : (blocks > 128 ? 128 : blocks);
+  // about 64 rows per wave (four 16-row steps), at most 512 blocks (2048 waves)
+  int64_t blocks = ceil_div(M, 256);
+  blocks = blocks < 1 ? 1 : (blocks > 512 ? 512 : blocks);
   t.nparts_x = static_cast<int>(blocks);
   t.rows_per_wave = ceil_div(ceil_div(M, blocks * kSeWaves), 16) * 16;
   return t;
@@ -1182,7 +1211,7 @@ extern "C" size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t 
   if (M < 0 || O < 0 || K < 0) return 0;
   const TnPlan t = tn_plan(M, O, K);
   const int64_t Opad = ((O + 15) / 16) * 16, Kpad = ((K + 15) / 16) * 16;
-  return static_cast<size_t>(t.nparts_x) * kSeWaves * Opad * Kpad * sizeof(float);
+  return static_cast<size_t>(t.nparts_x) * Opad * Kpad * sizeof(float);
 }
 
 extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B,
@@ -1211,7 +1240,7 @@ extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O
   GEO_TN(4, 2) GEO_TN(4, 4) GEO_TN(4, 6) GEO_TN(4, 8)
 #undef GEO_TN
   GEO_LAUNCH_CHECK("se3_gemm_tn");
-  const int nparts = t.nparts_x * kSeWaves;
+  const int nparts = t.nparts_x;
   hipLaunchKernelGGL(se3_gemm_tn_final,
                      dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(Opad) * Kpad, 64))),
                      dim3(kSeThreads), 0, st, part, nparts, Opad, Kpad, O, K, out, ldo);
