@@ -413,8 +413,8 @@ int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B, int32_t B
  */
 /*
  * Weight gradients as one long reduction: out[o * ldo + k] = sum_{r < M} A[r * lda + o] *
- * B[r * ldb + k] for o < O, k < K (fp32 MFMA, rows split over the grid, per-wave partials in the
- * workspace added in a fixed order).
+ * B[r * ldb + k] for o < O, k < K (fp32 MFMA, rows split over the grid, one partial per
+ * workgroup in the workspace, partials added in a fixed order).
  */
 size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t K);
 int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B, int32_t ldb,
