@@ -150,6 +150,7 @@ constexpr int kKnnGridMaxAxis = 1024;
 constexpr int kKnnGridMaxK = 32;
 constexpr double kKnnCellTarget = 0.25;  // points per cell per neighbour (measured best)
 constexpr int kKnnCellCap = 2;            // cells per point
+constexpr int64_t kKnnWideSources = 65536; // one cloud this large: 32 lanes per query for k <= 8
 
 struct KnnGrid {
   float ox, oy, oz, inv_h, h;
@@ -511,17 +512,28 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
   if (rc) return rc;
   hipLaunchKernelGGL(knn_grid_scatter, dim3(gs), dim3(kKnnGridThreads), 0, st, source, Ns, w);
   GEO_LAUNCH_CHECK("knn_grid_scatter");
-#define GEO_KNN_GRID_CASE(KV, GV)                                                               \
-  if (k <= KV) {                                                                                \
+  // Lanes per query: a wave runs as long as its slowest query.  In one scene-scale cloud (a
+  // lidar frame) density varies by orders of magnitude, so the few queries in dense regions
+  // scan hundreds of candidates: 32 lanes per query for k <= 8 there (C5: 0.42 -> 0.22 ms);
+  // batched object-scale clouds are near uniform and do best with 8 (32 costs them ~10%).
+  const bool wide = B == 1 && Ns >= kKnnWideSources;
+#define GEO_KNN_GRID_LAUNCH(KV, GV)                                                             \
+  {                                                                                             \
     const unsigned gq = static_cast<unsigned>(ceil_div(Nq * GV, kKnnGridThreads));             \
     hipLaunchKernelGGL((knn_grid_query<KV, GV>), dim3(gq), dim3(kKnnGridThreads), 0, st, query, \
                        Nq, ptr_q, B, w, k, out_idx, out_dist);                                  \
     GEO_LAUNCH_CHECK("knn_grid_query");                                                         \
     return GEO_OK;                                                                              \
   }
+#define GEO_KNN_GRID_CASE(KV, GV)                                                               \
+  if (k <= KV) {                                                                                \
+    if (GV == 8 && wide) GEO_KNN_GRID_LAUNCH(KV, 32)                                             \
+    GEO_KNN_GRID_LAUNCH(KV, GV)                                                                 \
+  }
   GEO_KNN_GRID_CASE(1, 8) GEO_KNN_GRID_CASE(2, 8) GEO_KNN_GRID_CASE(4, 8)
   GEO_KNN_GRID_CASE(8, 8) GEO_KNN_GRID_CASE(16, 16) GEO_KNN_GRID_CASE(32, 16)
 #undef GEO_KNN_GRID_CASE
+#undef GEO_KNN_GRID_LAUNCH
   return set_error(GEO_ERR_UNSUPPORTED, "knn: k=%d unsupported by the grid search", k);
 }
 

@@ -213,6 +213,15 @@ def _knn_grid_problem(kind, g):
         s = torch.randn(9000, 3, generator=g)
         q = torch.randn(800, 3, generator=g)
         return q, s, torch.tensor([50, 300, 300, 700]), _ptr([4000, 3000, 2000])
+    elif kind == "scene":    # one 70,000-point cloud, density varying ~1000x (32 lanes per query)
+        dense = torch.randn(20000, 3, generator=g) * 0.05
+        ring = torch.rand(30000, generator=g) * 6.2832
+        rad = 1.0 + 9.0 * torch.rand(30000, generator=g)
+        rings = torch.stack([rad * ring.cos(), rad * ring.sin(), 0.02 * torch.randn(30000, generator=g)], 1)
+        sparse = (torch.rand(20000, 3, generator=g) - 0.5) * torch.tensor([40.0, 40.0, 4.0])
+        s = torch.cat([dense, rings, sparse])
+        q = torch.cat([s[torch.randperm(70000, generator=g)[:500]], torch.randn(100, 3, generator=g) * 8])
+        ss, qs = [70000], [600]
     else:                    # "nonfinite": one source at inf -> the cloud falls back to one cell
         s = torch.randn(5000, 3, generator=g)
         s[17] = float("inf")
@@ -222,7 +231,7 @@ def _knn_grid_problem(kind, g):
 
 
 @pytest.mark.parametrize("kind", ["cube", "lattice", "sphere", "plane", "small_cloud", "uncovered",
-                                  "nonfinite"])
+                                  "nonfinite", "scene"])
 @pytest.mark.parametrize("k", [1, 3, 8, 16, 17, 32])
 def test_knn_grid_vs_oracle(dev, kind, k):
     g = torch.Generator().manual_seed(k * 31 + len(kind))
