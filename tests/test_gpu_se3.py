@@ -46,6 +46,30 @@ def test_gemm_kernel_vs_torch(dev):
         _close(out, want, 1e-5, 1e-6)
 
 
+def test_gemm_tn_kernel_vs_torch(dev):
+    """Weight-gradient GEMM out[o][k] = sum_r A[r][o] B[r][k] (rows split over up to 512
+    workgroups, the four waves of a workgroup added in LDS, partials added in a fixed order):
+    O and K off the 16-tiles, several tile groups along O and K, M below one 16-row step, M not a
+    multiple of 16, and a long M with strided rows (lda > O, ldb > K)."""
+    from gdl_amd import _native as nat
+    L = nat.lib()
+    g = torch.Generator().manual_seed(5)
+    for (M, O, K, lda, ldb) in [(7, 5, 9, 5, 9), (1000, 64, 80, 64, 80), (196611, 16, 96, 20, 100),
+                                (5000, 100, 200, 100, 200), (65536, 33, 17, 48, 32), (0, 8, 8, 8, 8)]:
+        A = torch.randn(M, lda, generator=g)
+        B = torch.randn(M, ldb, generator=g)
+        out = torch.full((O, K + 3), float("nan"), device=dev)
+        nbytes = L.geo_se3_gemm_tn_workspace_bytes(M, O, K)
+        ws = nat.workspace(nbytes, torch.device(dev))
+        Ad, Bd = A.to(dev), B.to(dev)
+        nat.check(L.geo_se3_gemm_tn(nat.ptr(Ad), M, lda, O, nat.ptr(Bd), ldb, K, nat.ptr(out), K + 3,
+                                    nat.ptr(ws), nbytes, nat.stream_of(torch.device(dev))),
+                  "geo_se3_gemm_tn")
+        want = A[:, :O].double().t() @ B[:, :K].double()
+        _close(out[:, :K], want, 1e-5, 1e-6)
+        assert torch.isnan(out[:, K:]).all()  # columns past K untouched
+
+
 def _graph(N, B, r, K, seed, shuffle):
     from gdl_amd.graph import SpatialGraph
     g = torch.Generator().manual_seed(seed)
