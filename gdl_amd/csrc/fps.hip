@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kFpsStreamThreads) void fps_stream_kernel(
 // runs it.  One 1024-thread workgroup per cloud; lane l of wave w holds the records of buckets
 // w + 16 (l + 64 r), r < kFpsLargeSlots: box, max min-distance, lowest index attaining it and
 // that point's position.  Per iteration each wave tests its buckets with the exact lower bound
-// above, reloads and updates only the buckets the new centroid can change (four at a time, so
+// above, reloads and updates only the buckets the new centroid can change (two at a time, so
 // their loads overlap), recomputes its best (distance, index) only when one of its buckets
 // changed, and the workgroup agrees on the winner with one LDS 64-bit atomic max per wave on
 // (bits << 32) | (index complement << 4 | wave) and one barrier.
@@ -664,8 +664,10 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
       act[r] = __ballot(__float_as_uint(lb) < bmax[r]);
     }
     while (act[0] | act[1] | act[2]) {
-      // up to four affected buckets of this wave per round, their loads issued together
-      constexpr int G = 4;
+      // up to two affected buckets of this wave per round, their loads issued together (C5:
+      // one or two per round 36.5 ms, three 37.3, four 38.6, eight 46.4: every slot of a round
+      // costs its loads and reductions, and the busiest wave rarely has more than two)
+      constexpr int G = 2;
       int rr[G], ll[G];
 #pragma unroll
       for (int j = 0; j < G; ++j) {
