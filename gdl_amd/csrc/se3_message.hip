@@ -244,7 +244,8 @@ __device__ __forceinline__ void node_range(const SeEdges& g, int64_t n, int& a, 
   b = b < a ? a : (b > g.E ? g.E : b);
 }
 
-constexpr int kSeUnroll = 4;  // edges whose source rows are in flight together
+constexpr int kSeUnroll = 2;  // edges whose source rows are in flight together (C2: 2, 3, 4 give
+                              // the same forward aggregate; the source-side backward 112 / 125 / 123 us)
 
 // The dispatcher hands workgroups to the 8 XCDs in turn (workgroup b to XCD b mod 8).  This
 // renumbering gives each XCD one contiguous range of the node space, so neighbouring nodes --
