@@ -44,6 +44,7 @@ _SIGNATURES = {
                                 c_int, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_csr_workspace_bytes": (c_size, [c_i64, c_i64]),
     "geo_csr_build": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
+    "geo_csr_build_noalloc": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_csr_from_row_ptr": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_spatial_graph_epilogue": (c_int, [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_i64,
                                            c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,

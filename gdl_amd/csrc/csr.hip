@@ -6,6 +6,8 @@
 // Targets outside [0, N) get key N and sort after all valid targets.  node_start/node_end come
 // from binary searches in the sorted keys (node_start[n] = first position with key >= n), so
 // empty targets get start == end and no atomics are involved.
+#include <mutex>
+
 #include "radix.hpp"
 
 namespace geo {
@@ -39,6 +41,73 @@ RadixBuffers carve_csr(void* base, int64_t E, size_t* bytes) {
   return r;
 }
 
+// The sort and the bounds, given the scratch (E > 0 or N > 0 checked by the caller).
+int csr_build_into(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted, int32_t* perm,
+                   int32_t* node_start, int32_t* node_end, const RadixBuffers& w, hipStream_t st) {
+  if (E == 0) {
+    if (N == 0) return GEO_OK;
+    int rc = device_fill<int32_t>(node_start, N, 0, st);
+    if (rc) return rc;
+    return device_fill<int32_t>(node_end, N, 0, st);
+  }
+  // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one pass
+  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),
+                                reinterpret_cast<uint32_t*>(col_sorted),
+                                reinterpret_cast<uint32_t*>(perm), w, st, true);
+  if (rc) return rc;
+  if (N > 0) {
+    hipLaunchKernelGGL(csr_bounds, dim3(ceil_div(N + 1, 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint32_t*>(col_sorted), E, N, node_start, node_end);
+    GEO_LAUNCH_CHECK("csr_bounds");
+  }
+  return GEO_OK;
+}
+
+int csr_check_args(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted, int32_t* perm,
+                   int32_t* node_start, int32_t* node_end) {
+  GEO_REQUIRE(E >= 0 && N >= 0, "csr_build: negative size (E=%lld N=%lld)", (long long)E,
+              (long long)N);
+  GEO_REQUIRE(E < 0x7fffffffLL && N < 0x7fffffffLL, "csr_build: sizes exceed int32 indexing");
+  GEO_REQUIRE(N == 0 || (node_start && node_end), "csr_build: null node_start/node_end");
+  GEO_REQUIRE(E == 0 || (col && col_sorted && perm), "csr_build: null edge arrays");
+  return GEO_OK;
+}
+
+// ------------------------------------------------------- build without allocation ---
+// Scratch of geo_csr_build_noalloc: one file-scope device array, so the entry point needs no
+// workspace argument and performs no allocation.  Sized for kNoAllocMaxEdges edges (the radix
+// buffers: four uint32 arrays of E entries, the per-tile digit histograms, the scan's tile sums
+// and the sorted-input flag; 20 MiB + 3 KiB at 2^20 edges).  The runtime gives every device its
+// own copy at its own address; the host never passes `scratch` itself to a kernel (in host code
+// it is a stand-in symbol, not a device address) but the address hipGetSymbolAddress returns
+// for the current device.
+constexpr int64_t kNoAllocMaxEdges = int64_t{1} << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t{20} << 20) + (size_t{64} << 10);
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kNoAllocMaxDevices];  // device address of `scratch` per device, set once
+
+// Device address of `scratch` on the current device (looked up on the first call per device).
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  GEO_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(GEO_ERR_UNSUPPORTED, "csr_build_noalloc: device %d beyond the %d supported",
+                     dev, kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    GEO_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr)
+      return set_error(GEO_ERR_HIP, "csr_build_noalloc: no device address for the scratch array");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return GEO_OK;
+}
+
 }  // namespace
 }  // namespace geo
 
@@ -54,35 +123,42 @@ extern "C" size_t geo_csr_workspace_bytes(int64_t E, int64_t N) {
 extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
                              int32_t* perm, int32_t* node_start, int32_t* node_end,
                              void* workspace, size_t workspace_bytes, void* stream) {
-  GEO_REQUIRE(E >= 0 && N >= 0, "csr_build: negative size (E=%lld N=%lld)", (long long)E,
-              (long long)N);
-  GEO_REQUIRE(E < 0x7fffffffLL && N < 0x7fffffffLL, "csr_build: sizes exceed int32 indexing");
-  hipStream_t st = as_stream(stream);
+  int rc = csr_check_args(col, E, N, col_sorted, perm, node_start, node_end);
+  if (rc) return rc;
   size_t need = 0;
   const RadixBuffers w = carve_csr(workspace, E, &need);
   if (workspace_bytes < need || workspace == nullptr)
     return set_error(GEO_ERR_WORKSPACE, "csr_build: workspace %zu bytes, need %zu",
                      workspace_bytes, need);
-  GEO_REQUIRE(N == 0 || (node_start && node_end), "csr_build: null node_start/node_end");
-  GEO_REQUIRE(E == 0 || (col && col_sorted && perm), "csr_build: null edge arrays");
-
-  if (E == 0) {
-    if (N == 0) return GEO_OK;
-    int rc = device_fill<int32_t>(node_start, N, 0, st);
-    if (rc) return rc;
-    return device_fill<int32_t>(node_end, N, 0, st);
-  }
-
-  // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one pass
-  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),
-                                reinterpret_cast<uint32_t*>(col_sorted),
-                                reinterpret_cast<uint32_t*>(perm), w, st, true);
-  if (rc) return rc;
-  if (N > 0) {
-    hipLaunchKernelGGL(csr_bounds, dim3(ceil_div(N + 1, 256)), dim3(256), 0, st,
-                       reinterpret_cast<const uint32_t*>(col_sorted), E, N, node_start, node_end);
-    GEO_LAUNCH_CHECK("csr_bounds");
-  }
-  return GEO_OK;
+  return csr_build_into(col, E, N, col_sorted, perm, node_start, node_end, w, as_stream(stream));
 }
 
+extern "C" int geo_csr_build_noalloc(const int64_t* col, int64_t E, int64_t N,
+                                     int32_t* col_sorted, int32_t* perm, int32_t* node_start,
+                                     int32_t* node_end, void* stream) {
+  int rc = csr_check_args(col, E, N, col_sorted, perm, node_start, node_end);
+  if (rc) return rc;
+  if (E > kNoAllocMaxEdges)
+    return set_error(GEO_ERR_INVALID,
+                     "csr_build_noalloc: %lld edges exceed the %lld its fixed scratch holds "
+                     "(use geo_csr_build with a workspace)",
+                     (long long)E, (long long)kNoAllocMaxEdges);
+  size_t need = 0;
+  carve_csr(nullptr, E, &need);
+  if (need > kNoAllocScratchBytes)  // cannot happen for E <= kNoAllocMaxEdges
+    return set_error(GEO_ERR_INVALID, "csr_build_noalloc: needs %zu scratch bytes, has %zu", need,
+                     kNoAllocScratchBytes);
+  hipStream_t st = as_stream(stream);
+  void* base = nullptr;
+  rc = noalloc_scratch(&base);
+  if (rc) return rc;
+  if (st != nullptr) {
+    int sdev = -1, cur = -1;
+    GEO_HIP_CHECK(hipStreamGetDevice(st, &sdev));
+    GEO_HIP_CHECK(hipGetDevice(&cur));
+    GEO_REQUIRE(sdev == cur, "csr_build_noalloc: stream of device %d, current device %d", sdev,
+                cur);
+  }
+  const RadixBuffers w = carve_csr(base, E, &need);
+  return csr_build_into(col, E, N, col_sorted, perm, node_start, node_end, w, st);
+}

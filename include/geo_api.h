@@ -7,11 +7,13 @@
  *   - All pointers are device pointers unless the comment says "host".
  *   - The caller allocates every output and workspace; the library never allocates or frees
  *     device memory.  Workspace sizes come from the matching *_workspace_bytes() function.
+ *     (geo_csr_build_noalloc uses a fixed device array of the library instead.)
  *   - All work is enqueued asynchronously on `stream` (a hipStream_t passed as void*; NULL is
  *     the legacy default stream).  No entry point synchronises the host.
  *   - Return value: GEO_OK (0) or a GEO_ERR_* code.  geo_last_error() returns a message for the
  *     last failure on the calling thread (thread-local; valid until the next failing call).
- *   - No mutable global state: entry points are re-entrant and thread-safe.
+ *   - No mutable global state (except the fixed scratch of geo_csr_build_noalloc): entry
+ *     points are re-entrant and thread-safe.
  *   - Index tensors: int64 where the reference's Python API exposes int64, int32 for the CSR
  *     arrays (the reference's CSR is int32 as well).
  *
@@ -205,6 +207,16 @@ size_t geo_csr_workspace_bytes(int64_t E, int64_t N);
 int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
                   int32_t* perm, int32_t* node_start, int32_t* node_end, void* workspace,
                   size_t workspace_bytes, void* stream);
+/* geo_csr_build without a workspace argument and without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The radix-sort scratch is a fixed
+ * 20 MiB device array inside the library, one copy per GPU, held until the process ends; E is
+ * limited to 2^20 = 1,048,576 edges (larger E returns GEO_ERR_INVALID: use geo_csr_build).  The
+ * scratch of a GPU is shared by every call on it, so calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.  `stream` must belong to
+ * the current device.  Same outputs as geo_csr_build, bit for bit. */
+int geo_csr_build_noalloc(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
+                          int32_t* perm, int32_t* node_start, int32_t* node_end, void* stream);
 /* The same four arrays for edges already grouped by target with int64 offsets row_ptr[N+1]
  * (the radius graph's CSR output): perm = identity, col_sorted = int32(col), node_start =
  * row_ptr[:-1], node_end = row_ptr[1:].  Replaces the casts and arange SpatialGraph.build

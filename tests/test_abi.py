@@ -65,6 +65,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     _err(L.geo_radius_count(nul, 10, nul, 1, 10, nul, 0.01, 0.1, 0, 0, nul, nul, 0, nul), "max_num_neighbors")
     _err(L.geo_csr_build(nul, -1, 5, nul, nul, nul, nul, nul, 0, nul), "negative")
     _err(L.geo_fps(nul, 10, nul, nul, 1, 11, nul, nul, 0, nul), "max_cloud")
+    # the no-allocation CSR build refuses more edges than its fixed scratch holds
+    _err(L.geo_csr_build_noalloc(8, (1 << 20) + 1, 4, 8, 8, 8, 8, nul), "exceed")
+    _err(L.geo_csr_build_noalloc(nul, 10, 4, 8, 8, 8, 8, nul), "null edge")
 
 
 def test_workspace_too_small_is_reported():
