@@ -168,12 +168,11 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
     """HIP-event time of single kernels of the fused rows on the C2 graph, with their algorithmic
     bytes (every access of the kernel's pattern counted once: gathered rows per gather) and the
     fraction of the 8 TB/s HBM peak."""
-    import ctypes
     from gdl_amd import _native as nat
     from gdl_amd.csrc import edge_geometry_hip
     from gdl_amd.functional.gather import gather_weighted_sum, idw_weights
     from gdl_amd.functional.segment_softmax import segment_softmax
-    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pad16, cg_11_2_cartesian, path_columns
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pad16, path_columns
 
     def entry(us, nbytes):
         gbs = nbytes / (us * 1e-6) / 1e9
@@ -182,7 +181,8 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
 
     out = {}
     E, N, H = row.numel(), pos.shape[0], scores.shape[1]
-    us = 1e3 * event_ms(lambda: segment_softmax(scores, perm, ns, ne, N), args.iters, 5)
+    us = 1e3 * event_ms(lambda: segment_softmax(scores, perm, ns, ne, N, contiguous_csr=True),
+                        args.iters, 5)
     out["segment_softmax_fwd"] = entry(us, 2 * E * H * 4 + E * 4 + 2 * N * 4)
     w = idw_weights(idx, dist)
     n_out, K = idx.shape
@@ -202,14 +202,14 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
     plan = _Plan(Cs, Cv, 0, conv.out_scalar_channels, conv.out_vector_channels, 0, pc, P, 9, False)
     Xs = torch.empty(N, plan.Ks, device=dev)
     Xv = torch.empty(N, 3, plan.Kv, device=dev)
-    cg = (ctypes.c_float * 45)(*cg_11_2_cartesian().reshape(-1).tolist())
+    assert pc[7] < 0   # no type-2 path: the kernels take no CG table
     s_, v_ = fs.detach().contiguous(), fv.detach().contiguous()
     Y, d = gr.Y.detach().contiguous(), gr.direction.detach().contiguous()
 
     def agg():
         nat.check(nat.lib().geo_se3_aggregate_fwd(
             nat.ptr(s_), nat.ptr(v_), None, N, Cs, Cv, 0, nat.ptr(gr.row), None, nat.ptr(gr.node_start),
-            nat.ptr(gr.node_end), E, nat.ptr(d), nat.ptr(Y), 9, nat.ptr(R), P, plan.pc_c, cg,
+            nat.ptr(gr.node_end), E, nat.ptr(d), nat.ptr(Y), 9, nat.ptr(R), P, plan.pc_c, None,
             nat.ptr(Xs), plan.Ks, nat.ptr(Xv), plan.Kv, None, 0, nat.stream_of(dev)), "aggregate")
 
     us = 1e3 * event_ms(agg, args.iters, 5)
@@ -338,7 +338,8 @@ def main() -> int:
         cs, pm, ns, ne = sort_and_build_csr(col, pos.shape[0])
         scores = torch.randn(row.numel(), 4, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
         legs["c2_softmax_fwd_us"] = round(1e3 * event_ms(
-            lambda: segment_softmax(scores, pm, ns, ne, pos.shape[0]), args.iters, 5), 2)
+            lambda: segment_softmax(scores, pm, ns, ne, pos.shape[0], contiguous_csr=True),
+            args.iters, 5), 2)
         legs["c2_sparse_softmax_us"] = round(1e3 * wall_ms(
             lambda: sparse_softmax(scores, col, pos.shape[0]), args.steps, 3), 2)
         log(f"  segment softmax (E={row.numel()}, H=4): {legs['c2_softmax_fwd_us']} us on the CSR, "

@@ -53,10 +53,10 @@ _SIGNATURES = {
                                        c_i64, c_vp, c_vp, c_int, c_vp]),
     "geo_segment_reduce_bwd": (c_int, [c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                        c_vp, c_i64, c_i64, c_i64, c_vp, c_vp]),
-    "geo_segment_softmax_fwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp,
-                                        c_vp]),
-    "geo_segment_softmax_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+    "geo_segment_softmax_fwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_int,
                                         c_vp, c_vp]),
+    "geo_segment_softmax_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
+                                        c_int, c_vp, c_vp]),
     "geo_gather_weighted_sum": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
                                         c_vp]),
     "geo_gather_weighted_sum_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,

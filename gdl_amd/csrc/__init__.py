@@ -25,6 +25,7 @@ from typing import Optional, Tuple
 import numpy as np
 import torch
 from torch import Tensor
+from torch.utils.weak import WeakIdKeyDictionary
 
 from gdl_amd import _native as _nat
 
@@ -86,8 +87,9 @@ def radius_graph_hip(
     batch: Optional[Tensor] = None,
     num_batch_elements: Optional[int] = None,
 ) -> Tuple[Tensor, Tensor]:
-    row, col, _ = radius_graph_csr_hip(x, r, max_num_neighbors=max_num_neighbors, loop=loop,
-                                       mask=mask, batch=batch, num_batch_elements=num_batch_elements)
+    row, col, _, _ = radius_graph_csr_hip(x, r, max_num_neighbors=max_num_neighbors, loop=loop,
+                                          mask=mask, batch=batch,
+                                          num_batch_elements=num_batch_elements)
     return row, col
 
 
@@ -100,12 +102,13 @@ def radius_graph_csr_hip(
     mask: Optional[Tensor] = None,
     batch: Optional[Tensor] = None,
     num_batch_elements: Optional[int] = None,
-) -> Tuple[Tensor, Tensor, Tensor]:
+) -> Tuple[Tensor, Tensor, Tensor, int]:
     """Radius graph on the GPU; returns (row=source, col=target) int64, sorted by target then
-    source.  Cloud membership comes from ``batch`` when given, otherwise from
-    ``num_batch_elements`` contiguous equal chunks (one cloud when neither is given).  ``r`` is a
-    Python number or a one-element device tensor (e.g. an adaptive radius computed on the GPU),
-    which the kernels read directly: no host round trip for the radius."""
+    source, the CSR row pointer (int64 [N+1]) and the number of clouds B.  Cloud membership comes
+    from ``batch`` when given, otherwise from ``num_batch_elements`` contiguous equal chunks (one
+    cloud when neither is given).  ``r`` is a Python number or a one-element device tensor (e.g.
+    an adaptive radius computed on the GPU), which the kernels read directly: no host round trip
+    for the radius."""
     _require_gpu("radius_graph", x, mask, batch)
     x = _positions("radius_graph", x)
     dev = x.device
@@ -122,7 +125,8 @@ def radius_graph_csr_hip(
     r = float(r)
     empty = torch.empty(0, dtype=torch.int64, device=dev)
     if N == 0 or K == 0 or not (r > 0.0):
-        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        B0 = int(num_batch_elements) if num_batch_elements is not None else 1
+        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev), B0
     r2 = fp32_radius_sq(r)
     if batch is not None:
         if batch.numel() != N:
@@ -138,7 +142,7 @@ def radius_graph_csr_hip(
             raise ValueError(f"radius_graph: {N} points do not split into {B} equal clouds")
         ppc = N // B
     if B < 1:
-        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev), B
     mask_u8 = None
     if mask is not None:
         if mask.numel() != N:
@@ -186,7 +190,7 @@ def radius_graph_csr_hip(
             if E > 0:
                 _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(row), _nat.ptr(col), _nat.ptr(ws),
                                 ws_bytes, s), "geo_radius_emit")
-    return row, col, row_ptr
+    return row, col, row_ptr, B
 
 
 def radius_graph_cuda(
@@ -246,6 +250,24 @@ def sort_and_build_csr_cuda(col: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor
                                    _nat.ptr(node_start), _nat.ptr(node_end), _nat.ptr(ws),
                                    ws_bytes, _nat.stream_of(dev)), "geo_csr_build")
     return col_sorted, perm, node_start, node_end
+
+
+_SOURCE_CSR = WeakIdKeyDictionary()
+
+
+def source_csr(row: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """(perm, node_start, node_end) of the edges grouped by source: the stable CSR of ``row``
+    (the backward passes of message passing and edge geometry scatter onto the sources with it).
+    Built once per ``row`` tensor and kept while that tensor lives, so the layers of a network
+    sharing one graph sort its sources once; an in-place change of ``row`` (its version counter)
+    or another N rebuilds it."""
+    key = (row._version, int(N), row.numel())
+    hit = _SOURCE_CSR.get(row)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    _, perm_r, ns_r, ne_r = sort_and_build_csr_cuda(row, N)
+    _SOURCE_CSR[row] = (key, (perm_r, ns_r, ne_r))
+    return perm_r, ns_r, ne_r
 
 
 def _dtype_code(name: str, t: Tensor) -> int:
@@ -348,8 +370,13 @@ def segment_softmax_forward_hip(
     node_start: Tensor,
     node_end: Tensor,
     N: int,
+    contiguous_csr: bool = False,
 ) -> Tensor:
-    """Softmax of scores[E, H] over each target segment of the CSR (rows in no segment -> 0)."""
+    """Softmax of scores[E, H] over each target segment of the CSR (rows in no segment -> 0).
+
+    ``contiguous_csr`` states that the node ranges are ascending and contiguous from 0 (the CSR
+    of ``sort_and_build_csr`` or of a radius graph): the kernel then also writes the zeros of
+    the rows after the last segment and the output needs no separate fill."""
     _require_gpu("segment_softmax", scores, perm, node_start, node_end)
     if scores.dim() != 2:
         raise ValueError(f"segment_softmax: scores must be [E, H], got {tuple(scores.shape)}")
@@ -365,11 +392,12 @@ def segment_softmax_forward_hip(
     if pm is not None and pm.numel() != E:
         raise ValueError(f"segment_softmax: perm has {pm.numel()} entries for E={E}")
     ns, ne = _i32(node_start, dev), _i32(node_end, dev)
-    out = torch.zeros_like(scores)
+    out = torch.empty_like(scores) if contiguous_csr else torch.zeros_like(scores)
     with torch.cuda.device(dev):
         _nat.check(_nat.lib().geo_segment_softmax_fwd(
             _nat.DTYPE_CODES[scores.dtype], _nat.ptr(scores), _nat.ptr(pm), _nat.ptr(ns),
-            _nat.ptr(ne), E, N, H, _nat.ptr(out), _nat.stream_of(dev)), "geo_segment_softmax_fwd")
+            _nat.ptr(ne), E, N, H, int(bool(contiguous_csr)), _nat.ptr(out), _nat.stream_of(dev)),
+            "geo_segment_softmax_fwd")
     return out
 
 
@@ -380,8 +408,10 @@ def segment_softmax_backward_hip(
     node_start: Tensor,
     node_end: Tensor,
     N: int,
+    contiguous_csr: bool = False,
 ) -> Tensor:
-    """grad_scores = out * (grad_out - segment sum of grad_out * out)."""
+    """grad_scores = out * (grad_out - segment sum of grad_out * out) (rows in no segment -> 0;
+    ``contiguous_csr`` as in the forward)."""
     _require_gpu("segment_softmax backward", grad_out, out, perm, node_start, node_end)
     dev = out.device
     grad_out = grad_out.to(out.dtype).contiguous()
@@ -389,12 +419,12 @@ def segment_softmax_backward_hip(
     E, H = out.shape
     pm = _i32(perm, dev)
     ns, ne = _i32(node_start, dev), _i32(node_end, dev)
-    grad = torch.zeros_like(out)
+    grad = torch.empty_like(out) if contiguous_csr else torch.zeros_like(out)
     with torch.cuda.device(dev):
         _nat.check(_nat.lib().geo_segment_softmax_bwd(
             _nat.DTYPE_CODES[out.dtype], _nat.ptr(grad_out), _nat.ptr(out), _nat.ptr(pm),
-            _nat.ptr(ns), _nat.ptr(ne), E, int(N), H, _nat.ptr(grad), _nat.stream_of(dev)),
-            "geo_segment_softmax_bwd")
+            _nat.ptr(ns), _nat.ptr(ne), E, int(N), H, int(bool(contiguous_csr)), _nat.ptr(grad),
+            _nat.stream_of(dev)), "geo_segment_softmax_bwd")
     return grad
 
 
@@ -739,7 +769,7 @@ def _fps_iterative_fallback(pos, ptr, k_per_batch):
 
 __all__ = [
     "get_radius_graph_backend", "radius_graph_cuda", "radius_graph_hip", "fp32_radius_sq",
-    "segment_reduce_available", "sort_and_build_csr_cuda", "segment_reduce_sum_cuda",
+    "segment_reduce_available", "sort_and_build_csr_cuda", "source_csr", "segment_reduce_sum_cuda",
     "segment_softmax_forward_hip", "segment_softmax_backward_hip",
     "gather_weighted_sum_forward_hip", "gather_weighted_sum_backward_hip", "idw_weights_hip",
     "knn_radius_stat_hip", "radius_graph_csr_hip", "edge_geometry_hip",

@@ -31,4 +31,4 @@ extern "C" const char* geo_build_info(void) {
          ", flags: " GEO_BUILD_FLAGS;
 }
 
-extern "C" int geo_abi_version(void) { return 1; }
+extern "C" int geo_abi_version(void) { return 2; }

@@ -56,7 +56,7 @@ struct SeEdges {
   const float* R;         // [E, P]
   int32_t P;
   int32_t pc[kSePaths];   // column of R for each path, -1 when the path is off
-  float cg[45];           // [3][3][5]
+  const float* cg;        // [3][3][5] device array; NULL when path 7 is off
 };
 
 struct SeFeat {
@@ -225,7 +225,16 @@ __device__ __forceinline__ EdgeCoef<T2> coef_at(const EdgeCoef<T2>& st, int j) {
 
 // D[j][m] = r * sum_i d_i cg[i][j][m]: path 7's per-edge coefficients, so that a lane's share
 // is sum_j v_j D[j][m] (forward) or sum_m D[j][m] w_m (source-side backward).
+// The table is read from device memory at a wave-uniform address (scalar loads, cached); a NULL
+// table (path 7 off) gives zeros.
 __device__ __forceinline__ void cg_coef(const float* cg, const float d[3], float r, float D[3][5]) {
+  if (cg == nullptr) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int m = 0; m < 5; ++m) D[j][m] = 0.f;
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 3; ++j)
 #pragma unroll
@@ -803,6 +812,10 @@ __device__ __forceinline__ void load_grow(GRow& G, const SeFeat& f, const float*
   for (int i = 0; i < 3; ++i)
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
+      if (cg == nullptr) {
+        G.v7c[i][j] = 0.f;
+        continue;
+      }
       const float* cc = cg + (i * 3 + j) * 5;
       G.v7c[i][j] = (((cc[0] * v7[0] + cc[1] * v7[1]) + cc[2] * v7[2]) + cc[3] * v7[3]) + cc[4] * v7[4];
     }
@@ -1042,7 +1055,7 @@ SeEdges make_edges(const int64_t* other, const int32_t* perm, const int32_t* ns,
   g.R = R;
   g.P = P;
   for (int i = 0; i < kSePaths; ++i) g.pc[i] = path_cols[i];
-  for (int i = 0; i < 45; ++i) g.cg[i] = cg[i];
+  g.cg = path_cols[7] >= 0 ? cg : nullptr;
   return g;
 }
 
@@ -1050,7 +1063,8 @@ int check_edges(const char* who, int64_t N, int64_t E, int ysh, int P, const int
                 const float* cg) {
   GEO_REQUIRE(N >= 0 && E >= 0, "%s: negative size", who);
   GEO_REQUIRE(N < 0x7fffffffLL && E < 0x7fffffffLL, "%s: sizes exceed int32 indexing", who);
-  GEO_REQUIRE(path_cols && cg, "%s: null path table or CG table", who);
+  GEO_REQUIRE(path_cols, "%s: null path table", who);
+  GEO_REQUIRE(path_cols[7] < 0 || cg, "%s: path 7 needs the CG table", who);
   GEO_REQUIRE(ysh >= 1, "%s: Y needs at least one channel", who);
   for (int i = 0; i < kSePaths; ++i)
     GEO_REQUIRE(path_cols[i] >= -1 && path_cols[i] < P, "%s: path %d uses column %d of R (P=%d)",

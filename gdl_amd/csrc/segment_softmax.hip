@@ -14,7 +14,7 @@
 // so the H threads of a segment read one row together.
 #include <initializer_list>
 
-#include "common.hpp"
+#include "scan.hpp"
 
 namespace geo {
 namespace {
@@ -30,6 +30,26 @@ __device__ __forceinline__ double exp_t<double>(double v) { return exp(v); }
 
 __device__ __forceinline__ int clamp_idx(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+// With zero_tail, the rows of the CSR positions [node_end[S-1], E) — the edges whose target lies
+// outside [0, S) in a CSR built by geo_csr_build, whose node ranges are ascending and contiguous
+// from 0 — are written as 0 by the grid's threads together, so no separate fill of the output is
+// needed.  The tail is empty for a CSR that covers every edge: one uniform load per thread.
+template <typename T>
+__device__ __forceinline__ void zero_tail_rows(T* __restrict__ out, const int32_t* __restrict__ perm,
+                                               const int32_t* __restrict__ ne, int32_t E, int64_t S,
+                                               int64_t H) {
+  const int t0 = clamp_idx(ne[S - 1], 0, E);
+  const int64_t n = static_cast<int64_t>(E - t0) * H;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int64_t q = i / H;
+    const int e = t0 + static_cast<int>(q);
+    const int r = perm ? perm[e] : e;
+    if (static_cast<unsigned>(r) < static_cast<unsigned>(E))
+      out[static_cast<int64_t>(r) * H + (i - q * H)] = T(0);
+  }
+}
+
 // Largest value over the wave (v >= 0; every lane active).
 __device__ __forceinline__ int uniform_max(int v) {
   return static_cast<int>(wave_max_u32(static_cast<uint32_t>(v)));
@@ -38,7 +58,9 @@ __device__ __forceinline__ int uniform_max(int v) {
 template <typename T>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_fwd_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
-    const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H, T* __restrict__ w) {
+    const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H, T* __restrict__ w,
+    int zero_tail) {
+  if (zero_tail) zero_tail_rows<T>(w, perm, ne, E, S, H);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= S * H) return;
   const int64_t s = t / H;
@@ -78,7 +100,8 @@ template <typename T>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_bwd_kernel(
     const T* __restrict__ g, const T* __restrict__ w, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S,
-    int32_t H, T* __restrict__ dx) {
+    int32_t H, T* __restrict__ dx, int zero_tail) {
+  if (zero_tail) zero_tail_rows<T>(dx, perm, ne, E, S, H);
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= S * H) return;
   const int64_t s = t / H;
@@ -156,7 +179,9 @@ __device__ __forceinline__ int sm_row(const int32_t* perm, int32_t E, int e) {
 
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_fwd(
     const float* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
-    const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H, float* __restrict__ w) {
+    const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H, float* __restrict__ w,
+    int zero_tail) {
+  if (zero_tail) zero_tail_rows<float>(w, perm, ne, E, S, H);
   const RowSeg g = row_seg(ns, ne, E, S);
   // chunks of 16 edges; every lane of the wave runs the wave's largest chunk count, so the row
   // reductions below see all sixteen lanes of every row.  The first two chunks (segments of up
@@ -228,7 +253,8 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_fwd(
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_bwd(
     const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H,
-    float* __restrict__ dx) {
+    float* __restrict__ dx, int zero_tail) {
+  if (zero_tail) zero_tail_rows<float>(dx, perm, ne, E, S, H);
   const RowSeg g = row_seg(ns, ne, E, S);
   const int nch = uniform_max((g.b - g.a + 15) >> 4);
   float dot[kSmRowHeads], g0[kSmRowHeads], w0[kSmRowHeads];
@@ -344,7 +370,8 @@ __device__ __forceinline__ void sm_bounds(const int32_t* ns, const int32_t* ne, 
 template <int HH, int LW>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
     const float* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
-    const int32_t* __restrict__ ne, int32_t E, int64_t S, float* __restrict__ w) {
+    const int32_t* __restrict__ ne, int32_t E, int64_t S, float* __restrict__ w, int zero_tail) {
+  if (zero_tail) zero_tail_rows<float>(w, perm, ne, E, S, HH);
   constexpr int SQ = sm_quads<HH, LW>();
   constexpr int KC = 32 / LW;
   const int li = lane_id() & (LW - 1);
@@ -449,9 +476,9 @@ template <int HH, int LW>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
     const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S,
-    float* __restrict__ dx) {
+    float* __restrict__ dx, int zero_tail) {
+  if (zero_tail) zero_tail_rows<float>(dx, perm, ne, E, S, HH);
   constexpr int SQ = sm_quads<HH, LW>();
-  constexpr int KC = 32 / LW;
   const int li = lane_id() & (LW - 1);
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kSmThreads / kWave) + threadIdx.x / kWave;
   int a[SQ], b[SQ], r0[SQ];
@@ -570,31 +597,44 @@ static int sm_check(int dtype, int64_t E, int64_t S, int64_t H) {
   return GEO_OK;
 }
 
+// S == 0 with zero_tail: every row is outside the CSR.
+static int sm_zero_all(int dtype, void* out, int64_t E, int64_t H, hipStream_t st) {
+  if (dtype == GEO_F32) return device_fill<float>(static_cast<float*>(out), E * H, 0.f, st);
+  return device_fill<double>(static_cast<double*>(out), E * H, 0.0, st);
+}
+
 extern "C" int geo_segment_softmax_fwd(int dtype, const void* scores, const int32_t* perm,
                                        const int32_t* node_start, const int32_t* node_end,
-                                       int64_t E, int64_t S, int64_t H, void* out, void* stream) {
+                                       int64_t E, int64_t S, int64_t H, int zero_tail, void* out,
+                                       void* stream) {
   int rc = sm_check(dtype, E, S, H);
   if (rc) return rc;
-  if (S == 0 || H == 0 || E == 0) return GEO_OK;
-  GEO_REQUIRE(scores && out && node_start && node_end, "segment_softmax: null pointer");
-  const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
   hipStream_t st = as_stream(stream);
+  if (H == 0 || E == 0) return GEO_OK;
+  GEO_REQUIRE(out, "segment_softmax: null output");
+  if (S == 0) return zero_tail ? sm_zero_all(dtype, out, E, H, st) : GEO_OK;
+  GEO_REQUIRE(scores && node_start && node_end, "segment_softmax: null pointer");
+  const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
+  const int zt = zero_tail ? 1 : 0;
   if (dtype == GEO_F32 && sm_vec_ok(H, {scores, out})) {
     sm_launch_vec<SmFwd>(E, H, S, st, static_cast<const float*>(scores), perm, node_start, node_end,
-                         static_cast<int32_t>(E), S, static_cast<float*>(out));
+                         static_cast<int32_t>(E), S, static_cast<float*>(out), zt);
   } else if (dtype == GEO_F32 && H <= kSmRowHeads) {
     const unsigned rgrid = static_cast<unsigned>(ceil_div(S, 4 * (kSmThreads / kWave)));
     hipLaunchKernelGGL(seg_softmax_rows_fwd, dim3(rgrid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(scores), perm, node_start, node_end,
-                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<float*>(out));
+                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<float*>(out),
+                       zt);
   } else if (dtype == GEO_F32)
     hipLaunchKernelGGL(seg_softmax_fwd_kernel<float>, dim3(grid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(scores), perm, node_start, node_end,
-                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<float*>(out));
+                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<float*>(out),
+                       zt);
   else
     hipLaunchKernelGGL(seg_softmax_fwd_kernel<double>, dim3(grid), dim3(kSmThreads), 0, st,
                        static_cast<const double*>(scores), perm, node_start, node_end,
-                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<double*>(out));
+                       static_cast<int32_t>(E), S, static_cast<int32_t>(H), static_cast<double*>(out),
+                       zt);
   GEO_LAUNCH_CHECK("seg_softmax_fwd_kernel");
   return GEO_OK;
 }
@@ -602,34 +642,36 @@ extern "C" int geo_segment_softmax_fwd(int dtype, const void* scores, const int3
 extern "C" int geo_segment_softmax_bwd(int dtype, const void* grad_out, const void* out,
                                        const int32_t* perm, const int32_t* node_start,
                                        const int32_t* node_end, int64_t E, int64_t S, int64_t H,
-                                       void* grad_scores, void* stream) {
+                                       int zero_tail, void* grad_scores, void* stream) {
   int rc = sm_check(dtype, E, S, H);
   if (rc) return rc;
-  if (S == 0 || H == 0 || E == 0) return GEO_OK;
-  GEO_REQUIRE(grad_out && out && grad_scores && node_start && node_end,
-              "segment_softmax_bwd: null pointer");
-  const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
   hipStream_t st = as_stream(stream);
+  if (H == 0 || E == 0) return GEO_OK;
+  GEO_REQUIRE(grad_scores, "segment_softmax_bwd: null output");
+  if (S == 0) return zero_tail ? sm_zero_all(dtype, grad_scores, E, H, st) : GEO_OK;
+  GEO_REQUIRE(grad_out && out && node_start && node_end, "segment_softmax_bwd: null pointer");
+  const unsigned grid = static_cast<unsigned>(ceil_div(S * H, kSmThreads));
+  const int zt = zero_tail ? 1 : 0;
   if (dtype == GEO_F32 && sm_vec_ok(H, {grad_out, out, grad_scores})) {
     sm_launch_vec<SmBwd>(E, H, S, st, static_cast<const float*>(grad_out), static_cast<const float*>(out),
                          perm, node_start, node_end, static_cast<int32_t>(E), S,
-                         static_cast<float*>(grad_scores));
+                         static_cast<float*>(grad_scores), zt);
   } else if (dtype == GEO_F32 && H <= kSmRowHeads) {
     const unsigned rgrid = static_cast<unsigned>(ceil_div(S, 4 * (kSmThreads / kWave)));
     hipLaunchKernelGGL(seg_softmax_rows_bwd, dim3(rgrid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(grad_out), static_cast<const float*>(out), perm,
                        node_start, node_end, static_cast<int32_t>(E), S, static_cast<int32_t>(H),
-                       static_cast<float*>(grad_scores));
+                       static_cast<float*>(grad_scores), zt);
   } else if (dtype == GEO_F32)
     hipLaunchKernelGGL(seg_softmax_bwd_kernel<float>, dim3(grid), dim3(kSmThreads), 0, st,
                        static_cast<const float*>(grad_out), static_cast<const float*>(out), perm,
                        node_start, node_end, static_cast<int32_t>(E), S, static_cast<int32_t>(H),
-                       static_cast<float*>(grad_scores));
+                       static_cast<float*>(grad_scores), zt);
   else
     hipLaunchKernelGGL(seg_softmax_bwd_kernel<double>, dim3(grid), dim3(kSmThreads), 0, st,
                        static_cast<const double*>(grad_out), static_cast<const double*>(out), perm,
                        node_start, node_end, static_cast<int32_t>(E), S, static_cast<int32_t>(H),
-                       static_cast<double*>(grad_scores));
+                       static_cast<double*>(grad_scores), zt);
   GEO_LAUNCH_CHECK("seg_softmax_bwd_kernel");
   return GEO_OK;
 }

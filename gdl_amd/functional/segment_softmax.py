@@ -28,17 +28,19 @@ from gdl_amd.csrc import (
 
 class _SegmentSoftmax(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, scores, perm, node_start, node_end, num_nodes):
-        out = segment_softmax_forward_hip(scores, perm, node_start, node_end, num_nodes)
+    def forward(ctx, scores, perm, node_start, node_end, num_nodes, contiguous_csr):
+        out = segment_softmax_forward_hip(scores, perm, node_start, node_end, num_nodes,
+                                          contiguous_csr)
         ctx.save_for_backward(out, perm, node_start, node_end)
-        ctx.num_nodes = num_nodes
+        ctx.num_nodes, ctx.contiguous_csr = num_nodes, contiguous_csr
         return out
 
     @staticmethod
     def backward(ctx, grad):
         out, perm, node_start, node_end = ctx.saved_tensors
-        g = segment_softmax_backward_hip(grad, out, perm, node_start, node_end, ctx.num_nodes)
-        return g, None, None, None, None
+        g = segment_softmax_backward_hip(grad, out, perm, node_start, node_end, ctx.num_nodes,
+                                         ctx.contiguous_csr)
+        return g, None, None, None, None, None
 
 
 def _compute_dtype(scores: Tensor) -> Tensor:
@@ -51,19 +53,24 @@ def segment_softmax(
     node_start: Tensor,
     node_end: Tensor,
     num_nodes: int,
+    *,
+    contiguous_csr: bool = False,
 ) -> Tensor:
     """Softmax of ``scores [E, H]`` (or ``[E]``) over each CSR segment: rows ``perm[e]`` for
-    ``e`` in ``[node_start[n], node_end[n])`` form target ``n``; ``perm`` may be None."""
+    ``e`` in ``[node_start[n], node_end[n])`` form target ``n``; ``perm`` may be None.  Rows in
+    no segment are 0.  ``contiguous_csr=True`` states that the node ranges are ascending and
+    contiguous from 0, as ``sort_and_build_csr`` and ``SpatialGraph`` produce them; the kernel
+    then writes those zeros itself instead of the output being zero-filled first."""
     squeeze = scores.dim() == 1
     x = _compute_dtype(scores.unsqueeze(-1) if squeeze else scores)
-    out = _SegmentSoftmax.apply(x, perm, node_start, node_end, int(num_nodes))
+    out = _SegmentSoftmax.apply(x, perm, node_start, node_end, int(num_nodes), bool(contiguous_csr))
     return out.squeeze(-1) if squeeze else out
 
 
 def sparse_softmax(scores: Tensor, index: Tensor, num_nodes: int) -> Tensor:
     """Softmax over sparse edges grouped by target node (reference argument order)."""
     _, perm, node_start, node_end = sort_and_build_csr_cuda(index, int(num_nodes))
-    return segment_softmax(scores, perm, node_start, node_end, num_nodes)
+    return segment_softmax(scores, perm, node_start, node_end, num_nodes, contiguous_csr=True)
 
 
 _sparse_softmax = sparse_softmax

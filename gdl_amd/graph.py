@@ -30,6 +30,7 @@ from gdl_amd.csrc import (
     radius_graph_csr_hip,
     segment_reduce_forward_hip,
     sort_and_build_csr_cuda,
+    source_csr,
 )
 
 
@@ -50,7 +51,7 @@ class _EdgeGeometry(torch.autograd.Function):
         N = ctx.N
         perm_c, ns_c, ne_c = ctx.col_csr if ctx.col_csr is not None else \
             sort_and_build_csr_cuda(col, N)[1:]
-        _, perm_r, ns_r, ne_r = sort_and_build_csr_cuda(row, N)
+        perm_r, ns_r, ne_r = source_csr(row, N)
         into_col = segment_reduce_forward_hip(g_diff, perm_c, ns_c, ne_c, N, "sum")[0]
         from_row = segment_reduce_forward_hip(g_diff, perm_r, ns_r, ne_r, N, "sum")[0]
         return into_col - from_row, None, None, None, None
@@ -94,14 +95,14 @@ class SpatialGraph:
         (geoembodied/nn/modules/spatial_graph.py:85-167).  ``radius`` may be a device tensor."""
         N = pos.shape[0]
         dev = pos.device
-        row, col, row_ptr = radius_graph_csr_hip(
+        row, col, row_ptr, B = radius_graph_csr_hip(
             pos, radius, max_num_neighbors=max_num_neighbors, batch=batch, mask=mask,
             num_batch_elements=num_batch_elements)
         E = row.shape[0]
         if E == 0:
             return SpatialGraph._empty(N, dev, max_l)
         if batch is not None:
-            B = int(num_batch_elements) if num_batch_elements is not None else int(batch.max().item()) + 1
+            # B comes from the radius graph (its batch.max() sync, or num_batch_elements)
             batch = batch.reshape(-1).to(device=dev, dtype=torch.int64)
             ppc = 0
         else:

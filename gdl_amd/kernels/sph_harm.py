@@ -15,7 +15,6 @@ the sphere:
 
 from __future__ import annotations
 
-import math
 from typing import List
 
 import torch
@@ -26,14 +25,6 @@ from gdl_amd.csrc import (
     spherical_harmonics_backward_hip,
     spherical_harmonics_hip,
 )
-
-_C0 = math.sqrt(1.0 / (4.0 * math.pi))
-_C1 = math.sqrt(3.0 / (4.0 * math.pi))
-_C2_0 = math.sqrt(5.0 / (16.0 * math.pi))
-_C2_1 = math.sqrt(15.0 / (4.0 * math.pi))
-_C2_2 = math.sqrt(15.0 / (16.0 * math.pi))
-_CHANNELS_PER_L = {0: 1, 1: 3, 2: 5}
-_TOTAL_CHANNELS_L2 = 9
 
 
 class SphericalHarmonicsFunction(torch.autograd.Function):

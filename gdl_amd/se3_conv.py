@@ -9,7 +9,8 @@ CSR, no per-edge tensor) and the weights applied once per node by an fp32 MFMA G
 epilogue divides by the average degree, adds the scalar bias and applies the mask.  The
 backward is the transposed structure: per-edge gradients of R, the direction and Y from
 per-node gradient rows, and source-side sums over the CSR of the sources followed by GEMMs
-with the transposed weights.  Weight gradients are plain GEMMs over nodes (torch.matmul).
+with the transposed weights.  Weight gradients are long reductions over nodes on the matrix
+cores (geo_se3_gemm_tn).
 
 Arithmetic is fp32 (inputs of lower precision are computed in fp32, as the reference does;
 float64 inputs are computed in fp32 and returned as float64).  Results equal the reference's
@@ -20,14 +21,14 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
 from torch import Tensor
 
 from gdl_amd import _native as _nat
-from gdl_amd.csrc import _require_gpu, sort_and_build_csr_cuda
+from gdl_amd.csrc import _require_gpu, source_csr
 
 PATH_NAMES = ("w_ss", "w_sv", "w_vv_scalar", "w_vs", "w_vv_cross", "w_st2", "w_t2t2", "w_vt2", "w_t2s")
 
@@ -125,25 +126,53 @@ def _gemm(A: Tensor, M: int, K: int, B: Tensor, O: int, G: int, out: Tensor, ost
         _nat.ptr(bias), _nat.ptr(mask), _nat.stream_of(A.device)), "geo_se3_gemm")
 
 
-class _SE3MessageAggregate(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, plan: _Plan, graph_arrays, cg_c, avg, mask_u8, s, v, t, direction, Y, R,
-                bias, *W):
-        row, col, perm, ns, ne, src_csr = graph_arrays
-        p = plan
-        dev = s.device
-        N, E = s.shape[0], row.shape[0]
-        f32 = dict(dtype=torch.float32, device=dev)
-        Xs = torch.empty(N, p.Ks, **f32) if p.Os > 0 else None
-        Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 else None
-        Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 else None
+def _plan_of(s: Tensor, v: Tensor, t: Optional[Tensor], Y: Tensor, R: Tensor, dims) -> _Plan:
+    """The plan of one call from the feature shapes and ``dims`` = [Os, Ov, Ot, pc_0 .. pc_8]
+    (Ot = 0 when no type-2 output is wanted)."""
+    Ct = t.shape[1] if t is not None else 0
+    Os, Ov, Ot = int(dims[0]), int(dims[1]), int(dims[2])
+    return _Plan(s.shape[1], v.shape[1], Ct, Os, Ov, Ot, [int(x) for x in dims[3:12]], R.shape[1],
+                 Y.shape[1], Ot > 0)
+
+
+def _u8(mask: Optional[Tensor]) -> Optional[Tensor]:
+    return None if mask is None else mask.view(torch.uint8)
+
+
+_EMPTY = (0,)
+
+
+# The fused forward and backward are torch.library custom ops with fake implementations, so
+# torch.compile traces SE3Conv through them (the reference checks the same transparency for its
+# segment-sum op, tests/test_torch_compile.py:83-197).  The nine path weights are separate
+# optional arguments; gradients that are not needed come back as empty tensors.
+@torch.library.custom_op("geoembodied::se3_conv_fwd", mutates_args=())
+def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Tensor,
+                perm: Optional[Tensor], node_start: Tensor, node_end: Tensor, direction: Tensor,
+                Y: Tensor, R: Tensor, avg: Tensor, mask: Optional[Tensor], bias: Optional[Tensor],
+                cg: Optional[Tensor], dims: List[int], w0: Optional[Tensor], w1: Optional[Tensor],
+                w2: Optional[Tensor], w3: Optional[Tensor], w4: Optional[Tensor],
+                w5: Optional[Tensor], w6: Optional[Tensor], w7: Optional[Tensor],
+                w8: Optional[Tensor]) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(s_out, v_out, t_out, Xs, Xv, Xt): outputs and the per-node aggregates (kept for the
+    backward; empty when their output is not computed)."""
+    W = (w0, w1, w2, w3, w4, w5, w6, w7, w8)
+    p = _plan_of(s, v, t, Y, R, dims)
+    dev = s.device
+    N, E = s.shape[0], row.shape[0]
+    f32 = dict(dtype=torch.float32, device=dev)
+    Xs = torch.empty(N, p.Ks, **f32) if p.Os > 0 else None
+    Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 else None
+    Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 else None
+    mask_u8 = _u8(mask)
+    with torch.cuda.device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
         _nat.check(L.geo_se3_aggregate_fwd(
             _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, p.Cs, p.Cv, p.Ct, _nat.ptr(row), _nat.ptr(perm),
-            _nat.ptr(ns), _nat.ptr(ne), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P,
-            p.pc_c, cg_c, _nat.ptr(Xs), p.Ks, _nat.ptr(Xv), p.Kv, _nat.ptr(Xt), p.Kt, st),
-            "geo_se3_aggregate_fwd")
+            _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh,
+            _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(Xs), p.Ks, _nat.ptr(Xv), p.Kv,
+            _nat.ptr(Xt), p.Kt, st), "geo_se3_aggregate_fwd")
         Ws, Wv, Wt = _pack(p, W, [(0, _pad64(p.Os), p.Ks), (1, _pad64(p.Ov), p.Kv),
                                   (2, _pad64(p.Ot), p.Kt)], dev)
         s_out = torch.empty(N, p.Os, **f32)
@@ -152,30 +181,59 @@ class _SE3MessageAggregate(torch.autograd.Function):
         _gemm(Xs, N, p.Ks, Ws, p.Os, 1, s_out, p.Os, avg, bias, mask_u8)
         _gemm(Xv, 3 * N, p.Kv, Wv, p.Ov, 3, v_out, 3 * p.Ov, avg, None, mask_u8)
         _gemm(Xt, 5 * N, p.Kt, Wt, p.Ot, 5, t_out, 5 * p.Ot, avg, None, mask_u8)
-        ctx.plan, ctx.graph_arrays, ctx.cg_c = plan, graph_arrays, cg_c
-        ctx.has_bias = bias is not None
-        ctx.save_for_backward(s, v, t, direction, Y, R, avg, mask_u8, Xs, Xv, Xt, *W)
-        return s_out, v_out, t_out
+    empty = s.new_empty(_EMPTY, dtype=torch.float32)
+    return (s_out, v_out, t_out, Xs if Xs is not None else empty,
+            Xv if Xv is not None else empty.clone(), Xt if Xt is not None else empty.clone())
 
-    @staticmethod
-    def backward(ctx, g_s, g_v, g_t):
-        p = ctx.plan
-        s, v, t, direction, Y, R, avg, mask_u8, Xs, Xv, Xt, *W = ctx.saved_tensors
-        row, col, perm, ns, ne, src_csr = ctx.graph_arrays
-        dev = s.device
-        N, E = s.shape[0], row.shape[0]
-        f32 = dict(dtype=torch.float32, device=dev)
+
+@_se3_fwd_op.register_fake
+def _se3_fwd_fake(s, v, t, row, col, perm, node_start, node_end, direction, Y, R, avg, mask, bias,
+                  cg, dims, w0, w1, w2, w3, w4, w5, w6, w7, w8):
+    p = _plan_of(s, v, t, Y, R, dims)
+    N = s.shape[0]
+    f = dict(dtype=torch.float32)
+    return (s.new_empty(N, p.Os, **f), s.new_empty(N, p.Ov, 3, **f), s.new_empty(N, p.Ot, 5, **f),
+            s.new_empty(N, p.Ks, **f) if p.Os > 0 else s.new_empty(_EMPTY, **f),
+            s.new_empty(N, 3, p.Kv, **f) if p.Ov > 0 else s.new_empty(_EMPTY, **f),
+            s.new_empty(N, 5, p.Kt, **f) if p.Ot > 0 else s.new_empty(_EMPTY, **f))
+
+
+# gradient slots of the backward op: ds, dv, dt, ddir, dY, dR, dbias, dW0 .. dW8
+_NEED_INPUTS = (0, 1, 2, 8, 9, 10, 13, 16, 17, 18, 19, 20, 21, 22, 23, 24)
+
+
+@torch.library.custom_op("geoembodied::se3_conv_bwd", mutates_args=())
+def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tensor], s: Tensor,
+                v: Tensor, t: Optional[Tensor], row: Tensor, col: Tensor, perm: Optional[Tensor],
+                node_start: Tensor, node_end: Tensor, direction: Tensor, Y: Tensor, R: Tensor,
+                avg: Tensor, mask: Optional[Tensor], cg: Optional[Tensor], Xs: Tensor, Xv: Tensor,
+                Xt: Tensor, dims: List[int], need: List[bool], w0: Optional[Tensor],
+                w1: Optional[Tensor], w2: Optional[Tensor], w3: Optional[Tensor],
+                w4: Optional[Tensor], w5: Optional[Tensor], w6: Optional[Tensor],
+                w7: Optional[Tensor], w8: Optional[Tensor]) -> List[Tensor]:
+    """[ds, dv, dt, ddir, dY, dR, dbias, dW0 .. dW8]; an entry not in ``need`` is empty."""
+    W = (w0, w1, w2, w3, w4, w5, w6, w7, w8)
+    p = _plan_of(s, v, t, Y, R, dims)
+    dev = s.device
+    N, E = s.shape[0], row.shape[0]
+    f32 = dict(dtype=torch.float32, device=dev)
+    mask_u8 = _u8(mask)
+    Xs = Xs if p.Os > 0 else None
+    Xv = Xv if p.Ov > 0 else None
+    Xt = Xt if p.Ot > 0 else None
+    need_s, need_v, need_t, need_dir, need_Y, need_R, need_bias = need[:7]
+    need_W = need[7:16]
+    with torch.cuda.device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
-        need = ctx.needs_input_grad  # (plan, graph, cg, avg, mask, s, v, t, dir, Y, R, bias, *W)
 
         def prep(g, O, G, OP):
             if O == 0:
                 return None
             out = torch.empty(N, G, OP, **f32)
             gc = (g if g is not None else torch.zeros(N, O, G, **f32)).to(torch.float32).contiguous()
-            _nat.check(L.geo_se3_grad_prep(_nat.ptr(gc), N, O, G, OP, _nat.ptr(avg), _nat.ptr(mask_u8),
-                                           _nat.ptr(out), st), "geo_se3_grad_prep")
+            _nat.check(L.geo_se3_grad_prep(_nat.ptr(gc), N, O, G, OP, _nat.ptr(avg),
+                                           _nat.ptr(mask_u8), _nat.ptr(out), st), "geo_se3_grad_prep")
             return out
 
         Gs = prep(g_s, p.Os, 1, p.OsP)
@@ -185,7 +243,7 @@ class _SE3MessageAggregate(torch.autograd.Function):
 
         # per-edge gradients of R, direction and Y from gX = G W (per target node)
         dR = ddir = dY = None
-        if (need[8] or need[9] or need[10]) and E > 0:
+        if (need_dir or need_Y or need_R) and E > 0:
             gXs = gXv = gXt = None
             WsT, WvT, WtT = _pack(p, W, [(3, _pad64(p.Ks), p.OsP if Gs is not None else 0),
                                          (4, _pad64(p.Kv), p.OvP if Gv is not None else 0),
@@ -199,29 +257,31 @@ class _SE3MessageAggregate(torch.autograd.Function):
             if Gt is not None:
                 gXt = torch.empty(N, 5, p.Kt, **f32)
                 _gemm(Gt, 5 * N, p.OtP, WtT, p.Kt, 1, gXt, p.Kt)
-            dR = torch.zeros(E, p.P, **f32) if need[10] else None
-            ddir = torch.zeros(E, 3, **f32) if need[8] else None
-            dY = torch.zeros(E, p.ysh, **f32) if need[9] else None
+            dR = torch.zeros(E, p.P, **f32) if need_R else None
+            ddir = torch.zeros(E, 3, **f32) if need_dir else None
+            dY = torch.zeros(E, p.ysh, **f32) if need_Y else None
             _nat.check(L.geo_se3_bwd_edge(
                 _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, Cs, Cv, Ct, _nat.ptr(row), _nat.ptr(perm),
-                _nat.ptr(ns), _nat.ptr(ne), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R),
-                p.P, p.pc_c, ctx.cg_c, _nat.ptr(gXs), p.Ks, _nat.ptr(gXv), p.Kv, _nat.ptr(gXt), p.Kt,
-                _nat.ptr(dR), _nat.ptr(ddir), _nat.ptr(dY), st), "geo_se3_bwd_edge")
+                _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh,
+                _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(gXs), p.Ks, _nat.ptr(gXv), p.Kv,
+                _nat.ptr(gXt), p.Kt, _nat.ptr(dR), _nat.ptr(ddir), _nat.ptr(dY), st),
+                "geo_se3_bwd_edge")
 
         # feature gradients: source-side sums over the CSR of the sources, then GEMMs with W^T
         ds = dv = dt = None
-        want_s, want_v, want_t = need[5] and Cs > 0, need[6] and Cv > 0, need[7] and Ct > 0
+        want_s, want_v, want_t = need_s and Cs > 0, need_v and Cv > 0, need_t and Ct > 0
         if want_s or want_v or want_t:
-            perm_r, ns_r, ne_r = src_csr()
+            perm_r, ns_r, ne_r = source_csr(row, N)
             Zs = torch.empty(N, p.KZs, **f32) if want_s else None
             Zv = torch.empty(N, 3, p.KZv, **f32) if want_v else None
             Zt = torch.empty(N, 5, p.KZt, **f32) if want_t and Ot > 0 else None
             Z8 = torch.empty(N, p.KZ8, **f32) if want_t and p.pc[8] >= 0 else None
             _nat.check(L.geo_se3_bwd_src(
                 _nat.ptr(Gs), Os, p.OsP, _nat.ptr(Gv), Ov, p.OvP, _nat.ptr(Gt), Ot, p.OtP, N,
-                _nat.ptr(col), _nat.ptr(perm_r), _nat.ptr(ns_r), _nat.ptr(ne_r), E, _nat.ptr(direction),
-                _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, ctx.cg_c, _nat.ptr(Zs), p.KZs, _nat.ptr(Zv),
-                p.KZv, _nat.ptr(Zt), p.KZt, _nat.ptr(Z8), p.KZ8, st), "geo_se3_bwd_src")
+                _nat.ptr(col), _nat.ptr(perm_r), _nat.ptr(ns_r), _nat.ptr(ne_r), E,
+                _nat.ptr(direction), _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg),
+                _nat.ptr(Zs), p.KZs, _nat.ptr(Zv), p.KZv, _nat.ptr(Zt), p.KZt, _nat.ptr(Z8), p.KZ8,
+                st), "geo_se3_bwd_src")
 
             t6 = want_t and Zt is not None and p.pc[6] >= 0
             Bs, Bv, Bt, B8 = _pack(p, W, [(6, _pad64(Cs), p.KZs if want_s else 0),
@@ -246,40 +306,88 @@ class _SE3MessageAggregate(torch.autograd.Function):
         # weight gradients: sums over nodes of (prepared output gradient) x (per-node aggregate)
         dW = [None] * 9
         for Gm, Xm, rows, OP, O_, KX, width, parts in (
-                (Gs, Xs, N, p.OsP, Os, p.Ks, Cs + Cv + Ct, ((0, 0, Cs), (3, Cs, Cs + Cv), (8, Cs + Cv, Cs + Cv + Ct))),
-                (Gv, Xv, 3 * N, p.OvP, Ov, p.Kv, Cs + 2 * Cv, ((1, 0, Cs), (2, Cs, Cs + Cv), (4, Cs + Cv, Cs + 2 * Cv))),
-                (Gt, Xt, 5 * N, p.OtP, Ot, p.Kt, Cs + Ct + Cv, ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)))):
-            if Gm is None or not any(need[12 + i] and p.pc[i] >= 0 for i, _, _ in parts) or width == 0:
+                (Gs, Xs, N, p.OsP, Os, p.Ks, Cs + Cv + Ct,
+                 ((0, 0, Cs), (3, Cs, Cs + Cv), (8, Cs + Cv, Cs + Cv + Ct))),
+                (Gv, Xv, 3 * N, p.OvP, Ov, p.Kv, Cs + 2 * Cv,
+                 ((1, 0, Cs), (2, Cs, Cs + Cv), (4, Cs + Cv, Cs + 2 * Cv))),
+                (Gt, Xt, 5 * N, p.OtP, Ot, p.Kt, Cs + Ct + Cv,
+                 ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)))):
+            if Gm is None or not any(need_W[i] and p.pc[i] >= 0 for i, _, _ in parts) or width == 0:
                 continue
             m = torch.empty(O_, width, **f32)
             nbytes = L.geo_se3_gemm_tn_workspace_bytes(rows, O_, width)
             ws = _nat.workspace(nbytes, dev)
-            _nat.check(L.geo_se3_gemm_tn(_nat.ptr(Gm), rows, OP, O_, _nat.ptr(Xm), KX, width, _nat.ptr(m),
-                                         width, _nat.ptr(ws), nbytes, st), "geo_se3_gemm_tn")
+            _nat.check(L.geo_se3_gemm_tn(_nat.ptr(Gm), rows, OP, O_, _nat.ptr(Xm), KX, width,
+                                         _nat.ptr(m), width, _nat.ptr(ws), nbytes, st),
+                       "geo_se3_gemm_tn")
             for i, a, b in parts:
-                if p.pc[i] >= 0:
-                    dW[i] = m[:, a:b]
+                if p.pc[i] >= 0 and need_W[i]:
+                    dW[i] = m[:, a:b].clone()   # outputs of a custom op may not alias each other
         dbias = None
-        if ctx.has_bias and need[11] and g_s is not None:
+        if need_bias and g_s is not None:
             gm = g_s if mask_u8 is None else g_s * mask_u8.view(N, 1).to(g_s.dtype)
             dbias = gm.sum(0)
-        dW = [dW[i] if (dW[i] is not None and need[12 + i]) else None for i in range(9)]
-        return (None, None, None, None, None, ds, dv, dt, ddir, dY, dR, dbias, *dW)
+        elif need_bias:
+            dbias = torch.zeros(Os, **f32)
+    # a requested gradient has its input's shape (zeros where nothing contributes: no channels,
+    # no edges, a path that does not run); one not requested is an empty placeholder
+    shapes = _bwd_shapes(s, v, t, row, Y, R, dims, need, W)
+    outs = [ds, dv, dt, ddir, dY, dR, dbias, *dW]
+    return [o if o is not None else torch.zeros(sh, **f32) for o, sh in zip(outs, shapes)]
 
 
-def _source_csr_getter(graph, row: Tensor, N: int):
-    def get():
-        cached = getattr(graph, "_source_csr", None)
-        if cached is not None:
-            return cached
-        _, perm_r, ns_r, ne_r = sort_and_build_csr_cuda(row, N)
-        out = (perm_r, ns_r, ne_r)
-        try:
-            object.__setattr__(graph, "_source_csr", out)
-        except (AttributeError, TypeError):
-            pass
-        return out
-    return get
+def _bwd_shapes(s, v, t, row, Y, R, dims, need, W):
+    """Shapes of the backward op's outputs: the input's shape where ``need``, else (0,)."""
+    N, E = s.shape[0], row.shape[0]
+    Ct = t.shape[1] if t is not None else 0
+    full = [(N, s.shape[1]), (N, v.shape[1], 3), (N, Ct, 5), (E, 3), (E, Y.shape[1]),
+            (E, R.shape[1]), (int(dims[0]),)]
+    full += [tuple(w.shape) if w is not None else _EMPTY for w in W]
+    return [sh if n else _EMPTY for sh, n in zip(full, need)]
+
+
+@_se3_bwd_op.register_fake
+def _se3_bwd_fake(g_s, g_v, g_t, s, v, t, row, col, perm, node_start, node_end, direction, Y, R,
+                  avg, mask, cg, Xs, Xv, Xt, dims, need, w0, w1, w2, w3, w4, w5, w6, w7, w8):
+    shapes = _bwd_shapes(s, v, t, row, Y, R, dims, need, (w0, w1, w2, w3, w4, w5, w6, w7, w8))
+    return [s.new_empty(sh, dtype=torch.float32) for sh in shapes]
+
+
+def _se3_setup(ctx, inputs, output) -> None:
+    (s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, mask, bias, cg, dims, *W) = inputs
+    s_out, v_out, t_out, Xs, Xv, Xt = output
+    ctx.dims = list(dims)
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(Xs, Xv, Xt)
+    ctx.save_for_backward(s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, mask, cg, Xs, Xv,
+                          Xt, *W)
+
+
+def _se3_backward(ctx, g_s, g_v, g_t, _gXs, _gXv, _gXt):
+    (s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, mask, cg, Xs, Xv, Xt,
+     *W) = ctx.saved_tensors
+    ni = ctx.needs_input_grad
+    need = [bool(ni[i]) for i in _NEED_INPUTS]
+    grads = torch.ops.geoembodied.se3_conv_bwd(g_s, g_v, g_t, s, v, t, row, col, perm, ns, ne,
+                                               direction, Y, R, avg, mask, cg, Xs, Xv, Xt,
+                                               ctx.dims, need, *W)
+    g = [x if n else None for x, n in zip(grads, need)]
+    ds, dv, dt, ddir, dY, dR, dbias, *dW = g
+    return (ds, dv, dt, None, None, None, None, None, ddir, dY, dR, None, None, dbias, None, None,
+            *dW)
+
+
+_se3_fwd_op.register_autograd(_se3_backward, setup_context=_se3_setup)
+
+_DEFAULT_CG: Dict[torch.device, Tensor] = {}
+
+
+def _cg_on(device: torch.device) -> Tensor:
+    """The CG(1,1->2) table on `device` (built once per device)."""
+    t = _DEFAULT_CG.get(device)
+    if t is None:
+        t = _DEFAULT_CG[device] = cg_11_2_cartesian(device=device).contiguous()
+    return t
 
 
 def se3_message_aggregate(
@@ -302,101 +410,125 @@ def se3_message_aggregate(
     the radial weights R on).  ``graph`` provides row, col, perm, node_start, node_end (CSR of the
     targets), direction, Y, avg_degree and N.  Returns (s [N, Cs_out], v [N, Cv_out, 3]) or with
     ``return_type2`` also t [N, Ct2_out, 5]; differentiable with respect to the features, the
-    graph's direction and Y, R, the weights and the bias."""
+    graph's direction and Y, R, the weights and the bias.  No host synchronisation."""
     _require_gpu("se3_message_aggregate", scalars, vectors, R)
     dev = scalars.device
     N = int(graph.N)
     f32 = torch.float32
     s = scalars.to(f32).contiguous()
     v = vectors.to(f32).contiguous()
-    Cs, Cv = s.shape[1], v.shape[1]
+    Cv = v.shape[1]
     if s.shape[0] != N or v.shape[0] != N or v.shape[2] != 3:
         raise ValueError(f"se3_message_aggregate: features {tuple(s.shape)}, {tuple(v.shape)} for N={N}")
     t = type2.to(f32).contiguous() if type2 is not None else None
     Ct = t.shape[1] if t is not None else 0
     Y = graph.Y.to(f32).contiguous()
     ysh = Y.shape[1]
-    has_y2 = ysh >= 9
-    pc = path_columns(weights, t is not None and Ct > 0, has_y2, Ct2_out)
+    pc = path_columns(weights, t is not None and Ct > 0, ysh >= 9, Ct2_out)
     if t is not None and Ct == 0:
         t = None
     R = R.to(f32).contiguous()
     P = R.shape[1]
     if max(pc) >= P:
         raise ValueError(f"se3_message_aggregate: {max(pc) + 1} paths run but R has {P} columns")
-    plan = _Plan(Cs, Cv, Ct, Cs_out, Cv_out, Ct2_out, pc, P, ysh, return_type2 and Ct2_out > 0)
-    cg = cg_11_2 if cg_11_2 is not None else cg_11_2_cartesian()
-    cg_c = (ctypes.c_float * 45)(*[float(x) for x in cg.detach().reshape(-1).cpu().tolist()])
+    Ot = Ct2_out if (return_type2 and Ct2_out > 0) else 0
+    dims = [int(Cs_out), int(Cv_out), int(Ot), *pc]
+    cg = None
+    if pc[7] >= 0:
+        cg = (cg_11_2.to(device=dev, dtype=f32).contiguous() if cg_11_2 is not None
+              else _cg_on(dev))
     row = graph.row.to(device=dev, dtype=torch.int64).contiguous()
     col = graph.col.to(device=dev, dtype=torch.int64).contiguous()
     perm = None if getattr(graph, "_perm_identity", False) else \
         graph.perm.to(device=dev, dtype=torch.int32).contiguous()
-    arrays = (row, col, perm,
-              graph.node_start.to(device=dev, dtype=torch.int32).contiguous(),
-              graph.node_end.to(device=dev, dtype=torch.int32).contiguous(),
-              _source_csr_getter(graph, row, N))
+    ns = graph.node_start.to(device=dev, dtype=torch.int32).contiguous()
+    ne = graph.node_end.to(device=dev, dtype=torch.int32).contiguous()
     avg = graph.avg_degree
     avg = (avg.to(device=dev, dtype=f32).contiguous() if avg is not None
            else torch.ones(N, dtype=f32, device=dev))
-    mask_u8 = None
+    m = None
     if mask is not None:
-        mask_u8 = mask.to(device=dev, dtype=torch.bool).reshape(-1).contiguous().view(torch.uint8)
+        m = mask.to(device=dev, dtype=torch.bool).reshape(-1).contiguous()
     b = bias.to(f32).contiguous() if bias is not None and Cs_out > 0 else None
-    Wl = [(weights.get(k).to(f32).contiguous() if weights.get(k) is not None else
-           torch.zeros(0, device=dev)) for k in PATH_NAMES]
+    Wl = [(weights.get(k).to(f32).contiguous() if weights.get(k) is not None else None)
+          for k in PATH_NAMES]
     direction = graph.direction.to(f32).contiguous()
-    with torch.cuda.device(dev):
-        s_out, v_out, t_out = _SE3MessageAggregate.apply(
-            plan, arrays, cg_c, avg, mask_u8, s, v, t, direction, Y, R, b, *Wl)
+    s_out, v_out, t_out, _, _, _ = torch.ops.geoembodied.se3_conv_fwd(
+        s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, m, b, cg, dims, *Wl)
     if return_type2:
         return s_out, v_out, (t_out if Ct2_out > 0 else None)
     return s_out, v_out
 
 
-class _RadialMLP(torch.autograd.Function):
-    """R = W2 silu(W1 (basis(dist) * envelope(dist)) + b1) + b2 in one kernel per direction."""
+@torch.library.custom_op("geoembodied::radial_mlp", mutates_args=())
+def _radial_op(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
+               b2: Tensor) -> Tensor:
+    """R = W2 silu(W1 (basis(dist) * envelope(dist)) + b1) + b2 in one kernel (fp32 inputs)."""
+    dev = dist.device
+    E = dist.shape[0]
+    H, NB = W1.shape
+    P = W2.shape[0]
+    R = torch.empty(E, P, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _nat.check(_nat.lib().geo_radial_mlp_fwd(
+            _nat.ptr(dist), E, _nat.ptr(freqs), NB, float(cutoff), _nat.ptr(W1), _nat.ptr(b1), H,
+            _nat.ptr(W2), _nat.ptr(b2), P, _nat.ptr(R), _nat.stream_of(dev)), "geo_radial_mlp_fwd")
+    return R
 
-    @staticmethod
-    def forward(ctx, dist, freqs, cutoff, W1, b1, W2, b2):
-        dev = dist.device
-        E = dist.shape[0]
-        H, NB = W1.shape
-        P = W2.shape[0]
-        d = dist.to(torch.float32).contiguous()
-        args = [x.to(torch.float32).contiguous() for x in (freqs, W1, b1, W2, b2)]
-        R = torch.empty(E, P, dtype=torch.float32, device=dev)
-        with torch.cuda.device(dev):
-            _nat.check(_nat.lib().geo_radial_mlp_fwd(
-                _nat.ptr(d), E, _nat.ptr(args[0]), NB, float(cutoff), _nat.ptr(args[1]),
-                _nat.ptr(args[2]), H, _nat.ptr(args[3]), _nat.ptr(args[4]), P, _nat.ptr(R),
-                _nat.stream_of(dev)), "geo_radial_mlp_fwd")
-        ctx.save_for_backward(d, *args)
-        ctx.cutoff, ctx.dims = float(cutoff), (E, NB, H, P)
-        return R
 
-    @staticmethod
-    def backward(ctx, dR):
-        d, freqs, W1, b1, W2, b2 = ctx.saved_tensors
-        E, NB, H, P = ctx.dims
-        dev = d.device
-        need = ctx.needs_input_grad
-        f32 = dict(dtype=torch.float32, device=dev)
-        dd = torch.empty(E, **f32) if need[0] else None
-        dW1 = torch.empty(H, NB, **f32) if need[3] else None
-        db1 = torch.empty(H, **f32) if need[4] else None
-        dW2 = torch.empty(P, H, **f32) if need[5] else None
-        db2 = torch.empty(P, **f32) if need[6] else None
-        g = dR.to(torch.float32).contiguous()
-        L = _nat.lib()
-        with torch.cuda.device(dev):
-            nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E)
-            ws = _nat.workspace(nbytes, dev)
-            _nat.check(L.geo_radial_mlp_bwd(
-                _nat.ptr(d), E, _nat.ptr(freqs), NB, ctx.cutoff, _nat.ptr(W1), _nat.ptr(b1), H,
-                _nat.ptr(W2), _nat.ptr(b2), P, _nat.ptr(g), _nat.ptr(dd), _nat.ptr(dW1), _nat.ptr(db1),
-                _nat.ptr(dW2), _nat.ptr(db2), _nat.ptr(ws), nbytes, _nat.stream_of(dev)),
-                "geo_radial_mlp_bwd")
-        return dd, None, None, dW1, db1, dW2, db2
+@_radial_op.register_fake
+def _radial_fake(dist, freqs, cutoff, W1, b1, W2, b2):
+    return dist.new_empty(dist.shape[0], W2.shape[0], dtype=torch.float32)
+
+
+@torch.library.custom_op("geoembodied::radial_mlp_bwd", mutates_args=())
+def _radial_bwd_op(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor,
+                   W2: Tensor, b2: Tensor, need: List[bool]) -> List[Tensor]:
+    """[d dist, dW1, db1, dW2, db2]; an entry not in ``need`` is empty."""
+    dev = dist.device
+    E = dist.shape[0]
+    H, NB = W1.shape
+    P = W2.shape[0]
+    f32 = dict(dtype=torch.float32, device=dev)
+    shapes = ((E,), (H, NB), (H,), (P, H), (P,))
+    outs = [torch.empty(sh, **f32) if n else None for sh, n in zip(shapes, need)]
+    g = dR.to(torch.float32).contiguous()
+    L = _nat.lib()
+    with torch.cuda.device(dev):
+        nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E)
+        ws = _nat.workspace(nbytes, dev)
+        _nat.check(L.geo_radial_mlp_bwd(
+            _nat.ptr(dist), E, _nat.ptr(freqs), NB, float(cutoff), _nat.ptr(W1), _nat.ptr(b1), H,
+            _nat.ptr(W2), _nat.ptr(b2), P, _nat.ptr(g), *[_nat.ptr(o) for o in outs], _nat.ptr(ws),
+            nbytes, _nat.stream_of(dev)), "geo_radial_mlp_bwd")
+    return [o if o is not None else dist.new_empty(_EMPTY, dtype=torch.float32) for o in outs]
+
+
+@_radial_bwd_op.register_fake
+def _radial_bwd_fake(dR, dist, freqs, cutoff, W1, b1, W2, b2, need):
+    E = dist.shape[0]
+    H, NB = W1.shape
+    P = W2.shape[0]
+    shapes = ((E,), (H, NB), (H,), (P, H), (P,))
+    return [dist.new_empty(sh if n else _EMPTY, dtype=torch.float32) for sh, n in zip(shapes, need)]
+
+
+def _radial_setup(ctx, inputs, output) -> None:
+    dist, freqs, cutoff, W1, b1, W2, b2 = inputs
+    ctx.cutoff = float(cutoff)
+    ctx.save_for_backward(dist, freqs, W1, b1, W2, b2)
+
+
+def _radial_backward(ctx, dR):
+    dist, freqs, W1, b1, W2, b2 = ctx.saved_tensors
+    ni = ctx.needs_input_grad
+    need = [bool(ni[i]) for i in (0, 3, 4, 5, 6)]
+    grads = torch.ops.geoembodied.radial_mlp_bwd(dR, dist, freqs, ctx.cutoff, W1, b1, W2, b2, need)
+    dd, dW1, db1, dW2, db2 = [x if n else None for x, n in zip(grads, need)]
+    return dd, None, None, dW1, db1, dW2, db2
+
+
+_radial_op.register_autograd(_radial_backward, setup_context=_radial_setup)
 
 
 def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
@@ -405,7 +537,8 @@ def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tenso
     hidden <= 64, outputs <= 16), differentiable with respect to dist and the four weights."""
     _require_gpu("radial_mlp", dist)
     f = torch.float32
-    return _RadialMLP.apply(dist.to(f), freqs.to(f), cutoff, W1.to(f), b1.to(f), W2.to(f), b2.to(f))
+    c = [x.to(f).contiguous() for x in (dist, freqs, W1, b1, W2, b2)]
+    return torch.ops.geoembodied.radial_mlp(c[0], c[1], float(cutoff), c[2], c[3], c[4], c[5])
 
 
 class RadialBasis(nn.Module):

@@ -52,7 +52,8 @@ extern "C" {
 const char* geo_last_error(void);
 /* Build identification: target arch, compiler, flags. */
 const char* geo_build_info(void);
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature or argument-meaning change (2: the SE3 CG table is a
+ * device array; segment softmax takes zero_tail). */
 int geo_abi_version(void);
 
 /* -------------------------------------------------------------------- FPS --- */
@@ -267,21 +268,25 @@ int geo_segment_reduce_bwd(int reduce, int dtype, const void* grad_out, const vo
  * 'amax' per target, exp(score - max), scatter_add, divide by the sum clamped at 1e-8) with one
  * kernel over the CSR of the targets.  scores and out are [E, H] row-major of `dtype` (GEO_F32
  * or GEO_F64); row perm[e] (e in [node_start[s], node_end[s])) belongs to segment s; perm may be
- * NULL (identity).  Rows that belong to no segment are not written.  NaN scores make their
- * segment NaN, as in the reference.
+ * NULL (identity).  NaN scores make their segment NaN, as in the reference.  Rows that belong
+ * to no segment are not written, except with zero_tail != 0, which states that the node ranges
+ * are ascending and contiguous from position 0 (node_start[0] = 0, node_start[s+1] =
+ * node_end[s]: the CSR geo_csr_build and the radius graph produce) and writes 0 to the rows
+ * perm[e] of the positions e in [node_end[S-1], E) (edges whose target is outside [0, S)), so
+ * every row of out is written without a separate fill.
  */
 int geo_segment_softmax_fwd(int dtype, const void* scores, const int32_t* perm,
                             const int32_t* node_start, const int32_t* node_end, int64_t E,
-                            int64_t S, int64_t H, void* out, void* stream);
+                            int64_t S, int64_t H, int zero_tail, void* out, void* stream);
 /*
  * Backward of the above (the gradient autograd forms for the reference's op sequence, whose
  * max-shift term cancels analytically): grad_scores[e] = out[e] * (grad_out[e] - sum over the
- * segment of grad_out * out).
+ * segment of grad_out * out).  zero_tail as in the forward (the tail rows' gradient is 0).
  */
 int geo_segment_softmax_bwd(int dtype, const void* grad_out, const void* out,
                             const int32_t* perm, const int32_t* node_start,
                             const int32_t* node_end, int64_t E, int64_t S, int64_t H,
-                            void* grad_scores, void* stream);
+                            int zero_tail, void* grad_scores, void* stream);
 
 /* --------------------------------------------------- neighbourhood gather-sum --- */
 /*
@@ -389,8 +394,9 @@ int geo_spatial_graph_epilogue(const float* pos, int64_t N, const int64_t* row, 
  * A7_m = sum r7 sum_ij d_i v_j cg[i][j][m], A8 = sum r8 |t|^2.  s [N, Cs], v [N, Cv, 3],
  * t [N, Ct, 5] fp32; dir [E, 3]; Y [E, ysh] (y0 = Y[:, 0], y2 = Y[:, 4:9]); R [E, P];
  * path_cols[9] (host array) = column of R of each path or -1 when the path is off (the
- * reference's runtime path numbering); cg[45] (host array) = CG(1,1->2) in Cartesian order
- * [3][3][5].  Xs / Xv / Xt may be NULL.
+ * reference's runtime path numbering); cg[45] (device array, e.g. the module's cg_11_2 buffer;
+ * may be NULL when path 7 is off) = CG(1,1->2) in Cartesian order [3][3][5].  Xs / Xv / Xt may
+ * be NULL.
  */
 int geo_se3_aggregate_fwd(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
                           int32_t Cv, int32_t Ct, const int64_t* row, const int32_t* perm,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 def test_build_info_and_version():
     info = _native.build_info()
     assert "gfx950" in info and "-ffp-contract=off" in info
-    assert _native.lib().geo_abi_version() == 1
+    assert _native.lib().geo_abi_version() == 2
 
 
 def test_workspace_sizes():

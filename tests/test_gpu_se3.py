@@ -163,7 +163,7 @@ def test_forward_and_gradients_vs_oracle(dev, cfg, shuffle):
         wg = cpu[k].grad
         gg_ = gpu[k].grad
         if wg is None:
-            assert gg_ is None or float(gg_.abs().max()) == 0.0, k
+            assert gg_ is None or gg_.numel() == 0 or float(gg_.abs().max()) == 0.0, k
             continue
         assert gg_ is not None, k
         _close(gg_, wg, 5e-4, 5e-5)

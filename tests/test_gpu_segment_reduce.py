@@ -282,6 +282,31 @@ def test_mean_and_max_match_reference_call_sites(dev):
     assert torch.allclose(mt.grad, mr.grad, atol=1e-6)
 
 
+def test_max_backward_exact_zero_maximum_differs_from_torch_by_design(dev):
+    """The one deliberate difference from the reference's scatter_reduce('amax',
+    include_self=False) on a zero-initialised output: when a segment's maximum is exactly 0.0,
+    PyTorch's backward also counts the initial 0 of the output as a tied maximum and gives each
+    tied input grad / (count + 1); this build gives grad / count (the gradient of the inputs'
+    maximum).  Segments whose maximum is not 0 agree exactly."""
+    seg, csr = _ops()
+    vals = torch.tensor([0.0, -1.0, 0.0,      # segment 0: maximum 0 attained twice
+                         0.0, -2.0,           # segment 1: maximum 0 attained once
+                         0.5, 0.5, -3.0,      # segment 2: maximum 0.5, two ties
+                         -0.0, -4.0],         # segment 3: maximum -0.0 (equal to 0)
+                        device=dev).unsqueeze(1)
+    col = torch.tensor([0, 0, 0, 1, 1, 2, 2, 2, 3, 3], device=dev)
+    g = torch.tensor([[6.0], [4.0], [2.0], [8.0]], device=dev)
+    ours = vals.clone().requires_grad_(True)
+    seg(ours, *csr(col, 4), 4, reduce="max").backward(g)
+    ref = vals.clone().requires_grad_(True)
+    torch.zeros(4, 1, device=dev).scatter_reduce(0, col.unsqueeze(1), ref, reduce="amax",
+                                                 include_self=False).backward(g)
+    want_ours = [3.0, 0.0, 3.0, 4.0, 0.0, 1.0, 1.0, 0.0, 8.0, 0.0]
+    want_torch = [2.0, 0.0, 2.0, 2.0, 0.0, 1.0, 1.0, 0.0, 4.0, 0.0]
+    assert ours.grad.squeeze(1).tolist() == want_ours
+    assert ref.grad.squeeze(1).tolist() == want_torch
+
+
 # ------------------------------------------------------------- many-segment forward path ---
 # S >= 4096 segments of average length <= 128 take the merge-path kernel: a wave's rows are
 # split evenly over its lane groups, so segments cross group boundaries and are completed from
@@ -376,7 +401,7 @@ def test_c3_full_size(dev):
     tot_seg = out.double().sum(0)
     tot_edge = msg.double().sum(0)
     assert torch.allclose(tot_seg, tot_edge, rtol=0, atol=1e-5 * msg.abs().double().sum(0).max().item())
-    # bf16 and max at full size: max exact against torch's segment reduction on the sorted rows
+    # max at full size: exact against torch's segment reduction on the sorted rows
     mx = seg(msg, cs, perm, ns, ne, S, reduce="max")
     ref_mx = torch.segment_reduce(msg, "max", lengths=(ne - ns).long(), unsafe=True)
     ref_mx = torch.where((ne - ns).unsqueeze(1) > 0, ref_mx, torch.zeros_like(ref_mx))

@@ -80,6 +80,39 @@ def test_softmax_special_values_and_unlisted_rows(dev):
     assert out.cpu().tolist() == [[0.5, 0.5], [0.5, 0.5], [1.0, 1.0], [0.0, 0.0], [0.0, 0.0]]
 
 
+@pytest.mark.parametrize("H,dtype", [(1, torch.float32), (2, torch.float32), (4, torch.float32),
+                                     (8, torch.float32), (3, torch.float32), (12, torch.float32),
+                                     (4, torch.float64)])
+def test_sparse_softmax_out_of_range_targets_zero_without_fill(dev, H, dtype):
+    """sparse_softmax allocates its output and gradient unfilled: the kernels themselves write 0
+    to the rows of targets outside [0, N) (the CSR build sorts them after the last segment), on
+    every kernel path (vector rows, runtime-H rows, one thread per head, float64); with N = 0
+    every row is such a row."""
+    _, sparse_softmax = _ops()
+    E, N = 5000, 300
+    g = torch.Generator().manual_seed(H)
+    index = torch.randint(0, N, (E,), generator=g)
+    index[::37] = -1
+    index[5::41] = N + 3
+    valid = ((index >= 0) & (index < N)).numpy()
+    x = (torch.randn(E, H, generator=g, dtype=torch.float64) * 3).to(dtype)
+    gr = torch.randn(E, H, generator=g, dtype=torch.float64).to(dtype)
+    for n_nodes in (N, 0):
+        xg = x.to(dev).requires_grad_(True)
+        w = sparse_softmax(xg, index.to(dev), n_nodes)
+        w.backward(gr.to(dev))
+        ref = np.zeros((E, H))
+        want = np.zeros((E, H))
+        if n_nodes:
+            ref[valid] = oracle.sparse_softmax(x.double().numpy()[valid], index.numpy()[valid], N)
+            want[valid] = oracle.sparse_softmax_bwd(gr.double().numpy()[valid],
+                                                    w.detach().cpu().double().numpy()[valid],
+                                                    index.numpy()[valid], N)
+        _check(w, ref, dtype)
+        _check(xg.grad, want, dtype)
+        assert np.all(w.detach().cpu().numpy()[~valid] == 0)
+
+
 def test_softmax_bf16_input_promoted(dev):
     _, sparse_softmax = _ops()
     x = torch.randn(1000, 2).bfloat16()

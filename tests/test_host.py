@@ -44,6 +44,60 @@ def test_product_does_not_import_oracle():
     assert out.stdout.strip() == "False"
 
 
+def test_se3_and_radial_custom_ops_fake_kernels():
+    """The SE3Conv forward runs through its custom ops' fake kernels on fake GPU tensors (the
+    shape inference torch.compile uses), and the backward op's fake outputs have the shapes the
+    real op returns: the inputs' shapes where a gradient is needed, empty elsewhere."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv, PATH_NAMES, path_columns
+    ops = torch.ops.geoembodied
+    for name in ("se3_conv_fwd", "se3_conv_bwd", "radial_mlp", "radial_mlp_bwd"):
+        assert hasattr(ops, name), name
+    torch.manual_seed(0)
+    conv_cpu = SE3Conv(8, 4, 6, 3, in_type2_channels=2, out_type2_channels=2, radius=1.0)
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        dev = torch.device("cuda:0")
+        conv = conv_cpu.to(dev)
+        N, E = 15, 70
+        i32 = dict(dtype=torch.int32, device=dev)
+        col = torch.randint(0, N, (E,), device=dev)
+        g = SpatialGraph(row=torch.randint(0, N, (E,), device=dev), col=col,
+                         direction=torch.randn(E, 3, device=dev), dist=torch.rand(E, device=dev),
+                         col_sorted=col.int(), perm=torch.arange(E, **i32),
+                         node_start=torch.zeros(N, **i32), node_end=torch.zeros(N, **i32),
+                         Y=torch.randn(E, 9, device=dev), N=N, E=E,
+                         avg_degree=torch.ones(N, device=dev))
+        s = torch.randn(N, 8, device=dev)
+        v = torch.randn(N, 4, 3, device=dev)
+        t = torch.randn(N, 2, 5, device=dev)
+        so, vo, to = conv(s, v, g, type2=t)
+        assert so.shape == (N, 6) and vo.shape == (N, 3, 3) and to.shape == (N, 2, 5)
+        R = conv.radial_basis(g.dist)
+        assert R.shape == (E, 9)
+        W = [getattr(conv, k).weight for k in PATH_NAMES]
+        pc = path_columns(dict(zip(PATH_NAMES, W)), True, True, 2)
+        assert pc == list(range(9))
+        dims = [6, 3, 2, *pc]
+        f = ops.se3_conv_fwd(s, v, t, g.row, g.col, None, g.node_start, g.node_end, g.direction,
+                             g.Y, R, g.avg_degree, None, conv.scalar_bias, conv.cg_11_2, dims, *W)
+        assert [tuple(x.shape) for x in f] == [(N, 6), (N, 3, 3), (N, 2, 5), (N, 16), (N, 3, 16),
+                                               (N, 5, 16)]
+        for need in ([True] * 16, [False] * 16, [True, False] * 8):
+            out = ops.se3_conv_bwd(f[0], f[1], f[2], s, v, t, g.row, g.col, None, g.node_start,
+                                   g.node_end, g.direction, g.Y, R, g.avg_degree, None,
+                                   conv.cg_11_2, f[3], f[4], f[5], dims, need, *W)
+            full = [(N, 8), (N, 4, 3), (N, 2, 5), (E, 3), (E, 9), (E, 9), (6,),
+                    *[tuple(w.shape) for w in W]]
+            want = [sh if n else (0,) for sh, n in zip(full, need)]
+            assert [tuple(x.shape) for x in out] == want
+        rb = conv.radial_basis
+        l1, l2 = rb.mlp[0], rb.mlp[2]
+        out = ops.radial_mlp_bwd(R, g.dist, rb.freqs, 1.0, l1.weight, l1.bias, l2.weight, l2.bias,
+                                 [True, False, True, True, False])
+        assert [tuple(x.shape) for x in out] == [(E,), (0,), (64,), (9, 64), (0,)]
+
+
 def test_custom_ops_registered_with_fake_kernels():
     from torch._subclasses.fake_tensor import FakeTensorMode
     ops = torch.ops.geoembodied
