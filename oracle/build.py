@@ -2,7 +2,8 @@
 
 ``python -m oracle.build`` compiles ``oracle/geo_oracle.c`` into ``oracle/lib/libgeo_oracle.so``
 with gcc.  ``-ffp-contract=off`` and ``-fno-fast-math`` keep every float operation a single
-IEEE fp32 operation, so the restated distances round like the reference's.
+IEEE fp32 operation, so the restated distances round like the reference's; ``-fopenmp`` runs
+independent queries / targets on several threads.
 
 The reference implementation itself cannot be built here: its kernels are CUDA sources that need
 nvcc, CUB and ATen (geoembodied/csrc/*.cu), none of which exist in this image, so there is no
@@ -20,7 +21,7 @@ HERE = Path(__file__).resolve().parent
 SRC = HERE / "geo_oracle.c"
 LIB = HERE / "lib" / "libgeo_oracle.so"
 CC = os.environ.get("CC", "gcc")
-FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+FLAGS = ["-O2", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
          "-Wall", "-Wextra", "-Wno-unused-parameter"]
 
 

@@ -5,7 +5,9 @@
  * this file; it is the checker used by tests/, __graft_entry__.smoke() and bench.py's CPU
  * baseline.
  *
- * Build: see oracle/build.py (gcc -O2 -ffp-contract=off -fPIC -shared).  Every float
+ * Build: see oracle/build.py (gcc -O2 -ffp-contract=off -fopenmp -fPIC -shared).  The KNN
+ * and radius loops run their queries / targets on OpenMP threads (each writes only its own
+ * outputs, so results do not depend on the thread count).  Every float
  * operation below is a single IEEE fp32 operation (x86-64 SSE, no contraction), so distances
  * round exactly like the reference's (fl(dx*dx) + fl(dy*dy)) + fl(dz*dz).
  */
@@ -119,23 +121,28 @@ void oracle_knn(const float* query, const float* source, const int64_t* ptr_q,
                 const int64_t* ptr_s, int64_t B, int64_t k, int64_t Nq, int64_t* out_idx,
                 float* out_dist) {
   for (int64_t i = 0; i < Nq * k; ++i) { out_idx[i] = -1; out_dist[i] = 1e30f; }
-  Key* heap = (Key*)malloc(sizeof(Key) * (size_t)(k > 0 ? k : 1));
   for (int64_t b = 0; b < B; ++b) {
     const int64_t qa = ptr_q[b], qc = ptr_q[b + 1], sa = ptr_s[b], sc = ptr_s[b + 1];
-    for (int64_t q = qa; q < qc; ++q) {
-      TopK t = {heap, 0, k};
-      for (int64_t j = sa; j < sc; ++j) {
-        Key key = {sqd(query + 3 * q, source + 3 * j), j};
-        topk_push(&t, key);
+    /* queries are independent: each thread owns its heap and writes only its query's row */
+#pragma omp parallel
+    {
+      Key* heap = (Key*)malloc(sizeof(Key) * (size_t)(k > 0 ? k : 1));
+#pragma omp for schedule(dynamic, 16)
+      for (int64_t q = qa; q < qc; ++q) {
+        TopK t = {heap, 0, k};
+        for (int64_t j = sa; j < sc; ++j) {
+          Key key = {sqd(query + 3 * q, source + 3 * j), j};
+          topk_push(&t, key);
+        }
+        qsort(heap, (size_t)t.n, sizeof(Key), key_cmp);
+        for (int64_t m = 0; m < t.n; ++m) {
+          out_idx[q * k + m] = heap[m].j;
+          out_dist[q * k + m] = heap[m].d;
+        }
       }
-      qsort(heap, (size_t)t.n, sizeof(Key), key_cmp);
-      for (int64_t m = 0; m < t.n; ++m) {
-        out_idx[q * k + m] = heap[m].j;
-        out_dist[q * k + m] = heap[m].d;
-      }
+      free(heap);
     }
   }
-  free(heap);
 }
 
 /*
@@ -161,8 +168,12 @@ void oracle_radius(const float* x, int64_t N, const int64_t* cloud, float r2, in
   int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nc > 0 ? nc : 1));
   for (int64_t c = 0; c < nc; ++c) fill[c] = start[c];
   for (int64_t i = 0; i < N; ++i) if (cloud[i] >= 0) members[fill[cloud[i]]++] = i;
+  /* targets are independent: each thread owns its heap and writes only its target's outputs */
+#pragma omp parallel
+  {
   Key* heap = (Key*)malloc(sizeof(Key) * (size_t)(K > 0 ? K : 1));
   int64_t* js = (int64_t*)malloc(sizeof(int64_t) * (size_t)(K > 0 ? K : 1));
+#pragma omp for schedule(dynamic, 64)
   for (int64_t i = 0; i < N; ++i) {
     if (deg && !row) deg[i] = 0;
     if (cloud[i] < 0) continue;
@@ -193,7 +204,9 @@ void oracle_radius(const float* x, int64_t N, const int64_t* cloud, float r2, in
       col[row_ptr[i] + m] = i;
     }
   }
-  free(js); free(heap); free(fill); free(members); free(start);
+  free(js); free(heap);
+  }
+  free(fill); free(members); free(start);
 }
 
 /*

