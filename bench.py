@@ -14,8 +14,14 @@ time from HIP events on the launch stream, algorithmic bytes E*C*4 + S*C*4 + (S+
 CPU baseline (``cpu_baseline``): the reference's CPU path (oracle/ref_cpu_path.py, same torch op
 sequences) on the same C2 batch, on this host's cores.
 
-Usage: python bench.py [--steps K] [--warmup W] [--all] [--no-cpu]
-One JSON line goes to stdout; progress goes to stderr.
+``legs`` holds every configuration (c1 ... c5): GPU times of each op, the fused-row kernels on
+the C2 graph, every C3 segment-reduce leg, and beside each configuration a CPU baseline of the
+reference's CPU path (bounded samples extrapolated where the full run would take minutes or
+would not fit in memory; each entry says what was timed).
+
+Usage: python bench.py [--steps K] [--warmup W] [--no-cpu] [--only LEG] [--iters I]
+One JSON line goes to stdout; progress goes to stderr.  ``--only`` with a single-kernel leg
+(fps_c2, knn_c5, c3max, ...) runs just that op, for counter collection with rocprofv3.
 """
 
 from __future__ import annotations
@@ -246,43 +252,48 @@ def event_ms(fn, iters: int, warmup: int) -> float:
     return s.elapsed_time(e) / iters
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--all", action="store_true", help="also time C1, C4, C5 and KNN legs")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", default=None,
-                    help="run one leg: c2 | c3 | c3bf16 | c3bwd | copy (HBM counter calibration)")
-    ap.add_argument("--iters", type=int, default=50, help="timed launches per C3 leg")
-    args = ap.parse_args()
+def cpu_ms(fn, runs: int = 3) -> float:
+    """Median wall time of ``runs`` calls on the host (ms)."""
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return sorted(ts)[len(ts) // 2]
 
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        log("bench.py measures one GPU: this build has no multi-GPU path (each op's work is a "
-            "single-GPU kernel; see DESIGN.md for how it would shard). Run with --gpus 1.")
-        return 2
-    if not torch.cuda.is_available():
-        log("bench.py needs a GPU")
-        return 2
 
+def _cpu_entry(value_ms: float, unit: str, sample: str) -> dict:
+    return {"value": round(value_ms, 2), "unit": unit, "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample}
+
+
+def _ops():
     import geoembodied  # noqa: F401  (registers the drop-in module paths)
     from geoembodied.functional.fps import farthest_point_sampling
     from geoembodied.functional.knn import knn
     from geoembodied.functional.radius_graph import radius_graph
     from geoembodied.functional.segment_reduce import segment_reduce, sort_and_build_csr
-    from gdl_amd import _native
+    return farthest_point_sampling, knn, radius_graph, segment_reduce, sort_and_build_csr
 
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    result: dict = {}
-    legs: dict = {}
 
-    # ---------------------------------------------------------------- C2 headline ---
+def _pair_keys(row, col, n) -> np.ndarray:
+    return np.asarray(row, dtype=np.int64) * n + np.asarray(col, dtype=np.int64)
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Configuration legs
+# ═══════════════════════════════════════════════════════════════════
+
+
+def leg_c2(args, dev) -> tuple:
+    """The headline step, its parts, the fused-row kernels on the C2 graph and the CPU baseline
+    of the step (the reference's CPU path) with the cdist disagreement diagnostic."""
+    fps, knn, radius_graph, _, sort_and_build_csr = _ops()
     c2 = make_c2()
     pos = c2["pos"].to(dev)
     batch = c2["batch"].to(dev)
     ptr = c2["ptr"].to(dev)
+    leg: dict = {}
 
     # FPS runs one workgroup per cloud (16 of 256 CUs) and the radius graph over all points does
     # not depend on it, so the radius graph runs on a second stream (default priority) beside
@@ -294,7 +305,7 @@ def main() -> int:
     def step():
         main = torch.cuda.current_stream(dev)
         s_rad.wait_stream(main)
-        idx = farthest_point_sampling(pos, c2["M"], ptr=ptr)
+        idx = fps(pos, c2["M"], ptr=ptr)
         with torch.cuda.stream(s_rad):
             row, col = radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
                                     num_batch_elements=c2["B"])
@@ -303,224 +314,113 @@ def main() -> int:
             x.record_stream(main)
         return idx, row, col
 
-    def step_sequential():
-        idx = farthest_point_sampling(pos, c2["M"], ptr=ptr)
+    def step_one_stream():
+        idx = fps(pos, c2["M"], ptr=ptr)
         row, col = radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
                                 num_batch_elements=c2["B"])
         return idx, row, col
 
-    ms_step = None
-    if args.only in (None, "c2"):
-        log("C2: FPS + radius_graph ...")
-        ms_step = wall_ms(step, args.steps, args.warmup)
-        idx, row, col = step()
-        legs["c2_fps_ms"] = wall_ms(lambda: farthest_point_sampling(pos, c2["M"], ptr=ptr),
-                                    args.steps, 3)
-        legs["c2_radius_ms"] = wall_ms(lambda: radius_graph(pos, c2["r"], max_num_neighbors=c2["K"],
-                                                            batch=batch, num_batch_elements=c2["B"]),
-                                       args.steps, 3)
-        legs["c2_step_sequential_ms"] = wall_ms(step_sequential, args.steps, 3)
-        legs["c2_edges"] = int(row.numel())
-        legs["c2_points_per_s"] = pos.shape[0] / (ms_step / 1e3)
-        legs["c2_edges_per_s"] = row.numel() / (legs["c2_radius_ms"] / 1e3)
-        legs["c2_fps_point_updates_per_s"] = c2["B"] * c2["N"] * c2["M"] / (legs["c2_fps_ms"] / 1e3)
-        cent = pos[idx]
-        ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
-        legs["c2_knn_ms"] = wall_ms(lambda: knn(cent, pos, ptr_q, ptr, c2["k"]), args.steps, 3)
-        legs["c2_radius_centres_ms"] = wall_ms(
-            lambda: radius_graph(cent, c2["r"], max_num_neighbors=c2["K"],
-                                 num_batch_elements=c2["B"]), args.steps, 3)
-        log(f"  step {ms_step:.3f} ms (sequential {legs['c2_step_sequential_ms']:.3f})  "
-            f"fps {legs['c2_fps_ms']:.3f}  radius {legs['c2_radius_ms']:.3f}"
-            f"  knn {legs['c2_knn_ms']:.3f}  edges {legs['c2_edges']}")
-        # attention softmax over the C2 graph (4 heads): CSR from the radius graph's target order
-        from gdl_amd.functional.segment_softmax import segment_softmax, sparse_softmax
-        cs, pm, ns, ne = sort_and_build_csr(col, pos.shape[0])
-        scores = torch.randn(row.numel(), 4, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
-        legs["c2_softmax_fwd_us"] = round(1e3 * event_ms(
-            lambda: segment_softmax(scores, pm, ns, ne, pos.shape[0], contiguous_csr=True),
-            args.iters, 5), 2)
-        legs["c2_sparse_softmax_us"] = round(1e3 * wall_ms(
-            lambda: sparse_softmax(scores, col, pos.shape[0]), args.steps, 3), 2)
-        log(f"  segment softmax (E={row.numel()}, H=4): {legs['c2_softmax_fwd_us']} us on the CSR, "
-            f"{legs['c2_sparse_softmax_us']} us from the target index")
-        # interpolation of 112-channel features (64 scalars + 16 vectors) from the centres back
-        # to every point with k = 3 IDW (the interpolation layer's shape)
-        from gdl_amd.functional.gather import knn_interpolate
-        ii, dd = knn(pos, cent, ptr, ptr_q, 3)
-        feats = torch.randn(cent.shape[0], 112, device=dev)
-        legs["c2_interp_k3_c112_us"] = round(1e3 * event_ms(lambda: knn_interpolate(feats, ii, dd),
-                                                            args.iters, 5), 2)
-        log(f"  knn_interpolate (65536 x k=3 x 112 ch): {legs['c2_interp_k3_c112_us']} us")
-        # the whole spatial graph: radius graph + CSR + directions, distances, SH (l <= 2) and
-        # average degrees, as one call
-        from gdl_amd.graph import SpatialGraph
-        legs["c2_spatial_graph_ms"] = wall_ms(
-            lambda: SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
-                                       num_batch_elements=c2["B"]), args.steps, 3)
-        log(f"  SpatialGraph.build: {legs['c2_spatial_graph_ms']:.3f} ms "
-            f"(radius graph alone {legs['c2_radius_ms']:.3f} ms)")
-        # one SE3Conv layer (64 scalar + 16 vector channels in and out, paths 0-4) on the C2 graph:
-        # fused message passing vs the reference's op sequence in PyTorch on the same GPU
-        from gdl_amd.se3_conv import SE3Conv
-        gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
-                                num_batch_elements=c2["B"])
-        torch.manual_seed(0)
-        conv = SE3Conv(64, 16, 64, 16, radius=c2["r"]).to(dev)
-        fs = torch.randn(gr.N, 64, device=dev, requires_grad=True)
-        fv = torch.randn(gr.N, 16, 3, device=dev, requires_grad=True)
+    log("C2: FPS + radius_graph ...")
+    ms_step = wall_ms(step, args.steps, args.warmup)
+    idx, row, col = step()
+    leg["step_ms"] = round(ms_step, 4)
+    leg["step_one_stream_ms"] = round(wall_ms(step_one_stream, args.steps, 3), 4)
+    leg["fps_ms"] = round(wall_ms(lambda: fps(pos, c2["M"], ptr=ptr), args.steps, 3), 4)
+    leg["radius_ms"] = round(wall_ms(lambda: radius_graph(
+        pos, c2["r"], max_num_neighbors=c2["K"], batch=batch, num_batch_elements=c2["B"]),
+        args.steps, 3), 4)
+    leg["edges"] = int(row.numel())
+    leg["points_per_s"] = round(pos.shape[0] / (ms_step / 1e3))
+    leg["edges_per_s"] = round(row.numel() / (leg["radius_ms"] / 1e3))
+    leg["fps_point_updates_per_s"] = round(c2["B"] * c2["N"] * c2["M"] / (leg["fps_ms"] / 1e3))
+    cent = pos[idx]
+    ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
+    leg["knn_k16_ms"] = round(wall_ms(lambda: knn(cent, pos, ptr_q, ptr, c2["k"]), args.steps, 3), 4)
+    leg["radius_centres_ms"] = round(wall_ms(
+        lambda: radius_graph(cent, c2["r"], max_num_neighbors=c2["K"], num_batch_elements=c2["B"]),
+        args.steps, 3), 4)
+    log(f"  step {ms_step:.3f} ms (one stream {leg['step_one_stream_ms']:.3f})  fps "
+        f"{leg['fps_ms']:.3f}  radius {leg['radius_ms']:.3f}  knn {leg['knn_k16_ms']:.3f}  "
+        f"edges {leg['edges']}")
+    # attention softmax over the C2 graph (4 heads): CSR from the radius graph's target order
+    from gdl_amd.functional.segment_softmax import segment_softmax, sparse_softmax
+    cs, pm, ns, ne = sort_and_build_csr(col, pos.shape[0])
+    scores = torch.randn(row.numel(), 4, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+    leg["softmax_fwd_us"] = round(1e3 * event_ms(
+        lambda: segment_softmax(scores, pm, ns, ne, pos.shape[0], contiguous_csr=True),
+        args.iters, 5), 2)
+    leg["sparse_softmax_us"] = round(1e3 * wall_ms(
+        lambda: sparse_softmax(scores, col, pos.shape[0]), args.steps, 3), 2)
+    log(f"  segment softmax (E={row.numel()}, H=4): {leg['softmax_fwd_us']} us on the CSR, "
+        f"{leg['sparse_softmax_us']} us from the target index")
+    # interpolation of 112-channel features (64 scalars + 16 vectors) from the centres back to
+    # every point with k = 3 IDW (the interpolation layer's shape)
+    from gdl_amd.functional.gather import knn_interpolate
+    ii, dd = knn(pos, cent, ptr, ptr_q, 3)
+    feats = torch.randn(cent.shape[0], 112, device=dev)
+    leg["interp_k3_c112_us"] = round(1e3 * event_ms(lambda: knn_interpolate(feats, ii, dd),
+                                                    args.iters, 5), 2)
+    log(f"  knn_interpolate (65536 x k=3 x 112 ch): {leg['interp_k3_c112_us']} us")
+    # the whole spatial graph: radius graph + CSR + directions, distances, SH (l <= 2) and
+    # average degrees, as one call
+    from gdl_amd.graph import SpatialGraph
+    leg["spatial_graph_ms"] = round(wall_ms(
+        lambda: SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                   num_batch_elements=c2["B"]), args.steps, 3), 4)
+    log(f"  SpatialGraph.build: {leg['spatial_graph_ms']:.3f} ms")
+    # one SE3Conv layer (64 scalar + 16 vector channels in and out, paths 0-4) on the C2 graph:
+    # fused message passing vs the reference's op sequence in PyTorch on the same GPU
+    from gdl_amd.se3_conv import SE3Conv
+    gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                            num_batch_elements=c2["B"])
+    torch.manual_seed(0)
+    conv = SE3Conv(64, 16, 64, 16, radius=c2["r"]).to(dev)
+    fs = torch.randn(gr.N, 64, device=dev, requires_grad=True)
+    fv = torch.randn(gr.N, 16, 3, device=dev, requires_grad=True)
 
-        def se3_fwd():
-            with torch.no_grad():
-                return conv(fs, fv, gr)
+    def se3_fwd():
+        with torch.no_grad():
+            return conv(fs, fv, gr)
 
-        # a training step's backward: gradients start empty (zero_grad(set_to_none=True)), so
-        # no accumulation adds enter either side's timing
-        def clear_grads():
-            conv.zero_grad(set_to_none=True)
-            fs.grad = None
-            fv.grad = None
+    # a training step's backward: gradients start empty (zero_grad(set_to_none=True)), so no
+    # accumulation adds enter either side's timing
+    def clear_grads():
+        conv.zero_grad(set_to_none=True)
+        fs.grad = None
+        fv.grad = None
 
-        def se3_fb():
-            clear_grads()
-            so, vo = conv(fs, fv, gr)
-            torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
+    def se3_fb():
+        clear_grads()
+        so, vo = conv(fs, fv, gr)
+        torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
 
-        def ref_fwd():
-            with torch.no_grad():
-                return _se3_reference_torch(conv, fs, fv, gr)
+    def ref_fwd():
+        with torch.no_grad():
+            return _se3_reference_torch(conv, fs, fv, gr)
 
-        def ref_fb():
-            clear_grads()
-            so, vo = _se3_reference_torch(conv, fs, fv, gr)
-            torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
+    def ref_fb():
+        clear_grads()
+        so, vo = _se3_reference_torch(conv, fs, fv, gr)
+        torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
 
-        legs["c2_se3conv_fwd_ms"] = wall_ms(se3_fwd, args.steps, 3)
-        legs["c2_se3conv_fwd_bwd_ms"] = wall_ms(se3_fb, args.steps, 3)
-        legs["c2_se3conv_torch_ref_fwd_ms"] = wall_ms(ref_fwd, args.steps, 3)
-        legs["c2_se3conv_torch_ref_fwd_bwd_ms"] = wall_ms(ref_fb, args.steps, 3)
-        log(f"  SE3Conv 64s+16v (E={gr.E}): fused {legs['c2_se3conv_fwd_ms']:.3f} ms fwd, "
-            f"{legs['c2_se3conv_fwd_bwd_ms']:.3f} ms fwd+bwd; reference op sequence in PyTorch "
-            f"{legs['c2_se3conv_torch_ref_fwd_ms']:.3f} / {legs['c2_se3conv_torch_ref_fwd_bwd_ms']:.3f} ms")
-        legs["c2_fused_rooflines"] = _fused_rooflines(args, dev, pos, row, col, pm, ns, ne, scores,
-                                                      feats, ii, dd, gr, conv, fs, fv)
-        for name, r in legs["c2_fused_rooflines"].items():
-            log(f"  {name}: {r['us']} us, {r['GB/s']} GB/s = {100 * r['frac']:.1f}% of 8 TB/s "
-                f"({r['bytes']} algorithmic bytes)")
+    leg["se3conv_fwd_ms"] = round(wall_ms(se3_fwd, args.steps, 3), 4)
+    leg["se3conv_fwd_bwd_ms"] = round(wall_ms(se3_fb, args.steps, 3), 4)
+    leg["se3conv_torch_ref_fwd_ms"] = round(wall_ms(ref_fwd, args.steps, 3), 4)
+    leg["se3conv_torch_ref_fwd_bwd_ms"] = round(wall_ms(ref_fb, args.steps, 3), 4)
+    log(f"  SE3Conv 64s+16v (E={gr.E}): fused {leg['se3conv_fwd_ms']:.3f} ms fwd, "
+        f"{leg['se3conv_fwd_bwd_ms']:.3f} ms fwd+bwd; reference op sequence in PyTorch "
+        f"{leg['se3conv_torch_ref_fwd_ms']:.3f} / {leg['se3conv_torch_ref_fwd_bwd_ms']:.3f} ms")
+    leg["fused_rooflines"] = _fused_rooflines(args, dev, pos, row, col, pm, ns, ne, scores, feats,
+                                              ii, dd, gr, conv, fs, fv)
+    for name, r in leg["fused_rooflines"].items():
+        log(f"  {name}: {r['us']} us, {r['GB/s']} GB/s = {100 * r['frac']:.1f}% of 8 TB/s "
+            f"({r['bytes']} algorithmic bytes)")
 
-    # ---------------------------------------------------------------- C3 roofline ---
-    roof = None
-    if args.only in (None, "c3", "c3bf16", "c3bwd"):
-        log("C3: segment reduce ...")
-        off = make_c3_offsets()
-        S, E, C = off.shape[0] - 1, int(off[-1]), 128
-        ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
-        ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
-        col_sorted = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32),
-                                             (ne - ns).long())
-        perm = torch.arange(E, device=dev, dtype=torch.int32)
-        gen = torch.Generator(device=dev).manual_seed(0)
-        msg = torch.randn(E, C, device=dev, generator=gen)
-        bytes_fwd = E * C * 4 + S * C * 4 + (S + 1) * 4
-        iters = args.iters
-        if args.only in (None, "c3"):
-            ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
-            gbs = bytes_fwd / (ms * 1e-3) / 1e9
-            roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_SUM_TRAFFIC_BYTES,
-                    "kernel": "seg_fwd_merge_kernel<float,16,SUM,perm>", "ms_per_launch": round(ms, 4),
-                    "algorithmic_bytes": bytes_fwd}
-            log(f"  fwd sum fp32: {ms:.4f} ms  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of peak)")
-            for red in ("mean", "max"):
-                extra = S * C * 4 if red == "max" else 0
-                msr = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S, reduce=red),
-                               iters, 5)
-                legs[f"c3_{red}_fp32_gbs"] = round((bytes_fwd + extra) / (msr * 1e-3) / 1e9, 1)
-                log(f"  fwd {red} fp32: {msr:.4f} ms  {legs[f'c3_{red}_fp32_gbs']} GB/s")
-        if args.only in (None, "c3bf16"):
-            mb = msg.bfloat16()
-            bytes_b = E * C * 2 + S * C * 2 + (S + 1) * 4
-            msb = event_ms(lambda: segment_reduce(mb, col_sorted, perm, ns, ne, S), iters, 5)
-            legs["c3_sum_bf16_ms"] = round(msb, 4)
-            legs["c3_sum_bf16_gbs"] = round(bytes_b / (msb * 1e-3) / 1e9, 1)
-            log(f"  fwd sum bf16: {msb:.4f} ms  {legs['c3_sum_bf16_gbs']} GB/s")
-            del mb
-        if args.only in (None, "c3bwd"):
-            from gdl_amd.csrc import segment_reduce_backward_hip
-            grad = torch.randn(S, C, device=dev, generator=gen)
-            bytes_bwd = S * C * 4 + E * C * 4 + (S + 1) * 4
-            msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, "sum"),
-                           iters, 5)
-            legs["c3_bwd_sum_fp32_gbs"] = round(bytes_bwd / (msb * 1e-3) / 1e9, 1)
-            log(f"  bwd sum fp32: {msb:.4f} ms  {legs['c3_bwd_sum_fp32_gbs']} GB/s")
-        col64 = col_sorted.long()
-        legs["c3_csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col64, S), 10, 2), 4)
-        # the same targets in random order (the sorted-input identity path does not apply)
-        col_sh = col64[torch.randperm(E, device=dev, generator=gen)]
-        legs["c3_csr_build_shuffled_ms"] = round(wall_ms(lambda: sort_and_build_csr(col_sh, S), 10, 2), 4)
-        del col_sh
-        del msg
-
-    # ------------------------------------------------------- HBM counter calibration ---
-    if args.only == "copy":
-        # A plain elementwise pass over 1 GiB (read 1 GiB, write 1 GiB with 16-byte vector
-        # accesses): the reference point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE.
-        src = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        ms = event_ms(lambda: torch.add(src, 1.0, out=dst), args.iters, 3)
-        legs["copy_1gib_ms"] = round(ms, 4)
-        legs["copy_1gib_gbs"] = round(2 * src.numel() * 4 / (ms * 1e-3) / 1e9, 1)
-        log(f"  copy 1 GiB: {ms:.4f} ms  {legs['copy_1gib_gbs']} GB/s")
-
-    # ---------------------------------------------------------------- extra legs ---
-    if args.all:
-        c1 = make_c1()
-        p1 = c1["pos"].to(dev)
-
-        def c1_step():
-            i = farthest_point_sampling(p1, c1["M"])
-            cen = p1[i]
-            row, col = radius_graph(cen, c1["r"], max_num_neighbors=c1["K"])
-            cs, pm, a, b = sort_and_build_csr(col, c1["M"])
-            return segment_reduce(c1["feat"].to(dev)[row], cs, pm, a, b, c1["M"])
-        legs["c1_ms"] = wall_ms(c1_step, 20, 3)
-        c4 = make_c4()
-        p4, ptr4 = c4["pos"].to(dev), c4["ptr"].to(dev)
-
-        def c4_step():
-            i1 = farthest_point_sampling(p4, 512, ptr=ptr4)
-            q1 = p4[i1]
-            ptr1 = torch.arange(c4["B"] + 1, device=dev, dtype=torch.int64) * 512
-            i2 = farthest_point_sampling(q1, 128, ptr=ptr1)
-            q2 = q1[i2]
-            outs = []
-            for pts, r, n, C in ((q1, 0.2, 512, 64), (q2, 0.4, 128, 128)):
-                row, col = radius_graph(pts, r, max_num_neighbors=64, num_batch_elements=c4["B"])
-                cs, pm, a, b = sort_and_build_csr(col, pts.shape[0])
-                f = torch.ones(pts.shape[0], C, device=dev)[row]
-                outs.append(segment_reduce(f, cs, pm, a, b, pts.shape[0], reduce="max"))
-                outs.append(segment_reduce(f, cs, pm, a, b, pts.shape[0], reduce="mean"))
-            return outs
-        legs["c4_ms"] = wall_ms(c4_step, 10, 2)
-        c5 = make_c5()
-        p5 = c5["pos"].to(dev)
-        t0 = time.perf_counter()
-        i5 = farthest_point_sampling(p5, c5["M"])
-        torch.cuda.synchronize()
-        legs["c5_fps_ms"] = (time.perf_counter() - t0) * 1e3
-        cen5 = p5[i5]
-        legs["c5_radius_ms"] = wall_ms(lambda: radius_graph(cen5, c5["r"], max_num_neighbors=64), 10, 2)
-        pq = torch.tensor([0, c5["M"]], device=dev, dtype=torch.int64)
-        ps = torch.tensor([0, p5.shape[0]], device=dev, dtype=torch.int64)
-        legs["c5_knn_ms"] = wall_ms(lambda: knn(cen5, p5, pq, ps, c5["k"]), 5, 1)
-        log(f"  extra legs: {legs}")
-
-    # ---------------------------------------------------------------- CPU baseline ---
     cpu = None
-    if not args.no_cpu and args.only in (None, "c2"):
+    if not args.no_cpu:
         from oracle import ref_cpu_path
         threads = torch.get_num_threads()
-        log(f"CPU baseline (reference CPU path, {threads} threads) ...")
+        log(f"C2 CPU baseline (reference CPU path, {threads} threads) ...")
         pc, ptrc = c2["pos"], c2["ptr"]
         kc = torch.full((c2["B"],), c2["M"], dtype=torch.int64)
         runs = []
@@ -528,18 +428,411 @@ def main() -> int:
             t0 = time.perf_counter()
             ref_cpu_path.fps(pc, ptrc, kc)
             t1 = time.perf_counter()
-            ref_cpu_path.radius_graph(pc, c2["r"], c2["B"], c2["K"])
+            rr, rc = ref_cpu_path.radius_graph(pc, c2["r"], c2["B"], c2["K"])
             t2 = time.perf_counter()
             runs.append((t2 - t0, t1 - t0, t2 - t1))
         tot, t_fps, t_rad = sorted(runs)[1]
-        per_batch_ms = tot * 1e3
-        cpu = {"value": round(per_batch_ms, 1), "unit": "ms/batch", "cores": threads,
-               "kind": "port",
+        cpu = {"value": round(tot * 1e3, 1), "unit": "ms/batch", "cores": threads, "kind": "port",
                "sample": f"reference CPU path (iterative FPS + batched cdist/topk radius graph, "
                          f"oracle/ref_cpu_path.py) on the full C2 batch, median of 3; fps "
                          f"{t_fps:.2f} s, radius {t_rad:.2f} s",
                "cpu_model": _cpu_model()}
-        log(f"  CPU: {per_batch_ms:.0f} ms/batch")
+        log(f"  CPU: {tot * 1e3:.0f} ms/batch")
+        # the survey's D3 diagnostic on the real batch: edges of the exact semantics (this GPU
+        # output) that the reference's cdist path does not produce, and the reverse
+        n = pos.shape[0]
+        mine = _pair_keys(row.cpu().numpy(), col.cpu().numpy(), n)
+        theirs = _pair_keys(rr.numpy(), rc.numpy(), n)
+        diff = np.setxor1d(mine, theirs)
+        p64 = c2["pos"].double().numpy()
+        r2 = float(np.float32(c2["r"] * c2["r"]))
+        rel = [abs(((p64[k // n] - p64[k % n]) ** 2).sum() - r2) / r2 for k in diff.tolist()]
+        leg["cdist_disagreement"] = {"directed_edges": int(diff.size),
+                                     "max_rel_dist_from_r2": float(max(rel)) if rel else 0.0}
+        log(f"  cdist-path disagreement: {diff.size} directed edges of {row.numel()}")
+    return ms_step, leg, cpu
+
+
+def leg_c3(args, dev) -> tuple:
+    """Segment reduce on C3: the roofline kernel (fp32 sum) and every other leg, the CSR build,
+    and the CPU baseline of the reference's loop."""
+    _, _, _, segment_reduce, sort_and_build_csr = _ops()
+    from gdl_amd.csrc import segment_reduce_backward_hip, segment_reduce_forward_hip
+    log("C3: segment reduce ...")
+    off = make_c3_offsets()
+    S, E, C = off.shape[0] - 1, int(off[-1]), 128
+    ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
+    ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
+    col_sorted = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32),
+                                         (ne - ns).long())
+    perm = torch.arange(E, device=dev, dtype=torch.int32)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    msg = torch.randn(E, C, device=dev, generator=gen)
+    bytes_fwd = E * C * 4 + S * C * 4 + (S + 1) * 4
+    iters = args.iters
+    leg: dict = {}
+    roof = None
+    if args.only in (None, "c3"):
+        ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
+        gbs = bytes_fwd / (ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_SUM_TRAFFIC_BYTES,
+                "kernel": "seg_fwd_merge_kernel<float,16,SUM,perm>", "ms_per_launch": round(ms, 4),
+                "algorithmic_bytes": bytes_fwd}
+        leg["sum_fp32_ms"] = round(ms, 4)
+        log(f"  fwd sum fp32: {ms:.4f} ms  {gbs:.0f} GB/s  ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+        for red in ("mean", "max"):
+            extra = S * C * 4 if red == "max" else 0
+            msr = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S, reduce=red),
+                           iters, 5)
+            leg[f"{red}_fp32_ms"] = round(msr, 4)
+            leg[f"{red}_fp32_gbs"] = round((bytes_fwd + extra) / (msr * 1e-3) / 1e9, 1)
+            log(f"  fwd {red} fp32: {msr:.4f} ms  {leg[f'{red}_fp32_gbs']} GB/s")
+    if args.only in (None, "c3bf16"):
+        mb = msg.bfloat16()
+        bytes_b = E * C * 2 + S * C * 2 + (S + 1) * 4
+        msb = event_ms(lambda: segment_reduce(mb, col_sorted, perm, ns, ne, S), iters, 5)
+        leg["sum_bf16_ms"] = round(msb, 4)
+        leg["sum_bf16_gbs"] = round(bytes_b / (msb * 1e-3) / 1e9, 1)
+        log(f"  fwd sum bf16: {msb:.4f} ms  {leg['sum_bf16_gbs']} GB/s")
+        del mb
+    if args.only in (None, "c3bwd"):
+        grad = torch.randn(S, C, device=dev, generator=gen)
+        bytes_bwd = S * C * 4 + E * C * 4 + (S + 1) * 4
+        for red in ("sum", "mean"):
+            msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, red),
+                           iters, 5)
+            leg[f"bwd_{red}_fp32_gbs"] = round(bytes_bwd / (msb * 1e-3) / 1e9, 1)
+            log(f"  bwd {red} fp32: {msb:.4f} ms  {leg[f'bwd_{red}_fp32_gbs']} GB/s")
+        out, arg = segment_reduce_forward_hip(msg, perm, ns, ne, S, "max")
+        msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, "max",
+                                                           msg=msg, out=out, arg=arg), iters, 5)
+        leg["bwd_max_fp32_gbs"] = round((bytes_bwd + S * C * 4) / (msb * 1e-3) / 1e9, 1)
+        log(f"  bwd max fp32: {msb:.4f} ms  {leg['bwd_max_fp32_gbs']} GB/s")
+        del out, arg, grad
+    col64 = col_sorted.long()
+    leg["csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col64, S), 10, 2), 4)
+    # the same targets in random order (the sorted-input identity path does not apply)
+    col_sh = col64[torch.randperm(E, device=dev, generator=gen)]
+    leg["csr_build_shuffled_ms"] = round(wall_ms(lambda: sort_and_build_csr(col_sh, S), 10, 2), 4)
+    log(f"  CSR build: {leg['csr_build_ms']} ms sorted, {leg['csr_build_shuffled_ms']} ms shuffled")
+    del col_sh, msg
+    if not args.no_cpu and args.only is None:
+        from oracle import ref_cpu_path
+        # the reference's CPU path: argsort + bincount CSR of all E targets, then its Python loop
+        # over segments (two .item() per segment) on a sample of 32,768 of the 262,144 segments
+        # (rows for those segments only), extrapolated linearly to S
+        sample = 32768
+        col_cpu = col64.cpu()
+        t_csr = cpu_ms(lambda: ref_cpu_path.sort_and_build_csr(col_cpu, S), 1)
+        rows = int(off[sample])
+        msg_cpu = torch.randn(rows, C, generator=torch.Generator().manual_seed(0))
+        perm_cpu = torch.arange(rows, dtype=torch.int32)
+        t_loop = cpu_ms(lambda: ref_cpu_path.segment_sum(
+            msg_cpu, perm_cpu, torch.from_numpy(off[:sample].astype(np.int32)),
+            torch.from_numpy(off[1:sample + 1].astype(np.int32)), sample), 1)
+        total = t_csr + t_loop * S / sample
+        leg["cpu"] = _cpu_entry(total, "ms/call", (
+            f"reference CPU path: sort_and_build_csr (argsort + bincount) of all {E} targets "
+            f"{t_csr:.0f} ms + the per-segment loop of segment_reduce on {sample} of {S} segments "
+            f"({rows} rows) {t_loop:.0f} ms, extrapolated x{S / sample:.0f}"))
+        log(f"  CPU: {total:.0f} ms (extrapolated)")
+    return roof, leg
+
+
+def leg_c1(args, dev) -> dict:
+    """C1: FPS 2048 -> 512, radius graph over the centres, CSR, segment sum of C = 32 features
+    gathered along the edges."""
+    fps, _, radius_graph, segment_reduce, sort_and_build_csr = _ops()
+    c1 = make_c1()
+    p1 = c1["pos"].to(dev)
+    f1 = c1["feat"].to(dev)
+
+    def c1_step():
+        i = fps(p1, c1["M"])
+        cen = p1[i]
+        row, col = radius_graph(cen, c1["r"], max_num_neighbors=c1["K"])
+        cs, pm, a, b = sort_and_build_csr(col, c1["M"])
+        return segment_reduce(f1[row], cs, pm, a, b, c1["M"])
+
+    leg = {"step_ms": round(wall_ms(c1_step, 20, 3), 4)}
+    leg["fps_ms"] = round(wall_ms(lambda: fps(p1, c1["M"]), 20, 3), 4)
+    log(f"C1: step {leg['step_ms']} ms (fps {leg['fps_ms']} ms)")
+    if not args.no_cpu:
+        from oracle import ref_cpu_path
+        pc, fc = c1["pos"], c1["feat"]
+
+        def cpu_step():
+            i = ref_cpu_path.fps(pc, torch.tensor([0, 2048]), torch.tensor([c1["M"]]))
+            row, col = ref_cpu_path.radius_graph(pc[i], c1["r"], 1, c1["K"])
+            cs, pm, a, b = ref_cpu_path.sort_and_build_csr(col, c1["M"])
+            return ref_cpu_path.segment_sum(fc[row], pm, a, b, c1["M"])
+
+        leg["cpu"] = _cpu_entry(cpu_ms(cpu_step, 3), "ms/step",
+                                "reference CPU path (iterative FPS, cdist radius graph, argsort "
+                                "CSR, per-segment loop) on the full C1 step, median of 3")
+        log(f"  CPU: {leg['cpu']['value']} ms")
+    return leg
+
+
+def leg_c4(args, dev) -> dict:
+    """C4: 32 superquadrics, FPS 2048 -> 512 -> 128, radius graphs r = 0.2 / 0.4 (K = 64), and
+    max + mean pooling of N(0, 1) features (C = 64 / 128) gathered along the edges."""
+    fps, _, radius_graph, segment_reduce, sort_and_build_csr = _ops()
+    c4 = make_c4()
+    p4, ptr4 = c4["pos"].to(dev), c4["ptr"].to(dev)
+    B = c4["B"]
+    g = torch.Generator(device=dev).manual_seed(4)
+    f1 = torch.randn(B * 512, 64, device=dev, generator=g)
+    f2 = torch.randn(B * 128, 128, device=dev, generator=g)
+    ptr1 = torch.arange(B + 1, device=dev, dtype=torch.int64) * 512
+
+    def c4_step():
+        i1 = fps(p4, 512, ptr=ptr4)
+        q1 = p4[i1]
+        i2 = fps(q1, 128, ptr=ptr1)
+        q2 = q1[i2]
+        outs = []
+        for pts, r, f in ((q1, 0.2, f1), (q2, 0.4, f2)):
+            row, col = radius_graph(pts, r, max_num_neighbors=64, num_batch_elements=B)
+            cs, pm, a, b = sort_and_build_csr(col, pts.shape[0])
+            msg = f[row]
+            outs.append(segment_reduce(msg, cs, pm, a, b, pts.shape[0], reduce="max"))
+            outs.append(segment_reduce(msg, cs, pm, a, b, pts.shape[0], reduce="mean"))
+        return outs
+
+    leg = {"step_ms": round(wall_ms(c4_step, 10, 2), 4)}
+    log(f"C4: step {leg['step_ms']} ms")
+    if not args.no_cpu:
+        from oracle import ref_cpu_path
+        pc, ptrc = c4["pos"], c4["ptr"]
+        f1c, f2c = f1.cpu(), f2.cpu()
+
+        def cpu_step():
+            i1 = ref_cpu_path.fps(pc, ptrc, torch.full((B,), 512))
+            q1 = pc[i1]
+            i2 = ref_cpu_path.fps(q1, torch.arange(B + 1) * 512, torch.full((B,), 128))
+            q2 = q1[i2]
+            for pts, r, f in ((q1, 0.2, f1c), (q2, 0.4, f2c)):
+                row, col = ref_cpu_path.radius_graph(pts, r, B, 64)
+                msg = f[row]
+                ref_cpu_path.segment_max(msg, col, pts.shape[0])
+                ref_cpu_path.segment_mean(msg, col, pts.shape[0])
+
+        leg["cpu"] = _cpu_entry(cpu_ms(cpu_step, 3), "ms/step",
+                                "reference CPU path (iterative FPS at both levels, batched cdist "
+                                "radius graphs, scatter max / mean pooling) on the full C4 step, "
+                                "median of 3")
+        log(f"  CPU: {leg['cpu']['value']} ms")
+    return leg
+
+
+def leg_c5(args, dev) -> dict:
+    """C5: one 131,072-point lidar frame: FPS to 16,384, radius graph r = 0.5 (K = 64) over the
+    centres (empty: the centres lie about a metre apart) and over all points (5.3 M edges),
+    KNN k = 8 from the centres, segment sum of C = 32 features over the all-points graph."""
+    fps, knn, radius_graph, segment_reduce, sort_and_build_csr = _ops()
+    c5 = make_c5()
+    p5 = c5["pos"].to(dev)
+    N, M = p5.shape[0], c5["M"]
+    leg = {"fps_ms": round(wall_ms(lambda: fps(p5, M), 3, 1), 3)}
+    i5 = fps(p5, M)
+    cen5 = p5[i5]
+    leg["radius_centres_ms"] = round(wall_ms(
+        lambda: radius_graph(cen5, c5["r"], max_num_neighbors=c5["K"]), 10, 2), 4)
+    leg["radius_all_points_ms"] = round(wall_ms(
+        lambda: radius_graph(p5, c5["r"], max_num_neighbors=c5["K"]), 10, 2), 4)
+    row, col = radius_graph(p5, c5["r"], max_num_neighbors=c5["K"])
+    leg["edges_all_points"] = int(row.numel())
+    pq = torch.tensor([0, M], device=dev, dtype=torch.int64)
+    ps = torch.tensor([0, N], device=dev, dtype=torch.int64)
+    leg["knn_k8_ms"] = round(wall_ms(lambda: knn(cen5, p5, pq, ps, c5["k"]), 10, 2), 4)
+    cs, pm, a, b = sort_and_build_csr(col, N)
+    feat = torch.randn(N, c5["C"], device=dev, generator=torch.Generator(device=dev).manual_seed(5))
+    msg = feat[row]
+    E = msg.shape[0]
+    ms = event_ms(lambda: segment_reduce(msg, cs, pm, a, b, N), args.iters, 3)
+    leg["segsum_all_points_ms"] = round(ms, 4)
+    leg["segsum_all_points_gbs"] = round((E * c5["C"] * 4 + N * c5["C"] * 4 + (N + 1) * 4 + E * 4)
+                                         / (ms * 1e-3) / 1e9, 1)
+    leg["frame_ms"] = round(leg["fps_ms"] + leg["radius_all_points_ms"] + leg["knn_k8_ms"] + ms, 3)
+    log(f"C5: fps {leg['fps_ms']} ms, radius centres {leg['radius_centres_ms']} ms, all points "
+        f"{leg['radius_all_points_ms']} ms ({E} edges), knn {leg['knn_k8_ms']} ms, segment sum "
+        f"{ms:.4f} ms ({leg['segsum_all_points_gbs']} GB/s)")
+    del msg
+    if not args.no_cpu:
+        from oracle import ref_cpu_path
+        pc = c5["pos"]
+        # FPS: the reference's Python loop for the first 512 of 16,384 steps (each step costs the
+        # same: one pass over all 131,072 points), extrapolated x32; KNN: the brute force over
+        # 256 of the 16,384 queries ([256, 131072, 3] difference tensor; the full one would be
+        # 25.8 GB), extrapolated x64; the all-points radius graph: the cdist rows of 2,048 of
+        # the 131,072 targets ([2048, 131072] distances; the full [N, N] matrix would be 68.7
+        # GB), extrapolated x64
+        steps = 512
+        t_fps = cpu_ms(lambda: ref_cpu_path.fps(pc, torch.tensor([0, N]), torch.tensor([M]),
+                                                max_steps=steps), 1)
+        cen_c = cen5.cpu()
+        nq = 256
+        t_knn = cpu_ms(lambda: ref_cpu_path.knn(cen_c[:nq], pc, torch.tensor([0, nq]),
+                                                torch.tensor([0, N]), c5["k"]), 1)
+        nt = 2048
+        r2 = c5["r"] * c5["r"]
+
+        def radius_rows():
+            d2 = torch.cdist(pc[:nt], pc).pow(2)
+            d2.masked_fill_(d2 >= r2, float("inf"))
+            vals, src = d2.topk(c5["K"], dim=1, largest=False)
+            return src[vals < float("inf")]
+
+        t_rad = cpu_ms(radius_rows, 1)
+        total = t_fps * M / steps + t_knn * M / nq + t_rad * N / nt
+        leg["cpu"] = _cpu_entry(total, "ms/frame", (
+            f"reference CPU path, extrapolated from samples: FPS loop {steps} of {M} steps "
+            f"{t_fps:.0f} ms (x{M // steps}), brute-force KNN {nq} of {M} queries {t_knn:.0f} ms "
+            f"(x{M // nq}), cdist radius rows of {nt} of {N} targets {t_rad:.0f} ms (x{N // nt})"))
+        log(f"  CPU: {total:.0f} ms/frame (extrapolated)")
+    return leg
+
+
+# ═══════════════════════════════════════════════════════════════════
+# Single-kernel legs for counter collection (rocprofv3 --pmc)
+# ═══════════════════════════════════════════════════════════════════
+
+PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "c3max", "c3sum_bf16",
+                "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2")
+
+
+def profile_leg(name: str, args, dev) -> dict:
+    """Runs one op of one configuration ``args.iters`` times after one warm-up call, so that a
+    counter run (rocprofv3 --pmc) sees a few dispatches of that kernel and little else."""
+    fps, knn, radius_graph, segment_reduce, sort_and_build_csr = _ops()
+    if name.endswith("c2") or name in ("softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2"):
+        c2 = make_c2()
+        pos, ptr, batch = c2["pos"].to(dev), c2["ptr"].to(dev), c2["batch"].to(dev)
+    if name == "fps_c2":
+        fn = lambda: fps(pos, c2["M"], ptr=ptr)  # noqa: E731
+    elif name == "radius_c2":
+        fn = lambda: radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,  # noqa: E731
+                                  num_batch_elements=c2["B"])
+    elif name == "knn_c2":
+        cent = pos[fps(pos, c2["M"], ptr=ptr)]
+        ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
+        fn = lambda: knn(cent, pos, ptr_q, ptr, c2["k"])  # noqa: E731
+    elif name in ("fps_c5", "knn_c5"):
+        c5 = make_c5()
+        p5 = c5["pos"].to(dev)
+        if name == "fps_c5":
+            fn = lambda: fps(p5, c5["M"])  # noqa: E731
+        else:
+            cen = p5[fps(p5, c5["M"])]
+            pq = torch.tensor([0, c5["M"]], device=dev)
+            ps = torch.tensor([0, p5.shape[0]], device=dev)
+            fn = lambda: knn(cen, p5, pq, ps, c5["k"])  # noqa: E731
+    elif name in ("c3max", "c3sum_bf16"):
+        off = make_c3_offsets()
+        S, E, C = off.shape[0] - 1, int(off[-1]), 128
+        ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
+        ne = torch.from_numpy(off[1:].astype(np.int32)).to(dev)
+        cs = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32), (ne - ns).long())
+        perm = torch.arange(E, device=dev, dtype=torch.int32)
+        msg = torch.randn(E, C, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
+        if name == "c3max":
+            fn = lambda: segment_reduce(msg, cs, perm, ns, ne, S, reduce="max")  # noqa: E731
+        else:
+            mb = msg.bfloat16()
+            del msg
+            fn = lambda: segment_reduce(mb, cs, perm, ns, ne, S)  # noqa: E731
+    elif name in ("softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2"):
+        from gdl_amd.graph import SpatialGraph
+        gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                num_batch_elements=c2["B"])
+        if name == "softmax_c2":
+            from gdl_amd.functional.segment_softmax import segment_softmax
+            scores = torch.randn(gr.E, 4, device=dev)
+            fn = lambda: segment_softmax(scores, None, gr.node_start, gr.node_end, gr.N,  # noqa: E731
+                                         contiguous_csr=True)
+        elif name == "gather_c2":
+            from gdl_amd.functional.gather import knn_interpolate
+            cent = pos[fps(pos, c2["M"], ptr=ptr)]
+            ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
+            ii, dd = knn(pos, cent, ptr, ptr_q, 3)
+            feats = torch.randn(cent.shape[0], 112, device=dev)
+            fn = lambda: knn_interpolate(feats, ii, dd)  # noqa: E731
+        else:
+            from gdl_amd.se3_conv import SE3Conv
+            torch.manual_seed(0)
+            conv = SE3Conv(64, 16, 64, 16, radius=c2["r"]).to(dev)
+            fs = torch.randn(gr.N, 64, device=dev)
+            fv = torch.randn(gr.N, 16, 3, device=dev)
+            if name == "radial_c2":
+                fn = lambda: conv.radial_basis(gr.dist)  # noqa: E731
+            else:
+                def fn():
+                    with torch.no_grad():
+                        return conv(fs, fv, gr)
+    else:
+        raise SystemExit(f"unknown leg {name!r}; profile legs: {', '.join(PROFILE_LEGS)}")
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.iters):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.iters
+    log(f"{name}: {ms:.4f} ms per call over {args.iters} calls")
+    return {"leg": name, "ms_per_call": round(ms, 4), "calls": args.iters}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only", default=None,
+                    help="run one leg: c2 | c3 | c3bf16 | c3bwd | copy (HBM counter calibration) "
+                         f"| one of the single-kernel profiling legs: {', '.join(PROFILE_LEGS)}")
+    ap.add_argument("--iters", type=int, default=50, help="timed launches per kernel leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py measures one GPU: this build has no multi-GPU path (each op's work is a "
+            "single-GPU kernel; see DESIGN.md for how it would shard). Run with --gpus 1.")
+        return 2
+    if not torch.cuda.is_available():
+        log("bench.py needs a GPU")
+        return 2
+
+    from gdl_amd import _native
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.only in PROFILE_LEGS:
+        print(json.dumps(profile_leg(args.only, args, dev)), flush=True)
+        return 0
+    if args.only == "copy":
+        # A plain elementwise pass over 1 GiB (read 1 GiB, write 1 GiB with 16-byte vector
+        # accesses): the reference point that scales rocprofv3's FETCH_SIZE / WRITE_SIZE.
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = event_ms(lambda: torch.add(src, 1.0, out=dst), args.iters, 3)
+        gbs = 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
+        log(f"  copy 1 GiB: {ms:.4f} ms  {gbs:.1f} GB/s")
+        print(json.dumps({"leg": "copy", "ms": round(ms, 4), "gbs": round(gbs, 1)}), flush=True)
+        return 0
+
+    legs: dict = {}
+    ms_step = cpu = roof = None
+    if args.only in (None, "c2"):
+        ms_step, legs["c2"], cpu = leg_c2(args, dev)
+    if args.only in (None, "c3", "c3bf16", "c3bwd"):
+        roof, legs["c3"] = leg_c3(args, dev)
+    if args.only is None:
+        legs["c1"] = leg_c1(args, dev)
+        legs["c4"] = leg_c4(args, dev)
+        legs["c5"] = leg_c5(args, dev)
 
     result = {
         "metric": METRIC,
@@ -549,6 +842,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4) if ms_step is not None else None,
+        "ms_per_step_one_stream": legs.get("c2", {}).get("step_one_stream_ms"),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -567,6 +861,9 @@ def main() -> int:
         "library": _native.build_info(),
         "device": torch.cuda.get_device_name(dev),
     }
+    if ms_step is not None:
+        log(f"headline: {ms_step:.4f} ms/batch (two streams), "
+            f"{result['ms_per_step_one_stream']} ms/batch on one stream")
     print(json.dumps(result), flush=True)
     return 0
 

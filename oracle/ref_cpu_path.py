@@ -13,6 +13,8 @@ is what a user of the reference pays on the CPU:
 * ``sort_and_build_csr`` / ``segment_sum`` — _sort_and_build_csr_pytorch and
                        _segment_reduce_pytorch, geoembodied/functional/segment_reduce.py:77-199:
                        argsort + bincount/cumsum, then a Python loop over segments.
+* ``segment_mean`` / ``segment_max`` — the pooling scatters, nn/modules/se3_net.py:226-270 and
+                       nn/modules/invariant_attention.py:212-219.
 * ``idw_interpolate`` — the interpolation layer's IDW weights and neighbourhood sum,
                        geoembodied/nn/modules/equivariant_interp.py:95-125.
 * ``sparse_softmax`` — _sparse_softmax, geoembodied/nn/modules/invariant_attention.py:202-230:
@@ -28,7 +30,8 @@ import torch
 from torch import Tensor
 
 
-def fps(pos: Tensor, ptr: Tensor, k_per_batch: Tensor) -> Tensor:
+def fps(pos: Tensor, ptr: Tensor, k_per_batch: Tensor, max_steps: int | None = None) -> Tensor:
+    """``max_steps`` stops each cloud's loop early (a bounded timing sample)."""
     picks = []
     for b in range(ptr.shape[0] - 1):
         lo, hi = int(ptr[b]), int(ptr[b + 1])
@@ -42,7 +45,7 @@ def fps(pos: Tensor, ptr: Tensor, k_per_batch: Tensor) -> Tensor:
         cloud = pos[lo:hi]
         chosen = torch.zeros(k, dtype=torch.long)
         nearest = torch.full((n,), float("inf"))
-        for step in range(k):
+        for step in range(k if max_steps is None else min(k, max_steps)):
             centre = cloud[chosen[step]]
             d = (cloud - centre.unsqueeze(0)).pow(2).sum(-1)
             nearest = torch.minimum(nearest, d)
@@ -104,6 +107,22 @@ def segment_sum(msg: Tensor, perm: Tensor, node_start: Tensor, node_end: Tensor,
         if a < b:
             out[n] = msg[perm[a:b].long()].sum(dim=0)
     return out
+
+
+def segment_mean(msg: Tensor, col: Tensor, N: int) -> Tensor:
+    """global_mean_pool's scatter formulation, geoembodied/nn/modules/se3_net.py:226-270:
+    scatter_add of the rows, divided by bincount clamped at 1."""
+    out = torch.zeros(N, msg.shape[1], dtype=msg.dtype)
+    out.scatter_add_(0, col.unsqueeze(1).expand_as(msg), msg)
+    return out / torch.bincount(col, minlength=N).clamp(min=1).unsqueeze(1).to(msg.dtype)
+
+
+def segment_max(msg: Tensor, col: Tensor, N: int) -> Tensor:
+    """scatter_reduce 'amax' into zeros with include_self=False,
+    geoembodied/nn/modules/invariant_attention.py:212-219."""
+    out = torch.zeros(N, msg.shape[1], dtype=msg.dtype)
+    return out.scatter_reduce_(0, col.unsqueeze(1).expand_as(msg), msg, reduce="amax",
+                               include_self=False)
 
 
 def sparse_softmax(scores: Tensor, index: Tensor, num_nodes: int) -> Tensor:

@@ -239,6 +239,34 @@ def test_radius_vs_reference_cpu_path():
         assert abs(((x64[i] - x64[j]) ** 2).sum() - 0.0625) < 3e-2 * 0.0625
 
 
+def test_c2_disagreement_with_reference_cdist_path():
+    """The survey's D3 diagnostic on the real C2 batch (16 x 4096 points, r = 0.1, K = 32): the
+    exact edge set against the reference's cdist/topk CPU path (radius_graph.py:204-275).  They
+    differ only in pairs whose exact squared distance lies within cdist's rounding band of r2:
+    cdist forms |x|^2 + |y|^2 - 2 x.y in fp32, so its error is a few ulps of |x|^2 + |y|^2
+    (bound used: 4 * 2^-24 * (|x_i|^2 + |x_j|^2)).  On this batch: 4 directed edges (2 pairs)
+    of 657,154."""
+    import bench
+    c = bench.make_c2()
+    x = c["pos"]
+    rr, rc = ref_cpu_path.radius_graph(x, c["r"], c["B"], c["K"])
+    orow, ocol = oracle.radius_graph(x.numpy(), c["r"], c["K"], batch=c["batch"].numpy(),
+                                     num_batch_elements=c["B"])
+    a = set(zip(rr.tolist(), rc.tolist()))
+    b = set(zip(orow.tolist(), ocol.tolist()))
+    assert len(b) == 657_154
+    diff = a ^ b
+    x64 = x.double().numpy()
+    r2 = oracle.fp32_radius_sq(c["r"])
+    for i, j in diff:
+        d = ((x64[i] - x64[j]) ** 2).sum()
+        band = 4 * 2.0 ** -24 * ((x64[i] ** 2).sum() + (x64[j] ** 2).sum())
+        assert abs(d - r2) <= band, (i, j, d)
+        assert ((i, j) in b) == (d < r2)        # the exact set is on the right side of r2
+    print(f"C2 disagreement with the cdist path: {len(diff)} directed edges of {len(b)}")
+    assert len(diff) == 4
+
+
 # ---------------------------------------------------------------------------- CSR build ---
 
 @pytest.mark.parametrize("E,N", [(0, 5), (1, 1), (1000, 17), (5000, 4000)])
