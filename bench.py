@@ -699,8 +699,8 @@ def leg_c5(args, dev) -> dict:
 # Single-kernel legs for counter collection (rocprofv3 --pmc)
 # ═══════════════════════════════════════════════════════════════════
 
-PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "c3max", "c3sum_bf16",
-                "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2")
+PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "radius_c5_all", "c3sum",
+                "c3max", "c3sum_bf16", "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2")
 
 
 def profile_leg(name: str, args, dev) -> dict:
@@ -719,17 +719,19 @@ def profile_leg(name: str, args, dev) -> dict:
         cent = pos[fps(pos, c2["M"], ptr=ptr)]
         ptr_q = torch.arange(c2["B"] + 1, device=dev, dtype=torch.int64) * c2["M"]
         fn = lambda: knn(cent, pos, ptr_q, ptr, c2["k"])  # noqa: E731
-    elif name in ("fps_c5", "knn_c5"):
+    elif name in ("fps_c5", "knn_c5", "radius_c5_all"):
         c5 = make_c5()
         p5 = c5["pos"].to(dev)
         if name == "fps_c5":
             fn = lambda: fps(p5, c5["M"])  # noqa: E731
+        elif name == "radius_c5_all":
+            fn = lambda: radius_graph(p5, c5["r"], max_num_neighbors=c5["K"])  # noqa: E731
         else:
             cen = p5[fps(p5, c5["M"])]
             pq = torch.tensor([0, c5["M"]], device=dev)
             ps = torch.tensor([0, p5.shape[0]], device=dev)
             fn = lambda: knn(cen, p5, pq, ps, c5["k"])  # noqa: E731
-    elif name in ("c3max", "c3sum_bf16"):
+    elif name in ("c3sum", "c3max", "c3sum_bf16"):
         off = make_c3_offsets()
         S, E, C = off.shape[0] - 1, int(off[-1]), 128
         ns = torch.from_numpy(off[:-1].astype(np.int32)).to(dev)
@@ -737,7 +739,9 @@ def profile_leg(name: str, args, dev) -> dict:
         cs = torch.repeat_interleave(torch.arange(S, device=dev, dtype=torch.int32), (ne - ns).long())
         perm = torch.arange(E, device=dev, dtype=torch.int32)
         msg = torch.randn(E, C, device=dev, generator=torch.Generator(device=dev).manual_seed(0))
-        if name == "c3max":
+        if name == "c3sum":
+            fn = lambda: segment_reduce(msg, cs, perm, ns, ne, S)  # noqa: E731
+        elif name == "c3max":
             fn = lambda: segment_reduce(msg, cs, perm, ns, ne, S, reduce="max")  # noqa: E731
         else:
             mb = msg.bfloat16()

@@ -19,8 +19,9 @@
 //   scan        row_ptr = exclusive scan of min(count, K) over target index
 // geo_radius_emit:
 //   rg_compact  kRgGroup lanes per target: the list sorted by source index into the CSR row;
-//               a target with more than K sources first rebuilds its list with the K smallest
-//               (d, j), found by a bitwise threshold search
+//               targets with more than K sources (or long lists) are done by the whole wave:
+//               the K smallest (d, j) by a binary search on the distance bits over the
+//               in-radius candidates held in LDS
 //   rg_emit     (lists too large for the workspace) re-scans the stencil per target instead
 // Traversal order inside a cell is not deterministic (atomic ranks) and does not matter: the
 // accepted set is defined by a total order and the output is sorted.
@@ -477,9 +478,152 @@ __global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __
 // The collected list is unsorted (traversal order); each source goes to position
 // row_ptr[i] + (number of smaller sources in the list), with the list held in the group's
 // registers (kRgSlots entries per lane) and compared through lane shuffles.  Targets with more
-// than K sources (rebuilt with the exact (d, j) threshold) or lists longer than the registers
-// hold are done by the group's first lane from the list in memory.
+// than K sources, or lists longer than the registers hold, are done afterwards by the whole
+// wave, one at a time (rg_wave_target).
 constexpr int kRgSlots = 8;
+// In-radius candidates of one target whose distance bits a wave keeps in LDS for the selection.
+constexpr int kRgSelCap = 1024;
+
+__device__ __forceinline__ void wave_lds_fence() {
+  // LDS writes of some lanes become visible to later reads of other lanes of the same wave
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// The 9 z-contiguous runs of the 3x3x3 stencil around (qx, qy, qz): start and length.
+__device__ __forceinline__ void stencil_runs(const RgWs& w, const Grid& g, float qx, float qy,
+                                             float qz, int (&ra)[9], int (&rn)[9]) {
+  const int cx = cell_coord(qx, g.ox, g.inv_h, g.dx);
+  const int cy = cell_coord(qy, g.oy, g.inv_h, g.dy);
+  const int cz = cell_coord(qz, g.oz, g.inv_h, g.dz);
+  const int z0 = cz > 0 ? cz - 1 : 0;
+  const int z1 = cz + 1 < g.dz ? cz + 1 : g.dz - 1;
+#pragma unroll
+  for (int r = 0; r < 9; ++r) {
+    const int ix = cx - 1 + r / 3, iy = cy - 1 + r % 3;
+    const bool in = ix >= 0 && ix < g.dx && iy >= 0 && iy < g.dy;
+    const int c0 = g.base + (ix * g.dy + iy) * g.dz;
+    ra[r] = in ? w.cell_start[c0 + z0] : 0;
+    rn[r] = in ? w.cell_start[c0 + z1 + 1] - ra[r] : 0;
+  }
+}
+
+// Calls f(d, j, ok) for every source of the stencil runs, 64 at a time across the wave (every
+// lane calls f the same number of times; ok marks a real candidate).
+template <typename F>
+__device__ __forceinline__ void wave_scan_runs(const RgWs& w, const int (&ra)[9], const int (&rn)[9],
+                                               float qx, float qy, float qz, F&& f) {
+  const int lane = lane_id();
+  for (int r = 0; r < 9; ++r) {
+    for (int b0 = 0; b0 < rn[r]; b0 += kWave) {  // wave-uniform trip count
+      const bool ok = b0 + lane < rn[r];
+      const float4 s = ok ? w.spos[ra[r] + b0 + lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+      f(sqdist(qx, qy, qz, s.x, s.y, s.z), __float_as_int(s.w), ok);
+    }
+  }
+}
+
+// One target done by the whole wave: c = its count of in-radius sources (c > 0).
+//  c <= K: the list L[0..c) (complete) sorted by index, 64 entries per step.
+//  c > K:  the K smallest (d, j): the in-radius distance bits collected in LDS (c <= kRgSelCap;
+//          beyond that each count re-scans the stencil), the K-th distance d* by binary search
+//          on the bits, the index threshold j* among the sources at d* when they are more than
+//          needed (re-scans), the accepted sources compacted and sorted by index.
+__device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
+                               const int64_t* __restrict__ batch, int64_t B, int64_t ppc, float r2,
+                               int K, bool lp, int64_t i, int c,
+                               const int64_t* __restrict__ row_ptr, int64_t* __restrict__ row_out,
+                               int64_t* __restrict__ col_out, uint32_t* __restrict__ key) {
+  const int lane = lane_id();
+  const int64_t o = row_ptr[i];
+  int32_t* L = w.list + i * K;
+  int32_t* acc = reinterpret_cast<int32_t*>(key);  // accepted sources (LDS) when K <= cap
+  if (c > K) {
+    const int b = cloud_of(i, batch, B, ppc);
+    const Grid g = w.grid[b];
+    const float qx = x[3 * i], qy = x[3 * i + 1], qz = x[3 * i + 2];
+    const int qi = static_cast<int>(i);
+    int ra[9], rn[9];
+    stencil_runs(w, g, qx, qy, qz, ra, rn);
+    const bool inl = c <= kRgSelCap;
+    int n = 0;
+    if (inl) {  // stage A: in-radius distance bits into LDS (wave compaction)
+      wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
+        const bool a = ok && (lp || j != qi) && d < r2;
+        const uint64_t m = __ballot(a);
+        const int slot = n + static_cast<int>(__popcll(m & lanemask_lt()));
+        if (a && slot < kRgSelCap) key[slot] = __float_as_uint(d);
+        n += static_cast<int>(__popcll(m));
+      });
+      n = n < kRgSelCap ? n : kRgSelCap;
+      wave_lds_fence();
+    }
+    // count of in-radius sources with (bits, j) <= (dmax, jmax) (j ignored when jmax < 0)
+    auto count_le = [&](uint32_t dmax, bool strict, int jeq_max) -> int {
+      int t = 0;
+      if (inl && jeq_max < 0) {
+        for (int m = lane; m < n; m += kWave) t += strict ? key[m] < dmax : key[m] <= dmax;
+      } else {
+        wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
+          const uint32_t db = __float_as_uint(d);
+          const bool a = ok && (lp || j != qi) && d < r2;
+          t += a && (jeq_max < 0 ? (strict ? db < dmax : db <= dmax) : (db == dmax && j <= jeq_max));
+        });
+      }
+      return wave_sum(t);
+    };
+    // stage B: the K-th smallest distance bits (every in-radius d has bits < bits(r2))
+    uint32_t lo = 0, hi = __float_as_uint(r2) - 1u;
+    while (lo < hi) {
+      const uint32_t mid = lo + ((hi - lo) >> 1);
+      if (count_le(mid, false, -1) >= K) hi = mid; else lo = mid + 1u;
+    }
+    const uint32_t dstar = lo;
+    // stage C: index threshold among the sources at d* when they are more than needed
+    const int less = count_le(dstar, true, -1);
+    const int need = K - less;
+    const int at = count_le(dstar, false, -1) - less;
+    int jstar = 0x7fffffff;
+    if (at > need) {
+      int jlo = 0, jhi = 0x7ffffffe;
+      while (jlo < jhi) {
+        const int mid = jlo + ((jhi - jlo) >> 1);
+        if (count_le(dstar, false, mid) >= need) jhi = mid; else jlo = mid + 1;
+      }
+      jstar = jlo;
+    }
+    // stage D: the K accepted sources, compacted into LDS (or the list when K exceeds it)
+    int32_t* dst = K <= kRgSelCap ? acc : L;
+    wave_lds_fence();
+    int m0 = 0;
+    wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
+      const uint32_t db = __float_as_uint(d);
+      const bool a = ok && (lp || j != qi) && d < r2 && (db < dstar || (db == dstar && j <= jstar));
+      const uint64_t m = __ballot(a);
+      const int slot = m0 + static_cast<int>(__popcll(m & lanemask_lt()));
+      if (a && slot < K) dst[slot] = j;
+      m0 += static_cast<int>(__popcll(m));
+    });
+    if (K > kRgSelCap) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    else wave_lds_fence();
+    // stage E: rank by index
+    for (int m = lane; m < K; m += kWave) {
+      const int v = dst[m];
+      int r = 0;
+      for (int q = 0; q < K; ++q) r += dst[q] < v;
+      row_out[o + r] = v;
+      col_out[o + m] = i;
+    }
+    wave_lds_fence();  // the LDS is reused by the next target
+    return;
+  }
+  for (int m = lane; m < c; m += kWave) {
+    const int v = L[m];
+    int r = 0;
+    for (int q = 0; q < c; ++q) r += L[q] < v;
+    row_out[o + r] = v;
+    col_out[o + m] = i;
+  }
+}
 
 __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __restrict__ x,
                                                          int64_t N, const int64_t* __restrict__ batch,
@@ -487,15 +631,15 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
                                                          int loop, const int64_t* __restrict__ row_ptr,
                                                          int64_t* __restrict__ row_out,
                                                          int64_t* __restrict__ col_out) {
+  __shared__ uint32_t s_key[kRgThreads / kWave][kRgSelCap];
   r2 = rg_r2(w, r2);
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * kRgThreads + threadIdx.x) / kRgGroup;
   const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
-  if (i >= N) return;
-  const int c = w.cnt[i];
-  if (c == 0) return;  // group-uniform
-  int32_t* L = w.list + i * K;
-  const int64_t o = row_ptr[i];
-  if (c <= K && c <= kRgGroup * kRgSlots) {
+  const int c = i < N ? w.cnt[i] : 0;
+  const bool group = c > 0 && c <= K && c <= kRgGroup * kRgSlots;  // group-uniform
+  if (group) {
+    const int32_t* L = w.list + i * K;
+    const int64_t o = row_ptr[i];
     int v[kRgSlots];
 #pragma unroll
     for (int k = 0; k < kRgSlots; ++k) {
@@ -524,32 +668,16 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
         col_out[o + a] = i;
       }
     }
-    return;
   }
-  if (sub != 0) return;
-  int m = c;
-  if (c > K) {
-    const int b = cloud_of(i, batch, B, ppc);
-    const Grid g = w.grid[b];
-    const float qx = x[3 * i], qy = x[3 * i + 1], qz = x[3 * i + 2];
-    uint32_t dstar;
-    int jstar;
-    threshold_select(w, g, qx, qy, qz, static_cast<int>(i), loop != 0, r2, K, dstar, jstar);
-    int n = 0;
-    for_each_candidate(w, g, qx, qy, qz, static_cast<int>(i), loop != 0, [&](float d, int j) {
-      if (d < r2) {
-        const uint32_t db = __float_as_uint(d);
-        if (db < dstar || (db == dstar && j <= jstar)) L[n++] = j;
-      }
-    });
-    m = K;
-  }
-  for (int a = 0; a < m; ++a) {
-    const int val = L[a];
-    int r = 0;
-    for (int q = 0; q < m; ++q) r += L[q] < val;
-    row_out[o + r] = val;
-    col_out[o + a] = i;
+  // the wave's remaining targets, one at a time with all 64 lanes
+  uint64_t rest = __ballot(sub == 0 && c > 0 && !group);
+  while (rest) {
+    const int leader = __builtin_ctzll(rest);
+    rest &= rest - 1;
+    const int64_t ti = __builtin_amdgcn_readlane(static_cast<int>(i), leader);
+    const int tc = __builtin_amdgcn_readlane(c, leader);
+    rg_wave_target(w, x, batch, B, ppc, r2, K, loop != 0, ti, tc, row_ptr, row_out, col_out,
+                   s_key[threadIdx.x / kWave]);
   }
 }
 
