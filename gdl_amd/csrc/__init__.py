@@ -75,6 +75,10 @@ def get_radius_graph_backend() -> str:
 # Largest N * max_num_neighbors whose bound-sized emit scratch (16 bytes per entry) is allocated
 # to overlap the edge-count sync with the emit pass (2^26 entries = 1 GiB); larger graphs wait.
 _RADIUS_ASYNC_MAX_EDGES = 1 << 26
+# Bound-sized scratch up to this size is returned as the outputs themselves (row / col are the
+# first E entries of its two rows), which saves the copy into exact-sized tensors at the cost of
+# holding N * max_num_neighbors entries instead of E (C2: 33.6 MB instead of 10.5 MB).
+_RADIUS_VIEW_MAX_BYTES = 256 << 20
 
 
 def radius_graph_hip(
@@ -128,12 +132,16 @@ def radius_graph_csr_hip(
         B0 = int(num_batch_elements) if num_batch_elements is not None else 1
         return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev), B0
     r2 = fp32_radius_sq(r)
+    ppc_try = 0
     if batch is not None:
         if batch.numel() != N:
             raise ValueError(f"radius_graph: batch has {batch.numel()} entries for {N} points")
         batch = _i64(batch.reshape(-1), dev)
         B = int(num_batch_elements) if num_batch_elements is not None else int(batch.max().item()) + 1
         ppc = 0
+        # sorted equal-size clouds (what the reference's GPU path assumes) take the per-cloud
+        # front end; the device checks that layout and reports a mismatch with the edge count
+        ppc_try = N // B if B >= 1 and N % B == 0 else 0
     else:
         B = int(num_batch_elements) if num_batch_elements is not None else 1
         if B < 1:
@@ -154,34 +162,45 @@ def radius_graph_csr_hip(
         ws_bytes = L.geo_radius_workspace_bytes(N, B, K)
         ws = _nat.workspace(ws_bytes, dev)
         row_ptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
-        if r_dev is None:
-            emit = L.geo_radius_emit
-            args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K,
-                    int(bool(loop)))
-        else:
-            emit = L.geo_radius_emit_dev
-            args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), _nat.ptr(r_dev), K,
-                    int(bool(loop)))
+        emit = L.geo_radius_emit if r_dev is None else L.geo_radius_emit_dev
         if N * K <= _RADIUS_ASYNC_MAX_EDGES:
             # emit into bound-sized scratch right behind the count; the host waits only for the
-            # count (an event) to learn E, then one copy gives exact-sized outputs
+            # count (an event) to learn E, and the first E entries are the graph
             edges_h, counted = _nat.sync_slot(dev)
-            _nat.check(L.geo_radius_count_async(
-                _nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, _nat.ptr(r_dev),
-                K, int(bool(loop)), _nat.ptr(row_ptr), edges_h.data_ptr(), _nat.ptr(ws), ws_bytes,
-                s), "geo_radius_count_async")
-            counted.record(torch.cuda.current_stream(dev))
-            scratch = torch.empty(2, N * K, dtype=torch.int64, device=dev)
-            _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(scratch[0]), _nat.ptr(scratch[1]),
-                            _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
-            counted.synchronize()
-            E = int(edges_h[0].item())
-            row = torch.empty(E, dtype=torch.int64, device=dev)
-            col = torch.empty(E, dtype=torch.int64, device=dev)
-            _nat.check(L.geo_radius_copy_edges(_nat.ptr(scratch[0]), _nat.ptr(scratch[1]), E,
-                                               _nat.ptr(row), _nat.ptr(col), s),
-                       "geo_radius_copy_edges")
+            for p_arg in ((ppc_try, 0) if ppc_try else (ppc,)):
+                if r_dev is None:
+                    args = (_nat.ptr(x), N, _nat.ptr(batch), B, p_arg, _nat.ptr(mask_u8), r2, r, K,
+                            int(bool(loop)))
+                else:
+                    args = (_nat.ptr(x), N, _nat.ptr(batch), B, p_arg, _nat.ptr(mask_u8),
+                            _nat.ptr(r_dev), K, int(bool(loop)))
+                _nat.check(L.geo_radius_count_async(
+                    _nat.ptr(x), N, _nat.ptr(batch), B, p_arg, _nat.ptr(mask_u8), r2, r,
+                    _nat.ptr(r_dev), K, int(bool(loop)), _nat.ptr(row_ptr), edges_h.data_ptr(),
+                    _nat.ptr(ws), ws_bytes, s), "geo_radius_count_async")
+                counted.record(torch.cuda.current_stream(dev))
+                scratch = torch.empty(2, N * K, dtype=torch.int64, device=dev)
+                _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(scratch[0]), _nat.ptr(scratch[1]),
+                                _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
+                counted.synchronize()
+                E, bad = edges_h[:2].tolist()
+                if bad == 0:
+                    break   # else: batch is not the chunk layout; the general path follows
+            if 16 * N * K <= _RADIUS_VIEW_MAX_BYTES:
+                row, col = scratch[0, :E], scratch[1, :E]
+            else:
+                row = torch.empty(E, dtype=torch.int64, device=dev)
+                col = torch.empty(E, dtype=torch.int64, device=dev)
+                _nat.check(L.geo_radius_copy_edges(_nat.ptr(scratch[0]), _nat.ptr(scratch[1]), E,
+                                                   _nat.ptr(row), _nat.ptr(col), s),
+                           "geo_radius_copy_edges")
         else:
+            if r_dev is None:
+                args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), r2, r, K,
+                        int(bool(loop)))
+            else:
+                args = (_nat.ptr(x), N, _nat.ptr(batch), B, ppc, _nat.ptr(mask_u8), _nat.ptr(r_dev),
+                        K, int(bool(loop)))
             count = L.geo_radius_count if r_dev is None else L.geo_radius_count_dev
             _nat.check(count(*args, _nat.ptr(row_ptr), _nat.ptr(ws), ws_bytes, s), "geo_radius_count")
             E = int(row_ptr[N].item())

@@ -100,6 +100,18 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
   return v;
 }
 
+// Sum over all 64 lanes (every lane must be active), wave-uniform: DPP sums within each 16-lane
+// row, then the four row totals read from lanes 0, 16, 32, 48 (no LDS round trips, unlike a
+// shuffle tree).
+__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
+  v += dpp_u32<kDppXor1>(v);
+  v += dpp_u32<kDppXor2>(v);
+  v += dpp_u32<kDppHalfMirror>(v);
+  v += dpp_u32<kDppMirror>(v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+
 // DPP move with bound_ctrl: lanes without a source read 0, which lets the compiler fuse the
 // move into the consuming v_max_u32 (one v_max_u32_dpp per step).  0 is the identity of an
 // unsigned max.
@@ -173,6 +185,27 @@ __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
   for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
   return v;
+}
+
+// The dispatcher hands workgroups to the 8 XCDs in turn (workgroup b to XCD b mod 8).  This
+// renumbering gives each XCD one contiguous range of workgroup indices, so neighbouring work
+// items -- which share input rows -- are processed under the same L2.
+__device__ __forceinline__ int64_t xcd_block() {
+  const int64_t G = gridDim.x, b = blockIdx.x;
+  const int64_t q = G / 8, r = G % 8, x = b % 8, k = b / 8;
+  return x * q + (x < r ? x : r) + k;
+}
+
+// The same idea with the workgroup space cut into runs of `run` consecutive workgroups handed
+// to the XCDs in turn: neighbouring work items still share an L2, and work whose cost varies
+// over the index space (dense regions of a scene) is spread over all XCDs.  Workgroups past the
+// last whole round of 8 runs keep their index.
+__device__ __forceinline__ int64_t xcd_block_runs(int64_t run) {
+  const int64_t G = gridDim.x, b = blockIdx.x;
+  const int64_t whole = G / (8 * run) * (8 * run);
+  if (b >= whole) return b;
+  const int64_t x = b % 8, k = b / 8;
+  return ((k / run) * 8 + x) * run + k % run;
 }
 
 // ---------------------------------------------------------- exact distance ---

@@ -54,6 +54,7 @@ struct RgWs {
   int32_t* deg;
   uint64_t* deg_scan;   // look-back status of the row-pointer scan (zeroed by rg_init)
   int32_t* list;  // [N][K] accepted sources per target (unsorted), or null when too large
+  int32_t* layout_bad;  // [B] per cloud: points of the chunk whose batch entry is another cloud
   int64_t cells_max;
   size_t bytes;
   const double* r_dev = nullptr;  // radius on the device (geo_radius_*_dev), else null
@@ -95,6 +96,7 @@ RgWs carve_rg(void* base, int64_t N, int64_t B, int64_t K) {
   w.cnt = c.take<int32_t>(nn);
   w.deg = c.take<int32_t>(nn);
   w.deg_scan = c.take<uint64_t>(scan_lookback_elems(N));
+  w.layout_bad = c.take<int32_t>(bb);
   const bool lists = K > 0 && N <= kRgListMaxEntries / K;
   w.list = lists ? c.take<int32_t>(N * K) : nullptr;
   if (lists && !base) w.list = reinterpret_cast<int32_t*>(1);  // size query: mark "present"
@@ -125,6 +127,43 @@ __global__ void rg_init(RgWs w, int64_t N, int64_t B) {
   }
 }
 
+// Grid of one cloud of n valid points with bounding box [mn, mx]: cell edge h >= r*(1+1/32),
+// grown until the cell count is at most 4n + 64 and no axis exceeds kRgMaxAxis cells (one cell
+// for the whole cloud if that fails).  Writes the cell count; g.base is left 0.
+__device__ Grid rg_grid(const float (&mn)[3], const float (&mx)[3], int64_t n, float r_cell,
+                        int64_t& cells) {
+  Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
+  const double cap = 4.0 * n + 64.0;
+  double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
+  double ext[3];
+  for (int a = 0; a < 3; ++a) {
+    const double e = static_cast<double>(mx[a]) - static_cast<double>(mn[a]);
+    ext[a] = (e >= 0.0 && e < 1e30) ? e : 0.0;  // non-finite input: one slab on that axis
+  }
+  int64_t d[3] = {1, 1, 1};
+  bool ok = false;
+  for (int iter = 0; iter < 64 && !ok; ++iter) {
+    double prod = 1.0, worst_axis = 0.0;
+    for (int a = 0; a < 3; ++a) {
+      const double q = floor(ext[a] / h) + 1.0;
+      d[a] = q < static_cast<double>(kRgMaxAxis) * 4 ? static_cast<int64_t>(q) : kRgMaxAxis * 4;
+      prod *= static_cast<double>(d[a]);
+      worst_axis = fmax(worst_axis, static_cast<double>(d[a]) / kRgMaxAxis);
+    }
+    ok = prod <= cap && worst_axis <= 1.0;
+    if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst_axis), 1.0) * 1.01;
+  }
+  g.ox = mn[0]; g.oy = mn[1]; g.oz = mn[2];
+  g.inv_h = static_cast<float>(1.0 / h);
+  if (!ok) {  // one cell holds the whole cloud
+    d[0] = d[1] = d[2] = 1;
+    g.inv_h = 0.f;
+  }
+  g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
+  cells = d[0] * d[1] * d[2];
+  return g;
+}
+
 // Single workgroup: grid parameters and cell bases for every cloud.
 __global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, float r_cell) {
   __shared__ int64_t lds[kScanThreads / kWave];
@@ -140,34 +179,7 @@ __global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, floa
                            float_from_order_key(bb[2])};
       const float mx[3] = {float_from_order_key(bb[3]), float_from_order_key(bb[4]),
                            float_from_order_key(bb[5])};
-      const double cap = 4.0 * w.cloud_n[b] + 64.0;
-      double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
-      double ext[3];
-      for (int a = 0; a < 3; ++a) {
-        const double e = static_cast<double>(mx[a]) - static_cast<double>(mn[a]);
-        ext[a] = (e >= 0.0 && e < 1e30) ? e : 0.0;  // non-finite input: one slab on that axis
-      }
-      int64_t d[3] = {1, 1, 1};
-      bool ok = false;
-      for (int iter = 0; iter < 64 && !ok; ++iter) {
-        double prod = 1.0, worst_axis = 0.0;
-        for (int a = 0; a < 3; ++a) {
-          const double q = floor(ext[a] / h) + 1.0;
-          d[a] = q < static_cast<double>(kRgMaxAxis) * 4 ? static_cast<int64_t>(q) : kRgMaxAxis * 4;
-          prod *= static_cast<double>(d[a]);
-          worst_axis = fmax(worst_axis, static_cast<double>(d[a]) / kRgMaxAxis);
-        }
-        ok = prod <= cap && worst_axis <= 1.0;
-        if (!ok) h *= fmax(fmax(cbrt(prod / cap), worst_axis), 1.0) * 1.01;
-      }
-      g.ox = mn[0]; g.oy = mn[1]; g.oz = mn[2];
-      g.inv_h = static_cast<float>(1.0 / h);
-      if (!ok) {  // one cell holds the whole cloud
-        d[0] = d[1] = d[2] = 1;
-        g.inv_h = 0.f;
-      }
-      g.dx = static_cast<int>(d[0]); g.dy = static_cast<int>(d[1]); g.dz = static_cast<int>(d[2]);
-      cells = d[0] * d[1] * d[2];
+      g = rg_grid(mn, mx, w.cloud_n[b], r_cell, cells);
     }
     int64_t total;
     const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
@@ -279,6 +291,170 @@ __global__ __launch_bounds__(kRgThreads) void rg_scatter(RgWs w, const float* __
   w.spos[p] = make_float4(x[3 * i], x[3 * i + 1], x[3 * i + 2], __int_as_float(static_cast<int>(i)));
 }
 
+// Clouds that are contiguous chunks of at most kRgFrontMax points (points_per_cloud given, or a
+// batch vector verified to be that layout): one workgroup per cloud does what rg_init .. rg_scatter
+// do for all clouds -- bounding box, grid, cell counts (LDS atomics, two 16-bit counts per
+// word), their scan and the cell-ordered points -- with no global atomics.  Cloud b owns cells
+// [b * (4 ppc + 64), ...) and spos slots [b * ppc, (b + 1) * ppc); masked points (and, with a
+// batch vector, points whose entry is not b, counted in layout_bad[b]) leave holes at the end
+// of the cloud's slots, marked by index -1.
+constexpr int kRgFrontThreads = 1024;
+constexpr int kRgFrontMax = 4096;
+constexpr int kRgFrontPer = kRgFrontMax / kRgFrontThreads;
+constexpr int kRgFrontCells = 4 * kRgFrontMax + 64;
+constexpr int kRgFrontWords = kRgFrontCells / 2 + 1;
+// beyond this many clouds (one 1024-thread workgroup each) the general path is cheaper
+constexpr int64_t kRgFrontMaxClouds = 4096;
+
+__device__ __forceinline__ uint32_t half_of(const uint32_t* s, int c) {
+  return (s[c >> 1] >> ((c & 1) * 16)) & 0xffffu;
+}
+
+__global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float* __restrict__ x,
+                                                            int64_t N, const int64_t* __restrict__ batch,
+                                                            int64_t B, int64_t ppc,
+                                                            const uint8_t* __restrict__ mask,
+                                                            float r_cell) {
+  constexpr int W = kRgFrontThreads / kWave;
+  __shared__ uint32_t s_cnt[kRgFrontWords];
+  __shared__ uint32_t s_red[7][W];
+  __shared__ Grid s_grid;
+  __shared__ int s_cells, s_nv;
+  const int b = blockIdx.x;
+  const int64_t lo = static_cast<int64_t>(b) * ppc;
+  const int tid = threadIdx.x, wv = tid / kWave, lane = lane_id();
+  r_cell = rg_rcell(w, r_cell);
+  float px[kRgFrontPer], py[kRgFrontPer], pz[kRgFrontPer];
+  bool ok[kRgFrontPer];
+  bool bad = false;
+  uint32_t nv = 0;
+  uint32_t kmin[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, kmax[3] = {0u, 0u, 0u};
+#pragma unroll
+  for (int k = 0; k < kRgFrontPer; ++k) {
+    const int il = tid + k * kRgFrontThreads;
+    ok[k] = false;
+    px[k] = py[k] = pz[k] = 0.f;
+    if (il < ppc) {
+      const int64_t i = lo + il;
+      bool v = !mask || mask[i];
+      if (batch && batch[i] != b) {
+        bad = true;
+        v = false;
+      }
+      if (v) {
+        px[k] = x[3 * i]; py[k] = x[3 * i + 1]; pz[k] = x[3 * i + 2];
+        const uint32_t kk[3] = {float_order_key(px[k]), float_order_key(py[k]), float_order_key(pz[k])};
+#pragma unroll
+        for (int a = 0; a < 3; ++a) { kmin[a] = min(kmin[a], kk[a]); kmax[a] = max(kmax[a], kk[a]); }
+        ok[k] = true;
+        ++nv;
+      }
+    }
+  }
+  // bounding box, valid count and layout check over the workgroup
+  uint32_t r7[7] = {wave_min_u32(kmin[0]), wave_min_u32(kmin[1]), wave_min_u32(kmin[2]),
+                    wave_max_u32(kmax[0]), wave_max_u32(kmax[1]), wave_max_u32(kmax[2]), 0u};
+  const uint32_t wnv = static_cast<uint32_t>(wave_sum(static_cast<int>(nv)));
+  const bool wbad = __ballot(bad) != 0ull;
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 6; ++q) s_red[q][wv] = r7[q];
+    s_red[6][wv] = wnv | (wbad ? 0x80000000u : 0u);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t mn_k[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, mx_k[3] = {0u, 0u, 0u};
+    uint32_t n = 0;
+    bool any_bad = false;
+    for (int q = 0; q < W; ++q) {
+      for (int a = 0; a < 3; ++a) {
+        mn_k[a] = min(mn_k[a], s_red[a][q]);
+        mx_k[a] = max(mx_k[a], s_red[3 + a][q]);
+      }
+      n += s_red[6][q] & 0x7fffffffu;
+      any_bad = any_bad || (s_red[6][q] >> 31);
+    }
+    int64_t cells = 0;
+    Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
+    if (n > 0) {
+      const float mn[3] = {float_from_order_key(mn_k[0]), float_from_order_key(mn_k[1]),
+                           float_from_order_key(mn_k[2])};
+      const float mx[3] = {float_from_order_key(mx_k[0]), float_from_order_key(mx_k[1]),
+                           float_from_order_key(mx_k[2])};
+      g = rg_grid(mn, mx, n, r_cell, cells);
+    }
+    g.base = static_cast<int>(static_cast<int64_t>(b) * (4 * ppc + 64));
+    s_grid = g;
+    s_cells = static_cast<int>(cells);
+    s_nv = static_cast<int>(n);
+    w.grid[b] = g;
+    if (batch) w.layout_bad[b] = any_bad ? 1 : 0;
+  }
+  __syncthreads();
+  const Grid g = s_grid;
+  const int cells = s_cells, n_valid = s_nv;
+  for (int q = tid; q < (cells >> 1) + 1; q += kRgFrontThreads) s_cnt[q] = 0u;
+  __syncthreads();
+  int cl[kRgFrontPer], rk[kRgFrontPer];
+#pragma unroll
+  for (int k = 0; k < kRgFrontPer; ++k) {
+    cl[k] = 0;
+    rk[k] = 0;
+    if (ok[k]) {
+      const int cx = cell_coord(px[k], g.ox, g.inv_h, g.dx);
+      const int cy = cell_coord(py[k], g.oy, g.inv_h, g.dy);
+      const int cz = cell_coord(pz[k], g.oz, g.inv_h, g.dz);
+      const int c = (cx * g.dy + cy) * g.dz + cz;
+      const uint32_t old = atomicAdd(&s_cnt[c >> 1], (c & 1) ? 0x10000u : 1u);
+      cl[k] = c;
+      rk[k] = static_cast<int>((old >> ((c & 1) * 16)) & 0xffffu);
+    }
+  }
+  __syncthreads();
+  // exclusive scan of the cell counts in place; each thread owns an even-aligned run of cells so
+  // that no two threads write halves of one word
+  const int per = ((cells + 2 * kRgFrontThreads - 1) / (2 * kRgFrontThreads)) * 2;
+  const int c0 = tid * per, c1 = min(c0 + per, cells);
+  uint32_t sum = 0;
+  for (int c = c0; c < c1; ++c) sum += half_of(s_cnt, c);
+  const uint32_t incl = static_cast<uint32_t>(wave_inclusive_sum(static_cast<int>(sum)));
+  if (lane == kWave - 1) s_red[0][wv] = incl;
+  __syncthreads();
+  uint32_t run = incl - sum;
+  for (int q = 0; q < wv; ++q) run += s_red[0][q];
+  int32_t* cs = w.cell_start + g.base;
+  for (int c = c0; c < c1; c += 2) {
+    const uint32_t a0 = half_of(s_cnt, c);
+    const uint32_t a1 = c + 1 < c1 ? half_of(s_cnt, c + 1) : 0u;
+    s_cnt[c >> 1] = run | ((run + a0) << 16);
+    cs[c] = static_cast<int32_t>(lo + run);
+    if (c + 1 < c1) cs[c + 1] = static_cast<int32_t>(lo + run + a0);
+    run += a0 + a1;
+  }
+  if (tid == 0) cs[cells] = static_cast<int32_t>(lo + n_valid);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kRgFrontPer; ++k) {
+    if (!ok[k]) continue;
+    const int64_t i = lo + tid + k * kRgFrontThreads;
+    const int64_t pos = lo + half_of(s_cnt, cl[k]) + rk[k];
+    w.spos[pos] = make_float4(px[k], py[k], pz[k], __int_as_float(static_cast<int>(i)));
+  }
+  // holes: NaN coordinates are within no radius of anything, so a stencil run that reaches one
+  // (the last cloud's end sentinel is the total slot when its grid uses its whole cell cap)
+  // accepts nothing from it
+  const float qnan = __builtin_nanf("");
+  for (int64_t h = n_valid + tid; h < ppc; h += kRgFrontThreads)
+    w.spos[lo + h] = make_float4(qnan, qnan, qnan, __int_as_float(-1));
+  for (int64_t il = tid; il < ppc; il += kRgFrontThreads) {
+    w.cnt[lo + il] = 0;
+    w.deg[lo + il] = 0;
+  }
+  if (b == 0)
+    for (int64_t q = tid; q < scan_lookback_elems(N); q += kRgFrontThreads) w.deg_scan[q] = 0;
+  if (b == B - 1 && tid == 0) w.cell_start[w.cells_max] = static_cast<int32_t>(N);
+}
+
 // Visits every source of the 27-cell stencil around the query as (d, j).
 template <typename F>
 __device__ __forceinline__ void for_each_candidate(const RgWs& w, const Grid& g, float qx, float qy,
@@ -377,6 +553,7 @@ __global__ void rg_emit(RgWs w, const int64_t* __restrict__ batch, int64_t B, in
   if (t >= total) return;
   const float4 q = w.spos[t];
   const int qi = __float_as_int(q.w);
+  if (qi < 0) return;  // a hole of the per-cloud layout
   const int b = cloud_of(qi, batch, B, ppc);
   const Grid g = w.grid[b];
   const bool lp = loop != 0;
@@ -413,17 +590,29 @@ __global__ void rg_emit(RgWs w, const int64_t* __restrict__ batch, int64_t B, in
 // longer runs continue chunk by chunk.  Accepted sources are appended to the target's list in
 // ballot order (the list is unsorted; the compaction sorts it), the count is the group's total.
 constexpr int kRgGroup = 8;
+// workgroups per XCD run (xcd_block_runs) of the count and compaction passes: 512 targets
+constexpr int64_t kRgXcdRun = 16;
 
 __global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __restrict__ batch,
                                                        int64_t B, int64_t ppc, float r2, int K,
-                                                       int loop) {
+                                                       int loop, int64_t* __restrict__ bad_out,
+                                                       int check_layout) {
+  if (bad_out && blockIdx.x == 0 && threadIdx.x == 0) {  // clouds failing the chunk layout
+    int64_t nb = 0;
+    if (check_layout)
+      for (int64_t b = 0; b < B; ++b) nb += w.layout_bad[b];
+    *bad_out = nb;
+  }
   r2 = rg_r2(w, r2);
-  const int64_t t = (static_cast<int64_t>(blockIdx.x) * kRgThreads + threadIdx.x) / kRgGroup;
+  // each XCD takes runs of 512 consecutive targets in cell order (neighbouring targets share
+  // stencil cells in its L2; dense regions are spread over all XCDs)
+  const int64_t t = (xcd_block_runs(kRgXcdRun) * kRgThreads + threadIdx.x) / kRgGroup;
   const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
   const int total = w.cell_start[w.cells_max];
   if (t >= total) return;  // the whole group leaves together
   const float4 q = w.spos[t];
   const int qi = __float_as_int(q.w);
+  if (qi < 0) return;  // a hole of the per-cloud layout (group-uniform)
   const int b = cloud_of(qi, batch, B, ppc);
   const Grid g = w.grid[b];
   const int cx = cell_coord(q.x, g.ox, g.inv_h, g.dx);
@@ -524,19 +713,20 @@ __device__ __forceinline__ void wave_scan_runs(const RgWs& w, const int (&ra)[9]
 
 // One target done by the whole wave: c = its count of in-radius sources (c > 0).
 //  c <= K: the list L[0..c) (complete) sorted by index, 64 entries per step.
-//  c > K:  the K smallest (d, j): the in-radius distance bits collected in LDS (c <= kRgSelCap;
-//          beyond that each count re-scans the stencil), the K-th distance d* by binary search
-//          on the bits, the index threshold j* among the sources at d* when they are more than
-//          needed (re-scans), the accepted sources compacted and sorted by index.
+//  c > K:  the K smallest (d, j): the in-radius sources as (distance bits, index) pairs collected
+//          in LDS in one stencil pass (c <= kRgSelCap; beyond that every step re-scans the
+//          stencil), the K-th distance d* by binary search on the bits, the index threshold j*
+//          among the sources at d* when they are more than needed, the accepted sources compacted
+//          in place and sorted by index.
 __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
                                const int64_t* __restrict__ batch, int64_t B, int64_t ppc, float r2,
                                int K, bool lp, int64_t i, int c,
                                const int64_t* __restrict__ row_ptr, int64_t* __restrict__ row_out,
-                               int64_t* __restrict__ col_out, uint32_t* __restrict__ key) {
+                               int64_t* __restrict__ col_out, uint32_t* __restrict__ key,
+                               int32_t* __restrict__ idx) {
   const int lane = lane_id();
   const int64_t o = row_ptr[i];
   int32_t* L = w.list + i * K;
-  int32_t* acc = reinterpret_cast<int32_t*>(key);  // accepted sources (LDS) when K <= cap
   if (c > K) {
     const int b = cloud_of(i, batch, B, ppc);
     const Grid g = w.grid[b];
@@ -546,33 +736,45 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
     stencil_runs(w, g, qx, qy, qz, ra, rn);
     const bool inl = c <= kRgSelCap;
     int n = 0;
-    if (inl) {  // stage A: in-radius distance bits into LDS (wave compaction)
+    if (inl) {  // stage A: in-radius (distance bits, index) into LDS (wave compaction)
       wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
         const bool a = ok && (lp || j != qi) && d < r2;
         const uint64_t m = __ballot(a);
         const int slot = n + static_cast<int>(__popcll(m & lanemask_lt()));
-        if (a && slot < kRgSelCap) key[slot] = __float_as_uint(d);
+        if (a && slot < kRgSelCap) {
+          key[slot] = __float_as_uint(d);
+          idx[slot] = j;
+        }
         n += static_cast<int>(__popcll(m));
       });
       n = n < kRgSelCap ? n : kRgSelCap;
       wave_lds_fence();
     }
-    // count of in-radius sources with (bits, j) <= (dmax, jmax) (j ignored when jmax < 0)
-    auto count_le = [&](uint32_t dmax, bool strict, int jeq_max) -> int {
+    // in-radius sources with bits <= dmax (< when strict), or with bits == dmax and j <= jmax
+    // (jmax >= 0)
+    auto count_le = [&](uint32_t dmax, bool strict, int jmax) -> int {
       int t = 0;
-      if (inl && jeq_max < 0) {
-        for (int m = lane; m < n; m += kWave) t += strict ? key[m] < dmax : key[m] <= dmax;
+      auto hit = [&](uint32_t db, int j) -> bool {
+        return jmax < 0 ? (strict ? db < dmax : db <= dmax) : (db == dmax && j <= jmax);
+      };
+      if (inl) {
+        for (int m = lane; m < n; m += kWave) t += hit(key[m], idx[m]);
       } else {
         wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
-          const uint32_t db = __float_as_uint(d);
-          const bool a = ok && (lp || j != qi) && d < r2;
-          t += a && (jeq_max < 0 ? (strict ? db < dmax : db <= dmax) : (db == dmax && j <= jeq_max));
+          t += ok && (lp || j != qi) && d < r2 && hit(__float_as_uint(d), j);
         });
       }
-      return wave_sum(t);
+      return static_cast<int>(wave_sum_dpp(static_cast<uint32_t>(t)));
     };
-    // stage B: the K-th smallest distance bits (every in-radius d has bits < bits(r2))
+    // stage B: the K-th smallest distance bits (every in-radius d has bits < bits(r2)), searched
+    // between the smallest and largest bits present
     uint32_t lo = 0, hi = __float_as_uint(r2) - 1u;
+    if (inl) {
+      uint32_t mn = 0xffffffffu, mx = 0u;
+      for (int m = lane; m < n; m += kWave) { mn = min(mn, key[m]); mx = max(mx, key[m]); }
+      lo = wave_min_u32(mn);
+      hi = wave_max_u32(mx);
+    }
     while (lo < hi) {
       const uint32_t mid = lo + ((hi - lo) >> 1);
       if (count_le(mid, false, -1) >= K) hi = mid; else lo = mid + 1u;
@@ -591,19 +793,32 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
       }
       jstar = jlo;
     }
-    // stage D: the K accepted sources, compacted into LDS (or the list when K exceeds it)
-    int32_t* dst = K <= kRgSelCap ? acc : L;
-    wave_lds_fence();
+    auto accept = [&](uint32_t db, int j) { return db < dstar || (db == dstar && j <= jstar); };
+    // stage D: the K accepted sources, compacted (in place over the LDS indices: a slot never
+    // passes the position being read) or into the list when K exceeds the LDS
+    int32_t* dst = (inl && K <= kRgSelCap) ? idx : L;
     int m0 = 0;
-    wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
-      const uint32_t db = __float_as_uint(d);
-      const bool a = ok && (lp || j != qi) && d < r2 && (db < dstar || (db == dstar && j <= jstar));
-      const uint64_t m = __ballot(a);
-      const int slot = m0 + static_cast<int>(__popcll(m & lanemask_lt()));
-      if (a && slot < K) dst[slot] = j;
-      m0 += static_cast<int>(__popcll(m));
-    });
-    if (K > kRgSelCap) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    if (inl) {
+      for (int base = 0; base < n; base += kWave) {  // wave-uniform trip count
+        const int m = base + lane;
+        const bool a = m < n && accept(key[m], idx[m]);
+        const int j = m < n ? idx[m] : 0;
+        const uint64_t bm = __ballot(a);
+        const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
+        wave_lds_fence();  // every lane has read its entry before any slot is written
+        if (a && slot < K) dst[slot] = j;
+        m0 += static_cast<int>(__popcll(bm));
+      }
+    } else {
+      wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
+        const bool a = ok && (lp || j != qi) && d < r2 && accept(__float_as_uint(d), j);
+        const uint64_t bm = __ballot(a);
+        const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
+        if (a && slot < K) dst[slot] = j;
+        m0 += static_cast<int>(__popcll(bm));
+      });
+    }
+    if (dst == L) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
     else wave_lds_fence();
     // stage E: rank by index
     for (int m = lane; m < K; m += kWave) {
@@ -632,8 +847,9 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
                                                          int64_t* __restrict__ row_out,
                                                          int64_t* __restrict__ col_out) {
   __shared__ uint32_t s_key[kRgThreads / kWave][kRgSelCap];
+  __shared__ int32_t s_idx[kRgThreads / kWave][kRgSelCap];
   r2 = rg_r2(w, r2);
-  const int64_t i = (static_cast<int64_t>(blockIdx.x) * kRgThreads + threadIdx.x) / kRgGroup;
+  const int64_t i = (xcd_block_runs(kRgXcdRun) * kRgThreads + threadIdx.x) / kRgGroup;
   const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
   const int c = i < N ? w.cnt[i] : 0;
   const bool group = c > 0 && c <= K && c <= kRgGroup * kRgSlots;  // group-uniform
@@ -677,7 +893,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
     const int64_t ti = __builtin_amdgcn_readlane(static_cast<int>(i), leader);
     const int tc = __builtin_amdgcn_readlane(c, leader);
     rg_wave_target(w, x, batch, B, ppc, r2, K, loop != 0, ti, tc, row_ptr, row_out, col_out,
-                   s_key[threadIdx.x / kWave]);
+                   s_key[threadIdx.x / kWave], s_idx[threadIdx.x / kWave]);
   }
 }
 
@@ -709,6 +925,9 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                              const double* r_dev, int64_t max_num_neighbors, int loop,
                              int64_t* row_ptr, void* workspace, size_t workspace_bytes,
                              void* stream, int64_t* edges_host = nullptr) {
+  // Contiguous clouds of at most kRgFrontMax points take the per-cloud front end: given by
+  // points_per_cloud alone, or by a batch vector that the front end verifies (only when the
+  // caller can learn the result: edges_host[1] receives the count of clouds that fail).
   int rc = check_common(x, N, B, points_per_cloud, batch, r2, max_num_neighbors);
   if (rc) return rc;
   GEO_REQUIRE(r_cell > 0.f, "radius_graph: r_cell must be positive");
@@ -720,6 +939,22 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
                      workspace_bytes, w.bytes);
   hipStream_t st = as_stream(stream);
   const int K = static_cast<int>(max_num_neighbors);
+  const bool front = N > 0 && points_per_cloud > 0 && points_per_cloud <= kRgFrontMax &&
+                     B <= kRgFrontMaxClouds && points_per_cloud * B == N &&
+                     (batch == nullptr || edges_host != nullptr);
+  int64_t* bad_out = edges_host ? edges_host + 1 : nullptr;
+  if (front) {
+    hipLaunchKernelGGL(rg_front, dim3(static_cast<unsigned>(B)), dim3(kRgFrontThreads), 0, st, w, x,
+                       N, batch, B, points_per_cloud, mask, r_cell);
+    GEO_LAUNCH_CHECK("rg_front");
+    const int64_t gblocks = ceil_div(N * kRgGroup, kRgThreads);
+    hipLaunchKernelGGL(rg_count, dim3(gblocks), dim3(kRgThreads), 0, st, w, batch, B,
+                       points_per_cloud, r2, K, loop, bad_out, batch ? 1 : 0);
+    GEO_LAUNCH_CHECK("rg_count");
+    return device_exclusive_scan_lookback<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true,
+                                                            w.deg_scan, st, edges_host);
+  }
+  if (batch) points_per_cloud = 0;  // the general path reads cloud membership from batch
   {
     int64_t span = w.cells_max + 1;
     if (N > span) span = N;
@@ -749,11 +984,11 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
     GEO_LAUNCH_CHECK("rg_scatter");
     const int64_t gblocks = ceil_div(N * kRgGroup, kRgThreads);
     hipLaunchKernelGGL(rg_count, dim3(gblocks), dim3(kRgThreads), 0, st, w, batch, B,
-                       points_per_cloud, r2, K, loop);
+                       points_per_cloud, r2, K, loop, bad_out, 0);
     GEO_LAUNCH_CHECK("rg_count");
   }
-  if (N == 0 && edges_host) {  // no scan launch to carry the total: zero it from a fill
-    rc = device_fill<int64_t>(edges_host, 1, int64_t{0}, st);
+  if (N == 0 && edges_host) {  // no scan launch to carry the total: zero it (and the failures)
+    rc = device_fill<int64_t>(edges_host, 2, int64_t{0}, st);
     if (rc) return rc;
   }
   return device_exclusive_scan_lookback<int32_t, int64_t>(w.deg, N, row_ptr, nullptr, true,

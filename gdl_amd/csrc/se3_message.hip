@@ -256,14 +256,8 @@ __device__ __forceinline__ void node_range(const SeEdges& g, int64_t n, int& a, 
 constexpr int kSeUnroll = 2;  // edges whose source rows are in flight together (C2: 2, 3, 4 give
                               // the same forward aggregate; the source-side backward 112 / 125 / 123 us)
 
-// The dispatcher hands workgroups to the 8 XCDs in turn (workgroup b to XCD b mod 8).  This
-// renumbering gives each XCD one contiguous range of the node space, so neighbouring nodes --
-// which share source rows -- are processed under the same L2.
-__device__ __forceinline__ int64_t xcd_block() {
-  const int64_t G = gridDim.x, b = blockIdx.x;
-  const int64_t q = G / 8, r = G % 8, x = b % 8, k = b / 8;
-  return x * q + (x < r ? x : r) + k;
-}
+// xcd_block() (common.hpp) gives each XCD one contiguous range of the node space, so
+// neighbouring nodes -- which share source rows -- are processed under the same L2.
 
 // ------------------------------------------------------------------ forward aggregate ---
 // One wave per target node, lanes over input channels (chunks of 64).  The node's edges are

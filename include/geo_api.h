@@ -166,12 +166,21 @@ int geo_radius_emit_dev(const float* x, int64_t N, const int64_t* batch, int64_t
 
 /*
  * The two phases without a host wait between them.  geo_radius_count_async is geo_radius_count
- * (or geo_radius_count_dev when radius_dev is not NULL) that also writes E into edges_host, one
- * int64 of mapped pinned host memory (hipHostMalloc'd, e.g. a pin_memory tensor).  The caller
- * records an event, calls geo_radius_emit[_dev] at once with outputs of the bound size
- * N * max_num_neighbors, waits for the event, reads E, allocates row_out[E], col_out[E] and calls
- * geo_radius_copy_edges to move the first E emitted entries there.  The same sync as the
- * reference's (geoembodied/csrc/__init__.py:130-186), taken off the GPU's critical path.
+ * (or geo_radius_count_dev when radius_dev is not NULL) that also writes E into edges_host[0]
+ * (two int64 of mapped pinned host memory: hipHostMalloc'd, e.g. a pin_memory tensor).  The
+ * caller records an event, calls geo_radius_emit[_dev] at once with outputs of the bound size
+ * N * max_num_neighbors, waits for the event and reads E: the first E entries of the outputs are
+ * the graph (geo_radius_copy_edges moves them into exact-sized arrays if wanted).  The same sync
+ * as the reference's (geoembodied/csrc/__init__.py:130-186), taken off the GPU's critical path.
+ *
+ * Clouds given as contiguous chunks of points_per_cloud <= 4096 points take a one-workgroup-per-
+ * cloud front end.  With batch != NULL and points_per_cloud > 0, batch is expected to be that
+ * chunk layout (batch[i] = i / points_per_cloud: the sorted equal-size batches the reference's
+ * GPU path assumes, geoembodied/functional/radius_graph.py:70-85); the front end checks it and
+ * edges_host[1] receives the number of clouds where it does not hold, in which case the results
+ * are invalid and the caller repeats both phases with points_per_cloud = 0 (the general path).
+ * Otherwise edges_host[1] is 0.  (geo_radius_count / _dev ignore points_per_cloud when batch is
+ * given.)
  */
 int geo_radius_count_async(const float* x, int64_t N, const int64_t* batch, int64_t B,
                            int64_t points_per_cloud, const uint8_t* mask, float r2, float r_cell,

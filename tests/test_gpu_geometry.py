@@ -340,6 +340,43 @@ def test_radius_reference_kats(dev):
     assert get_radius_graph_backend() == "cuda"
 
 
+@pytest.mark.parametrize("layout", ["chunks", "shuffled", "unequal", "foreign_id"])
+def test_radius_batch_layouts(dev, layout):
+    """A batch vector with N % B == 0 first takes the per-cloud front end, which checks on the
+    device that batch[i] == i // (N / B); any other layout is reported with the edge count and
+    redone on the general path.  Every layout must give the oracle's graph."""
+    B, n = 6, 700
+    N = B * n
+    g = torch.Generator().manual_seed(len(layout))
+    x = torch.randn(N, 3, generator=g) * 0.7
+    batch = torch.arange(B).repeat_interleave(n)
+    if layout == "shuffled":                  # equal counts, interleaved
+        batch = batch[torch.randperm(N, generator=g)]
+    elif layout == "unequal":                 # sorted, unequal sizes
+        batch = torch.repeat_interleave(torch.arange(B), torch.tensor([900, 500, 700, 800, 600, 700]))
+    elif layout == "foreign_id":              # one entry outside [0, B) (excluded point)
+        batch[1234] = B + 2
+    _rg_check(dev, x, 0.3, 12, batch=batch, nb=B)
+    _rg_check(dev, x, 0.3, 12, loop=True, batch=batch, nb=B)
+
+
+@pytest.mark.parametrize("ppc", [1, 63, 1000, 4096])
+def test_radius_per_cloud_front_masks_and_caps(dev, ppc):
+    """Contiguous clouds given by num_batch_elements (the per-cloud front end up to 4096 points):
+    masked points leave holes in the cell-ordered slots; loops, K caps with ties (integer
+    lattice) and clouds with no valid point."""
+    B = 5
+    g = torch.Generator().manual_seed(ppc)
+    x = torch.randn(B * ppc, 3, generator=g) * 0.5
+    mask = torch.rand(B * ppc, generator=g) > 0.3
+    mask[:ppc] = False                                   # cloud 0 entirely masked
+    _rg_check(dev, x, 0.25, 9, mask=mask, nb=B)
+    _rg_check(dev, x, 0.25, 9, loop=True, mask=mask, nb=B)
+    lat = _lattice(16, 5)[: B * min(ppc, 800)]
+    if lat.shape[0] >= B:
+        _rg_check(dev, lat, 1.5, 7, nb=B)                # d^2 in {1, 2}: ties at the cap
+
+
 @pytest.mark.parametrize("N", [10000, 50000])
 def test_radius_large(dev, N):
     torch.manual_seed(N)
@@ -355,6 +392,21 @@ def test_radius_degenerate_extent(dev):
     x2 = torch.zeros(300, 3)   # all coincident
     _rg_check(dev, x2, 0.1, 7)
     _rg_check(dev, x2, 0.1, 400, loop=True)
+
+
+def test_radius_dense_blob_wave_selection_paths(dev):
+    """Targets with more than K in-radius sources are selected by a whole wave: up to 1024 of
+    them kept in LDS, beyond that re-scanned from the cell lists; K above 1024 compacts into the
+    global list.  A 2500-point blob (every pair within r) beside a sparse cloud, with exact-tie
+    lattice points, checked at K = 20 and K = 1100."""
+    g = torch.Generator().manual_seed(17)
+    blob = torch.rand(2500, 3, generator=g) * 0.01
+    lat = _lattice(8, 3) * 0.004 + 0.02       # 512 points, many equal distances
+    sparse = torch.rand(1500, 3, generator=g) * 4 + 1
+    x = torch.cat([blob, lat, sparse])
+    _rg_check(dev, x, 0.05, 20)
+    _rg_check(dev, x, 0.05, 1100)
+    _rg_check(dev, x, 0.05, 1100, loop=True)
 
 
 # ------------------------------------------------------------------------ BASELINE configs ---
