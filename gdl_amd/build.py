@@ -40,6 +40,14 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-file device flags.  fps.hip: the sampling loops end every iteration with one lane's LDS
+# atomic max; the atomic optimizer would wrap it in a single-lane election (mbcnt, compare, exec
+# mask) that lengthens the path to the barrier in every wave, every iteration.
+FILE_FLAGS = {
+    "fps.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def lib_path() -> Path:
     return LIBDIR / LIBNAME
 
@@ -68,7 +76,8 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = BUILDDIR / (src.stem + ".o")
-        cmd = [HIPCC, *DEVICE_FLAGS, define, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), define, "-c", str(src), "-o",
+               str(obj)]
         if verbose:
             print(" ".join(cmd))
         _run(cmd)

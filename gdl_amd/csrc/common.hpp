@@ -123,6 +123,16 @@ __device__ __forceinline__ uint32_t dpp0_u32(uint32_t v) {
   return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also orders global memory,
+// which on gfx950 means waiting for every outstanding vector memory operation of the wave,
+// stores included, before the barrier; loops whose waves exchange data only through LDS use this
+// one, so their global stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave-uniform max over all 64 lanes (every lane must be active): four in-row steps, two row
 // broadcasts, lane 63 holds the result.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kFpsThreads) void fps_register_kernel(
     wave_argmax(bbits, bidx, wbits, widx);
     FpsSlot* sl = slots[it & 1];
     if (lane_id() == 0) sl[w] = FpsSlot{wbits, widx};
-    __syncthreads();
+    lds_barrier();  // waves share only LDS in this loop
     uint32_t gbits = sl[0].dist_bits, gidx = sl[0].idx;
 #pragma unroll
     for (int ww = 1; ww < kFpsWaves; ++ww) {
@@ -208,11 +208,14 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   // Launched before the host has seen the prepare kernel's summary: do nothing unless ptr was
   // valid and every cloud fits this variant (the host then launches the right one).
   if (guard != nullptr && (guard[2] != 0 || guard[1] > PTS * THREADS)) return;
-  // Cross-wave argmax: one 64-bit LDS atomic max per wave on key (bits << 32) | ~index, so the
-  // largest distance wins and, among equal distances, the lowest index.  Three slots rotate:
-  // iteration it uses slot it % 3 and clears slot (it + 1) % 3, whose last readers finished
-  // before the previous barrier and whose next writers start after this one.
-  __shared__ unsigned long long slots[3];
+  // Cross-wave argmax: one 64-bit LDS atomic max per wave on the key
+  //   (it << 45) | (bits << 13) | (8191 - index)
+  // so the largest distance wins and, among equal distances, the lowest index (clouds here have
+  // at most 8192 points and iterations).  Iteration it uses slot it % 2; the iteration number in
+  // the key's top bits makes every key of it larger than any left from it - 2, so no slot is
+  // ever cleared; a slot is reused only after the barrier that every reader of its previous
+  // round passed first.
+  __shared__ unsigned long long slots[2];
   __shared__ int hist[kCells];
   __shared__ uint32_t red[6][WAVES];
   extern __shared__ float4 table[];  // sort scratch (12 B/point), then positions by index
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   }
   __syncthreads();  // order[] is dead: the scratch becomes the position table
   for (int i = t; i < n; i += THREADS) table[i] = make_float4(P[3 * i], P[3 * i + 1], P[3 * i + 2], 0.f);
-  if (t < 3) slots[t] = 0ull;
+  if (t < 2) slots[t] = 0ull;
 
   // 4. bucket records: box in lane s (bucket of slot s); max min-distance bits and a cached
   //    lowest index attaining the max (invalidated by an update) as scalars bm[s], bi[s].
@@ -354,8 +357,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   bool dirty = true;
   __syncthreads();
 
-  int p = 1;  // it % 3
-  for (int it = 1; it < k; ++it, p = p == 2 ? 0 : p + 1) {
+  for (int it = 1; it < k; ++it) {
     float gx, gy, gz;
     {
 #pragma clang fp contract(off)
@@ -371,8 +373,10 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
 #pragma unroll
       for (int s = 0; s < PTS; ++s) {
         if (act & (1ull << s)) {
+          // distances are non-negative floats, ordered like their bit patterns: the running
+          // minimum is an integer min (no NaN canonicalisation step)
           const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
-          md[s] = __builtin_amdgcn_fmed3f(d, md[s], -__builtin_inff());
+          md[s] = __uint_as_float(min(__float_as_uint(d), __float_as_uint(md[s])));
           const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
           bm[s] = m;
           if (lane == s) bmax = m;
@@ -406,11 +410,14 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
       widx = best;
       dirty = false;
     }
+    // one lane of the wave issues the atomic (the build turns the atomic optimizer off for this
+    // file: its single-lane election would add three dependent VALU steps before the barrier)
     if (lane == 0)
-      atomicMax(&slots[p], (static_cast<unsigned long long>(wbits) << 32) | static_cast<uint32_t>(~widx));
-    if (t == 0) slots[p == 2 ? 0 : p + 1] = 0ull;
-    __syncthreads();
-    const uint32_t gidx = ~static_cast<uint32_t>(slots[p]);
+      atomicMax(&slots[it & 1], (static_cast<unsigned long long>(it) << 45) |
+                                    (static_cast<unsigned long long>(wbits) << 13) |
+                                    static_cast<unsigned long long>(8191u - (widx & 8191u)));
+    lds_barrier();  // waves share only LDS in this loop
+    const uint32_t gidx = 8191u - (static_cast<uint32_t>(slots[it & 1]) & 8191u);
     const float4 c = table[gidx];
     cx = c.x; cy = c.y; cz = c.z;
     if (t == 0) out_idx[o0 + it] = start + gidx;
@@ -470,7 +477,7 @@ __global__ __launch_bounds__(kFpsStreamThreads) void fps_stream_kernel(
     wave_argmax(bbits, bidx, wbits, widx);
     FpsSlot* sl = slots[it & 1];
     if (lane_id() == 0) sl[w] = FpsSlot{wbits, widx};
-    __syncthreads();
+    lds_barrier();  // each thread reads back only its own M entries: waves share only LDS
     uint32_t gbits = sl[0].dist_bits, gidx = sl[0].idx;
     for (int ww = 1; ww < kFpsStreamWaves; ++ww) {
       const FpsSlot o = sl[ww];
@@ -492,12 +499,14 @@ __global__ __launch_bounds__(kFpsStreamThreads) void fps_stream_kernel(
 // consecutive sorted points.  Positions (with the original index) and running min distances
 // stay in the workspace, 20 bytes per point, which for one cloud fits the L2 of the XCD that
 // runs it.  One 1024-thread workgroup per cloud; lane l of wave w holds the records of buckets
-// w + 16 (l + 64 r), r < kFpsLargeSlots: box, max min-distance, lowest index attaining it and
-// that point's position.  Per iteration each wave tests its buckets with the exact lower bound
-// above, reloads and updates only the buckets the new centroid can change (two at a time, so
-// their loads overlap), recomputes its best (distance, index) only when one of its buckets
-// changed, and the workgroup agrees on the winner with one LDS 64-bit atomic max per wave on
-// (bits << 32) | (index complement << 4 | wave) and one barrier.
+// w + 16 (l + 64 r), r < kFpsLargeSlots: box, max min-distance, lowest index attaining it, the
+// lane of that point and its position.  Per iteration each wave tests its buckets with the exact
+// lower bound above, reloads and updates only the buckets the new centroid can change (two at a
+// time, so their loads overlap), re-reduces a bucket's record only when the point holding its
+// maximum fell (C5: 12% of touched buckets), rescans its best (distance, index) only when the
+// bucket that best came from changed (about one wave per iteration: the winner's), and the
+// workgroup agrees on the winner with one LDS 64-bit atomic max per wave on
+// (bits << 32) | (index complement << 4 | wave) and one LDS-only barrier.
 constexpr int kFpsLargeThreads = 1024;
 constexpr int kFpsLargeWaves = kFpsLargeThreads / kWave;
 constexpr int kFpsLargeSlots = 3;
@@ -616,9 +625,10 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
 
   // Bucket records of this lane (empty buckets: +inf box, max 0, never tested or chosen).
   float blx[S], bly[S], blz[S], bhx[S], bhy[S], bhz[S], bcx[S], bcy[S], bcz[S];
-  uint32_t bmax[S], bidx[S];
+  uint32_t bmax[S], bidx[S], blane[S];  // blane: lane (point) holding the max, 64 = unknown
 #pragma unroll
   for (int r = 0; r < S; ++r) {
+    blane[r] = kWave;
     blx[r] = bly[r] = blz[r] = __builtin_inff();
     bhx[r] = bhy[r] = bhz[r] = -__builtin_inff();
     bcx[r] = bcy[r] = bcz[r] = 0.f;
@@ -647,21 +657,29 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
   unsigned long long best_key = 0ull;
   float4 best_c = make_float4(0.f, 0.f, 0.f, 0.f);
   bool dirty = true;
+  int best_r = -1, best_l = 0;  // the bucket the wave's best record comes from (slot, lane)
   __syncthreads();
+
+  // slots that hold buckets at all: slot r holds buckets [1024 r, 1024 (r + 1)); the others are
+  // neither tested nor searched
+  const int s_used = (nb + kFpsLargeThreads - 1) / kFpsLargeThreads;
 
   for (int it = 1; it < k; ++it) {
     uint64_t act[S];
 #pragma unroll
     for (int r = 0; r < S; ++r) {
-      float gx, gy, gz;
-      {
+      act[r] = 0ull;
+      if (r < s_used) {  // wave-uniform
+        float gx, gy, gz;
+        {
 #pragma clang fp contract(off)
-        gx = fmaxf(fmaxf(blx[r] - cx, cx - bhx[r]), 0.f);
-        gy = fmaxf(fmaxf(bly[r] - cy, cy - bhy[r]), 0.f);
-        gz = fmaxf(fmaxf(blz[r] - cz, cz - bhz[r]), 0.f);
+          gx = fmaxf(fmaxf(blx[r] - cx, cx - bhx[r]), 0.f);
+          gy = fmaxf(fmaxf(bly[r] - cy, cy - bhy[r]), 0.f);
+          gz = fmaxf(fmaxf(blz[r] - cz, cz - bhz[r]), 0.f);
+        }
+        const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
+        act[r] = __ballot(__float_as_uint(lb) < bmax[r]);
       }
-      const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
-      act[r] = __ballot(__float_as_uint(lb) < bmax[r]);
     }
     while (act[0] | act[1] | act[2]) {
       // up to two affected buckets of this wave per round, their loads issued together (C5:
@@ -687,8 +705,12 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
       for (int j = 0; j < G; ++j) {
         const int q = (w + kFpsLargeWaves * (ll[j] + kWave * (rr[j] < 0 ? 0 : rr[j]))) * kWave + lane;
         v[j] = rr[j] >= 0 && q < n;
-        p[j] = Q[v[j] ? q : 0];
-        mo[j] = M[v[j] ? q : 0];
+        p[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        mo[j] = 0.f;
+        if (rr[j] >= 0) {  // wave-uniform: no load left in flight for an unused slot
+          p[j] = Q[v[j] ? q : 0];
+          mo[j] = M[v[j] ? q : 0];
+        }
       }
 #pragma unroll
       for (int j = 0; j < G; ++j) {
@@ -696,43 +718,87 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
         const int q = (w + kFpsLargeWaves * (ll[j] + kWave * rr[j])) * kWave + lane;
         const float d = sqdist(p[j].x, p[j].y, p[j].z, cx, cy, cz);
         const float m = __builtin_amdgcn_fmed3f(d, mo[j], -__builtin_inff());
-        if (v[j] && m < mo[j]) M[q] = m;
+        const bool fell = v[j] && m < mo[j];
+        if (fell) M[q] = m;
+        // Values only fall, so while the point holding the bucket's maximum keeps its value the
+        // record (max, lowest index attaining it) stands: no other point can reach the max, and
+        // points tied with it have higher indices.  Most touched buckets end here.
+        const uint32_t al = static_cast<uint32_t>(__builtin_amdgcn_readlane(
+            static_cast<int>(rr[j] == 0 ? blane[0] : (rr[j] == 1 ? blane[1] : blane[2])), ll[j]));
+        if (al < static_cast<uint32_t>(kWave) && !((__ballot(fell) >> al) & 1ull)) continue;
         const uint32_t bits = v[j] ? __float_as_uint(m) : 0u;
         const uint32_t bm = wave_max_u32(bits);
         const uint32_t li = __float_as_uint(p[j].w) - ustart;
-        const uint32_t ii = wave_min_u32(v[j] && bits == bm ? li : 0xffffffffu);
-        const uint64_t src = __ballot(v[j] && bits == bm && li == ii);
-        const int sl = __builtin_ctzll(src | (1ull << 63));
+        const uint64_t at = __ballot(v[j] && bits == bm);
+        uint32_t ii;
+        int sl;
+        if (__builtin_popcountll(at) == 1) {  // wave-uniform; the usual case: one lane attains it
+          sl = __builtin_ctzll(at);
+          ii = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(li), sl));
+        } else {  // ties: the lowest index among them
+          ii = wave_min_u32(v[j] && bits == bm ? li : 0xffffffffu);
+          sl = __builtin_ctzll(__ballot(v[j] && bits == bm && li == ii) | (1ull << 63));
+        }
         const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].x), sl));
         const float y = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].y), sl));
         const float z = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j].z), sl));
-#pragma unroll
-        for (int r = 0; r < S; ++r) {
-          if (r == rr[j] && lane == ll[j]) {
-            bmax[r] = bm; bidx[r] = ii; bcx[r] = x; bcy[r] = y; bcz[r] = z;
+        if (lane == ll[j]) {
+          if (rr[j] == 0) {
+            bmax[0] = bm; bidx[0] = ii; blane[0] = sl; bcx[0] = x; bcy[0] = y; bcz[0] = z;
+          } else if (rr[j] == 1) {
+            bmax[1] = bm; bidx[1] = ii; blane[1] = sl; bcx[1] = x; bcy[1] = y; bcz[1] = z;
+          } else {
+            bmax[2] = bm; bidx[2] = ii; blane[2] = sl; bcx[2] = x; bcy[2] = y; bcz[2] = z;
           }
         }
+        // a record's key (max, then lower index) never rises, so only a change of the bucket the
+        // wave's best came from can change the wave's best
+        if (rr[j] == best_r && ll[j] == best_l) dirty = true;
       }
-      dirty = true;
     }
     if (dirty) {  // the wave's best record: largest max, then lowest index
-      uint32_t lh = 0u, llo = 0u;
-      float ex = 0.f, ey = 0.f, ez = 0.f;
+      uint32_t m3 = 0u;
+#pragma unroll
+      for (int r = 0; r < S; ++r) m3 = max(m3, bmax[r]);
+      const uint32_t wh = wave_max_u32(m3);
+      uint64_t e[S];
+      int cnt = 0;
 #pragma unroll
       for (int r = 0; r < S; ++r) {
-        const uint32_t h = bmax[r];
-        const uint32_t l = bidx[r] <= kFpsLargeIdxMask
-                               ? ((kFpsLargeIdxMask - bidx[r]) << 4) | static_cast<uint32_t>(w)
-                               : 0u;
-        if (h > lh || (h == lh && l > llo)) { lh = h; llo = l; ex = bcx[r]; ey = bcy[r]; ez = bcz[r]; }
+        e[r] = __ballot(bmax[r] == wh && bidx[r] != 0xffffffffu);
+        cnt += __builtin_popcountll(e[r]);
       }
-      const uint32_t wh = wave_max_u32(lh);
-      const uint32_t wl = wave_max_u32(lh == wh ? llo : 0u);
-      const int sl = __builtin_ctzll(__ballot(lh == wh && llo == wl) | (1ull << 63));
-      best_key = (static_cast<unsigned long long>(wh) << 32) | wl;
-      best_c = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), sl)),
-                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ey), sl)),
-                           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ez), sl)), 0.f);
+      if (cnt != 1) {  // wave-uniform: ties (or no bucket at all): the lowest index among them
+        uint32_t li = 0xffffffffu;
+#pragma unroll
+        for (int r = 0; r < S; ++r) li = bmax[r] == wh ? min(li, bidx[r]) : li;
+        const uint32_t mi = wave_min_u32(li);
+#pragma unroll
+        for (int r = 0; r < S; ++r) e[r] = __ballot(bmax[r] == wh && bidx[r] == mi && mi != 0xffffffffu);
+      }
+      const int rs = e[0] ? 0 : (e[1] ? 1 : (e[2] ? 2 : -1));
+      best_r = rs;
+      if (rs < 0) {  // a wave without buckets never wins
+        best_key = 0ull;
+      } else {
+        const int ls = __builtin_ctzll(rs == 0 ? e[0] : (rs == 1 ? e[1] : e[2]));
+        best_l = ls;
+        uint32_t bi;
+        float ex, ey, ez;
+        if (rs == 0) {
+          bi = bidx[0]; ex = bcx[0]; ey = bcy[0]; ez = bcz[0];
+        } else if (rs == 1) {
+          bi = bidx[1]; ex = bcx[1]; ey = bcy[1]; ez = bcz[1];
+        } else {
+          bi = bidx[2]; ex = bcx[2]; ey = bcy[2]; ez = bcz[2];
+        }
+        bi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bi), ls));
+        best_key = (static_cast<unsigned long long>(wh) << 32) |
+                   (((kFpsLargeIdxMask - bi) << 4) | static_cast<uint32_t>(w));
+        best_c = make_float4(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), ls)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ey), ls)),
+                             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ez), ls)), 0.f);
+      }
       dirty = false;
     }
     const int ps = it % 3;
@@ -741,7 +807,7 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
       atomicMax(&slots[ps], best_key);
     }
     if (t == 0) slots[ps == 2 ? 0 : ps + 1] = 0ull;
-    __syncthreads();
+    lds_barrier();  // each bucket's points are read and written by its own wave only
     const unsigned long long key = slots[ps];
     const uint32_t low = static_cast<uint32_t>(key);
     const float4 c = cand[it & 1][low & 15u];
