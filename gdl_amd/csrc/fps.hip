@@ -4,19 +4,23 @@
 // CPU path _fps_iterative_fallback (geoembodied/csrc/__init__.py:600-654): start at the first
 // point of the cloud, each step take the LOWEST index attaining max(min squared distance).
 //
-// Three kernels, chosen by the largest cloud of the batch:
+// Four kernels, chosen by the largest cloud of the batch:
 //   bucketed (clouds of up to 8192 points, the common case): one 1024-thread workgroup per
 //     cloud, points ordered along a Morton cell grid so that each register slot of a wave holds
 //     a compact bucket of 64 points; a bucket is only updated when the new centroid can lower
 //     one of its distances (an exact test, see below), and the argmax is assembled from cached
 //     per-bucket maxima.
-//   register (up to 16384 points): thread t owns local points t, t+256, ... (PTS of them) with
-//     x, y, z and the running min distance in VGPRs; every point is updated every iteration.
+//   register (8193 to 16384 points): thread t owns local points t, t+256, ... (PTS of them)
+//     with x, y, z and the running min distance in VGPRs; every point is updated every
+//     iteration.
+//   large (16385 to 196,608 points): the bucket scheme with points sorted by Morton code in the
+//     workspace and bucket records in registers (see its section below).
 //   streaming (larger clouds): positions read from HBM/L2 each iteration, running min
 //     distance in the workspace.
-// All three reduce (distance bits, index) per iteration as: wave max of the bits (DPP), then
-// the lowest index among the lanes holding it, then one LDS record per wave, double-buffered
-// by iteration parity so that a single barrier per iteration suffices.  Squared distances are
+// Each reduces (distance bits, index) per iteration to one winner with one barrier: a wave max
+// of the bits (DPP), the lowest index among the lanes holding it, then either one LDS record per
+// wave double-buffered by iteration parity (register, streaming) or one LDS 64-bit atomic max per
+// wave on a (distance, index complement) key (bucketed, large).  Squared distances are
 // non-negative floats, whose bit patterns order like the values.
 #include "radix.hpp"
 
@@ -174,9 +178,10 @@ __global__ __launch_bounds__(kFpsThreads) void fps_register_kernel(
 // Clouds of up to 8192 points.  The cloud is first ordered along a 16^3 Morton cell grid
 // (LDS counting sort), so the 64 points a wave holds in one register slot — a bucket — lie
 // close together.  Each bucket keeps its bounding box in lane s of six VGPRs and its (max
-// min-distance, lowest index attaining it) as wave-uniform scalars, so a wave's best is a few
-// scalar max / compare instructions after an update instead of another cross-lane reduction.  Per iteration the wave tests all its buckets at once
-// (one lane per bucket): with
+// min-distance, lowest index attaining it, lane holding that point) as wave-uniform scalars, so
+// a wave's best is a few scalar max / compare instructions after an update instead of another
+// cross-lane reduction, and an updated bucket is re-reduced only when the point holding its
+// maximum fell.  Per iteration the wave tests all its buckets at once (one lane per bucket): with
 //   g_a = max(lo_a - c_a, c_a - hi_a, 0),  lb = (g_x*g_x + g_y*g_y) + g_z*g_z
 // evaluated with the same fp32 operations as the distance, every rounded operation is monotone,
 // so lb <= d(p, c) holds exactly for every point p of the bucket; when lb >= the bucket's max
@@ -323,15 +328,14 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   for (int i = t; i < n; i += THREADS) table[i] = make_float4(P[3 * i], P[3 * i + 1], P[3 * i + 2], 0.f);
   if (t < 2) slots[t] = 0ull;
 
-  // 4. bucket records: box in lane s (bucket of slot s); max min-distance bits and a cached
-  //    lowest index attaining the max (invalidated by an update) as scalars bm[s], bi[s].
+  // 4. bucket records: box in lane s (bucket of slot s); max min-distance bits, lowest index
+  //    attaining the max and the lane holding that point as scalars bm[s], bi[s], al[s].
   float blx = __builtin_inff(), bly = __builtin_inff(), blz = __builtin_inff();
   float bhx = -__builtin_inff(), bhy = -__builtin_inff(), bhz = -__builtin_inff();
   uint32_t bmax = 0u;
-  // Bucket maxima and cached lowest indices attaining them are wave-uniform: kept as scalars
-  // (bm, bi), with bmax (lane s = bucket s) the per-lane copy the skip test reads.
-  uint32_t bm[PTS], bi[PTS];
-  uint64_t stale = 0;  // buckets whose cached index is out of date
+  // Bucket records are wave-uniform, kept as scalars; bmax (lane s = bucket s) is the per-lane
+  // copy of bm the bound test reads.
+  uint32_t bm[PTS], bi[PTS], al[PTS];  // al: lane holding the max (lowest index), kWave = unknown
 #pragma unroll
   for (int s = 0; s < PTS; ++s) {
     const bool valid = oi[s] != 0xffffffffu;
@@ -344,6 +348,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const uint32_t mi = wave_min_u32(oi[s]);
     bm[s] = mi != 0xffffffffu ? 0x7f800000u : 0u;
     bi[s] = 0xffffffffu;
+    al[s] = kWave;
     if (lane == s && mi != 0xffffffffu) {
       blx = float_from_order_key(l0); bly = float_from_order_key(l1); blz = float_from_order_key(l2);
       bhx = float_from_order_key(h0); bhy = float_from_order_key(h1); bhz = float_from_order_key(h2);
@@ -368,45 +373,44 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const float lb = sqdist(gx, gy, gz, 0.f, 0.f, 0.f);
     const uint64_t act = __ballot(__float_as_uint(lb) < bmax);  // bmax = 0 on lanes >= PTS
     if (act) {
-      stale |= act;
-      dirty = true;
 #pragma unroll
       for (int s = 0; s < PTS; ++s) {
         if (act & (1ull << s)) {
           // distances are non-negative floats, ordered like their bit patterns: the running
           // minimum is an integer min (no NaN canonicalisation step)
           const float d = sqdist(px[s], py[s], pz[s], cx, cy, cz);
-          md[s] = __uint_as_float(min(__float_as_uint(d), __float_as_uint(md[s])));
-          const uint32_t m = wave_max_u32(__float_as_uint(md[s]));
+          const uint32_t old = __float_as_uint(md[s]);
+          const uint32_t mb = min(__float_as_uint(d), old);
+          md[s] = __uint_as_float(mb);
+          // Values only fall: while the point holding the bucket's max keeps its value, the
+          // record (max, lowest index attaining it) stands.  Most touched buckets end here.
+          if (al[s] < static_cast<uint32_t>(kWave) && !((__ballot(mb < old) >> al[s]) & 1ull))
+            continue;
+          const uint32_t m = wave_max_u32(mb);
           bm[s] = m;
           if (lane == s) bmax = m;
+          const uint64_t hit = __ballot(mb == m);
+          if ((hit & (hit - 1)) == 0) {  // one lane holds the maximum (distance ties are rare)
+            al[s] = static_cast<uint32_t>(__builtin_ctzll(hit));
+            bi[s] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(oi[s]), al[s]));
+          } else {
+            bi[s] = wave_min_u32(mb == m ? oi[s] : 0xffffffffu);
+            al[s] = static_cast<uint32_t>(__builtin_ctzll(__ballot(mb == m && oi[s] == bi[s]) | (1ull << 63)));
+          }
+          dirty = true;
         }
       }
     }
     if (dirty) {
-      // wave best: the largest bucket max (scalar), then the lowest index over the buckets
-      // holding it, refreshing the cached index of a tied bucket that changed
+      // wave best: the largest bucket max, then the lowest index among the buckets holding it
+      // (all scalars)
       uint32_t wb = 0u;
 #pragma unroll
       for (int s = 0; s < PTS; ++s) wb = bm[s] > wb ? bm[s] : wb;
       wbits = wb;
       uint32_t best = 0xffffffffu;
 #pragma unroll
-      for (int s = 0; s < PTS; ++s) {
-        if (bm[s] == wb) {
-          if ((stale >> s) & 1ull) {
-            const uint32_t mb = __float_as_uint(md[s]);
-            const uint64_t hit = __ballot(mb == wb);
-            // one lane holds the maximum (distance ties are rare): take its index directly
-            bi[s] = (hit & (hit - 1)) == 0
-                        ? static_cast<uint32_t>(__builtin_amdgcn_readlane(
-                              static_cast<int>(oi[s]), __builtin_ctzll(hit | (1ull << 63))))
-                        : wave_min_u32(mb == wb ? oi[s] : 0xffffffffu);
-            stale &= ~(1ull << s);
-          }
-          best = bi[s] < best ? bi[s] : best;
-        }
-      }
+      for (int s = 0; s < PTS; ++s) best = (bm[s] == wb && bi[s] < best) ? bi[s] : best;
       widx = best;
       dirty = false;
     }
