@@ -7,6 +7,7 @@ operation raises ``RuntimeError`` naming the path that was tried.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -168,6 +169,17 @@ def ptr(t: torch.Tensor | None):
 
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def on_device(device: torch.device):
+    """Context making ``device`` the current HIP device for a library call: a shared no-op
+    context when it already is (entering torch.cuda.device costs microseconds per call)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _SAME_DEVICE
+    return torch.cuda.device(device)
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

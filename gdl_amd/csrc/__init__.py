@@ -157,7 +157,7 @@ def radius_graph_csr_hip(
             raise ValueError(f"radius_graph: mask has {mask.numel()} entries for {N} points")
         mask_u8 = mask.to(device=dev, dtype=torch.bool).reshape(-1).contiguous().view(torch.uint8)
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         s = _nat.stream_of(dev)
         ws_bytes = L.geo_radius_workspace_bytes(N, B, K)
         ws = _nat.workspace(ws_bytes, dev)
@@ -262,7 +262,7 @@ def sort_and_build_csr_cuda(col: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor
     node_start = torch.empty(N, **i32)
     node_end = torch.empty(N, **i32)
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         ws_bytes = L.geo_csr_workspace_bytes(E, N)
         ws = _nat.workspace(ws_bytes, dev)
         _nat.check(L.geo_csr_build(_nat.ptr(col), E, N, _nat.ptr(col_sorted), _nat.ptr(perm),
@@ -297,7 +297,11 @@ def _dtype_code(name: str, t: Tensor) -> int:
 
 
 def _i32(t: Optional[Tensor], device: torch.device) -> Optional[Tensor]:
-    return None if t is None else t.to(device=device, dtype=torch.int32).contiguous()
+    if t is None:
+        return None
+    if t.dtype == torch.int32 and t.device == device and t.is_contiguous():
+        return t
+    return t.to(device=device, dtype=torch.int32).contiguous()
 
 
 def segment_reduce_forward_hip(
@@ -328,7 +332,7 @@ def segment_reduce_forward_hip(
     ns, ne = _i32(node_start, dev), _i32(node_end, dev)
     out = torch.empty(N, C, dtype=msg.dtype, device=dev)
     arg = torch.empty(N, C, dtype=torch.int32, device=dev) if reduce == "max" else None
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_segment_reduce_fwd(
             _nat.REDUCE_CODES[reduce], code, _nat.ptr(msg), _nat.ptr(perm), _nat.ptr(ns),
             _nat.ptr(ne), E, N, C, _nat.ptr(out), _nat.ptr(arg), int(tie_mode),
@@ -364,7 +368,7 @@ def segment_reduce_backward_hip(
         out = out.to(grad_out.dtype).contiguous()
     if arg is not None:
         arg = arg.contiguous()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_segment_reduce_bwd(
             _nat.REDUCE_CODES[reduce], code, _nat.ptr(grad_out), _nat.ptr(msg), _nat.ptr(out),
             _nat.ptr(arg), _nat.ptr(cs), _nat.ptr(pm), _nat.ptr(ns), _nat.ptr(ne), int(E), S, C,
@@ -412,7 +416,7 @@ def segment_softmax_forward_hip(
         raise ValueError(f"segment_softmax: perm has {pm.numel()} entries for E={E}")
     ns, ne = _i32(node_start, dev), _i32(node_end, dev)
     out = torch.empty_like(scores) if contiguous_csr else torch.zeros_like(scores)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_segment_softmax_fwd(
             _nat.DTYPE_CODES[scores.dtype], _nat.ptr(scores), _nat.ptr(pm), _nat.ptr(ns),
             _nat.ptr(ne), E, N, H, int(bool(contiguous_csr)), _nat.ptr(out), _nat.stream_of(dev)),
@@ -439,7 +443,7 @@ def segment_softmax_backward_hip(
     pm = _i32(perm, dev)
     ns, ne = _i32(node_start, dev), _i32(node_end, dev)
     grad = torch.empty_like(out) if contiguous_csr else torch.zeros_like(out)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_segment_softmax_bwd(
             _nat.DTYPE_CODES[out.dtype], _nat.ptr(grad_out), _nat.ptr(out), _nat.ptr(pm),
             _nat.ptr(ns), _nat.ptr(ne), E, int(N), H, int(bool(contiguous_csr)), _nat.ptr(grad),
@@ -460,7 +464,7 @@ def gather_weighted_sum_forward_hip(feat: Tensor, idx: Tensor, w: Tensor) -> Ten
     w = w.to(device=dev, dtype=feat.dtype).contiguous()
     (N_src, C), (N_out, K) = feat.shape, idx.shape
     out = torch.empty(N_out, C, dtype=feat.dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_gather_weighted_sum(
             code, _nat.ptr(feat), N_src, C, _nat.ptr(idx), _nat.ptr(w), N_out, K, _nat.ptr(out),
             _nat.stream_of(dev)), "geo_gather_weighted_sum")
@@ -493,7 +497,7 @@ def gather_weighted_sum_backward_hip(
         if csr is None:
             csr = sort_and_build_csr_cuda(idx.reshape(-1), N_src)
         _, pm, ns, ne = csr
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_gather_weighted_sum_bwd(
             code, _nat.ptr(grad_out), _nat.ptr(feat), _nat.ptr(w), _nat.ptr(idx), N_src, C,
             N_out, K, _nat.ptr(pm), _nat.ptr(ns), _nat.ptr(ne), _nat.ptr(grad_feat),
@@ -511,7 +515,7 @@ def idw_weights_hip(idx: Tensor, dist: Tensor) -> Tensor:
         raise ValueError("idw_weights: idx and dist must both be [N_out, K]")
     N_out, K = idx.shape
     w = torch.empty(N_out, K, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_idw_weights(_nat.ptr(idx), _nat.ptr(dist), N_out, K, _nat.ptr(w),
                                               _nat.stream_of(dev)), "geo_idw_weights")
     return w
@@ -531,7 +535,7 @@ def knn_radius_stat_hip(dist: Tensor, col: int, mode: str, multiplier: float) ->
     N, k = d.shape
     out = torch.empty((), dtype=torch.float64, device=dev)
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         ws_bytes = L.geo_knn_radius_stat_workspace_bytes(N)
         ws = _nat.workspace(ws_bytes, dev)
         _nat.check(L.geo_knn_radius_stat(_nat.ptr(d), N, k, int(col) % k, codes[mode],
@@ -551,7 +555,7 @@ def edge_geometry_hip(pos: Tensor, row: Tensor, col: Tensor, max_l: int = 2,
     direction = torch.empty(E, 3, dtype=torch.float32, device=dev)
     dist = torch.empty(E, dtype=torch.float32, device=dev)
     Y = torch.empty(E, (max_l + 1) ** 2, dtype=torch.float32, device=dev) if with_sh else None
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_edge_geometry(
             _nat.ptr(pos), pos.shape[0], _nat.ptr(row), _nat.ptr(col), E, int(max_l),
             _nat.ptr(direction), _nat.ptr(dist), _nat.ptr(Y), _nat.stream_of(dev)), "geo_edge_geometry")
@@ -570,7 +574,7 @@ def edge_geometry_backward_hip(direction: Tensor, dist: Tensor, grad_direction: 
         return None if t is None else t.to(torch.float32).contiguous()
 
     gd, gl, gy = f32(grad_direction), f32(grad_dist), f32(grad_Y)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_edge_geometry_bwd(
             _nat.ptr(direction), _nat.ptr(dist), _nat.ptr(gd), _nat.ptr(gl), _nat.ptr(gy), E,
             int(max_l), _nat.ptr(out), _nat.stream_of(dev)), "geo_edge_geometry_bwd")
@@ -586,7 +590,7 @@ def spherical_harmonics_hip(xyz: Tensor, max_l: int, normalize: bool):
     Y = torch.empty(N, (max_l + 1) ** 2, dtype=torch.float32, device=dev)
     unit = torch.empty(N, 3, dtype=torch.float32, device=dev) if normalize else None
     norm = torch.empty(N, dtype=torch.float32, device=dev) if normalize else None
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_spherical_harmonics(
             _nat.ptr(xyz), N, int(max_l), int(bool(normalize)), _nat.ptr(Y), _nat.ptr(unit),
             _nat.ptr(norm), _nat.stream_of(dev)), "geo_spherical_harmonics")
@@ -598,7 +602,7 @@ def spherical_harmonics_backward_hip(xyz: Tensor, grad_Y: Tensor, max_l: int) ->
     N = xyz.shape[0]
     out = torch.empty(N, 3, dtype=torch.float32, device=dev)
     gY = grad_Y.to(torch.float32).contiguous()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_spherical_harmonics_bwd(
             _nat.ptr(xyz), _nat.ptr(gY), N, int(max_l), _nat.ptr(out), _nat.stream_of(dev)),
             "geo_spherical_harmonics_bwd")
@@ -614,7 +618,7 @@ def graph_avg_degree_hip(row_ptr: Tensor, N: int, batch: Optional[Tensor], B: in
     ppc = 0 if batch is not None else N // max(B, 1)
     b = None if batch is None else _i64(batch.reshape(-1), dev)
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         ws_bytes = L.geo_graph_avg_degree_workspace_bytes(B)
         ws = _nat.workspace(ws_bytes, dev)
         _nat.check(L.geo_graph_avg_degree(_nat.ptr(row_ptr.contiguous()), N, _nat.ptr(b), B, ppc,
@@ -658,7 +662,7 @@ def knn_cuda(
     if Nq == 0 or k == 0:
         return out_idx, out_d
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         ws_bytes = L.geo_knn_workspace_bytes(Nq, Ns, max(B, 0), k)
         ws = _nat.workspace(ws_bytes, dev)
         _nat.check(L.geo_knn(_nat.ptr(q), Nq, _nat.ptr(s), Ns, _nat.ptr(pq), _nat.ptr(ps),
@@ -726,7 +730,7 @@ def fps_uniform_hip(pos: Tensor, ptr: Tensor, num_samples: int) -> Tensor:
     N = pos.shape[0]
     k = max(int(num_samples), 0)
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         s = _nat.stream_of(dev)
         out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
         info = torch.empty(3, dtype=torch.int64, device=dev)
@@ -762,7 +766,7 @@ def _fps_run(pos: Tensor, p: Tensor, B: int, prepare) -> Tensor:
     dev = pos.device
     N = pos.shape[0]
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         s = _nat.stream_of(dev)
         out_ptr = torch.empty(B + 1, dtype=torch.int64, device=dev)
         info = torch.empty(3, dtype=torch.int64, device=dev)

@@ -63,7 +63,12 @@ def segment_softmax(
     then writes those zeros itself instead of the output being zero-filled first."""
     squeeze = scores.dim() == 1
     x = _compute_dtype(scores.unsqueeze(-1) if squeeze else scores)
-    out = _SegmentSoftmax.apply(x, perm, node_start, node_end, int(num_nodes), bool(contiguous_csr))
+    if torch.is_grad_enabled() and x.requires_grad:
+        out = _SegmentSoftmax.apply(x, perm, node_start, node_end, int(num_nodes),
+                                    bool(contiguous_csr))
+    else:  # nothing to differentiate: the kernel call without the autograd node
+        out = segment_softmax_forward_hip(x, perm, node_start, node_end, int(num_nodes),
+                                          bool(contiguous_csr))
     return out.squeeze(-1) if squeeze else out
 
 

@@ -114,7 +114,7 @@ class SpatialGraph:
         L = _nat.lib()
         if torch.is_grad_enabled() and pos.requires_grad:
             # differentiable geometry (autograd function), CSR arrays and degrees separately
-            with torch.cuda.device(dev):
+            with _nat.on_device(dev):
                 _nat.check(L.geo_csr_from_row_ptr(
                     _nat.ptr(row_ptr), N, _nat.ptr(col), E, _nat.ptr(col_sorted), _nat.ptr(perm),
                     _nat.ptr(node_start), _nat.ptr(node_end), _nat.stream_of(dev)),
@@ -129,7 +129,7 @@ class SpatialGraph:
             dist = fbuf[3 * E:4 * E]
             Y = fbuf[4 * E:(4 + nsh) * E].view(E, nsh)
             avg = fbuf[(4 + nsh) * E:]
-            with torch.cuda.device(dev):
+            with _nat.on_device(dev):
                 ws_bytes = L.geo_graph_avg_degree_workspace_bytes(B)
                 ws = _nat.workspace(ws_bytes, dev)
                 _nat.check(L.geo_spatial_graph_epilogue(

@@ -165,7 +165,7 @@ def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Ten
     Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 else None
     Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 else None
     mask_u8 = _u8(mask)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
         _nat.check(L.geo_se3_aggregate_fwd(
@@ -223,7 +223,7 @@ def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tens
     Xt = Xt if p.Ot > 0 else None
     need_s, need_v, need_t, need_dir, need_Y, need_R, need_bias = need[:7]
     need_W = need[7:16]
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
 
@@ -469,7 +469,7 @@ def _radial_op(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tenso
     H, NB = W1.shape
     P = W2.shape[0]
     R = torch.empty(E, P, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         _nat.check(_nat.lib().geo_radial_mlp_fwd(
             _nat.ptr(dist), E, _nat.ptr(freqs), NB, float(cutoff), _nat.ptr(W1), _nat.ptr(b1), H,
             _nat.ptr(W2), _nat.ptr(b2), P, _nat.ptr(R), _nat.stream_of(dev)), "geo_radial_mlp_fwd")
@@ -494,7 +494,7 @@ def _radial_bwd_op(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: T
     outs = [torch.empty(sh, **f32) if n else None for sh, n in zip(shapes, need)]
     g = dR.to(torch.float32).contiguous()
     L = _nat.lib()
-    with torch.cuda.device(dev):
+    with _nat.on_device(dev):
         nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E)
         ws = _nat.workspace(nbytes, dev)
         _nat.check(L.geo_radial_mlp_bwd(
