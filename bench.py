@@ -846,7 +846,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4) if ms_step is not None else None,
-        "ms_per_step_one_stream": legs.get("c2", {}).get("step_one_stream_ms"),
+        "c2_step_sequential_ms": legs.get("c2", {}).get("step_one_stream_ms"),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -867,7 +867,7 @@ def main() -> int:
     }
     if ms_step is not None:
         log(f"headline: {ms_step:.4f} ms/batch (two streams), "
-            f"{result['ms_per_step_one_stream']} ms/batch on one stream")
+            f"{result['c2_step_sequential_ms']} ms/batch sequential on one stream")
     print(json.dumps(result), flush=True)
     return 0
 
