@@ -687,8 +687,8 @@ __global__ __launch_bounds__(kFpsLargeThreads) void fps_large_kernel(
     }
     while (act[0] | act[1] | act[2]) {
       // up to two affected buckets of this wave per round, their loads issued together (C5:
-      // one or two per round 36.5 ms, three 37.3, four 38.6, eight 46.4: every slot of a round
-      // costs its loads and reductions, and the busiest wave rarely has more than two)
+      // two per round 27.3 ms, three 27.4, four 28.8: fewer rounds for the busiest wave, but
+      // every slot of a round costs its selection, address and bookkeeping)
       constexpr int G = 2;
       int rr[G], ll[G];
 #pragma unroll

@@ -71,6 +71,21 @@ def test_fps_large_tie_lattice(dev):
     _fps_check(dev, pos, _ptr([27000]), torch.tensor([3000]))
 
 
+def test_fps_duplicate_points(dev):
+    """Exact duplicates: once every distinct location is taken, every remaining point has min
+    distance 0 and the lowest index among them must be taken next.  This drives the bucket
+    records through ties at equal maxima (the point holding a bucket's maximum falls while an
+    equal value at a higher index stays), in the bucketed kernel (4096 points) and the
+    Morton-bucket kernel for large clouds (24,576 points)."""
+    g = torch.Generator().manual_seed(21)
+    base = torch.randn(1024, 3, generator=g)
+    pos = base[torch.randint(0, 1024, (4096,), generator=g)]
+    _fps_check(dev, pos, _ptr([4096]), torch.tensor([1500]))
+    big = torch.randn(3000, 3, generator=g)
+    pos2 = big[torch.randint(0, 3000, (24576,), generator=g)]
+    _fps_check(dev, pos2, _ptr([24576]), torch.tensor([4000]))
+
+
 def test_fps_tie_lattice(dev):
     pos = _lattice(8)  # 512 integer points: exact distances, many ties
     _fps_check(dev, pos, _ptr([512]), torch.tensor([200]))
