@@ -470,10 +470,14 @@ def leg_c3(args, dev) -> tuple:
     msg = torch.randn(E, C, device=dev, generator=gen)
     bytes_fwd = E * C * 4 + S * C * 4 + (S + 1) * 4
     iters = args.iters
+    # Warm-up of each timed C3 kernel: ~20 ms of launches.  The C2 CPU baseline before this leg
+    # leaves the GPU idle for seconds, and with 5 warm-up launches the first timed launches of a
+    # 0.4 ms kernel still run at a lower clock (0.415 against 0.397 ms per launch in steady state).
+    wu = 50
     leg: dict = {}
     roof = None
     if args.only in (None, "c3"):
-        ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, 5)
+        ms = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S), iters, wu)
         gbs = bytes_fwd / (ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": C3_SUM_TRAFFIC_BYTES,
@@ -484,14 +488,14 @@ def leg_c3(args, dev) -> tuple:
         for red in ("mean", "max"):
             extra = S * C * 4 if red == "max" else 0
             msr = event_ms(lambda: segment_reduce(msg, col_sorted, perm, ns, ne, S, reduce=red),
-                           iters, 5)
+                           iters, wu)
             leg[f"{red}_fp32_ms"] = round(msr, 4)
             leg[f"{red}_fp32_gbs"] = round((bytes_fwd + extra) / (msr * 1e-3) / 1e9, 1)
             log(f"  fwd {red} fp32: {msr:.4f} ms  {leg[f'{red}_fp32_gbs']} GB/s")
     if args.only in (None, "c3bf16"):
         mb = msg.bfloat16()
         bytes_b = E * C * 2 + S * C * 2 + (S + 1) * 4
-        msb = event_ms(lambda: segment_reduce(mb, col_sorted, perm, ns, ne, S), iters, 5)
+        msb = event_ms(lambda: segment_reduce(mb, col_sorted, perm, ns, ne, S), iters, wu)
         leg["sum_bf16_ms"] = round(msb, 4)
         leg["sum_bf16_gbs"] = round(bytes_b / (msb * 1e-3) / 1e9, 1)
         log(f"  fwd sum bf16: {msb:.4f} ms  {leg['sum_bf16_gbs']} GB/s")
@@ -501,12 +505,12 @@ def leg_c3(args, dev) -> tuple:
         bytes_bwd = S * C * 4 + E * C * 4 + (S + 1) * 4
         for red in ("sum", "mean"):
             msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, red),
-                           iters, 5)
+                           iters, wu)
             leg[f"bwd_{red}_fp32_gbs"] = round(bytes_bwd / (msb * 1e-3) / 1e9, 1)
             log(f"  bwd {red} fp32: {msb:.4f} ms  {leg[f'bwd_{red}_fp32_gbs']} GB/s")
         out, arg = segment_reduce_forward_hip(msg, perm, ns, ne, S, "max")
         msb = event_ms(lambda: segment_reduce_backward_hip(grad, col_sorted, perm, ns, ne, E, "max",
-                                                           msg=msg, out=out, arg=arg), iters, 5)
+                                                           msg=msg, out=out, arg=arg), iters, wu)
         leg["bwd_max_fp32_gbs"] = round((bytes_bwd + S * C * 4) / (msb * 1e-3) / 1e9, 1)
         log(f"  bwd max fp32: {msb:.4f} ms  {leg['bwd_max_fp32_gbs']} GB/s")
         del out, arg, grad
