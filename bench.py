@@ -41,7 +41,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of seg_fwd_merge_kernel<float,16,SUM,perm> on C3, from rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE x 1.0 (factors from a plain 1 GiB elementwise pass); the run and its arithmetic are
 # in profiles/seg_fwd_merge_kernel_c3_fp32.md.
-C3_SUM_TRAFFIC_BYTES = 2_329_600_000
+C3_SUM_TRAFFIC_BYTES = 2_327_800_000
 
 
 def log(*a):
