@@ -16,6 +16,9 @@
 #include "scan.hpp"
 
 namespace geo {
+// Internal linkage: every translation unit that includes this header gets its own copy of the
+// radix sort kernels and helpers, so no two units can share a definition built differently.
+namespace {
 
 constexpr int kRxThreads = 256;
 constexpr int kRxItems = 8;
@@ -284,4 +287,5 @@ int radix_sort(const void* keys, const uint32_t* vals, int64_t n, int64_t N, int
   return GEO_OK;
 }
 
+}  // namespace
 }  // namespace geo

@@ -5,6 +5,9 @@
 #include "common.hpp"
 
 namespace geo {
+// Internal linkage: every translation unit that includes this header gets its own copy of the
+// scan kernels and helpers, so no two units can share a definition built differently.
+namespace {
 
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 8;
@@ -303,4 +306,5 @@ int device_fill(T* p, int64_t n, T v, hipStream_t stream) {
   return GEO_OK;
 }
 
+}  // namespace
 }  // namespace geo
