@@ -143,7 +143,8 @@ int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
 // cell edge and shrunk by 1e-5 relative (the fp32 distance of a farther point can round down
 // by less than that).  The stop test is strict, so a source at exactly the k-th distance with a
 // smaller index cannot be missed.  Candidates arrive in cell order, so the register list keeps
-// the total order (d, j) explicitly.
+// the total order (d, j) explicitly, as one 64-bit key per entry (distance bits, index): one
+// unsigned compare per step instead of a distance compare plus an index tie-break.
 constexpr int kKnnGridThreads = 256;
 constexpr int kKnnSetupThreads = 1024;
 constexpr int kKnnGridMaxAxis = 1024;
@@ -339,23 +340,25 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_scatter(const float*
       make_float4(source[3 * i], source[3 * i + 1], source[3 * i + 2], __int_as_float(static_cast<int>(i)));
 }
 
-// (d, j) < (e, i) in the total order used throughout: distance, then source index.
-__device__ __forceinline__ bool knn_less(float d, int j, float e, int i) {
-  return d < e || (d == e && j < i);
+// Candidate key: the distance's bits above the source index.  Squared distances are
+// non-negative floats, whose bits order like the values, so one unsigned compare of keys gives
+// the total order used throughout: distance, then source index.  An empty slot holds ~0.
+__device__ __forceinline__ uint64_t knn_key(float d, int j) {
+  return (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(j);
 }
 
-// Sorted top-KMAX list of one lane; inserts (d, j) if it is among the KMAX smallest.
+// Sorted top-KMAX list of one lane; inserts (d, j) if it is among the KMAX smallest (infinite and
+// NaN distances never enter).
 template <int KMAX>
-__device__ __forceinline__ void knn_insert(float (&D)[KMAX], int (&J)[KMAX], float d, int j) {
-  if (d < __builtin_inff() && knn_less(d, j, D[KMAX - 1], J[KMAX - 1])) {
+__device__ __forceinline__ void knn_insert(uint64_t (&L)[KMAX], float d, int j) {
+  const uint64_t key = knn_key(d, j);
+  if (__float_as_uint(d) < 0x7f800000u && key < L[KMAX - 1]) {
 #pragma unroll
     for (int m = KMAX - 1; m > 0; --m) {
-      const bool shift = knn_less(d, j, D[m - 1], J[m - 1]);
-      const bool here = !shift && knn_less(d, j, D[m], J[m]);
-      D[m] = shift ? D[m - 1] : (here ? d : D[m]);
-      J[m] = shift ? J[m - 1] : (here ? j : J[m]);
+      const uint64_t kept = key < L[m] ? key : L[m];
+      L[m] = key < L[m - 1] ? L[m - 1] : kept;
     }
-    if (knn_less(d, j, D[0], J[0])) { D[0] = d; J[0] = j; }
+    L[0] = key < L[0] ? key : L[0];
   }
 }
 
@@ -363,34 +366,28 @@ __device__ __forceinline__ void knn_insert(float (&D)[KMAX], int (&J)[KMAX], flo
 // element-wise minimum of one list and the other reversed is bitonic and holds exactly the KMAX
 // smallest; half-cleaners sort it.  Both lanes end with the same list.
 template <int KMAX>
-__device__ __forceinline__ void knn_merge_xor(float (&D)[KMAX], int (&J)[KMAX], int mask) {
-  float PD[KMAX];
-  int PJ[KMAX];
+__device__ __forceinline__ void knn_merge_xor(uint64_t (&L)[KMAX], int mask) {
+  uint64_t P[KMAX];
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
-    PD[i] = __shfl_xor(D[i], mask, kWave);
-    PJ[i] = __shfl_xor(J[i], mask, kWave);
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(L[i])), mask, kWave));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(L[i] >> 32)), mask, kWave));
+    P[i] = (static_cast<uint64_t>(hi) << 32) | lo;
   }
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
-    const float od = PD[KMAX - 1 - i];
-    const int oj = PJ[KMAX - 1 - i];
-    const bool take = knn_less(od, oj, D[i], J[i]);
-    D[i] = take ? od : D[i];
-    J[i] = take ? oj : J[i];
+    const uint64_t o = P[KMAX - 1 - i];
+    L[i] = o < L[i] ? o : L[i];
   }
 #pragma unroll
   for (int sd = KMAX / 2; sd > 0; sd >>= 1) {
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
       if ((i & sd) == 0) {
-        const bool sw = knn_less(D[i + sd], J[i + sd], D[i], J[i]);
-        const float d0 = D[i];
-        const int j0 = J[i];
-        D[i] = sw ? D[i + sd] : d0;
-        J[i] = sw ? J[i + sd] : j0;
-        D[i + sd] = sw ? d0 : D[i + sd];
-        J[i + sd] = sw ? j0 : J[i + sd];
+        const uint64_t a = L[i], c = L[i + sd];
+        const bool sw = c < a;
+        L[i] = sw ? c : a;
+        L[i + sd] = sw ? a : c;
       }
     }
   }
@@ -423,16 +420,14 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_query(
   const int cx = knn_cell_coord(qx, g.ox, g.inv_h, g.dx, &ux);
   const int cy = knn_cell_coord(qy, g.oy, g.inv_h, g.dy, &uy);
   const int cz = knn_cell_coord(qz, g.oz, g.inv_h, g.dz, &uz);
-  constexpr int kNone = 0x7fffffff;
-  float D[KMAX];
-  int J[KMAX];
+  uint64_t L[KMAX];
 #pragma unroll
-  for (int i = 0; i < KMAX; ++i) { D[i] = __builtin_inff(); J[i] = kNone; }
+  for (int i = 0; i < KMAX; ++i) L[i] = ~0ull;
 
   auto visit = [&](int a, int e) {
     for (int p = a + gl; p < e; p += G) {
       const float4 s = w.spos[p];
-      knn_insert<KMAX>(D, J, sqdist(qx, qy, qz, s.x, s.y, s.z), __float_as_int(s.w));
+      knn_insert<KMAX>(L, sqdist(qx, qy, qz, s.x, s.y, s.z), __float_as_int(s.w));
     }
   };
   const int maxr = max(max(g.dx, g.dy), g.dz);
@@ -464,22 +459,24 @@ __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_query(
     if (gap == __builtin_inff()) break;  // every cell of the cloud visited
     const float gr = (gap - 1e-3f) * g.h;
     const float bound = gap > 1e-3f ? gr * gr * (1.0f - 1e-5f) : 0.0f;
+    const uint64_t bound_key = static_cast<uint64_t>(__float_as_uint(bound)) << 32;
     int below = 0;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) below += D[i] < bound ? 1 : 0;
+    for (int i = 0; i < KMAX; ++i) below += L[i] < bound_key ? 1 : 0;
 #pragma unroll
     for (int m = 1; m < G; m <<= 1) below += __shfl_xor(below, m, kWave);
     if (below >= k) break;
   }
 #pragma unroll
-  for (int m = 1; m < G; m <<= 1) knn_merge_xor<KMAX>(D, J, m);
+  for (int m = 1; m < G; m <<= 1) knn_merge_xor<KMAX>(L, m);
   int64_t* oi = out_idx + q * k;
   float* od = out_dist + q * k;
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
     if (i < k && i % G == gl) {
-      oi[i] = J[i] != kNone ? static_cast<int64_t>(J[i]) : -1;
-      od[i] = J[i] != kNone ? D[i] : 1e30f;
+      const bool any = L[i] != ~0ull;
+      oi[i] = any ? static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(L[i]))) : -1;
+      od[i] = any ? __uint_as_float(static_cast<uint32_t>(L[i] >> 32)) : 1e30f;
     }
   }
 }
