@@ -152,6 +152,8 @@ constexpr int kKnnGridMaxK = 32;
 constexpr double kKnnCellTarget = 0.25;  // points per cell per neighbour (measured best)
 constexpr int kKnnCellCap = 2;            // cells per point
 constexpr int64_t kKnnWideSources = 65536; // one cloud this large: 32 lanes per query for k <= 8
+constexpr int kKnnBoxParts = 64;           // most workgroups per cloud for the bounding box
+constexpr int64_t kKnnBoxChunk = 16384;    // points per bounding-box workgroup
 
 struct KnnGrid {
   float ox, oy, oz, inv_h, h;
@@ -166,6 +168,7 @@ struct KnnGridWs {
   int32_t* pt_cell;
   int32_t* pt_rank;
   float4* spos;
+  uint32_t* box_part;  // [B][kKnnBoxParts][6] partial bounding boxes (order keys)
   int64_t cells_max;
 };
 
@@ -181,16 +184,57 @@ KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
   w.pt_cell = c.take<int32_t>(nn);
   w.pt_rank = c.take<int32_t>(nn);
   w.spos = c.take<float4>(nn);
+  w.box_part = c.take<uint32_t>(bb * kKnnBoxParts * 6);
   *bytes = c.used;
   return w;
 }
 
 __device__ __forceinline__ int64_t clamp_range(int64_t v, int64_t n) { return v < 0 ? 0 : (v > n ? n : v); }
 
-// One block per source cloud: bounding box, then (thread 0) the grid of that cloud.
+// Partial bounding boxes of large clouds: block (p, b) reduces the p-th of `parts` equal slices
+// of cloud b into box_part[b][p] (order keys, so the minimum and maximum are integer ones).
+__global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_box_part(
+    const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int parts,
+    uint32_t* __restrict__ box_part) {
+  constexpr int W = kKnnSetupThreads / kWave;
+  __shared__ uint32_t red[6][W];
+  const int p = blockIdx.x, b = blockIdx.y;
+  const int64_t sa = clamp_range(ptr_s[b], Ns);
+  const int64_t sc = sa > clamp_range(ptr_s[b + 1], Ns) ? sa : clamp_range(ptr_s[b + 1], Ns);
+  const int64_t chunk = (sc - sa + parts - 1) / parts;
+  const int64_t pa = sa + p * chunk, pc = min(sc, pa + chunk);
+  const int t = threadIdx.x, w = t / kWave;
+  uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
+  for (int64_t i = pa + t; i < pc; i += kKnnSetupThreads) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const uint32_t kk = float_order_key(source[3 * i + a]);
+      mn[a] = min(mn[a], kk);
+      mx[a] = max(mx[a], kk);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    mn[a] = wave_min_u32(mn[a]);
+    mx[a] = wave_max_u32(mx[a]);
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
+  }
+  __syncthreads();
+  if (t < 6) {
+    uint32_t v = red[t][0];
+    for (int ww = 1; ww < W; ++ww) v = t < 3 ? min(v, red[t][ww]) : max(v, red[t][ww]);
+    box_part[(static_cast<int64_t>(b) * kKnnBoxParts + p) * 6 + t] = v;
+  }
+}
+
+// One block per source cloud: bounding box (from `parts` partial boxes when parts > 0), then
+// (thread 0) the grid of that cloud.
 __global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_setup(
     const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int k,
-    KnnGrid* __restrict__ grid) {
+    KnnGrid* __restrict__ grid, const uint32_t* __restrict__ box_part, int parts) {
   constexpr int W = kKnnSetupThreads / kWave;
   __shared__ uint32_t red[6][W];
   const int b = blockIdx.x;
@@ -198,13 +242,21 @@ __global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_setup(
   const int64_t sc = sa > clamp_range(ptr_s[b + 1], Ns) ? sa : clamp_range(ptr_s[b + 1], Ns);
   const int t = threadIdx.x, w = t / kWave;
   uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
-#pragma unroll 4
-  for (int64_t i = sa + t; i < sc; i += kKnnSetupThreads) {
+  if (parts > 0) {
+    if (t < parts) {
+      const uint32_t* bp = box_part + (static_cast<int64_t>(b) * kKnnBoxParts + t) * 6;
 #pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      const uint32_t kk = float_order_key(source[3 * i + a]);
-      mn[a] = min(mn[a], kk);
-      mx[a] = max(mx[a], kk);
+      for (int a = 0; a < 3; ++a) { mn[a] = bp[a]; mx[a] = bp[3 + a]; }
+    }
+  } else {
+#pragma unroll 4
+    for (int64_t i = sa + t; i < sc; i += kKnnSetupThreads) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const uint32_t kk = float_order_key(source[3 * i + a]);
+        mn[a] = min(mn[a], kk);
+        mx[a] = max(mx[a], kk);
+      }
     }
   }
 #pragma unroll
@@ -490,8 +542,19 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
                     float* out_dist, void* workspace, hipStream_t st) {
   size_t bytes = 0;
   const KnnGridWs w = carve_knn_grid(workspace, Ns, B, &bytes);
+  // Clouds of more than 2 * kKnnBoxChunk points on average: the bounding box is reduced by up to
+  // kKnnBoxParts workgroups per cloud first (one workgroup reading a 131,072-point cloud took
+  // 23 us), the setup then combines their partial boxes.
+  const int64_t avg = ceil_div(Ns, B);
+  const int64_t want = ceil_div(avg, kKnnBoxChunk);
+  const int parts = avg > 2 * kKnnBoxChunk ? static_cast<int>(want < kKnnBoxParts ? want : kKnnBoxParts) : 0;
+  if (parts > 0) {
+    hipLaunchKernelGGL(knn_grid_box_part, dim3(parts, static_cast<unsigned>(B)),
+                       dim3(kKnnSetupThreads), 0, st, source, Ns, ptr_s, parts, w.box_part);
+    GEO_LAUNCH_CHECK("knn_grid_box_part");
+  }
   hipLaunchKernelGGL(knn_grid_setup, dim3(B), dim3(kKnnSetupThreads), 0, st, source, Ns, ptr_s, k,
-                     w.grid);
+                     w.grid, w.box_part, parts);
   GEO_LAUNCH_CHECK("knn_grid_setup");
   hipLaunchKernelGGL(knn_grid_base, dim3(1), dim3(kScanThreads), 0, st, w.grid, B);
   GEO_LAUNCH_CHECK("knn_grid_base");
