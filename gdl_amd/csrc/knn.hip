@@ -151,7 +151,7 @@ constexpr int kKnnGridMaxAxis = 1024;
 constexpr int kKnnGridMaxK = 32;
 constexpr double kKnnCellTarget = 0.25;  // points per cell per neighbour (measured best)
 constexpr int kKnnCellCap = 2;            // cells per point
-constexpr int64_t kKnnWideSources = 65536; // one cloud this large: 32 lanes per query for k <= 8
+constexpr int64_t kKnnWideSources = 65536; // one cloud this large: a wave per query for k <= 8
 constexpr int kKnnBoxParts = 64;           // most workgroups per cloud for the bounding box
 constexpr int64_t kKnnBoxChunk = 16384;    // points per bounding-box workgroup
 
@@ -574,8 +574,9 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
   GEO_LAUNCH_CHECK("knn_grid_scatter");
   // Lanes per query: a wave runs as long as its slowest query.  In one scene-scale cloud (a
   // lidar frame) density varies by orders of magnitude, so the few queries in dense regions
-  // scan hundreds of candidates: 32 lanes per query for k <= 8 there (C5: 0.42 -> 0.22 ms);
-  // batched object-scale clouds are near uniform and do best with 8 (32 costs them ~10%).
+  // scan hundreds of candidates: a whole wave per query for k <= 8 there (C5 with 8 lanes
+  // 0.42 ms, 16 lanes 0.196, 32 lanes 0.152, 64 lanes 0.147 ms); batched object-scale clouds
+  // are near uniform and do best with 8 (32 costs them ~10%).
   const bool wide = B == 1 && Ns >= kKnnWideSources;
 #define GEO_KNN_GRID_LAUNCH(KV, GV)                                                             \
   {                                                                                             \
@@ -587,7 +588,7 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
   }
 #define GEO_KNN_GRID_CASE(KV, GV)                                                               \
   if (k <= KV) {                                                                                \
-    if (GV == 8 && wide) GEO_KNN_GRID_LAUNCH(KV, 32)                                             \
+    if (GV == 8 && wide) GEO_KNN_GRID_LAUNCH(KV, 64)                                             \
     GEO_KNN_GRID_LAUNCH(KV, GV)                                                                 \
   }
   GEO_KNN_GRID_CASE(1, 8) GEO_KNN_GRID_CASE(2, 8) GEO_KNN_GRID_CASE(4, 8)
