@@ -146,6 +146,26 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return ~wave_max_u32(~v); }
 
+// DPP move into the rows of ROWS (bit r = row r) with bound_ctrl: sources outside the row, and
+// rows outside ROWS, read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp0_rows_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xF, true));
+}
+
+// Wave-wide inclusive prefix sum of 32-bit values (every lane must be active), all in DPP:
+// Hillis-Steele steps within each 16-lane row (row_shr 1, 2, 4, 8), then each row's total
+// carried up (lane 15 of the row below into rows 1 and 3, lane 31 into rows 2 and 3).
+__device__ __forceinline__ uint32_t wave_inclusive_sum_dpp(uint32_t v) {
+  v += dpp0_rows_u32<0x111, 0xF>(v);  // row_shr:1
+  v += dpp0_rows_u32<0x112, 0xF>(v);  // row_shr:2
+  v += dpp0_rows_u32<0x114, 0xF>(v);  // row_shr:4
+  v += dpp0_rows_u32<0x118, 0xF>(v);  // row_shr:8
+  v += dpp0_rows_u32<kDppBcast15, 0xA>(v);
+  v += dpp0_rows_u32<kDppBcast31, 0xC>(v);
+  return v;
+}
+
 // Max / min over lanes 0..15 only (row 0); other lanes' values are ignored.
 __device__ __forceinline__ uint32_t row0_max_u32(uint32_t v) {
   v = max(v, dpp0_u32<kDppXor1>(v));

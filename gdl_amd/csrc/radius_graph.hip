@@ -354,26 +354,27 @@ __global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float*
   // bounding box, valid count and layout check over the workgroup
   uint32_t r7[7] = {wave_min_u32(kmin[0]), wave_min_u32(kmin[1]), wave_min_u32(kmin[2]),
                     wave_max_u32(kmax[0]), wave_max_u32(kmax[1]), wave_max_u32(kmax[2]), 0u};
-  const uint32_t wnv = static_cast<uint32_t>(wave_sum(static_cast<int>(nv)));
+  const uint32_t wnv = wave_sum_dpp(nv);
   const bool wbad = __ballot(bad) != 0ull;
   if (lane == 0) {
 #pragma unroll
     for (int q = 0; q < 6; ++q) s_red[q][wv] = r7[q];
     s_red[6][wv] = wnv | (wbad ? 0x80000000u : 0u);
   }
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t mn_k[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, mx_k[3] = {0u, 0u, 0u};
-    uint32_t n = 0;
-    bool any_bad = false;
-    for (int q = 0; q < W; ++q) {
-      for (int a = 0; a < 3; ++a) {
-        mn_k[a] = min(mn_k[a], s_red[a][q]);
-        mx_k[a] = max(mx_k[a], s_red[3 + a][q]);
-      }
-      n += s_red[6][q] & 0x7fffffffu;
-      any_bad = any_bad || (s_red[6][q] >> 31);
+  // This workgroup shares only LDS: its global writes are read by later kernels, so its
+  // barriers need not wait for them.
+  lds_barrier();
+  if (wv == 0) {  // lanes 0 .. W - 1 combine the waves' partials
+    static_assert(W <= 16, "one partial per lane of row 0");
+    uint32_t mn_k[3], mx_k[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      mn_k[a] = row0_min_u32(lane < W ? s_red[a][lane] : 0xffffffffu);
+      mx_k[a] = row0_max_u32(lane < W ? s_red[3 + a][lane] : 0u);
     }
+    const uint32_t pv = lane < W ? s_red[6][lane] : 0u;
+    const uint32_t n = wave_sum_dpp(pv & 0x7fffffffu);
+    const bool any_bad = __ballot(pv >> 31) != 0ull;
     int64_t cells = 0;
     Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
     if (n > 0) {
@@ -384,17 +385,19 @@ __global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float*
       g = rg_grid(mn, mx, n, r_cell, cells);
     }
     g.base = static_cast<int>(static_cast<int64_t>(b) * (4 * ppc + 64));
-    s_grid = g;
-    s_cells = static_cast<int>(cells);
-    s_nv = static_cast<int>(n);
-    w.grid[b] = g;
-    if (batch) w.layout_bad[b] = any_bad ? 1 : 0;
+    if (tid == 0) {
+      s_grid = g;
+      s_cells = static_cast<int>(cells);
+      s_nv = static_cast<int>(n);
+      w.grid[b] = g;
+      if (batch) w.layout_bad[b] = any_bad ? 1 : 0;
+    }
   }
-  __syncthreads();
+  lds_barrier();
   const Grid g = s_grid;
   const int cells = s_cells, n_valid = s_nv;
   for (int q = tid; q < (cells >> 1) + 1; q += kRgFrontThreads) s_cnt[q] = 0u;
-  __syncthreads();
+  lds_barrier();
   int cl[kRgFrontPer], rk[kRgFrontPer];
 #pragma unroll
   for (int k = 0; k < kRgFrontPer; ++k) {
@@ -410,35 +413,36 @@ __global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float*
       rk[k] = static_cast<int>((old >> ((c & 1) * 16)) & 0xffffu);
     }
   }
-  __syncthreads();
+  lds_barrier();
   // exclusive scan of the cell counts in place; each thread owns an even-aligned run of cells so
   // that no two threads write halves of one word
   const int per = ((cells + 2 * kRgFrontThreads - 1) / (2 * kRgFrontThreads)) * 2;
   const int c0 = tid * per, c1 = min(c0 + per, cells);
   uint32_t sum = 0;
   for (int c = c0; c < c1; ++c) sum += half_of(s_cnt, c);
-  const uint32_t incl = static_cast<uint32_t>(wave_inclusive_sum(static_cast<int>(sum)));
+  const uint32_t incl = wave_inclusive_sum_dpp(sum);
   if (lane == kWave - 1) s_red[0][wv] = incl;
-  __syncthreads();
+  lds_barrier();
   uint32_t run = incl - sum;
   for (int q = 0; q < wv; ++q) run += s_red[0][q];
-  int32_t* cs = w.cell_start + g.base;
   for (int c = c0; c < c1; c += 2) {
     const uint32_t a0 = half_of(s_cnt, c);
     const uint32_t a1 = c + 1 < c1 ? half_of(s_cnt, c + 1) : 0u;
     s_cnt[c >> 1] = run | ((run + a0) << 16);
-    cs[c] = static_cast<int32_t>(lo + run);
-    if (c + 1 < c1) cs[c + 1] = static_cast<int32_t>(lo + run + a0);
     run += a0 + a1;
   }
+  lds_barrier();
+  // cell starts from the scanned counts, one cell per thread per step (coalesced)
+  int32_t* cs = w.cell_start + g.base;
+  for (int c = tid; c < cells; c += kRgFrontThreads) cs[c] = static_cast<int32_t>(lo + half_of(s_cnt, c));
   if (tid == 0) cs[cells] = static_cast<int32_t>(lo + n_valid);
-  __syncthreads();
 #pragma unroll
   for (int k = 0; k < kRgFrontPer; ++k) {
     if (!ok[k]) continue;
     const int64_t i = lo + tid + k * kRgFrontThreads;
     const int64_t pos = lo + half_of(s_cnt, cl[k]) + rk[k];
-    w.spos[pos] = make_float4(px[k], py[k], pz[k], __int_as_float(static_cast<int>(i)));
+    if (pos < lo + ppc)  // always: the counts sum to the cloud's valid points
+      w.spos[pos] = make_float4(px[k], py[k], pz[k], __int_as_float(static_cast<int>(i)));
   }
   // holes: NaN coordinates are within no radius of anything, so a stencil run that reaches one
   // (the last cloud's end sentinel is the total slot when its grid uses its whole cell cap)
