@@ -111,6 +111,22 @@ __device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
   return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
          __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
 }
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return (static_cast<uint64_t>(dpp_u32<CTRL>(static_cast<uint32_t>(v >> 32))) << 32) |
+         dpp_u32<CTRL>(static_cast<uint32_t>(v));
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l))) << 32) |
+         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+__device__ __forceinline__ uint64_t wave_sum_dpp(uint64_t v) {
+  v += dpp_u64<kDppXor1>(v);
+  v += dpp_u64<kDppXor2>(v);
+  v += dpp_u64<kDppHalfMirror>(v);
+  v += dpp_u64<kDppMirror>(v);
+  return readlane_u64(v, 0) + readlane_u64(v, 16) + readlane_u64(v, 32) + readlane_u64(v, 48);
+}
 
 // DPP move with bound_ctrl: lanes without a source read 0, which lets the compiler fuse the
 // move into the consuming v_max_u32 (one v_max_u32_dpp per step).  0 is the identity of an
@@ -166,6 +182,22 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum_dpp(uint32_t v) {
   return v;
 }
 
+// The same two DPP patterns on 64-bit values, both halves moved by the same control.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp0_rows_u64(uint64_t v) {
+  return (static_cast<uint64_t>(dpp0_rows_u32<CTRL, ROWS>(static_cast<uint32_t>(v >> 32))) << 32) |
+         dpp0_rows_u32<CTRL, ROWS>(static_cast<uint32_t>(v));
+}
+__device__ __forceinline__ uint64_t wave_inclusive_sum_dpp(uint64_t v) {
+  v += dpp0_rows_u64<0x111, 0xF>(v);
+  v += dpp0_rows_u64<0x112, 0xF>(v);
+  v += dpp0_rows_u64<0x114, 0xF>(v);
+  v += dpp0_rows_u64<0x118, 0xF>(v);
+  v += dpp0_rows_u64<kDppBcast15, 0xA>(v);
+  v += dpp0_rows_u64<kDppBcast31, 0xC>(v);
+  return v;
+}
+
 // Max / min over lanes 0..15 only (row 0); other lanes' values are ignored.
 __device__ __forceinline__ uint32_t row0_max_u32(uint32_t v) {
   v = max(v, dpp0_u32<kDppXor1>(v));
@@ -208,6 +240,21 @@ __device__ __forceinline__ T wave_inclusive_sum(T v) {
     if (l >= d) v += o;
   }
   return v;
+}
+
+// Inclusive prefix sum and sum of 4- or 8-byte integers over the wave, all in DPP (every lane
+// must be active).
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_sum_int(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit integers");
+  if constexpr (sizeof(T) == 4) return static_cast<T>(wave_inclusive_sum_dpp(static_cast<uint32_t>(v)));
+  else return static_cast<T>(wave_inclusive_sum_dpp(static_cast<uint64_t>(v)));
+}
+template <typename T>
+__device__ __forceinline__ T wave_sum_int(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit integers");
+  if constexpr (sizeof(T) == 4) return static_cast<T>(wave_sum_dpp(static_cast<uint32_t>(v)));
+  else return static_cast<T>(wave_sum_dpp(static_cast<uint64_t>(v)));
 }
 
 template <typename T>

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     int v[PER], s = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) { v[j] = hist[t * PER + j]; s += v[j]; }
-    const int incl = wave_inclusive_sum(s);
+    const int incl = wave_inclusive_sum_int(s);
     __syncthreads();
     if (lane == kWave - 1) red[0][w] = static_cast<uint32_t>(incl);
     __syncthreads();

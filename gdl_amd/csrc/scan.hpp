@@ -19,7 +19,7 @@ template <typename T>
 __device__ __forceinline__ T block_exclusive_scan(T v, T* lds, T& total) {
   const int wave = threadIdx.x / kWave;
   constexpr int kWaves = kScanThreads / kWave;
-  T inc = wave_inclusive_sum(v);
+  T inc = wave_inclusive_sum_int(v);
   if (lane_id() == kWave - 1) lds[wave] = inc;
   __syncthreads();
   T wave_off = 0, tot = 0;
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_lookback(
           __builtin_amdgcn_s_sleep(1);
         }
         const bool take = ((need >> lane) & 1ull) != 0;
-        prefix += wave_sum<TOut>(take ? static_cast<TOut>(w & kScanValMask) : TOut(0));
+        prefix += wave_sum_int<TOut>(take ? static_cast<TOut>(w & kScanValMask) : TOut(0));
         if (isp & need) break;  // reached an inclusive prefix
         top -= kWave;
       }
