@@ -230,6 +230,19 @@ __device__ __forceinline__ int wave_aggregated_rank(int* counter, int key) {
   return __shfl(base, my_leader, kWave) + my_rank;
 }
 
+// Rank of this point in its cell's counter (counter = its cell's count, key = its cell).  Points
+// in scan order (lidar) put long runs of a wave into one cell: there one atomic per distinct cell
+// (wave-aggregated) avoids serialising 64 atomics on one address; scattered points take plain
+// per-lane atomics, since aggregation would loop over up to 64 distinct cells.  The run count
+// comes from neighbouring-lane equality.
+__device__ __forceinline__ int cell_rank(int* counter, int key) {
+  const int lane = lane_id();
+  const int prev = __shfl_up(key, 1, kWave);
+  const int runs = __popcll(__ballot(lane == 0 || prev != key));
+  if (runs <= 16) return wave_aggregated_rank(counter, key);
+  return atomicAdd(counter, 1);
+}
+
 // Wave-wide inclusive prefix sum (all lanes active).
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_sum(T v) {

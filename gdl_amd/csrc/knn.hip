@@ -350,18 +350,6 @@ __device__ __forceinline__ int64_t cloud_of_index(const int64_t* __restrict__ pt
   return lo;
 }
 
-// Rank of this point in its cell's counter.  Points in scan order (lidar) put long runs of a
-// wave into one cell: there one atomic per distinct cell (wave-aggregated) avoids serialising
-// 64 atomics on one address; scattered points take plain per-lane atomics, since aggregation
-// would loop over up to 64 distinct cells.  The run count comes from neighbouring-lane equality.
-__device__ __forceinline__ int cell_rank(int* counter, int key) {
-  const int lane = lane_id();
-  const int prev = __shfl_up(key, 1, kWave);
-  const int runs = __popcll(__ballot(lane == 0 || prev != key));
-  if (runs <= 16) return wave_aggregated_rank(counter, key);
-  return atomicAdd(counter, 1);
-}
-
 __global__ __launch_bounds__(kKnnGridThreads) void knn_grid_cell(
     const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int64_t B,
     KnnGridWs w) {

@@ -254,6 +254,44 @@ __global__ __launch_bounds__(kRgThreads) void rg_bbox(RgWs w, const float* __res
   }
 }
 
+// One cloud of all N points (no batch vector, no mask): a grid-stride loop per thread and one
+// reduction per workgroup, so at most kRgBoxBlocks workgroups issue the cloud's atomics (one
+// workgroup per 256 points put ~3,600 atomics on the same six words for a 131,072-point frame).
+constexpr int kRgBoxBlocks = 64;
+__global__ __launch_bounds__(kRgThreads) void rg_bbox_one(RgWs w, const float* __restrict__ x,
+                                                          int64_t N) {
+  constexpr int W = kRgThreads / kWave;
+  __shared__ uint32_t s_red[6][W];
+  uint32_t mn[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, mx[3] = {0u, 0u, 0u};
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < N; i += stride) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const uint32_t k = float_order_key(x[3 * i + a]);
+      mn[a] = min(mn[a], k);
+      mx[a] = max(mx[a], k);
+    }
+  }
+  const int wv = threadIdx.x / kWave;
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    mn[a] = wave_min_u32(mn[a]);
+    mx[a] = wave_max_u32(mx[a]);
+  }
+  if (lane_id() == 0) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a) { s_red[a][wv] = mn[a]; s_red[3 + a][wv] = mx[a]; }
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const int q = threadIdx.x;
+    uint32_t r = s_red[q][0];
+    for (int ww = 1; ww < W; ++ww) r = q < 3 ? min(r, s_red[q][ww]) : max(r, s_red[q][ww]);
+    if (q < 3) atomicMin(&w.bbox[q], r); else atomicMax(&w.bbox[q], r);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) w.cloud_n[0] = static_cast<int>(N);
+}
+
 __device__ __forceinline__ int cell_coord(float p, float o, float inv_h, int dim) {
 #pragma clang fp contract(off)
   const float u = (p - o) * inv_h;
@@ -278,7 +316,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_cell(RgWs w, const float* __res
   const int cz = cell_coord(x[3 * i + 2], g.oz, g.inv_h, g.dz);
   const int c = g.base + (cx * g.dy + cy) * g.dz + cz;
   w.pt_cell[i] = c;
-  w.pt_rank[i] = atomicAdd(&w.cell_cnt[c], 1);
+  w.pt_rank[i] = cell_rank(&w.cell_cnt[c], c);
 }
 
 __global__ __launch_bounds__(kRgThreads) void rg_scatter(RgWs w, const float* __restrict__ x,
@@ -970,9 +1008,15 @@ static int radius_count_impl(const float* x, int64_t N, const int64_t* batch, in
   }
   if (N > 0) {
     const int64_t blocks = ceil_div(N, kRgThreads);
-    hipLaunchKernelGGL(rg_bbox, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N, batch, B,
-                       points_per_cloud, mask);
-    GEO_LAUNCH_CHECK("rg_bbox");
+    if (B == 1 && batch == nullptr && mask == nullptr) {
+      hipLaunchKernelGGL(rg_bbox_one, dim3(static_cast<unsigned>(blocks < kRgBoxBlocks ? blocks : kRgBoxBlocks)),
+                         dim3(kRgThreads), 0, st, w, x, N);
+      GEO_LAUNCH_CHECK("rg_bbox_one");
+    } else {
+      hipLaunchKernelGGL(rg_bbox, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N, batch, B,
+                         points_per_cloud, mask);
+      GEO_LAUNCH_CHECK("rg_bbox");
+    }
     hipLaunchKernelGGL(rg_setup, dim3(1), dim3(kScanThreads), 0, st, w, B, r_cell);
     GEO_LAUNCH_CHECK("rg_setup");
     hipLaunchKernelGGL(rg_cell, dim3(blocks), dim3(kRgThreads), 0, st, w, x, N, batch, B,
