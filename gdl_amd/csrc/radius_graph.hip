@@ -765,7 +765,7 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
                                int K, bool lp, int64_t i, int c,
                                const int64_t* __restrict__ row_ptr, int64_t* __restrict__ row_out,
                                int64_t* __restrict__ col_out, uint32_t* __restrict__ key,
-                               int32_t* __restrict__ idx) {
+                               int32_t* __restrict__ idx, int32_t* __restrict__ hist) {
   const int lane = lane_id();
   const int64_t o = row_ptr[i];
   int32_t* L = w.list + i * K;
@@ -808,20 +808,49 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
       }
       return static_cast<int>(wave_sum_dpp(static_cast<uint32_t>(t)));
     };
-    // stage B: the K-th smallest distance bits (every in-radius d has bits < bits(r2)), searched
-    // between the smallest and largest bits present
-    uint32_t lo = 0, hi = __float_as_uint(r2) - 1u;
+    // stage B: the K-th smallest distance bits (every in-radius d has bits < bits(r2)).  Staged
+    // candidates: a radix select, 8 bits per pass -- a 256-bin LDS histogram of the keys that
+    // match the digits chosen so far, then the bin holding the K-th by one wave scan (lane l
+    // holds bins 4l .. 4l + 3).  Otherwise a binary search on the bits over the stencil.
+    uint32_t dstar;
     if (inl) {
-      uint32_t mn = 0xffffffffu, mx = 0u;
-      for (int m = lane; m < n; m += kWave) { mn = min(mn, key[m]); mx = max(mx, key[m]); }
-      lo = wave_min_u32(mn);
-      hi = wave_max_u32(mx);
+      uint32_t prefix = 0u, decided = 0u;
+      int k = K;  // rank of the K-th among the keys that match prefix (1 <= k <= their count)
+      for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int q = lane; q < 256; q += kWave) hist[q] = 0;
+        wave_lds_fence();
+        for (int m = lane; m < n; m += kWave) {
+          const uint32_t v = key[m];
+          if ((v & decided) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1);
+        }
+        wave_lds_fence();
+        const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2];
+        const int h3 = hist[4 * lane + 3];
+        const int sum = h0 + h1 + h2 + h3;
+        const int excl = static_cast<int>(wave_inclusive_sum_dpp(static_cast<uint32_t>(sum))) - sum;
+        const int L = __builtin_ctzll(__ballot(excl < k && k <= excl + sum) | (1ull << 63));
+        int d = 4 * lane, below = excl;
+        if (k > below + h0) {
+          d += 1; below += h0;
+          if (k > below + h1) {
+            d += 1; below += h1;
+            if (k > below + h2) { d += 1; below += h2; }
+          }
+        }
+        k -= __builtin_amdgcn_readlane(below, L);
+        prefix |= static_cast<uint32_t>(__builtin_amdgcn_readlane(d, L)) << shift;
+        decided |= 0xffu << shift;
+        wave_lds_fence();  // every lane has read the histogram before the next pass clears it
+      }
+      dstar = prefix;
+    } else {
+      uint32_t lo = 0, hi = __float_as_uint(r2) - 1u;
+      while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (count_le(mid, false, -1) >= K) hi = mid; else lo = mid + 1u;
+      }
+      dstar = lo;
     }
-    while (lo < hi) {
-      const uint32_t mid = lo + ((hi - lo) >> 1);
-      if (count_le(mid, false, -1) >= K) hi = mid; else lo = mid + 1u;
-    }
-    const uint32_t dstar = lo;
     // stage C: index threshold among the sources at d* when they are more than needed
     const int less = count_le(dstar, true, -1);
     const int need = K - less;
@@ -890,6 +919,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
                                                          int64_t* __restrict__ col_out) {
   __shared__ uint32_t s_key[kRgThreads / kWave][kRgSelCap];
   __shared__ int32_t s_idx[kRgThreads / kWave][kRgSelCap];
+  __shared__ int32_t s_hist[kRgThreads / kWave][256];
   r2 = rg_r2(w, r2);
   const int64_t i = (xcd_block_runs(kRgXcdRun) * kRgThreads + threadIdx.x) / kRgGroup;
   const int sub = static_cast<int>(threadIdx.x) & (kRgGroup - 1);
@@ -935,7 +965,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
     const int64_t ti = __builtin_amdgcn_readlane(static_cast<int>(i), leader);
     const int tc = __builtin_amdgcn_readlane(c, leader);
     rg_wave_target(w, x, batch, B, ppc, r2, K, loop != 0, ti, tc, row_ptr, row_out, col_out,
-                   s_key[threadIdx.x / kWave], s_idx[threadIdx.x / kWave]);
+                   s_key[threadIdx.x / kWave], s_idx[threadIdx.x / kWave], s_hist[threadIdx.x / kWave]);
   }
 }
 
