@@ -714,6 +714,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __
 constexpr int kRgSlots = 8;
 // In-radius candidates of one target whose distance bits a wave keeps in LDS for the selection.
 constexpr int kRgSelCap = 1024;
+constexpr int kRgStageLoads = 4;  // chunks of 64 stencil sources loaded together when staging
 
 __device__ __forceinline__ void wave_lds_fence() {
   // LDS writes of some lanes become visible to later reads of other lanes of the same wave
@@ -778,17 +779,40 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
     stencil_runs(w, g, qx, qy, qz, ra, rn);
     const bool inl = c <= kRgSelCap;
     int n = 0;
-    if (inl) {  // stage A: in-radius (distance bits, index) into LDS (wave compaction)
-      wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
-        const bool a = ok && (lp || j != qi) && d < r2;
-        const uint64_t m = __ballot(a);
-        const int slot = n + static_cast<int>(__popcll(m & lanemask_lt()));
-        if (a && slot < kRgSelCap) {
-          key[slot] = __float_as_uint(d);
-          idx[slot] = j;
+    if (inl) {
+      // stage A: in-radius (distance bits, index) into LDS (wave compaction).  The nine runs are
+      // one index space (source t of the stencil is ra[r] + t - pre[r] in the run r holding it),
+      // so kRgStageLoads chunks of 64 sources are loaded together.
+      int pre[9];
+      pre[0] = 0;
+#pragma unroll
+      for (int r = 1; r < 9; ++r) pre[r] = pre[r - 1] + rn[r - 1];
+      const int tot = pre[8] + rn[8];
+      for (int base = 0; base < tot; base += kWave * kRgStageLoads) {  // wave-uniform
+        float4 sv[kRgStageLoads];
+#pragma unroll
+        for (int u = 0; u < kRgStageLoads; ++u) {
+          const int t = base + u * kWave + lane;
+          int off = ra[0];
+#pragma unroll
+          for (int r = 1; r < 9; ++r) off = t >= pre[r] ? ra[r] - pre[r] : off;
+          sv[u] = t < tot ? w.spos[off + t] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        n += static_cast<int>(__popcll(m));
-      });
+#pragma unroll
+        for (int u = 0; u < kRgStageLoads; ++u) {
+          const int t = base + u * kWave + lane;
+          const float d = sqdist(qx, qy, qz, sv[u].x, sv[u].y, sv[u].z);
+          const int j = __float_as_int(sv[u].w);
+          const bool a = t < tot && (lp || j != qi) && d < r2;
+          const uint64_t m = __ballot(a);
+          const int slot = n + static_cast<int>(__popcll(m & lanemask_lt()));
+          if (a && slot < kRgSelCap) {
+            key[slot] = __float_as_uint(d);
+            idx[slot] = j;
+          }
+          n += static_cast<int>(__popcll(m));
+        }
+      }
       n = n < kRgSelCap ? n : kRgSelCap;
       wave_lds_fence();
     }
