@@ -714,7 +714,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __
 constexpr int kRgSlots = 8;
 // In-radius candidates of one target whose distance bits a wave keeps in LDS for the selection.
 constexpr int kRgSelCap = 1024;
-constexpr int kRgStageLoads = 4;  // chunks of 64 stencil sources loaded together when staging
+constexpr int kRgStageLoads = 8;  // chunks of 64 stencil sources loaded together when staging
 
 __device__ __forceinline__ void wave_lds_fence() {
   // LDS writes of some lanes become visible to later reads of other lanes of the same wave
@@ -837,6 +837,7 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
     // match the digits chosen so far, then the bin holding the K-th by one wave scan (lane l
     // holds bins 4l .. 4l + 3).  Otherwise a binary search on the bits over the stencil.
     uint32_t dstar;
+    int less = 0, at = 0;  // sources below d*, sources at d*
     if (inl) {
       uint32_t prefix = 0u, decided = 0u;
       int k = K;  // rank of the K-th among the keys that match prefix (1 <= k <= their count)
@@ -853,20 +854,22 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
         const int sum = h0 + h1 + h2 + h3;
         const int excl = static_cast<int>(wave_inclusive_sum_dpp(static_cast<uint32_t>(sum))) - sum;
         const int L = __builtin_ctzll(__ballot(excl < k && k <= excl + sum) | (1ull << 63));
-        int d = 4 * lane, below = excl;
+        int d = 4 * lane, below = excl, hs = h0;
         if (k > below + h0) {
-          d += 1; below += h0;
+          d += 1; below += h0; hs = h1;
           if (k > below + h1) {
-            d += 1; below += h1;
-            if (k > below + h2) { d += 1; below += h2; }
+            d += 1; below += h1; hs = h2;
+            if (k > below + h2) { d += 1; below += h2; hs = h3; }
           }
         }
         k -= __builtin_amdgcn_readlane(below, L);
+        at = __builtin_amdgcn_readlane(hs, L);  // after the last pass: the sources at d*
         prefix |= static_cast<uint32_t>(__builtin_amdgcn_readlane(d, L)) << shift;
         decided |= 0xffu << shift;
         wave_lds_fence();  // every lane has read the histogram before the next pass clears it
       }
       dstar = prefix;
+      less = K - k;
     } else {
       uint32_t lo = 0, hi = __float_as_uint(r2) - 1u;
       while (lo < hi) {
@@ -874,11 +877,11 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
         if (count_le(mid, false, -1) >= K) hi = mid; else lo = mid + 1u;
       }
       dstar = lo;
+      less = count_le(dstar, true, -1);
+      at = count_le(dstar, false, -1) - less;
     }
     // stage C: index threshold among the sources at d* when they are more than needed
-    const int less = count_le(dstar, true, -1);
     const int need = K - less;
-    const int at = count_le(dstar, false, -1) - less;
     int jstar = 0x7fffffff;
     if (at > need) {
       int jlo = 0, jhi = 0x7ffffffe;
@@ -889,11 +892,11 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
       jstar = jlo;
     }
     auto accept = [&](uint32_t db, int j) { return db < dstar || (db == dstar && j <= jstar); };
-    // stage D: the K accepted sources, compacted (in place over the LDS indices: a slot never
-    // passes the position being read) or into the list when K exceeds the LDS
-    int32_t* dst = (inl && K <= kRgSelCap) ? idx : L;
-    int m0 = 0;
-    if (inl) {
+    // stage D: the K accepted sources, compacted in place over the LDS indices (a slot never
+    // passes the position being read) or into the list when K exceeds the LDS; stage E: ranked
+    // by index.  The two forms are separate so that the LDS one reads with LDS instructions.
+    if (inl && K <= kRgSelCap) {
+      int m0 = 0;
       for (int base = 0; base < n; base += kWave) {  // wave-uniform trip count
         const int m = base + lane;
         const bool a = m < n && accept(key[m], idx[m]);
@@ -901,27 +904,50 @@ __device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
         const uint64_t bm = __ballot(a);
         const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
         wave_lds_fence();  // every lane has read its entry before any slot is written
-        if (a && slot < K) dst[slot] = j;
+        if (a && slot < K) idx[slot] = j;
         m0 += static_cast<int>(__popcll(bm));
       }
+      wave_lds_fence();
+      const int K4 = K & ~3;
+      for (int m = lane; m < K; m += kWave) {
+        const int v = idx[m];
+        int r = 0;
+        for (int q = 0; q < K4; q += 4) {  // 16-byte broadcast reads
+          const int4 u = *reinterpret_cast<const int4*>(idx + q);
+          r += (u.x < v) + (u.y < v) + (u.z < v) + (u.w < v);
+        }
+        for (int q = K4; q < K; ++q) r += idx[q] < v;
+        row_out[o + r] = v;
+        col_out[o + m] = i;
+      }
     } else {
-      wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
-        const bool a = ok && (lp || j != qi) && d < r2 && accept(__float_as_uint(d), j);
-        const uint64_t bm = __ballot(a);
-        const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
-        if (a && slot < K) dst[slot] = j;
-        m0 += static_cast<int>(__popcll(bm));
-      });
-    }
-    if (dst == L) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    else wave_lds_fence();
-    // stage E: rank by index
-    for (int m = lane; m < K; m += kWave) {
-      const int v = dst[m];
-      int r = 0;
-      for (int q = 0; q < K; ++q) r += dst[q] < v;
-      row_out[o + r] = v;
-      col_out[o + m] = i;
+      int m0 = 0;
+      if (inl) {
+        for (int base = 0; base < n; base += kWave) {  // wave-uniform trip count
+          const int m = base + lane;
+          const bool a = m < n && accept(key[m], idx[m]);
+          const uint64_t bm = __ballot(a);
+          const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
+          if (a && slot < K) L[slot] = idx[m];
+          m0 += static_cast<int>(__popcll(bm));
+        }
+      } else {
+        wave_scan_runs(w, ra, rn, qx, qy, qz, [&](float d, int j, bool ok) {
+          const bool a = ok && (lp || j != qi) && d < r2 && accept(__float_as_uint(d), j);
+          const uint64_t bm = __ballot(a);
+          const int slot = m0 + static_cast<int>(__popcll(bm & lanemask_lt()));
+          if (a && slot < K) L[slot] = j;
+          m0 += static_cast<int>(__popcll(bm));
+        });
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      for (int m = lane; m < K; m += kWave) {
+        const int v = L[m];
+        int r = 0;
+        for (int q = 0; q < K; ++q) r += L[q] < v;
+        row_out[o + r] = v;
+        col_out[o + m] = i;
+      }
     }
     wave_lds_fence();  // the LDS is reused by the next target
     return;
@@ -942,7 +968,7 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
                                                          int64_t* __restrict__ row_out,
                                                          int64_t* __restrict__ col_out) {
   __shared__ uint32_t s_key[kRgThreads / kWave][kRgSelCap];
-  __shared__ int32_t s_idx[kRgThreads / kWave][kRgSelCap];
+  __shared__ __align__(16) int32_t s_idx[kRgThreads / kWave][kRgSelCap];
   __shared__ int32_t s_hist[kRgThreads / kWave][256];
   r2 = rg_r2(w, r2);
   const int64_t i = (xcd_block_runs(kRgXcdRun) * kRgThreads + threadIdx.x) / kRgGroup;
