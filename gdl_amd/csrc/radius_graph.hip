@@ -739,6 +739,21 @@ __device__ __forceinline__ void stencil_runs(const RgWs& w, const Grid& g, float
   }
 }
 
+// Run r (0..8) of the stencil around (qx, qy, qz): start and length.
+__device__ __forceinline__ void stencil_run(const RgWs& w, const Grid& g, float qx, float qy, float qz,
+                                            int r, int& a, int& n) {
+  const int cx = cell_coord(qx, g.ox, g.inv_h, g.dx);
+  const int cy = cell_coord(qy, g.oy, g.inv_h, g.dy);
+  const int cz = cell_coord(qz, g.oz, g.inv_h, g.dz);
+  const int z0 = cz > 0 ? cz - 1 : 0;
+  const int z1 = cz + 1 < g.dz ? cz + 1 : g.dz - 1;
+  const int ix = cx - 1 + r / 3, iy = cy - 1 + r % 3;
+  const bool in = ix >= 0 && ix < g.dx && iy >= 0 && iy < g.dy;
+  const int c0 = g.base + (ix * g.dy + iy) * g.dz;
+  a = in ? w.cell_start[c0 + z0] : 0;
+  n = in ? w.cell_start[c0 + z1 + 1] - a : 0;
+}
+
 // Calls f(d, j, ok) for every source of the stencil runs, 64 at a time across the wave (every
 // lane calls f the same number of times; ok marks a real candidate).
 template <typename F>
@@ -761,22 +776,16 @@ __device__ __forceinline__ void wave_scan_runs(const RgWs& w, const int (&ra)[9]
 //          stencil), the K-th distance d* by binary search on the bits, the index threshold j*
 //          among the sources at d* when they are more than needed, the accepted sources compacted
 //          in place and sorted by index.
-__device__ void rg_wave_target(const RgWs& w, const float* __restrict__ x,
-                               const int64_t* __restrict__ batch, int64_t B, int64_t ppc, float r2,
-                               int K, bool lp, int64_t i, int c,
-                               const int64_t* __restrict__ row_ptr, int64_t* __restrict__ row_out,
-                               int64_t* __restrict__ col_out, uint32_t* __restrict__ key,
-                               int32_t* __restrict__ idx, int32_t* __restrict__ hist) {
+// The target's row offset o, and for c > K its position and stencil runs, come from the caller.
+__device__ void rg_wave_target(const RgWs& w, float r2, int K, bool lp, int64_t i, int c, int64_t o,
+                               float qx, float qy, float qz, const int (&ra)[9], const int (&rn)[9],
+                               int64_t* __restrict__ row_out, int64_t* __restrict__ col_out,
+                               uint32_t* __restrict__ key, int32_t* __restrict__ idx,
+                               int32_t* __restrict__ hist) {
   const int lane = lane_id();
-  const int64_t o = row_ptr[i];
   int32_t* L = w.list + i * K;
   if (c > K) {
-    const int b = cloud_of(i, batch, B, ppc);
-    const Grid g = w.grid[b];
-    const float qx = x[3 * i], qy = x[3 * i + 1], qz = x[3 * i + 2];
     const int qi = static_cast<int>(i);
-    int ra[9], rn[9];
-    stencil_runs(w, g, qx, qy, qz, ra, rn);
     const bool inl = c <= kRgSelCap;
     int n = 0;
     if (inl) {
@@ -1007,14 +1016,43 @@ __global__ __launch_bounds__(kRgThreads) void rg_compact(RgWs w, const float* __
       }
     }
   }
-  // the wave's remaining targets, one at a time with all 64 lanes
-  uint64_t rest = __ballot(sub == 0 && c > 0 && !group);
+  // the wave's remaining targets, one at a time with all 64 lanes.  Their row offsets and, for
+  // those with more than K sources, positions and stencil runs are loaded first for all of them
+  // at once: run r of a group's target by the group's lane r (the ninth by its first lane).
+  static_assert(kRgGroup == 8, "one lane per stencil run of the group's target");
+  const bool rest_t = c > 0 && !group;  // group-uniform
+  int64_t po = 0;
+  float pqx = 0.f, pqy = 0.f, pqz = 0.f;
+  int pa = 0, pn = 0, pa8 = 0, pn8 = 0;
+  if (rest_t) {
+    po = row_ptr[i];
+    if (c > K) {
+      const Grid g = w.grid[cloud_of(i, batch, B, ppc)];
+      pqx = x[3 * i]; pqy = x[3 * i + 1]; pqz = x[3 * i + 2];
+      stencil_run(w, g, pqx, pqy, pqz, sub, pa, pn);
+      if (sub == 0) stencil_run(w, g, pqx, pqy, pqz, 8, pa8, pn8);
+    }
+  }
+  uint64_t rest = __ballot(sub == 0 && rest_t);
   while (rest) {
     const int leader = __builtin_ctzll(rest);
     rest &= rest - 1;
     const int64_t ti = __builtin_amdgcn_readlane(static_cast<int>(i), leader);
     const int tc = __builtin_amdgcn_readlane(c, leader);
-    rg_wave_target(w, x, batch, B, ppc, r2, K, loop != 0, ti, tc, row_ptr, row_out, col_out,
+    const int64_t to = (static_cast<int64_t>(__builtin_amdgcn_readlane(static_cast<int>(po >> 32), leader)) << 32) |
+                       static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(po), leader));
+    int ra[9], rn[9];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      ra[r] = __builtin_amdgcn_readlane(pa, leader + r);
+      rn[r] = __builtin_amdgcn_readlane(pn, leader + r);
+    }
+    ra[8] = __builtin_amdgcn_readlane(pa8, leader);
+    rn[8] = __builtin_amdgcn_readlane(pn8, leader);
+    const float tx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pqx), leader));
+    const float ty = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pqy), leader));
+    const float tz = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pqz), leader));
+    rg_wave_target(w, r2, K, loop != 0, ti, tc, to, tx, ty, tz, ra, rn, row_out, col_out,
                    s_key[threadIdx.x / kWave], s_idx[threadIdx.x / kWave], s_hist[threadIdx.x / kWave]);
   }
 }
