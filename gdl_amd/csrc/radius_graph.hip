@@ -7,10 +7,13 @@
 //
 // geo_radius_count:
 //   rg_init     zero counters, reset bounding boxes
-//   rg_bbox     per-cloud point count and bounding box (wave-reduced atomics)
-//   rg_setup    per cloud: cell edge h >= r*(1+1/32), grid dims (capped at 4*n+64 cells and
-//               16384 per axis so that the 3x3x3 stencil stays exact), cell base offsets
-//   rg_cell     cell id per point, rank inside the cell (atomic counter)
+//   rg_bbox     per-cloud point count and bounding box (wave-reduced atomics; one cloud without
+//               batch vector or mask: rg_bbox_one, at most 64 workgroups)
+//   rg_setup    per cloud: cell edge h >= r*(1+1/32), grid dims (capped at 4*n+64 cells, 8*n+64
+//               for scene-scale clouds, and 16384 per axis so that the 3x3x3 stencil stays
+//               exact), cell base offsets
+//   rg_cell     cell id per point, rank inside the cell (atomic counter, one per run of equal
+//               cells in a wave)
 //   scan        cell offsets (single pass, decoupled look-back)
 //   rg_scatter  points in cell order as float4 (x, y, z, index bits)
 //   rg_count    kRgGroup lanes per point in cell order (neighbouring groups share cells): count
@@ -56,6 +59,7 @@ struct RgWs {
   int32_t* list;  // [N][K] accepted sources per target (unsorted), or null when too large
   int32_t* layout_bad;  // [B] per cloud: points of the chunk whose batch entry is another cloud
   int64_t cells_max;
+  int cell_factor;  // grid cells allowed per point of a cloud (cap cell_factor * n + 64)
   size_t bytes;
   const double* r_dev = nullptr;  // radius on the device (geo_radius_*_dev), else null
 };
@@ -73,7 +77,12 @@ __device__ __forceinline__ float rg_rcell(const RgWs& w, float r_cell) {
   return r > 0.0 ? static_cast<float>(r) : 1.0f;
 }
 
-int64_t cells_cap(int64_t N, int64_t B) { return 4 * N + 64 * B; }
+// Grid cells allowed per point: 4, or 8 for clouds of 16,384 points or more on average -- a
+// scene-scale cloud (the lidar frame: 0.63 m cells at 4 per point against 0.52 m at 8, 865
+// against 589 stencil sources per target at r = 0.5 m) pays more in stencil scans than its
+// cell scan costs.  The one-workgroup front end keeps 4 (its LDS grid).
+int rg_cell_factor(int64_t N, int64_t B) { return B > 0 && N / B >= 16384 ? 8 : 4; }
+int64_t cells_cap(int64_t N, int64_t B) { return rg_cell_factor(N, B) * N + 64 * B; }
 
 // The per-target source lists are kept when they fit in 1 GiB of workspace; beyond that the
 // emit pass re-scans the candidates instead.
@@ -84,6 +93,7 @@ RgWs carve_rg(void* base, int64_t N, int64_t B, int64_t K) {
   RgWs w;
   const int64_t nn = N > 0 ? N : 1, bb = B > 0 ? B : 1;
   w.cells_max = cells_cap(N, B);
+  w.cell_factor = rg_cell_factor(N, B);
   w.cloud_n = c.take<int32_t>(bb);
   w.bbox = c.take<uint32_t>(6 * bb);
   w.grid = c.take<Grid>(bb);
@@ -128,12 +138,12 @@ __global__ void rg_init(RgWs w, int64_t N, int64_t B) {
 }
 
 // Grid of one cloud of n valid points with bounding box [mn, mx]: cell edge h >= r*(1+1/32),
-// grown until the cell count is at most 4n + 64 and no axis exceeds kRgMaxAxis cells (one cell
-// for the whole cloud if that fails).  Writes the cell count; g.base is left 0.
+// grown until the cell count is at most factor * n + 64 and no axis exceeds kRgMaxAxis cells
+// (one cell for the whole cloud if that fails).  Writes the cell count; g.base is left 0.
 __device__ Grid rg_grid(const float (&mn)[3], const float (&mx)[3], int64_t n, float r_cell,
-                        int64_t& cells) {
+                        int64_t& cells, int factor) {
   Grid g{0.f, 0.f, 0.f, 0.f, 0, 0, 0, 0};
-  const double cap = 4.0 * n + 64.0;
+  const double cap = static_cast<double>(factor) * n + 64.0;
   double h = static_cast<double>(r_cell) * (1.0 + 1.0 / 32.0);
   double ext[3];
   for (int a = 0; a < 3; ++a) {
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(kScanThreads) void rg_setup(RgWs w, int64_t B, floa
                            float_from_order_key(bb[2])};
       const float mx[3] = {float_from_order_key(bb[3]), float_from_order_key(bb[4]),
                            float_from_order_key(bb[5])};
-      g = rg_grid(mn, mx, w.cloud_n[b], r_cell, cells);
+      g = rg_grid(mn, mx, w.cloud_n[b], r_cell, cells, w.cell_factor);
     }
     int64_t total;
     const int64_t off = block_exclusive_scan<int64_t>(cells, lds, total);
@@ -420,7 +430,7 @@ __global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float*
                            float_from_order_key(mn_k[2])};
       const float mx[3] = {float_from_order_key(mx_k[0]), float_from_order_key(mx_k[1]),
                            float_from_order_key(mx_k[2])};
-      g = rg_grid(mn, mx, n, r_cell, cells);
+      g = rg_grid(mn, mx, n, r_cell, cells, 4);  // the front end's LDS grid: 4n + 64 cells
     }
     g.base = static_cast<int>(static_cast<int64_t>(b) * (4 * ppc + 64));
     if (tid == 0) {
