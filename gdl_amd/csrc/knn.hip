@@ -135,9 +135,8 @@ int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
 // --------------------------------------------------------------------------- grid search ---
 // Clouds of many sources and k <= 32: each source cloud is binned into a uniform grid (cell
 // edge chosen so a cell holds about k/4 points at the cloud's mean density, at most 1024 cells
-// per axis and 2n + 64 cells, 8n + 64 for scene-scale clouds), sources are counting-sorted by
-// cell, and each query visits the cells in shells of growing Chebyshev radius around its own
-// cell.  After a shell it stops when
+// per axis and 2n + 64 cells), sources are counting-sorted by cell, and each query visits the
+// cells in shells of growing Chebyshev radius around its own cell.  After a shell it stops when
 // its k-th distance is below a bound that every unvisited source provably exceeds: the query's
 // distance to the faces of the visited block, measured in cell units minus 1e-3 of a cell (the
 // cell coordinates are rounded fp32 values below 1024, accurate to ~1e-4 cells), scaled by the
@@ -151,15 +150,10 @@ constexpr int kKnnSetupThreads = 1024;
 constexpr int kKnnGridMaxAxis = 1024;
 constexpr int kKnnGridMaxK = 32;
 constexpr double kKnnCellTarget = 0.25;  // points per cell per neighbour (measured best)
+constexpr int kKnnCellCap = 2;            // cells per point
 constexpr int64_t kKnnWideSources = 65536; // one cloud this large: a wave per query for k <= 8
 constexpr int kKnnBoxParts = 64;           // most workgroups per cloud for the bounding box
 constexpr int64_t kKnnBoxChunk = 16384;    // points per bounding-box workgroup
-
-// Grid cells allowed per source point: 2, or 8 when clouds average 16,384 sources or more -- a
-// scene-scale cloud (the lidar frame) is mostly empty space, so its mean-density cells hit the
-// cap of 2 per point and come out coarse where the points are (C5 KNN 0.19 -> 0.16 ms at 8);
-// small clouds keep 2, since the cell arrays are zeroed and scanned whole on every call.
-int knn_cell_cap(int64_t Ns, int64_t B) { return B > 0 && Ns / B >= 16384 ? 8 : 2; }
 
 struct KnnGrid {
   float ox, oy, oz, inv_h, h;
@@ -176,15 +170,13 @@ struct KnnGridWs {
   float4* spos;
   uint32_t* box_part;  // [B][kKnnBoxParts][6] partial bounding boxes (order keys)
   int64_t cells_max;
-  int cell_cap;  // cells per point (see knn_cell_cap)
 };
 
 KnnGridWs carve_knn_grid(void* base, int64_t Ns, int64_t B, size_t* bytes) {
   Carver c(base);
   KnnGridWs w;
   const int64_t nn = Ns > 0 ? Ns : 1, bb = B > 0 ? B : 1;
-  w.cell_cap = knn_cell_cap(Ns, B);
-  w.cells_max = w.cell_cap * Ns + 64 * bb;
+  w.cells_max = kKnnCellCap * Ns + 64 * bb;
   w.grid = c.take<KnnGrid>(bb);
   w.cell_cnt = c.take<int32_t>(w.cells_max + 1);
   w.cell_scan = c.take<uint64_t>(scan_lookback_elems(w.cells_max + 1));
@@ -242,7 +234,7 @@ __global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_box_part(
 // (thread 0) the grid of that cloud.
 __global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_setup(
     const float* __restrict__ source, int64_t Ns, const int64_t* __restrict__ ptr_s, int k,
-    KnnGrid* __restrict__ grid, const uint32_t* __restrict__ box_part, int parts, int cell_cap) {
+    KnnGrid* __restrict__ grid, const uint32_t* __restrict__ box_part, int parts) {
   constexpr int W = kKnnSetupThreads / kWave;
   __shared__ uint32_t red[6][W];
   const int b = blockIdx.x;
@@ -300,7 +292,7 @@ __global__ __launch_bounds__(kKnnSetupThreads) void knn_grid_setup(
     for (int it = 0; it < 12 && h > 0.0; ++it)
       h = cbrt(fmax(ext[0], h) * fmax(ext[1], h) * fmax(ext[2], h) * target / static_cast<double>(n));
     if (h > 0.0) {
-      const double cap = static_cast<double>(cell_cap) * static_cast<double>(n) + 64.0;
+      const double cap = kKnnCellCap * static_cast<double>(n) + 64.0;
       int64_t d[3] = {1, 1, 1};
       bool ok = false;
       for (int it = 0; it < 64 && !ok; ++it) {
@@ -550,7 +542,7 @@ int launch_knn_grid(const float* query, int64_t Nq, const float* source, int64_t
     GEO_LAUNCH_CHECK("knn_grid_box_part");
   }
   hipLaunchKernelGGL(knn_grid_setup, dim3(B), dim3(kKnnSetupThreads), 0, st, source, Ns, ptr_s, k,
-                     w.grid, w.box_part, parts, w.cell_cap);
+                     w.grid, w.box_part, parts);
   GEO_LAUNCH_CHECK("knn_grid_setup");
   hipLaunchKernelGGL(knn_grid_base, dim3(1), dim3(kScanThreads), 0, st, w.grid, B);
   GEO_LAUNCH_CHECK("knn_grid_base");
