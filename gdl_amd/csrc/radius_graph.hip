@@ -6,6 +6,8 @@
 // cloud, both valid, loop or i != j, d < r2; per target the K smallest (d, j)).
 //
 // geo_radius_count:
+//   rg_front    clouds that are contiguous chunks of at most 4096 points: one workgroup per cloud
+//               does all that rg_init .. rg_scatter do below, in LDS, then rg_count and the scan
 //   rg_init     zero counters, reset bounding boxes
 //   rg_bbox     per-cloud point count and bounding box (wave-reduced atomics; one cloud without
 //               batch vector or mask: rg_bbox_one, at most 64 workgroups)
@@ -23,8 +25,8 @@
 // geo_radius_emit:
 //   rg_compact  kRgGroup lanes per target: the list sorted by source index into the CSR row;
 //               targets with more than K sources (or long lists) are done by the whole wave:
-//               the K smallest (d, j) by a binary search on the distance bits over the
-//               in-radius candidates held in LDS
+//               the K smallest (d, j) by a radix select on the distance bits of the in-radius
+//               candidates staged in LDS (a binary search over the stencil beyond kRgSelCap)
 //   rg_emit     (lists too large for the workspace) re-scans the stencil per target instead
 // Traversal order inside a cell is not deterministic (atomic ranks) and does not matter: the
 // accepted set is defined by a total order and the output is sorted.
@@ -732,24 +734,6 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
-// The 9 z-contiguous runs of the 3x3x3 stencil around (qx, qy, qz): start and length.
-__device__ __forceinline__ void stencil_runs(const RgWs& w, const Grid& g, float qx, float qy,
-                                             float qz, int (&ra)[9], int (&rn)[9]) {
-  const int cx = cell_coord(qx, g.ox, g.inv_h, g.dx);
-  const int cy = cell_coord(qy, g.oy, g.inv_h, g.dy);
-  const int cz = cell_coord(qz, g.oz, g.inv_h, g.dz);
-  const int z0 = cz > 0 ? cz - 1 : 0;
-  const int z1 = cz + 1 < g.dz ? cz + 1 : g.dz - 1;
-#pragma unroll
-  for (int r = 0; r < 9; ++r) {
-    const int ix = cx - 1 + r / 3, iy = cy - 1 + r % 3;
-    const bool in = ix >= 0 && ix < g.dx && iy >= 0 && iy < g.dy;
-    const int c0 = g.base + (ix * g.dy + iy) * g.dz;
-    ra[r] = in ? w.cell_start[c0 + z0] : 0;
-    rn[r] = in ? w.cell_start[c0 + z1 + 1] - ra[r] : 0;
-  }
-}
-
 // Run r (0..8) of the stencil around (qx, qy, qz): start and length.
 __device__ __forceinline__ void stencil_run(const RgWs& w, const Grid& g, float qx, float qy, float qz,
                                             int r, int& a, int& n) {
@@ -784,7 +768,8 @@ __device__ __forceinline__ void wave_scan_runs(const RgWs& w, const int (&ra)[9]
 //  c <= K: the list L[0..c) (complete) sorted by index, 64 entries per step.
 //  c > K:  the K smallest (d, j): the in-radius sources as (distance bits, index) pairs collected
 //          in LDS in one stencil pass (c <= kRgSelCap; beyond that every step re-scans the
-//          stencil), the K-th distance d* by binary search on the bits, the index threshold j*
+//          stencil), the K-th distance d* by radix select on the bits (binary search over the
+//          stencil beyond kRgSelCap), the index threshold j*
 //          among the sources at d* when they are more than needed, the accepted sources compacted
 //          in place and sorted by index.
 // The target's row offset o, and for c > K its position and stencil runs, come from the caller.
