@@ -149,6 +149,11 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// LDS writes of some lanes become visible to later reads of other lanes of the same wave.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
 // Wave-uniform max over all 64 lanes (every lane must be active): four in-row steps, two row
 // broadcasts, lane 63 holds the result.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {

@@ -729,11 +729,6 @@ constexpr int kRgSelCap = 1024;
 // Chunks of 64 stencil sources loaded together when staging (eight measured 1.5% slower at C5).
 constexpr int kRgStageLoads = 4;
 
-__device__ __forceinline__ void wave_lds_fence() {
-  // LDS writes of some lanes become visible to later reads of other lanes of the same wave
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-}
-
 // Run r (0..8) of the stencil around (qx, qy, qz): start and length.
 __device__ __forceinline__ void stencil_run(const RgWs& w, const Grid& g, float qx, float qy, float qz,
                                             int r, int& a, int& n) {

@@ -33,12 +33,17 @@ __device__ __forceinline__ int clamp_idx(int v, int lo, int hi) { return v < lo 
 // With zero_tail, the rows of the CSR positions [node_end[S-1], E) — the edges whose target lies
 // outside [0, S) in a CSR built by geo_csr_build, whose node ranges are ascending and contiguous
 // from 0 — are written as 0 by the grid's threads together, so no separate fill of the output is
-// needed.  The tail is empty for a CSR that covers every edge: one uniform load per thread.
+// needed.  The tail is empty for a CSR that covers every edge.  The fp32 kernels load its start
+// (one uniform load) together with their CSR bounds and write the zeros after their own work,
+// so the load adds no step to their chain of dependent loads.
+__device__ __forceinline__ int tail_start(int zero_tail, const int32_t* __restrict__ ne, int32_t E,
+                                          int64_t S) {
+  return zero_tail ? clamp_idx(ne[S - 1], 0, E) : E;
+}
+
 template <typename T>
-__device__ __forceinline__ void zero_tail_rows(T* __restrict__ out, const int32_t* __restrict__ perm,
-                                               const int32_t* __restrict__ ne, int32_t E, int64_t S,
-                                               int64_t H) {
-  const int t0 = clamp_idx(ne[S - 1], 0, E);
+__device__ __forceinline__ void zero_rows_from(T* __restrict__ out, const int32_t* __restrict__ perm,
+                                               int t0, int32_t E, int64_t H) {
   const int64_t n = static_cast<int64_t>(E - t0) * H;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -48,6 +53,13 @@ __device__ __forceinline__ void zero_tail_rows(T* __restrict__ out, const int32_
     if (static_cast<unsigned>(r) < static_cast<unsigned>(E))
       out[static_cast<int64_t>(r) * H + (i - q * H)] = T(0);
   }
+}
+
+template <typename T>
+__device__ __forceinline__ void zero_tail_rows(T* __restrict__ out, const int32_t* __restrict__ perm,
+                                               const int32_t* __restrict__ ne, int32_t E, int64_t S,
+                                               int64_t H) {
+  zero_rows_from<T>(out, perm, clamp_idx(ne[S - 1], 0, E), E, H);
 }
 
 // Largest value over the wave (v >= 0; every lane active).
@@ -177,11 +189,31 @@ __device__ __forceinline__ int sm_row(const int32_t* perm, int32_t E, int e) {
   return static_cast<unsigned>(r) < static_cast<unsigned>(E) ? r : -1;
 }
 
+// Rows of the CSR positions e[i] where ok[i] (-1 elsewhere, and for a permutation entry outside
+// [0, E)).  Every permutation entry is loaded before any is checked: with the check right after
+// its load the compiler waits for each load in turn.  Positions that are not ok read entry 0
+// (E >= 1).
+template <int NR>
+__device__ __forceinline__ void sm_rows(const int32_t* __restrict__ perm, int32_t E,
+                                        const int (&e)[NR], const bool (&ok)[NR], int (&r)[NR]) {
+  if (perm) {
+    int v[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) v[i] = perm[ok[i] ? e[i] : 0];
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+      r[i] = ok[i] && static_cast<unsigned>(v[i]) < static_cast<unsigned>(E) ? v[i] : -1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) r[i] = ok[i] ? e[i] : -1;
+  }
+}
+
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_fwd(
     const float* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
     const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H, float* __restrict__ w,
     int zero_tail) {
-  if (zero_tail) zero_tail_rows<float>(w, perm, ne, E, S, H);
+  const int t0 = tail_start(zero_tail, ne, E, S);
   const RowSeg g = row_seg(ns, ne, E, S);
   // chunks of 16 edges; every lane of the wave runs the wave's largest chunk count, so the row
   // reductions below see all sixteen lanes of every row.  The first two chunks (segments of up
@@ -202,10 +234,15 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_fwd(
   auto val = [&](int c, int r, int h) -> float {
     return c == 0 ? keep[0][h] : (c == 1 ? keep[1][h] : x[static_cast<int64_t>(r) * H + h]);
   };
+  {
+    int e[2];
+    bool ok[2];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int e = g.a + 16 * c + g.li;
-    rk[c] = (c < nch && e < g.b) ? sm_row(perm, E, e) : -1;
+    for (int c = 0; c < 2; ++c) {
+      e[c] = g.a + 16 * c + g.li;
+      ok[c] = c < nch && e[c] < g.b;
+    }
+    sm_rows<2>(perm, E, e, ok, rk);
   }
 #pragma unroll
   for (int c = 0; c < 2; ++c)
@@ -248,13 +285,14 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_fwd(
     for (int h = 0; h < kSmRowHeads; ++h)
       if (h < H && r >= 0) w[static_cast<int64_t>(r) * H + h] = expf(val(c, r, h) - m[h]) / z[h];
   }
+  zero_rows_from<float>(w, perm, t0, E, H);
 }
 
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_bwd(
     const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S, int32_t H,
     float* __restrict__ dx, int zero_tail) {
-  if (zero_tail) zero_tail_rows<float>(dx, perm, ne, E, S, H);
+  const int t0 = tail_start(zero_tail, ne, E, S);
   const RowSeg g = row_seg(ns, ne, E, S);
   const int nch = uniform_max((g.b - g.a + 15) >> 4);
   float dot[kSmRowHeads], g0[kSmRowHeads], w0[kSmRowHeads];
@@ -291,6 +329,7 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_rows_bwd(
       }
     }
   }
+  zero_rows_from<float>(dx, perm, t0, E, H);
 }
 
 
@@ -371,7 +410,7 @@ template <int HH, int LW>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
     const float* __restrict__ x, const int32_t* __restrict__ perm, const int32_t* __restrict__ ns,
     const int32_t* __restrict__ ne, int32_t E, int64_t S, float* __restrict__ w, int zero_tail) {
-  if (zero_tail) zero_tail_rows<float>(w, perm, ne, E, S, HH);
+  const int t0 = tail_start(zero_tail, ne, E, S);
   constexpr int SQ = sm_quads<HH, LW>();
   constexpr int KC = 32 / LW;
   const int li = lane_id() & (LW - 1);
@@ -380,13 +419,22 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
   float v[SQ][KC][HH];
 #pragma unroll
   for (int q = 0; q < SQ; ++q) sm_bounds<LW>(ns, ne, E, S, wave * SQ + q, a[q], b[q]);
+  {
+    int e[SQ * KC], r[SQ * KC];
+    bool ok[SQ * KC];
 #pragma unroll
-  for (int q = 0; q < SQ; ++q)
+    for (int q = 0; q < SQ; ++q)
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const int e = a[q] + LW * c + li;
-      rk[q][c] = e < b[q] ? sm_row(perm, E, e) : -1;
-    }
+      for (int c = 0; c < KC; ++c) {
+        e[q * KC + c] = a[q] + LW * c + li;
+        ok[q * KC + c] = e[q * KC + c] < b[q];
+      }
+    sm_rows<SQ * KC>(perm, E, e, ok, r);
+#pragma unroll
+    for (int q = 0; q < SQ; ++q)
+#pragma unroll
+      for (int c = 0; c < KC; ++c) rk[q][c] = r[q * KC + c];
+  }
 #pragma unroll
   for (int q = 0; q < SQ; ++q)
 #pragma unroll
@@ -470,6 +518,7 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
       }
     }
   }
+  zero_rows_from<float>(w, perm, t0, E, HH);
 }
 
 template <int HH, int LW>
@@ -477,7 +526,7 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
     const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ ns, const int32_t* __restrict__ ne, int32_t E, int64_t S,
     float* __restrict__ dx, int zero_tail) {
-  if (zero_tail) zero_tail_rows<float>(dx, perm, ne, E, S, HH);
+  const int t0 = tail_start(zero_tail, ne, E, S);
   constexpr int SQ = sm_quads<HH, LW>();
   const int li = lane_id() & (LW - 1);
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kSmThreads / kWave) + threadIdx.x / kWave;
@@ -543,6 +592,7 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
       }
     }
   }
+  zero_rows_from<float>(dx, perm, t0, E, HH);
 }
 
 }  // namespace

@@ -194,3 +194,64 @@ def test_segment_softmax_misaligned_rows_match_aligned(dev):
     _check(a, ref, torch.float32)
     _check(b, ref, torch.float32)
     torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-7)
+
+
+def _contiguous_case(g, N, deg, H, tail):
+    """Shuffled edges with target degrees ``deg`` plus ``tail`` edges whose target is N (outside
+    every segment: the CSR puts them after the last one); perm = stable sort by target."""
+    index = torch.cat([torch.repeat_interleave(torch.arange(N), deg),
+                       torch.full((tail,), N, dtype=torch.int64)])
+    index = index[torch.randperm(index.numel(), generator=g)]
+    perm = torch.sort(index, stable=True).indices
+    cnt = torch.bincount(index[index < N], minlength=N)
+    ne = cnt.cumsum(0).int()
+    ns = ne - cnt.int()
+    x = torch.randn(index.numel(), H, generator=g) * 3
+    return index, perm, ns, ne, x
+
+
+@pytest.mark.parametrize("H", [1, 2, 4, 8])
+@pytest.mark.parametrize("kind", ["graph", "long", "bad_perm"])
+def test_segment_softmax_contiguous_csr_short_segments(dev, H, kind):
+    """A contiguous CSR whose segments average at most 12 edges (a radius graph's: 8 lanes per
+    segment), called with contiguous_csr=True, so the kernel writes the rows after the last
+    segment itself and its permutation entries are loaded together before they are checked.
+    graph: degrees 0..20, a NaN score, edges after the last segment (written as 0).
+    long: short segments with some of 600..1200 edges (chunks past the fourth re-read).
+    bad_perm: permutation entries outside [0, E) at some positions: those are skipped."""
+    from gdl_amd.csrc import segment_softmax_forward_hip
+    g = torch.Generator().manual_seed(7 + 11 * H + len(kind))
+    N = 4000
+    if kind == "long":
+        deg = torch.randint(0, 8, (N,), generator=g)
+        deg[0::320] = torch.randint(600, 1201, (deg[0::320].numel(),), generator=g)
+        deg[45::300] = torch.randint(600, 1201, (deg[45::300].numel(),), generator=g)
+    else:
+        deg = torch.randint(0, 21, (N,), generator=g)
+    deg[3::17] = 0
+    tail = 0 if kind == "bad_perm" else 333
+    index, perm, ns, ne, x = _contiguous_case(g, N, deg, H, tail)
+    E = index.numel()
+    assert E - tail <= 12 * N
+    x[int(perm[int(ns[5])]), 0] = float("nan")
+    pos_ok = torch.ones(E, dtype=torch.bool)
+    if kind == "bad_perm":
+        bad = torch.randperm(E, generator=g)[:E // 50]
+        pos_ok[bad] = False
+        perm_dev = perm.clone()
+        perm_dev[bad[0::2]] = -1
+        perm_dev[bad[1::2]] = E + 5
+    else:
+        perm_dev = perm
+    w = segment_softmax_forward_hip(x.to(dev), perm_dev.int().to(dev), ns.to(dev), ne.to(dev), N,
+                                    contiguous_csr=True).cpu().double().numpy()
+    seg_of_pos = torch.sort(index, stable=True).values
+    use = pos_ok & (seg_of_pos < N)
+    rows = perm[use]
+    ref = oracle.sparse_softmax(x[rows].double().numpy(), seg_of_pos[use].numpy(), N)
+    got = w[rows.numpy()]
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.all(np.abs(got[ok] - ref[ok]) <= 2e-6 + 1e-5 * np.abs(ref[ok]))
+    if tail:
+        assert np.all(w[perm[seg_of_pos >= N].numpy()] == 0)
