@@ -56,7 +56,7 @@ def test_fps_vs_oracle(dev, sizes, ks, seed):
 
 
 def test_fps_large_clouds(dev):
-    """Clouds above 16384 points take the Morton-bucket path with points in the workspace:
+    """Clouds above 16384 points take the Hilbert-bucket path with points in the workspace:
     several clouds, empty and tiny clouds, points outside every cloud, k = n and k = 0."""
     g = torch.Generator().manual_seed(11)
     pos = torch.randn(47100, 3, generator=g) * torch.tensor([30.0, 5.0, 1.0])
@@ -76,7 +76,7 @@ def test_fps_duplicate_points(dev):
     distance 0 and the lowest index among them must be taken next.  This drives the bucket
     records through ties at equal maxima (the point holding a bucket's maximum falls while an
     equal value at a higher index stays), in the bucketed kernel (4096 points) and the
-    Morton-bucket kernel for large clouds (24,576 points)."""
+    Hilbert-bucket kernel for large clouds (24,576 points)."""
     g = torch.Generator().manual_seed(21)
     base = torch.randn(1024, 3, generator=g)
     pos = base[torch.randint(0, 1024, (4096,), generator=g)]
