@@ -84,22 +84,6 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false));
 }
 
-// Every lane receives the max / min of its 16-lane row.
-__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
-  v = max(v, dpp_u32<kDppXor1>(v));
-  v = max(v, dpp_u32<kDppXor2>(v));
-  v = max(v, dpp_u32<kDppHalfMirror>(v));
-  v = max(v, dpp_u32<kDppMirror>(v));
-  return v;
-}
-__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
-  v = min(v, dpp_u32<kDppXor1>(v));
-  v = min(v, dpp_u32<kDppXor2>(v));
-  v = min(v, dpp_u32<kDppHalfMirror>(v));
-  v = min(v, dpp_u32<kDppMirror>(v));
-  return v;
-}
-
 // Sum over all 64 lanes (every lane must be active), wave-uniform: DPP sums within each 16-lane
 // row, then the four row totals read from lanes 0, 16, 32, 48 (no LDS round trips, unlike a
 // shuffle tree).
@@ -246,18 +230,6 @@ __device__ __forceinline__ int cell_rank(int* counter, int key) {
   const int runs = __popcll(__ballot(lane == 0 || prev != key));
   if (runs <= 16) return wave_aggregated_rank(counter, key);
   return atomicAdd(counter, 1);
-}
-
-// Wave-wide inclusive prefix sum (all lanes active).
-template <typename T>
-__device__ __forceinline__ T wave_inclusive_sum(T v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    T o = __shfl_up(v, d, kWave);
-    if (l >= d) v += o;
-  }
-  return v;
 }
 
 // Inclusive prefix sum and sum of 4- or 8-byte integers over the wave, all in DPP (every lane

@@ -124,22 +124,6 @@ __device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, i
   return q;
 }
 
-// The staged scalars of lane j (j wave-uniform).
-__device__ __forceinline__ EdgeScalars edge_at(const EdgeScalars& st, int j) {
-  EdgeScalars q;
-  q.other = __builtin_amdgcn_readlane(st.other, j);
-  q.e = __builtin_amdgcn_readlane(st.e, j);
-  q.ok = __builtin_amdgcn_readlane(st.ok, j);
-#pragma unroll
-  for (int i = 0; i < kSePaths; ++i) q.r[i] = rlane(st.r[i], j);
-#pragma unroll
-  for (int k = 0; k < 3; ++k) q.d[k] = rlane(st.d[k], j);
-  q.y0 = rlane(st.y0, j);
-#pragma unroll
-  for (int m = 0; m < 5; ++m) q.y2[m] = rlane(st.y2[m], j);
-  return q;
-}
-
 // The staged scalars of lane j (j may differ between lanes).
 __device__ __forceinline__ EdgeScalars edge_from(const EdgeScalars& st, int j) {
   EdgeScalars q;
