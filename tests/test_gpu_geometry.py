@@ -66,6 +66,18 @@ def test_fps_large_clouds(dev):
     _fps_check(dev, pos[:20000], _ptr([20000]), torch.tensor([4000]))
 
 
+@pytest.mark.parametrize("n,k", [(8192, 300), (8193, 300), (16384, 300), (16385, 300),
+                                 (196608, 48), (196609, 48)])
+def test_fps_kernel_boundaries(dev, n, k):
+    """One cloud at each kernel-selection boundary: the bucketed kernel's largest cloud (8192),
+    the register kernel's smallest and largest (8193, 16384), the large kernel's smallest and its
+    full capacity (16385; 196,608 = 3 slots x 1024 lanes x 64 points), and the streaming kernel
+    above it (196,609)."""
+    g = torch.Generator().manual_seed(n)
+    pos = torch.randn(n, 3, generator=g) * torch.tensor([4.0, 2.0, 1.0])
+    _fps_check(dev, pos, _ptr([n]), torch.tensor([k]))
+
+
 def test_fps_large_tie_lattice(dev):
     pos = _lattice(30, 3)  # 27,000 integer points: exact distances, ties at every step
     _fps_check(dev, pos, _ptr([27000]), torch.tensor([3000]))
