@@ -436,6 +436,24 @@ def test_radius_dense_blob_wave_selection_paths(dev):
     _rg_check(dev, x, 0.05, 1100, loop=True)
 
 
+@pytest.mark.parametrize("per,r", [(1025, 0.13), (5000, 0.078)])
+def test_radius_without_lists(dev, per, r):
+    """When N x K exceeds the per-target lists the workspace holds (2^28 entries), the rows come
+    from the emit kernel, which re-scans each target's stencil: rows sorted in LDS for K <= 256,
+    the K-th distance and the index threshold found by binary search for targets above K.
+    About 1.05 M points with K = 256, in clouds of 1025 points (the per-cloud front end) or of
+    5000 (the general grid build), each cloud in its own unit cube (~10 sources per target);
+    three clouds are blobs 0.02 across, where every target has more than K sources."""
+    K = 256
+    B = -(-1049600 // per)
+    N = B * per
+    assert N * K > (1 << 28)
+    g = torch.Generator().manual_seed(per)
+    x = torch.rand(N, 3, generator=g)
+    x[: 3 * per] *= 0.02
+    _rg_check(dev, x, r, K, nb=B)
+
+
 # ------------------------------------------------------------------------ BASELINE configs ---
 
 def test_config_c1(dev):
