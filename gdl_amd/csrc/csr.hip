@@ -2,7 +2,8 @@
 // geoembodied/csrc/segment_reduce_kernel.cu:100-169, which uses CUB radix sort + transition
 // detection).
 //
-// Stable LSD radix sort (radix.hpp) of the int32 target ids with the edge index as value.
+// Stable LSD radix sort (radix.hpp) of the int32 target ids with the edge index as value (small
+// inputs: one workgroup sorting in LDS, csr_small).
 // Targets outside [0, N) get key N and sort after all valid targets.  node_start/node_end come
 // from binary searches in the sorted keys (node_start[n] = first position with key >= n), so
 // empty targets get start == end and no atomics are involved.
@@ -28,6 +29,105 @@ __global__ void csr_bounds(const uint32_t* __restrict__ sorted_keys, int64_t E, 
   if (n > 0) node_end[n - 1] = static_cast<int32_t>(lo);
 }
 
+// Small inputs (E <= kCsrSmallMaxE, N <= kCsrSmallMaxN) in one launch: one workgroup holds the
+// (key, index) pairs in LDS as 64-bit words key << 32 | index; input already in key order is
+// written as it is, anything else is first sorted in LDS by a stable LSD radix sort of the keys
+// (two 8-bit passes: keys <= N < 2^16); the bounds are binary searches in the LDS keys.  The
+// radix path costs about a dozen launches, which for a few thousand edges is most of its time.
+constexpr int kCsrSmallThreads = 1024;
+constexpr int kCsrSmallWaves = kCsrSmallThreads / kWave;
+constexpr int kCsrSmallChunks = 2;
+constexpr int kCsrSmallMaxE = kCsrSmallChunks * kCsrSmallThreads;
+constexpr int64_t kCsrSmallMaxN = 16384;
+constexpr int kCsrSmallCounts = 256 * kCsrSmallChunks * kCsrSmallWaves;  // (digit, chunk, wave)
+static_assert(kCsrSmallCounts == 8 * kCsrSmallThreads, "eight counters per thread in the scan");
+
+__global__ __launch_bounds__(kCsrSmallThreads) void csr_small(const int64_t* __restrict__ col, int E,
+                                                             int N, int32_t* __restrict__ col_sorted,
+                                                             int32_t* __restrict__ perm,
+                                                             int32_t* __restrict__ node_start,
+                                                             int32_t* __restrict__ node_end) {
+  __shared__ uint64_t s_kv[kCsrSmallMaxE];
+  __shared__ uint64_t s_tmp[kCsrSmallMaxE];
+  __shared__ uint32_t s_cnt[kCsrSmallCounts];
+  __shared__ uint32_t s_wsum[kCsrSmallWaves];
+  __shared__ int s_down;
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = lane_id();
+  if (t == 0) s_down = 0;
+  for (int i = t; i < E; i += kCsrSmallThreads) {
+    const int64_t c = col[i];
+    const uint32_t k = (c >= 0 && c < N) ? static_cast<uint32_t>(c) : static_cast<uint32_t>(N);
+    s_kv[i] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(i);
+  }
+  __syncthreads();
+  bool down = false;
+  for (int i = t + 1; i < E; i += kCsrSmallThreads) down |= (s_kv[i] >> 32) < (s_kv[i - 1] >> 32);
+  if (down) s_down = 1;
+  __syncthreads();
+  if (s_down) {  // block-uniform
+    // element c * kCsrSmallThreads + t of a pass's source is thread t's chunk c, so the order
+    // (digit, chunk, wave, lane) is the stable order of the pass
+    const uint64_t lt = lanemask_lt();
+    uint64_t* src = s_kv;
+    uint64_t* dst = s_tmp;
+    for (int pass = 0; pass < 2; ++pass) {
+      const int shift = 32 + 8 * pass;
+      for (int q = t; q < kCsrSmallCounts; q += kCsrSmallThreads) s_cnt[q] = 0;
+      __syncthreads();
+      uint64_t v[kCsrSmallChunks];
+      uint32_t d[kCsrSmallChunks], r[kCsrSmallChunks];
+      bool ok[kCsrSmallChunks];
+#pragma unroll
+      for (int c = 0; c < kCsrSmallChunks; ++c) {
+        const int i = c * kCsrSmallThreads + t;
+        ok[c] = i < E;
+        v[c] = ok[c] ? src[i] : 0ull;
+        d[c] = static_cast<uint32_t>(v[c] >> shift) & 255u;
+        const uint64_t peers = rx_peers<8>(d[c], ok[c]);  // same digit, same chunk and wave
+        r[c] = static_cast<uint32_t>(__popcll(peers & lt));
+        if (ok[c] && r[c] == 0)
+          s_cnt[(d[c] * kCsrSmallChunks + c) * kCsrSmallWaves + w] = static_cast<uint32_t>(__popcll(peers));
+      }
+      __syncthreads();
+      uint32_t loc[8], sum = 0;  // exclusive scan of the counters in place, eight per thread
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { loc[j] = s_cnt[8 * t + j]; sum += loc[j]; }
+      const uint32_t inc = wave_inclusive_sum_dpp(sum);
+      if (lane == kWave - 1) s_wsum[w] = inc;
+      __syncthreads();
+      uint32_t off = inc - sum;
+      for (int ww = 0; ww < w; ++ww) off += s_wsum[ww];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { s_cnt[8 * t + j] = off; off += loc[j]; }
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < kCsrSmallChunks; ++c)
+        if (ok[c]) dst[s_cnt[(d[c] * kCsrSmallChunks + c) * kCsrSmallWaves + w] + r[c]] = v[c];
+      __syncthreads();
+      uint64_t* tmp = src;
+      src = dst;
+      dst = tmp;
+    }
+    // two passes: the result is back in s_kv
+  }
+  for (int i = t; i < E; i += kCsrSmallThreads) {
+    const uint64_t v = s_kv[i];
+    col_sorted[i] = static_cast<int32_t>(v >> 32);
+    perm[i] = static_cast<int32_t>(static_cast<uint32_t>(v));
+  }
+  for (int n = t; n <= N; n += kCsrSmallThreads) {  // lb(n): node_start[n], node_end[n - 1]
+    int lo = 0, hi = E;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (static_cast<uint32_t>(s_kv[mid] >> 32) < static_cast<uint32_t>(n)) lo = mid + 1; else hi = mid;
+    }
+    if (n < N) node_start[n] = lo;
+    if (n > 0) node_end[n - 1] = lo;
+  }
+}
+
 int radix_key_bits(int64_t N) {
   int bits = 0;
   while (bits < 32 && (static_cast<uint64_t>(N) >> bits) != 0) ++bits;  // bits to hold key N
@@ -49,6 +149,12 @@ int csr_build_into(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted
     int rc = device_fill<int32_t>(node_start, N, 0, st);
     if (rc) return rc;
     return device_fill<int32_t>(node_end, N, 0, st);
+  }
+  if (E <= kCsrSmallMaxE && N <= kCsrSmallMaxN) {
+    hipLaunchKernelGGL(csr_small, dim3(1), dim3(kCsrSmallThreads), 0, st, col, static_cast<int>(E),
+                       static_cast<int>(N), col_sorted, perm, node_start, node_end);
+    GEO_LAUNCH_CHECK("csr_small");
+    return GEO_OK;
   }
   // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one pass
   int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),

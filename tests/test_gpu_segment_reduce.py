@@ -42,7 +42,10 @@ def _np(t):
 # ----------------------------------------------------------------------------- CSR build ---
 
 @pytest.mark.parametrize("E,N,seed", [(1, 1, 0), (1000, 10, 1), (5000, 300, 2), (70000, 70000, 3),
-                                      (200000, 5000, 4), (300000, 20_000_000, 5)])
+                                      (200000, 5000, 4), (300000, 20_000_000, 5),
+                                      # either side of the one-workgroup path (E <= 2048, N <= 16384)
+                                      (2048, 16384, 6), (2049, 16384, 7), (2048, 16385, 8),
+                                      (2048, 3, 9)])
 def test_csr_matches_oracle(dev, E, N, seed):
     _, csr = _ops()
     g = torch.Generator().manual_seed(seed)
