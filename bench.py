@@ -171,19 +171,25 @@ def _se3_reference_torch(conv, s, v, gr):
 
 def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx, dist, gr, conv,
                      fs, fv) -> dict:
-    """HIP-event time of single kernels of the fused rows on the C2 graph, with their algorithmic
-    bytes (every access of the kernel's pattern counted once: gathered rows per gather) and the
-    fraction of the 8 TB/s HBM peak."""
+    """HIP-event time of single kernels of the fused rows on the C2 graph.  ``bytes`` are the
+    compulsory bytes (every input element read once, however often it is gathered, every output
+    written once) and ``frac`` their fraction of the 8 TB/s HBM peak; ``gathered_bytes`` counts a
+    gathered row once per gather (the traffic the kernel's access pattern asks of L2, of which
+    the L2 serves the repeats)."""
     from gdl_amd import _native as nat
     from gdl_amd.csrc import edge_geometry_hip
     from gdl_amd.functional.gather import gather_weighted_sum, idw_weights
     from gdl_amd.functional.segment_softmax import segment_softmax
     from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pad16, path_columns
 
-    def entry(us, nbytes):
+    def entry(us, nbytes, gathered=None):
         gbs = nbytes / (us * 1e-6) / 1e9
-        return {"us": round(us, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
-                "frac": round(gbs / 8000.0, 4)}
+        e = {"us": round(us, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1),
+             "frac": round(gbs / 8000.0, 4)}
+        if gathered is not None:
+            e["gathered_bytes"] = int(gathered)
+            e["gathered_GB/s"] = round(gathered / (us * 1e-6) / 1e9, 1)
+        return e
 
     out = {}
     E, N, H = row.numel(), pos.shape[0], scores.shape[1]
@@ -203,10 +209,12 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
     n_out, K = idx.shape
     C = feats.shape[1]
     us = 1e3 * event_ms(lambda: gather_weighted_sum(feats, idx, w), args.iters, 5)
-    out["gather_weighted_sum_k3_c112"] = entry(us, n_out * K * (8 + 4 + C * 4) + n_out * C * 4)
+    out["gather_weighted_sum_k3_c112"] = entry(
+        us, feats.shape[0] * C * 4 + n_out * K * (8 + 4) + n_out * C * 4,
+        n_out * K * (8 + 4 + C * 4) + n_out * C * 4)
     with torch.no_grad():
         us = 1e3 * event_ms(lambda: edge_geometry_hip(pos, row, col, 2), args.iters, 5)
-    out["edge_geometry_l2"] = entry(us, E * (16 + 24 + 52))
+    out["edge_geometry_l2"] = entry(us, N * 12 + E * (16 + 52), E * (16 + 24 + 52))
     # the SE3 forward aggregate alone (sums of r-weighted source features per target)
     Cs, Cv = fs.shape[1], fv.shape[1]
     weights = {k: getattr(conv, k).weight if getattr(conv, k) is not None else None for k in PATH_NAMES}
@@ -228,8 +236,10 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
             nat.ptr(Xs), plan.Ks, nat.ptr(Xv), plan.Kv, None, 0, nat.stream_of(dev)), "aggregate")
 
     us = 1e3 * event_ms(agg, args.iters, 5)
+    per_edge = E * (8 + 4 * P + 12 + 4)        # source id, R row, direction, Y_0
     out["se3_fwd_aggregate_64s16v"] = entry(
-        us, E * (Cs + 3 * Cv) * 4 + E * (8 + 4 * P + 12 + 4) + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4)
+        us, N * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4,
+        E * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4)
     assert _pad16(Cs + 2 * Cv) == plan.Kv
     return out
 
@@ -271,9 +281,56 @@ def cpu_ms(fn, runs: int = 3) -> float:
     return sorted(ts)[len(ts) // 2]
 
 
+def cpu_threads() -> dict:
+    """The host's CPU counts and the threads the CPU baselines run on.  The baselines run with
+    every CPU this process may use (its affinity set, at most OMP_NUM_THREADS when that is set:
+    a GPU box allots a fixed CPU share to each GPU whatever os.cpu_count() reports); the counts
+    are reported beside every CPU figure."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    use = affinity
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        use = min(use, int(omp))
+    return {"os_cpu_count": os.cpu_count(), "affinity": affinity, "threads": use}
+
+
 def _cpu_entry(value_ms: float, unit: str, sample: str) -> dict:
+    t = cpu_threads()
     return {"value": round(value_ms, 2), "unit": unit, "cores": torch.get_num_threads(),
-            "kind": "port", "sample": sample}
+            "os_cpu_count": t["os_cpu_count"], "kind": "port", "sample": sample}
+
+
+def compulsory(nbytes: int, ms: float) -> dict:
+    """Compulsory HBM bytes of one call (inputs read once, outputs written once) and the fraction
+    of the 8 TB/s peak they make at the measured time."""
+    return {"bytes": int(nbytes), "ms": round(ms, 4),
+            "frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 5)}
+
+
+def fps_bytes(n_points: int, n_samples: int) -> int:
+    """FPS: positions read once (12 B per point), int64 sample indices written."""
+    return n_points * 12 + n_samples * 8
+
+
+def knn_bytes(n_q: int, n_s: int, k: int, n_clouds: int) -> int:
+    """KNN: queries and sources read once, both cloud offset arrays, [n_q, k] int64 indices and
+    fp32 distances written."""
+    return (n_q + n_s) * 12 + 2 * (n_clouds + 1) * 8 + n_q * k * 12
+
+
+def radius_bytes(n_points: int, n_edges: int, batch: bool) -> int:
+    """Radius graph: positions read once (and the int64 batch vector when given), int64 row and
+    col written."""
+    return n_points * 12 + (n_points * 8 if batch else 0) + n_edges * 16
+
+
+def csr_bytes(n_edges: int, n_nodes: int) -> int:
+    """CSR build: int64 targets read, int32 col_sorted and perm written, int32 node_start and
+    node_end written."""
+    return n_edges * 8 + n_edges * 8 + n_nodes * 8
 
 
 def _ops():
@@ -348,6 +405,18 @@ def leg_c2(args, dev) -> tuple:
     leg["radius_centres_ms"] = round(wall_ms(
         lambda: radius_graph(cent, c2["r"], max_num_neighbors=c2["K"], num_batch_elements=c2["B"]),
         args.steps, 3), 4)
+    e_cent = int(radius_graph(cent, c2["r"], max_num_neighbors=c2["K"],
+                              num_batch_elements=c2["B"])[0].numel())
+    leg["csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col, pos.shape[0]),
+                                        args.steps, 3), 4)
+    n2, m2 = pos.shape[0], c2["B"] * c2["M"]
+    leg["compulsory"] = {
+        "fps": compulsory(fps_bytes(n2, m2), leg["fps_ms"]),
+        "radius_all_points": compulsory(radius_bytes(n2, leg["edges"], True), leg["radius_ms"]),
+        "radius_centres": compulsory(radius_bytes(m2, e_cent, False), leg["radius_centres_ms"]),
+        "knn_k16": compulsory(knn_bytes(m2, n2, c2["k"], c2["B"]), leg["knn_k16_ms"]),
+        "csr_build": compulsory(csr_bytes(leg["edges"], n2), leg["csr_build_ms"]),
+    }
     log(f"  step {ms_step:.3f} ms (one stream {leg['step_one_stream_ms']:.3f})  fps "
         f"{leg['fps_ms']:.3f}  radius {leg['radius_ms']:.3f}  knn {leg['knn_k16_ms']:.3f}  "
         f"edges {leg['edges']}")
@@ -441,7 +510,8 @@ def leg_c2(args, dev) -> tuple:
             t2 = time.perf_counter()
             runs.append((t2 - t0, t1 - t0, t2 - t1))
         tot, t_fps, t_rad = sorted(runs)[1]
-        cpu = {"value": round(tot * 1e3, 1), "unit": "ms/batch", "cores": threads, "kind": "port",
+        cpu = {"value": round(tot * 1e3, 1), "unit": "ms/batch", "cores": threads,
+               "os_cpu_count": os.cpu_count(), "kind": "port",
                "sample": f"reference CPU path (iterative FPS + batched cdist/topk radius graph, "
                          f"oracle/ref_cpu_path.py) on the full C2 batch, median of 3; fps "
                          f"{t_fps:.2f} s, radius {t_rad:.2f} s",
@@ -528,6 +598,9 @@ def leg_c3(args, dev) -> tuple:
     # the same targets in random order (the sorted-input identity path does not apply)
     col_sh = col64[torch.randperm(E, device=dev, generator=gen)]
     leg["csr_build_shuffled_ms"] = round(wall_ms(lambda: sort_and_build_csr(col_sh, S), 10, 2), 4)
+    leg["compulsory"] = {"csr_build_sorted": compulsory(csr_bytes(E, S), leg["csr_build_ms"]),
+                         "csr_build_shuffled": compulsory(csr_bytes(E, S),
+                                                          leg["csr_build_shuffled_ms"])}
     log(f"  CSR build: {leg['csr_build_ms']} ms sorted, {leg['csr_build_shuffled_ms']} ms shuffled")
     del col_sh, msg
     if not args.no_cpu and args.only is None:
@@ -570,6 +643,7 @@ def leg_c1(args, dev) -> dict:
 
     leg = {"step_ms": round(wall_ms(c1_step, 20, 3), 4)}
     leg["fps_ms"] = round(wall_ms(lambda: fps(p1, c1["M"]), 20, 3), 4)
+    leg["compulsory"] = {"fps": compulsory(fps_bytes(2048, c1["M"]), leg["fps_ms"])}
     log(f"C1: step {leg['step_ms']} ms (fps {leg['fps_ms']} ms)")
     if not args.no_cpu:
         from oracle import ref_cpu_path
@@ -669,6 +743,13 @@ def leg_c5(args, dev) -> dict:
     leg["segsum_all_points_gbs"] = round((E * c5["C"] * 4 + N * c5["C"] * 4 + (N + 1) * 4 + E * 4)
                                          / (ms * 1e-3) / 1e9, 1)
     leg["frame_ms"] = round(leg["fps_ms"] + leg["radius_all_points_ms"] + leg["knn_k8_ms"] + ms, 3)
+    leg["csr_build_ms"] = round(wall_ms(lambda: sort_and_build_csr(col, N), 10, 2), 4)
+    leg["compulsory"] = {
+        "fps": compulsory(fps_bytes(N, M), leg["fps_ms"]),
+        "radius_all_points": compulsory(radius_bytes(N, E, False), leg["radius_all_points_ms"]),
+        "knn_k8": compulsory(knn_bytes(M, N, c5["k"], 1), leg["knn_k8_ms"]),
+        "csr_build": compulsory(csr_bytes(E, N), leg["csr_build_ms"]),
+    }
     log(f"C5: fps {leg['fps_ms']} ms, radius centres {leg['radius_centres_ms']} ms, all points "
         f"{leg['radius_all_points_ms']} ms ({E} edges), knn {leg['knn_k8_ms']} ms, segment sum "
         f"{ms:.4f} ms ({leg['segsum_all_points_gbs']} GB/s)")
@@ -840,6 +921,8 @@ def main() -> int:
         print(json.dumps({"leg": "copy", "ms": round(ms, 4), "gbs": round(gbs, 1)}), flush=True)
         return 0
 
+    if not args.no_cpu:
+        torch.set_num_threads(cpu_threads()["threads"])
     legs: dict = {}
     ms_step = cpu = roof = None
     if args.only in (None, "c2"):
@@ -875,6 +958,8 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": cpu,
         "legs": legs,
+        "host_cpu": {**cpu_threads(), "torch_threads": torch.get_num_threads(),
+                     "model": _cpu_model()},
         "library": _native.build_info(),
         "device": torch.cuda.get_device_name(dev),
     }

@@ -64,20 +64,26 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile all HIP sources and link the shared library; returns its path."""
+def build(verbose: bool = False, extra_flags: list[str] | None = None,
+          out_dir: Path | None = None) -> Path:
+    """Compile all HIP sources and link the shared library; returns its path.  ``extra_flags``
+    are appended to every compile and link line; with ``out_dir`` the objects and the library
+    go there instead of ``_build/`` and ``lib/`` (a checking build beside the one that ships)."""
     if not Path(HIPCC).exists() and shutil.which(HIPCC) is None:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    BUILDDIR.mkdir(exist_ok=True)
-    LIBDIR.mkdir(exist_ok=True)
+    extra = list(extra_flags or [])
+    builddir = BUILDDIR if out_dir is None else Path(out_dir)
+    out = lib_path() if out_dir is None else Path(out_dir) / LIBNAME
+    builddir.mkdir(parents=True, exist_ok=True)
+    out.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     flags_str = " ".join(DEVICE_FLAGS)
     define = f"-DGEO_BUILD_FLAGS=\"{flags_str}\""
 
     def compile_one(src: Path) -> Path:
-        obj = BUILDDIR / (src.stem + ".o")
-        cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), define, "-c", str(src), "-o",
-               str(obj)]
+        obj = builddir / (src.stem + ".o")
+        cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, define, "-c", str(src),
+               "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
         _run(cmd)
@@ -86,10 +92,11 @@ def build(verbose: bool = False) -> Path:
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
         objs = list(pool.map(compile_one, sources))
-    tmp = LIBDIR / (LIBNAME + ".tmp")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
-    os.replace(tmp, lib_path())
-    return lib_path()
+    tmp = out.with_name(out.name + ".tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *extra, *map(str, objs), "-o",
+          str(tmp)])
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

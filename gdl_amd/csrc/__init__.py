@@ -75,10 +75,14 @@ def get_radius_graph_backend() -> str:
 # Largest N * max_num_neighbors whose bound-sized emit scratch (16 bytes per entry) is allocated
 # to overlap the edge-count sync with the emit pass (2^26 entries = 1 GiB); larger graphs wait.
 _RADIUS_ASYNC_MAX_EDGES = 1 << 26
-# Bound-sized scratch up to this size is returned as the outputs themselves (row / col are the
-# first E entries of its two rows), which saves the copy into exact-sized tensors at the cost of
-# holding N * max_num_neighbors entries instead of E (C2: 33.6 MB instead of 10.5 MB).
+# Bound-sized scratch is returned as the outputs themselves (row / col are views of the first E
+# entries of its two rows, sharing one storage) only when the graph fills at least half of it
+# and it is at most this large; otherwise the edges are copied into exact-sized tensors (one
+# kernel, ~4 us for C2's 657k edges) so a kept graph never holds more than twice its size.
 _RADIUS_VIEW_MAX_BYTES = 256 << 20
+# batch tensors (by identity, with their version counter) whose clouds proved not to be the
+# contiguous equal-chunk layout: later calls with the same unchanged tensor skip that attempt
+_BATCH_NOT_CHUNKED: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
 
 
 def radius_graph_hip(
@@ -133,6 +137,7 @@ def radius_graph_csr_hip(
         return empty, empty.clone(), torch.zeros(N + 1, dtype=torch.int64, device=dev), B0
     r2 = fp32_radius_sq(r)
     ppc_try = 0
+    batch_key = batch
     if batch is not None:
         if batch.numel() != N:
             raise ValueError(f"radius_graph: batch has {batch.numel()} entries for {N} points")
@@ -142,6 +147,8 @@ def radius_graph_csr_hip(
         # sorted equal-size clouds (what the reference's GPU path assumes) take the per-cloud
         # front end; the device checks that layout and reports a mismatch with the edge count
         ppc_try = N // B if B >= 1 and N % B == 0 else 0
+        if ppc_try and _BATCH_NOT_CHUNKED.get(batch_key) == batch_key._version:
+            ppc_try = 0
     else:
         B = int(num_batch_elements) if num_batch_elements is not None else 1
         if B < 1:
@@ -186,7 +193,8 @@ def radius_graph_csr_hip(
                 E, bad = edges_h[:2].tolist()
                 if bad == 0:
                     break   # else: batch is not the chunk layout; the general path follows
-            if 16 * N * K <= _RADIUS_VIEW_MAX_BYTES:
+                _BATCH_NOT_CHUNKED[batch_key] = batch_key._version
+            if 16 * N * K <= _RADIUS_VIEW_MAX_BYTES and 2 * E >= N * K:
                 row, col = scratch[0, :E], scratch[1, :E]
             else:
                 row = torch.empty(E, dtype=torch.int64, device=dev)

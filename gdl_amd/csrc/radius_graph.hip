@@ -651,11 +651,19 @@ __global__ __launch_bounds__(kRgThreads) void rg_count(RgWs w, const int64_t* __
                                                        int64_t B, int64_t ppc, float r2, int K,
                                                        int loop, int64_t* __restrict__ bad_out,
                                                        int check_layout) {
-  if (bad_out && blockIdx.x == 0 && threadIdx.x == 0) {  // clouds failing the chunk layout
-    int64_t nb = 0;
+  if (bad_out && blockIdx.x == 0) {  // clouds failing the chunk layout, summed by workgroup 0
+    __shared__ uint32_t s_bad[kRgThreads / kWave];
+    uint32_t nb = 0;
     if (check_layout)
-      for (int64_t b = 0; b < B; ++b) nb += w.layout_bad[b];
-    *bad_out = nb;
+      for (int64_t b = threadIdx.x; b < B; b += kRgThreads) nb += static_cast<uint32_t>(w.layout_bad[b]);
+    nb = wave_sum_dpp(nb);
+    if (lane_id() == 0) s_bad[threadIdx.x / kWave] = nb;
+    __syncthreads();  // workgroup-uniform: the whole of workgroup 0 takes this branch
+    if (threadIdx.x == 0) {
+      uint32_t t = 0;
+      for (int q = 0; q < kRgThreads / kWave; ++q) t += s_bad[q];
+      *bad_out = t;
+    }
   }
   r2 = rg_r2(w, r2);
   // each XCD takes runs of 512 consecutive targets in cell order (neighbouring targets share

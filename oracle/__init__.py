@@ -23,12 +23,15 @@ is exact, scipy / numpy library routines and brute force on tiny inputs.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "lib" / "libgeo_oracle.so"
+# GEO_ORACLE_LIB selects another build of geo_oracle.c (e.g. the sanitizer build of
+# oracle/build.py, which the sanitizer tests load)
+_LIB_PATH = Path(os.environ.get("GEO_ORACLE_LIB", str(_HERE / "lib" / "libgeo_oracle.so")))
 _lib = None
 
 _P = ctypes.c_void_p

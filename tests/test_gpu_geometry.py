@@ -293,7 +293,7 @@ def _rg_check(dev, x, r, K=32, loop=False, mask=None, batch=None, nb=None):
                   batch=None if batch is None else batch.to(dev), num_batch_elements=nb)
     wr, wc = oracle.radius_graph(x.numpy(), r, K, loop,
                                  mask=None if mask is None else mask.numpy(),
-                                 batch=None if batch is None else batch.numpy(),
+                                 batch=None if batch is None else batch.cpu().numpy(),
                                  num_batch_elements=nb)
     assert row.dtype == torch.int64 and col.dtype == torch.int64
     np.testing.assert_array_equal(col.cpu().numpy(), wc)
@@ -385,6 +385,28 @@ def test_radius_batch_layouts(dev, layout):
         batch[1234] = B + 2
     _rg_check(dev, x, 0.3, 12, batch=batch, nb=B)
     _rg_check(dev, x, 0.3, 12, loop=True, batch=batch, nb=B)
+    from gdl_amd.csrc import _BATCH_NOT_CHUNKED, radius_graph_hip
+    bd = batch.to(dev)
+    radius_graph_hip(x.to(dev), 0.3, max_num_neighbors=12, batch=bd, num_batch_elements=B)
+    # a layout the device rejected is remembered for the same unchanged tensor, so the next
+    # call goes straight to the general path (and still gives the oracle's graph)
+    assert (bd in _BATCH_NOT_CHUNKED) == (layout != "chunks")
+    _rg_check(dev, x, 0.3, 12, batch=bd, nb=B)
+
+
+def test_radius_outputs_exact_size(dev):
+    """A sparse graph (E well below N * max_num_neighbors) comes back in exact-sized tensors, not
+    as views of the bound-sized scratch; a dense one may share the scratch."""
+    from gdl_amd.csrc import radius_graph_hip
+    g = torch.Generator().manual_seed(2)
+    x = (torch.rand(3000, 3, generator=g) * 4).to(dev)
+    row, col = radius_graph_hip(x, 0.2, max_num_neighbors=32)
+    assert row.numel() < 3000 * 16
+    for t in (row, col):
+        assert t.untyped_storage().nbytes() == 8 * t.numel()
+    xd = (torch.rand(3000, 3, generator=g) * 0.01).to(dev)   # every target has > K sources
+    row, col = radius_graph_hip(xd, 0.2, max_num_neighbors=8)
+    assert row.numel() == 3000 * 8
 
 
 @pytest.mark.parametrize("ppc", [1, 63, 1000, 4096])

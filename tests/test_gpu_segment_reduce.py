@@ -412,7 +412,8 @@ def test_c3_full_size(dev):
 
 
 @pytest.mark.parametrize("reduce,dtype", [("sum", torch.float32), ("mean", torch.float32),
-                                          ("max", torch.float32), ("sum", torch.bfloat16)])
+                                          ("max", torch.float32), ("sum", torch.bfloat16),
+                                          ("mean", torch.bfloat16), ("max", torch.bfloat16)])
 def test_c3_full_size_every_leg(dev, reduce, dtype):
     """Every C3 leg at full size (E = 4,194,304, S = 262,144, C = 128), forward and backward,
     against float64 library routines on the GPU: sum / mean within TOL * sum|msg| of an fp64
