@@ -794,14 +794,15 @@ def leg_c5(args, dev) -> dict:
 # ═══════════════════════════════════════════════════════════════════
 
 PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "radius_c5_all", "c3sum",
-                "c3max", "c3sum_bf16", "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2")
+                "c3max", "c3sum_bf16", "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2",
+                "csr_c3_sorted", "csr_c3_shuffled", "csr_c2", "sparse_softmax_c2")
 
 
 def profile_leg(name: str, args, dev) -> dict:
     """Runs one op of one configuration ``args.iters`` times after one warm-up call, so that a
     counter run (rocprofv3 --pmc) sees a few dispatches of that kernel and little else."""
     fps, knn, radius_graph, segment_reduce, sort_and_build_csr = _ops()
-    if name.endswith("c2") or name in ("softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2"):
+    if name.endswith("c2"):
         c2 = make_c2()
         pos, ptr, batch = c2["pos"].to(dev), c2["ptr"].to(dev), c2["batch"].to(dev)
     if name == "fps_c2":
@@ -841,6 +842,25 @@ def profile_leg(name: str, args, dev) -> dict:
             mb = msg.bfloat16()
             del msg
             fn = lambda: segment_reduce(mb, cs, perm, ns, ne, S)  # noqa: E731
+    elif name in ("csr_c3_sorted", "csr_c3_shuffled"):
+        off = make_c3_offsets()
+        S = off.shape[0] - 1
+        col = torch.repeat_interleave(torch.arange(S, device=dev),
+                                      torch.from_numpy(np.diff(off)).to(dev))
+        if name == "csr_c3_shuffled":
+            gen = torch.Generator(device=dev).manual_seed(0)
+            col = col[torch.randperm(col.numel(), device=dev, generator=gen)]
+        fn = lambda: sort_and_build_csr(col, S)  # noqa: E731
+    elif name == "csr_c2":  # the radius graph's targets, already in order
+        row, col = radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                num_batch_elements=c2["B"])
+        fn = lambda: sort_and_build_csr(col, pos.shape[0])  # noqa: E731
+    elif name == "sparse_softmax_c2":
+        from gdl_amd.functional.segment_softmax import sparse_softmax
+        row, col = radius_graph(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
+                                num_batch_elements=c2["B"])
+        scores = torch.randn(col.numel(), 4, device=dev)
+        fn = lambda: sparse_softmax(scores, col, pos.shape[0])  # noqa: E731
     elif name in ("softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2"):
         from gdl_amd.graph import SpatialGraph
         gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,

@@ -83,6 +83,10 @@ _RADIUS_VIEW_MAX_BYTES = 256 << 20
 # batch tensors (by identity, with their version counter) whose clouds proved not to be the
 # contiguous equal-chunk layout: later calls with the same unchanged tensor skip that attempt
 _BATCH_NOT_CHUNKED: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
+# radius-graph target tensors (by identity, with their version counter) -> the graph's row
+# pointer.  The graph's edges are already grouped by target in CSR order, so the CSR build of
+# those unchanged targets over the same node count is the row pointer itself: one pass, no sort.
+_TARGETS_ROW_PTR: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
 
 
 def radius_graph_hip(
@@ -95,9 +99,10 @@ def radius_graph_hip(
     batch: Optional[Tensor] = None,
     num_batch_elements: Optional[int] = None,
 ) -> Tuple[Tensor, Tensor]:
-    row, col, _, _ = radius_graph_csr_hip(x, r, max_num_neighbors=max_num_neighbors, loop=loop,
-                                          mask=mask, batch=batch,
-                                          num_batch_elements=num_batch_elements)
+    row, col, row_ptr, _ = radius_graph_csr_hip(x, r, max_num_neighbors=max_num_neighbors,
+                                                loop=loop, mask=mask, batch=batch,
+                                                num_batch_elements=num_batch_elements)
+    _TARGETS_ROW_PTR[col] = (col._version, row_ptr)
     return row, col
 
 
@@ -262,6 +267,7 @@ def sort_and_build_csr_cuda(col: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor
     if N < 0:
         raise ValueError(f"sort_and_build_csr: N must be >= 0, got {N}")
     dev = col.device
+    known = _TARGETS_ROW_PTR.get(col)
     col = _i64(col, dev)
     E = col.shape[0]
     i32 = dict(dtype=torch.int32, device=dev)
@@ -270,6 +276,13 @@ def sort_and_build_csr_cuda(col: Tensor, N: int) -> Tuple[Tensor, Tensor, Tensor
     node_start = torch.empty(N, **i32)
     node_end = torch.empty(N, **i32)
     L = _nat.lib()
+    if known is not None and known[0] == col._version and known[1].numel() == N + 1:
+        with _nat.on_device(dev):  # a radius graph's unchanged targets: its row pointer
+            _nat.check(L.geo_csr_from_row_ptr(_nat.ptr(known[1]), N, _nat.ptr(col), E,
+                                              _nat.ptr(col_sorted), _nat.ptr(perm),
+                                              _nat.ptr(node_start), _nat.ptr(node_end),
+                                              _nat.stream_of(dev)), "geo_csr_from_row_ptr")
+        return col_sorted, perm, node_start, node_end
     with _nat.on_device(dev):
         ws_bytes = L.geo_csr_workspace_bytes(E, N)
         ws = _nat.workspace(ws_bytes, dev)

@@ -3,9 +3,10 @@
 // detection).
 //
 // Stable LSD radix sort (radix.hpp) of the int32 target ids with the edge index as value (small
-// inputs: one workgroup sorting in LDS, csr_small).
+// inputs: one workgroup sorting in LDS, csr_small).  Targets that arrive in order cost the sort's
+// histogram read alone, which then also writes the identity result.
 // Targets outside [0, N) get key N and sort after all valid targets.  node_start/node_end come
-// from binary searches in the sorted keys (node_start[n] = first position with key >= n), so
+// from the transitions of the sorted keys (node_start[n] = first position with key >= n), so
 // empty targets get start == end and no atomics are involved.
 #include <mutex>
 
@@ -14,19 +15,56 @@
 namespace geo {
 namespace {
 
-// Thread n in [0, N] computes lb(n) = first sorted position with key >= n; that is
-// node_start[n] (n < N) and node_end[n - 1] (n > 0).
-__global__ void csr_bounds(const uint32_t* __restrict__ sorted_keys, int64_t E, int64_t N,
-                           int32_t* __restrict__ node_start, int32_t* __restrict__ node_end) {
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (n > N) return;
-  int64_t lo = 0, hi = E;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (sorted_keys[mid] < static_cast<uint32_t>(n)) lo = mid + 1; else hi = mid;
+// Node bounds of sorted keys (after a sort of unsorted input; sorted input gets its bounds from
+// the sort's first histogram): positions 0..E (position E standing for key N) in tiles of
+// kRxTile, each wave's 1024 positions staged in LDS for rx_wave_bounds.  Runs only when *active
+// is set; sets *fallback when a wave's span covers too many nodes.
+__global__ __launch_bounds__(kRxThreads) void csr_bounds_runs(const int32_t* __restrict__ sorted_keys,
+                                                              int64_t E, int64_t N,
+                                                              int32_t* __restrict__ node_start,
+                                                              int32_t* __restrict__ node_end,
+                                                              uint32_t* __restrict__ fallback,
+                                                              const uint32_t* __restrict__ active,
+                                                              int64_t ntiles) {
+  if (*active == 0u) return;
+  __shared__ uint32_t s_keys[kRxWaves][kRxWaveSpan];
+  const int w = threadIdx.x / kWave;
+  const int lane = lane_id();
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t wbase = tile * kRxTile + static_cast<int64_t>(w) * kRxWaveSpan;
+    if (wbase > E) continue;  // wave-uniform
+    const int64_t before = wbase > 0 ? static_cast<int64_t>(sorted_keys[wbase - 1]) : -1;
+#pragma unroll
+    for (int i = 0; i < kRxItems; ++i) {
+      const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
+      if (idx <= E) s_keys[w][i * kWave + lane] = idx < E ? static_cast<uint32_t>(sorted_keys[idx])
+                                                          : static_cast<uint32_t>(N);
+    }
+    wave_lds_fence();
+    const int cnt = static_cast<int>(min(static_cast<int64_t>(kRxWaveSpan), E + 1 - wbase));
+    const bool ok = rx_wave_bounds(s_keys[w], cnt, wbase, before, s_keys[w][cnt - 1], node_start,
+                                   node_end, N);
+    if (!ok && lane == 0) *fallback = 1u;  // plain store: many waves may set it
+    wave_lds_fence();  // the next tile's staging follows this tile's searches
   }
-  if (n < N) node_start[n] = static_cast<int32_t>(lo);
-  if (n > 0) node_end[n - 1] = static_cast<int32_t>(lo);
+}
+
+// Thread n in [0, N] computes lb(n) by binary search over the sorted keys; runs only when
+// *active is set (a wave found gaps too long to write).
+__global__ void csr_bounds(const int32_t* __restrict__ sorted_keys, int64_t E, int64_t N,
+                           int32_t* __restrict__ node_start, int32_t* __restrict__ node_end,
+                           const uint32_t* __restrict__ active) {
+  if (*active == 0u) return;
+  for (int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; n <= N;
+       n += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t lo = 0, hi = E;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (static_cast<int64_t>(sorted_keys[mid]) < n) lo = mid + 1; else hi = mid;
+    }
+    if (n < N) node_start[n] = static_cast<int32_t>(lo);
+    if (n > 0) node_end[n - 1] = static_cast<int32_t>(lo);
+  }
 }
 
 // Small inputs (E <= kCsrSmallMaxE, N <= kCsrSmallMaxN) in one launch: one workgroup holds the
@@ -134,9 +172,9 @@ int radix_key_bits(int64_t N) {
   return bits == 0 ? 1 : bits;
 }
 
-RadixBuffers carve_csr(void* base, int64_t E, size_t* bytes) {
+RadixBuffers carve_csr(void* base, int64_t E, int64_t N, size_t* bytes) {
   Carver c(base);
-  RadixBuffers r = carve_radix(c, E);
+  RadixBuffers r = carve_radix(c, E, radix_key_bits(N));
   *bytes = c.used;
   return r;
 }
@@ -156,14 +194,26 @@ int csr_build_into(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted
     GEO_LAUNCH_CHECK("csr_small");
     return GEO_OK;
   }
-  // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one pass
-  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, radix_key_bits(N),
-                                reinterpret_cast<uint32_t*>(col_sorted),
-                                reinterpret_cast<uint32_t*>(perm), w, st, true);
+  // targets that arrive sorted (a radius graph's output, CSR-ordered messages) cost one read,
+  // which also writes the identity result and the node bounds
+  RxDetect det;
+  if (N > 0) {
+    det.node_start = node_start;
+    det.node_end = node_end;
+    det.nodes = N;
+  }
+  int rc = radix_sort<kRxCol64>(col, nullptr, E, N, reinterpret_cast<uint32_t*>(col_sorted),
+                                reinterpret_cast<uint32_t*>(perm), w, st, &det);
   if (rc) return rc;
   if (N > 0) {
-    hipLaunchKernelGGL(csr_bounds, dim3(ceil_div(N + 1, 256)), dim3(256), 0, st,
-                       reinterpret_cast<const uint32_t*>(col_sorted), E, N, node_start, node_end);
+    const int64_t ptiles = ceil_div(E + 1, kRxTile);
+    hipLaunchKernelGGL(csr_bounds_runs, dim3(ptiles < kRxGrid ? ptiles : kRxGrid),
+                       dim3(kRxThreads), 0, st, col_sorted, E, N, node_start, node_end, w.aux,
+                       w.unsorted, ptiles);
+    GEO_LAUNCH_CHECK("csr_bounds_runs");
+    const int64_t nblocks = ceil_div(N + 1, 256);
+    hipLaunchKernelGGL(csr_bounds, dim3(nblocks < 1024 ? nblocks : 1024), dim3(256), 0, st,
+                       col_sorted, E, N, node_start, node_end, w.aux);
     GEO_LAUNCH_CHECK("csr_bounds");
   }
   return GEO_OK;
@@ -181,14 +231,16 @@ int csr_check_args(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted
 
 // ------------------------------------------------------- build without allocation ---
 // Scratch of geo_csr_build_noalloc: one file-scope device array, so the entry point needs no
-// workspace argument and performs no allocation.  Sized for kNoAllocMaxEdges edges (the radix
-// buffers: four uint32 arrays of E entries, the per-tile digit histograms, the scan's tile sums
-// and the sorted-input flag; 20 MiB + 3 KiB at 2^20 edges).  The runtime gives every device its
-// own copy at its own address; the host never passes `scratch` itself to a kernel (in host code
-// it is a stand-in symbol, not a device address) but the address hipGetSymbolAddress returns
-// for the current device.
+// workspace argument and performs no allocation.  Sized for kNoAllocMaxEdges edges and any N
+// (the radix buffers: intermediate keys and values, the per-tile digit counts and offsets, the
+// look-back words of four 8-bit passes' scans and the flags; 8.5 MiB at 2^20 edges).  The
+// array is part of the library's code object, so every GPU on which the library is loaded holds
+// its own copy, at its own address, from the load until the process ends, whether or not this
+// entry point is called.  The host never passes `scratch` itself to a kernel (in host code it
+// is a stand-in symbol, not a device address) but the address hipGetSymbolAddress returns for
+// the current device.
 constexpr int64_t kNoAllocMaxEdges = int64_t{1} << 20;
-constexpr size_t kNoAllocScratchBytes = (size_t{20} << 20) + (size_t{64} << 10);
+constexpr size_t kNoAllocScratchBytes = size_t{9} << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kNoAllocMaxDevices = 64;
@@ -222,7 +274,7 @@ using namespace geo;
 extern "C" size_t geo_csr_workspace_bytes(int64_t E, int64_t N) {
   if (E < 0 || N < 0) return 0;
   size_t bytes = 0;
-  carve_csr(nullptr, E, &bytes);
+  carve_csr(nullptr, E, N, &bytes);
   return bytes;
 }
 
@@ -232,7 +284,7 @@ extern "C" int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* 
   int rc = csr_check_args(col, E, N, col_sorted, perm, node_start, node_end);
   if (rc) return rc;
   size_t need = 0;
-  const RadixBuffers w = carve_csr(workspace, E, &need);
+  const RadixBuffers w = carve_csr(workspace, E, N, &need);
   if (workspace_bytes < need || workspace == nullptr)
     return set_error(GEO_ERR_WORKSPACE, "csr_build: workspace %zu bytes, need %zu",
                      workspace_bytes, need);
@@ -250,7 +302,7 @@ extern "C" int geo_csr_build_noalloc(const int64_t* col, int64_t E, int64_t N,
                      "(use geo_csr_build with a workspace)",
                      (long long)E, (long long)kNoAllocMaxEdges);
   size_t need = 0;
-  carve_csr(nullptr, E, &need);
+  carve_csr(nullptr, E, N, &need);
   if (need > kNoAllocScratchBytes)  // cannot happen for E <= kNoAllocMaxEdges
     return set_error(GEO_ERR_INVALID, "csr_build_noalloc: needs %zu scratch bytes, has %zu", need,
                      kNoAllocScratchBytes);
@@ -265,6 +317,6 @@ extern "C" int geo_csr_build_noalloc(const int64_t* col, int64_t E, int64_t N,
     GEO_REQUIRE(sdev == cur, "csr_build_noalloc: stream of device %d, current device %d", sdev,
                 cur);
   }
-  const RadixBuffers w = carve_csr(base, E, &need);
+  const RadixBuffers w = carve_csr(base, E, N, &need);
   return csr_build_into(col, E, N, col_sorted, perm, node_start, node_end, w, st);
 }

@@ -852,6 +852,17 @@ struct FpsLargeWs {
   RadixBuffers rx;
 };
 
+// Width of the sort keys (cloud + 1, Hilbert position): the cloud field holds 0 .. B + 1 and each
+// axis of the Hilbert grid gets the same share of the rest, at most 10 bits.
+int fps_large_key_bits(int64_t B, int* axis_bits) {
+  int cbits = 0;
+  while ((static_cast<uint64_t>(B + 1) >> cbits) != 0) ++cbits;
+  int mbits = (32 - cbits) / 3;
+  if (mbits > 10) mbits = 10;
+  if (axis_bits) *axis_bits = mbits;
+  return cbits + 3 * mbits;
+}
+
 FpsLargeWs carve_fps_large(void* base, int64_t B, int64_t N, size_t* bytes) {
   Carver c(base);
   FpsLargeWs w;
@@ -861,7 +872,7 @@ FpsLargeWs carve_fps_large(void* base, int64_t B, int64_t N, size_t* bytes) {
   w.keys = c.take<uint32_t>(N);
   w.skeys = c.take<uint32_t>(N);
   w.order = c.take<uint32_t>(N);
-  w.rx = carve_radix(c, N);
+  w.rx = carve_radix(c, N, fps_large_key_bits(B, nullptr));
   *bytes = c.used;
   return w;
 }
@@ -876,16 +887,13 @@ int launch_large(const float* pos, int64_t N, const int64_t* ptr, const int64_t*
   const FpsLargeWs w = carve_fps_large(workspace, B, N, &bytes);
   hipLaunchKernelGGL(fps_large_bbox_kernel, dim3(B), dim3(kFpsLargeThreads), 0, st, pos, ptr, w.bbox);
   GEO_LAUNCH_CHECK("fps_large_bbox_kernel");
-  int cbits = 0;
-  while ((static_cast<uint64_t>(B + 1) >> cbits) != 0) ++cbits;  // holds cloud field 0 .. B + 1
-  int mbits = (32 - cbits) / 3;
-  if (mbits > 10) mbits = 10;
-  const int bits = cbits + 3 * mbits;
+  int mbits = 0;
+  fps_large_key_bits(B, &mbits);
   const unsigned grid = static_cast<unsigned>(ceil_div(N, 256));
   hipLaunchKernelGGL(fps_large_keys_kernel, dim3(grid), dim3(256), 0, st, pos, ptr, B, N, w.bbox,
                      mbits, w.keys);
   GEO_LAUNCH_CHECK("fps_large_keys_kernel");
-  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, bits, w.skeys, w.order, w.rx, st);
+  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, w.skeys, w.order, w.rx, st);
   if (rc) return rc;
   hipLaunchKernelGGL(fps_large_gather_kernel, dim3(grid), dim3(256), 0, st, pos, w.order, N, w.q, w.md);
   GEO_LAUNCH_CHECK("fps_large_gather_kernel");

@@ -183,7 +183,9 @@ __device__ TOut scan_tile_sum_direct(const TIn* __restrict__ in, int64_t n, int6
 template <typename TIn, typename TOut>
 __global__ __launch_bounds__(kScanThreads) void scan_lookback(
     const TIn* __restrict__ in, int64_t n, TOut* __restrict__ out_excl, TOut* __restrict__ out_incl,
-    int write_total, uint64_t* __restrict__ status, TOut* __restrict__ total_host) {
+    int write_total, uint64_t* __restrict__ status, TOut* __restrict__ total_host,
+    const uint32_t* __restrict__ active) {
+  if (active != nullptr && *active == 0u) return;
   __shared__ TOut lds[kScanThreads / kWave];
   __shared__ int64_t s_tile;
   __shared__ TOut s_prefix;
@@ -274,16 +276,17 @@ __global__ __launch_bounds__(kScanThreads) void scan_lookback(
 
 // Single-pass variant of device_exclusive_scan (n >= 1); status zeroed by the caller.
 // total_host (optional) is a device-side address of mapped pinned host memory that receives the
-// grand total as well.
+// grand total as well.  With `active` (device word), the scan does nothing when it reads 0.
 template <typename TIn, typename TOut>
 int device_exclusive_scan_lookback(const TIn* in, int64_t n, TOut* out_excl, TOut* out_incl,
                                    bool write_total, uint64_t* status, hipStream_t stream,
-                                   TOut* total_host = nullptr) {
+                                   TOut* total_host = nullptr,
+                                   const uint32_t* active = nullptr) {
   if (n <= 0) return device_exclusive_scan<TIn, TOut>(in, n, out_excl, out_incl, write_total,
                                                       nullptr, stream);
   hipLaunchKernelGGL((scan_lookback<TIn, TOut>), dim3(ceil_div(n, kScanTile)), dim3(kScanThreads),
                      0, stream, in, n, out_excl, out_incl, write_total ? 1 : 0, status,
-                     total_host);
+                     total_host, active);
   GEO_LAUNCH_CHECK("scan_lookback");
   return GEO_OK;
 }

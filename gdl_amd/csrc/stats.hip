@@ -88,7 +88,7 @@ StWs carve_st(void* base, int64_t N, size_t* bytes) {
   w.keys = c.take<uint32_t>(n);
   w.skeys = c.take<uint32_t>(n);
   w.order = c.take<uint32_t>(n);
-  w.rx = carve_radix(c, n);
+  w.rx = carve_radix(c, n, 32);
   *bytes = c.used;
   return w;
 }
@@ -134,7 +134,7 @@ extern "C" int geo_knn_radius_stat(const float* dist, int64_t N, int64_t k, int6
   hipLaunchKernelGGL(st_median_keys, dim3(static_cast<unsigned>(ceil_div(N, 256))), dim3(256), 0, st,
                      dist, N, k, col, w.keys);
   GEO_LAUNCH_CHECK("st_median_keys");
-  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, 32, w.skeys, w.order, w.rx, st);
+  int rc = radix_sort<kRxKeysIota>(w.keys, nullptr, N, 0, w.skeys, w.order, w.rx, st);
   if (rc) return rc;
   hipLaunchKernelGGL(st_median_final, dim3(1), dim3(64), 0, st, w.skeys, N, multiplier, out);
   GEO_LAUNCH_CHECK("st_median_final");

@@ -220,7 +220,9 @@ int geo_csr_build(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted,
 /* geo_csr_build without a workspace argument and without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The radix-sort scratch is a fixed
- * 20 MiB device array inside the library, one copy per GPU, held until the process ends; E is
+ * 9 MiB device array inside the library's code object: every GPU on which the library
+ * is loaded holds one copy from the load until the process ends, whether or not this entry
+ * point is ever called; E is
  * limited to 2^20 = 1,048,576 edges (larger E returns GEO_ERR_INVALID: use geo_csr_build).  The
  * scratch of a GPU is shared by every call on it, so calls that overlap on one GPU (other
  * streams, other threads) race and must be serialised by the caller.  `stream` must belong to

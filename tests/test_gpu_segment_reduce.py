@@ -87,6 +87,68 @@ def test_csr_sorted_input_detection(dev, kind, E, N):
         np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
 
 
+@pytest.mark.parametrize("E,N,seed", [(4_194_304, 262_144, 11),      # C3 size, two passes
+                                      (1_000_000, 1_000, 12),        # ~1000 equal keys per target
+                                      (500_000, 40_000_000, 13),     # 26-bit keys, three passes
+                                      (4097, 5_000, 14), (12_289, 2, 15)])  # ragged last tiles
+@pytest.mark.parametrize("order", ["shuffled", "sorted"])
+def test_csr_radix_paths(dev, E, N, seed, order):
+    """The multi-tile radix sort (look-back over 4096-key tiles) and the identity path of sorted
+    input, on sizes that give one, two and three digit passes, partial last tiles and targets
+    sparser than the edges (whose node bounds fall back to a binary search)."""
+    _, csr = _ops()
+    g = torch.Generator().manual_seed(seed)
+    col = torch.randint(0, N, (E,), generator=g)
+    if order == "sorted":
+        col = col.sort().values
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    r = oracle.sort_and_build_csr(col.numpy(), N)
+    for got, want, name in zip((cs, pm, ns, ne), r, ("col_sorted", "perm", "node_start", "node_end")):
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
+
+
+@pytest.mark.parametrize("gaps", [(4, 5), (64, 65), (4096, 4097), (4160, 20_000), (1, 300_000)])
+def test_csr_sorted_gaps(dev, gaps):
+    """Sorted targets with runs of empty nodes between them: gaps of up to four nodes are written
+    by one thread, longer ones by the whole wave, and a wave whose long gaps exceed its budget of
+    64 steps of 64 nodes hands every bound to the binary-search kernel."""
+    _, csr = _ops()
+    g = torch.Generator().manual_seed(sum(gaps))
+    E = 60_000
+    step = torch.randint(0, 2, (E,), generator=g)            # 0 or 1: repeats and unit steps
+    big = torch.randint(0, E, (40,), generator=g)
+    step[big] = torch.tensor(gaps)[torch.arange(40) % 2]     # a few long runs of empty nodes
+    col = torch.cumsum(step, 0)
+    N = int(col[-1]) + gaps[1]                               # empty nodes after the last target too
+    cs, pm, ns, ne = csr(col.to(dev), N)
+    r = oracle.sort_and_build_csr(col.numpy(), N)
+    for got, want, name in zip((cs, pm, ns, ne), r, ("col_sorted", "perm", "node_start", "node_end")):
+        np.testing.assert_array_equal(got.cpu().numpy(), want, err_msg=name)
+
+
+def test_csr_of_radius_graph_targets(dev):
+    """The targets of a radius graph are already in CSR order: their CSR build comes from the
+    graph's row pointer.  It must equal the oracle's stable CSR; a different node count, or the
+    targets changed in place, take the sort instead and still match the oracle."""
+    import geoembodied  # noqa: F401
+    from geoembodied.functional.radius_graph import radius_graph
+    _, csr = _ops()
+    g = torch.Generator().manual_seed(21)
+    pos = torch.rand(3000, 3, generator=g)
+    row, col = radius_graph(pos.to(dev), 0.12, max_num_neighbors=16)
+    N = pos.shape[0]
+    for n_nodes in (N, N + 5):
+        got = csr(col, n_nodes)
+        want = oracle.sort_and_build_csr(col.cpu().numpy(), n_nodes)
+        for g_, w_, name in zip(got, want, ("col_sorted", "perm", "node_start", "node_end")):
+            np.testing.assert_array_equal(g_.cpu().numpy(), w_, err_msg=f"{name} N={n_nodes}")
+    col[0] = N - 1          # in place: no longer the graph's targets, nor sorted
+    got = csr(col, N)
+    want = oracle.sort_and_build_csr(col.cpu().numpy(), N)
+    for g_, w_, name in zip(got, want, ("col_sorted", "perm", "node_start", "node_end")):
+        np.testing.assert_array_equal(g_.cpu().numpy(), w_, err_msg=f"{name} after in-place change")
+
+
 def test_csr_empty(dev):
     _, csr = _ops()
     cs, pm, ns, ne = csr(torch.empty(0, dtype=torch.long, device=dev), 7)
