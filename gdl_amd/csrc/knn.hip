@@ -43,12 +43,19 @@ __global__ __launch_bounds__(kScanThreads) void knn_prepare_kernel(const int64_t
   if (threadIdx.x == 0) tiles[B] = carry;
 }
 
-template <int KMAX>
+// k above the largest list (kKnnMaxList) is served in passes of at most kKnnMaxList columns:
+// pass p writes columns [col0, col0 + width) of each row (LB = true for p > 0) and admits only
+// sources whose key (d, j) is above the key in column col0 - 1, which the previous pass wrote,
+// so the passes together list the k smallest keys in order.  A row whose column col0 - 1 is
+// padding has no further neighbours: the pass leaves its padding.
+constexpr int kKnnMaxList = 128;
+
+template <int KMAX, bool LB = false>
 __global__ __launch_bounds__(kKnnThreads) void knn_kernel(
     const float* __restrict__ query, int64_t Nq, const float* __restrict__ source, int64_t Ns,
     const int64_t* __restrict__ ptr_q, const int64_t* __restrict__ ptr_s,
     const int64_t* __restrict__ tiles, int64_t B, int k, int64_t* __restrict__ out_idx,
-    float* __restrict__ out_dist) {
+    float* __restrict__ out_dist, int col0, int width) {
   __shared__ float4 tile[kKnnTile];
   const int64_t blk = blockIdx.x;
   if (blk >= tiles[B]) return;
@@ -66,7 +73,16 @@ __global__ __launch_bounds__(kKnnThreads) void knn_kernel(
   sa = sa < 0 ? 0 : (sa > Ns ? Ns : sa);
   sc = sc < sa ? sa : (sc > Ns ? Ns : sc);
   const int64_t q = qa + (blk - tiles[b]) * kKnnThreads + threadIdx.x;
-  const bool qok = q < qc;
+  bool qok = q < qc;
+  float lbd = -__builtin_inff();  // key of column col0 - 1 (passes after the first)
+  int64_t lbj = -1;
+  if constexpr (LB) {
+    if (qok) {
+      lbj = out_idx[q * k + col0 - 1];
+      lbd = out_dist[q * k + col0 - 1];
+      qok = lbj >= 0;  // padding there: nothing further to list
+    }
+  }
 
   float qx = 0.f, qy = 0.f, qz = 0.f;
   if (qok) {
@@ -92,7 +108,9 @@ __global__ __launch_bounds__(kKnnThreads) void knn_kernel(
     for (int i = 0; i < n; ++i) {
       const float4 p = tile[i];
       const float d = sqdist(qx, qy, qz, p.x, p.y, p.z);
-      if (d < D[KMAX - 1]) {
+      bool above = true;
+      if constexpr (LB) above = d > lbd || (d == lbd && s0 + i > lbj);
+      if (above && d < D[KMAX - 1]) {
         const int j = static_cast<int>(s0 + i);
 #pragma unroll
         for (int m = KMAX - 1; m > 0; --m) {
@@ -109,11 +127,11 @@ __global__ __launch_bounds__(kKnnThreads) void knn_kernel(
     }
   }
   if (qok) {
-    int64_t* oi = out_idx + q * k;
-    float* od = out_dist + q * k;
+    int64_t* oi = out_idx + q * k + col0;
+    float* od = out_dist + q * k + col0;
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
-      if (i < k) {
+      if (i < width) {
         oi[i] = J[i] >= 0 ? static_cast<int64_t>(J[i]) : -1;
         od[i] = J[i] >= 0 ? D[i] : 1e30f;
       }
@@ -124,10 +142,15 @@ __global__ __launch_bounds__(kKnnThreads) void knn_kernel(
 template <int KMAX>
 int launch_knn(const float* query, int64_t Nq, const float* source, int64_t Ns,
                const int64_t* ptr_q, const int64_t* ptr_s, const int64_t* tiles, int64_t B, int k,
-               int64_t* out_idx, float* out_dist, hipStream_t st) {
+               int64_t* out_idx, float* out_dist, hipStream_t st, int col0 = 0, int width = -1) {
   const int64_t grid = ceil_div(Nq, kKnnThreads) + B;
-  hipLaunchKernelGGL((knn_kernel<KMAX>), dim3(grid), dim3(kKnnThreads), 0, st, query, Nq, source,
-                     Ns, ptr_q, ptr_s, tiles, B, k, out_idx, out_dist);
+  if (width < 0) width = k;
+  if (col0 == 0)
+    hipLaunchKernelGGL((knn_kernel<KMAX, false>), dim3(grid), dim3(kKnnThreads), 0, st, query, Nq,
+                       source, Ns, ptr_q, ptr_s, tiles, B, k, out_idx, out_dist, col0, width);
+  else
+    hipLaunchKernelGGL((knn_kernel<KMAX, true>), dim3(grid), dim3(kKnnThreads), 0, st, query, Nq,
+                       source, Ns, ptr_q, ptr_s, tiles, B, k, out_idx, out_dist, col0, width);
   GEO_LAUNCH_CHECK("knn_kernel");
   return GEO_OK;
 }
@@ -608,7 +631,7 @@ extern "C" int geo_knn(const float* query, int64_t Nq, const float* source, int6
                        void* stream) {
   GEO_REQUIRE(Nq >= 0 && Ns >= 0 && B >= 0, "knn: negative size");
   GEO_REQUIRE(k >= 0, "knn: k must be non-negative (got %lld)", (long long)k);
-  GEO_REQUIRE(k <= 128, "knn: k=%lld above the supported maximum of 128", (long long)k);
+  GEO_REQUIRE(k < 0x7fffffffLL, "knn: k=%lld exceeds int32", (long long)k);
   GEO_REQUIRE(Nq < 0x7fffffffLL && Ns < 0x7fffffffLL, "knn: sizes exceed int32 indexing");
   if (Nq == 0 || k == 0) return GEO_OK;
   GEO_REQUIRE(query && out_idx && out_dist && ptr_q && ptr_s, "knn: null pointer");
@@ -637,6 +660,21 @@ extern "C" int geo_knn(const float* query, int64_t Nq, const float* source, int6
   if (rc) return rc;
   hipLaunchKernelGGL(knn_prepare_kernel, dim3(1), dim3(kScanThreads), 0, st, ptr_q, B, Nq, tiles);
   GEO_LAUNCH_CHECK("knn_prepare_kernel");
+  if (kk > kKnnMaxList) {  // passes of kKnnMaxList columns, the last one narrower
+    for (int col0 = 0; col0 < kk; col0 += kKnnMaxList) {
+      const int width = kk - col0 < kKnnMaxList ? kk - col0 : kKnnMaxList;
+      rc = width <= 32 ? launch_knn<32>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx,
+                                        out_dist, st, col0, width)
+         : width <= 64 ? launch_knn<64>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx,
+                                        out_dist, st, col0, width)
+         : width <= 96 ? launch_knn<96>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx,
+                                        out_dist, st, col0, width)
+                       : launch_knn<128>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx,
+                                         out_dist, st, col0, width);
+      if (rc) return rc;
+    }
+    return GEO_OK;
+  }
 #define GEO_KNN_CASE(KV) \
   if (kk <= KV) return launch_knn<KV>(query, Nq, source, Ns, ptr_q, ptr_s, tiles, B, kk, out_idx, out_dist, st);
   GEO_KNN_CASE(1) GEO_KNN_CASE(2) GEO_KNN_CASE(3) GEO_KNN_CASE(4) GEO_KNN_CASE(5)

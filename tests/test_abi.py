@@ -60,7 +60,7 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     _err(L.geo_segment_reduce_fwd(2, 0, 8, nul, 8, 8, 1, 1, 4, 8, nul, 0, nul), "arg")
     _err(L.geo_segment_reduce_bwd(2, 0, 8, nul, nul, nul, 8, nul, nul, nul, 1, 1, 1, 8, nul), "max needs")
     _err(L.geo_knn(nul, 1, nul, 1, nul, nul, 1, -1, nul, nul, nul, 0, nul), "k must")
-    _err(L.geo_knn(nul, 1, nul, 1, nul, nul, 1, 1000, nul, nul, nul, 0, nul), "maximum")
+    _err(L.geo_knn(nul, 1, nul, 1, nul, nul, 1, 1000, nul, nul, nul, 0, nul), "null")
     _err(L.geo_radius_count(nul, 10, nul, 0, 10, nul, 0.01, 0.1, 32, 0, nul, nul, 0, nul), "B >= 1")
     _err(L.geo_radius_count(nul, 10, nul, 3, 3, nul, 0.01, 0.1, 32, 0, nul, nul, 0, nul), "points_per_cloud")
     _err(L.geo_radius_count(nul, 10, nul, 1, 10, nul, 0.01, 0.1, 0, 0, nul, nul, 0, nul), "max_num_neighbors")

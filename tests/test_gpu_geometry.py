@@ -280,8 +280,23 @@ def test_knn_bad_args(dev):
     x = torch.randn(5, 3, device=dev)
     with pytest.raises(ValueError):
         knn(x, x, torch.tensor([0, 5], device=dev), torch.tensor([0, 2, 5], device=dev), 2)
-    with pytest.raises(RuntimeError):
-        knn(x, x, torch.tensor([0, 5], device=dev), torch.tensor([0, 5], device=dev), 129)
+    with pytest.raises(ValueError):
+        knn(x, x, torch.tensor([0, 5], device=dev), torch.tensor([0, 5], device=dev), -1)
+
+
+@pytest.mark.parametrize("k", [129, 200, 256, 300, 513])
+def test_knn_large_k_vs_oracle(dev, k):
+    """k above 128 is listed in passes of 128 columns, each admitting only keys (d, j) above the
+    previous pass's last: clouds larger and smaller than k (padding), an empty cloud, and a
+    lattice with ties everywhere; the reference path accepts any k (csrc/__init__.py:484-486)."""
+    g = torch.Generator().manual_seed(k)
+    qs, ss = [40, 0, 90, 7, 33], [600, 10, 2500, 0, 150]
+    q = torch.randn(sum(qs), 3, generator=g)
+    s = torch.randn(sum(ss), 3, generator=g)
+    _knn_check(dev, q, s, _ptr(qs), _ptr(ss), k)
+    lat = _lattice(9)                        # 729 integer points: equal distances in runs
+    ql = _lattice(3, 4) + 0.5 * (torch.arange(27).reshape(-1, 1) % 2)
+    _knn_check(dev, ql, lat, _ptr([27]), _ptr([729]), k)
 
 
 # -------------------------------------------------------------------------- radius graph ---
