@@ -95,7 +95,7 @@ _SIGNATURES = {
                                  c_i32, c_vp, c_i32, c_vp, c_vp, c_vp, c_vp]),
     "geo_radial_mlp_fwd": (c_int, [c_vp, c_i64, c_vp, c_i32, c_f32, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
                                    c_vp, c_vp]),
-    "geo_radial_mlp_bwd_workspace_bytes": (c_size, [c_i64]),
+    "geo_radial_mlp_bwd_workspace_bytes": (c_size, [c_i64, c_i32, c_i32, c_i32]),
     "geo_radial_mlp_bwd": (c_int, [c_vp, c_i64, c_vp, c_i32, c_f32, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32,
                                    c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_se3_bwd_src": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64,

@@ -5,7 +5,8 @@
 //   x_i = sin(f_i d) / max(d, 1e-8) * env(d),  env(d) = max(0.5 (1 + cos((pi d) / cutoff)), 0)
 //   z_j = b1_j + sum_i W1[j][i] x_i,  h_j = silu(z_j) = z_j / (1 + exp(-z_j))
 //   R_p = b2_p + sum_j W2[p][j] h_j
-// with i < NB <= 16 basis functions, j < H <= 64 hidden units and p < P <= 16 outputs.  PyTorch
+// with i < NB basis functions, j < H hidden units and p < P outputs (the matrix-core kernels below
+// take NB <= 16, H <= 64, P <= 16; larger layers take the general kernels further down).  PyTorch
 // runs this as a dozen kernels with [E, 64] intermediates, and its weight gradients as GEMMs
 // whose reduction dimension is E.  Here one wave takes 16 edges at a time through fp32 MFMA
 // (v_mfma_f32_16x16x4_f32) tiles, nothing per edge but d, R and dR touches memory, and the weight
@@ -348,11 +349,186 @@ __global__ __launch_bounds__(kRbThreads) void radial_bwd_final(const float* __re
   }
 }
 
+// --------------------------------------------------------------- any layer sizes ---
+// Layers beyond the MFMA kernels' 16 basis functions, 64 hidden units or 16 outputs.  A
+// workgroup takes TE edges at a time (TE from the layer sizes, so the tile's values fit 48 KB of
+// LDS): the basis values x[i][e], the hidden pre-activations z[j][e] and, in the backward, their
+// gradients are staged in LDS with the edge index fastest (consecutive threads, consecutive
+// edges: no bank conflicts), and every sum runs over its index in ascending order.  The weight
+// rows are read from global memory (the same row by all threads of a step: cached).  The
+// backward keeps per-workgroup weight-gradient partials in the workspace (each element owned by
+// one thread) and sums them over the workgroups in order, as the MFMA path does, so the results
+// are deterministic.
+constexpr int kRgLdsFloats = 12288;  // 48 KB
+constexpr int kRgMaxBlocks = 512;
+
+__host__ __device__ inline int rg_tile_fwd(int NB, int H) {
+  const int t = kRgLdsFloats / (NB + H);
+  return t < 1 ? 1 : (t > 64 ? 64 : t);
+}
+__host__ __device__ inline int rg_tile_bwd(int NB, int H, int P) {
+  const int t = kRgLdsFloats / (2 * NB + 2 * H + P);
+  return t < 1 ? 1 : (t > 64 ? 64 : t);
+}
+__host__ __device__ inline int64_t rg_part_elems(int NB, int H, int P) {
+  return static_cast<int64_t>(H) * NB + static_cast<int64_t>(P) * H + H + P;
+}
+
+// x[i][e] (and dx/dd) of the tile's edges; env/rdc per edge first.
+__device__ __forceinline__ void rg_basis_tile(const RbParams& p, int64_t e0, int te, float pic,
+                                              float* x, float* dxdd) {
+  for (int q = threadIdx.x; q < te * p.NB; q += kRbThreads) {
+    const int i = q / te, e = q % te;
+    const int64_t ge = e0 + e;
+    const float d = ge < p.E ? p.dist[ge] : 1.f;
+    float env, denv;
+    envelope(d, pic, env, denv);
+    float dx = 0.f;
+    x[i * te + e] = basis(p.freqs[i], d, rb_rdc(d), env, denv, dxdd ? &dx : nullptr);
+    if (dxdd) dxdd[i * te + e] = dx;
+  }
+}
+
+__global__ __launch_bounds__(kRbThreads) void radial_fwd_general(RbParams p, float* __restrict__ R) {
+  extern __shared__ float smem[];
+  const int te = rg_tile_fwd(p.NB, p.H);
+  float* x = smem;                // [NB][te]
+  float* h = smem + p.NB * te;    // [H][te]
+  const float pic = 3.14159265358979323846f / p.cutoff;
+  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * te; e0 < p.E;
+       e0 += static_cast<int64_t>(gridDim.x) * te) {
+    rg_basis_tile(p, e0, te, pic, x, nullptr);
+    __syncthreads();
+    for (int q = threadIdx.x; q < te * p.H; q += kRbThreads) {
+      const int j = q / te, e = q % te;
+      const float* w = p.W1 + static_cast<int64_t>(j) * p.NB;
+      float z = 0.f;
+      for (int i = 0; i < p.NB; ++i) z += w[i] * x[i * te + e];
+      h[j * te + e] = silu(z + p.b1[j]);
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < te * p.P; q += kRbThreads) {
+      const int e = q / p.P, pp = q % p.P;  // output-major: consecutive threads, consecutive R
+      const int64_t ge = e0 + e;
+      const float* w = p.W2 + static_cast<int64_t>(pp) * p.H;
+      float r = 0.f;
+      for (int j = 0; j < p.H; ++j) r += w[j] * h[j * te + e];
+      if (ge < p.E) R[ge * p.P + pp] = r + p.b2[pp];
+    }
+    __syncthreads();
+  }
+}
+
+// Backward of one tile per step; part (rg_part_elems floats per workgroup) accumulates
+// dW1 [H][NB] | dW2 [P][H] | db1 [H] | db2 [P] over the workgroup's tiles.
+__global__ __launch_bounds__(kRbThreads) void radial_bwd_general(RbParams p, const float* __restrict__ dR,
+                                                                 float* __restrict__ ddist,
+                                                                 float* __restrict__ part) {
+  extern __shared__ float smem[];
+  const int NB = p.NB, H = p.H, P = p.P;
+  const int te = rg_tile_bwd(NB, H, P);
+  float* x = smem;             // [NB][te]
+  float* dxdd = x + NB * te;   // [NB][te]
+  float* h = dxdd + NB * te;   // [H][te]
+  float* dz = h + H * te;      // [H][te]: z, then its gradient
+  float* dr = dz + H * te;     // [P][te]
+  const float pic = 3.14159265358979323846f / p.cutoff;
+  const int64_t np = rg_part_elems(NB, H, P);
+  float* mine = part + static_cast<int64_t>(blockIdx.x) * np;
+  for (int64_t q = threadIdx.x; q < np; q += kRbThreads) mine[q] = 0.f;
+  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * te; e0 < p.E;
+       e0 += static_cast<int64_t>(gridDim.x) * te) {
+    rg_basis_tile(p, e0, te, pic, x, dxdd);
+    for (int q = threadIdx.x; q < te * P; q += kRbThreads) {
+      const int e = q / P, pp = q % P;
+      const int64_t ge = e0 + e;
+      dr[pp * te + e] = ge < p.E ? dR[ge * P + pp] : 0.f;  // edges past E add nothing
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < te * H; q += kRbThreads) {
+      const int j = q / te, e = q % te;
+      const float* w = p.W1 + static_cast<int64_t>(j) * NB;
+      float z = 0.f;
+      for (int i = 0; i < NB; ++i) z += w[i] * x[i * te + e];
+      z += p.b1[j];
+      const float sg = sigmoid(z);
+      h[j * te + e] = z * sg;
+      float g = 0.f;  // dH = dR W2
+      for (int pp = 0; pp < P; ++pp) g += dr[pp * te + e] * p.W2[static_cast<int64_t>(pp) * H + j];
+      dz[j * te + e] = g * (sg * (1.f + z * (1.f - sg)));  // silu'(z)
+    }
+    __syncthreads();
+    // d dist: dX = dZ W1, then sum_i dX_i dx_i/dd
+    if (ddist)
+      for (int e = threadIdx.x; e < te; e += kRbThreads) {
+        const int64_t ge = e0 + e;
+        float dd = 0.f;
+        for (int i = 0; i < NB; ++i) {
+          float gx = 0.f;
+          for (int j = 0; j < H; ++j) gx += dz[j * te + e] * p.W1[static_cast<int64_t>(j) * NB + i];
+          dd += gx * dxdd[i * te + e];
+        }
+        if (ge < p.E) ddist[ge] = dd;
+      }
+    // weight gradients of the tile, added to this workgroup's partials
+    for (int64_t q = threadIdx.x; q < np; q += kRbThreads) {
+      float s = 0.f;
+      if (q < static_cast<int64_t>(H) * NB) {
+        const int j = static_cast<int>(q / NB), i = static_cast<int>(q % NB);
+        for (int e = 0; e < te; ++e) s += dz[j * te + e] * x[i * te + e];
+      } else if (q < static_cast<int64_t>(H) * NB + static_cast<int64_t>(P) * H) {
+        const int64_t r = q - static_cast<int64_t>(H) * NB;
+        const int pp = static_cast<int>(r / H), j = static_cast<int>(r % H);
+        for (int e = 0; e < te; ++e) s += dr[pp * te + e] * h[j * te + e];
+      } else if (q < static_cast<int64_t>(H) * NB + static_cast<int64_t>(P) * H + H) {
+        const int j = static_cast<int>(q - static_cast<int64_t>(H) * NB - static_cast<int64_t>(P) * H);
+        for (int e = 0; e < te; ++e) s += dz[j * te + e];
+      } else {
+        const int pp = static_cast<int>(q - static_cast<int64_t>(H) * NB - static_cast<int64_t>(P) * H - H);
+        for (int e = 0; e < te; ++e) s += dr[pp * te + e];
+      }
+      mine[q] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// Sums the workgroups' partials in workgroup order into the requested gradients.
+__global__ __launch_bounds__(kRbThreads) void radial_bwd_general_final(
+    const float* __restrict__ part, int nblk, int NB, int H, int P, float* __restrict__ dW1,
+    float* __restrict__ db1, float* __restrict__ dW2, float* __restrict__ db2) {
+  const int64_t np = rg_part_elems(NB, H, P);
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kRbThreads + threadIdx.x;
+  if (q >= np) return;
+  float s = 0.f;
+  for (int b = 0; b < nblk; ++b) s += part[static_cast<int64_t>(b) * np + q];
+  const int64_t a = static_cast<int64_t>(H) * NB, b2 = a + static_cast<int64_t>(P) * H;
+  if (q < a) {
+    if (dW1) dW1[q] = s;  // [H][NB], the same layout
+  } else if (q < b2) {
+    if (dW2) dW2[q - a] = s;  // [P][H]
+  } else if (q < b2 + H) {
+    if (db1) db1[q - b2] = s;
+  } else if (db2) {
+    db2[q - b2 - H] = s;
+  }
+}
+
+bool rb_fits_mfma(int NB, int H, int P) {
+  return NB <= kRbMaxBasis && H <= kRbMaxHidden && P <= kRbMaxOut;
+}
+
+unsigned rg_blocks(int64_t E, int te) {
+  const int64_t b = ceil_div(E, te);
+  return static_cast<unsigned>(b < 1 ? 1 : (b > kRgMaxBlocks ? kRgMaxBlocks : b));
+}
+
 int rb_check(const char* who, int64_t E, int NB, int H, int P, float cutoff) {
   GEO_REQUIRE(E >= 0, "%s: negative E", who);
-  GEO_REQUIRE(NB >= 1 && NB <= kRbMaxBasis, "%s: num_basis=%d outside [1, %d]", who, NB, kRbMaxBasis);
-  GEO_REQUIRE(H >= 1 && H <= kRbMaxHidden, "%s: hidden=%d outside [1, %d]", who, H, kRbMaxHidden);
-  GEO_REQUIRE(P >= 1 && P <= kRbMaxOut, "%s: outputs=%d outside [1, %d]", who, P, kRbMaxOut);
+  GEO_REQUIRE(NB >= 1 && H >= 1 && P >= 1, "%s: layer sizes must be positive (num_basis=%d, "
+              "hidden=%d, outputs=%d)", who, NB, H, P);
+  GEO_REQUIRE(static_cast<int64_t>(NB) + H <= kRgLdsFloats && 2LL * NB + 2LL * H + P <= kRgLdsFloats,
+              "%s: layer sizes too large (num_basis=%d, hidden=%d, outputs=%d)", who, NB, H, P);
   GEO_REQUIRE(cutoff > 0.f, "%s: cutoff must be positive", who);
   return GEO_OK;
 }
@@ -376,13 +552,23 @@ extern "C" int geo_radial_mlp_fwd(const float* dist, int64_t E, const float* fre
   if (E == 0) return GEO_OK;
   GEO_REQUIRE(dist && freqs && W1 && b1 && W2 && b2 && R, "radial_mlp_fwd: null pointer");
   RbParams p{dist, E, freqs, NB, cutoff, W1, b1, H, W2, b2, P};
+  if (!rb_fits_mfma(NB, H, P)) {
+    const int te = rg_tile_fwd(NB, H);
+    hipLaunchKernelGGL(radial_fwd_general, dim3(rg_blocks(E, te)), dim3(kRbThreads),
+                       static_cast<size_t>(te) * (NB + H) * sizeof(float), as_stream(stream), p, R);
+    GEO_LAUNCH_CHECK("radial_fwd_general");
+    return GEO_OK;
+  }
   hipLaunchKernelGGL(radial_fwd_kernel, dim3(rb_blocks(E)), dim3(kRbThreads), 0, as_stream(stream), p, R);
   GEO_LAUNCH_CHECK("radial_fwd_kernel");
   return GEO_OK;
 }
 
-extern "C" size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E) {
-  if (E < 0) return 0;
+extern "C" size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E, int32_t NB, int32_t H, int32_t P) {
+  if (E < 0 || NB < 1 || H < 1 || P < 1) return 0;
+  if (!rb_fits_mfma(NB, H, P))
+    return static_cast<size_t>(rg_blocks(E, rg_tile_bwd(NB, H, P))) * rg_part_elems(NB, H, P) *
+           sizeof(float);
   return static_cast<size_t>(rb_blocks(E)) * kRbPart * sizeof(float);
 }
 
@@ -403,11 +589,26 @@ extern "C" int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* fre
     return GEO_OK;
   }
   GEO_REQUIRE(dist && dR, "radial_mlp_bwd: null pointer");
-  const size_t need = geo_radial_mlp_bwd_workspace_bytes(E);
+  const size_t need = geo_radial_mlp_bwd_workspace_bytes(E, NB, H, P);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(GEO_ERR_WORKSPACE, "radial_mlp_bwd: workspace %zu bytes, need %zu",
                      workspace_bytes, need);
   RbParams p{dist, E, freqs, NB, cutoff, W1, b1, H, W2, b2, P};
+  if (!rb_fits_mfma(NB, H, P)) {
+    const int te = rg_tile_bwd(NB, H, P);
+    const unsigned nb = rg_blocks(E, te);
+    float* part = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(radial_bwd_general, dim3(nb), dim3(kRbThreads),
+                       static_cast<size_t>(te) * (2 * NB + 2 * H + P) * sizeof(float), st, p, dR,
+                       d_dist, part);
+    GEO_LAUNCH_CHECK("radial_bwd_general");
+    hipLaunchKernelGGL(radial_bwd_general_final,
+                       dim3(static_cast<unsigned>(ceil_div(rg_part_elems(NB, H, P), kRbThreads))),
+                       dim3(kRbThreads), 0, st, part, static_cast<int>(nb), NB, H, P, dW1, db1, dW2,
+                       db2);
+    GEO_LAUNCH_CHECK("radial_bwd_general_final");
+    return GEO_OK;
+  }
   // three waves per SIMD fit the backward: one resident round of 768 blocks on 256 CUs
   const unsigned nblk = rb_blocks(E) < 768u ? rb_blocks(E) : 768u;
   float* part = static_cast<float*>(workspace);

@@ -495,7 +495,7 @@ def _radial_bwd_op(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: T
     g = dR.to(torch.float32).contiguous()
     L = _nat.lib()
     with _nat.on_device(dev):
-        nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E)
+        nbytes = L.geo_radial_mlp_bwd_workspace_bytes(E, NB, H, P)
         ws = _nat.workspace(nbytes, dev)
         _nat.check(L.geo_radial_mlp_bwd(
             _nat.ptr(dist), E, _nat.ptr(freqs), NB, float(cutoff), _nat.ptr(W1), _nat.ptr(b1), H,
@@ -533,8 +533,9 @@ _radial_op.register_autograd(_radial_backward, setup_context=_radial_setup)
 
 def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
                b2: Tensor) -> Tensor:
-    """Radial weights [E, P] of edge lengths ``dist`` [E] (fp32, on the GPU; num_basis <= 16,
-    hidden <= 64, outputs <= 16), differentiable with respect to dist and the four weights."""
+    """Radial weights [E, P] of edge lengths ``dist`` [E] (fp32, on the GPU; any layer sizes:
+    matrix-core kernels up to 16 basis functions, 64 hidden units and 16 outputs, LDS-tiled
+    kernels beyond), differentiable with respect to dist and the four weights."""
     _require_gpu("radial_mlp", dist)
     f = torch.float32
     c = [x.to(f).contiguous() for x in (dist, freqs, W1, b1, W2, b2)]

@@ -482,14 +482,15 @@ int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const float* gv, i
  * Radial basis MLP of SE3Conv (geoembodied/nn/modules/se3_conv.py:238-282), per edge length d:
  *   x_i = sin(freqs[i] d) / max(d, 1e-8) * max(0.5 (1 + cos((pi d) / cutoff)), 0)   (i < NB)
  *   R[e][p] = b2[p] + sum_j W2[p][j] silu(b1[j] + sum_i W1[j][i] x_i)          (j < H, p < P)
- * fp32, NB <= 16, H <= 64, P <= 16; W1 [H][NB], W2 [P][H] row-major.  The backward writes
- * d loss / d dist (d_dist, may be NULL) and the weight gradients (each may be NULL; written,
- * not accumulated) from dR [E, P]; its workspace holds per-block partial sums.
+ * fp32, any layer sizes with NB + H <= 12288 and 2 NB + 2 H + P <= 12288 (matrix-core kernels
+ * for NB <= 16, H <= 64, P <= 16, LDS-tiled kernels beyond); W1 [H][NB], W2 [P][H] row-major.
+ * The backward writes d loss / d dist (d_dist, may be NULL) and the weight gradients (each may
+ * be NULL; written, not accumulated) from dR [E, P]; its workspace holds per-block partial sums.
  */
 int geo_radial_mlp_fwd(const float* dist, int64_t E, const float* freqs, int32_t NB, float cutoff,
                        const float* W1, const float* b1, int32_t H, const float* W2, const float* b2,
                        int32_t P, float* R, void* stream);
-size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E);
+size_t geo_radial_mlp_bwd_workspace_bytes(int64_t E, int32_t NB, int32_t H, int32_t P);
 int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* freqs, int32_t NB, float cutoff,
                        const float* W1, const float* b1, int32_t H, const float* W2, const float* b2,
                        int32_t P, const float* dR, float* d_dist, float* dW1, float* db1, float* dW2,

@@ -23,7 +23,10 @@ def _close(got, want, rtol, arel):
 
 
 @pytest.mark.parametrize("E,NB,H,P", [(1000, 16, 64, 5), (70001, 16, 64, 9), (333, 8, 32, 1),
-                                      (16, 16, 64, 16), (5, 3, 7, 2)])
+                                      (16, 16, 64, 16), (5, 3, 7, 2),
+                                      # beyond the matrix-core kernels: the LDS-tiled kernels
+                                      (3000, 32, 64, 5), (2001, 16, 128, 9), (777, 16, 64, 20),
+                                      (40000, 48, 200, 33), (3, 17, 65, 17)])
 def test_radial_mlp_vs_oracle(dev, E, NB, H, P):
     from gdl_amd.se3_conv import radial_mlp
     g = torch.Generator().manual_seed(E + P)
@@ -60,3 +63,24 @@ def test_radial_basis_module_matches_reference_formula(dev):
                              l2.weight.cpu(), l2.bias.cpu())
     _close(R, want, 1e-5, 1e-5)
     assert rb(torch.empty(0, device=dev)).shape == (0, 5)
+
+
+def test_se3conv_with_32_radial_basis_functions(dev):
+    """SE3Conv(num_radial_basis=32) -- the radial MLP beyond 16 basis functions -- runs forward and
+    backward, and its radial weights match the float64 oracle."""
+    from gdl_amd.graph import SpatialGraph
+    from gdl_amd.se3_conv import SE3Conv
+    torch.manual_seed(3)
+    pos = torch.rand(2000, 3, device=dev)
+    gr = SpatialGraph.build(pos, 0.12, max_num_neighbors=16)
+    conv = SE3Conv(8, 4, 8, 4, radius=0.12, num_radial_basis=32).to(dev)
+    fs = torch.randn(gr.N, 8, device=dev, requires_grad=True)
+    fv = torch.randn(gr.N, 4, 3, device=dev, requires_grad=True)
+    s, v = conv(fs, fv, gr)
+    (s.square().sum() + v.square().sum()).backward()
+    assert torch.isfinite(fs.grad).all() and torch.isfinite(fv.grad).all()
+    rb = conv.radial_basis
+    l1, l2 = rb.mlp[0], rb.mlp[2]
+    want = ose3.radial_basis(gr.dist.detach().cpu(), rb.freqs.cpu(), rb.cutoff, l1.weight.cpu(),
+                             l1.bias.cpu(), l2.weight.cpu(), l2.bias.cpu())
+    _close(rb(gr.dist.detach()), want, 1e-5, 1e-5)
