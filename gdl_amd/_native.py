@@ -47,6 +47,9 @@ _SIGNATURES = {
     "geo_csr_build": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_csr_build_noalloc": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_csr_from_row_ptr": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "geo_spatial_graph_epilogue_dev": (c_int, [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_i64,
+                                               c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                               c_vp]),
     "geo_spatial_graph_epilogue": (c_int, [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_int, c_vp, c_i64,
                                            c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                            c_vp, c_size, c_vp]),

@@ -115,13 +115,18 @@ def radius_graph_csr_hip(
     mask: Optional[Tensor] = None,
     batch: Optional[Tensor] = None,
     num_batch_elements: Optional[int] = None,
+    after_emit=None,
 ) -> Tuple[Tensor, Tensor, Tensor, int]:
     """Radius graph on the GPU; returns (row=source, col=target) int64, sorted by target then
     source, the CSR row pointer (int64 [N+1]) and the number of clouds B.  Cloud membership comes
     from ``batch`` when given, otherwise from ``num_batch_elements`` contiguous equal chunks (one
     cloud when neither is given).  ``r`` is a Python number or a one-element device tensor (e.g.
     an adaptive radius computed on the GPU), which the kernels read directly: no host round trip
-    for the radius."""
+    for the radius.  ``after_emit(row_scratch, col_scratch, row_ptr, cap, ppc)``, if given, is
+    called after each launch of the emit pass into bound-sized scratch (cap rows, the first E of
+    them the graph), before the host waits for E, with the cloud size ppc that pass assumed (0
+    for clouds given by a batch vector of any layout); it is not called when the graph is too
+    large for bound-sized scratch."""
     _require_gpu("radius_graph", x, mask, batch)
     x = _positions("radius_graph", x)
     dev = x.device
@@ -194,6 +199,8 @@ def radius_graph_csr_hip(
                 scratch = torch.empty(2, N * K, dtype=torch.int64, device=dev)
                 _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(scratch[0]), _nat.ptr(scratch[1]),
                                 _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
+                if after_emit is not None:
+                    after_emit(scratch[0], scratch[1], row_ptr, N * K, p_arg)
                 counted.synchronize()
                 E, bad = edges_h[:2].tolist()
                 if bad == 0:

@@ -83,21 +83,20 @@ __device__ __forceinline__ void sh_grad(const ShConst& c, float x, float y, floa
   }
 }
 
-// One thread per edge; the block's direction and Y rows are staged in LDS and written back as
-// contiguous runs (a thread's own rows are 12 and 36 bytes apart from its neighbours').
-__global__ __launch_bounds__(kEgThreads) void edge_geom_kernel(
-    const float* __restrict__ pos, int64_t N, const int64_t* __restrict__ row,
-    const int64_t* __restrict__ col, int64_t E, int max_l, ShConst c, float* __restrict__ dir,
-    float* __restrict__ dist, float* __restrict__ Y) {
+// One thread per edge of the tile [e0, e0 + cnt); the tile's direction and Y rows are staged in
+// LDS and written back as contiguous runs (a thread's own rows are 12 and 36 bytes apart from
+// its neighbours').  The caller synchronises before reusing the LDS.
+__device__ __forceinline__ void edge_geom_tile(const float* __restrict__ pos, int64_t N,
+                                               const int64_t* __restrict__ row,
+                                               const int64_t* __restrict__ col, int64_t e0,
+                                               int cnt, int max_l, const ShConst& c,
+                                               float* __restrict__ dir, float* __restrict__ dist,
+                                               float* __restrict__ Y, float* s_dir, float* s_y) {
 #pragma clang fp contract(off)
-  __shared__ float s_dir[3 * kEgThreads];
-  __shared__ float s_y[9 * kEgThreads];
   const int t = static_cast<int>(threadIdx.x);
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads;
   const int64_t e = e0 + t;
-  const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
   const int nsh = (max_l + 1) * (max_l + 1);
-  if (e < E) {
+  if (t < cnt) {
     int64_t i = col[e], j = row[e];
     const bool ok = i >= 0 && i < N && j >= 0 && j < N;
     i = ok ? i : 0;
@@ -122,6 +121,56 @@ __global__ __launch_bounds__(kEgThreads) void edge_geom_kernel(
   for (int q = t; q < 3 * cnt; q += kEgThreads) dir[3 * e0 + q] = s_dir[q];
   if (Y)
     for (int q = t; q < nsh * cnt; q += kEgThreads) Y[nsh * e0 + q] = s_y[q];
+}
+
+__global__ __launch_bounds__(kEgThreads) void edge_geom_kernel(
+    const float* __restrict__ pos, int64_t N, const int64_t* __restrict__ row,
+    const int64_t* __restrict__ col, int64_t E, int max_l, ShConst c, float* __restrict__ dir,
+    float* __restrict__ dist, float* __restrict__ Y) {
+  __shared__ float s_dir[3 * kEgThreads];
+  __shared__ float s_y[9 * kEgThreads];
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads;
+  const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
+  edge_geom_tile(pos, N, row, col, e0, cnt, max_l, c, dir, dist, Y, s_dir, s_y);
+}
+
+// The SpatialGraph epilogue of a radius graph whose edge count the host does not know yet:
+// launched right behind the emit pass, it reads E = row_ptr[N] on the device (at most `cap`,
+// the size of the bound-sized outputs) and walks the edges and nodes in grid-stride loops.
+// Edges: the geometry of edge_geom_kernel, the int32 target and the identity permutation (the
+// graph is grouped by target).  Nodes: their CSR range from row_ptr and, for contiguous clouds
+// of ppc points, the cloud's average degree (its edge count, row_ptr at its last node minus at
+// its first, over ppc; at least 1), the value graph_avg_degree computes.
+__global__ __launch_bounds__(kEgThreads) void graph_epilogue_dev(
+    const float* __restrict__ pos, int64_t N, const int64_t* __restrict__ row,
+    const int64_t* __restrict__ col, const int64_t* __restrict__ row_ptr, int64_t cap, int max_l,
+    ShConst c, int64_t ppc, float* __restrict__ dir, float* __restrict__ dist,
+    float* __restrict__ Y, int32_t* __restrict__ col32, int32_t* __restrict__ perm,
+    int32_t* __restrict__ node_start, int32_t* __restrict__ node_end, float* __restrict__ avg) {
+  __shared__ float s_dir[3 * kEgThreads];
+  __shared__ float s_y[9 * kEgThreads];
+  int64_t E = row_ptr[N];
+  E = E < 0 ? 0 : (E > cap ? cap : E);
+  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads; e0 < E;
+       e0 += static_cast<int64_t>(gridDim.x) * kEgThreads) {
+    const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
+    edge_geom_tile(pos, N, row, col, e0, cnt, max_l, c, dir, dist, Y, s_dir, s_y);
+    const int64_t e = e0 + threadIdx.x;
+    if (static_cast<int>(threadIdx.x) < cnt) {
+      col32[e] = static_cast<int32_t>(col[e]);
+      perm[e] = static_cast<int32_t>(e);
+    }
+    __syncthreads();  // the next tile reuses the LDS
+  }
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEgThreads + threadIdx.x; i < N;
+       i += static_cast<int64_t>(gridDim.x) * kEgThreads) {
+    node_start[i] = static_cast<int32_t>(row_ptr[i]);
+    node_end[i] = static_cast<int32_t>(row_ptr[i + 1]);
+    const int64_t b0 = i / ppc * ppc;
+    const float s = static_cast<float>(static_cast<unsigned long long>(row_ptr[b0 + ppc] - row_ptr[b0]));
+    const float a = s / static_cast<float>(ppc);
+    avg[i] = a < 1.f ? 1.f : a;
+  }
 }
 
 __global__ __launch_bounds__(kEgThreads) void edge_geom_bwd_kernel(
@@ -442,6 +491,34 @@ extern "C" int geo_csr_from_row_ptr(const int64_t* row_ptr, int64_t N, const int
   hipLaunchKernelGGL(csr_from_row_ptr, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      as_stream(stream), row_ptr, N, col, E, col32, perm, node_start, node_end);
   GEO_LAUNCH_CHECK("csr_from_row_ptr");
+  return GEO_OK;
+}
+
+extern "C" int geo_spatial_graph_epilogue_dev(const float* pos, int64_t N, const int64_t* row,
+                                              const int64_t* col, const int64_t* row_ptr,
+                                              int64_t cap, int max_l, int64_t points_per_cloud,
+                                              float* direction, float* dist, float* Y,
+                                              int32_t* col_sorted, int32_t* perm,
+                                              int32_t* node_start, int32_t* node_end,
+                                              float* avg_degree, void* stream) {
+  GEO_REQUIRE(N >= 1 && cap >= 0, "spatial_graph_epilogue_dev: need N >= 1 and cap >= 0");
+  GEO_REQUIRE(N < 0x7fffffffLL && cap < 0x7fffffffLL, "spatial_graph_epilogue_dev: sizes exceed int32");
+  GEO_REQUIRE(max_l >= 0 && max_l <= 2, "spatial_graph_epilogue_dev: max_l must be 0, 1 or 2");
+  GEO_REQUIRE(points_per_cloud >= 1 && N % points_per_cloud == 0,
+              "spatial_graph_epilogue_dev: N=%lld is not a whole number of clouds of %lld points",
+              (long long)N, (long long)points_per_cloud);
+  GEO_REQUIRE(pos && row && col && row_ptr && direction && dist && col_sorted && perm &&
+                  node_start && node_end && avg_degree,
+              "spatial_graph_epilogue_dev: null pointer");
+  const int64_t span = cap > N ? cap : N;
+  int64_t blocks = ceil_div(span, kEgThreads);
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(graph_epilogue_dev, dim3(static_cast<unsigned>(blocks)), dim3(kEgThreads), 0,
+                     as_stream(stream), pos, N, row, col, row_ptr, cap, max_l, sh_constants(),
+                     points_per_cloud, direction, dist, Y, col_sorted, perm, node_start, node_end,
+                     avg_degree);
+  GEO_LAUNCH_CHECK("graph_epilogue_dev");
   return GEO_OK;
 }
 

@@ -33,6 +33,12 @@ from gdl_amd.csrc import (
     source_csr,
 )
 
+# SpatialGraph.build computes the edge geometry, CSR arrays and degrees on the device right behind
+# the radius graph's emit pass, before the host knows E, into buffers of N * max_num_neighbors
+# rows (the graph's fields are views of their first E rows), when those buffers stay below this
+# size; larger graphs get exact-sized fields after the host has read E.
+_FUSED_EPILOGUE_MAX_BYTES = 256 << 20
+
 
 class _EdgeGeometry(torch.autograd.Function):
     @staticmethod
@@ -95,24 +101,66 @@ class SpatialGraph:
         (geoembodied/nn/modules/spatial_graph.py:85-167).  ``radius`` may be a device tensor."""
         N = pos.shape[0]
         dev = pos.device
+        nsh = (max_l + 1) ** 2
+        K = int(max_num_neighbors)
+        differentiable = torch.is_grad_enabled() and pos.requires_grad
+        fused = {}
+        after_emit = None
+        if (not differentiable and N >= 1 and K >= 1
+                and N * K * (4 + nsh + 2) * 4 <= _FUSED_EPILOGUE_MAX_BYTES):
+            p32 = _positions("spatial_graph", pos)
+
+            def after_emit(row_s, col_s, row_ptr_d, cap, ppc_used):
+                # the epilogue runs on the device behind the emit pass, while the host waits for
+                # E; only for contiguous clouds (their average degree comes from row_ptr).  As
+                # in the reference (spatial_graph.py:157-158), without a batch vector the whole
+                # graph is one cloud for the degree, whatever chunks the radius search used.
+                fused.clear()
+                if ppc_used <= 0:
+                    return
+                deg_ppc = ppc_used if batch is not None else N
+                fbuf = torch.empty(cap * (4 + nsh) + N, dtype=torch.float32, device=dev)
+                ibuf = torch.empty(2 * cap + 2 * N, dtype=torch.int32, device=dev)
+                f = dict(direction=fbuf[:3 * cap].view(cap, 3), dist=fbuf[3 * cap:4 * cap],
+                         Y=fbuf[4 * cap:(4 + nsh) * cap].view(cap, nsh),
+                         avg=fbuf[(4 + nsh) * cap:], col_sorted=ibuf[:cap],
+                         perm=ibuf[cap:2 * cap], node_start=ibuf[2 * cap:2 * cap + N],
+                         node_end=ibuf[2 * cap + N:])
+                with _nat.on_device(dev):
+                    _nat.check(_nat.lib().geo_spatial_graph_epilogue_dev(
+                        _nat.ptr(p32), N, _nat.ptr(row_s), _nat.ptr(col_s), _nat.ptr(row_ptr_d),
+                        cap, int(max_l), int(deg_ppc), *[_nat.ptr(f[k]) for k in (
+                            "direction", "dist", "Y", "col_sorted", "perm", "node_start",
+                            "node_end", "avg")], _nat.stream_of(dev)),
+                        "geo_spatial_graph_epilogue_dev")
+                fused.update(f)
+
         row, col, row_ptr, B = radius_graph_csr_hip(
             pos, radius, max_num_neighbors=max_num_neighbors, batch=batch, mask=mask,
-            num_batch_elements=num_batch_elements)
+            num_batch_elements=num_batch_elements, after_emit=after_emit)
         E = row.shape[0]
         if E == 0:
             return SpatialGraph._empty(N, dev, max_l)
+        if fused:
+            # views of the first E rows of the bound-sized fields the device epilogue wrote
+            graph = SpatialGraph(row=row, col=col, direction=fused["direction"][:E],
+                                 dist=fused["dist"][:E], col_sorted=fused["col_sorted"][:E],
+                                 perm=fused["perm"][:E], node_start=fused["node_start"],
+                                 node_end=fused["node_end"], Y=fused["Y"][:E], N=N, E=E,
+                                 avg_degree=fused["avg"])
+            object.__setattr__(graph, "_perm_identity", True)
+            return graph
         if batch is not None:
             # B comes from the radius graph (its batch.max() sync, or num_batch_elements)
             batch = batch.reshape(-1).to(device=dev, dtype=torch.int64)
             ppc = 0
         else:
             B, ppc = 1, N
-        nsh = (max_l + 1) ** 2
         ibuf = torch.empty(2 * E + 2 * N, dtype=torch.int32, device=dev)
         col_sorted, perm = ibuf[:E], ibuf[E:2 * E]
         node_start, node_end = ibuf[2 * E:2 * E + N], ibuf[2 * E + N:]
         L = _nat.lib()
-        if torch.is_grad_enabled() and pos.requires_grad:
+        if differentiable:
             # differentiable geometry (autograd function), CSR arrays and degrees separately
             with _nat.on_device(dev):
                 _nat.check(L.geo_csr_from_row_ptr(

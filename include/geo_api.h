@@ -387,6 +387,19 @@ int geo_spatial_graph_epilogue(const float* pos, int64_t N, const int64_t* row, 
                                float* Y, int32_t* col_sorted, int32_t* perm, int32_t* node_start,
                                int32_t* node_end, float* avg_degree, void* workspace,
                                size_t workspace_bytes, void* stream);
+/* The same epilogue for a radius graph whose edge count the host does not know yet (the same
+ * reference lines): launched on the stream right behind geo_radius_emit, it reads
+ * E = row_ptr[N] on the device, so it runs while the host waits for E.  row, col and the edge
+ * outputs (direction [cap, 3], dist [cap], Y [cap, (max_l+1)^2], col_sorted, perm [cap]) hold
+ * cap >= E rows, of which the first E are read and written; node_start, node_end, avg_degree
+ * are [N].  The clouds are contiguous runs of points_per_cloud points (N a multiple of it); the
+ * average degree of a cloud is its edge count over points_per_cloud, at least 1. */
+int geo_spatial_graph_epilogue_dev(const float* pos, int64_t N, const int64_t* row,
+                                   const int64_t* col, const int64_t* row_ptr, int64_t cap,
+                                   int max_l, int64_t points_per_cloud, float* direction,
+                                   float* dist, float* Y, int32_t* col_sorted, int32_t* perm,
+                                   int32_t* node_start, int32_t* node_end, float* avg_degree,
+                                   void* stream);
 
 /* ------------------------------------------ SE(3) message passing (fused aggregate) --- */
 /*

@@ -81,6 +81,52 @@ def test_spatial_graph_build_vs_oracle(dev, B, N, r, K):
                                oracle.graph_avg_degree(ns, ne, batch.numpy(), B), rtol=1e-7)
 
 
+@pytest.mark.parametrize("layout", ["batch_chunks", "num_batch_elements", "one_cloud", "mask"])
+def test_spatial_graph_device_epilogue_matches_exact_sized(dev, layout):
+    """SpatialGraph.build without gradients computes its fields on the device behind the radius
+    graph's emit pass (bound-sized buffers, views of the first E rows); with gradients it takes
+    the exact-sized path after the edge count.  Both must agree bit for bit, for every layout of
+    contiguous equal clouds."""
+    _, SpatialGraph = _f()
+    B = 1 if layout == "one_cloud" else 4
+    pos, batch = _cloud(1500, B, 77 + B)
+    kw = dict(max_num_neighbors=24)
+    if layout == "batch_chunks":
+        kw.update(batch=batch.to(dev), num_batch_elements=B)
+    elif layout in ("num_batch_elements", "mask"):
+        kw.update(num_batch_elements=B)
+    if layout == "mask":
+        m = torch.ones(pos.shape[0], dtype=torch.bool)
+        m[::7] = False
+        kw.update(mask=m.to(dev))
+    with torch.no_grad():
+        fast = SpatialGraph.build(pos.to(dev), 0.12, **kw)
+    with torch.enable_grad():
+        exact = SpatialGraph.build(pos.to(dev).requires_grad_(True), 0.12, **kw)
+    assert fast.E == exact.E > 0
+    for name in ("row", "col", "direction", "dist", "Y", "col_sorted", "perm", "node_start",
+                 "node_end", "avg_degree"):
+        a, b = getattr(fast, name), getattr(exact, name).detach()
+        assert a.shape == b.shape and torch.equal(a, b), name
+
+
+def test_spatial_graph_shuffled_batch_takes_exact_path(dev):
+    """A batch vector whose clouds are not contiguous chunks: the device epilogue is skipped (its
+    degree formula assumes chunks) and the fields still match the oracle."""
+    _, SpatialGraph = _f()
+    pos, batch = _cloud(800, 3, 5)
+    sh = torch.randperm(pos.shape[0], generator=torch.Generator().manual_seed(1))
+    pos, batch = pos[sh], batch[sh]
+    graph = SpatialGraph.build(pos.to(dev), 0.2, max_num_neighbors=16, batch=batch.to(dev),
+                               num_batch_elements=3)
+    wr, wc = oracle.radius_graph(pos.numpy(), 0.2, 16, batch=batch.numpy(), num_batch_elements=3)
+    np.testing.assert_array_equal(graph.col.cpu().numpy(), wc)
+    cs, pm, ns, ne = oracle.sort_and_build_csr(wc, pos.shape[0])
+    np.testing.assert_array_equal(graph.node_start.cpu().numpy(), ns)
+    np.testing.assert_allclose(graph.avg_degree.cpu().numpy(),
+                               oracle.graph_avg_degree(ns, ne, batch.numpy(), 3), rtol=1e-7)
+
+
 def _avg_degree_np(row_ptr, batch, B):
     deg = np.diff(row_ptr).astype(np.float64)
     valid = (batch >= 0) & (batch < B)
