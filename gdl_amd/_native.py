@@ -85,6 +85,11 @@ _SIGNATURES = {
     "geo_se3_aggregate_fwd": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp,
                                       c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp,
                                       c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "geo_se3_fwd_fused_lds_bytes": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "geo_se3_fwd_fused": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp,
+                                  c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp, c_i32, c_vp,
+                                  c_i32, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp,
+                                  c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_se3_gemm": (c_int, [c_vp, c_i64, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp, c_vp,
                              c_vp, c_vp]),
     "geo_se3_gemm_tn_workspace_bytes": (c_size, [c_i64, c_i32, c_i32]),

@@ -29,6 +29,8 @@
 // se3_bwd_src sums the gradient rows of each source's targets with the per-edge weights (one wave
 // per source node over the CSR of the sources), after which GEMMs with the transposed weights
 // give the feature gradients.
+#include <type_traits>
+
 #include "common.hpp"
 
 // The library is built with -ffp-contract=off because the geometry kernels must round like the
@@ -83,10 +85,10 @@ struct EdgeScalars {
   float y2[5];
 };
 
-// Lane j of the wave loads the scalars of the edge at CSR position base + j (j < cnt), so the
+// Each lane loads the scalars of the edge at its CSR position `pos` (when `valid`), so the
 // edges of a node are fetched in one round of parallel loads; the edge loops then read them
 // from lane j with v_readlane (uniform j) or a lane shuffle (per-row j).
-__device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, int cnt, int lane) {
+__device__ __forceinline__ EdgeScalars stage_edges_at(const SeEdges& g, int pos, bool valid) {
   EdgeScalars q;
   q.other = 0;
   q.e = 0;
@@ -97,8 +99,8 @@ __device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, i
   q.y0 = 0.f;
 #pragma unroll
   for (int m = 0; m < 5; ++m) q.y2[m] = 0.f;
-  if (lane < cnt) {
-    const int e = g.perm ? g.perm[base + lane] : base + lane;
+  if (valid) {
+    const int e = g.perm ? g.perm[pos] : pos;
     if (static_cast<unsigned>(e) < static_cast<unsigned>(g.E)) {
       const int64_t o = g.other[e];
       if (o >= 0 && o < g.N) {
@@ -122,6 +124,11 @@ __device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, i
     }
   }
   return q;
+}
+
+// Lane j stages the edge at CSR position base + j (j < cnt).
+__device__ __forceinline__ EdgeScalars stage_edges(const SeEdges& g, int base, int cnt, int lane) {
+  return stage_edges_at(g, base + lane, lane < cnt);
 }
 
 // The staged scalars of lane j (j may differ between lanes).
@@ -157,8 +164,15 @@ struct EdgeCoef {
 __device__ __forceinline__ void cg_coef(const float* cg, const float d[3], float r, float D[3][5]);
 
 template <bool T2>
+__device__ __forceinline__ EdgeCoef<T2> coef_of(const SeEdges& g, const EdgeScalars& q);
+
+template <bool T2>
 __device__ __forceinline__ EdgeCoef<T2> stage_coef(const SeEdges& g, int base, int cnt, int lane) {
-  const EdgeScalars q = stage_edges(g, base, cnt, lane);
+  return coef_of<T2>(g, stage_edges(g, base, cnt, lane));
+}
+
+template <bool T2>
+__device__ __forceinline__ EdgeCoef<T2> coef_of(const SeEdges& g, const EdgeScalars& q) {
   EdgeCoef<T2> c;
   c.other = q.other;
   c.ok = q.ok;
@@ -244,8 +258,143 @@ constexpr int kSeUnroll = 2;  // edges whose source rows are in flight together 
 // neighbouring nodes -- which share source rows -- are processed under the same L2.
 
 // ------------------------------------------------------------------ forward aggregate ---
+// Per-lane sums of one target node's r-weighted source features, one input channel per lane
+// (the type-2 sums compile out without T2).
+template <bool T2>
+struct NodeAcc {
+  float A0, A1[3], A2[3], A3, A4[3];
+  float A5[5], A6[5], A7[5], A8;
+  __device__ __forceinline__ void zero() {
+    A0 = A3 = A8 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) A1[k] = A2[k] = A4[k] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) A5[k] = A6[k] = A7[k] = 0.f;
+  }
+};
+
+// Adds one edge (coefficients q; the lane's source values x, v[3], t[5]) to A.  hs / hv / ht:
+// the lane's channel exists in s / v / t; t_out: type-2 outputs are computed.
+template <bool T2>
+__device__ __forceinline__ void accumulate_edge(NodeAcc<T2>& A, const SeEdges& g,
+                                                const EdgeCoef<T2>& q, bool hs, bool hv, bool ht,
+                                                bool t_out, float x, const float* v,
+                                                const float* t) {
+  if (hs) {
+    if (g.pc[0] >= 0) A.A0 += q.c0 * x;
+    if (g.pc[1] >= 0) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) A.A1[k] += q.c1[k] * x;
+    }
+    if (T2 && g.pc[5] >= 0) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k) A.A5[k] += q.c5[k] * x;
+    }
+  }
+  if (hv) {
+    if (g.pc[2] >= 0) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) A.A2[k] += q.c2 * v[k];
+    }
+    if (g.pc[3] >= 0) A.A3 += (q.c3[0] * v[0] + q.c3[1] * v[1]) + q.c3[2] * v[2];
+    if (g.pc[4] >= 0) {
+      A.A4[0] += q.c4[1] * v[2] - q.c4[2] * v[1];
+      A.A4[1] += q.c4[2] * v[0] - q.c4[0] * v[2];
+      A.A4[2] += q.c4[0] * v[1] - q.c4[1] * v[0];
+    }
+    if (T2 && g.pc[7] >= 0 && t_out) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k)
+        A.A7[k] += (q.d7[0][k] * v[0] + q.d7[1][k] * v[1]) + q.d7[2][k] * v[2];
+    }
+  }
+  if (ht) {
+    if (g.pc[6] >= 0) {
+#pragma unroll
+      for (int k = 0; k < 5; ++k) A.A6[k] += q.c6 * t[k];
+    }
+    if (g.pc[8] >= 0)
+      A.A8 += q.c8 * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
+  }
+}
+
+// The lane's channel in each feature kind as a byte offset inside a source row, clamped to the
+// kind's last channel: every lane loads (a lane past a kind's channels reads a channel it will
+// not use), so the loads carry no per-lane condition.  A source row is read by buffer loads
+// through a resource built from its wave-uniform address (scalar registers) and this 32-bit
+// offset: no per-lane address arithmetic and no address registers per load, so a wave's rows are
+// all in flight together.  (With per-lane conditions and 64-bit per-lane addresses the compiler
+// waited for each row before issuing the next.)
+struct LaneCh {
+  uint32_t s, v, t;
+  __device__ __forceinline__ LaneCh(const SeFeat& f, int c)
+      : s(4u * min(c, max(f.Cs - 1, 0))),
+        v(12u * min(c, max(f.Cv - 1, 0))),
+        t(20u * min(c, max(f.Ct - 1, 0))) {}
+};
+
+// A buffer resource over `bytes` bytes at p: loads through it read zeros past the end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+// The float at byte offset `byte`.
+__device__ __forceinline__ float ld_row(__amdgpu_buffer_rsrc_t r, uint32_t byte) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte, 0, 0));
+}
+
+// Loads the lane's channel of source row m (wave-uniform): s, v (3) and t (5), for the kinds
+// the features have.
+template <bool T2>
+__device__ __forceinline__ void load_source(const SeFeat& f, int m, const LaneCh& ch, float& x,
+                                            float* v, float* t) {
+  if (f.Cs > 0) x = ld_row(row_rsrc(f.s + static_cast<int64_t>(m) * f.Cs, 4 * f.Cs), ch.s);
+  if (f.Cv > 0) {
+    const auto r = row_rsrc(f.v + static_cast<int64_t>(m) * (3 * f.Cv), 12 * f.Cv);
+    v[0] = ld_row(r, ch.v);
+    v[1] = ld_row(r, ch.v + 4);
+    v[2] = ld_row(r, ch.v + 8);
+  }
+  if (T2 && f.Ct > 0) {
+    const auto r = row_rsrc(f.t + static_cast<int64_t>(m) * (5 * f.Ct), 20 * f.Ct);
+#pragma unroll
+    for (int k = 0; k < 5; ++k) t[k] = ld_row(r, ch.t + 4 * k);
+  }
+}
+
+// Writes the lane's channel c of a node's aggregate rows (layout in the header comment):
+// xs [Ks] = A0 | A3 | A8, xv row k (k < 3, rows sv apart) = A1_k | A2_k | A4_k, xt row m
+// (m < 5, rows st apart) = A5_m | A6_m | A7_m.  A NULL row pointer skips that kind.
+template <bool T2>
+__device__ __forceinline__ void store_node(const NodeAcc<T2>& A, const SeFeat& f, int c, bool hs,
+                                           bool hv, bool ht, float* xs, float* xv, int sv,
+                                           float* xt, int st) {
+  if (xs) {
+    if (hs) xs[c] = A.A0;
+    if (hv) xs[f.Cs + c] = A.A3;
+    if (ht) xs[f.Cs + f.Cv + c] = A.A8;
+  }
+  if (xv) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float* row = xv + k * sv;
+      if (hs) row[c] = A.A1[k];
+      if (hv) row[f.Cs + c] = A.A2[k];
+      if (hv) row[f.Cs + f.Cv + c] = A.A4[k];
+    }
+  }
+  if (T2 && xt) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+      float* row = xt + k * st;
+      if (hs) row[c] = A.A5[k];
+      if (ht) row[f.Cs + c] = A.A6[k];
+      if (hv) row[f.Cs + f.Ct + c] = A.A7[k];
+    }
+  }
+}
+
 // One wave per target node, lanes over input channels (chunks of 64).  The node's edges are
-// staged in lanes, then walked four at a time: the four source rows are loaded first, then
+// staged in lanes, then walked kSeUnroll at a time: the source rows are loaded first, then
 // accumulated in CSR order.
 template <bool T2>  // T2: type-2 features or outputs present (else their paths compile out)
 __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFeat f,
@@ -258,12 +407,13 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
   int a, b;
   node_range(g, n, a, b);
   const int cmax = max(f.Cs, max(f.Cv, f.Ct));
+  const bool t_out = Xt != nullptr;
   for (int c0 = 0; c0 < cmax; c0 += kWave) {
     const int c = c0 + lane;
     const bool hs = c < f.Cs, hv = c < f.Cv, ht = T2 && c < f.Ct;
-    float A0 = 0.f, A1[3] = {0.f, 0.f, 0.f}, A5[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-    float A2[3] = {0.f, 0.f, 0.f}, A3 = 0.f, A4[3] = {0.f, 0.f, 0.f};
-    float A7[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A6[5] = {0.f, 0.f, 0.f, 0.f, 0.f}, A8 = 0.f;
+    const LaneCh ch(f, c);
+    NodeAcc<T2> A;
+    A.zero();
     for (int base = a; base < b; base += kWave) {
       const int cnt = min(kWave, b - base);
       const EdgeCoef<T2> st = stage_coef<T2>(g, base, cnt, lane);
@@ -272,89 +422,20 @@ __global__ __launch_bounds__(kSeThreads) void se3_fwd_aggregate(SeEdges g, SeFea
 #pragma unroll
         for (int u = 0; u < kSeUnroll; ++u) {
           const int j = min(j0 + u, kWave - 1);
-          const int64_t m = __builtin_amdgcn_readlane(st.other, j);  // 0 past cnt: in bounds
-          if (hs) sv[u] = f.s[m * f.Cs + c];
-          if (hv) {
-            const float* vp = f.v + (m * f.Cv + c) * 3;
-            vv[u][0] = vp[0]; vv[u][1] = vp[1]; vv[u][2] = vp[2];
-          }
-          if (ht) {
-            const float* tp = f.t + (m * f.Ct + c) * 5;
-#pragma unroll
-            for (int k = 0; k < 5; ++k) tt[u][k] = tp[k];
-          }
+          const int m = __builtin_amdgcn_readlane(st.other, j);  // 0 past cnt: in bounds
+          load_source<T2>(f, m, ch, sv[u], vv[u], tt[u]);
         }
 #pragma unroll
         for (int u = 0; u < kSeUnroll; ++u) {
           if (j0 + u >= cnt) break;
           const EdgeCoef<T2> q = coef_at<T2>(st, j0 + u);
           if (!q.ok) continue;
-          if (hs) {
-            const float x = sv[u];
-            if (g.pc[0] >= 0) A0 += q.c0 * x;
-            if (g.pc[1] >= 0) {
-#pragma unroll
-              for (int k = 0; k < 3; ++k) A1[k] += q.c1[k] * x;
-            }
-            if (T2 && g.pc[5] >= 0) {
-#pragma unroll
-              for (int k = 0; k < 5; ++k) A5[k] += q.c5[k] * x;
-            }
-          }
-          if (hv) {
-            const float* v = vv[u];
-            if (g.pc[2] >= 0) {
-#pragma unroll
-              for (int k = 0; k < 3; ++k) A2[k] += q.c2 * v[k];
-            }
-            if (g.pc[3] >= 0) A3 += (q.c3[0] * v[0] + q.c3[1] * v[1]) + q.c3[2] * v[2];
-            if (g.pc[4] >= 0) {
-              A4[0] += q.c4[1] * v[2] - q.c4[2] * v[1];
-              A4[1] += q.c4[2] * v[0] - q.c4[0] * v[2];
-              A4[2] += q.c4[0] * v[1] - q.c4[1] * v[0];
-            }
-            if (T2 && g.pc[7] >= 0 && Xt) {
-#pragma unroll
-              for (int k = 0; k < 5; ++k)
-                A7[k] += (q.d7[0][k] * v[0] + q.d7[1][k] * v[1]) + q.d7[2][k] * v[2];
-            }
-          }
-          if (ht) {
-            const float* t = tt[u];
-            if (g.pc[6] >= 0) {
-#pragma unroll
-              for (int k = 0; k < 5; ++k) A6[k] += q.c6 * t[k];
-            }
-            if (g.pc[8] >= 0)
-              A8 += q.c8 * ((((t[0] * t[0] + t[1] * t[1]) + t[2] * t[2]) + t[3] * t[3]) + t[4] * t[4]);
-          }
+          accumulate_edge<T2>(A, g, q, hs, hv, ht, t_out, sv[u], vv[u], tt[u]);
         }
       }
     }
-    if (Xs) {
-      float* row = Xs + n * Ks;
-      if (hs) row[c] = A0;
-      if (hv) row[f.Cs + c] = A3;
-      if (ht) row[f.Cs + f.Cv + c] = A8;
-    }
-    if (Xv) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        float* row = Xv + (n * 3 + k) * Kv;
-        if (hs) row[c] = A1[k];
-        if (hv) row[f.Cs + c] = A2[k];
-        if (hv) row[f.Cs + f.Cv + c] = A4[k];
-      }
-    }
-    if (T2 && Xt) {
-#pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        float* row = Xt + (n * 5 + k) * Kt;
-        if (hs) row[c] = A5[k];
-        if (ht) row[f.Cs + c] = A6[k];
-        if (hv) row[f.Cs + f.Ct + c] = A7[k];
-      }
-    }
+    store_node<T2>(A, f, c, hs, hv, ht, Xs ? Xs + n * Ks : nullptr, Xv ? Xv + n * 3 * Kv : nullptr,
+                   Kv, (T2 && Xt) ? Xt + n * 5 * Kt : nullptr, Kt);
   }
   if (Xs) zero_pad(Xs + n * Ks, f.Cs + f.Cv + f.Ct, Ks);
   if (Xv)
@@ -455,6 +536,448 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm(const float* __restrict__
         orow[static_cast<int64_t>(col0 + cb * 16 + li) * G] = keep ? val : 0.f;
       }
     }
+}
+
+// ---------------------------------------------- fused forward: aggregate + per-node GEMM ---
+// One workgroup per tile of kFuTile consecutive target nodes.  Each wave sums the r-weighted
+// source features of kFuNodes nodes (one input channel per lane, as se3_fwd_aggregate) into the
+// tile's aggregate rows in LDS; then the waves multiply the tile by the packed weights with
+// v_mfma_f32_16x16x4_f32 (the se3_gemm fragment layout, A from LDS) and apply the epilogue
+// (1 / avg, bias, mask).  The aggregates reach HBM only when the caller asks for them (the
+// weight gradients need them).
+//
+// Edges: the kFuNodes nodes' CSR ranges are concatenated into one flat list, staged 64 at a time
+// (lane l takes flat edge fb + l, wherever its node's range lies), and walked U at a time with
+// all U source rows loaded before any is used; the sums are flushed to LDS when the walk passes
+// a node's last edge.  A node's edges are still added in CSR order.
+constexpr int kFuTile = 16;                   // nodes per workgroup = MFMA rows of a scalar block
+constexpr int kFuNodes = kFuTile / kSeWaves;  // nodes per wave
+constexpr int kFuLdsMax = 64 * 1024;          // larger aggregate tiles take the unfused path
+static_assert(kFuNodes == 4, "the flat edge walk below is written for 4 nodes per wave");
+
+struct SeFused {
+  const float* W[3];   // packed weights [rows >= 16 ceil(O / 16)][K] (kinds: s, v, t)
+  float* out[3];       // s_out [N, Os], v_out [N, Ov, 3], t_out [N, Ot, 5]
+  float* X[3];         // optional HBM copies of the aggregate rows ([N, K], [N, 3, K], [N, 5, K])
+  int O[3];            // output channels (0: kind absent)
+  int K[3];            // aggregate row length (multiple of 16)
+  int ld[3];           // LDS row stride (K + 4 floats)
+  int off[3];          // LDS offset of the kind's tile (floats)
+  const float* avg;
+  const float* bias;
+  const uint8_t* mask;
+};
+
+// The tile's MFMA blocks of one kind: block b (< G ceil(O / 16)) is row block b / ncb, column
+// block b % ncb; wave w takes the blocks whose running number base + b is w mod 4.  The
+// epilogue's per-row operands are requested first and the weight fragments four 16-wide k chunks
+// at a time, so a block waits for global memory about once per 64 k instead of once per chunk.
+// (Holding a column block's weights for all G row blocks needs G accumulators and per-row
+// operands at once: 147 VGPRs for the whole kernel, whose walk then ran at a lower occupancy.)
+template <int G>
+__device__ __forceinline__ void fused_gemm(const float* __restrict__ tile, int ld, int K,
+                                           const float* __restrict__ W, int O,
+                                           float* __restrict__ out, const SeFused& p,
+                                           int64_t node0, int64_t N, int base, int wave, int lane) {
+  const int ncb = (O + 15) / 16;
+  const int nblk = G * ncb;
+  const int li = lane & 15, lk = lane >> 4;
+  for (int b = (wave - base % kSeWaves + kSeWaves) % kSeWaves; b < nblk; b += kSeWaves) {
+    const int rb = b / ncb, cb = b % ncb;
+    const int o = cb * 16 + li;
+    const float bo = (G == 1 && p.bias && o < O) ? p.bias[o] : 0.f;
+    float scale[4];
+    bool keep[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = node0 + (rb * 16 + 4 * lk + q) / G;
+      const bool in = n < N;
+      scale[q] = (in && p.avg) ? 1.0f / p.avg[n] : 1.0f;
+      keep[q] = !in || p.mask == nullptr || p.mask[n] != 0;
+    }
+    const float* ap = tile + (rb * 16 + li) * ld + 4 * lk;
+    const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 64) {
+      floatx4 a[4], w[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
+        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
+        a[c] = *reinterpret_cast<const floatx4*>(ap + k);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (k0 + 16 * c >= K) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = rb * 16 + 4 * lk + q;  // tile row: node r / G, component r % G
+      const int64_t n = node0 + r / G;
+      if (n >= N || o >= O) continue;
+      const float val = acc[q] * scale[q] + bo;
+      out[(n * O + o) * G + r % G] = keep[q] ? val : 0.f;
+    }
+  }
+}
+
+// Zeroes the padding columns [used, K) of every row of the tile; the walks write every used column.
+__device__ __forceinline__ void zero_tile_pads(const SeFeat& f, const SeFused& p, float* lds) {
+  const int used[3] = {f.Cs + f.Cv + f.Ct, f.Cs + 2 * f.Cv, f.Cs + f.Ct + f.Cv};
+  const int rows[3] = {kFuTile, 3 * kFuTile, 5 * kFuTile};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int pad = p.K[k] - used[k];
+    if (p.O[k] <= 0 || pad <= 0) continue;
+    for (int i = threadIdx.x; i < rows[k] * pad; i += kSeThreads)
+      lds[p.off[k] + (i / pad) * p.ld[k] + used[k] + i % pad] = 0.f;
+  }
+}
+
+// After the tile's aggregate rows are complete in LDS (behind a barrier): copies them to HBM
+// when the caller keeps them (a tile's rows are contiguous there), then computes the outputs,
+// the kinds' MFMA blocks spread over the four waves.
+template <bool T2>
+__device__ __forceinline__ void fused_tile_out(const SeFused& p, const float* lds, int64_t node0,
+                                               int64_t N, int wave, int lane) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int G = k == 0 ? 1 : (k == 1 ? 3 : 5);
+    if (p.O[k] <= 0 || p.X[k] == nullptr || (k == 2 && !T2)) continue;
+    const int64_t rows = min(static_cast<int64_t>(kFuTile), N - node0) * G;
+    const int K = p.K[k];
+    float* dst = p.X[k] + node0 * G * K;
+    for (int64_t i = threadIdx.x; i < rows * K; i += kSeThreads)
+      dst[i] = lds[p.off[k] + (i / K) * p.ld[k] + i % K];
+  }
+  const int nb0 = p.O[0] > 0 ? (p.O[0] + 15) / 16 : 0;
+  const int nb1 = p.O[1] > 0 ? 3 * ((p.O[1] + 15) / 16) : 0;
+  if (p.O[0] > 0)
+    fused_gemm<1>(lds + p.off[0], p.ld[0], p.K[0], p.W[0], p.O[0], p.out[0], p, node0, N, 0, wave,
+                  lane);
+  if (p.O[1] > 0)
+    fused_gemm<3>(lds + p.off[1], p.ld[1], p.K[1], p.W[1], p.O[1], p.out[1], p, node0, N, nb0,
+                  wave, lane);
+  if (T2 && p.O[2] > 0)
+    fused_gemm<5>(lds + p.off[2], p.ld[2], p.K[2], p.W[2], p.O[2], p.out[2], p, node0, N,
+                  nb0 + nb1, wave, lane);
+}
+
+template <bool T2, int U>  // U: source rows in flight per lane
+__global__ __launch_bounds__(kSeThreads) void se3_fwd_fused(SeEdges g, SeFeat f, SeFused p) {
+  extern __shared__ floatx4 fu_lds[];
+  float* lds = reinterpret_cast<float*>(fu_lds);
+  const int64_t node0 = xcd_block() * kFuTile;  // grid = ceil(N / kFuTile): node0 < N
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  float* ts = p.O[0] > 0 ? lds + p.off[0] : nullptr;
+  float* tv = p.O[1] > 0 ? lds + p.off[1] : nullptr;
+  float* tt = (T2 && p.O[2] > 0) ? lds + p.off[2] : nullptr;
+
+  zero_tile_pads(f, p, lds);
+
+  // the wave's nodes: CSR ranges loaded by lanes 0..3, concatenated into one flat edge list
+  const int64_t nw = node0 + wave * kFuNodes;
+  int la = 0, lb = 0;
+  if (lane < kFuNodes && nw + lane < g.N) node_range(g, nw + lane, la, lb);
+  const int a0 = __builtin_amdgcn_readlane(la, 0), a1 = __builtin_amdgcn_readlane(la, 1);
+  const int a2 = __builtin_amdgcn_readlane(la, 2), a3 = __builtin_amdgcn_readlane(la, 3);
+  const int cnt_l = lb - la;
+  const int e1 = __builtin_amdgcn_readlane(cnt_l, 0);           // flat end of node 0
+  const int e2 = e1 + __builtin_amdgcn_readlane(cnt_l, 1);      // of node 1
+  const int e3 = e2 + __builtin_amdgcn_readlane(cnt_l, 2);      // of node 2
+  const int total = e3 + __builtin_amdgcn_readlane(cnt_l, 3);  // of node 3
+  const bool t_out = tt != nullptr;
+  const int cmax = max(f.Cs, max(f.Cv, f.Ct));
+  for (int c0 = 0; c0 < cmax; c0 += kWave) {
+    const int c = c0 + lane;
+    const bool hs = c < f.Cs, hv = c < f.Cv, ht = T2 && c < f.Ct;
+    const LaneCh ch(f, c);
+    NodeAcc<T2> A;
+    A.zero();
+    int cur = 0, cur_end = e1;  // node being summed and its flat end
+    auto flush = [&](int i) {
+      const int nt = wave * kFuNodes + i;
+      store_node<T2>(A, f, c, hs, hv, ht, ts ? ts + nt * p.ld[0] : nullptr,
+                     tv ? tv + nt * 3 * p.ld[1] : nullptr, p.ld[1],
+                     tt ? tt + nt * 5 * p.ld[2] : nullptr, p.ld[2]);
+      A.zero();
+    };
+    for (int fb = 0; fb < total; fb += kWave) {
+      const int fl = fb + lane;
+      const int i = (fl >= e1) + (fl >= e2) + (fl >= e3);
+      const int start = i == 0 ? a0 : (i == 1 ? a1 : (i == 2 ? a2 : a3));
+      const int first = i == 0 ? 0 : (i == 1 ? e1 : (i == 2 ? e2 : e3));
+      const EdgeCoef<T2> st = coef_of<T2>(g, stage_edges_at(g, start + fl - first, fl < total));
+      const int cnt = min(kWave, total - fb);
+      for (int j0 = 0; j0 < cnt; j0 += U) {
+        float sv[U], vv[U][3], tw[U][5];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = min(j0 + u, kWave - 1);
+          const int m = __builtin_amdgcn_readlane(st.other, j);  // 0 past the list: in bounds
+          load_source<T2>(f, m, ch, sv[u], vv[u], tw[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (j0 + u >= cnt) break;
+          while (fb + j0 + u >= cur_end) {  // past the current node's last edge
+            flush(cur);
+            ++cur;
+            cur_end = cur == 1 ? e2 : (cur == 2 ? e3 : total);
+          }
+          const EdgeCoef<T2> q = coef_at<T2>(st, j0 + u);
+          if (!q.ok) continue;
+          accumulate_edge<T2>(A, g, q, hs, hv, ht, t_out, sv[u], vv[u], tw[u]);
+        }
+      }
+    }
+    for (; cur < kFuNodes; ++cur) flush(cur);
+  }
+  __syncthreads();
+  fused_tile_out<T2>(p, lds, node0, g.N, wave, lane);
+}
+
+// ------------------------------ fused forward, one node per 16-lane row (no type-2 paths) ---
+// Layers without type-2 features or outputs whose Cs <= 64 and Cv <= 16 (Cs a multiple of 4;
+// e.g. 64 scalar + 16 vector channels): a wave sums four nodes at once, one per 16-lane row.
+// Lane j of a row holds scalar channels 4j..4j+3 and vector channel j, so one 16-byte load (s)
+// and one 12-byte load (v) per lane fetch a source row for each of the four nodes -- two
+// vector-memory instructions per four edges where the channel-per-lane walk above issues four
+// per edge.  That walk keeps the texture address unit busy ~70% of its time (counters at C2);
+// this one needs an eighth of its instructions.  A row's edges are staged one per lane, 16 per
+// round, and edge u's source and coefficients reach the row's lanes by DPP row_newbcast:u.
+constexpr int kRowNodes = kFuTile / kSeWaves;  // nodes per wave = 16-lane rows
+constexpr int kRowStage = 16;                  // edges staged per row per round
+constexpr uint32_t kPastRows = 0x80000000u;    // a byte offset past every array (each < 2 GiB)
+static_assert(kRowNodes * 16 == kWave, "one node per 16-lane row");
+
+// Lane u of the lane's 16-lane row (u a compile-time constant).
+template <int u>
+__device__ __forceinline__ int row_bcast(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, 0x150 + u, 0xf, 0xf, false);  // row_newbcast:u
+}
+template <int u>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, row_bcast<u>(__builtin_bit_cast(int, x)));
+}
+
+// Calls f(std::integral_constant<int, I>) for I = B, B + 1, ..., E - 1.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Per-lane sums of the row's node: scalar channels 4j..4j+3 (A0, A1_k) and vector channel j
+// (A2_k, A3, A4_k).
+struct RowAcc {
+  float A0[4], A1[3][4];
+  float A2[3], A3, A4[3];
+};
+
+// Staging of the row kernel: the lane's edge at CSR position pos (when valid) -- its source, the
+// radial weights of paths 0-4, the direction (one 12-byte load) and Y_0^0 -- as coefficients
+// (coef_of's c0..c4).  The loads go through buffer resources and a lane without an edge reads
+// past the arrays (zeros), so none of them waits on a branch or on the source load; only the
+// permutation, when there is one, comes first.  Every array here is below 2 GiB (the host checks).
+__device__ __forceinline__ EdgeCoef<false> stage_rows(const SeEdges& g, int pos, bool valid) {
+  constexpr uint32_t kPast = kPastRows;
+  int e = valid ? pos : -1;
+  if (g.perm) {
+    const auto rp = row_rsrc(g.perm, g.E * 4);
+    e = valid ? static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rp, 4u * pos, 0, 0)) : -1;
+  }
+  const bool ein = static_cast<unsigned>(e) < static_cast<unsigned>(g.E);
+  const uint32_t ue = ein ? static_cast<uint32_t>(e) : 0u;
+  const auto ro = row_rsrc(g.other, g.E * 8);
+  const auto w = __builtin_amdgcn_raw_buffer_load_b64(ro, ein ? 8u * ue : kPast, 0, 0);
+  const uint32_t lo = w[0], hi = w[1];
+  const int64_t o = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  const auto rr = row_rsrc(g.R, g.E * g.P * 4);
+  float r[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i)
+    r[i] = g.pc[i] >= 0 ? ld_row(rr, ein ? 4u * (ue * g.P + g.pc[i]) : kPast) : 0.f;
+  const auto rd = row_rsrc(g.dir, g.E * 12);
+  const auto dv = __builtin_amdgcn_raw_buffer_load_b96(rd, ein ? 12u * ue : kPast, 0, 0);
+  const float d[3] = {__uint_as_float(dv[0]), __uint_as_float(dv[1]), __uint_as_float(dv[2])};
+  const auto ry = row_rsrc(g.Y, g.E * g.ysh * 4);
+  const float y0 = ld_row(ry, ein ? 4u * ue * g.ysh : kPast);
+  const bool ok = ein && o >= 0 && o < g.N;
+  EdgeCoef<false> c;
+  c.other = ok ? static_cast<int32_t>(o) : 0;
+  c.ok = ok ? 1 : 0;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) r[i] = ok ? r[i] : 0.f;
+  c.c0 = r[0] * y0;
+  c.c2 = r[2] * y0;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    c.c1[k] = r[1] * d[k];
+    c.c3[k] = r[3] * d[k];
+    c.c4[k] = r[4] * d[k];
+  }
+  return c;
+}
+
+template <int U>
+__global__ __launch_bounds__(kSeThreads) void se3_fwd_fused_rows(SeEdges g, SeFeat f, SeFused p) {
+  extern __shared__ floatx4 fu_lds[];
+  float* lds = reinterpret_cast<float*>(fu_lds);
+  const int64_t node0 = xcd_block() * kFuTile;  // grid = ceil(N / kFuTile): node0 < N
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  const int j = lane & 15;
+  const int nt = wave * kRowNodes + (lane >> 4);  // the row's node in the tile
+  zero_tile_pads(f, p, lds);
+
+  int a = 0, b = 0;
+  if (node0 + nt < g.N) node_range(g, node0 + nt, a, b);
+  const int deg = b - a;
+  const int maxdeg = max(max(__builtin_amdgcn_readlane(deg, 0), __builtin_amdgcn_readlane(deg, 16)),
+                         max(__builtin_amdgcn_readlane(deg, 32), __builtin_amdgcn_readlane(deg, 48)));
+  // whole-array resources (the host keeps both arrays below 4 GiB): a lane past the row's
+  // channels reads the next row (unused) or, past the array, zeros
+  const auto rs = row_rsrc(f.s, static_cast<int>(g.N * f.Cs * 4));
+  const auto rv = row_rsrc(f.v, static_cast<int>(g.N * f.Cv * 12));
+  const uint32_t rowb_s = 4u * f.Cs, rowb_v = 12u * f.Cv;
+  const uint32_t js = 16u * j, jv = 12u * j;
+
+  RowAcc A;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    A.A0[i] = 0.f;
+    A.A1[0][i] = A.A1[1][i] = A.A1[2][i] = 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) A.A2[k] = A.A4[k] = 0.f;
+  A.A3 = 0.f;
+
+  for (int base = 0; base < maxdeg; base += kRowStage) {
+    const EdgeCoef<false> st = stage_rows(g, a + base + j, base + j < deg);
+    const int cnt = min(kRowStage, maxdeg - base);
+    static_for<0, kRowStage / U>([&](auto ci) {
+      constexpr int c0 = decltype(ci)::value * U;
+      if (c0 >= cnt) return;
+      floatx4 sx[U];
+      float vx[U][3];
+      static_for<0, U>([&](auto ui) {  // the U source rows of every row in flight together
+        constexpr int u = c0 + decltype(ui)::value;
+        // a row without edge u (its node has fewer edges) reads past the arrays: zeros, no traffic
+        const bool have = row_bcast<u>(st.ok) != 0;
+        const uint32_t m = static_cast<uint32_t>(row_bcast<u>(st.other));
+        const auto ls = __builtin_amdgcn_raw_buffer_load_b128(rs, have ? m * rowb_s + js : kPastRows,
+                                                              0, 0);
+        const auto lv = __builtin_amdgcn_raw_buffer_load_b96(rv, have ? m * rowb_v + jv : kPastRows,
+                                                             0, 0);
+        // element by value: __builtin_bit_cast of a vector element reads the vector's first
+        // element whatever the index
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sx[decltype(ui)::value][i] = __uint_as_float(ls[i]);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) vx[decltype(ui)::value][k] = __uint_as_float(lv[k]);
+      });
+      static_for<0, U>([&](auto ui) {
+        constexpr int uu = decltype(ui)::value;
+        constexpr int u = c0 + uu;
+        // an edge that is not there (past the row's degree, or a source out of range) adds
+        // nothing: its values are replaced by zeros, so a non-finite row 0 cannot leak in
+        const bool ok = row_bcast<u>(st.ok) != 0;
+        float x[4], v[3];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = ok ? sx[uu][i] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) v[k] = ok ? vx[uu][k] : 0.f;
+        if (g.pc[0] >= 0) {
+          const float c = row_bcast<u>(st.c0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) A.A0[i] += c * x[i];
+        }
+        if (g.pc[1] >= 0) {
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+            const float c = row_bcast<u>(st.c1[k]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) A.A1[k][i] += c * x[i];
+          }
+        }
+        if (g.pc[2] >= 0) {
+          const float c = row_bcast<u>(st.c2);
+#pragma unroll
+          for (int k = 0; k < 3; ++k) A.A2[k] += c * v[k];
+        }
+        if (g.pc[3] >= 0) {
+          const float d0 = row_bcast<u>(st.c3[0]), d1 = row_bcast<u>(st.c3[1]);
+          const float d2 = row_bcast<u>(st.c3[2]);
+          A.A3 += (d0 * v[0] + d1 * v[1]) + d2 * v[2];
+        }
+        if (g.pc[4] >= 0) {
+          const float e0 = row_bcast<u>(st.c4[0]), e1 = row_bcast<u>(st.c4[1]);
+          const float e2 = row_bcast<u>(st.c4[2]);
+          A.A4[0] += e1 * v[2] - e2 * v[1];
+          A.A4[1] += e2 * v[0] - e0 * v[2];
+          A.A4[2] += e0 * v[1] - e1 * v[0];
+        }
+      });
+    });
+  }
+
+  // the node's aggregate rows into the tile (layout as se3_fwd_aggregate's rows)
+  float* ts = p.O[0] > 0 ? lds + p.off[0] + nt * p.ld[0] : nullptr;
+  float* tv = p.O[1] > 0 ? lds + p.off[1] + nt * 3 * p.ld[1] : nullptr;
+  if (4 * j < f.Cs) {
+    if (ts) *reinterpret_cast<floatx4*>(ts + 4 * j) = floatx4{A.A0[0], A.A0[1], A.A0[2], A.A0[3]};
+    if (tv)
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        *reinterpret_cast<floatx4*>(tv + k * p.ld[1] + 4 * j) =
+            floatx4{A.A1[k][0], A.A1[k][1], A.A1[k][2], A.A1[k][3]};
+  }
+  if (j < f.Cv) {
+    if (ts) ts[f.Cs + j] = A.A3;
+    if (tv)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        tv[k * p.ld[1] + f.Cs + j] = A.A2[k];
+        tv[k * p.ld[1] + f.Cs + f.Cv + j] = A.A4[k];
+      }
+  }
+  __syncthreads();
+  fused_tile_out<false>(p, lds, node0, g.N, wave, lane);
+}
+
+// Whether se3_fwd_fused_rows covers the layer (see its comment), with every array it reads
+// through a buffer resource below 2 GiB.
+bool fused_rows_ok(int64_t N, int Cs, int Cv, bool t2, int64_t E, int P, int ysh) {
+  const int64_t lim = int64_t{1} << 31;
+  return !t2 && Cs <= 64 && Cv <= 16 && Cs % 4 == 0 && N * Cs * 4 < lim && N * Cv * 12 < lim &&
+         E * 12 < lim && E * P * 4 < lim && E * ysh * 4 < lim;
+}
+
+// LDS layout of the fused kernel's tile: per present kind, kFuTile * G rows of K + 4 floats.
+// Returns the bytes, or 0 when they exceed kFuLdsMax.
+size_t fused_layout(int Os, int Ov, int Ot, int Ks, int Kv, int Kt, SeFused* p) {
+  const int O[3] = {Os, Ov, Ot}, K[3] = {Ks, Kv, Kt}, G[3] = {1, 3, 5};
+  size_t floats = 0;
+  for (int k = 0; k < 3; ++k) {
+    const int ld = K[k] + 4;
+    if (p) {
+      p->O[k] = O[k] > 0 ? O[k] : 0;
+      p->K[k] = O[k] > 0 ? K[k] : 0;
+      p->ld[k] = ld;
+      p->off[k] = static_cast<int>(floats);
+    }
+    if (O[k] > 0) floats += static_cast<size_t>(kFuTile) * G[k] * ld;
+  }
+  const size_t bytes = floats * sizeof(float);
+  return bytes <= static_cast<size_t>(kFuLdsMax) ? bytes : 0;
 }
 
 // ------------------------------------------------------------ split-K transposed GEMM ---
@@ -1119,6 +1642,80 @@ extern "C" int geo_se3_gemm(const float* A, int64_t M, int32_t K, const float* B
   GEO_GEMM(1, 5) GEO_GEMM(2, 5) GEO_GEMM(4, 5)
 #undef GEO_GEMM
   GEO_LAUNCH_CHECK("se3_gemm");
+  return GEO_OK;
+}
+
+extern "C" size_t geo_se3_fwd_fused_lds_bytes(int32_t Os, int32_t Ov, int32_t Ot, int32_t Ks,
+                                              int32_t Kv, int32_t Kt) {
+  if (Os < 0 || Ov < 0 || Ot < 0 || Ks < 0 || Kv < 0 || Kt < 0) return 0;
+  return fused_layout(Os, Ov, Ot, Ks, Kv, Kt, nullptr);
+}
+
+extern "C" int geo_se3_fwd_fused(const float* s, const float* v, const float* t, int64_t N,
+                                 int32_t Cs, int32_t Cv, int32_t Ct, const int64_t* row,
+                                 const int32_t* perm, const int32_t* node_start,
+                                 const int32_t* node_end, int64_t E, const float* dir,
+                                 const float* Y, int32_t ysh, const float* R, int32_t P,
+                                 const int32_t* path_cols, const float* cg, const float* Ws,
+                                 int32_t Ws_rows, const float* Wv, int32_t Wv_rows, const float* Wt,
+                                 int32_t Wt_rows, int32_t Os, int32_t Ov, int32_t Ot, int32_t Ks,
+                                 int32_t Kv, int32_t Kt, const float* avg, const float* bias,
+                                 const uint8_t* mask, float* s_out, float* v_out, float* t_out,
+                                 float* Xs, float* Xv, float* Xt, void* stream) {
+  int rc = check_edges("se3_fwd_fused", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(Cs >= 0 && Cv >= 0 && Ct >= 0 && Os >= 0 && Ov >= 0 && Ot >= 0,
+              "se3_fwd_fused: negative channel count");
+  GEO_REQUIRE((Cs == 0 || s) && (Cv == 0 || v) && (Ct == 0 || t), "se3_fwd_fused: null features");
+  GEO_REQUIRE(path_cols[6] < 0 || Ct > 0, "se3_fwd_fused: path 6 without type-2 input");
+  GEO_REQUIRE(path_cols[8] < 0 || Ct > 0, "se3_fwd_fused: path 8 without type-2 input");
+  const int used[3] = {Cs + Cv + Ct, Cs + 2 * Cv, Cs + Ct + Cv};
+  const int32_t O[3] = {Os, Ov, Ot}, K[3] = {Ks, Kv, Kt}, rows[3] = {Ws_rows, Wv_rows, Wt_rows};
+  const float* W[3] = {Ws, Wv, Wt};
+  float* out[3] = {s_out, v_out, t_out};
+  const char* kind[3] = {"scalar", "vector", "type-2"};
+  for (int k = 0; k < 3; ++k) {
+    if (O[k] == 0) continue;
+    GEO_REQUIRE(K[k] >= used[k] && K[k] % 16 == 0,
+                "se3_fwd_fused: %s row length %d must be a multiple of 16 and >= %d", kind[k], K[k],
+                used[k]);
+    GEO_REQUIRE(W[k] && out[k], "se3_fwd_fused: null %s weights or output", kind[k]);
+    GEO_REQUIRE((reinterpret_cast<uintptr_t>(W[k]) & 15) == 0,
+                "se3_fwd_fused: %s weights must be 16-byte aligned", kind[k]);
+    GEO_REQUIRE(rows[k] >= (O[k] + 15) / 16 * 16, "se3_fwd_fused: %s weights have %d rows, need %d",
+                kind[k], rows[k], (O[k] + 15) / 16 * 16);
+  }
+  SeFused p{};
+  const size_t lds = fused_layout(Os, Ov, Ot, Ks, Kv, Kt, &p);
+  GEO_REQUIRE(lds > 0 || (Os == 0 && Ov == 0 && Ot == 0),
+              "se3_fwd_fused: aggregate tile exceeds %d bytes of LDS (use the unfused path)",
+              kFuLdsMax);
+  if (N == 0 || lds == 0) return GEO_OK;
+  GEO_REQUIRE(node_start && node_end && (E == 0 || (row && dir && Y && R)),
+              "se3_fwd_fused: null graph array");
+  for (int k = 0; k < 3; ++k) {
+    p.W[k] = W[k];
+    p.out[k] = out[k];
+  }
+  p.X[0] = Xs;
+  p.X[1] = Xv;
+  p.X[2] = Xt;
+  p.avg = avg;
+  p.bias = bias;
+  p.mask = mask;
+  SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  SeFeat f{s, v, t, Cs, Cv, Ct};
+  const bool t2 = Ct > 0 || Ot > 0 || path_cols[5] >= 0 || path_cols[6] >= 0 ||
+                  path_cols[7] >= 0 || path_cols[8] >= 0;
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kFuTile)));
+  hipStream_t st = as_stream(stream);
+  if (fused_rows_ok(N, Cs, Cv, t2, E, P, ysh))
+    hipLaunchKernelGGL((se3_fwd_fused_rows<4>), grid, dim3(kSeThreads), lds, st, g, f, p);
+  else if (t2)
+    hipLaunchKernelGGL((se3_fwd_fused<true, 4>), grid, dim3(kSeThreads), lds, st, g, f, p);
+  else
+    hipLaunchKernelGGL((se3_fwd_fused<false, 8>), grid, dim3(kSeThreads), lds, st, g, f, p);
+  GEO_LAUNCH_CHECK("se3_fwd_fused");
   return GEO_OK;
 }
 

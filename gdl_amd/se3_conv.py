@@ -135,6 +135,11 @@ def _plan_of(s: Tensor, v: Tensor, t: Optional[Tensor], Y: Tensor, R: Tensor, di
                  Y.shape[1], Ot > 0)
 
 
+def _fused(p: _Plan) -> bool:
+    """True when the forward runs as one fused launch (its aggregate tile fits in LDS)."""
+    return _nat.lib().geo_se3_fwd_fused_lds_bytes(p.Os, p.Ov, p.Ot, p.Ks, p.Kv, p.Kt) > 0
+
+
 def _u8(mask: Optional[Tensor]) -> Optional[Tensor]:
     return None if mask is None else mask.view(torch.uint8)
 
@@ -155,32 +160,47 @@ def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Ten
                 w5: Optional[Tensor], w6: Optional[Tensor], w7: Optional[Tensor],
                 w8: Optional[Tensor]) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(s_out, v_out, t_out, Xs, Xv, Xt): outputs and the per-node aggregates (kept for the
-    backward; empty when their output is not computed)."""
+    weight gradients when ``dims[12]`` is 1; empty when not kept or their output is not
+    computed)."""
     W = (w0, w1, w2, w3, w4, w5, w6, w7, w8)
     p = _plan_of(s, v, t, Y, R, dims)
+    keep = len(dims) <= 12 or int(dims[12]) != 0
     dev = s.device
     N, E = s.shape[0], row.shape[0]
     f32 = dict(dtype=torch.float32, device=dev)
-    Xs = torch.empty(N, p.Ks, **f32) if p.Os > 0 else None
-    Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 else None
-    Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 else None
     mask_u8 = _u8(mask)
     with _nat.on_device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
-        _nat.check(L.geo_se3_aggregate_fwd(
-            _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, p.Cs, p.Cv, p.Ct, _nat.ptr(row), _nat.ptr(perm),
-            _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh,
-            _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(Xs), p.Ks, _nat.ptr(Xv), p.Kv,
-            _nat.ptr(Xt), p.Kt, st), "geo_se3_aggregate_fwd")
+        fused = _fused(p)
+        keep = keep or not fused
+        Xs = torch.empty(N, p.Ks, **f32) if p.Os > 0 and keep else None
+        Xv = torch.empty(N, 3, p.Kv, **f32) if p.Ov > 0 and keep else None
+        Xt = torch.empty(N, 5, p.Kt, **f32) if p.Ot > 0 and keep else None
         Ws, Wv, Wt = _pack(p, W, [(0, _pad64(p.Os), p.Ks), (1, _pad64(p.Ov), p.Kv),
                                   (2, _pad64(p.Ot), p.Kt)], dev)
         s_out = torch.empty(N, p.Os, **f32)
         v_out = torch.empty(N, p.Ov, 3, **f32)
         t_out = torch.empty(N, p.Ot, 5, **f32)
-        _gemm(Xs, N, p.Ks, Ws, p.Os, 1, s_out, p.Os, avg, bias, mask_u8)
-        _gemm(Xv, 3 * N, p.Kv, Wv, p.Ov, 3, v_out, 3 * p.Ov, avg, None, mask_u8)
-        _gemm(Xt, 5 * N, p.Kt, Wt, p.Ot, 5, t_out, 5 * p.Ot, avg, None, mask_u8)
+        if fused:
+            # one launch: aggregates in LDS, weights applied there (aggregates to HBM only if kept)
+            _nat.check(L.geo_se3_fwd_fused(
+                _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, p.Cs, p.Cv, p.Ct, _nat.ptr(row),
+                _nat.ptr(perm), _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction),
+                _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(Ws),
+                Ws.shape[0], _nat.ptr(Wv), Wv.shape[0], _nat.ptr(Wt), Wt.shape[0], p.Os, p.Ov, p.Ot,
+                p.Ks, p.Kv, p.Kt, _nat.ptr(avg), _nat.ptr(bias), _nat.ptr(mask_u8), _nat.ptr(s_out),
+                _nat.ptr(v_out), _nat.ptr(t_out), _nat.ptr(Xs), _nat.ptr(Xv), _nat.ptr(Xt), st),
+                "geo_se3_fwd_fused")
+        else:
+            _nat.check(L.geo_se3_aggregate_fwd(
+                _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, p.Cs, p.Cv, p.Ct, _nat.ptr(row),
+                _nat.ptr(perm), _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction),
+                _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(Xs), p.Ks,
+                _nat.ptr(Xv), p.Kv, _nat.ptr(Xt), p.Kt, st), "geo_se3_aggregate_fwd")
+            _gemm(Xs, N, p.Ks, Ws, p.Os, 1, s_out, p.Os, avg, bias, mask_u8)
+            _gemm(Xv, 3 * N, p.Kv, Wv, p.Ov, 3, v_out, 3 * p.Ov, avg, None, mask_u8)
+            _gemm(Xt, 5 * N, p.Kt, Wt, p.Ot, 5, t_out, 5 * p.Ot, avg, None, mask_u8)
     empty = s.new_empty(_EMPTY, dtype=torch.float32)
     return (s_out, v_out, t_out, Xs if Xs is not None else empty,
             Xv if Xv is not None else empty.clone(), Xt if Xt is not None else empty.clone())
@@ -190,12 +210,13 @@ def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Ten
 def _se3_fwd_fake(s, v, t, row, col, perm, node_start, node_end, direction, Y, R, avg, mask, bias,
                   cg, dims, w0, w1, w2, w3, w4, w5, w6, w7, w8):
     p = _plan_of(s, v, t, Y, R, dims)
+    keep = len(dims) <= 12 or int(dims[12]) != 0 or not _fused(p)
     N = s.shape[0]
     f = dict(dtype=torch.float32)
     return (s.new_empty(N, p.Os, **f), s.new_empty(N, p.Ov, 3, **f), s.new_empty(N, p.Ot, 5, **f),
-            s.new_empty(N, p.Ks, **f) if p.Os > 0 else s.new_empty(_EMPTY, **f),
-            s.new_empty(N, 3, p.Kv, **f) if p.Ov > 0 else s.new_empty(_EMPTY, **f),
-            s.new_empty(N, 5, p.Kt, **f) if p.Ot > 0 else s.new_empty(_EMPTY, **f))
+            s.new_empty(N, p.Ks, **f) if p.Os > 0 and keep else s.new_empty(_EMPTY, **f),
+            s.new_empty(N, 3, p.Kv, **f) if p.Ov > 0 and keep else s.new_empty(_EMPTY, **f),
+            s.new_empty(N, 5, p.Kt, **f) if p.Ot > 0 and keep else s.new_empty(_EMPTY, **f))
 
 
 # gradient slots of the backward op: ds, dv, dt, ddir, dY, dR, dbias, dW0 .. dW8
@@ -223,6 +244,10 @@ def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tens
     Xt = Xt if p.Ot > 0 else None
     need_s, need_v, need_t, need_dir, need_Y, need_R, need_bias = need[:7]
     need_W = need[7:16]
+    if any(need_W[i] and p.pc[i] >= 0 for i in range(9)) and any(
+            X is not None and X.dim() == 1 for X in (Xs, Xv, Xt)):
+        raise RuntimeError("se3_conv_bwd: weight gradients need the per-node aggregates, which the "
+                           "forward kept only if a weight required gradients under grad mode")
     with _nat.on_device(dev):
         L = _nat.lib()
         st = _nat.stream_of(dev)
@@ -432,7 +457,10 @@ def se3_message_aggregate(
     if max(pc) >= P:
         raise ValueError(f"se3_message_aggregate: {max(pc) + 1} paths run but R has {P} columns")
     Ot = Ct2_out if (return_type2 and Ct2_out > 0) else 0
-    dims = [int(Cs_out), int(Cv_out), int(Ot), *pc]
+    # the per-node aggregates go to HBM only when a weight gradient will need them
+    keep = torch.is_grad_enabled() and any(w is not None and w.requires_grad
+                                           for w in weights.values())
+    dims = [int(Cs_out), int(Cv_out), int(Ot), *pc, int(keep)]
     cg = None
     if pc[7] >= 0:
         cg = (cg_11_2.to(device=dev, dtype=f32).contiguous() if cg_11_2 is not None

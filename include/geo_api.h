@@ -429,6 +429,34 @@ int geo_se3_aggregate_fwd(const float* s, const float* v, const float* t, int64_
                           const int32_t* path_cols, const float* cg, float* Xs, int32_t Ks,
                           float* Xv, int32_t Kv, float* Xt, int32_t Kt, void* stream);
 /*
+ * The forward of one SE3Conv layer from the radial weights on (se3_conv.py:482-566) in one
+ * launch: the per-node sums of geo_se3_aggregate_fwd for a tile of 16 target nodes are kept in
+ * LDS and multiplied there by the packed weights (fp32 MFMA) with the epilogue of geo_se3_gemm:
+ *   s_out[n][o]    = e(n, sum_k Xs[n][k] Ws[o][k]) + bias[o]      o < Os
+ *   v_out[n][o][k] = e(n, sum_j Xv[n][k][j] Wv[o][j])             o < Ov, k < 3
+ *   t_out[n][o][m] = e(n, sum_j Xt[n][m][j] Wt[o][j])             o < Ot, m < 5
+ * with e(n, x) = x / avg[n] (avg may be NULL), 0 where mask[n] == 0 (mask may be NULL; bias may
+ * be NULL).  Ws / Wv / Wt: the packed weight blocks of geo_se3_pack_weights (kinds 0-2), 16-byte
+ * aligned, at least 16 * ceil(O / 16) rows of Ks / Kv / Kt floats (multiples of 16, at least
+ * Cs+Cv+Ct / Cs+2Cv / Cs+Ct+Cv).  A kind with O = 0 is skipped (its pointers may be NULL).
+ * Xs / Xv / Xt, when not NULL, also receive the aggregate rows in geo_se3_aggregate_fwd's layout
+ * (the weight gradients need them).  Other arguments as geo_se3_aggregate_fwd.  The tile must
+ * fit 64 KiB of LDS: geo_se3_fwd_fused_lds_bytes returns its size, or 0 when it does not fit
+ * (then run geo_se3_aggregate_fwd and geo_se3_gemm).  No reference counterpart as one call: it
+ * replaces the message tensor, segment_reduce and output mixing of se3_conv.py:486-566.
+ */
+size_t geo_se3_fwd_fused_lds_bytes(int32_t Os, int32_t Ov, int32_t Ot, int32_t Ks, int32_t Kv,
+                                   int32_t Kt);
+int geo_se3_fwd_fused(const float* s, const float* v, const float* t, int64_t N, int32_t Cs,
+                      int32_t Cv, int32_t Ct, const int64_t* row, const int32_t* perm,
+                      const int32_t* node_start, const int32_t* node_end, int64_t E,
+                      const float* dir, const float* Y, int32_t ysh, const float* R, int32_t P,
+                      const int32_t* path_cols, const float* cg, const float* Ws, int32_t Ws_rows,
+                      const float* Wv, int32_t Wv_rows, const float* Wt, int32_t Wt_rows,
+                      int32_t Os, int32_t Ov, int32_t Ot, int32_t Ks, int32_t Kv, int32_t Kt,
+                      const float* avg, const float* bias, const uint8_t* mask, float* s_out,
+                      float* v_out, float* t_out, float* Xs, float* Xv, float* Xt, void* stream);
+/*
  * fp32 MFMA GEMM with the SE3Conv output epilogue (se3_conv.py:547-566): for r < M, o < O,
  *   v = sum_k A[r, k] B[o, k];  v = v / avg[n] (avg may be NULL);  v += bias[o] (may be NULL);
  *   v = 0 where mask[n] == 0 (mask may be NULL);  out[n * out_stride + o * G + g] = v,

@@ -46,6 +46,17 @@ def test_workspace_sizes():
     assert L.geo_csr_workspace_bytes(-1, 5) == 0
 
 
+def test_se3_fused_tile_size_rule():
+    """The fused SE3 forward runs when 16 nodes' aggregate rows (K + 4 floats each; 1 / 3 / 5 rows
+    per node for the present output kinds) fit 64 KiB of LDS; larger layers take the two-kernel
+    path (geo_se3_aggregate_fwd + geo_se3_gemm)."""
+    L = _native.lib()
+    assert L.geo_se3_fwd_fused_lds_bytes(64, 16, 0, 80, 96, 96) == 4 * 16 * (84 + 3 * 100)
+    assert L.geo_se3_fwd_fused_lds_bytes(70, 10, 4, 112, 128, 112) == 0      # 69,888 bytes
+    assert L.geo_se3_fwd_fused_lds_bytes(0, 16, 0, 80, 96, 96) == 4 * 16 * 3 * 100
+    assert L.geo_se3_fwd_fused_lds_bytes(-1, 16, 0, 80, 96, 96) == 0
+
+
 def _err(rc, fragment):
     assert rc != 0
     assert fragment in _native.last_error(), _native.last_error()
@@ -69,6 +80,18 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     # the no-allocation CSR build refuses more edges than its fixed scratch holds
     _err(L.geo_csr_build_noalloc(8, (1 << 20) + 1, 4, 8, 8, 8, 8, nul), "exceed")
     _err(L.geo_csr_build_noalloc(nul, 10, 4, 8, 8, 8, 8, nul), "null edge")
+    # fused SE3 forward: row length not a multiple of 16, weights without enough rows, and a
+    # tile beyond 64 KiB of LDS
+    pc = (ctypes.c_int32 * 9)(*([-1] * 9))
+
+    def fused(Os, Ks, Ws_rows, W=16):
+        return L.geo_se3_fwd_fused(nul, nul, nul, 10, 0, 0, 0, nul, nul, nul, nul, 0, nul, nul, 1,
+                                   nul, 1, pc, nul, W, Ws_rows, nul, 0, nul, 0, Os, 0, 0, Ks, 16, 16,
+                                   nul, nul, nul, 8, nul, nul, nul, nul, nul, nul)
+    _err(fused(4, 20, 16), "multiple of 16")
+    _err(fused(20, 16, 16), "rows, need 32")
+    _err(fused(4, 16, 16, W=4), "16-byte aligned")
+    _err(fused(4, 1024, 16), "exceeds")
 
 
 def test_workspace_too_small_is_reported():

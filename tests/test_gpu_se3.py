@@ -351,3 +351,117 @@ def test_se3conv_run_to_run_bitwise(dev, type2):
         else:
             for i, (a, b) in enumerate(zip(got, outs_ref)):
                 assert torch.equal(a, b), (rep, i)
+
+
+# Fused forward (aggregate tile in LDS, weights applied there) against the two-kernel path
+# (geo_se3_aggregate_fwd + geo_se3_gemm): both add a node's edges in CSR order with the same
+# per-edge arithmetic and the same MFMA k order, so outputs and kept aggregates are bit-identical.
+FUSED_CONFIGS = [
+    # Cs, Cv, Ct, Os, Ov, Ot
+    (64, 16, 0, 64, 16, 0),    # the C2 layer
+    (8, 4, 0, 8, 4, 0),
+    (96, 8, 0, 40, 8, 0),      # two 64-channel chunks, three scalar column blocks
+    (12, 6, 0, 10, 5, 3),      # type-2 output from scalars and vectors only
+    (5, 0, 2, 4, 0, 3),
+    (0, 4, 0, 3, 2, 0),
+    (16, 4, 3, 16, 4, 2),      # every path
+    (60, 13, 0, 33, 7, 0),     # one node per 16-lane row: partial lanes in both kinds
+    (64, 0, 0, 32, 0, 0),      # scalars only
+    (4, 1, 0, 5, 3, 0),
+]
+
+
+def _abi_forward(cfg, gr, s, v, t, W, R, bias, mask, fused, keep, dev):
+    import ctypes
+    from gdl_amd import _native as nat
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _cg_on, _gemm, _pack, _pad64, path_columns
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    N, E = gr.N, gr.E
+    pc = path_columns(W, t is not None, True, Ot)
+    p = _Plan(Cs, Cv, Ct, Os, Ov, Ot, pc, R.shape[1], gr.Y.shape[1], Ot > 0)
+    Wl = [W[k] for k in PATH_NAMES]
+    Ws, Wv, Wt = _pack(p, Wl, [(0, _pad64(p.Os), p.Ks), (1, _pad64(p.Ov), p.Kv),
+                               (2, _pad64(p.Ot), p.Kt)], dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    so = torch.full((N, Os), float("nan"), **f32)
+    vo = torch.full((N, Ov, 3), float("nan"), **f32)
+    to = torch.full((N, Ot, 5), float("nan"), **f32)
+    Xs = torch.full((N, p.Ks), float("nan"), **f32) if Os > 0 and keep else None
+    Xv = torch.full((N, 3, p.Kv), float("nan"), **f32) if Ov > 0 and keep else None
+    Xt = torch.full((N, 5, p.Kt), float("nan"), **f32) if Ot > 0 and keep else None
+    perm = None if getattr(gr, "_perm_identity", False) else gr.perm
+    cg = _cg_on(dev) if pc[7] >= 0 else None
+    avg, mask_u8 = gr.avg_degree, mask.view(torch.uint8)
+    L, st = nat.lib(), nat.stream_of(dev)
+    common = (nat.ptr(s), nat.ptr(v), nat.ptr(t), N, Cs, Cv, Ct, nat.ptr(gr.row), nat.ptr(perm),
+              nat.ptr(gr.node_start), nat.ptr(gr.node_end), E, nat.ptr(gr.direction), nat.ptr(gr.Y),
+              gr.Y.shape[1], nat.ptr(R), R.shape[1], p.pc_c, nat.ptr(cg))
+    if fused:
+        assert L.geo_se3_fwd_fused_lds_bytes(Os, Ov, Ot, p.Ks, p.Kv, p.Kt) > 0
+        nat.check(L.geo_se3_fwd_fused(
+            *common, nat.ptr(Ws), Ws.shape[0], nat.ptr(Wv), Wv.shape[0], nat.ptr(Wt), Wt.shape[0],
+            Os, Ov, Ot, p.Ks, p.Kv, p.Kt, nat.ptr(avg), nat.ptr(bias), nat.ptr(mask_u8),
+            nat.ptr(so), nat.ptr(vo), nat.ptr(to), nat.ptr(Xs), nat.ptr(Xv), nat.ptr(Xt), st),
+            "geo_se3_fwd_fused")
+    else:
+        nat.check(L.geo_se3_aggregate_fwd(*common, nat.ptr(Xs), p.Ks, nat.ptr(Xv), p.Kv,
+                                          nat.ptr(Xt), p.Kt, st), "geo_se3_aggregate_fwd")
+        _gemm(Xs, N, p.Ks, Ws, Os, 1, so, Os, avg, bias, mask_u8)
+        _gemm(Xv, 3 * N, p.Kv, Wv, Ov, 3, vo, 3 * Ov, avg, None, mask_u8)
+        _gemm(Xt, 5 * N, p.Kt, Wt, Ot, 5, to, 5 * Ot, avg, None, mask_u8)
+    torch.cuda.synchronize()
+    return (so, vo, to), (Xs, Xv, Xt)
+
+
+@pytest.mark.parametrize("cfg", FUSED_CONFIGS, ids=[str(c) for c in FUSED_CONFIGS])
+@pytest.mark.parametrize("graph", ["sorted", "shuffled", "dense"])
+def test_fused_forward_bitwise_vs_two_kernel_path(dev, cfg, graph):
+    """Also covers partial tiles (N = 600 and 250 are not multiples of 16), nodes without edges,
+    and (dense: K = 100) nodes whose edges fill more than one 64-edge staging round."""
+    if graph == "dense":
+        gr = _graph(250, 1, 0.45, 100, 7, False)
+        assert int((gr.node_end - gr.node_start).max()) > 64
+    else:
+        gr = _graph(300, 2, 0.22, 24, sum(cfg), graph == "shuffled")
+    s, v, t, W, R, bias, mask = _inputs(cfg, gr, 3, dev)
+    s, v, R, mask = s.to(dev), v.to(dev), R.to(dev), mask.to(dev)
+    t = t.to(dev) if t is not None else None
+    bias = bias.to(dev) if bias is not None else None
+    W = {k: (w.to(dev) if w is not None else None) for k, w in W.items()}
+    print(f"[se3 fused] cfg={cfg} graph={graph} N={gr.N} E={gr.E}", flush=True)
+    want, Xw = _abi_forward(cfg, gr, s, v, t, W, R, bias, mask, False, True, dev)
+    got, Xg = _abi_forward(cfg, gr, s, v, t, W, R, bias, mask, True, True, dev)
+    got0, _ = _abi_forward(cfg, gr, s, v, t, W, R, bias, mask, True, False, dev)
+    for a, b, c in zip(got, got0, want):
+        assert torch.isfinite(c).all()
+        assert torch.equal(a, c) and torch.equal(b, c)
+    for a, b in zip(Xg, Xw):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cfg", FUSED_CONFIGS + [CONFIGS[2]], ids=[str(c) for c in FUSED_CONFIGS + [CONFIGS[2]]])
+def test_forward_without_grad_vs_oracle(dev, cfg):
+    """Under no_grad nothing keeps the aggregates: the fused forward writes only the outputs."""
+    from gdl_amd.se3_conv import se3_message_aggregate
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    gr = _graph(300, 2, 0.22, 24, sum(cfg) + 3, True)
+    s, v, t, W, R, bias, mask = _inputs(cfg, gr, 4, dev)
+    Wg = {k: (w.to(dev).requires_grad_(True) if w is not None else None) for k, w in W.items()}
+    with torch.no_grad():
+        outs = se3_message_aggregate(s.to(dev), v.to(dev), gr, R.to(dev), Wg, Os, Ov, Ot,
+                                     type2=t.to(dev) if t is not None else None,
+                                     bias=bias.to(dev) if bias is not None else None,
+                                     mask=mask.to(dev), return_type2=True)
+    Wc = {k: (w.double() if w is not None else None) for k, w in W.items()}
+    want = ose3.se3_conv(s.double(), v.double(), t.double() if t is not None else None,
+                         gr.row.cpu(), gr.col.cpu(), gr.direction.cpu().double(),
+                         gr.Y.cpu().double(), R.double(), Wc, ose3.cg_11_2_cartesian(), Os, Ov, Ot,
+                         gr.avg_degree.cpu(), bias=bias.double() if bias is not None else None,
+                         mask=mask)
+    for o, w in zip(outs, want):
+        if w is None:
+            assert o is None or o.numel() == 0
+            continue
+        _close(o, w, 2e-4, 2e-5)

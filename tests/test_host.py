@@ -83,6 +83,11 @@ def test_se3_and_radial_custom_ops_fake_kernels():
                              g.Y, R, g.avg_degree, None, conv.scalar_bias, conv.cg_11_2, dims, *W)
         assert [tuple(x.shape) for x in f] == [(N, 6), (N, 3, 3), (N, 2, 5), (N, 16), (N, 3, 16),
                                                (N, 5, 16)]
+        # keep flag 0 (no weight gradient to come): the fused forward returns no aggregates
+        f0 = ops.se3_conv_fwd(s, v, t, g.row, g.col, None, g.node_start, g.node_end, g.direction,
+                              g.Y, R, g.avg_degree, None, conv.scalar_bias, conv.cg_11_2,
+                              dims + [0], *W)
+        assert [tuple(x.shape) for x in f0] == [(N, 6), (N, 3, 3), (N, 2, 5), (0,), (0,), (0,)]
         for need in ([True] * 16, [False] * 16, [True, False] * 8):
             out = ops.se3_conv_bwd(f[0], f[1], f[2], s, v, t, g.row, g.col, None, g.node_start,
                                    g.node_end, g.direction, g.Y, R, g.avg_degree, None,
