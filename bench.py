@@ -180,7 +180,7 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
     from gdl_amd.csrc import edge_geometry_hip
     from gdl_amd.functional.gather import gather_weighted_sum, idw_weights
     from gdl_amd.functional.segment_softmax import segment_softmax
-    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pad16, path_columns
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _pack, _pad16, _pad64, path_columns
 
     def entry(us, nbytes, gathered=None):
         gbs = nbytes / (us * 1e-6) / 1e9
@@ -241,6 +241,30 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
         us, N * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4,
         E * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * (plan.Ks + 3 * plan.Kv) * 4)
     assert _pad16(Cs + 2 * Cv) == plan.Kv
+    # the whole forward in one launch (aggregates in LDS, weights applied there): what
+    # SE3Conv.forward runs when no weight gradient is wanted
+    Os, Ov = plan.Os, plan.Ov
+    Ws, Wv, _ = _pack(plan, [weights[k] for k in PATH_NAMES],
+                      [(0, _pad64(Os), plan.Ks), (1, _pad64(Ov), plan.Kv), (2, 0, plan.Kt)], dev)
+    s_out = torch.empty(N, Os, device=dev)
+    v_out = torch.empty(N, Ov, 3, device=dev)
+    avg = gr.avg_degree.contiguous()
+    bias = conv.scalar_bias.detach().contiguous()
+    assert lib.geo_se3_fwd_fused_lds_bytes(Os, Ov, 0, plan.Ks, plan.Kv, plan.Kt) > 0
+
+    def fused():
+        nat.check(lib.geo_se3_fwd_fused(
+            nat.ptr(s_), nat.ptr(v_), None, N, Cs, Cv, 0, nat.ptr(gr.row), None,
+            nat.ptr(gr.node_start), nat.ptr(gr.node_end), E, nat.ptr(d), nat.ptr(Y), 9, nat.ptr(R),
+            P, plan.pc_c, None, nat.ptr(Ws), Ws.shape[0], nat.ptr(Wv), Wv.shape[0], None, 0, Os, Ov,
+            0, plan.Ks, plan.Kv, plan.Kt, nat.ptr(avg), nat.ptr(bias), None, nat.ptr(s_out),
+            nat.ptr(v_out), None, None, None, None, st), "fused forward")
+
+    us = 1e3 * event_ms(fused, args.iters, 5)
+    w_bytes = (Ws.numel() + Wv.numel()) * 4
+    out["se3_fwd_fused_64s16v"] = entry(
+        us, N * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * 4 + w_bytes + N * (Os + 3 * Ov) * 4,
+        E * (Cs + 3 * Cv) * 4 + per_edge + 2 * N * 4 + N * 4 + w_bytes + N * (Os + 3 * Ov) * 4)
     return out
 
 

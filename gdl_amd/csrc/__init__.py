@@ -126,7 +126,9 @@ def radius_graph_csr_hip(
     called after each launch of the emit pass into bound-sized scratch (cap rows, the first E of
     them the graph), before the host waits for E, with the cloud size ppc that pass assumed (0
     for clouds given by a batch vector of any layout); it is not called when the graph is too
-    large for bound-sized scratch."""
+    large for bound-sized scratch.  When its last call returns True (the caller keeps views of
+    bound-sized buffers of its own), row and col are views of the scratch whatever E is, instead
+    of exact-sized copies of a sparse graph."""
     _require_gpu("radius_graph", x, mask, batch)
     x = _positions("radius_graph", x)
     dev = x.device
@@ -184,6 +186,7 @@ def radius_graph_csr_hip(
             # emit into bound-sized scratch right behind the count; the host waits only for the
             # count (an event) to learn E, and the first E entries are the graph
             edges_h, counted = _nat.sync_slot(dev)
+            caller_views = False
             for p_arg in ((ppc_try, 0) if ppc_try else (ppc,)):
                 if r_dev is None:
                     args = (_nat.ptr(x), N, _nat.ptr(batch), B, p_arg, _nat.ptr(mask_u8), r2, r, K,
@@ -200,13 +203,13 @@ def radius_graph_csr_hip(
                 _nat.check(emit(*args, _nat.ptr(row_ptr), _nat.ptr(scratch[0]), _nat.ptr(scratch[1]),
                                 _nat.ptr(ws), ws_bytes, s), "geo_radius_emit")
                 if after_emit is not None:
-                    after_emit(scratch[0], scratch[1], row_ptr, N * K, p_arg)
+                    caller_views = bool(after_emit(scratch[0], scratch[1], row_ptr, N * K, p_arg))
                 counted.synchronize()
                 E, bad = edges_h[:2].tolist()
                 if bad == 0:
                     break   # else: batch is not the chunk layout; the general path follows
                 _BATCH_NOT_CHUNKED[batch_key] = batch_key._version
-            if 16 * N * K <= _RADIUS_VIEW_MAX_BYTES and 2 * E >= N * K:
+            if 16 * N * K <= _RADIUS_VIEW_MAX_BYTES and (2 * E >= N * K or caller_views):
                 row, col = scratch[0, :E], scratch[1, :E]
             else:
                 row = torch.empty(E, dtype=torch.int64, device=dev)

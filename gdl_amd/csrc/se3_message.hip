@@ -648,11 +648,12 @@ __device__ __forceinline__ void fused_tile_out(const SeFused& p, const float* ld
   for (int k = 0; k < 3; ++k) {
     const int G = k == 0 ? 1 : (k == 1 ? 3 : 5);
     if (p.O[k] <= 0 || p.X[k] == nullptr || (k == 2 && !T2)) continue;
-    const int64_t rows = min(static_cast<int64_t>(kFuTile), N - node0) * G;
-    const int K = p.K[k];
-    float* dst = p.X[k] + node0 * G * K;
-    for (int64_t i = threadIdx.x; i < rows * K; i += kSeThreads)
-      dst[i] = lds[p.off[k] + (i / K) * p.ld[k] + i % K];
+    const int rows = static_cast<int>(min(static_cast<int64_t>(kFuTile), N - node0)) * G;
+    const int K4 = p.K[k] / 4;  // 16-byte pieces per row (K is a multiple of 16)
+    floatx4* dst = reinterpret_cast<floatx4*>(p.X[k] + node0 * G * p.K[k]);
+    for (int r = wave; r < rows; r += kSeWaves)
+      for (int c = lane; c < K4; c += kWave)
+        dst[r * K4 + c] = *reinterpret_cast<const floatx4*>(lds + p.off[k] + r * p.ld[k] + 4 * c);
   }
   const int nb0 = p.O[0] > 0 ? (p.O[0] + 15) / 16 : 0;
   const int nb1 = p.O[1] > 0 ? 3 * ((p.O[1] + 15) / 16) : 0;
@@ -1700,6 +1701,9 @@ extern "C" int geo_se3_fwd_fused(const float* s, const float* v, const float* t,
   p.X[0] = Xs;
   p.X[1] = Xv;
   p.X[2] = Xt;
+  for (int k = 0; k < 3; ++k)
+    GEO_REQUIRE((reinterpret_cast<uintptr_t>(p.X[k]) & 15) == 0,
+                "se3_fwd_fused: kept %s aggregates must be 16-byte aligned", kind[k]);
   p.avg = avg;
   p.bias = bias;
   p.mask = mask;

@@ -117,7 +117,7 @@ class SpatialGraph:
                 # graph is one cloud for the degree, whatever chunks the radius search used.
                 fused.clear()
                 if ppc_used <= 0:
-                    return
+                    return False
                 deg_ppc = ppc_used if batch is not None else N
                 fbuf = torch.empty(cap * (4 + nsh) + N, dtype=torch.float32, device=dev)
                 ibuf = torch.empty(2 * cap + 2 * N, dtype=torch.int32, device=dev)
@@ -134,6 +134,7 @@ class SpatialGraph:
                             "node_end", "avg")], _nat.stream_of(dev)),
                         "geo_spatial_graph_epilogue_dev")
                 fused.update(f)
+                return True   # the graph keeps views of bound-sized fields: row / col may be too
 
         row, col, row_ptr, B = radius_graph_csr_hip(
             pos, radius, max_num_neighbors=max_num_neighbors, batch=batch, mask=mask,

@@ -439,8 +439,8 @@ int geo_se3_aggregate_fwd(const float* s, const float* v, const float* t, int64_
  * be NULL).  Ws / Wv / Wt: the packed weight blocks of geo_se3_pack_weights (kinds 0-2), 16-byte
  * aligned, at least 16 * ceil(O / 16) rows of Ks / Kv / Kt floats (multiples of 16, at least
  * Cs+Cv+Ct / Cs+2Cv / Cs+Ct+Cv).  A kind with O = 0 is skipped (its pointers may be NULL).
- * Xs / Xv / Xt, when not NULL, also receive the aggregate rows in geo_se3_aggregate_fwd's layout
- * (the weight gradients need them).  Other arguments as geo_se3_aggregate_fwd.  The tile must
+ * Xs / Xv / Xt, when not NULL (16-byte aligned), also receive the aggregate rows in
+ * geo_se3_aggregate_fwd's layout (the weight gradients need them).  Other arguments as geo_se3_aggregate_fwd.  The tile must
  * fit 64 KiB of LDS: geo_se3_fwd_fused_lds_bytes returns its size, or 0 when it does not fit
  * (then run geo_se3_aggregate_fwd and geo_se3_gemm).  No reference counterpart as one call: it
  * replaces the message tensor, segment_reduce and output mixing of se3_conv.py:486-566.
