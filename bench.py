@@ -268,6 +268,39 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
     return out
 
 
+def _se3_two_kernel_forward(conv, fs, fv, gr, dev):
+    """The SE3Conv forward of a layer as the two-kernel path runs it (per-node aggregates to HBM,
+    then the MFMA GEMMs; what layers too large for the fused kernel take), through the C entry
+    points with the layer's weights and radial weights: for counters beside the fused forward."""
+    from gdl_amd import _native as nat
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _gemm, _pack, _pad64, path_columns
+    weights = {k: getattr(conv, k).weight if getattr(conv, k) is not None else None for k in PATH_NAMES}
+    pc = path_columns(weights, False, True, 0)
+    with torch.no_grad():
+        R = conv.radial_basis(gr.dist)
+    Cs, Cv, N, E = fs.shape[1], fv.shape[1], gr.N, gr.E
+    plan = _Plan(Cs, Cv, 0, conv.out_scalar_channels, conv.out_vector_channels, 0, pc, R.shape[1],
+                 gr.Y.shape[1], False)
+    Ws, Wv, _ = _pack(plan, [weights[k] for k in PATH_NAMES],
+                      [(0, _pad64(plan.Os), plan.Ks), (1, _pad64(plan.Ov), plan.Kv), (2, 0, plan.Kt)],
+                      dev)
+    Xs = torch.empty(N, plan.Ks, device=dev)
+    Xv = torch.empty(N, 3, plan.Kv, device=dev)
+    s_out = torch.empty(N, plan.Os, device=dev)
+    v_out = torch.empty(N, plan.Ov, 3, device=dev)
+    bias = conv.scalar_bias.detach().contiguous()
+
+    def fn():
+        nat.check(nat.lib().geo_se3_aggregate_fwd(
+            nat.ptr(fs), nat.ptr(fv), None, N, Cs, Cv, 0, nat.ptr(gr.row), None,
+            nat.ptr(gr.node_start), nat.ptr(gr.node_end), E, nat.ptr(gr.direction), nat.ptr(gr.Y),
+            gr.Y.shape[1], nat.ptr(R), R.shape[1], plan.pc_c, None, nat.ptr(Xs), plan.Ks,
+            nat.ptr(Xv), plan.Kv, None, 0, nat.stream_of(dev)), "geo_se3_aggregate_fwd")
+        _gemm(Xs, N, plan.Ks, Ws, plan.Os, 1, s_out, plan.Os, gr.avg_degree, bias, None)
+        _gemm(Xv, 3 * N, plan.Kv, Wv, plan.Ov, 3, v_out, 3 * plan.Ov, gr.avg_degree, None, None)
+    return fn
+
+
 def wall_ms(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
@@ -818,7 +851,8 @@ def leg_c5(args, dev) -> dict:
 # ═══════════════════════════════════════════════════════════════════
 
 PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "radius_c5_all", "c3sum",
-                "c3max", "c3sum_bf16", "softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2",
+                "c3max", "c3sum_bf16", "softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "radial_c2",
+                "gather_c2",
                 "csr_c3_sorted", "csr_c3_shuffled", "csr_c2", "sparse_softmax_c2")
 
 
@@ -885,7 +919,7 @@ def profile_leg(name: str, args, dev) -> dict:
                                 num_batch_elements=c2["B"])
         scores = torch.randn(col.numel(), 4, device=dev)
         fn = lambda: sparse_softmax(scores, col, pos.shape[0])  # noqa: E731
-    elif name in ("softmax_c2", "se3_aggregate_c2", "radial_c2", "gather_c2"):
+    elif name in ("softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "radial_c2", "gather_c2"):
         from gdl_amd.graph import SpatialGraph
         gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
                                 num_batch_elements=c2["B"])
@@ -909,6 +943,8 @@ def profile_leg(name: str, args, dev) -> dict:
             fv = torch.randn(gr.N, 16, 3, device=dev)
             if name == "radial_c2":
                 fn = lambda: conv.radial_basis(gr.dist)  # noqa: E731
+            elif name == "se3_unfused_c2":
+                fn = _se3_two_kernel_forward(conv, fs, fv, gr, dev)
             else:
                 def fn():
                     with torch.no_grad():
