@@ -236,6 +236,81 @@ __device__ __forceinline__ int cell16(float p, float lo, float scale) {
 }
 
 
+// order[q] = local index of the cloud's q-th point along the Hilbert curve of a 16^3 cell grid
+// over the cloud's bounding box (LDS counting sort by cell; the order within a cell follows the
+// atomics, which only changes which bucket a point joins, never a result).  hist holds kCells
+// ints, red 6 x (THREADS / 64) words, code_rank 8 n and order 4 n bytes; ends behind a barrier.
+template <int THREADS>
+__device__ void fps_hilbert_order(const float* __restrict__ P, int n, int* hist,
+                                  uint32_t (*red)[THREADS / kWave], int2* code_rank, int* order) {
+  constexpr int WAVES = THREADS / kWave;
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = lane_id();
+  // 1. bounding box of the cloud
+  {
+    uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
+    for (int i = t; i < n; i += THREADS) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        const uint32_t kk = float_order_key(P[3 * i + a]);
+        mn[a] = min(mn[a], kk);
+        mx[a] = max(mx[a], kk);
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      mn[a] = wave_min_u32(mn[a]);
+      mx[a] = wave_max_u32(mx[a]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
+    }
+    for (int i = t; i < kCells; i += THREADS) hist[i] = 0;
+    __syncthreads();
+  }
+  float lo[3], scale[3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    uint32_t m0 = red[a][0], m1 = red[3 + a][0];
+    for (int ww = 1; ww < WAVES; ++ww) { m0 = min(m0, red[a][ww]); m1 = max(m1, red[3 + a][ww]); }
+    lo[a] = float_from_order_key(m0);
+    const float ext = float_from_order_key(m1) - lo[a];
+    scale[a] = ext > 0.f ? 16.f / ext : 0.f;
+  }
+
+  // 2. counting sort by Hilbert cell: int2 (code, rank) per point, then the order
+  for (int i = t; i < n; i += THREADS) {
+    const int cx = cell16(P[3 * i], lo[0], scale[0]);
+    const int cy = cell16(P[3 * i + 1], lo[1], scale[1]);
+    const int cz = cell16(P[3 * i + 2], lo[2], scale[2]);
+    const int code = static_cast<int>(hilbert3(cx, cy, cz, kCellBits));
+    code_rank[i] = make_int2(code, atomicAdd(&hist[code], 1));
+  }
+  __syncthreads();
+  {  // exclusive scan of hist in place: thread t owns kCells / THREADS consecutive cells
+    constexpr int PER = kCells / THREADS;
+    int v[PER], s = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { v[j] = hist[t * PER + j]; s += v[j]; }
+    const int incl = wave_inclusive_sum_int(s);
+    __syncthreads();
+    if (lane == kWave - 1) red[0][w] = static_cast<uint32_t>(incl);
+    __syncthreads();
+    int off = incl - s;
+    for (int ww = 0; ww < w; ++ww) off += static_cast<int>(red[0][ww]);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { hist[t * PER + j] = off; off += v[j]; }
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += THREADS) {
+    const int2 cr = code_rank[i];
+    order[hist[cr.x] + cr.y] = i;
+  }
+  __syncthreads();
+}
+
 template <int PTS, int THREADS>
 __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
     const float* __restrict__ pos, const int64_t* __restrict__ ptr,
@@ -273,70 +348,10 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   }
   const float* P = pos + start * 3;
 
-  // 1. bounding box of the cloud
-  {
-    uint32_t mn[3] = {~0u, ~0u, ~0u}, mx[3] = {0u, 0u, 0u};
-    for (int i = t; i < n; i += THREADS) {
-#pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        const uint32_t kk = float_order_key(P[3 * i + a]);
-        mn[a] = min(mn[a], kk);
-        mx[a] = max(mx[a], kk);
-      }
-    }
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      mn[a] = wave_min_u32(mn[a]);
-      mx[a] = wave_max_u32(mx[a]);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int a = 0; a < 3; ++a) { red[a][w] = mn[a]; red[3 + a][w] = mx[a]; }
-    }
-    for (int i = t; i < kCells; i += THREADS) hist[i] = 0;
-    __syncthreads();
-  }
-  float lo[3], scale[3];
-#pragma unroll
-  for (int a = 0; a < 3; ++a) {
-    uint32_t m0 = red[a][0], m1 = red[3 + a][0];
-    for (int ww = 1; ww < WAVES; ++ww) { m0 = min(m0, red[a][ww]); m1 = max(m1, red[3 + a][ww]); }
-    lo[a] = float_from_order_key(m0);
-    const float ext = float_from_order_key(m1) - lo[a];
-    scale[a] = ext > 0.f ? 16.f / ext : 0.f;
-  }
-
-  // 2. counting sort by Hilbert cell: int2 (code, rank) at [0, 8n), order at [8n, 12n)
+  // 1-2. the cloud ordered along the Hilbert curve of its cell grid
   int2* code_rank = reinterpret_cast<int2*>(table);
   int* order = reinterpret_cast<int*>(reinterpret_cast<char*>(table) + 8 * static_cast<size_t>(n));
-  for (int i = t; i < n; i += THREADS) {
-    const int cx = cell16(P[3 * i], lo[0], scale[0]);
-    const int cy = cell16(P[3 * i + 1], lo[1], scale[1]);
-    const int cz = cell16(P[3 * i + 2], lo[2], scale[2]);
-    const int code = static_cast<int>(hilbert3(cx, cy, cz, kCellBits));
-    code_rank[i] = make_int2(code, atomicAdd(&hist[code], 1));
-  }
-  __syncthreads();
-  {  // exclusive scan of hist in place: thread t owns kCells / THREADS consecutive cells
-    constexpr int PER = kCells / THREADS;
-    int v[PER], s = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) { v[j] = hist[t * PER + j]; s += v[j]; }
-    const int incl = wave_inclusive_sum_int(s);
-    __syncthreads();
-    if (lane == kWave - 1) red[0][w] = static_cast<uint32_t>(incl);
-    __syncthreads();
-    int off = incl - s;
-    for (int ww = 0; ww < w; ++ww) off += static_cast<int>(red[0][ww]);
-#pragma unroll
-    for (int j = 0; j < PER; ++j) { hist[t * PER + j] = off; off += v[j]; }
-  }
-  __syncthreads();
-  for (int i = t; i < n; i += THREADS) {
-    const int2 cr = code_rank[i];
-    order[hist[cr.x] + cr.y] = i;
-  }
-  __syncthreads();
+  fps_hilbert_order<THREADS>(P, n, hist, red, code_rank, order);
 
   // 3. registers.  Bucket j = 64 consecutive sorted points; wave w owns buckets w, w+WAVES, ...
   //    (neighbouring buckets on different waves, so the buckets near a centroid spread over
