@@ -1220,10 +1220,11 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(s);
 }
 
-// Lane 0 of a row turns the 21 per-edge sums into the edge's gradients of R, the direction and Y.
+// Lane 0 of a row turns the 21 per-edge sums into the edge's gradients of R, the direction and Y
+// (without T2 only S[0..15] are read).
 template <bool T2>
 __device__ __forceinline__ void write_edge_grads(const SeEdges& g, const EdgeScalars& q,
-                                                 const float S[21], float* dR, float* ddir,
+                                                 const float* S, float* dR, float* ddir,
                                                  float* dY) {
   const int64_t e = q.e;
   const float* d = q.d;
@@ -1405,6 +1406,97 @@ __global__ __launch_bounds__(kSeThreads, T2 ? 1 : 6) void se3_bwd_edge(SeEdges g
   }
 }
 
+// Per-edge gradients for layers without type-2 paths, Cs <= 64 (a multiple of 4), Cv <= 16 (the target's
+// gradient row in registers, as se3_bwd_edge<true, false>): the same sums in the same order, with
+// the source rows read by buffer loads whose offsets point past the arrays for channels a lane
+// does not hold (zeros), so no load carries a per-lane condition, and U steps of four edges
+// (row r: edge j0 + 4 u + r) in flight.
+template <int U>
+__global__ __launch_bounds__(kSeThreads, 6) void se3_bwd_edge_rows(SeEdges g, SeFeat f,
+                                                                  const float* __restrict__ Gs,
+                                                                  int Ks,
+                                                                  const float* __restrict__ Gv,
+                                                                  int Kv, float* __restrict__ dR,
+                                                                  float* __restrict__ ddir,
+                                                                  float* __restrict__ dY) {
+  const int64_t n = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
+  if (n >= g.N) return;
+  const int lane = lane_id();
+  const int row = lane >> 4, li = lane & 15;
+  int a, b;
+  node_range(g, n, a, b);
+  GRow G;
+  load_grow<false>(G, f, nullptr, n, 0, li, Gs, Ks, Gv, Kv, nullptr, 0);
+  const auto rs = row_rsrc(f.s, static_cast<int>(g.N * f.Cs * 4));
+  const auto rv = row_rsrc(f.v, static_cast<int>(g.N * f.Cv * 12));
+  // byte offset of the lane's scalar channels 4 li .. 4 li + 3 inside a row (Cs is a multiple of
+  // 4), or past the arrays
+  const uint32_t cs = 4 * li < f.Cs ? 16u * li : kPastRows;
+  const uint32_t cv = li < f.Cv ? 12u * li : kPastRows;
+  for (int base = a; base < b; base += kWave) {
+    const int cnt = min(kWave, b - base);
+    const EdgeScalars st = stage_edges(g, base, cnt, lane);
+    for (int j0 = 0; j0 < cnt; j0 += 4 * U) {
+      float x[U][4], v[U][3];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {  // every step's source rows first
+        const int jj = j0 + 4 * u + row;
+        // the shuffles run on every lane: a lane shuffle under a condition reads zeros from
+        // source lanes the condition switched off (the staging lane of an edge sits in another row)
+        const int src = __shfl(st.other, min(jj, kWave - 1), kWave);
+        const int okl = __shfl(st.ok, min(jj, kWave - 1), kWave);
+        const bool ok = jj < cnt && okl != 0;
+        const uint32_t ms = ok ? static_cast<uint32_t>(src) * (4u * f.Cs) : kPastRows;
+        const uint32_t mv = ok ? static_cast<uint32_t>(src) * (12u * f.Cv) : kPastRows;
+        const auto xs = __builtin_amdgcn_raw_buffer_load_b128(rs, cs == kPastRows ? kPastRows : ms + cs,
+                                                              0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[u][q] = __uint_as_float(xs[q]);  // element by value
+        const uint32_t vo = cv == kPastRows ? kPastRows : mv + cv;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) v[u][k] = ld_row(rv, vo + 4u * k);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int jj = j0 + 4 * u + row;
+        if (j0 + 4 * u >= cnt) break;  // wave-uniform
+        float S[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (4 * li + q < f.Cs) {
+            S[0] += G.s0[q] * x[u][q];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) S[1 + k] += G.s1[k][q] * x[u][q];
+          }
+        }
+        if (li < f.Cv) {
+          const float* w = v[u];
+          S[9] += (G.v2[0] * w[0] + G.v2[1] * w[1]) + G.v2[2] * w[2];
+#pragma unroll
+          for (int k = 0; k < 3; ++k) S[10 + k] += G.v3 * w[k];
+          S[13] += w[1] * G.v4[2] - w[2] * G.v4[1];  // v x G4
+          S[14] += w[2] * G.v4[0] - w[0] * G.v4[2];
+          S[15] += w[0] * G.v4[1] - w[1] * G.v4[0];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < 4 || i >= 9) S[i] = row_total(S[i]);
+        const EdgeScalars q = edge_from(st, min(jj, kWave - 1));
+        // without the type-2 paths write_edge_grads reads S[0..15] only
+        if (li == 0 && jj < cnt && q.ok) write_edge_grads<false>(g, q, S, dR, ddir, dY);
+      }
+    }
+  }
+}
+
+// Whether se3_bwd_edge_rows covers the call, with both feature arrays below 2 GiB.
+bool bwd_edge_rows_ok(int64_t N, int Cs, int Cv, bool t2) {
+  const int64_t lim = int64_t{1} << 31;
+  return !t2 && Cs <= 64 && Cs % 4 == 0 && Cv <= 16 && N * Cs * 4 < lim && N * Cv * 12 < lim;
+}
+
 // Source-side sums of the output-gradient rows (edges grouped by source m; the wave's lanes
 // run over output channels, the target's rows are gathered per edge, four edges in flight):
 //   Zs[m]    = [Z0 (Os) | Z1 (Ov) | Z5 (Ot)]                 -> ds = Zs [W0|W1|W5]
@@ -1540,6 +1632,126 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
       if (!(q < Os && gs)) Z8[m * KZ8 + q] = 0.f;
 }
 
+
+// Source-side sums in the row layout of se3_fwd_fused_rows (layers without type-2 paths,
+// Os <= 64, Ov <= 16): a wave takes four sources, one per 16-lane row, over the CSR of the
+// sources; lane j holds scalar-gradient channels 4j..4j+3 (one 16-byte load of the target's
+// prepared row) and vector channel j (one dword per component row), so the gradient rows of four
+// edges cost four vector-memory instructions where the channel-per-lane walk above issues four
+// per edge.  Same products, in the same order, as se3_bwd_src.
+template <int U>
+__global__ __launch_bounds__(kSeThreads) void se3_bwd_src_rows(SeEdges g, const float* __restrict__ gs,
+                                                              int Os, int OsP,
+                                                              const float* __restrict__ gv, int Ov,
+                                                              int OvP, float* __restrict__ Zs,
+                                                              int KZs, float* __restrict__ Zv,
+                                                              int KZv) {
+  const int lane = lane_id();
+  const int j = lane & 15;
+  const int64_t m = (xcd_block() * kSeWaves + uniform(threadIdx.x / kWave)) * kRowNodes + (lane >> 4);
+  int a = 0, b = 0;
+  if (m < g.N) node_range(g, m, a, b);
+  const int deg = b - a;
+  const int maxdeg = max(max(__builtin_amdgcn_readlane(deg, 0), __builtin_amdgcn_readlane(deg, 16)),
+                         max(__builtin_amdgcn_readlane(deg, 32), __builtin_amdgcn_readlane(deg, 48)));
+  // whole-array resources (each below 2 GiB, checked by the host); an absent kind reads zeros
+  const auto rs = row_rsrc(gs, gs ? static_cast<int>(g.N * OsP * 4) : 0);
+  const auto rv = row_rsrc(gv, gv ? static_cast<int>(g.N * 3 * OvP * 4) : 0);
+  const uint32_t rowb_s = 4u * OsP, rowb_v = 12u * OvP, kb = 4u * OvP;
+  const uint32_t js = 16u * j, jv = 4u * j;
+  float z0[4] = {0.f, 0.f, 0.f, 0.f}, z3[3][4] = {};
+  float z1 = 0.f, z2[3] = {0.f, 0.f, 0.f}, z4[3] = {0.f, 0.f, 0.f};
+  for (int base = 0; base < maxdeg; base += kRowStage) {
+    const EdgeCoef<false> st = stage_rows(g, a + base + j, base + j < deg);
+    const int cnt = min(kRowStage, maxdeg - base);
+    static_for<0, kRowStage / U>([&](auto ci) {
+      constexpr int c0 = decltype(ci)::value * U;
+      if (c0 >= cnt) return;
+      float sx[U][4], vx[U][3];
+      static_for<0, U>([&](auto ui) {  // the U gradient rows of every row in flight together
+        constexpr int uu = decltype(ui)::value;
+        constexpr int u = c0 + uu;
+        const bool have = row_bcast<u>(st.ok) != 0;
+        const uint32_t n = static_cast<uint32_t>(row_bcast<u>(st.other));
+        const auto ls = __builtin_amdgcn_raw_buffer_load_b128(rs, have ? n * rowb_s + js : kPastRows,
+                                                              0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sx[uu][i] = __uint_as_float(ls[i]);  // element by value
+        const uint32_t vo = have ? n * rowb_v + jv : kPastRows;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          vx[uu][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, vo + k * kb, 0, 0));
+      });
+      static_for<0, U>([&](auto ui) {
+        constexpr int uu = decltype(ui)::value;
+        constexpr int u = c0 + uu;
+        const bool ok = row_bcast<u>(st.ok) != 0;  // an absent edge adds nothing
+        float x[4], w[3];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = ok ? sx[uu][i] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) w[k] = ok ? vx[uu][k] : 0.f;
+        const float c0v = row_bcast<u>(st.c0), c2v = row_bcast<u>(st.c2);
+        float c1[3], c3[3], c4[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          c1[k] = row_bcast<u>(st.c1[k]);
+          c3[k] = row_bcast<u>(st.c3[k]);
+          c4[k] = row_bcast<u>(st.c4[k]);
+        }
+        if (gs) {  // an absent kind leaves its sums at zero, as se3_bwd_src does
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            z0[i] += c0v * x[i];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) z3[k][i] += c3[k] * x[i];
+          }
+        }
+        if (gv) {
+          z1 += (c1[0] * w[0] + c1[1] * w[1]) + c1[2] * w[2];
+#pragma unroll
+          for (int k = 0; k < 3; ++k) z2[k] += c2v * w[k];
+          z4[0] += w[1] * c4[2] - w[2] * c4[1];  // w x (r4 d)
+          z4[1] += w[2] * c4[0] - w[0] * c4[2];
+          z4[2] += w[0] * c4[1] - w[1] * c4[0];
+        }
+      });
+    });
+  }
+  if (m >= g.N) return;
+  // rows as se3_bwd_src writes them; columns of absent kinds and the padding are zeros
+  if (Zs) {
+    float* row = Zs + m * KZs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * j + i < Os) row[4 * j + i] = z0[i];
+    if (j < Ov) row[Os + j] = z1;
+    for (int q = Os + Ov + j; q < KZs; q += 16) row[q] = 0.f;
+  }
+  if (Zv) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      float* row = Zv + (m * 3 + k) * KZv;
+      if (j < Ov) {
+        row[j] = z2[k];
+        row[Ov + Os + j] = z4[k];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * j + i < Os) row[Ov + 4 * j + i] = z3[k][i];
+      for (int q = 2 * Ov + Os + j; q < KZv; q += 16) row[q] = 0.f;
+    }
+  }
+}
+
+// Whether se3_bwd_src_rows covers the call, with every array it reads through a buffer
+// resource below 2 GiB.
+bool bwd_src_rows_ok(int64_t N, int Os, int OsP, int Ov, int OvP, bool t2, int64_t E, int P,
+                     int ysh) {
+  const int64_t lim = int64_t{1} << 31;
+  return !t2 && Os <= 64 && Ov <= 16 && OsP % 4 == 0 && N * OsP * 4 < lim &&
+         N * 3 * OvP * 4 < lim && E * 12 < lim && E * P * 4 < lim && E * ysh * 4 < lim;
+}
 
 SeEdges make_edges(const int64_t* other, const int32_t* perm, const int32_t* ns, const int32_t* ne,
                    int64_t N, int64_t E, const float* dir, const float* Y, int ysh, const float* R,
@@ -1761,6 +1973,12 @@ extern "C" int geo_se3_bwd_edge(const float* s, const float* v, const float* t, 
 #define GEO_BWD_EDGE(ONE_, T2_)                                                                    \
   hipLaunchKernelGGL((se3_bwd_edge<ONE_, T2_>), grid, dim3(kSeThreads), 0, st, g, f, gXs, Ks, gXv, Kv, \
                      gXt, Kt, dR, ddir, dY)
+  if (bwd_edge_rows_ok(N, Cs, Cv, t2)) {
+    hipLaunchKernelGGL((se3_bwd_edge_rows<1>), grid, dim3(kSeThreads), 0, st, g, f, gXs, Ks, gXv, Kv,
+                       dR, ddir, dY);
+    GEO_LAUNCH_CHECK("se3_bwd_edge_rows");
+    return GEO_OK;
+  }
   if (one && t2) GEO_BWD_EDGE(true, true);
   else if (one) GEO_BWD_EDGE(true, false);
   else if (t2) GEO_BWD_EDGE(false, true);
@@ -1790,6 +2008,15 @@ extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const f
   GEO_REQUIRE(node_start && node_end && (E == 0 || (col && dir && Y && R)),
               "se3_bwd_src: null graph array");
   SeEdges g = make_edges(col, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  const bool t2 = (gt != nullptr && Ot > 0) || Zt != nullptr || Z8 != nullptr || path_cols[5] >= 0 ||
+                  path_cols[6] >= 0 || path_cols[7] >= 0 || path_cols[8] >= 0;
+  if (bwd_src_rows_ok(N, Os, OsP, Ov, OvP, t2, E, P, ysh)) {
+    const dim3 grid4(static_cast<unsigned>(ceil_div(N, kSeWaves * kRowNodes)));
+    hipLaunchKernelGGL((se3_bwd_src_rows<4>), grid4, dim3(kSeThreads), 0, as_stream(stream), g, gs,
+                       Os, OsP, gv, Ov, OvP, Zs, KZs, Zv, KZv);
+    GEO_LAUNCH_CHECK("se3_bwd_src_rows");
+    return GEO_OK;
+  }
   const dim3 grid(static_cast<unsigned>(ceil_div(N, kSeWaves)));
   if (gt != nullptr && Ot > 0)
     hipLaunchKernelGGL(se3_bwd_src<true>, grid, dim3(kSeThreads), 0, as_stream(stream), g, gs, Os,
