@@ -87,6 +87,23 @@ _BATCH_NOT_CHUNKED: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
 # pointer.  The graph's edges are already grouped by target in CSR order, so the CSR build of
 # those unchanged targets over the same node count is the row pointer itself: one pass, no sort.
 _TARGETS_ROW_PTR: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
+# the same target tensors -> (version, int32 copy of the row pointer), made on first use by a
+# consumer that needs only the CSR bounds (node_start / node_end are its two shifted views)
+_TARGETS_BOUNDS32: "WeakIdKeyDictionary" = WeakIdKeyDictionary()
+
+
+def target_bounds(col: Tensor, N: int) -> Optional[Tuple[Tensor, Tensor]]:
+    """(node_start, node_end) int32 [N] of a radius graph's unchanged target tensor ``col`` over N
+    nodes: its CSR permutation is the identity, so these and perm = None are the whole CSR.  None
+    for any other index tensor (callers then build the CSR)."""
+    known = _TARGETS_ROW_PTR.get(col)
+    if known is None or known[0] != col._version or known[1].numel() != N + 1:
+        return None
+    b = _TARGETS_BOUNDS32.get(col)
+    if b is None or b[0] != col._version or b[1].numel() != N + 1:
+        b = (col._version, known[1].to(torch.int32))  # E < 2^31: the CSR arrays are int32
+        _TARGETS_BOUNDS32[col] = b
+    return b[1][:-1], b[1][1:]
 
 
 def radius_graph_hip(

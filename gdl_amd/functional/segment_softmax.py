@@ -23,6 +23,7 @@ from gdl_amd.csrc import (
     segment_softmax_backward_hip,
     segment_softmax_forward_hip,
     sort_and_build_csr_cuda,
+    target_bounds,
 )
 
 
@@ -74,6 +75,9 @@ def segment_softmax(
 
 def sparse_softmax(scores: Tensor, index: Tensor, num_nodes: int) -> Tensor:
     """Softmax over sparse edges grouped by target node (reference argument order)."""
+    bounds = target_bounds(index, int(num_nodes)) if isinstance(index, Tensor) else None
+    if bounds is not None:  # a radius graph's targets: its row pointer is the CSR, perm identity
+        return segment_softmax(scores, None, bounds[0], bounds[1], num_nodes, contiguous_csr=True)
     _, perm, node_start, node_end = sort_and_build_csr_cuda(index, int(num_nodes))
     return segment_softmax(scores, perm, node_start, node_end, num_nodes, contiguous_csr=True)
 

@@ -255,3 +255,35 @@ def test_segment_softmax_contiguous_csr_short_segments(dev, H, kind):
     assert np.all(np.abs(got[ok] - ref[ok]) <= 2e-6 + 1e-5 * np.abs(ref[ok]))
     if tail:
         assert np.all(w[perm[seg_of_pos >= N].numpy()] == 0)
+
+
+@pytest.mark.parametrize("H", [1, 4])
+def test_sparse_softmax_of_radius_graph_targets(dev, H):
+    """sparse_softmax over a radius graph's own target tensor takes the graph's row pointer as the
+    CSR (identity permutation, no CSR build): bit-identical to the same targets through the CSR
+    build, forward and backward, and against the oracle; an in-place change of the targets
+    drops back to the CSR build."""
+    from gdl_amd.csrc import target_bounds
+    from gdl_amd.functional.radius_graph import radius_graph
+    _, sparse_softmax = _ops()
+    g = torch.Generator().manual_seed(3)
+    pos = torch.rand(3000, 3, generator=g).to(dev)
+    row, col = radius_graph(pos, 0.08, max_num_neighbors=20)
+    N, E = pos.shape[0], col.numel()
+    assert target_bounds(col, N) is not None and target_bounds(col.clone(), N) is None
+    x = torch.randn(E, H, generator=g, dtype=torch.float64).float().to(dev)
+    xa = x.clone().requires_grad_(True)
+    xb = x.clone().requires_grad_(True)
+    wa = sparse_softmax(xa, col, N)
+    wb = sparse_softmax(xb, col.clone(), N)
+    assert torch.equal(wa, wb)
+    gr = torch.randn(E, H, generator=g).to(dev)
+    wa.backward(gr)
+    wb.backward(gr)
+    assert torch.equal(xa.grad, xb.grad)
+    _check(wa, oracle.sparse_softmax(x.double().cpu().numpy(), col.cpu().numpy(), N), torch.float32)
+    col_mod = col
+    col_mod[0] = col_mod[-1]  # in place: the cached row pointer no longer describes it
+    assert target_bounds(col_mod, N) is None
+    w2 = sparse_softmax(x, col_mod, N)
+    assert torch.equal(w2, sparse_softmax(x, col_mod.clone(), N))
