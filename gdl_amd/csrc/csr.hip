@@ -51,6 +51,8 @@ __global__ __launch_bounds__(kRxThreads) void csr_bounds_runs(const int32_t* __r
 
 // Thread n in [0, N] computes lb(n) by binary search over the sorted keys; runs only when
 // *active is set (a wave found gaps too long to write).
+constexpr int64_t kCsrBoundsGrid = 256;  // workgroups of the fallback bounds kernel
+
 __global__ void csr_bounds(const int32_t* __restrict__ sorted_keys, int64_t E, int64_t N,
                            int32_t* __restrict__ node_start, int32_t* __restrict__ node_end,
                            const uint32_t* __restrict__ active) {
@@ -211,9 +213,11 @@ int csr_build_into(const int64_t* col, int64_t E, int64_t N, int32_t* col_sorted
                        dim3(kRxThreads), 0, st, col_sorted, E, N, node_start, node_end, w.aux,
                        w.unsorted, ptiles);
     GEO_LAUNCH_CHECK("csr_bounds_runs");
+    // the fallback runs only when a wave's keys spanned too many nodes; it strides over the
+    // nodes, so a small grid does its work and costs little when it only reads its flag
     const int64_t nblocks = ceil_div(N + 1, 256);
-    hipLaunchKernelGGL(csr_bounds, dim3(nblocks < 1024 ? nblocks : 1024), dim3(256), 0, st,
-                       col_sorted, E, N, node_start, node_end, w.aux);
+    hipLaunchKernelGGL(csr_bounds, dim3(nblocks < kCsrBoundsGrid ? nblocks : kCsrBoundsGrid),
+                       dim3(256), 0, st, col_sorted, E, N, node_start, node_end, w.aux);
     GEO_LAUNCH_CHECK("csr_bounds");
   }
   return GEO_OK;
