@@ -103,67 +103,196 @@ __device__ __forceinline__ float sigmoid(float z) {
 }
 __device__ __forceinline__ float silu(float z) { return z * sigmoid(z); }
 
+// A buffer resource over the `count` floats at p (none when count <= 0): loads past the end read
+// 0 and stores past the end are dropped, so a tile's edge and output bounds need no branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rb_rsrc(const float* p, int64_t count) {
+  const int bytes = count <= 0 ? 0 : static_cast<int>(4 * count);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, bytes, 0x00020000);
+}
+
+// Distance of edge e0 + li (e0 wave-uniform); 0 for edges at or past E (their basis values are
+// 0 and their outputs are not stored).  The loaded value is returned as it is, so the wait for it
+// falls where the next tile first uses it, not in the tile that issued the load.
+__device__ __forceinline__ float rb_dist(const RbParams& p, int64_t e0, int li) {
+  const int64_t left = p.E - e0;
+  const auto rs = rb_rsrc(left > 0 ? p.dist + e0 : p.dist, left > 16 ? 16 : left);
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 4u * li, 0, 0));
+}
+
+// Tiles whose sine and cosine arguments (f d and pi d / cutoff) are all below kRbFastArg in
+// magnitude -- every edge of a radius graph -- evaluate the basis without per-call range checks.
+constexpr float kRbFastArg = 1000.f;
+
+// x[q] = x_{4g+q}(d), the lane's four basis values.  When every lane of the wave passes the
+// argument test (a wave-uniform branch), the hardware sine and cosine are called directly and
+// 1 / max(d, 1e-8) comes from the hardware reciprocal (within 1 ulp); a column past NB has
+// f = 0 and so the value 0.  Other tiles take the range-checked functions.
+__device__ __forceinline__ void rb_basis_fwd(const float* fr, int NB, int g, float pic, float d,
+                                             float* x) {
+  const float t = pic * d;
+  float a[4];
+  bool fast = fabsf(t) < kRbFastArg;  // false for NaN
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    a[q] = fr[q] * d;
+    fast &= fabsf(a[q]) < kRbFastArg;
+  }
+  if (__ballot(!fast) == 0ull) {
+    const float e = 0.5f * (1.0f + __builtin_amdgcn_cosf(t * kInv2Pi));
+    const float env = e < 0.f ? 0.f : e;
+    const float rdc = __builtin_amdgcn_rcpf(d < 1e-8f ? 1e-8f : d);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = (__builtin_amdgcn_sinf(a[q] * kInv2Pi) * rdc) * env;
+  } else {
+    float env, denv;
+    envelope(d, pic, env, denv);
+    const float rdc = rb_rdc(d);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = 4 * g + q < NB ? basis(fr[q], d, rdc, env, denv, nullptr) : 0.f;
+  }
+}
+
+// Weights of the forward in MFMA operand layout (see the header), per lane.
+struct RbFwdWeights {
+  float w1[4][4], b1r[4][4], w2[4][4], fr[4], b2r[4];
+};
+
+// One 16-edge tile of the forward: R[e0 + li][4g + q] from the lane's distance d.  (Measured
+// with the counters: the matrix core and the vector ALU do not run at the same time in this
+// kernel -- no co-executed cycles -- so its time is close to the sum of the two; this is why the
+// tile keeps the VALU work per edge small rather than interleaving it with the MFMAs.)
+__device__ __forceinline__ void rb_fwd_tile(const RbParams& p, const RbFwdWeights& w, float pic,
+                                            int g, int li, int64_t e0, float d,
+                                            float* __restrict__ R) {
+  float x[4];
+  rb_basis_fwd(w.fr, p.NB, g, pic, d, x);
+  // the biases start the accumulators: Z^T = b1 + W1 X^T, R^T = b2 + W2 H^T
+  floatx4 h[4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    floatx4 z = {w.b1r[jb][0], w.b1r[jb][1], w.b1r[jb][2], w.b1r[jb][3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) z = mfma4(w.w1[jb][q], x[q], z);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[jb][q] = silu(z[q]);
+  }
+  floatx4 r = {w.b2r[0], w.b2r[1], w.b2r[2], w.b2r[3]};
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r = mfma4(w.w2[c][q], h[c][q], r);
+  // lanes past E and outputs >= P store nothing (out of the resource)
+  const int64_t left = p.E - e0;
+  const auto rs = rb_rsrc(R + e0 * p.P, (left > 16 ? 16 : left) * p.P);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int pp = 4 * g + q;
+    const uint32_t off = pp < p.P ? 4u * static_cast<uint32_t>(li * p.P + pp) : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(r[q]), rs, off, 0, 0);
+  }
+}
+
 __global__ __launch_bounds__(kRbThreads) void radial_fwd_kernel(RbParams p, float* __restrict__ R) {
   const float pic = 3.14159265358979323846f / p.cutoff;
   const int lane = lane_id();
   const int g = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  float w1[4][4], b1r[4][4], w2[4][4], fr[4], b2r[4];
+  RbFwdWeights w;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int i = 4 * g + q;
-    fr[q] = i < p.NB ? p.freqs[i] : 0.f;
-    b2r[q] = i < p.P ? p.b2[i] : 0.f;
+    w.fr[q] = i < p.NB ? p.freqs[i] : 0.f;
+    w.b2r[q] = i < p.P ? p.b2[i] : 0.f;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
       const int j = 16 * jb + li;
-      w1[jb][q] = (j < p.H && i < p.NB) ? p.W1[j * p.NB + i] : 0.f;      // A of Z^T: W1[j][i]
+      w.w1[jb][q] = (j < p.H && i < p.NB) ? p.W1[j * p.NB + i] : 0.f;      // A of Z^T: W1[j][i]
       const int jj = 16 * jb + 4 * g + q;
-      b1r[jb][q] = jj < p.H ? p.b1[jj] : 0.f;                              // rows of Z^T
-      w2[jb][q] = (li < p.P && jj < p.H) ? p.W2[li * p.H + jj] : 0.f;      // A of R^T: W2[p][j]
+      w.b1r[jb][q] = jj < p.H ? p.b1[jj] : 0.f;                              // rows of Z^T
+      w.w2[jb][q] = (li < p.P && jj < p.H) ? p.W2[li * p.H + jj] : 0.f;      // A of R^T: W2[p][j]
     }
   }
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kRbWaves * 16;
   const int64_t first = (static_cast<int64_t>(blockIdx.x) * kRbWaves + wave) * 16;
-  float d_next = first + li < p.E ? p.dist[first + li] : 1.f;  // distances one tile ahead
-  for (int64_t e0 = first; e0 < p.E; e0 += stride) {
-    const int64_t e = e0 + li;
-    const bool ok = e < p.E;
-    const float d = d_next;
-    d_next = e + stride < p.E ? p.dist[e + stride] : 1.f;
-    float env, denv;
-    envelope(d, pic, env, denv);
-    const float rdc = rb_rdc(d);
-    float x[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) x[q] = 4 * g + q < p.NB ? basis(fr[q], d, rdc, env, denv, nullptr) : 0.f;
-    floatx4 h[4];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      floatx4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) z = mfma4(w1[jb][q], x[q], z);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) h[jb][q] = silu(z[q] + b1r[jb][q]);
-    }
-    // four independent accumulation chains (one per 16-wide hidden chunk), summed at the end
-    floatx4 rc[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) rc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) rc[c] = mfma4(w2[c][q], h[c][q], rc[c]);
-    const floatx4 r = (rc[0] + rc[1]) + (rc[2] + rc[3]);
-    if (ok) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (4 * g + q < p.P) R[e * p.P + 4 * g + q] = r[q] + b2r[q];
-    }
+  // Two tiles per trip, each tile's distances requested one tile ahead into its own register:
+  // the wait for a load falls at the tile that uses it, a whole tile after the request.
+  float da = rb_dist(p, first, li);
+  for (int64_t e0 = first; e0 < p.E; e0 += 2 * stride) {
+    const float db = rb_dist(p, e0 + stride, li);
+    rb_fwd_tile(p, w, pic, g, li, e0, da, R);
+    if (e0 + stride >= p.E) break;  // wave-uniform
+    da = rb_dist(p, e0 + 2 * stride, li);
+    rb_fwd_tile(p, w, pic, g, li, e0 + stride, db, R);
   }
 }
 
-__global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, const float* __restrict__ dR,
+// x_i(d) and dx_i/dd through the range-checked functions, returned by value.
+__device__ __forceinline__ float2 basis_checked(float f, float d, float rdc, float env, float denv) {
+#pragma clang fp contract(off)
+  const float s = rb_sin(f * d);
+  const float b = s * rdc;
+  // d/dd [sin(f d) / dc] = f cos(f d) / dc - [d >= 1e-8] sin(f d) / dc^2
+  const float db = f * rb_cos(f * d) * rdc - (d >= 1e-8f ? b * rdc : 0.f);
+  return make_float2(b * env, db * env + b * denv);
+}
+
+// The lane's four basis values x_{4g+q}(d) and their derivatives in d.
+struct RbBasis {
+  float x[4], dx[4];
+};
+
+// Basis values and derivatives: the fast path as in rb_basis_fwd (wave-uniform), otherwise the
+// range-checked functions.  Returned by value: output pointers into the caller's arrays kept
+// those arrays in scratch memory.
+__device__ __forceinline__ RbBasis rb_basis_bwd(const float* fr, int NB, int g, float pic, float d) {
+  RbBasis r;
+  const float t = pic * d;
+  float a[4];
+  bool fast = fabsf(t) < kRbFastArg;  // false for NaN
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    a[q] = fr[q] * d;
+    fast &= fabsf(a[q]) < kRbFastArg;
+  }
+  if (__ballot(!fast) == 0ull) {
+    const float tr = t * kInv2Pi;
+    const float e = 0.5f * (1.0f + __builtin_amdgcn_cosf(tr));
+    const float env = e < 0.f ? 0.f : e;
+    const float denv = -0.5f * __builtin_amdgcn_sinf(tr) * pic;
+    const bool big = d >= 1e-8f;
+    const float rdc = __builtin_amdgcn_rcpf(big ? d : 1e-8f);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float ar = a[q] * kInv2Pi;
+      const float b = __builtin_amdgcn_sinf(ar) * rdc;
+      const float db = fr[q] * __builtin_amdgcn_cosf(ar) * rdc - (big ? b * rdc : 0.f);
+      r.dx[q] = db * env + b * denv;
+      r.x[q] = b * env;
+    }
+  } else {
+    float env, denv;
+    envelope(d, pic, env, denv);
+    const float rdc = rb_rdc(d);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float2 v = 4 * g + q < NB ? basis_checked(fr[q], d, rdc, env, denv) : make_float2(0.f, 0.f);
+      r.x[q] = v.x;
+      r.dx[q] = v.y;
+    }
+  }
+  return r;
+}
+
+// Backward.  NQP = ceil(P / 4): in the products over the outputs (dH = dR W2) lane group g of MFMA
+// q holds output 4q + g, so only the first NQP of the four k chunks are non-zero and issued
+// (P = 5: 8 of the 16 MFMAs).  Distances and dR rows come through per-tile buffer resources:
+// edges past E read 0 (basis values 0, dR 0), so they add nothing and need no branches.
+// Waves per SIMD of the backward: three fit its registers for P <= 8; more outputs need two.
+template <int NQP>
+constexpr int rb_bwd_waves() { return NQP <= 2 ? 3 : 2; }
+
+template <int NQP>
+__global__ __launch_bounds__(kRbThreads, rb_bwd_waves<NQP>()) void radial_bwd_kernel(RbParams p, const float* __restrict__ dR,
                                                                float* __restrict__ ddist,
                                                                float* __restrict__ part) {
   // The edge-loop transposes (tz, tx) and the final per-wave partials (red) share one LDS buffer
@@ -180,7 +309,7 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
   const int g = lane >> 4, li = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   float fr[4];
-  float w1[4][4], w2b[4][4], w1t[4][4], b1z[4];
+  float w1[4][4], w2b[4][NQP], w1t[4][4], b1z[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int i = 4 * g + q;
@@ -189,7 +318,8 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
     for (int jb = 0; jb < 4; ++jb) {
       const int j = 16 * jb + li;
       w1[jb][q] = (j < p.H && i < p.NB) ? p.W1[j * p.NB + i] : 0.f;   // B of Z = X W1^T
-      w2b[jb][q] = (i < p.P && j < p.H) ? p.W2[i * p.H + j] : 0.f;    // B of dH = dR W2
+      const int po = 4 * q + g;
+      if (q < NQP) w2b[jb][q] = (po < p.P && j < p.H) ? p.W2[po * p.H + j] : 0.f;  // B of dH = dR W2
       const int jj = 16 * jb + 4 * g + q;
       w1t[jb][q] = (jj < p.H && li < p.NB) ? p.W1[jj * p.NB + li] : 0.f;  // A of dX^T = W1^T dZ^T
     }
@@ -205,32 +335,34 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
   }
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kRbWaves * 16;
   for (int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kRbWaves + wave) * 16; e0 < p.E; e0 += stride) {
-    // edge li: x_i, i = 4g + q (A of Z; also the layout of dX^T) and dR[e][4g + q] (A of dH)
-    const int64_t ea = e0 + li;
-    const bool oka = ea < p.E;
-    const float da = oka ? p.dist[ea] : 1.f;
-    float enva, denva;
-    envelope(da, pic, enva, denva);
-    const float rdca = rb_rdc(da);
-    float xa[4], dxa[4], dra[4];
+    const int64_t left = p.E - e0;
+    const int64_t nr = left > 16 ? 16 : left;
+    const auto rsd = rb_rsrc(p.dist + e0, nr);
+    const auto rsg = rb_rsrc(dR + e0 * p.P, nr * p.P);
+    // edge li: x_i, i = 4g + q (A of Z; also the layout of dX^T) and dR[e][4q + g] (A of dH)
+    const float da = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsd, 4u * li, 0, 0));
+    float dra[NQP], drb[4];
+#pragma unroll
+    for (int q = 0; q < NQP; ++q) {
+      const int po = 4 * q + g;
+      const uint32_t off = po < p.P ? 4u * static_cast<uint32_t>(li * p.P + po) : 0x80000000u;
+      dra[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsg, off, 0, 0));
+    }
+    // edges 4g + q: dR[e][li] (A of dW2)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int i = 4 * g + q;
-      xa[q] = i < p.NB ? basis(fr[q], da, rdca, enva, denva, &dxa[q]) : 0.f;
-      if (i >= p.NB) dxa[q] = 0.f;
-      dra[q] = (oka && i < p.P) ? dR[ea * p.P + i] : 0.f;
+      const uint32_t off = li < p.P ? 4u * static_cast<uint32_t>((4 * g + q) * p.P + li) : 0x80000000u;
+      drb[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsg, off, 0, 0));
     }
-    // edges 4g + q: x_li (A of dW1^T, the transpose of xa through LDS) and dR[e][li] (A of dW2)
+    const RbBasis bs = rb_basis_bwd(fr, p.NB, g, pic, da);
+    const float* xa = bs.x;
+    const float* dxa = bs.dx;
+    // edges 4g + q: x_li (A of dW1^T, the transpose of xa through LDS)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) tx[wave][li][4 * g + q] = oka ? xa[q] : 0.f;
-    float xb[4], drb[4];
+    for (int q = 0; q < 4; ++q) tx[wave][li][4 * g + q] = xa[q];
+    float xb[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t eb = e0 + 4 * g + q;
-      const bool okb = eb < p.E;
-      drb[q] = (okb && li < p.P) ? dR[eb * p.P + li] : 0.f;
-      db2p += drb[q];
-    }
+    for (int q = 0; q < 4; ++q) db2p += drb[q];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -238,16 +370,16 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
     for (int q = 0; q < 4; ++q) xb[q] = tx[wave][4 * g + q][li];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
-      floatx4 z = {0.f, 0.f, 0.f, 0.f}, dh = {0.f, 0.f, 0.f, 0.f};
+      // the bias starts the accumulator: Z = b1 + X W1^T
+      floatx4 z = {b1z[jb], b1z[jb], b1z[jb], b1z[jb]}, dh = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        z = mfma4(xa[q], w1[jb][q], z);     // Z[e = 4g + q'][j = 16 jb + li]
-        dh = mfma4(dra[q], w2b[jb][q], dh);  // dH, same layout
-      }
+      for (int q = 0; q < 4; ++q) z = mfma4(xa[q], w1[jb][q], z);     // Z[e = 4g + q'][j = 16 jb + li]
+#pragma unroll
+      for (int q = 0; q < NQP; ++q) dh = mfma4(dra[q], w2b[jb][q], dh);  // dH, same layout
       floatx4 h, dz;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float zz = z[q] + b1z[jb];
+        const float zz = z[q];
         const float sg = sigmoid(zz);
         h[q] = zz * sg;
         dz[q] = dh[q] * (sg * (1.0f + zz * (1.0f - sg)));  // silu'(z) = s (1 + z (1 - s))
@@ -264,21 +396,17 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (ddist) {
-      floatx4 dxc[4];  // four independent accumulation chains, summed at the end
+      floatx4 dx = {0.f, 0.f, 0.f, 0.f};  // dX^T[i = 4g + q][e = li]
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dxc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) dxc[c] = mfma4(w1t[c][q], tz[wave][li][16 * c + 4 * g + q], dxc[c]);
-      const floatx4 dx = (dxc[0] + dxc[1]) + (dxc[2] + dxc[3]);
-      // dX^T[i = 4g + q][e = li]
+        for (int q = 0; q < 4; ++q) dx = mfma4(w1t[c][q], tz[wave][li][16 * c + 4 * g + q], dx);
       float s = 0.f;
 #pragma unroll
       for (int q = 0; q < 4; ++q) s += dx[q] * dxa[q];
       s += __shfl_xor(s, 16, kWave);
       s += __shfl_xor(s, 32, kWave);
-      if (g == 0 && oka) ddist[ea] = s;
+      if (g == 0 && li < nr) ddist[e0 + li] = s;
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -314,26 +442,33 @@ __global__ __launch_bounds__(kRbThreads, 3) void radial_bwd_kernel(RbParams p, c
 }
 
 // Sum of the per-block partials, then scattered into the gradient tensors.  Each block sums 64
-// entries over all partial blocks with four thread groups (group g takes blocks b = g mod 4 in
-// order), then adds the four group sums in order: a fixed order, so results are deterministic.
-__global__ __launch_bounds__(kRbThreads) void radial_bwd_final(const float* __restrict__ part, int nblk,
+// entries over all partial blocks with kRbFinalGroups thread groups (group g takes blocks
+// b = g mod kRbFinalGroups in order), then adds the group sums in order: a fixed order, so results
+// are deterministic.  Sixteen groups keep about 50 independent loads per thread in flight for
+// 768 partial blocks (four groups left the kernel waiting on 192 loads per thread).
+constexpr int kRbFinalGroups = 16;
+constexpr int kRbFinalThreads = 64 * kRbFinalGroups;
+
+__global__ __launch_bounds__(kRbFinalThreads) void radial_bwd_final(const float* __restrict__ part, int nblk,
                                                               int NB, int H, int P,
                                                               float* __restrict__ dW1,
                                                               float* __restrict__ db1,
                                                               float* __restrict__ dW2,
                                                               float* __restrict__ db2) {
-  __shared__ float red[4][64];
+  __shared__ float red[kRbFinalGroups][64];
   const int kl = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + kl;
   float s = 0.f;
   if (k < kRbPart) {
 #pragma unroll 8
-    for (int b = grp; b < nblk; b += 4) s += part[static_cast<int64_t>(b) * kRbPart + k];
+    for (int b = grp; b < nblk; b += kRbFinalGroups) s += part[static_cast<int64_t>(b) * kRbPart + k];
   }
   red[grp][kl] = s;
   __syncthreads();
   if (grp != 0 || k >= kRbPart) return;
-  s = ((red[0][kl] + red[1][kl]) + red[2][kl]) + red[3][kl];
+  s = red[0][kl];
+#pragma unroll
+  for (int gg = 1; gg < kRbFinalGroups; ++gg) s += red[gg][kl];
   if (k < 1024) {
     const int i = k / 64, j = k % 64;
     if (i < NB && j < H && dW1) dW1[j * NB + i] = s;
@@ -609,13 +744,20 @@ extern "C" int geo_radial_mlp_bwd(const float* dist, int64_t E, const float* fre
     GEO_LAUNCH_CHECK("radial_bwd_general_final");
     return GEO_OK;
   }
-  // three waves per SIMD fit the backward: one resident round of 768 blocks on 256 CUs
-  const unsigned nblk = rb_blocks(E) < 768u ? rb_blocks(E) : 768u;
+  // one resident round: three (P <= 8) or two waves per SIMD, 768 or 512 blocks on 256 CUs
+  const unsigned cap = P <= 8 ? 768u : 512u;
+  const unsigned nblk = rb_blocks(E) < cap ? rb_blocks(E) : cap;
   float* part = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(radial_bwd_kernel, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part);
+  switch ((P + 3) / 4) {
+    case 1: hipLaunchKernelGGL(radial_bwd_kernel<1>, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part); break;
+    case 2: hipLaunchKernelGGL(radial_bwd_kernel<2>, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part); break;
+    case 3: hipLaunchKernelGGL(radial_bwd_kernel<3>, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part); break;
+    default: hipLaunchKernelGGL(radial_bwd_kernel<4>, dim3(nblk), dim3(kRbThreads), 0, st, p, dR, d_dist, part); break;
+  }
   GEO_LAUNCH_CHECK("radial_bwd_kernel");
   hipLaunchKernelGGL(radial_bwd_final, dim3(static_cast<unsigned>(ceil_div(kRbPart, 64))),
-                     dim3(kRbThreads), 0, st, part, static_cast<int>(nblk), NB, H, P, dW1, db1, dW2, db2);
+                     dim3(kRbFinalThreads), 0, st, part, static_cast<int>(nblk), NB, H, P, dW1, db1,
+                     dW2, db2);
   GEO_LAUNCH_CHECK("radial_bwd_final");
   return GEO_OK;
 }
