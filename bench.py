@@ -851,8 +851,8 @@ def leg_c5(args, dev) -> dict:
 # ═══════════════════════════════════════════════════════════════════
 
 PROFILE_LEGS = ("fps_c2", "fps_c5", "knn_c2", "knn_c5", "radius_c2", "radius_c5_all", "c3sum",
-                "c3max", "c3sum_bf16", "softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "radial_c2",
-                "gather_c2",
+                "c3max", "c3sum_bf16", "softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "se3_train_c2",
+                "radial_c2", "gather_c2",
                 "csr_c3_sorted", "csr_c3_shuffled", "csr_c2", "sparse_softmax_c2")
 
 
@@ -919,7 +919,8 @@ def profile_leg(name: str, args, dev) -> dict:
                                 num_batch_elements=c2["B"])
         scores = torch.randn(col.numel(), 4, device=dev)
         fn = lambda: sparse_softmax(scores, col, pos.shape[0])  # noqa: E731
-    elif name in ("softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "radial_c2", "gather_c2"):
+    elif name in ("softmax_c2", "se3_fwd_c2", "se3_unfused_c2", "se3_train_c2", "radial_c2",
+                  "gather_c2"):
         from gdl_amd.graph import SpatialGraph
         gr = SpatialGraph.build(pos, c2["r"], max_num_neighbors=c2["K"], batch=batch,
                                 num_batch_elements=c2["B"])
@@ -945,6 +946,16 @@ def profile_leg(name: str, args, dev) -> dict:
                 fn = lambda: conv.radial_basis(gr.dist)  # noqa: E731
             elif name == "se3_unfused_c2":
                 fn = _se3_two_kernel_forward(conv, fs, fv, gr, dev)
+            elif name == "se3_train_c2":  # forward + backward, gradients cleared as in the c2 leg
+                fs.requires_grad_(True)
+                fv.requires_grad_(True)
+
+                def fn():
+                    conv.zero_grad(set_to_none=True)
+                    fs.grad = None
+                    fv.grad = None
+                    so, vo = conv(fs, fv, gr)
+                    torch.autograd.backward((so, vo), (torch.ones_like(so), torch.ones_like(vo)))
             else:
                 def fn():
                     with torch.no_grad():

@@ -95,6 +95,10 @@ _SIGNATURES = {
     "geo_se3_gemm_tn_workspace_bytes": (c_size, [c_i64, c_i32, c_i32]),
     "geo_se3_gemm_tn": (c_int, [c_vp, c_i64, c_i32, c_i32, c_vp, c_i32, c_i32, c_vp, c_i32, c_vp, c_size,
                                 c_vp]),
+    "geo_se3_gemm_tn_split": (c_int, [c_vp, c_i64, c_i32, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                      c_vp, c_size, c_vp]),
+    "geo_se3_colsum_workspace_bytes": (c_size, [c_i64, c_i32]),
+    "geo_se3_colsum": (c_int, [c_vp, c_i64, c_i32, c_vp, c_vp, c_vp, c_size, c_vp]),
     "geo_se3_pack_weights": (c_int, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
                                      c_vp, c_vp, c_vp]),
     "geo_se3_grad_prep": (c_int, [c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),

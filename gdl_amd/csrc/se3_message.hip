@@ -1071,10 +1071,18 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn(const float* __restric
       }
 }
 
+// Destinations of the product's columns: part j (j < n <= 3) covers columns [c[j], c[j+1]) and
+// is written row-major with row stride ld[j] at p[j] (skipped when p[j] is null).
+struct TnOut {
+  int n;
+  int c[4];
+  float* p[3];
+  int ld[3];
+};
+
 __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn_final(const float* __restrict__ part,
                                                                int nparts, int Opad, int Kpad,
-                                                               int O, int K,
-                                                               float* __restrict__ out, int ldo) {
+                                                               int O, int K, TnOut out) {
   __shared__ float red[4][64];
   const int kl = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 64 + kl;
@@ -1088,7 +1096,144 @@ __global__ __launch_bounds__(kSeThreads) void se3_gemm_tn_final(const float* __r
   __syncthreads();
   if (grp != 0 || idx >= n) return;
   const int o = static_cast<int>(idx / Kpad), k = static_cast<int>(idx % Kpad);
-  if (o < O && k < K) out[static_cast<int64_t>(o) * ldo + k] = ((red[0][kl] + red[1][kl]) + red[2][kl]) + red[3][kl];
+  if (o >= O || k >= K) return;
+  int j = 0;
+  while (j + 1 < out.n && k >= out.c[j + 1]) ++j;
+  if (out.p[j] != nullptr)
+    out.p[j][static_cast<int64_t>(o) * out.ld[j] + (k - out.c[j])] =
+        ((red[0][kl] + red[1][kl]) + red[2][kl]) + red[3][kl];
+}
+
+// Column sums of a row-major [N][O] matrix over the rows whose mask byte is non-zero (all rows
+// without a mask), in two launches with a fixed summation order (results reproducible bit for
+// bit).  se3_colsum_part: block b sums rows [b R, (b + 1) R) into part[b][o].  When O is a
+// multiple of 4 and the matrix 16-byte aligned, a lane holds four columns (16-byte loads), the
+// lanes of a 64-column chunk form 16-lane rows, and a wave issues its rows sixteen loads at a time
+// before adding them (16 KB in flight per wave: about one memory round trip for the whole
+// matrix); the four 16-lane rows of a wave and then the four waves are added in order.  Otherwise
+// a thread per column walks every fourth row, eight in flight.  se3_colsum_final adds the block
+// partials, sixteen groups over the blocks, in group order.
+constexpr int kColsumBlocks = 256;
+constexpr int kColsumFinalThreads = 1024;  // 16 groups of 64 columns
+
+template <bool VEC4>
+__global__ __launch_bounds__(kSeThreads) void se3_colsum_part(const float* __restrict__ g,
+                                                             int64_t N, int O,
+                                                             const uint8_t* __restrict__ mask,
+                                                             int64_t R, float* __restrict__ part) {
+  __shared__ float red[kSeWaves][64];
+  const int lane = lane_id(), w = threadIdx.x / kWave;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t r1 = r0 + R < N ? r0 + R : N;
+  if constexpr (VEC4) {
+    // wave w takes rows r0 + 4 w + rr (rr = lane / 16), then every 16th row; lane % 16 = column quad
+    const int cq = lane & 15, rr = lane >> 4;
+    for (int c0 = 0; c0 < O; c0 += 64) {
+      const int o = c0 + 4 * cq;  // first of the lane's four columns
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (o < O) {
+        int64_t r = r0 + 4 * w + rr;
+        for (; r + 15 * 16 < r1; r += 16 * 16) {
+          float4 v[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const int64_t q = r + 16 * k;
+            const float4 x = *reinterpret_cast<const float4*>(g + q * O + o);
+            const bool on = mask == nullptr || mask[q] != 0;
+            v[k] = on ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int k = 0; k < 16; ++k) { s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w; }
+        }
+        for (; r < r1; r += 16) {
+          const float4 x = *reinterpret_cast<const float4*>(g + r * O + o);
+          if (mask == nullptr || mask[r] != 0) { s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w; }
+        }
+      }
+      // the wave's four 16-lane rows, in order: lanes cq, cq + 16, cq + 32, cq + 48
+      float t[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a1 = __shfl(t[k], cq + 16, kWave), a2 = __shfl(t[k], cq + 32, kWave),
+                    a3 = __shfl(t[k], cq + 48, kWave), a0 = __shfl(t[k], cq, kWave);
+        t[k] = ((a0 + a1) + a2) + a3;
+      }
+      if (rr == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) red[w][4 * cq + k] = t[k];
+      }
+      __syncthreads();
+      if (w == 0 && c0 + lane < O) {
+        float u = red[0][lane];
+#pragma unroll
+        for (int ww = 1; ww < kSeWaves; ++ww) u += red[ww][lane];
+        part[static_cast<int64_t>(blockIdx.x) * O + c0 + lane] = u;
+      }
+      __syncthreads();
+    }
+  } else {
+    // a thread per column: wave w takes rows r0 + w, r0 + w + 4, ...
+    for (int c0 = 0; c0 < O; c0 += 64) {
+      const int o = c0 + lane;
+      float s = 0.f;
+      if (o < O) {
+        int64_t r = r0 + w;
+        for (; r + 28 < r1; r += 32) {
+          float v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const int64_t q = r + 4 * k;
+            const float x = g[q * O + o];
+            v[k] = (mask == nullptr || mask[q] != 0) ? x : 0.f;
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) s += v[k];
+        }
+        for (; r < r1; r += 4) {
+          const float x = g[r * O + o];
+          s += (mask == nullptr || mask[r] != 0) ? x : 0.f;
+        }
+      }
+      red[w][lane] = s;
+      __syncthreads();
+      if (w == 0 && o < O) {
+        float u = red[0][lane];
+#pragma unroll
+        for (int ww = 1; ww < kSeWaves; ++ww) u += red[ww][lane];
+        part[static_cast<int64_t>(blockIdx.x) * O + o] = u;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(kColsumFinalThreads) void se3_colsum_final(const float* __restrict__ part,
+                                                                        int nb, int O,
+                                                                        float* __restrict__ out) {
+  constexpr int kGroups = kColsumFinalThreads / 64;
+  __shared__ float red[kGroups][64];
+  const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int o = blockIdx.x * 64 + cl;
+  float s = 0.f;
+  if (o < O) {
+    int b = grp;
+    for (; b + 7 * kGroups < nb; b += 8 * kGroups) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = part[static_cast<int64_t>(b + k * kGroups) * O + o];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += v[k];
+    }
+    for (; b < nb; b += kGroups) s += part[static_cast<int64_t>(b) * O + o];
+  }
+  red[grp][cl] = s;
+  __syncthreads();
+  if (grp == 0 && o < O) {
+    float t = red[0][cl];
+#pragma unroll
+    for (int gg = 1; gg < kGroups; ++gg) t += red[gg][cl];
+    out[o] = t;
+  }
 }
 
 struct TnPlan {
@@ -2035,14 +2180,17 @@ extern "C" size_t geo_se3_gemm_tn_workspace_bytes(int64_t M, int32_t O, int32_t 
   return static_cast<size_t>(t.nparts_x) * Opad * Kpad * sizeof(float);
 }
 
-extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B,
-                               int32_t ldb, int32_t K, float* out, int32_t ldo, void* workspace,
-                               size_t workspace_bytes, void* stream) {
-  GEO_REQUIRE(M >= 0 && O >= 0 && K >= 0 && lda >= O && ldb >= K && ldo >= K,
-              "se3_gemm_tn: bad sizes (M=%lld O=%d K=%d lda=%d ldb=%d ldo=%d)", (long long)M, O, K,
-              lda, ldb, ldo);
+namespace geo {
+namespace {
+
+int gemm_tn_into(const float* A, int64_t M, int32_t lda, int32_t O, const float* B, int32_t ldb,
+                 int32_t K, const TnOut& dst, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  GEO_REQUIRE(M >= 0 && O >= 0 && K >= 0 && lda >= O && ldb >= K,
+              "se3_gemm_tn: bad sizes (M=%lld O=%d K=%d lda=%d ldb=%d)", (long long)M, O, K, lda,
+              ldb);
   if (O == 0 || K == 0) return GEO_OK;
-  GEO_REQUIRE(out && (M == 0 || (A && B)), "se3_gemm_tn: null pointer");
+  GEO_REQUIRE(M == 0 || (A && B), "se3_gemm_tn: null pointer");
   const size_t need = geo_se3_gemm_tn_workspace_bytes(M, O, K);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(GEO_ERR_WORKSPACE, "se3_gemm_tn: workspace %zu bytes, need %zu",
@@ -2064,8 +2212,76 @@ extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O
   const int nparts = t.nparts_x;
   hipLaunchKernelGGL(se3_gemm_tn_final,
                      dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(Opad) * Kpad, 64))),
-                     dim3(kSeThreads), 0, st, part, nparts, Opad, Kpad, O, K, out, ldo);
+                     dim3(kSeThreads), 0, st, part, nparts, Opad, Kpad, O, K, dst);
   GEO_LAUNCH_CHECK("se3_gemm_tn_final");
+  return GEO_OK;
+}
+
+}  // namespace
+}  // namespace geo
+
+extern "C" int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const float* B,
+                               int32_t ldb, int32_t K, float* out, int32_t ldo, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  GEO_REQUIRE(ldo >= K, "se3_gemm_tn: ldo %d < K %d", ldo, K);
+  GEO_REQUIRE(out || O == 0 || K == 0, "se3_gemm_tn: null pointer");
+  TnOut dst{};
+  dst.n = 1;
+  dst.c[0] = 0;
+  dst.c[1] = K;
+  dst.p[0] = out;
+  dst.ld[0] = ldo;
+  return gemm_tn_into(A, M, lda, O, B, ldb, K, dst, workspace, workspace_bytes, stream);
+}
+
+extern "C" int geo_se3_gemm_tn_split(const float* A, int64_t M, int32_t lda, int32_t O,
+                                     const float* B, int32_t ldb, int32_t K, int32_t nsplit,
+                                     const int32_t* cols, float* const* outs, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  GEO_REQUIRE(nsplit >= 1 && nsplit <= 3 && cols && outs, "se3_gemm_tn_split: 1 to 3 parts");
+  GEO_REQUIRE(cols[0] == 0 && cols[nsplit] == K, "se3_gemm_tn_split: parts must cover 0..K");
+  TnOut dst{};
+  dst.n = nsplit;
+  for (int j = 0; j <= nsplit; ++j) dst.c[j] = cols[j];
+  for (int j = 0; j < nsplit; ++j) {
+    GEO_REQUIRE(cols[j + 1] >= cols[j], "se3_gemm_tn_split: part bounds must ascend");
+    dst.p[j] = outs[j];
+    dst.ld[j] = cols[j + 1] - cols[j];
+  }
+  return gemm_tn_into(A, M, lda, O, B, ldb, K, dst, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t geo_se3_colsum_workspace_bytes(int64_t N, int32_t O) {
+  if (N < 0 || O < 0) return 0;
+  return static_cast<size_t>(kColsumBlocks) * static_cast<size_t>(O) * sizeof(float);
+}
+
+extern "C" int geo_se3_colsum(const float* g, int64_t N, int32_t O, const uint8_t* mask, float* out,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  GEO_REQUIRE(N >= 0 && O >= 0, "se3_colsum: bad sizes (N=%lld O=%d)", (long long)N, O);
+  if (O == 0) return GEO_OK;
+  GEO_REQUIRE(out && (N == 0 || g), "se3_colsum: null pointer");
+  hipStream_t st = as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+  int nb = 0;  // N == 0: the final kernel adds no partials and writes zeros
+  if (N > 0) {
+    const size_t need = geo_se3_colsum_workspace_bytes(N, O);
+    if (workspace == nullptr || workspace_bytes < need)
+      return set_error(GEO_ERR_WORKSPACE, "se3_colsum: workspace %zu bytes, need %zu",
+                       workspace_bytes, need);
+    const int64_t R = ceil_div(N, static_cast<int64_t>(kColsumBlocks));
+    if (O % 4 == 0 && (reinterpret_cast<uintptr_t>(g) & 15) == 0)
+      hipLaunchKernelGGL(se3_colsum_part<true>, dim3(kColsumBlocks), dim3(kSeThreads), 0, st, g,
+                         N, O, mask, R, part);
+    else
+      hipLaunchKernelGGL(se3_colsum_part<false>, dim3(kColsumBlocks), dim3(kSeThreads), 0, st, g,
+                         N, O, mask, R, part);
+    GEO_LAUNCH_CHECK("se3_colsum_part");
+    nb = kColsumBlocks;
+  }
+  hipLaunchKernelGGL(se3_colsum_final, dim3(static_cast<unsigned>(ceil_div(static_cast<int64_t>(O), 64))),
+                     dim3(kColsumFinalThreads), 0, st, part, nb, O, out);
+  GEO_LAUNCH_CHECK("se3_colsum_final");
   return GEO_OK;
 }
 

@@ -339,19 +339,28 @@ def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tens
                  ((5, 0, Cs), (6, Cs, Cs + Ct), (7, Cs + Ct, Cs + Ct + Cv)))):
             if Gm is None or not any(need_W[i] and p.pc[i] >= 0 for i, _, _ in parts) or width == 0:
                 continue
-            m = torch.empty(O_, width, **f32)
-            nbytes = L.geo_se3_gemm_tn_workspace_bytes(rows, O_, width)
-            ws = _nat.workspace(nbytes, dev)
-            _nat.check(L.geo_se3_gemm_tn(_nat.ptr(Gm), rows, OP, O_, _nat.ptr(Xm), KX, width,
-                                         _nat.ptr(m), width, _nat.ptr(ws), nbytes, st),
-                       "geo_se3_gemm_tn")
+            # each path's block of the product straight into its own gradient tensor (outputs
+            # of a custom op may not alias each other, so no views of one shared result)
             for i, a, b in parts:
                 if p.pc[i] >= 0 and need_W[i]:
-                    dW[i] = m[:, a:b].clone()   # outputs of a custom op may not alias each other
+                    dW[i] = torch.empty(O_, b - a, **f32)
+            cols = (ctypes.c_int32 * 4)(*[a for _, a, _ in parts], parts[-1][2])
+            outs = (ctypes.c_void_p * 3)(*[dW[i].data_ptr() if dW[i] is not None else None
+                                           for i, _, _ in parts])
+            nbytes = L.geo_se3_gemm_tn_workspace_bytes(rows, O_, width)
+            ws = _nat.workspace(nbytes, dev)
+            _nat.check(L.geo_se3_gemm_tn_split(_nat.ptr(Gm), rows, OP, O_, _nat.ptr(Xm), KX, width,
+                                               len(parts), cols, outs, _nat.ptr(ws), nbytes, st),
+                       "geo_se3_gemm_tn_split")
         dbias = None
         if need_bias and g_s is not None:
-            gm = g_s if mask_u8 is None else g_s * mask_u8.view(N, 1).to(g_s.dtype)
-            dbias = gm.sum(0)
+            # sum over the (unmasked) nodes of the scalar output gradient, in a fixed order
+            dbias = torch.empty(Os, **f32)
+            gc = g_s.to(torch.float32).contiguous()
+            nbytes = L.geo_se3_colsum_workspace_bytes(N, Os)
+            ws = _nat.workspace(nbytes, dev)
+            _nat.check(L.geo_se3_colsum(_nat.ptr(gc), N, Os, _nat.ptr(mask_u8), _nat.ptr(dbias),
+                                        _nat.ptr(ws), nbytes, st), "geo_se3_colsum")
         elif need_bias:
             dbias = torch.zeros(Os, **f32)
     # a requested gradient has its input's shape (zeros where nothing contributes: no channels,

@@ -491,6 +491,25 @@ int geo_se3_gemm_tn(const float* A, int64_t M, int32_t lda, int32_t O, const flo
                     int32_t K, float* out, int32_t ldo, void* workspace, size_t workspace_bytes,
                     void* stream);
 /*
+ * The same product written in column ranges: part j < nsplit (1 to 3) holds columns
+ * [cols[j], cols[j + 1]) (cols[0] = 0, cols[nsplit] = K, ascending) as its own row-major
+ * O x (cols[j + 1] - cols[j]) matrix at outs[j] (NULL: not written), so that the weight gradients
+ * of the paths that share one product land in separate tensors.  Host arrays cols, outs;
+ * workspace as for geo_se3_gemm_tn.
+ */
+int geo_se3_gemm_tn_split(const float* A, int64_t M, int32_t lda, int32_t O, const float* B,
+                          int32_t ldb, int32_t K, int32_t nsplit, const int32_t* cols,
+                          float* const* outs, void* workspace, size_t workspace_bytes,
+                          void* stream);
+/*
+ * Bias gradient: out[o] = sum of g[n * O + o] over the rows n with mask[n] != 0 (every row when
+ * mask is NULL), g row-major [N, O]; rows summed in a fixed order (per-workgroup partials in the
+ * workspace, added in workgroup order), so results are reproducible bit for bit.
+ */
+size_t geo_se3_colsum_workspace_bytes(int64_t N, int32_t O);
+int geo_se3_colsum(const float* g, int64_t N, int32_t O, const uint8_t* mask, float* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+/*
  * Zero-padded weight blocks for geo_se3_gemm, built in one launch from the nine path weights
  * W[p] ([out][in] row-major fp32 device pointers, NULL for absent paths; path order w_ss, w_sv,
  * w_vv_scalar, w_vs, w_vv_cross, w_st2, w_t2t2, w_vt2, w_t2s).  Output j is a rows[j] x cols[j]

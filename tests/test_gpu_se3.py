@@ -70,6 +70,65 @@ def test_gemm_tn_kernel_vs_torch(dev):
         assert torch.isnan(out[:, K:]).all()  # columns past K untouched
 
 
+def test_gemm_tn_split_writes_each_part_bitwise(dev):
+    """geo_se3_gemm_tn_split: the product's column ranges written as separate row-major matrices
+    equal the unsplit result bit for bit (same partials, same order); a NULL part is skipped and
+    its neighbours' memory is untouched."""
+    import ctypes
+    from gdl_amd import _native as nat
+    L = nat.lib()
+    g = torch.Generator().manual_seed(7)
+    for (M, O, K, cuts) in [(65536, 64, 112, (0, 64, 80, 112)), (1000, 16, 40, (0, 16, 40)),
+                            (333, 5, 9, (0, 9)), (4097, 33, 50, (0, 10, 10, 50))]:
+        A = torch.randn(M, O, generator=g).to(dev)
+        B = torch.randn(M, K, generator=g).to(dev)
+        nbytes = L.geo_se3_gemm_tn_workspace_bytes(M, O, K)
+        ws = nat.workspace(nbytes, torch.device(dev))
+        st = nat.stream_of(torch.device(dev))
+        full = torch.empty(O, K, device=dev)
+        nat.check(L.geo_se3_gemm_tn(nat.ptr(A), M, O, O, nat.ptr(B), K, K, nat.ptr(full), K,
+                                    nat.ptr(ws), nbytes, st), "geo_se3_gemm_tn")
+        n = len(cuts) - 1
+        parts = [torch.full((O, cuts[j + 1] - cuts[j]), float("nan"), device=dev) for j in range(n)]
+        skip = n - 1 if n > 1 else -1   # the last part of a multi-part split is not requested
+        cols = (ctypes.c_int32 * (n + 1))(*cuts)
+        outs = (ctypes.c_void_p * n)(*[None if j == skip else parts[j].data_ptr() for j in range(n)])
+        nat.check(L.geo_se3_gemm_tn_split(nat.ptr(A), M, O, O, nat.ptr(B), K, K, n, cols, outs,
+                                          nat.ptr(ws), nbytes, st), "geo_se3_gemm_tn_split")
+        for j in range(n):
+            if j == skip:
+                assert torch.isnan(parts[j]).all()
+            else:
+                assert torch.equal(parts[j], full[:, cuts[j]:cuts[j + 1]])
+
+
+def test_colsum_bias_gradient(dev):
+    """geo_se3_colsum: column sums over the unmasked rows (fixed order: bitwise equal on a
+    repeat), against a float64 sum; N = 0 gives zeros."""
+    from gdl_amd import _native as nat
+    L = nat.lib()
+    g = torch.Generator().manual_seed(9)
+    st = nat.stream_of(torch.device(dev))
+    for (N, O, masked) in [(65536, 64, False), (65536, 64, True), (1000, 130, True), (3, 5, False),
+                           (0, 7, False)]:
+        x = torch.randn(N, O, generator=g)
+        mask = (torch.rand(N, generator=g) > 0.3) if masked else None
+        xd = x.to(dev)
+        md = mask.to(dev).view(torch.uint8) if masked else None
+        nbytes = L.geo_se3_colsum_workspace_bytes(N, O)
+        ws = nat.workspace(nbytes, torch.device(dev))
+        outs = []
+        for _ in range(2):
+            out = torch.full((O,), float("nan"), device=dev)
+            nat.check(L.geo_se3_colsum(nat.ptr(xd), N, O, nat.ptr(md), nat.ptr(out), nat.ptr(ws),
+                                       nbytes, st), "geo_se3_colsum")
+            outs.append(out)
+        assert torch.equal(outs[0], outs[1])
+        want = (x.double() * (mask.double().view(N, 1) if masked else 1.0)).sum(0)
+        scale = x.abs().double().sum(0).clamp(min=1e-30)
+        assert ((outs[0].double().cpu() - want).abs() <= 1e-5 * scale + 1e-30).all()
+
+
 def _graph(N, B, r, K, seed, shuffle):
     from gdl_amd.graph import SpatialGraph
     g = torch.Generator().manual_seed(seed)
