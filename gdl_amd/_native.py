@@ -113,6 +113,10 @@ _SIGNATURES = {
     "geo_se3_bwd_src": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64,
                                 c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp,
                                 c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "geo_se3_bwd_src_fused": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_vp, c_vp, c_vp,
+                                      c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_i32,
+                                      c_i32, c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, c_vp,
+                                      c_vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -164,6 +168,9 @@ def loaded() -> bool:
 def last_error() -> str:
     msg = lib().geo_last_error()
     return msg.decode() if msg else ""
+
+
+GEO_ERR_UNSUPPORTED = 4  # include/geo_api.h: the call declined a case it does not cover
 
 
 def check(rc: int, what: str) -> None:

@@ -1784,13 +1784,19 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src(SeEdges g, const float
 // prepared row) and vector channel j (one dword per component row), so the gradient rows of four
 // edges cost four vector-memory instructions where the channel-per-lane walk above issues four
 // per edge.  Same products, in the same order, as se3_bwd_src.
-template <int U>
+//
+// FUSED: the block's 16 sources (four waves x four rows: consecutive nodes) write their Z rows
+// into an LDS tile laid out as the fused forward's aggregate tile (q.off / q.ld), and after a
+// barrier the block multiplies the tile by the packed transposed weights there (fused_tile_out:
+// ds = Zs Bs^T, dv = Zv Bv^T), so Z never reaches HBM.  q's epilogue operands (avg, bias, mask)
+// and aggregate copies are NULL.
+template <int U, bool FUSED>
 __global__ __launch_bounds__(kSeThreads) void se3_bwd_src_rows(SeEdges g, const float* __restrict__ gs,
                                                               int Os, int OsP,
                                                               const float* __restrict__ gv, int Ov,
                                                               int OvP, float* __restrict__ Zs,
                                                               int KZs, float* __restrict__ Zv,
-                                                              int KZv) {
+                                                              int KZv, SeFused q) {
   const int lane = lane_id();
   const int j = lane & 15;
   const int64_t m = (xcd_block() * kSeWaves + uniform(threadIdx.x / kWave)) * kRowNodes + (lane >> 4);
@@ -1862,6 +1868,41 @@ __global__ __launch_bounds__(kSeThreads) void se3_bwd_src_rows(SeEdges g, const 
         }
       });
     });
+  }
+  if constexpr (FUSED) {
+    extern __shared__ floatx4 src_lds[];
+    float* lds = reinterpret_cast<float*>(src_lds);
+    const int64_t node0 = xcd_block() * kFuTile;  // m = node0 + 4 wave + lane / 16
+    const int r = static_cast<int>(m - node0);
+    if (m < g.N) {  // rows of nodes past N are never multiplied into an output
+      // the tile rows as se3_bwd_src writes Zs / Zv, padding zeroed (the packed weights are
+      // zero there, so a stale value could only turn into NaN)
+      if (q.O[0] > 0) {
+        float* row = lds + q.off[0] + r * q.ld[0];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * j + i < Os) row[4 * j + i] = z0[i];
+        if (j < Ov) row[Os + j] = z1;
+        for (int c = Os + Ov + j; c < KZs; c += 16) row[c] = 0.f;
+      }
+      if (q.O[1] > 0) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          float* row = lds + q.off[1] + (3 * r + k) * q.ld[1];
+          if (j < Ov) {
+            row[j] = z2[k];
+            row[Ov + Os + j] = z4[k];
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * j + i < Os) row[Ov + 4 * j + i] = z3[k][i];
+          for (int c = 2 * Ov + Os + j; c < KZv; c += 16) row[c] = 0.f;
+        }
+      }
+    }
+    __syncthreads();
+    fused_tile_out<false>(q, lds, node0, g.N, uniform(threadIdx.x / kWave), lane);
+    return;
   }
   if (m >= g.N) return;
   // rows as se3_bwd_src writes them; columns of absent kinds and the padding are zeros
@@ -2157,8 +2198,8 @@ extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const f
                   path_cols[6] >= 0 || path_cols[7] >= 0 || path_cols[8] >= 0;
   if (bwd_src_rows_ok(N, Os, OsP, Ov, OvP, t2, E, P, ysh)) {
     const dim3 grid4(static_cast<unsigned>(ceil_div(N, kSeWaves * kRowNodes)));
-    hipLaunchKernelGGL((se3_bwd_src_rows<4>), grid4, dim3(kSeThreads), 0, as_stream(stream), g, gs,
-                       Os, OsP, gv, Ov, OvP, Zs, KZs, Zv, KZv);
+    hipLaunchKernelGGL((se3_bwd_src_rows<4, false>), grid4, dim3(kSeThreads), 0, as_stream(stream),
+                       g, gs, Os, OsP, gv, Ov, OvP, Zs, KZs, Zv, KZv, SeFused{});
     GEO_LAUNCH_CHECK("se3_bwd_src_rows");
     return GEO_OK;
   }
@@ -2170,6 +2211,58 @@ extern "C" int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const f
     hipLaunchKernelGGL(se3_bwd_src<false>, grid, dim3(kSeThreads), 0, as_stream(stream), g, gs, Os,
                        OsP, gv, Ov, OvP, gt, Ot, OtP, Zs, KZs, Zv, KZv, Zt, KZt, Z8, KZ8);
   GEO_LAUNCH_CHECK("se3_bwd_src");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_bwd_src_fused(const float* gs, int32_t Os, int32_t OsP, const float* gv,
+                                     int32_t Ov, int32_t OvP, int64_t N, const int64_t* col,
+                                     const int32_t* perm, const int32_t* node_start,
+                                     const int32_t* node_end, int64_t E, const float* dir,
+                                     const float* Y, int32_t ysh, const float* R, int32_t P,
+                                     const int32_t* path_cols, const float* cg, int32_t KZs,
+                                     int32_t KZv, const float* Bs, int32_t Bs_rows, int32_t Cs,
+                                     float* ds, const float* Bv, int32_t Bv_rows, int32_t Cv,
+                                     float* dv, void* stream) {
+  int rc = check_edges("se3_bwd_src_fused", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(Os >= 0 && Ov >= 0 && Cs >= 0 && Cv >= 0, "se3_bwd_src_fused: negative channel count");
+  GEO_REQUIRE((!gs || OsP >= Os) && (!gv || OvP >= Ov), "se3_bwd_src_fused: padded widths too small");
+  GEO_REQUIRE(KZs >= Os + Ov && KZs % 16 == 0 && KZv >= 2 * Ov + Os && KZv % 16 == 0,
+              "se3_bwd_src_fused: KZs / KZv too small or not multiples of 16");
+  const bool want_s = ds != nullptr && Cs > 0, want_v = dv != nullptr && Cv > 0;
+  GEO_REQUIRE(!want_s || (Bs && Bs_rows >= 16 * ((Cs + 15) / 16)), "se3_bwd_src_fused: Bs too short");
+  GEO_REQUIRE(!want_v || (Bv && Bv_rows >= 16 * ((Cv + 15) / 16)), "se3_bwd_src_fused: Bv too short");
+  GEO_REQUIRE((!want_s || (reinterpret_cast<uintptr_t>(Bs) & 15) == 0) &&
+              (!want_v || (reinterpret_cast<uintptr_t>(Bv) & 15) == 0),
+              "se3_bwd_src_fused: packed weights must be 16-byte aligned");
+  const bool t2 = path_cols[5] >= 0 || path_cols[6] >= 0 || path_cols[7] >= 0 || path_cols[8] >= 0;
+  if (!bwd_src_rows_ok(N, Os, OsP, Ov, OvP, t2, E, P, ysh))
+    return set_error(GEO_ERR_UNSUPPORTED, "se3_bwd_src_fused: layer not covered by the row kernel "
+                                          "(type-2 paths, Os > 64, Ov > 16 or arrays of 2 GiB)");
+  SeFused q{};
+  q.W[0] = Bs;
+  q.W[1] = Bv;
+  q.out[0] = ds;
+  q.out[1] = dv;
+  q.O[0] = want_s ? Cs : 0;
+  q.O[1] = want_v ? Cv : 0;
+  q.K[0] = KZs;
+  q.K[1] = KZv;
+  q.ld[0] = KZs + 4;
+  q.ld[1] = KZv + 4;
+  q.off[0] = 0;
+  q.off[1] = kFuTile * q.ld[0];
+  const size_t lds = static_cast<size_t>(q.off[1] + 3 * kFuTile * q.ld[1]) * sizeof(float);
+  if (lds > static_cast<size_t>(kFuLdsMax))
+    return set_error(GEO_ERR_UNSUPPORTED, "se3_bwd_src_fused: tile of %zu bytes exceeds LDS", lds);
+  if (N == 0 || (!want_s && !want_v)) return GEO_OK;
+  GEO_REQUIRE(node_start && node_end && (E == 0 || (col && dir && Y && R)),
+              "se3_bwd_src_fused: null graph array");
+  SeEdges g = make_edges(col, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kFuTile)));  // tile <= 64 KB: default LDS limit
+  hipLaunchKernelGGL((se3_bwd_src_rows<4, true>), grid, dim3(kSeThreads), lds, as_stream(stream), g,
+                     gs, Os, OsP, gv, Ov, OvP, nullptr, KZs, nullptr, KZv, q);
+  GEO_LAUNCH_CHECK("se3_bwd_src_rows");
   return GEO_OK;
 }
 

@@ -295,7 +295,28 @@ def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tens
         # feature gradients: source-side sums over the CSR of the sources, then GEMMs with W^T
         ds = dv = dt = None
         want_s, want_v, want_t = need_s and Cs > 0, need_v and Cv > 0, need_t and Ct > 0
-        if want_s or want_v or want_t:
+        fused_src = False
+        if (want_s or want_v) and not want_t and all(p.pc[i] < 0 for i in (5, 6, 7, 8)):
+            # no type-2 paths: the source-side sums and the GEMMs with the transposed weights in
+            # one launch (the sums stay in LDS); layers the row kernel does not cover fall back
+            perm_r, ns_r, ne_r = source_csr(row, N)
+            Bs, Bv = _pack(p, W, [(6, _pad64(Cs), p.KZs if want_s else 0),
+                                  (7, _pad64(Cv), p.KZv if want_v else 0)], dev)
+            ds = torch.empty(N, Cs, **f32) if want_s else None
+            dv = torch.empty(N, Cv, 3, **f32) if want_v else None
+            rc = L.geo_se3_bwd_src_fused(
+                _nat.ptr(Gs), Os, p.OsP, _nat.ptr(Gv), Ov, p.OvP, N, _nat.ptr(col),
+                _nat.ptr(perm_r), _nat.ptr(ns_r), _nat.ptr(ne_r), E, _nat.ptr(direction),
+                _nat.ptr(Y), p.ysh, _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), p.KZs, p.KZv,
+                _nat.ptr(Bs), Bs.shape[0], Cs, _nat.ptr(ds), _nat.ptr(Bv), Bv.shape[0], Cv,
+                _nat.ptr(dv), st)
+            if rc == 0:
+                fused_src = True
+            elif rc == _nat.GEO_ERR_UNSUPPORTED:
+                ds = dv = None
+            else:
+                _nat.check(rc, "geo_se3_bwd_src_fused")
+        if (want_s or want_v or want_t) and not fused_src:
             perm_r, ns_r, ne_r = source_csr(row, N)
             Zs = torch.empty(N, p.KZs, **f32) if want_s else None
             Zv = torch.empty(N, 3, p.KZv, **f32) if want_v else None

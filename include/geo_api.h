@@ -537,6 +537,23 @@ int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const float* gv, i
                     int32_t ysh, const float* R, int32_t P, const int32_t* path_cols,
                     const float* cg, float* Zs, int32_t KZs, float* Zv, int32_t KZv, float* Zt,
                     int32_t KZt, float* Z8, int32_t KZ8, void* stream);
+/*
+ * geo_se3_bwd_src and the feature-gradient GEMMs in one launch, for layers without type-2 paths:
+ * each workgroup keeps its 16 sources' Zs / Zv rows (row lengths KZs, KZv, multiples of 16) in LDS
+ * and multiplies them there by the packed transposed weights Bs ([Bs_rows >= 16 ceil(Cs / 16)]
+ * [KZs], pack kind 6) and Bv ([..][KZv], kind 7), 16-byte aligned:
+ *   ds [N, Cs] = Zs Bs^T,  dv [N, Cv, 3] = Zv Bv^T  (either may be NULL).
+ * Returns GEO_ERR_UNSUPPORTED, having done nothing, for layers the row kernel does not cover
+ * (type-2 paths, Os > 64, Ov > 16, arrays of 2 GiB or more, tiles beyond 64 KB of LDS): the
+ * caller then uses geo_se3_bwd_src and the GEMMs.
+ */
+int geo_se3_bwd_src_fused(const float* gs, int32_t Os, int32_t OsP, const float* gv, int32_t Ov,
+                          int32_t OvP, int64_t N, const int64_t* col, const int32_t* perm,
+                          const int32_t* node_start, const int32_t* node_end, int64_t E,
+                          const float* dir, const float* Y, int32_t ysh, const float* R, int32_t P,
+                          const int32_t* path_cols, const float* cg, int32_t KZs, int32_t KZv,
+                          const float* Bs, int32_t Bs_rows, int32_t Cs, float* ds, const float* Bv,
+                          int32_t Bv_rows, int32_t Cv, float* dv, void* stream);
 
 /*
  * Radial basis MLP of SE3Conv (geoembodied/nn/modules/se3_conv.py:238-282), per edge length d:

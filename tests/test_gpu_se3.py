@@ -500,6 +500,105 @@ def test_fused_forward_bitwise_vs_two_kernel_path(dev, cfg, graph):
             assert torch.equal(a, b)
 
 
+def _abi_src_backward(cfg, gr, W, R, fused, dev, seed):
+    """Feature gradients from prepared output gradients (random rows, zero padding) through the
+    C ABI: geo_se3_bwd_src_fused, or geo_se3_bwd_src + geo_se3_gemm.  Returns (ds, dv) (NaN where
+    nothing was written), or None when the fused entry point declines the layer."""
+    from gdl_amd import _native as nat
+    from gdl_amd.csrc import source_csr
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _cg_on, _gemm, _pack, _pad64, path_columns
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    N, E = gr.N, gr.E
+    pc = path_columns(W, Ct > 0, True, Ot)
+    p = _Plan(Cs, Cv, Ct, Os, Ov, Ot, pc, R.shape[1], gr.Y.shape[1], Ot > 0)
+    g = torch.Generator().manual_seed(seed)
+    f32 = dict(dtype=torch.float32, device=dev)
+    Gs = torch.zeros(N, p.OsP)
+    Gs[:, :Os] = torch.randn(N, Os, generator=g)
+    Gv = torch.zeros(N, 3, p.OvP)
+    Gv[:, :, :Ov] = torch.randn(N, 3, Ov, generator=g)
+    Gs, Gv = (Gs.to(dev) if Os > 0 else None), (Gv.to(dev) if Ov > 0 else None)
+    Wl = [W[k] for k in PATH_NAMES]
+    Bs, Bv = _pack(p, Wl, [(6, _pad64(Cs), p.KZs if Cs > 0 else 0),
+                           (7, _pad64(Cv), p.KZv if Cv > 0 else 0)], dev)
+    ds = torch.full((N, Cs), float("nan"), **f32) if Cs > 0 else None
+    dv = torch.full((N, Cv, 3), float("nan"), **f32) if Cv > 0 else None
+    perm_r, ns_r, ne_r = source_csr(gr.row, N)
+    cg = _cg_on(dev) if pc[7] >= 0 else None
+    L, st = nat.lib(), nat.stream_of(dev)
+    graph = (N, nat.ptr(gr.col), nat.ptr(perm_r), nat.ptr(ns_r), nat.ptr(ne_r), E,
+             nat.ptr(gr.direction), nat.ptr(gr.Y), gr.Y.shape[1], nat.ptr(R), R.shape[1], p.pc_c,
+             nat.ptr(cg))
+    if fused:
+        rc = L.geo_se3_bwd_src_fused(nat.ptr(Gs), Os, p.OsP, nat.ptr(Gv), Ov, p.OvP, *graph, p.KZs,
+                                     p.KZv, nat.ptr(Bs), Bs.shape[0], Cs, nat.ptr(ds), nat.ptr(Bv),
+                                     Bv.shape[0], Cv, nat.ptr(dv), st)
+        torch.cuda.synchronize()
+        if rc == nat.GEO_ERR_UNSUPPORTED:
+            for o in (ds, dv):  # declined: nothing written
+                assert o is None or torch.isnan(o).all()
+            return None
+        nat.check(rc, "geo_se3_bwd_src_fused")
+    else:
+        Zs = torch.empty(N, p.KZs, **f32) if Cs > 0 else None
+        Zv = torch.empty(N, 3, p.KZv, **f32) if Cv > 0 else None
+        nat.check(L.geo_se3_bwd_src(nat.ptr(Gs), Os, p.OsP, nat.ptr(Gv), Ov, p.OvP, None, 0, 0,
+                                    *graph, nat.ptr(Zs), p.KZs, nat.ptr(Zv), p.KZv, None, 0, None, 0,
+                                    st), "geo_se3_bwd_src")
+        if Cs > 0:
+            _gemm(Zs, N, p.KZs, Bs, Cs, 1, ds, Cs)
+        if Cv > 0:
+            _gemm(Zv, 3 * N, p.KZv, Bv, Cv, 3, dv, 3 * Cv)
+        torch.cuda.synchronize()
+    return ds, dv
+
+
+SRC_FUSED_CONFIGS = [
+    # Cs, Cv, Ct, Os, Ov, Ot
+    (64, 16, 0, 64, 16, 0),    # the C2 layer
+    (8, 4, 0, 8, 4, 0),
+    (96, 8, 0, 40, 8, 0),      # six scalar column blocks of ds
+    (0, 4, 0, 3, 2, 0),        # no scalar input: only dv
+    (20, 0, 0, 6, 0, 0),       # no vector channels: only ds
+]
+
+
+@pytest.mark.parametrize("cfg", SRC_FUSED_CONFIGS, ids=[str(c) for c in SRC_FUSED_CONFIGS])
+@pytest.mark.parametrize("graph", ["sorted", "shuffled", "dense"])
+def test_fused_source_backward_bitwise_vs_two_step_path(dev, cfg, graph):
+    """geo_se3_bwd_src_fused (source-side sums kept in LDS, multiplied there by the transposed
+    weights) equals geo_se3_bwd_src + geo_se3_gemm bit for bit: the same sums in the same order,
+    the same MFMA accumulation.  Partial tiles (N not a multiple of 16), sources without edges and
+    (dense) sources with more than 16 edges per staging round."""
+    if graph == "dense":
+        gr = _graph(250, 1, 0.45, 100, 7, False)
+    else:
+        gr = _graph(300, 2, 0.22, 24, sum(cfg), graph == "shuffled")
+    _, _, _, W, R, _, _ = _inputs(cfg, gr, 5, dev)
+    R = R.to(dev)
+    W = {k: (w.to(dev) if w is not None else None) for k, w in W.items()}
+    print(f"[se3 src fused] cfg={cfg} graph={graph} N={gr.N} E={gr.E}", flush=True)
+    got = _abi_src_backward(cfg, gr, W, R, True, dev, 11)
+    want = _abi_src_backward(cfg, gr, W, R, False, dev, 11)
+    assert got is not None
+    for a, b in zip(got, want):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.isfinite(b).all()
+            assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cfg", [(80, 20, 6, 70, 10, 4), (8, 4, 0, 70, 4, 0), (8, 20, 0, 8, 20, 0)],
+                         ids=["type2", "Os70", "Ov20"])
+def test_fused_source_backward_declines_uncovered_layers(dev, cfg):
+    """Type-2 paths, more than 64 scalar or 16 vector output channels: GEO_ERR_UNSUPPORTED and
+    nothing written (the layer then takes geo_se3_bwd_src and the GEMMs)."""
+    gr = _graph(300, 2, 0.22, 24, sum(cfg), False)
+    _, _, _, W, R, _, _ = _inputs(cfg, gr, 6, dev)
+    W = {k: (w.to(dev) if w is not None else None) for k, w in W.items()}
+    assert _abi_src_backward(cfg, gr, W, R.to(dev), True, dev, 12) is None
+
+
 @pytest.mark.parametrize("cfg", FUSED_CONFIGS + [CONFIGS[2]], ids=[str(c) for c in FUSED_CONFIGS + [CONFIGS[2]]])
 def test_forward_without_grad_vs_oracle(dev, cfg):
     """Under no_grad nothing keeps the aggregates: the fused forward writes only the outputs."""
