@@ -151,8 +151,7 @@ _EMPTY = (0,)
 # torch.compile traces SE3Conv through them (the reference checks the same transparency for its
 # segment-sum op, tests/test_torch_compile.py:83-197).  The nine path weights are separate
 # optional arguments; gradients that are not needed come back as empty tensors.
-@torch.library.custom_op("geoembodied::se3_conv_fwd", mutates_args=())
-def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Tensor,
+def _se3_fwd_impl(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Tensor,
                 perm: Optional[Tensor], node_start: Tensor, node_end: Tensor, direction: Tensor,
                 Y: Tensor, R: Tensor, avg: Tensor, mask: Optional[Tensor], bias: Optional[Tensor],
                 cg: Optional[Tensor], dims: List[int], w0: Optional[Tensor], w1: Optional[Tensor],
@@ -206,6 +205,9 @@ def _se3_fwd_op(s: Tensor, v: Tensor, t: Optional[Tensor], row: Tensor, col: Ten
             Xv if Xv is not None else empty.clone(), Xt if Xt is not None else empty.clone())
 
 
+_se3_fwd_op = torch.library.custom_op("geoembodied::se3_conv_fwd", mutates_args=())(_se3_fwd_impl)
+
+
 @_se3_fwd_op.register_fake
 def _se3_fwd_fake(s, v, t, row, col, perm, node_start, node_end, direction, Y, R, avg, mask, bias,
                   cg, dims, w0, w1, w2, w3, w4, w5, w6, w7, w8):
@@ -223,8 +225,7 @@ def _se3_fwd_fake(s, v, t, row, col, perm, node_start, node_end, direction, Y, R
 _NEED_INPUTS = (0, 1, 2, 8, 9, 10, 13, 16, 17, 18, 19, 20, 21, 22, 23, 24)
 
 
-@torch.library.custom_op("geoembodied::se3_conv_bwd", mutates_args=())
-def _se3_bwd_op(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tensor], s: Tensor,
+def _se3_bwd_impl(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Tensor], s: Tensor,
                 v: Tensor, t: Optional[Tensor], row: Tensor, col: Tensor, perm: Optional[Tensor],
                 node_start: Tensor, node_end: Tensor, direction: Tensor, Y: Tensor, R: Tensor,
                 avg: Tensor, mask: Optional[Tensor], cg: Optional[Tensor], Xs: Tensor, Xv: Tensor,
@@ -401,6 +402,9 @@ def _bwd_shapes(s, v, t, row, Y, R, dims, need, W):
     return [sh if n else _EMPTY for sh, n in zip(full, need)]
 
 
+_se3_bwd_op = torch.library.custom_op("geoembodied::se3_conv_bwd", mutates_args=())(_se3_bwd_impl)
+
+
 @_se3_bwd_op.register_fake
 def _se3_bwd_fake(g_s, g_v, g_t, s, v, t, row, col, perm, node_start, node_end, direction, Y, R,
                   avg, mask, cg, Xs, Xv, Xt, dims, need, w0, w1, w2, w3, w4, w5, w6, w7, w8):
@@ -418,21 +422,48 @@ def _se3_setup(ctx, inputs, output) -> None:
                           Xt, *W)
 
 
-def _se3_backward(ctx, g_s, g_v, g_t, _gXs, _gXv, _gXt):
+def _se3_grads(ctx, g_s, g_v, g_t, bwd):
+    """Gradients of the forward's inputs, in its argument order, from the backward ``bwd``."""
     (s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, mask, cg, Xs, Xv, Xt,
      *W) = ctx.saved_tensors
     ni = ctx.needs_input_grad
     need = [bool(ni[i]) for i in _NEED_INPUTS]
-    grads = torch.ops.geoembodied.se3_conv_bwd(g_s, g_v, g_t, s, v, t, row, col, perm, ns, ne,
-                                               direction, Y, R, avg, mask, cg, Xs, Xv, Xt,
-                                               ctx.dims, need, *W)
+    grads = bwd(g_s, g_v, g_t, s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, mask, cg,
+                Xs, Xv, Xt, ctx.dims, need, *W)
     g = [x if n else None for x, n in zip(grads, need)]
     ds, dv, dt, ddir, dY, dR, dbias, *dW = g
     return (ds, dv, dt, None, None, None, None, None, ddir, dY, dR, None, None, dbias, None, None,
             *dW)
 
 
+def _se3_backward(ctx, g_s, g_v, g_t, _gXs, _gXv, _gXt):
+    return _se3_grads(ctx, g_s, g_v, g_t, torch.ops.geoembodied.se3_conv_bwd)
+
+
 _se3_fwd_op.register_autograd(_se3_backward, setup_context=_se3_setup)
+
+
+def _plain_eager(x: Tensor) -> bool:
+    """True for a plain tensor outside tracing: the eager path may call the implementations
+    directly.  Fake or other subclassed tensors, and torch.compile, take the custom ops."""
+    return type(x) is torch.Tensor and not torch.compiler.is_compiling()
+
+
+class _SE3ConvEager(torch.autograd.Function):
+    """Eager mode: the custom ops' forward and backward implementations called directly.  The
+    custom-op layers (schema defaults, dispatch, the registered autograd) cost more host time per
+    call than a C2 layer's kernels take; under torch.compile the custom ops are used, so the
+    compiled graph still traces through them."""
+
+    @staticmethod
+    def forward(ctx, *args):
+        out = _se3_fwd_impl(*args)
+        _se3_setup(ctx, args, out)
+        return tuple(out)
+
+    @staticmethod
+    def backward(ctx, g_s, g_v, g_t, _gXs, _gXv, _gXt):
+        return _se3_grads(ctx, g_s, g_v, g_t, _se3_bwd_impl)
 
 _DEFAULT_CG: Dict[torch.device, Tensor] = {}
 
@@ -511,15 +542,17 @@ def se3_message_aggregate(
     Wl = [(weights.get(k).to(f32).contiguous() if weights.get(k) is not None else None)
           for k in PATH_NAMES]
     direction = graph.direction.to(f32).contiguous()
-    s_out, v_out, t_out, _, _, _ = torch.ops.geoembodied.se3_conv_fwd(
-        s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, m, b, cg, dims, *Wl)
+    args = (s, v, t, row, col, perm, ns, ne, direction, Y, R, avg, m, b, cg, dims, *Wl)
+    if _plain_eager(s):
+        s_out, v_out, t_out, _, _, _ = _SE3ConvEager.apply(*args)
+    else:
+        s_out, v_out, t_out, _, _, _ = torch.ops.geoembodied.se3_conv_fwd(*args)
     if return_type2:
         return s_out, v_out, (t_out if Ct2_out > 0 else None)
     return s_out, v_out
 
 
-@torch.library.custom_op("geoembodied::radial_mlp", mutates_args=())
-def _radial_op(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
+def _radial_impl(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
                b2: Tensor) -> Tensor:
     """R = W2 silu(W1 (basis(dist) * envelope(dist)) + b1) + b2 in one kernel (fp32 inputs)."""
     dev = dist.device
@@ -534,13 +567,15 @@ def _radial_op(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tenso
     return R
 
 
+_radial_op = torch.library.custom_op("geoembodied::radial_mlp", mutates_args=())(_radial_impl)
+
+
 @_radial_op.register_fake
 def _radial_fake(dist, freqs, cutoff, W1, b1, W2, b2):
     return dist.new_empty(dist.shape[0], W2.shape[0], dtype=torch.float32)
 
 
-@torch.library.custom_op("geoembodied::radial_mlp_bwd", mutates_args=())
-def _radial_bwd_op(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor,
+def _radial_bwd_impl(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor,
                    W2: Tensor, b2: Tensor, need: List[bool]) -> List[Tensor]:
     """[d dist, dW1, db1, dW2, db2]; an entry not in ``need`` is empty."""
     dev = dist.device
@@ -562,6 +597,10 @@ def _radial_bwd_op(dR: Tensor, dist: Tensor, freqs: Tensor, cutoff: float, W1: T
     return [o if o is not None else dist.new_empty(_EMPTY, dtype=torch.float32) for o in outs]
 
 
+_radial_bwd_op = torch.library.custom_op("geoembodied::radial_mlp_bwd",
+                                         mutates_args=())(_radial_bwd_impl)
+
+
 @_radial_bwd_op.register_fake
 def _radial_bwd_fake(dR, dist, freqs, cutoff, W1, b1, W2, b2, need):
     E = dist.shape[0]
@@ -577,16 +616,34 @@ def _radial_setup(ctx, inputs, output) -> None:
     ctx.save_for_backward(dist, freqs, W1, b1, W2, b2)
 
 
-def _radial_backward(ctx, dR):
+def _radial_grads(ctx, dR, bwd):
     dist, freqs, W1, b1, W2, b2 = ctx.saved_tensors
     ni = ctx.needs_input_grad
     need = [bool(ni[i]) for i in (0, 3, 4, 5, 6)]
-    grads = torch.ops.geoembodied.radial_mlp_bwd(dR, dist, freqs, ctx.cutoff, W1, b1, W2, b2, need)
+    grads = bwd(dR, dist, freqs, ctx.cutoff, W1, b1, W2, b2, need)
     dd, dW1, db1, dW2, db2 = [x if n else None for x, n in zip(grads, need)]
     return dd, None, None, dW1, db1, dW2, db2
 
 
+def _radial_backward(ctx, dR):
+    return _radial_grads(ctx, dR, torch.ops.geoembodied.radial_mlp_bwd)
+
+
 _radial_op.register_autograd(_radial_backward, setup_context=_radial_setup)
+
+
+class _RadialEager(torch.autograd.Function):
+    """Eager mode: the radial custom ops' implementations called directly (as _SE3ConvEager)."""
+
+    @staticmethod
+    def forward(ctx, *args):
+        R = _radial_impl(*args)
+        _radial_setup(ctx, args, R)
+        return R
+
+    @staticmethod
+    def backward(ctx, dR):
+        return _radial_grads(ctx, dR, _radial_bwd_impl)
 
 
 def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tensor, W2: Tensor,
@@ -597,7 +654,10 @@ def radial_mlp(dist: Tensor, freqs: Tensor, cutoff: float, W1: Tensor, b1: Tenso
     _require_gpu("radial_mlp", dist)
     f = torch.float32
     c = [x.to(f).contiguous() for x in (dist, freqs, W1, b1, W2, b2)]
-    return torch.ops.geoembodied.radial_mlp(c[0], c[1], float(cutoff), c[2], c[3], c[4], c[5])
+    args = (c[0], c[1], float(cutoff), c[2], c[3], c[4], c[5])
+    if _plain_eager(c[0]):
+        return _RadialEager.apply(*args)
+    return torch.ops.geoembodied.radial_mlp(*args)
 
 
 class RadialBasis(nn.Module):
