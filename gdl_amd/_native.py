@@ -113,6 +113,10 @@ _SIGNATURES = {
     "geo_se3_bwd_src": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64,
                                 c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp,
                                 c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp]),
+    "geo_se3_bwd_edge_fused": (c_int, [c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                       c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_vp, c_i32, c_vp,
+                                       c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                       c_vp, c_vp]),
     "geo_se3_bwd_src_fused": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_vp, c_vp, c_vp,
                                       c_vp, c_i64, c_vp, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp, c_i32,
                                       c_i32, c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_i32, c_vp,

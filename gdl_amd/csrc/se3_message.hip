@@ -1557,21 +1557,12 @@ __global__ __launch_bounds__(kSeThreads, T2 ? 1 : 6) void se3_bwd_edge(SeEdges g
 // does not hold (zeros), so no load carries a per-lane condition, and U steps of four edges
 // (row r: edge j0 + 4 u + r) in flight.
 template <int U>
-__global__ __launch_bounds__(kSeThreads, 6) void se3_bwd_edge_rows(SeEdges g, SeFeat f,
-                                                                  const float* __restrict__ Gs,
-                                                                  int Ks,
-                                                                  const float* __restrict__ Gv,
-                                                                  int Kv, float* __restrict__ dR,
-                                                                  float* __restrict__ ddir,
-                                                                  float* __restrict__ dY) {
-  const int64_t n = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
-  if (n >= g.N) return;
-  const int lane = lane_id();
+__device__ __forceinline__ void edge_rows_walk(const SeEdges& g, const SeFeat& f, int64_t n,
+                                               const GRow& G, int lane, float* __restrict__ dR,
+                                               float* __restrict__ ddir, float* __restrict__ dY) {
   const int row = lane >> 4, li = lane & 15;
   int a, b;
   node_range(g, n, a, b);
-  GRow G;
-  load_grow<false>(G, f, nullptr, n, 0, li, Gs, Ks, Gv, Kv, nullptr, 0);
   const auto rs = row_rsrc(f.s, static_cast<int>(g.N * f.Cs * 4));
   const auto rv = row_rsrc(f.v, static_cast<int>(g.N * f.Cv * 12));
   // byte offset of the lane's scalar channels 4 li .. 4 li + 3 inside a row (Cs is a multiple of
@@ -1633,6 +1624,114 @@ __global__ __launch_bounds__(kSeThreads, 6) void se3_bwd_edge_rows(SeEdges g, Se
         if (li == 0 && jj < cnt && q.ok) write_edge_grads<false>(g, q, S, dR, ddir, dY);
       }
     }
+  }
+}
+
+template <int U>
+__global__ __launch_bounds__(kSeThreads, 6) void se3_bwd_edge_rows(SeEdges g, SeFeat f,
+                                                                  const float* __restrict__ Gs,
+                                                                  int Ks,
+                                                                  const float* __restrict__ Gv,
+                                                                  int Kv, float* __restrict__ dR,
+                                                                  float* __restrict__ ddir,
+                                                                  float* __restrict__ dY) {
+  const int64_t n = xcd_block() * kSeWaves + uniform(threadIdx.x / kWave);
+  if (n >= g.N) return;
+  const int lane = lane_id();
+  GRow G;
+  load_grow<false>(G, f, nullptr, n, 0, lane & 15, Gs, Ks, Gv, Kv, nullptr, 0);
+  edge_rows_walk<U>(g, f, n, G, lane, dR, ddir, dY);
+}
+
+// The tile's rows times the packed weights, into LDS: out[r][o] = sum_k A[r][k] W[o][k] for the
+// 16 G rows r of A (LDS, row stride lda) and the columns o < 16 ceil(O / 16) (W has that many
+// rows, zero past O), written with row stride ldo.  The MFMA fragments and the k order are
+// fused_gemm's (and se3_gemm's), so the result equals theirs bit for bit.  Wave w takes the
+// blocks whose running number base + b is w mod 4.
+template <int G>
+__device__ __forceinline__ void lds_gemm(const float* A, int lda, int K, const float* __restrict__ W,
+                                         int O, float* out, int ldo, int base, int wave, int lane) {
+  const int ncb = (O + 15) / 16;
+  const int nblk = G * ncb;
+  const int li = lane & 15, lk = lane >> 4;
+  for (int b = (wave - base % kSeWaves + kSeWaves) % kSeWaves; b < nblk; b += kSeWaves) {
+    const int rb = b / ncb, cb = b % ncb;
+    const float* ap = A + (rb * 16 + li) * lda + 4 * lk;
+    const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 64) {
+      floatx4 a[4], w[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
+        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
+        a[c] = *reinterpret_cast<const floatx4*>(ap + k);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (k0 + 16 * c >= K) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[(rb * 16 + 4 * lk + q) * ldo + cb * 16 + li] = acc[q];
+  }
+}
+
+// se3_bwd_edge_rows with gX formed in LDS: a workgroup takes 16 consecutive targets, stages their
+// prepared output-gradient rows (Gs [16][OsP], Gv [48][OvP]; zeros past N or for an absent kind),
+// multiplies them there by the packed transposed weights (gXs = Gs WsT^T, gXv = Gv WvT^T, as the
+// GEMMs of the unfused path compute them, bit for bit), and each wave then walks the edges of
+// four of the targets in turn, its gradient row read from the tile; gX never reaches HBM.
+struct SeEdgeTile {
+  const float* Gs;   // [N][OsP] or NULL
+  const float* Gv;   // [N][3][OvP] or NULL
+  const float* WsT;  // [>= 16 ceil(Ks / 16)][OsP]
+  const float* WvT;  // [>= 16 ceil(Kv / 16)][OvP]
+  int OsP, OvP, Ks, Kv;
+};
+
+__host__ __device__ inline size_t edge_tile_floats(int OsP, int OvP, int Ks, int Kv) {
+  return static_cast<size_t>(kFuTile) * (OsP + 4) + 3 * kFuTile * (OvP + 4) +
+         static_cast<size_t>(kFuTile) * (Ks + 4) + 3 * kFuTile * (Kv + 4);
+}
+
+template <int U>
+__global__ __launch_bounds__(kSeThreads, 5) void se3_bwd_edge_tile(SeEdges g, SeFeat f, SeEdgeTile q,
+                                                                  float* __restrict__ dR,
+                                                                  float* __restrict__ ddir,
+                                                                  float* __restrict__ dY) {
+  extern __shared__ floatx4 et_lds[];
+  float* gS = reinterpret_cast<float*>(et_lds);
+  const int ldgs = q.OsP + 4, ldgv = q.OvP + 4, ldxs = q.Ks + 4, ldxv = q.Kv + 4;
+  float* gV = gS + kFuTile * ldgs;
+  float* xS = gV + 3 * kFuTile * ldgv;
+  float* xV = xS + kFuTile * ldxs;
+  const int64_t node0 = xcd_block() * kFuTile;
+  const int wave = uniform(threadIdx.x / kWave), lane = lane_id();
+  for (int i = threadIdx.x; i < kFuTile * q.OsP; i += kSeThreads) {
+    const int r = i / q.OsP, c = i % q.OsP;
+    gS[r * ldgs + c] = (q.Gs && node0 + r < g.N) ? q.Gs[(node0 + r) * q.OsP + c] : 0.f;
+  }
+  for (int i = threadIdx.x; i < 3 * kFuTile * q.OvP; i += kSeThreads) {
+    const int r = i / q.OvP, c = i % q.OvP;  // tile row r: node r / 3, component r % 3
+    gV[r * ldgv + c] = (q.Gv && node0 + r / 3 < g.N) ? q.Gv[(node0 * 3 + r) * q.OvP + c] : 0.f;
+  }
+  __syncthreads();
+  const int nb0 = q.Gs ? (q.Ks + 15) / 16 : 0;
+  if (q.Gs) lds_gemm<1>(gS, ldgs, q.OsP, q.WsT, q.Ks, xS, ldxs, 0, wave, lane);
+  if (q.Gv) lds_gemm<3>(gV, ldgv, q.OvP, q.WvT, q.Kv, xV, ldxv, nb0, wave, lane);
+  __syncthreads();
+  for (int tt = 0; tt < kFuTile / kSeWaves; ++tt) {
+    const int r = (kFuTile / kSeWaves) * wave + tt;
+    const int64_t n = node0 + r;
+    if (n >= g.N) break;  // wave-uniform
+    GRow G;
+    load_grow<false>(G, f, nullptr, r, 0, lane & 15, q.Gs ? xS : nullptr, ldxs,
+                     q.Gv ? xV : nullptr, ldxv, nullptr, 0);
+    edge_rows_walk<U>(g, f, n, G, lane, dR, ddir, dY);
   }
 }
 
@@ -2171,6 +2270,46 @@ extern "C" int geo_se3_bwd_edge(const float* s, const float* v, const float* t, 
   else GEO_BWD_EDGE(false, false);
 #undef GEO_BWD_EDGE
   GEO_LAUNCH_CHECK("se3_bwd_edge");
+  return GEO_OK;
+}
+
+extern "C" int geo_se3_bwd_edge_fused(const float* s, const float* v, int64_t N, int32_t Cs,
+                                      int32_t Cv, const int64_t* row, const int32_t* perm,
+                                      const int32_t* node_start, const int32_t* node_end, int64_t E,
+                                      const float* dir, const float* Y, int32_t ysh, const float* R,
+                                      int32_t P, const int32_t* path_cols, const float* cg,
+                                      const float* Gs, int32_t OsP, const float* Gv, int32_t OvP,
+                                      const float* WsT, int32_t WsT_rows, const float* WvT,
+                                      int32_t WvT_rows, int32_t Ks, int32_t Kv, float* dR,
+                                      float* ddir, float* dY, void* stream) {
+  int rc = check_edges("se3_bwd_edge_fused", N, E, ysh, P, path_cols, cg);
+  if (rc) return rc;
+  GEO_REQUIRE(Cs >= 0 && Cv >= 0, "se3_bwd_edge_fused: negative channel count");
+  GEO_REQUIRE(Ks >= Cs + Cv && Ks % 16 == 0 && Kv >= Cs + 2 * Cv && Kv % 16 == 0,
+              "se3_bwd_edge_fused: Ks / Kv too small or not multiples of 16");
+  GEO_REQUIRE((!Gs || (OsP > 0 && OsP % 16 == 0)) && (!Gv || (OvP > 0 && OvP % 16 == 0)),
+              "se3_bwd_edge_fused: OsP / OvP must be positive multiples of 16");
+  GEO_REQUIRE(!Gs || (WsT && WsT_rows >= Ks), "se3_bwd_edge_fused: WsT too short");
+  GEO_REQUIRE(!Gv || (WvT && WvT_rows >= Kv), "se3_bwd_edge_fused: WvT too short");
+  GEO_REQUIRE((!Gs || (reinterpret_cast<uintptr_t>(WsT) & 15) == 0) &&
+              (!Gv || (reinterpret_cast<uintptr_t>(WvT) & 15) == 0),
+              "se3_bwd_edge_fused: packed weights must be 16-byte aligned");
+  GEO_REQUIRE((Cs == 0 || s) && (Cv == 0 || v), "se3_bwd_edge_fused: null features");
+  const bool t2 = path_cols[5] >= 0 || path_cols[6] >= 0 || path_cols[7] >= 0 || path_cols[8] >= 0;
+  const size_t lds = edge_tile_floats(Gs ? OsP : 0, Gv ? OvP : 0, Ks, Kv) * sizeof(float);
+  if (!bwd_edge_rows_ok(N, Cs, Cv, t2) || lds > static_cast<size_t>(kFuLdsMax))
+    return set_error(GEO_ERR_UNSUPPORTED, "se3_bwd_edge_fused: layer not covered by the tile kernel "
+                                          "(type-2 paths, Cs > 64 or not a multiple of 4, Cv > 16, "
+                                          "arrays of 2 GiB, tiles beyond 64 KB of LDS)");
+  if (N == 0 || E == 0 || (!dR && !ddir && !dY)) return GEO_OK;
+  GEO_REQUIRE(row && node_start && node_end && dir && Y && R, "se3_bwd_edge_fused: null graph array");
+  SeEdges g = make_edges(row, perm, node_start, node_end, N, E, dir, Y, ysh, R, P, path_cols, cg);
+  SeFeat f{s, v, nullptr, Cs, Cv, 0};
+  SeEdgeTile q{Gs, Gv, WsT, WvT, Gs ? OsP : 0, Gv ? OvP : 0, Ks, Kv};
+  const dim3 grid(static_cast<unsigned>(ceil_div(N, kFuTile)));
+  hipLaunchKernelGGL((se3_bwd_edge_tile<1>), grid, dim3(kSeThreads), lds, as_stream(stream), g, f, q,
+                     dR, ddir, dY);
+  GEO_LAUNCH_CHECK("se3_bwd_edge_tile");
   return GEO_OK;
 }
 

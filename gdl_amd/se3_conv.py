@@ -269,11 +269,30 @@ def _se3_bwd_impl(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Te
 
         # per-edge gradients of R, direction and Y from gX = G W (per target node)
         dR = ddir = dY = None
+        gXs = gXv = gXt = None
+        fused_edge = False
         if (need_dir or need_Y or need_R) and E > 0:
-            gXs = gXv = gXt = None
             WsT, WvT, WtT = _pack(p, W, [(3, _pad64(p.Ks), p.OsP if Gs is not None else 0),
                                          (4, _pad64(p.Kv), p.OvP if Gv is not None else 0),
                                          (5, _pad64(p.Kt), p.OtP if Gt is not None else 0)], dev)
+            dR = torch.zeros(E, p.P, **f32) if need_R else None
+            ddir = torch.zeros(E, 3, **f32) if need_dir else None
+            dY = torch.zeros(E, p.ysh, **f32) if need_Y else None
+            fused_edge = False
+            if Gt is None and Ct == 0 and all(p.pc[i] < 0 for i in (5, 6, 7, 8)):
+                # gX formed per tile of targets on the chip and used there (never in HBM);
+                # layers the tile kernel does not cover fall back to the GEMMs below
+                rc = L.geo_se3_bwd_edge_fused(
+                    _nat.ptr(s), _nat.ptr(v), N, Cs, Cv, _nat.ptr(row), _nat.ptr(perm),
+                    _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction), _nat.ptr(Y),
+                    p.ysh, _nat.ptr(R), p.P, p.pc_c, _nat.ptr(cg), _nat.ptr(Gs), p.OsP,
+                    _nat.ptr(Gv), p.OvP, _nat.ptr(WsT), WsT.shape[0], _nat.ptr(WvT), WvT.shape[0],
+                    p.Ks, p.Kv, _nat.ptr(dR), _nat.ptr(ddir), _nat.ptr(dY), st)
+                if rc == 0:
+                    fused_edge = True
+                elif rc != _nat.GEO_ERR_UNSUPPORTED:
+                    _nat.check(rc, "geo_se3_bwd_edge_fused")
+        if (need_dir or need_Y or need_R) and E > 0 and not fused_edge:
             if Gs is not None:
                 gXs = torch.empty(N, p.Ks, **f32)
                 _gemm(Gs, N, p.OsP, WsT, p.Ks, 1, gXs, p.Ks)
@@ -283,9 +302,6 @@ def _se3_bwd_impl(g_s: Optional[Tensor], g_v: Optional[Tensor], g_t: Optional[Te
             if Gt is not None:
                 gXt = torch.empty(N, 5, p.Kt, **f32)
                 _gemm(Gt, 5 * N, p.OtP, WtT, p.Kt, 1, gXt, p.Kt)
-            dR = torch.zeros(E, p.P, **f32) if need_R else None
-            ddir = torch.zeros(E, 3, **f32) if need_dir else None
-            dY = torch.zeros(E, p.ysh, **f32) if need_Y else None
             _nat.check(L.geo_se3_bwd_edge(
                 _nat.ptr(s), _nat.ptr(v), _nat.ptr(t), N, Cs, Cv, Ct, _nat.ptr(row), _nat.ptr(perm),
                 _nat.ptr(node_start), _nat.ptr(node_end), E, _nat.ptr(direction), _nat.ptr(Y), p.ysh,

@@ -530,6 +530,24 @@ int geo_se3_bwd_edge(const float* s, const float* v, const float* t, int64_t N, 
                      const int32_t* path_cols, const float* cg, const float* gXs, int32_t Ks,
                      const float* gXv, int32_t Kv, const float* gXt, int32_t Kt, float* dR,
                      float* ddir, float* dY, void* stream);
+/*
+ * geo_se3_bwd_edge with gX formed on the chip, for layers without type-2 paths (Cs <= 64 and a
+ * multiple of 4, Cv <= 16): each workgroup stages its 16 targets' prepared output-gradient rows
+ * Gs ([N][OsP]) and Gv ([N][3][OvP]) (OsP, OvP multiples of 16; either NULL) in LDS, multiplies
+ * them there by the packed transposed weights WsT ([WsT_rows >= Ks][OsP], pack kind 3) and WvT
+ * ([..][OvP], kind 4), 16-byte aligned -- gXs = Gs WsT^T, gXv = Gv WvT^T, bit for bit as the
+ * GEMMs of the two-step path -- and walks the targets' edges with those rows.  Returns
+ * GEO_ERR_UNSUPPORTED, having done nothing, for layers it does not cover: the caller then forms
+ * gX with geo_se3_gemm and calls geo_se3_bwd_edge.
+ */
+int geo_se3_bwd_edge_fused(const float* s, const float* v, int64_t N, int32_t Cs, int32_t Cv,
+                           const int64_t* row, const int32_t* perm, const int32_t* node_start,
+                           const int32_t* node_end, int64_t E, const float* dir, const float* Y,
+                           int32_t ysh, const float* R, int32_t P, const int32_t* path_cols,
+                           const float* cg, const float* Gs, int32_t OsP, const float* Gv,
+                           int32_t OvP, const float* WsT, int32_t WsT_rows, const float* WvT,
+                           int32_t WvT_rows, int32_t Ks, int32_t Kv, float* dR, float* ddir,
+                           float* dY, void* stream);
 int geo_se3_bwd_src(const float* gs, int32_t Os, int32_t OsP, const float* gv, int32_t Ov,
                     int32_t OvP, const float* gt, int32_t Ot, int32_t OtP, int64_t N,
                     const int64_t* col, const int32_t* perm, const int32_t* node_start,

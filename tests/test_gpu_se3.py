@@ -599,6 +599,105 @@ def test_fused_source_backward_declines_uncovered_layers(dev, cfg):
     assert _abi_src_backward(cfg, gr, W, R.to(dev), True, dev, 12) is None
 
 
+def _abi_edge_backward(cfg, gr, s, v, W, R, fused, dev, seed):
+    """Per-edge gradients (dR, ddir, dY; NaN-initialised, then zero-filled like the module) from
+    prepared output gradients (random rows, zero padding) through the C ABI:
+    geo_se3_bwd_edge_fused, or gX by geo_se3_gemm + geo_se3_bwd_edge.  None when the fused entry
+    point declines the layer."""
+    from gdl_amd import _native as nat
+    from gdl_amd.se3_conv import PATH_NAMES, _Plan, _cg_on, _gemm, _pack, _pad64, path_columns
+    Cs, Cv, Ct, Os, Ov, Ot = cfg
+    N, E = gr.N, gr.E
+    pc = path_columns(W, Ct > 0, True, Ot)
+    p = _Plan(Cs, Cv, Ct, Os, Ov, Ot, pc, R.shape[1], gr.Y.shape[1], Ot > 0)
+    g = torch.Generator().manual_seed(seed)
+    f32 = dict(dtype=torch.float32, device=dev)
+    Gs = torch.zeros(N, p.OsP)
+    Gs[:, :Os] = torch.randn(N, Os, generator=g)
+    Gv = torch.zeros(N, 3, p.OvP)
+    Gv[:, :, :Ov] = torch.randn(N, 3, Ov, generator=g)
+    Gs, Gv = (Gs.to(dev) if Os > 0 else None), (Gv.to(dev) if Ov > 0 else None)
+    Wl = [W[k] for k in PATH_NAMES]
+    WsT, WvT = _pack(p, Wl, [(3, _pad64(p.Ks), p.OsP if Gs is not None else 0),
+                             (4, _pad64(p.Kv), p.OvP if Gv is not None else 0)], dev)
+    dR = torch.zeros(E, p.P, **f32)
+    ddir = torch.zeros(E, 3, **f32)
+    dY = torch.zeros(E, p.ysh, **f32)
+    perm = None if getattr(gr, "_perm_identity", False) else gr.perm
+    cg = _cg_on(dev) if pc[7] >= 0 else None
+    L, st = nat.lib(), nat.stream_of(dev)
+    graph = (nat.ptr(gr.row), nat.ptr(perm), nat.ptr(gr.node_start), nat.ptr(gr.node_end), E,
+             nat.ptr(gr.direction), nat.ptr(gr.Y), gr.Y.shape[1], nat.ptr(R), R.shape[1], p.pc_c,
+             nat.ptr(cg))
+    if fused:
+        rc = L.geo_se3_bwd_edge_fused(nat.ptr(s), nat.ptr(v), N, Cs, Cv, *graph, nat.ptr(Gs), p.OsP,
+                                      nat.ptr(Gv), p.OvP, nat.ptr(WsT), WsT.shape[0], nat.ptr(WvT),
+                                      WvT.shape[0], p.Ks, p.Kv, nat.ptr(dR), nat.ptr(ddir),
+                                      nat.ptr(dY), st)
+        torch.cuda.synchronize()
+        if rc == nat.GEO_ERR_UNSUPPORTED:
+            for o in (dR, ddir, dY):  # declined: nothing written
+                assert not o.any()
+            return None
+        nat.check(rc, "geo_se3_bwd_edge_fused")
+    else:
+        gXs = torch.empty(N, p.Ks, **f32) if Gs is not None else None
+        gXv = torch.empty(N, 3, p.Kv, **f32) if Gv is not None else None
+        if Gs is not None:
+            _gemm(Gs, N, p.OsP, WsT, p.Ks, 1, gXs, p.Ks)
+        if Gv is not None:
+            _gemm(Gv, 3 * N, p.OvP, WvT, p.Kv, 1, gXv, p.Kv)
+        nat.check(L.geo_se3_bwd_edge(nat.ptr(s), nat.ptr(v), None, N, Cs, Cv, 0, *graph,
+                                     nat.ptr(gXs), p.Ks, nat.ptr(gXv), p.Kv, None, 0, nat.ptr(dR),
+                                     nat.ptr(ddir), nat.ptr(dY), st), "geo_se3_bwd_edge")
+        torch.cuda.synchronize()
+    return dR, ddir, dY
+
+
+EDGE_FUSED_CONFIGS = [
+    # Cs, Cv, Ct, Os, Ov, Ot (the edge path's limits are on the inputs: Cs <= 64, Cv <= 16)
+    (64, 16, 0, 64, 16, 0),    # the C2 layer
+    (8, 4, 0, 8, 4, 0),
+    (40, 8, 0, 96, 8, 0),      # 96 output channels: a 96-wide gradient tile
+    (0, 4, 0, 3, 2, 0),        # no scalar input
+    (20, 0, 0, 6, 0, 0),       # no vector channels
+]
+
+
+@pytest.mark.parametrize("cfg", EDGE_FUSED_CONFIGS, ids=[str(c) for c in EDGE_FUSED_CONFIGS])
+@pytest.mark.parametrize("graph", ["sorted", "shuffled", "dense"])
+def test_fused_edge_backward_bitwise_vs_two_step_path(dev, cfg, graph):
+    """geo_se3_bwd_edge_fused (gX formed per tile of 16 targets in LDS) equals the gX GEMMs +
+    geo_se3_bwd_edge bit for bit: partial tiles, targets without edges, dense targets with more
+    than 64 edges (several staging rounds), a shuffled edge order."""
+    if graph == "dense":
+        gr = _graph(250, 1, 0.45, 100, 7, False)
+    else:
+        gr = _graph(300, 2, 0.22, 24, sum(cfg) + 1, graph == "shuffled")
+    s, v, _, W, R, _, _ = _inputs(cfg, gr, 8, dev)
+    s, v, R = s.to(dev), v.to(dev), R.to(dev)
+    W = {k: (w.to(dev) if w is not None else None) for k, w in W.items()}
+    print(f"[se3 edge fused] cfg={cfg} graph={graph} N={gr.N} E={gr.E}", flush=True)
+    got = _abi_edge_backward(cfg, gr, s, v, W, R, True, dev, 13)
+    want = _abi_edge_backward(cfg, gr, s, v, W, R, False, dev, 13)
+    assert got is not None
+    for a, b in zip(got, want):
+        assert torch.isfinite(b).all()
+        assert torch.equal(a, b)
+    assert want[0].abs().sum() > 0
+
+
+@pytest.mark.parametrize("cfg", [(80, 20, 6, 70, 10, 4), (96, 4, 0, 8, 4, 0), (8, 20, 0, 8, 20, 0)],
+                         ids=["type2", "Cs96", "Cv20"])
+def test_fused_edge_backward_declines_uncovered_layers(dev, cfg):
+    """Type-2 paths, more than 64 scalar or 16 vector input channels: GEO_ERR_UNSUPPORTED and
+    nothing written (the layer then takes the gX GEMMs and geo_se3_bwd_edge)."""
+    gr = _graph(300, 2, 0.22, 24, sum(cfg), False)
+    s, v, _, W, R, _, _ = _inputs(cfg, gr, 9, dev)
+    W = {k: (w.to(dev) if w is not None else None) for k, w in W.items()}
+    assert _abi_edge_backward(cfg, gr, s.to(dev), v.to(dev), W, R.to(dev), True, dev, 14) is None
+
+
 @pytest.mark.parametrize("cfg", FUSED_CONFIGS + [CONFIGS[2]], ids=[str(c) for c in FUSED_CONFIGS + [CONFIGS[2]]])
 def test_forward_without_grad_vs_oracle(dev, cfg):
     """Under no_grad nothing keeps the aggregates: the fused forward writes only the outputs."""
