@@ -1680,11 +1680,50 @@ __device__ __forceinline__ void lds_gemm(const float* A, int lda, int K, const f
   }
 }
 
-// se3_bwd_edge_rows with gX formed in LDS: a workgroup takes 16 consecutive targets, stages their
-// prepared output-gradient rows (Gs [16][OsP], Gv [48][OvP]; zeros past N or for an absent kind),
-// multiplies them there by the packed transposed weights (gXs = Gs WsT^T, gXv = Gv WvT^T, as the
-// GEMMs of the unfused path compute them, bit for bit), and each wave then walks the edges of
-// four of the targets in turn, its gradient row read from the tile; gX never reaches HBM.
+// lds_gemm with A read from global memory: rows row0 .. row0 + 16 G - 1 of a row-major [rows][K]
+// matrix behind the buffer resource ra (rows past its end read zeros).
+template <int G>
+__device__ __forceinline__ void lds_gemm_ga(__amdgpu_buffer_rsrc_t ra, int64_t row0, int K,
+                                            const float* __restrict__ W, int O, float* out, int ldo,
+                                            int base, int wave, int lane) {
+  const int ncb = (O + 15) / 16;
+  const int nblk = G * ncb;
+  const int li = lane & 15, lk = lane >> 4;
+  for (int b = (wave - base % kSeWaves + kSeWaves) % kSeWaves; b < nblk; b += kSeWaves) {
+    const int rb = b / ncb, cb = b % ncb;
+    const uint32_t arow = static_cast<uint32_t>((row0 + rb * 16 + li) * K * 4 + 16 * lk);
+    const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += 64) {
+      floatx4 a[4], w[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
+        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, arow + 4u * k, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[c][q] = __uint_as_float(v[q]);  // element by value
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (k0 + 16 * c >= K) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[(rb * 16 + 4 * lk + q) * ldo + cb * 16 + li] = acc[q];
+  }
+}
+
+// se3_bwd_edge_rows with gX formed in LDS: a workgroup takes 16 consecutive targets, multiplies
+// their prepared output-gradient rows (Gs [16][OsP], Gv [48][OvP], read as MFMA fragments straight
+// from memory; zeros past N) by the packed transposed weights into the tile's gX rows in LDS
+// (gXs = Gs WsT^T, gXv = Gv WvT^T, as the GEMMs of the unfused path compute them, bit for bit),
+// and each wave then walks the edges of four of the targets in turn, its gradient row read from
+// the tile; gX never reaches HBM.  (Staging the gradient rows in LDS as well took 32 KB per
+// workgroup: five waves per SIMD instead of six.)
 struct SeEdgeTile {
   const float* Gs;   // [N][OsP] or NULL
   const float* Gv;   // [N][3][OvP] or NULL
@@ -1693,9 +1732,8 @@ struct SeEdgeTile {
   int OsP, OvP, Ks, Kv;
 };
 
-__host__ __device__ inline size_t edge_tile_floats(int OsP, int OvP, int Ks, int Kv) {
-  return static_cast<size_t>(kFuTile) * (OsP + 4) + 3 * kFuTile * (OvP + 4) +
-         static_cast<size_t>(kFuTile) * (Ks + 4) + 3 * kFuTile * (Kv + 4);
+__host__ __device__ inline size_t edge_tile_floats(int Ks, int Kv) {
+  return static_cast<size_t>(kFuTile) * (Ks + 4) + 3 * kFuTile * (Kv + 4);
 }
 
 template <int U>
@@ -1704,25 +1742,19 @@ __global__ __launch_bounds__(kSeThreads, 5) void se3_bwd_edge_tile(SeEdges g, Se
                                                                   float* __restrict__ ddir,
                                                                   float* __restrict__ dY) {
   extern __shared__ floatx4 et_lds[];
-  float* gS = reinterpret_cast<float*>(et_lds);
-  const int ldgs = q.OsP + 4, ldgv = q.OvP + 4, ldxs = q.Ks + 4, ldxv = q.Kv + 4;
-  float* gV = gS + kFuTile * ldgs;
-  float* xS = gV + 3 * kFuTile * ldgv;
+  const int ldxs = q.Ks + 4, ldxv = q.Kv + 4;
+  float* xS = reinterpret_cast<float*>(et_lds);
   float* xV = xS + kFuTile * ldxs;
   const int64_t node0 = xcd_block() * kFuTile;
   const int wave = uniform(threadIdx.x / kWave), lane = lane_id();
-  for (int i = threadIdx.x; i < kFuTile * q.OsP; i += kSeThreads) {
-    const int r = i / q.OsP, c = i % q.OsP;
-    gS[r * ldgs + c] = (q.Gs && node0 + r < g.N) ? q.Gs[(node0 + r) * q.OsP + c] : 0.f;
-  }
-  for (int i = threadIdx.x; i < 3 * kFuTile * q.OvP; i += kSeThreads) {
-    const int r = i / q.OvP, c = i % q.OvP;  // tile row r: node r / 3, component r % 3
-    gV[r * ldgv + c] = (q.Gv && node0 + r / 3 < g.N) ? q.Gv[(node0 * 3 + r) * q.OvP + c] : 0.f;
-  }
-  __syncthreads();
+  // the A fragments straight from the gradient rows (rows past N read zeros)
   const int nb0 = q.Gs ? (q.Ks + 15) / 16 : 0;
-  if (q.Gs) lds_gemm<1>(gS, ldgs, q.OsP, q.WsT, q.Ks, xS, ldxs, 0, wave, lane);
-  if (q.Gv) lds_gemm<3>(gV, ldgv, q.OvP, q.WvT, q.Kv, xV, ldxv, nb0, wave, lane);
+  if (q.Gs)
+    lds_gemm_ga<1>(row_rsrc(q.Gs, static_cast<int>(g.N * q.OsP * 4)), node0, q.OsP, q.WsT, q.Ks, xS,
+                   ldxs, 0, wave, lane);
+  if (q.Gv)
+    lds_gemm_ga<3>(row_rsrc(q.Gv, static_cast<int>(g.N * 3 * q.OvP * 4)), node0 * 3, q.OvP, q.WvT,
+                   q.Kv, xV, ldxv, nb0, wave, lane);
   __syncthreads();
   for (int tt = 0; tt < kFuTile / kSeWaves; ++tt) {
     const int r = (kFuTile / kSeWaves) * wave + tt;
@@ -2296,8 +2328,10 @@ extern "C" int geo_se3_bwd_edge_fused(const float* s, const float* v, int64_t N,
               "se3_bwd_edge_fused: packed weights must be 16-byte aligned");
   GEO_REQUIRE((Cs == 0 || s) && (Cv == 0 || v), "se3_bwd_edge_fused: null features");
   const bool t2 = path_cols[5] >= 0 || path_cols[6] >= 0 || path_cols[7] >= 0 || path_cols[8] >= 0;
-  const size_t lds = edge_tile_floats(Gs ? OsP : 0, Gv ? OvP : 0, Ks, Kv) * sizeof(float);
-  if (!bwd_edge_rows_ok(N, Cs, Cv, t2) || lds > static_cast<size_t>(kFuLdsMax))
+  const size_t lds = edge_tile_floats(Ks, Kv) * sizeof(float);
+  const int64_t lim = int64_t{1} << 31;  // the gradient rows are read through buffer resources
+  if (!bwd_edge_rows_ok(N, Cs, Cv, t2) || lds > static_cast<size_t>(kFuLdsMax) ||
+      N * OsP * 4 >= lim || N * 3 * OvP * 4 >= lim)
     return set_error(GEO_ERR_UNSUPPORTED, "se3_bwd_edge_fused: layer not covered by the tile kernel "
                                           "(type-2 paths, Cs > 64 or not a multiple of 4, Cv > 16, "
                                           "arrays of 2 GiB, tiles beyond 64 KB of LDS)");
