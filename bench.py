@@ -205,15 +205,33 @@ def _fused_rooflines(args, dev, pos, row, col, perm, ns, ne, scores, feats, idx,
         raise RuntimeError("segment softmax: C entry point and API call disagree")
     us = 1e3 * event_ms(lambda: lib.geo_segment_softmax_fwd(*sm_args), args.iters, 5)
     out["segment_softmax_fwd"] = entry(us, 2 * E * H * 4 + E * 4 + 2 * N * 4)
+    # the gather and edge-geometry kernels (13-14 us) are shorter than their wrappers' host
+    # time too: the same C-entry-point timing, each checked once against the API call
     w = idw_weights(idx, dist)
     n_out, K = idx.shape
     C = feats.shape[1]
-    us = 1e3 * event_ms(lambda: gather_weighted_sum(feats, idx, w), args.iters, 5)
+    idx64, feats_c = idx.contiguous(), feats.contiguous()
+    g_out = torch.empty(n_out, C, device=dev)
+    gw_args = (nat.DTYPE_CODES[torch.float32], nat.ptr(feats_c), feats_c.shape[0], C, nat.ptr(idx64),
+               nat.ptr(w), n_out, K, nat.ptr(g_out), st)
+    nat.check(lib.geo_gather_weighted_sum(*gw_args), "geo_gather_weighted_sum")
+    if not torch.equal(g_out, gather_weighted_sum(feats, idx, w)):
+        raise RuntimeError("gather_weighted_sum: C entry point and API call disagree")
+    us = 1e3 * event_ms(lambda: lib.geo_gather_weighted_sum(*gw_args), args.iters, 5)
     out["gather_weighted_sum_k3_c112"] = entry(
         us, feats.shape[0] * C * 4 + n_out * K * (8 + 4) + n_out * C * 4,
         n_out * K * (8 + 4 + C * 4) + n_out * C * 4)
+    pos_c, row64, col64 = pos.contiguous(), row.contiguous(), col.contiguous()
+    e_dir, e_dist, e_Y = (torch.empty(E, 3, device=dev), torch.empty(E, device=dev),
+                          torch.empty(E, 9, device=dev))
+    eg_args = (nat.ptr(pos_c), N, nat.ptr(row64), nat.ptr(col64), E, 2, nat.ptr(e_dir),
+               nat.ptr(e_dist), nat.ptr(e_Y), st)
+    nat.check(lib.geo_edge_geometry(*eg_args), "geo_edge_geometry")
     with torch.no_grad():
-        us = 1e3 * event_ms(lambda: edge_geometry_hip(pos, row, col, 2), args.iters, 5)
+        ref_geom = edge_geometry_hip(pos, row, col, 2)
+    if not all(torch.equal(a, b) for a, b in zip((e_dir, e_dist, e_Y), ref_geom)):
+        raise RuntimeError("edge_geometry: C entry point and API call disagree")
+    us = 1e3 * event_ms(lambda: lib.geo_edge_geometry(*eg_args), args.iters, 5)
     out["edge_geometry_l2"] = entry(us, N * 12 + E * (16 + 52), E * (16 + 24 + 52))
     # the SE3 forward aggregate alone (sums of r-weighted source features per target)
     Cs, Cv = fs.shape[1], fv.shape[1]

@@ -66,6 +66,8 @@ _SIGNATURES = {
     "geo_gather_weighted_sum_bwd": (c_int, [c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64,
                                             c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "geo_idw_weights": (c_int, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "geo_idw_interpolate": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp,
+                                    c_vp, c_vp]),
     "geo_radius_count_dev": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_vp, c_i64, c_int,
                                      c_vp, c_vp, c_size, c_vp]),
     "geo_radius_count_async": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_vp, c_f32, c_f32, c_vp,

@@ -569,6 +569,28 @@ def idw_weights_hip(idx: Tensor, dist: Tensor) -> Tensor:
     return w
 
 
+def idw_interpolate_forward_hip(feat: Tensor, idx: Tensor, dist: Tensor) -> Tuple[Tensor, Tensor]:
+    """(out, w): the IDW weights of ``idw_weights_hip`` (float32) and the gather-sum of ``feat``
+    with them (rounded to feat's dtype), in one kernel; bitwise equal to the two calls."""
+    _require_gpu("idw_interpolate", feat, idx, dist)
+    if feat.dim() != 2 or idx.dim() != 2 or dist.shape != idx.shape:
+        raise ValueError(f"idw_interpolate: feat [N_src, C], idx and dist [N_out, K]; got "
+                         f"{tuple(feat.shape)}, {tuple(idx.shape)}, {tuple(dist.shape)}")
+    code = _dtype_code("idw_interpolate", feat)
+    dev = feat.device
+    feat = feat.contiguous()
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    dist = dist.to(device=dev, dtype=torch.float32).contiguous()
+    (N_src, C), (N_out, K) = feat.shape, idx.shape
+    out = torch.empty(N_out, C, dtype=feat.dtype, device=dev)
+    w = torch.empty(N_out, K, dtype=torch.float32, device=dev)
+    with _nat.on_device(dev):
+        _nat.check(_nat.lib().geo_idw_interpolate(
+            code, _nat.ptr(feat), N_src, C, _nat.ptr(idx), _nat.ptr(dist), N_out, K, _nat.ptr(out),
+            _nat.ptr(w), _nat.stream_of(dev)), "geo_idw_interpolate")
+    return out, w
+
+
 def knn_radius_stat_hip(dist: Tensor, col: int, mode: str, multiplier: float) -> Tensor:
     """multiplier * (mean of sqrt(clamp(d, 1e-8, 1e20)) | lower median of sqrt(max(d, 1e-12)))
     over column ``col`` of a KNN distance matrix, as a float64 device scalar (no host sync)."""
@@ -843,6 +865,7 @@ __all__ = [
     "segment_reduce_available", "sort_and_build_csr_cuda", "source_csr", "segment_reduce_sum_cuda",
     "segment_softmax_forward_hip", "segment_softmax_backward_hip",
     "gather_weighted_sum_forward_hip", "gather_weighted_sum_backward_hip", "idw_weights_hip",
+    "idw_interpolate_forward_hip",
     "knn_radius_stat_hip", "radius_graph_csr_hip", "edge_geometry_hip",
     "edge_geometry_backward_hip", "spherical_harmonics_hip", "spherical_harmonics_backward_hip",
     "graph_avg_degree_hip",

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kEgThreads) void edge_geom_kernel(
     float* __restrict__ dist, float* __restrict__ Y) {
   __shared__ float s_dir[3 * kEgThreads];
   __shared__ float s_y[9 * kEgThreads];
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads;
+  const int64_t e0 = xcd_block() * kEgThreads;  // one contiguous edge range per XCD: shared pos rows
   const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
   edge_geom_tile(pos, N, row, col, e0, cnt, max_l, c, dir, dist, Y, s_dir, s_y);
 }
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kEgThreads) void graph_epilogue_dev(
   __shared__ float s_y[9 * kEgThreads];
   int64_t E = row_ptr[N];
   E = E < 0 ? 0 : (E > cap ? cap : E);
-  for (int64_t e0 = static_cast<int64_t>(blockIdx.x) * kEgThreads; e0 < E;
+  for (int64_t e0 = xcd_block() * kEgThreads; e0 < E;
        e0 += static_cast<int64_t>(gridDim.x) * kEgThreads) {
     const int cnt = static_cast<int>(E - e0 < kEgThreads ? E - e0 : kEgThreads);
     edge_geom_tile(pos, N, row, col, e0, cnt, max_l, c, dir, dist, Y, s_dir, s_y);

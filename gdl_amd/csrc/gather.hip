@@ -11,6 +11,9 @@
 // Here it is one pass without the temporary.  A row of C features is read as 16-byte (or
 // narrower) vectors by L lanes, a wave holds R = 64/L output rows, and the K neighbour rows of
 // an output row are loaded together (all in flight at once) and summed in ascending k order.
+// Workgroups take their rows through xcd_block(): each XCD serves one contiguous range of
+// output rows (of source rows in the feature backward), so the feature rows gathered by the
+// points of one cloud are fetched from HBM into one XCD's L2 rather than into all eight.
 // geo_idw_weights computes the interpolation layer's inverse-distance weights
 // (equivariant_interp.py:95-99).  The backward is two kernels: grad_w[n, k] =
 // <grad_out[n], feat[idx[n, k]]> (one lane group per output row, a group-wide dot product) and
@@ -54,8 +57,21 @@ struct GwVec {
   __device__ __forceinline__ void store(T* p) const { *reinterpret_cast<typename GwRaw<VB>::type*>(p) = raw; }
 };
 
-// Weights of (equivariant_interp.py:95-99): inverse of sqrt(max(d, 1e-4)) for valid neighbours,
-// normalised by the row sum clamped at 1e-8.  One thread per output row.
+// Weights of (equivariant_interp.py:95-99): inverse of sqrt(max(d, 1e-4)) for valid neighbours
+// (idx >= 0), normalised by the row sum clamped at 1e-8.  One thread per output row; the fused
+// interpolation computes them with the same helpers in the same order.
+__device__ __forceinline__ float idw_inv(int64_t j, float d) {
+  return j >= 0 ? 1.0f / sqrtf(d < 1e-4f ? 1e-4f : d) : 0.0f;
+}
+__device__ __forceinline__ float idw_den(float sum) { return sum < 1e-8f ? 1e-8f : sum; }
+
+// The weight as the gather uses it: rounded to the feature type first, as the two-step path
+// converts the float32 weights to the features' dtype before the gather.
+template <typename T> __device__ __forceinline__ typename GwAcc<T>::type idw_as(float w);
+template <> __device__ __forceinline__ float idw_as<float>(float w) { return w; }
+template <> __device__ __forceinline__ float idw_as<uint16_t>(float w) { return bf16_to_f32(f32_to_bf16(w)); }
+template <> __device__ __forceinline__ double idw_as<double>(float w) { return static_cast<double>(w); }
+
 __global__ void idw_weights_kernel(const int64_t* __restrict__ idx, const float* __restrict__ dist,
                                    int64_t N_out, int K, float* __restrict__ w) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -67,22 +83,29 @@ __global__ void idw_weights_kernel(const int64_t* __restrict__ idx, const float*
 #pragma unroll
   for (int k = 0; k < kGwMaxK; ++k) {
     if (k < K) {
-      const float d = dr[k];
-      const float v = ir[k] >= 0 ? 1.0f / sqrtf(d < 1e-4f ? 1e-4f : d) : 0.0f;
+      const float v = idw_inv(ir[k], dr[k]);
       inv[k] = v;
       sum += v;
     }
   }
-  const float den = sum < 1e-8f ? 1e-8f : sum;
+  const float den = idw_den(sum);
 #pragma unroll
   for (int k = 0; k < kGwMaxK; ++k)
     if (k < K) w[n * K + k] = inv[k] / den;
 }
 
-template <typename T, int VB, int KK>
+// A wave serves RP blocks of R consecutive output rows, (wave * RP + r) * R + g for r < RP: with
+// RP > 1 (K <= 4) the neighbour rows of all RP rows of a lane group are requested together, so
+// more loads are in flight per wave and fewer waves are dispatched.  With `dist` (fused IDW
+// interpolation) the weights are computed from the squared distances instead of read from `w`,
+// once the group's first feature loads are in flight, and written to w_out (float32) by the
+// group's first lane.
+template <typename T, int VB, int KK, int RP>
 __global__ __launch_bounds__(kGwThreads) void gws_fwd_kernel(
     const T* __restrict__ feat, int64_t N_src, int64_t C, const int64_t* __restrict__ idx,
-    const T* __restrict__ w, int64_t N_out, int K, int vpr, int log_l, T* __restrict__ out) {
+    const T* __restrict__ w, int64_t N_out, int K, int vpr, int log_l, T* __restrict__ out,
+    const float* __restrict__ dist, float* __restrict__ w_out) {
+  static_assert(RP == 1 || KK <= 4, "several rows per group only for K <= 4");
   using A = typename GwAcc<T>::type;
   using V = GwVec<T, VB>;
   constexpr int EPV = V::EPV;
@@ -91,40 +114,130 @@ __global__ __launch_bounds__(kGwThreads) void gws_fwd_kernel(
   const int R = kWave >> log_l;
   const int g = lane >> log_l;
   const int vl = lane & (L - 1);
-  const int64_t n = (static_cast<int64_t>(blockIdx.x) * kGwWaves + threadIdx.x / kWave) * R + g;
-  if (n >= N_out) return;
-  int32_t src[KK];
-  A wk[KK];
+  const int64_t wb = (xcd_block() * kGwWaves + threadIdx.x / kWave) * RP;
+  int64_t n[RP];
 #pragma unroll
-  for (int k = 0; k < KK; ++k) {
-    const int64_t j = k < K ? idx[n * K + k] : -1;
-    const bool ok = j >= 0 && j < N_src;
-    src[k] = ok ? static_cast<int32_t>(j) : -1;
-    wk[k] = ok ? gw_to(w[n * K + k]) : A(0);
+  for (int r = 0; r < RP; ++r) n[r] = (wb + r) * R + g;
+  if (n[0] >= N_out) return;  // rows grow with r: nothing for this group
+  // src: the source row, -1 for idx < 0, -2 for idx >= N_src (a neighbour for the IDW weights,
+  // which count every idx >= 0, but none for the gather, which reads rows src >= 0 only)
+  int32_t src[RP][KK];
+  A wk[RP][KK];
+  float dk[RP][KK];   // fused IDW: the squared distances
+  // every load unconditional (row and column clamped into range, K >= 1, n[0] < N_out) and
+  // the values selected afterwards: a load under a per-lane condition becomes a branch and a
+  // wait for its data before the next load
+  // (in chunks of at most 8 neighbours, which bounds the registers the 64-bit indices hold)
+  auto at = [&](int r, int k) -> int64_t {
+    return (n[r] < N_out ? n[r] : n[0]) * K + (k < K ? k : K - 1);
+  };
+  constexpr int PC = KK < 8 ? KK : 8;
+#pragma unroll
+  for (int k0 = 0; k0 < KK; k0 += PC) {
+    int64_t jr[RP][PC];
+#pragma unroll
+    for (int r = 0; r < RP; ++r)
+#pragma unroll
+      for (int k = 0; k < PC; ++k) jr[r][k] = idx[at(r, k0 + k)];
+    if (dist == nullptr) {
+#pragma unroll
+      for (int r = 0; r < RP; ++r)
+#pragma unroll
+        for (int k = 0; k < PC; ++k) wk[r][k0 + k] = gw_to(w[at(r, k0 + k)]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < RP; ++r)
+#pragma unroll
+        for (int k = 0; k < PC; ++k) dk[r][k0 + k] = dist[at(r, k0 + k)];
+    }
+#pragma unroll
+    for (int r = 0; r < RP; ++r)
+#pragma unroll
+      for (int k = 0; k < PC; ++k) {
+        const bool in = k0 + k < K && n[r] < N_out;
+        const int64_t j = in ? jr[r][k] : -1;
+        const bool ok = j >= 0 && j < N_src;
+        src[r][k0 + k] = ok ? static_cast<int32_t>(j) : (j >= 0 ? -2 : -1);
+        if (dist == nullptr) {
+          wk[r][k0 + k] = ok ? wk[r][k0 + k] : A(0);
+        } else {
+          dk[r][k0 + k] = in ? dk[r][k0 + k] : 0.f;
+        }
+      }
   }
-  constexpr int KC = KK < 8 ? KK : 8;  // neighbour rows in flight at once
-  for (int vb = vl; vb < vpr; vb += L) {
-    const int64_t col = static_cast<int64_t>(vb) * EPV;
-    A acc[EPV];
+  // the IDW weights of the group's rows (geo_idw_weights' operations in its order); called
+  // once, after the first feature loads are issued
+  bool need_w = dist != nullptr;
+  auto idw_fill = [&]() {
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) acc[i] = A(0);
+    for (int r = 0; r < RP; ++r) {
+      float inv[KK];
+      float sum = 0.f;
 #pragma unroll
-    for (int k0 = 0; k0 < KK; k0 += KC) {
-      V buf[KC];
+      for (int k = 0; k < KK; ++k) {
+        inv[k] = k < K ? idw_inv(src[r][k] != -1 ? 0 : -1, dk[r][k]) : 0.f;
+        sum += inv[k];  // k < K only: the others add 0
+      }
+      const float den = idw_den(sum);
 #pragma unroll
-      for (int k = 0; k < KC; ++k)
-        buf[k].load(feat + static_cast<int64_t>(src[k0 + k] >= 0 ? src[k0 + k] : 0) * C + col);
-#pragma unroll
-      for (int k = 0; k < KC; ++k) {
-#pragma unroll
-        for (int i = 0; i < EPV; ++i)
-          acc[i] += src[k0 + k] >= 0 ? wk[k0 + k] * gw_to(buf[k].e[i]) : A(0);
+      for (int k = 0; k < KK; ++k) {
+        const float wf = inv[k] / den;
+        if (vl == 0 && k < K && n[r] < N_out) w_out[n[r] * K + k] = wf;
+        wk[r][k] = src[r][k] >= 0 ? idw_as<T>(wf) : A(0);
       }
     }
-    V res;
+    need_w = false;
+  };
+  constexpr int KC = KK < 8 ? KK : 8;  // neighbour rows in flight at once (RP == 1)
+  for (int vb = vl; vb < vpr; vb += L) {
+    const int64_t col = static_cast<int64_t>(vb) * EPV;
+    if constexpr (RP == 1) {
+      A acc[EPV];
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) res.e[i] = gw_from<T>(acc[i]);
-    res.store(out + n * C + col);
+      for (int i = 0; i < EPV; ++i) acc[i] = A(0);
+#pragma unroll
+      for (int k0 = 0; k0 < KK; k0 += KC) {
+        V buf[KC];
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+          buf[k].load(feat + static_cast<int64_t>(src[0][k0 + k] >= 0 ? src[0][k0 + k] : 0) * C + col);
+        if (need_w) idw_fill();
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+#pragma unroll
+          for (int i = 0; i < EPV; ++i)
+            acc[i] += src[0][k0 + k] >= 0 ? wk[0][k0 + k] * gw_to(buf[k].e[i]) : A(0);
+        }
+      }
+      V res;
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) res.e[i] = gw_from<T>(acc[i]);
+      res.store(out + n[0] * C + col);
+    } else {
+      V buf[RP][KK];
+#pragma unroll
+      for (int r = 0; r < RP; ++r)
+#pragma unroll
+        for (int k = 0; k < KK; ++k)
+          buf[r][k].load(feat + static_cast<int64_t>(src[r][k] >= 0 ? src[r][k] : 0) * C + col);
+      if (need_w) idw_fill();
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        A acc[EPV];
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) acc[i] = A(0);
+#pragma unroll
+        for (int k = 0; k < KK; ++k) {
+#pragma unroll
+          for (int i = 0; i < EPV; ++i)
+            acc[i] += src[r][k] >= 0 ? wk[r][k] * gw_to(buf[r][k].e[i]) : A(0);
+        }
+        V res;
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) res.e[i] = gw_from<T>(acc[i]);
+        if (n[r] < N_out) res.store(out + n[r] * C + col);
+      }
+    }
   }
 }
 
@@ -142,13 +255,14 @@ __global__ __launch_bounds__(kGwThreads) void gws_bwd_w_kernel(
   const int R = kWave >> log_l;
   const int g = lane >> log_l;
   const int vl = lane & (L - 1);
-  int64_t n = (static_cast<int64_t>(blockIdx.x) * kGwWaves + threadIdx.x / kWave) * R + g;
+  int64_t n = (xcd_block() * kGwWaves + threadIdx.x / kWave) * R + g;
   const bool live = n < N_out;  // dead groups still take part in the shuffles below
   if (!live) n = N_out - 1;
   int32_t src[KK];
 #pragma unroll
-  for (int k = 0; k < KK; ++k) {
-    const int64_t j = k < K ? idx[n * K + k] : -1;
+  for (int k = 0; k < KK; ++k) {  // unconditional loads (column clamped), values selected after
+    const int64_t jr = idx[n * K + (k < K ? k : K - 1)];
+    const int64_t j = k < K ? jr : -1;
     src[k] = (j >= 0 && j < N_src) ? static_cast<int32_t>(j) : -1;
   }
   A dot[KK];
@@ -202,7 +316,7 @@ __global__ __launch_bounds__(kGwThreads) void gws_bwd_feat_kernel(
   const int R = kWave >> log_l;
   const int g = lane >> log_l;
   const int vl = lane & (L - 1);
-  const int64_t j = (static_cast<int64_t>(blockIdx.x) * kGwWaves + threadIdx.x / kWave) * R + g;
+  const int64_t j = (xcd_block() * kGwWaves + threadIdx.x / kWave) * R + g;
   if (j >= N_src) return;
   const int64_t P = N_out * K;
   int64_t a = ns[j], b = ne[j];
@@ -269,32 +383,62 @@ int gw_zero(int dtype, void* p, int64_t n, hipStream_t st) {
   return device_fill<double>(static_cast<double*>(p), n, 0.0, st);
 }
 
-unsigned gw_blocks(int64_t rows, int log_l) {
-  const int64_t per_block = static_cast<int64_t>(kGwWaves) * (kWave >> log_l);
+unsigned gw_blocks(int64_t rows, int log_l, int rp = 1) {
+  const int64_t per_block = static_cast<int64_t>(kGwWaves) * (kWave >> log_l) * rp;
   return static_cast<unsigned>(ceil_div(rows, per_block));
 }
 
-// Dispatch on the vector width, then on K rounded up to 1, 2, 4, 8, 16 or 32 neighbours.
+// Dispatch on the vector width, then on K rounded up to 1, 2, 3, 4, 8, 16 or 32 neighbours.
 #define GEO_GW_K_SWITCH(KVAR, BODY)                   \
   do {                                                \
     if (KVAR <= 1) { constexpr int KK = 1; BODY; }    \
     else if (KVAR <= 2) { constexpr int KK = 2; BODY; } \
+    else if (KVAR <= 3) { constexpr int KK = 3; BODY; } \
     else if (KVAR <= 4) { constexpr int KK = 4; BODY; } \
     else if (KVAR <= 8) { constexpr int KK = 8; BODY; } \
     else if (KVAR <= 16) { constexpr int KK = 16; BODY; } \
     else { constexpr int KK = 32; BODY; }            \
   } while (0)
 
+// Output rows per lane group of the forward kernel: two when each wave would otherwise carry
+// little work (K <= 4) and enough waves remain to fill the chip (C2 interpolation, K = 3:
+// 14.5 -> 13.6 us; four rows per group 14.6 us).
+int gw_rows_per_group(int64_t N_out, int log_l, int K) {
+  if (K > 4) return 1;
+  const int64_t waves = ceil_div(N_out, static_cast<int64_t>(kWave >> log_l));  // at one row
+  return waves >= 2 * 8192 ? 2 : 1;
+}
+
+template <typename T, int VBV, int KK>
+void gws_fwd_launch(int rp, int log_l, hipStream_t st, const T* feat, int64_t N_src, int64_t C,
+                    const int64_t* idx, const T* w, int64_t N_out, int K, int vpr, T* out,
+                    const float* dist, float* w_out) {
+  if constexpr (KK <= 4) {
+    if (rp == 2) {
+      hipLaunchKernelGGL((gws_fwd_kernel<T, VBV, KK, 2>), dim3(gw_blocks(N_out, log_l, 2)),
+                         dim3(kGwThreads), 0, st, feat, N_src, C, idx, w, N_out, K, vpr, log_l, out,
+                         dist, w_out);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gws_fwd_kernel<T, VBV, KK, 1>), dim3(gw_blocks(N_out, log_l)),
+                     dim3(kGwThreads), 0, st, feat, N_src, C, idx, w, N_out, K, vpr, log_l, out,
+                     dist, w_out);
+}
+
+// The forward gather; with `dist` the IDW weights are computed in the kernel (w unused) and
+// written to w_out.
 template <typename T>
 int gws_fwd(const GwLayout& lay, const T* feat, int64_t N_src, int64_t C, const int64_t* idx,
-            const T* w, int64_t N_out, int K, T* out, hipStream_t st) {
-  const unsigned blocks = gw_blocks(N_out, lay.log_l);
+            const T* w, int64_t N_out, int K, T* out, hipStream_t st,
+            const float* dist = nullptr, float* w_out = nullptr) {
+  const int rp = gw_rows_per_group(N_out, lay.log_l, K);
 #define GEO_GW_FWD(VBV)                                                                      \
   case VBV:                                                                                  \
     if constexpr (VBV >= static_cast<int>(sizeof(T))) {                                      \
-      GEO_GW_K_SWITCH(K, hipLaunchKernelGGL((gws_fwd_kernel<T, VBV, KK>), dim3(blocks),      \
-                                            dim3(kGwThreads), 0, st, feat, N_src, C, idx, w, \
-                                            N_out, K, lay.vpr, lay.log_l, out));              \
+      GEO_GW_K_SWITCH(K, (gws_fwd_launch<T, VBV, KK>(rp, lay.log_l, st, feat, N_src, C, idx, \
+                                                      w, N_out, K, lay.vpr, out, dist,       \
+                                                      w_out)));                              \
     }                                                                                        \
     break;
   switch (lay.vb) {
@@ -382,6 +526,34 @@ extern "C" int geo_gather_weighted_sum(int dtype, const void* feat, int64_t N_sr
                              static_cast<const uint16_t*>(w), N_out, k, static_cast<uint16_t*>(out), st);
   return gws_fwd<double>(lay, static_cast<const double*>(feat), N_src, C, idx,
                          static_cast<const double*>(w), N_out, k, static_cast<double*>(out), st);
+}
+
+extern "C" int geo_idw_interpolate(int dtype, const void* feat, int64_t N_src, int64_t C,
+                                   const int64_t* idx, const float* dist, int64_t N_out, int64_t K,
+                                   void* out, float* w_out, void* stream) {
+  int rc = gw_check(dtype, N_src, C, N_out, K);
+  if (rc) return rc;
+  if (N_out == 0) return GEO_OK;
+  GEO_REQUIRE(idx && dist && w_out, "idw_interpolate: null idx, dist or w_out");
+  GEO_REQUIRE(C == 0 || out != nullptr, "idw_interpolate: null output");
+  hipStream_t st = as_stream(stream);
+  if (K == 0 || N_src == 0 || C == 0) {  // the weights alone, as geo_idw_weights computes them
+    rc = geo_idw_weights(idx, dist, N_out, K, w_out, stream);
+    if (rc || C == 0) return rc;
+    return gw_zero(dtype, out, N_out * C, st);
+  }
+  GEO_REQUIRE(feat != nullptr, "idw_interpolate: null feat");
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(feat) | reinterpret_cast<uintptr_t>(out);
+  const GwLayout lay = gw_layout(C, gw_esize(dtype), bits);
+  const int k = static_cast<int>(K);
+  if (dtype == GEO_F32)
+    return gws_fwd<float>(lay, static_cast<const float*>(feat), N_src, C, idx, nullptr, N_out, k,
+                          static_cast<float*>(out), st, dist, w_out);
+  if (dtype == GEO_BF16)
+    return gws_fwd<uint16_t>(lay, static_cast<const uint16_t*>(feat), N_src, C, idx, nullptr, N_out,
+                             k, static_cast<uint16_t*>(out), st, dist, w_out);
+  return gws_fwd<double>(lay, static_cast<const double*>(feat), N_src, C, idx, nullptr, N_out, k,
+                         static_cast<double*>(out), st, dist, w_out);
 }
 
 extern "C" int geo_gather_weighted_sum_bwd(int dtype, const void* grad_out, const void* feat,

@@ -22,6 +22,7 @@ from torch import Tensor
 from gdl_amd.csrc import (
     gather_weighted_sum_backward_hip,
     gather_weighted_sum_forward_hip,
+    idw_interpolate_forward_hip,
     idw_weights_hip,
 )
 
@@ -43,6 +44,23 @@ class _GatherWeightedSum(torch.autograd.Function):
         return gf, None, gw
 
 
+class _IdwInterpolate(torch.autograd.Function):
+    """IDW weights and gather-sum in one kernel; the weights (functions of the KNN distances
+    alone, which carry no gradient here, as in the two-step path) are kept for the backward."""
+
+    @staticmethod
+    def forward(ctx, feat, idx, dist):
+        out, w = idw_interpolate_forward_hip(feat, idx, dist)
+        ctx.save_for_backward(feat, idx, w.to(feat.dtype))
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        feat, idx, w = ctx.saved_tensors
+        gf, _ = gather_weighted_sum_backward_hip(grad, feat, idx, w, True, False)
+        return gf, None, None
+
+
 def gather_weighted_sum(feat: Tensor, idx: Tensor, w: Tensor) -> Tensor:
     """``out[n] = sum_k w[n, k] * feat[idx[n, k]]`` for ``feat [N_src, ...]``, ``idx, w
     [N_out, K]``; returns ``[N_out, ...]`` in ``feat``'s dtype."""
@@ -58,6 +76,10 @@ def idw_weights(idx: Tensor, dist: Tensor) -> Tensor:
 
 
 def knn_interpolate(feat: Tensor, idx: Tensor, dist: Tensor, weights: Optional[Tensor] = None) -> Tensor:
-    """IDW interpolation of ``feat`` at the query points of a KNN result (idx, squared dist)."""
-    w = idw_weights(idx, dist) if weights is None else weights
-    return gather_weighted_sum(feat, idx, w)
+    """IDW interpolation of ``feat`` at the query points of a KNN result (idx, squared dist).
+    Without ``weights`` the inverse-distance weights and the gather-sum run as one kernel."""
+    if weights is not None:
+        return gather_weighted_sum(feat, idx, weights)
+    shape = feat.shape
+    out = _IdwInterpolate.apply(feat.reshape(shape[0], -1), idx, dist.detach())
+    return out.reshape((idx.shape[0],) + tuple(shape[1:]))

@@ -334,6 +334,15 @@ int geo_gather_weighted_sum_bwd(int dtype, const void* grad_out, const void* fea
  */
 int geo_idw_weights(const int64_t* idx, const float* dist, int64_t N_out, int64_t K, float* w,
                     void* stream);
+/*
+ * The interpolation layer's whole forward (equivariant_interp.py:95-125) in one launch: the IDW
+ * weights of geo_idw_weights, written to w_out (fp32 [N_out, K], for the backward), and the
+ * gather-sum of geo_gather_weighted_sum with those weights rounded to `dtype`, bitwise equal
+ * to the two calls in turn.
+ */
+int geo_idw_interpolate(int dtype, const void* feat, int64_t N_src, int64_t C,
+                        const int64_t* idx, const float* dist, int64_t N_out, int64_t K,
+                        void* out, float* w_out, void* stream);
 
 /* ----------------------------------------------- spatial-graph edge epilogue --- */
 /*

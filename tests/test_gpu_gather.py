@@ -34,8 +34,11 @@ def _close(got, ref, scale, dtype):
     assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) - bound))
 
 
+# the last two shapes are large enough for two output rows per lane group (the kernel's choice
+# when K <= 4 and at least 16384 waves would run at one row each)
 @pytest.mark.parametrize("Ns,No,K,C", [(1, 1, 1, 1), (100, 60, 3, 5), (3000, 5000, 8, 64),
-                                       (2000, 3000, 16, 112), (500, 700, 32, 13), (4000, 4000, 3, 300)])
+                                       (2000, 3000, 16, 112), (500, 700, 32, 13), (4000, 4000, 3, 300),
+                                       (9000, 40001, 3, 112), (3000, 70001, 2, 64)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
 def test_gather_weighted_sum_vs_oracle(dev, Ns, No, K, C, dtype):
     gws, _, _ = _f()
@@ -100,3 +103,37 @@ def test_gather_gradcheck_fp64(dev):
     f = torch.randn(20, 3, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
     w = torch.randn(15, 4, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
     assert torch.autograd.gradcheck(lambda a, b: gws(a, idx, b), (f, w))
+
+
+@pytest.mark.parametrize("No,K,C", [(1, 1, 1), (777, 3, 112), (40001, 3, 112), (5000, 4, 48),
+                                    (3000, 8, 64), (2000, 16, 20), (600, 32, 7), (70001, 2, 64)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float64])
+def test_fused_idw_interpolate_bitwise_vs_two_calls(dev, No, K, C, dtype):
+    """knn_interpolate without weights runs IDW weights + gather-sum as one kernel: output,
+    weights and feature gradient bitwise equal to idw_weights then gather_weighted_sum, with
+    padding (-1), indices past the sources (weighted by IDW, skipped by the gather), zero and
+    huge distances."""
+    from geoembodied.csrc import idw_interpolate_forward_hip
+    gws, idw, knn_interp = _f()
+    Ns = 3000
+    g = torch.Generator().manual_seed(No + K + C)
+    idx = torch.randint(-1, Ns + 5, (No, K), generator=g)
+    dist = torch.rand(No, K, generator=g) * 0.05
+    dist[:, 0] = torch.where(torch.rand(No, generator=g) < 0.05, 0.0, dist[:, 0])
+    dist[: max(1, No // 50)] = 1e30
+    idx[-max(1, No // 40):] = -1
+    feat = torch.randn(Ns, C, generator=g, dtype=torch.float64).to(dtype).to(dev)
+    idx, dist = idx.to(dev), dist.to(dev)
+    out_f, w_f = idw_interpolate_forward_hip(feat, idx, dist)
+    w_2 = idw(idx, dist)
+    assert torch.equal(w_f, w_2)
+    assert torch.equal(out_f, gws(feat, idx, w_2))
+    fa = feat.clone().requires_grad_(True)
+    fb = feat.clone().requires_grad_(True)
+    out_a = knn_interp(fa, idx, dist)
+    out_b = gws(fb, idx, idw(idx, dist))
+    assert torch.equal(out_a, out_b)
+    go = torch.randn(No, C, generator=g, dtype=torch.float64).to(dtype).to(dev)
+    out_a.backward(go)
+    out_b.backward(go)
+    assert torch.equal(fa.grad, fb.grad)
