@@ -435,16 +435,24 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
 #pragma unroll
       for (int c = 0; c < KC; ++c) rk[q][c] = r[q * KC + c];
   }
+  // unconditional loads (a lane without a row reads row 0, E >= 1) and the values selected
+  // after: loads under a per-lane condition leave the compiler's wait counting unsure which
+  // are still in flight, and it then waits before later stores
 #pragma unroll
   for (int q = 0; q < SQ; ++q)
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      if (rk[q][c] >= 0) sm_load<HH>(x, rk[q][c], v[q][c]);
-      else
+    for (int c = 0; c < KC; ++c) sm_load<HH>(x, rk[q][c] >= 0 ? rk[q][c] : 0, v[q][c]);
 #pragma unroll
-        for (int h = 0; h < HH; ++h) v[q][c][h] = 0.f;
-    }
+  for (int q = 0; q < SQ; ++q)
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int h = 0; h < HH; ++h) v[q][c][h] = rk[q][c] >= 0 ? v[q][c][h] : 0.f;
 
+  // Register-held chunks (c < KC) and the tail of longer segments (c >= KC, rows loaded again
+  // per pass) are walked by separate loops, in the same chunk order: the outputs of the register
+  // chunks are computed first and stored back to back (interleaving each store with the next
+  // chunk's divisions made the compiler wait for every store before the next chunk).
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
     const int nch = uniform_max((b[q] - a[q] + LW - 1) / LW);
@@ -457,20 +465,19 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
     float m[HH], z[HH];
 #pragma unroll
     for (int h = 0; h < HH; ++h) { m[h] = -__builtin_inff(); z[h] = 0.f; }
-    for (int c = 0; c < nch; ++c) {
-      float t[HH];
-      int r;
-      if (c < KC) {
-        r = rk[q][c];
 #pragma unroll
-        for (int h = 0; h < HH; ++h) t[h] = v[q][c][h];
-      } else {
-        r = row_of(c);
-        if (r >= 0) sm_load<HH>(x, r, t);
-      }
-      if (r >= 0)
+    for (int c = 0; c < KC; ++c)
+      if (rk[q][c] >= 0)
+#pragma unroll
+        for (int h = 0; h < HH; ++h) m[h] = v[q][c][h] > m[h] ? v[q][c][h] : m[h];
+    for (int c = KC; c < nch; ++c) {
+      const int r = row_of(c);
+      if (r >= 0) {
+        float t[HH];
+        sm_load<HH>(x, r, t);
 #pragma unroll
         for (int h = 0; h < HH; ++h) m[h] = t[h] > m[h] ? t[h] : m[h];
+      }
     }
 #pragma unroll
     for (int h = 0; h < HH; ++h) m[h] = grp_maxf<LW>(m[h]);
@@ -480,19 +487,18 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
       if (c < nch)
 #pragma unroll
         for (int h = 0; h < HH; ++h) v[q][c][h] = expf(v[q][c][h] - m[h]);
-    for (int c = 0; c < nch; ++c) {
-      if (c < KC) {
-        if (rk[q][c] >= 0)
 #pragma unroll
-          for (int h = 0; h < HH; ++h) z[h] += v[q][c][h];
-      } else {
-        const int r = row_of(c);
-        if (r >= 0) {
-          float t[HH];
-          sm_load<HH>(x, r, t);
+    for (int c = 0; c < KC; ++c)
+      if (rk[q][c] >= 0)
 #pragma unroll
-          for (int h = 0; h < HH; ++h) z[h] += expf(t[h] - m[h]);
-        }
+        for (int h = 0; h < HH; ++h) z[h] += v[q][c][h];
+    for (int c = KC; c < nch; ++c) {
+      const int r = row_of(c);
+      if (r >= 0) {
+        float t[HH];
+        sm_load<HH>(x, r, t);
+#pragma unroll
+        for (int h = 0; h < HH; ++h) z[h] += expf(t[h] - m[h]);
       }
     }
 #pragma unroll
@@ -500,27 +506,32 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_fwd(
       const float zz = grp_sumf<LW>(z[h]);
       z[h] = zz < 1e-8f ? 1e-8f : zz;  // clamp(min=1e-8) keeps NaN, as torch's does
     }
-    for (int c = 0; c < nch; ++c) {
-      float o[HH];
-      if (c < KC) {
-        if (rk[q][c] < 0) continue;
 #pragma unroll
-        for (int h = 0; h < HH; ++h) o[h] = v[q][c][h] / z[h];
-        sm_store<HH>(w, rk[q][c], o);
-      } else {
-        const int r = row_of(c);
-        if (r < 0) continue;
-        float t[HH];
-        sm_load<HH>(x, r, t);
+    for (int c = 0; c < KC; ++c)
+      if (c < nch)  // wave-uniform: chunks past the wave's longest segment hold no row
 #pragma unroll
-        for (int h = 0; h < HH; ++h) o[h] = expf(t[h] - m[h]) / z[h];
-        sm_store<HH>(w, r, o);
-      }
+        for (int h = 0; h < HH; ++h) v[q][c][h] = v[q][c][h] / z[h];
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      if (rk[q][c] >= 0) sm_store<HH>(w, rk[q][c], v[q][c]);
+    for (int c = KC; c < nch; ++c) {
+      const int r = row_of(c);
+      if (r < 0) continue;
+      float t[HH], o[HH];
+      sm_load<HH>(x, r, t);
+#pragma unroll
+      for (int h = 0; h < HH; ++h) o[h] = expf(t[h] - m[h]) / z[h];
+      sm_store<HH>(w, r, o);
     }
   }
   zero_rows_from<float>(w, perm, t0, E, HH);
 }
 
+// Backward: the first KC chunks of a segment's rows (g and w) are loaded once into registers
+// with all their loads in flight, the dot product is summed in chunk order, and their outputs
+// are computed before any is stored; longer segments walk the remaining chunks twice (dot, then
+// outputs).  On this GPU loads and stores share one counter, so a load issued after a store
+// waits for that store too: interleaving per-chunk loads and stores serialised them.
 template <int HH, int LW>
 __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
     const float* __restrict__ g_, const float* __restrict__ w, const int32_t* __restrict__ perm,
@@ -528,27 +539,46 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
     float* __restrict__ dx, int zero_tail) {
   const int t0 = tail_start(zero_tail, ne, E, S);
   constexpr int SQ = sm_quads<HH, LW>();
+  constexpr int KC = 32 / LW;
   const int li = lane_id() & (LW - 1);
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kSmThreads / kWave) + threadIdx.x / kWave;
-  int a[SQ], b[SQ], r0[SQ];
-  float g0[SQ][HH], w0[SQ][HH];
+  int a[SQ], b[SQ], rk[SQ][KC];
+  float gv[SQ][KC][HH], wv[SQ][KC][HH];
 #pragma unroll
   for (int q = 0; q < SQ; ++q) sm_bounds<LW>(ns, ne, E, S, wave * SQ + q, a[q], b[q]);
+  {
+    int e[SQ * KC], r[SQ * KC];
+    bool ok[SQ * KC];
 #pragma unroll
-  for (int q = 0; q < SQ; ++q) {
-    const int e = a[q] + li;
-    r0[q] = e < b[q] ? sm_row(perm, E, e) : -1;
+    for (int q = 0; q < SQ; ++q)
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        e[q * KC + c] = a[q] + LW * c + li;
+        ok[q * KC + c] = e[q * KC + c] < b[q];
+      }
+    sm_rows<SQ * KC>(perm, E, e, ok, r);
+#pragma unroll
+    for (int q = 0; q < SQ; ++q)
+#pragma unroll
+      for (int c = 0; c < KC; ++c) rk[q][c] = r[q * KC + c];
   }
 #pragma unroll
-  for (int q = 0; q < SQ; ++q) {
-    if (r0[q] >= 0) {
-      sm_load<HH>(g_, r0[q], g0[q]);
-      sm_load<HH>(w, r0[q], w0[q]);
-    } else {
+  for (int q = 0; q < SQ; ++q)
 #pragma unroll
-      for (int h = 0; h < HH; ++h) { g0[q][h] = 0.f; w0[q][h] = 0.f; }
+    for (int c = 0; c < KC; ++c) {  // unconditional, as in the forward
+      const int r = rk[q][c] >= 0 ? rk[q][c] : 0;
+      sm_load<HH>(g_, r, gv[q][c]);
+      sm_load<HH>(w, r, wv[q][c]);
     }
-  }
+#pragma unroll
+  for (int q = 0; q < SQ; ++q)
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int h = 0; h < HH; ++h) {
+        gv[q][c][h] = rk[q][c] >= 0 ? gv[q][c][h] : 0.f;
+        wv[q][c][h] = rk[q][c] >= 0 ? wv[q][c][h] : 0.f;
+      }
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
     const int nch = uniform_max((b[q] - a[q] + LW - 1) / LW);
@@ -558,38 +588,39 @@ __global__ __launch_bounds__(kSmThreads) void seg_softmax_vec_bwd(
     };
     float dot[HH];
 #pragma unroll
-    for (int h = 0; h < HH; ++h) {
-      dot[h] = 0.f;
-      if (r0[q] >= 0) dot[h] += g0[q][h] * w0[q][h];
-    }
-    for (int c = 1; c < nch; ++c) {
+    for (int h = 0; h < HH; ++h) dot[h] = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      if (rk[q][c] >= 0)
+#pragma unroll
+        for (int h = 0; h < HH; ++h) dot[h] += gv[q][c][h] * wv[q][c][h];
+    for (int c = KC; c < nch; ++c) {
       const int r = row_of(c);
       if (r < 0) continue;
-      float gv[HH], wv[HH];
-      sm_load<HH>(g_, r, gv);
-      sm_load<HH>(w, r, wv);
+      float gt[HH], wt[HH];
+      sm_load<HH>(g_, r, gt);
+      sm_load<HH>(w, r, wt);
 #pragma unroll
-      for (int h = 0; h < HH; ++h) dot[h] += gv[h] * wv[h];
+      for (int h = 0; h < HH; ++h) dot[h] += gt[h] * wt[h];
     }
 #pragma unroll
     for (int h = 0; h < HH; ++h) dot[h] = grp_sumf<LW>(dot[h]);
-    for (int c = 0; c < nch; ++c) {
-      float o[HH];
-      if (c == 0) {
-        if (r0[q] < 0) continue;
 #pragma unroll
-        for (int h = 0; h < HH; ++h) o[h] = w0[q][h] * (g0[q][h] - dot[h]);
-        sm_store<HH>(dx, r0[q], o);
-      } else {
-        const int r = row_of(c);
-        if (r < 0) continue;
-        float gv[HH], wv[HH];
-        sm_load<HH>(g_, r, gv);
-        sm_load<HH>(w, r, wv);
+    for (int c = 0; c < KC; ++c)
 #pragma unroll
-        for (int h = 0; h < HH; ++h) o[h] = wv[h] * (gv[h] - dot[h]);
-        sm_store<HH>(dx, r, o);
-      }
+      for (int h = 0; h < HH; ++h) gv[q][c][h] = wv[q][c][h] * (gv[q][c][h] - dot[h]);
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      if (rk[q][c] >= 0) sm_store<HH>(dx, rk[q][c], gv[q][c]);
+    for (int c = KC; c < nch; ++c) {
+      const int r = row_of(c);
+      if (r < 0) continue;
+      float gt[HH], wt[HH], o[HH];
+      sm_load<HH>(g_, r, gt);
+      sm_load<HH>(w, r, wt);
+#pragma unroll
+      for (int h = 0; h < HH; ++h) o[h] = wt[h] * (gt[h] - dot[h]);
+      sm_store<HH>(dx, r, o);
     }
   }
   zero_rows_from<float>(dx, perm, t0, E, HH);
