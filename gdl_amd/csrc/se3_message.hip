@@ -568,10 +568,45 @@ struct SeFused {
   const uint8_t* mask;
 };
 
+// The k loop of the tile GEMMs (K a multiple of 16): 16-wide chunks, four per step and then
+// the remaining one to three, each step's fragments all requested before its MFMAs.  la(k) /
+// lw(k) return this lane's A / W fragment at column k.  (Loading four chunks and skipping the
+// MFMAs of those past K let the compiler sink each chunk's loads behind its test, so every chunk
+// waited for its own loads.)  The accumulation order is chunk by chunk, q = 0..3 within each.
+template <int NC, class LA, class LW>
+__device__ __forceinline__ floatx4 mfma_k_step(const LA& la, const LW& lw, int k0, floatx4 acc) {
+  floatx4 a[NC], w[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    w[c] = lw(k0 + 16 * c);
+    a[c] = la(k0 + 16 * c);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
+  return acc;
+}
+
+template <class LA, class LW>
+__device__ __forceinline__ floatx4 mfma_k_loop(const LA& la, const LW& lw, int K) {
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  int k0 = 0;
+  for (; k0 + 64 <= K; k0 += 64) acc = mfma_k_step<4>(la, lw, k0, acc);
+  switch ((K - k0) >> 4) {  // wave-uniform
+    case 3: acc = mfma_k_step<3>(la, lw, k0, acc); break;
+    case 2: acc = mfma_k_step<2>(la, lw, k0, acc); break;
+    case 1: acc = mfma_k_step<1>(la, lw, k0, acc); break;
+    default: break;
+  }
+  return acc;
+}
+
 // The tile's MFMA blocks of one kind: block b (< G ceil(O / 16)) is row block b / ncb, column
 // block b % ncb; wave w takes the blocks whose running number base + b is w mod 4.  The
 // epilogue's per-row operands are requested first and the weight fragments four 16-wide k chunks
-// at a time, so a block waits for global memory about once per 64 k instead of once per chunk.
+// at a time (mfma_k_loop), so a block waits for global memory about once per 64 k.
 // (Holding a column block's weights for all G row blocks needs G accumulators and per-row
 // operands at once: 147 VGPRs for the whole kernel, whose walk then ran at a lower occupancy.)
 template <int G>
@@ -585,35 +620,38 @@ __device__ __forceinline__ void fused_gemm(const float* __restrict__ tile, int l
   for (int b = (wave - base % kSeWaves + kSeWaves) % kSeWaves; b < nblk; b += kSeWaves) {
     const int rb = b / ncb, cb = b % ncb;
     const int o = cb * 16 + li;
-    const float bo = (G == 1 && p.bias && o < O) ? p.bias[o] : 0.f;
+    // bias, degrees and mask loaded without per-lane conditions (indices clamped into range,
+    // values selected after; the pointer tests are uniform): a load under a per-lane condition
+    // left the compiler waiting for all memory operations, earlier stores included, before
+    // each output store
+    float bo = 0.f;
+    if (G == 1 && p.bias) {
+      const float bl = p.bias[o < O ? o : O - 1];
+      bo = o < O ? bl : 0.f;
+    }
     float scale[4];
     bool keep[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t n = node0 + (rb * 16 + 4 * lk + q) / G;
       const bool in = n < N;
-      scale[q] = (in && p.avg) ? 1.0f / p.avg[n] : 1.0f;
-      keep[q] = !in || p.mask == nullptr || p.mask[n] != 0;
+      const int64_t nc = in ? n : N - 1;
+      float av = 1.0f;
+      if (p.avg) av = p.avg[nc];
+      scale[q] = (in && p.avg) ? 1.0f / av : 1.0f;
+      bool mk = true;
+      if (p.mask) mk = p.mask[nc] != 0;
+      keep[q] = !in || mk;
     }
     const float* ap = tile + (rb * 16 + li) * ld + 4 * lk;
     const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += 64) {
-      floatx4 a[4], w[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
-        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
-        a[c] = *reinterpret_cast<const floatx4*>(ap + k);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (k0 + 16 * c >= K) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
-      }
-    }
+    const floatx4 acc = mfma_k_loop(
+        [&](int k) { return *reinterpret_cast<const floatx4*>(ap + k); },
+        [&](int k) { return *reinterpret_cast<const floatx4*>(bp + k); }, K);
+    // every load of the block has completed here (the k loop waited for its later ones); the
+    // explicit wait, free at this point, tells the compiler so, which otherwise waited for all
+    // memory operations, the previous store included, before each store below
+    __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = rb * 16 + 4 * lk + q;  // tile row: node r / G, component r % G
@@ -1658,23 +1696,9 @@ __device__ __forceinline__ void lds_gemm(const float* A, int lda, int K, const f
     const int rb = b / ncb, cb = b % ncb;
     const float* ap = A + (rb * 16 + li) * lda + 4 * lk;
     const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += 64) {
-      floatx4 a[4], w[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
-        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
-        a[c] = *reinterpret_cast<const floatx4*>(ap + k);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (k0 + 16 * c >= K) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
-      }
-    }
+    const floatx4 acc = mfma_k_loop(
+        [&](int k) { return *reinterpret_cast<const floatx4*>(ap + k); },
+        [&](int k) { return *reinterpret_cast<const floatx4*>(bp + k); }, K);
 #pragma unroll
     for (int q = 0; q < 4; ++q) out[(rb * 16 + 4 * lk + q) * ldo + cb * 16 + li] = acc[q];
   }
@@ -1693,25 +1717,15 @@ __device__ __forceinline__ void lds_gemm_ga(__amdgpu_buffer_rsrc_t ra, int64_t r
     const int rb = b / ncb, cb = b % ncb;
     const uint32_t arow = static_cast<uint32_t>((row0 + rb * 16 + li) * K * 4 + 16 * lk);
     const float* bp = W + static_cast<int64_t>(cb * 16 + li) * K + 4 * lk;
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += 64) {
-      floatx4 a[4], w[4];
+    const floatx4 acc = mfma_k_loop(
+        [&](int k) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, arow + 4u * k, 0, 0);
+          floatx4 a;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int k = min(k0 + 16 * c, K - 16);  // chunks past K reload the last one (unused)
-        w[c] = *reinterpret_cast<const floatx4*>(bp + k);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, arow + 4u * k, 0, 0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) a[c][q] = __uint_as_float(v[q]);  // element by value
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (k0 + 16 * c >= K) break;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][q], w[c][q], acc, 0, 0, 0);
-      }
-    }
+          for (int q = 0; q < 4; ++q) a[q] = __uint_as_float(v[q]);  // element by value
+          return a;
+        },
+        [&](int k) { return *reinterpret_cast<const floatx4*>(bp + k); }, K);
 #pragma unroll
     for (int q = 0; q < 4; ++q) out[(rb * 16 + 4 * lk + q) * ldo + cb * 16 + li] = acc[q];
   }
