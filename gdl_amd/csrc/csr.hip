@@ -34,11 +34,16 @@ __global__ __launch_bounds__(kRxThreads) void csr_bounds_runs(const int32_t* __r
     const int64_t wbase = tile * kRxTile + static_cast<int64_t>(w) * kRxWaveSpan;
     if (wbase > E) continue;  // wave-uniform
     const int64_t before = wbase > 0 ? static_cast<int64_t>(sorted_keys[wbase - 1]) : -1;
+    uint32_t kv[kRxItems];  // clamped, unconditional loads, then the selects and LDS writes
 #pragma unroll
     for (int i = 0; i < kRxItems; ++i) {
       const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
-      if (idx <= E) s_keys[w][i * kWave + lane] = idx < E ? static_cast<uint32_t>(sorted_keys[idx])
-                                                          : static_cast<uint32_t>(N);
+      kv[i] = static_cast<uint32_t>(sorted_keys[idx < E ? idx : E - 1]);
+    }
+#pragma unroll
+    for (int i = 0; i < kRxItems; ++i) {
+      const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
+      if (idx <= E) s_keys[w][i * kWave + lane] = idx < E ? kv[i] : static_cast<uint32_t>(N);
     }
     wave_lds_fence();
     const int cnt = static_cast<int>(min(static_cast<int64_t>(kRxWaveSpan), E + 1 - wbase));

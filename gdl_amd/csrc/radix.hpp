@@ -224,11 +224,16 @@ __global__ __launch_bounds__(kRxThreads) void radix_hist(const void* __restrict_
     }
     const int64_t wbase = tile * kRxTile + static_cast<int64_t>(w) * kRxWaveSpan;
     uint32_t key[kRxItems];
+    // loads at clamped positions, values selected after: a load under a per-lane condition
+    // became a branch and a wait before the next load
 #pragma unroll
     for (int i = 0; i < kRxItems; ++i) {
       const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
-      key[i] = idx < n ? rx_fetch_key<SRC>(keys, idx, N) : 0u;
+      key[i] = rx_fetch_key<SRC>(keys, idx < n ? idx : n - 1, N);
     }
+#pragma unroll
+    for (int i = 0; i < kRxItems; ++i)
+      key[i] = wbase + static_cast<int64_t>(i) * kWave + lane < n ? key[i] : 0u;
     uint32_t before = 0u;  // key preceding the wave's range
     if (det.unsorted != nullptr && lane == 0 && wbase > 0 && wbase < n)
       before = rx_fetch_key<SRC>(keys, wbase - 1, N);
@@ -331,15 +336,21 @@ __global__ __launch_bounds__(kRxThreads) void radix_scatter(
     const int64_t wbase = tile * kRxTile + static_cast<int64_t>(w) * kRxWaveSpan;
     uint32_t key[kRxItems], val[kRxItems], rank[kRxItems];
 #pragma unroll
-    for (int i = 0; i < kRxItems; ++i) {
+    for (int i = 0; i < kRxItems; ++i) {  // clamped, unconditional loads (as in radix_hist)
       const int64_t idx = wbase + static_cast<int64_t>(i) * kWave + lane;
-      const bool valid = idx < n;
-      key[i] = valid ? rx_fetch_key<SRC>(keys_in, idx, N) : 0u;
+      const int64_t ic = idx < n ? idx : n - 1;
+      key[i] = rx_fetch_key<SRC>(keys_in, ic, N);
       if constexpr (SRC == kRxPairs) {
-        val[i] = valid ? vals_in[idx] : 0u;
+        val[i] = vals_in[ic];
       } else {
         val[i] = static_cast<uint32_t>(idx);
       }
+    }
+#pragma unroll
+    for (int i = 0; i < kRxItems; ++i) {
+      const bool valid = wbase + static_cast<int64_t>(i) * kWave + lane < n;
+      key[i] = valid ? key[i] : 0u;
+      if constexpr (SRC == kRxPairs) val[i] = valid ? val[i] : 0u;
     }
     __syncthreads();
     // stable rank among the wave's keys of the same digit, in (item, lane) = index order
@@ -476,6 +487,8 @@ template <int SRC>
 int radix_sort(const void* keys, const uint32_t* vals, int64_t n, int64_t N, uint32_t* keys_out,
                uint32_t* vals_out, const RadixBuffers& r, hipStream_t st,
                const RxDetect* detect = nullptr) {
+  if (n <= 0)  // the kernels clamp positions into [0, n)
+    return set_error(GEO_ERR_INVALID, "radix_sort: needs at least one key (n=%lld)", (long long)n);
   if (SRC == kRxPairs && detect != nullptr)
     return set_error(GEO_ERR_INVALID, "radix_sort: sorted-input detection needs index values");
   const RxPlan& plan = r.plan;
