@@ -78,14 +78,28 @@ __global__ void idw_weights_kernel(const int64_t* __restrict__ idx, const float*
   if (n >= N_out) return;
   const int64_t* ir = idx + n * K;
   const float* dr = dist + n * K;
+  // loads in chunks of eight at clamped columns, values used for k < K only (a load under
+  // `k < K` became a branch and a wait before the next one)
   float inv[kGwMaxK];
   float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < kGwMaxK; ++k) {
-    if (k < K) {
-      const float v = idw_inv(ir[k], dr[k]);
-      inv[k] = v;
-      sum += v;
+  for (int k0 = 0; k0 < kGwMaxK; k0 += 8) {
+    if (k0 >= K) break;  // uniform across the chunk's loads
+    int64_t jv[8];
+    float dv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int kc = k0 + k < K ? k0 + k : K - 1;
+      jv[k] = ir[kc];
+      dv[k] = dr[kc];
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k0 + k < K) {
+        const float v = idw_inv(jv[k], dv[k]);
+        inv[k0 + k] = v;
+        sum += v;
+      }
     }
   }
   const float den = idw_den(sum);
