@@ -358,22 +358,26 @@ __global__ __launch_bounds__(THREADS) void fps_bucket_kernel(
   //    the SIMDs); slot s of wave w holds bucket s*WAVES + w.
   float px[PTS], py[PTS], pz[PTS], md[PTS];
   uint32_t oi[PTS];
+  // loads at clamped slots, values selected after (a load under `q < n` became a branch and a
+  // wait before the next slot's)
 #pragma unroll
   for (int s = 0; s < PTS; ++s) {
     const int q = (s * WAVES + w) * kWave + lane;
-    if (q < n) {
-      const int i = order[q];
-      oi[s] = static_cast<uint32_t>(i);
-      px[s] = P[3 * i]; py[s] = P[3 * i + 1]; pz[s] = P[3 * i + 2];
-      md[s] = __builtin_inff();
-    } else {
-      oi[s] = 0xffffffffu;
-      px[s] = py[s] = pz[s] = 0.f;
-      md[s] = 0.f;  // padding: never changes, never wins
-    }
+    const bool in = q < n;
+    const int i = order[in ? q : 0];
+    const float x = P[3 * i], y = P[3 * i + 1], z = P[3 * i + 2];
+    oi[s] = in ? static_cast<uint32_t>(i) : 0xffffffffu;
+    px[s] = in ? x : 0.f;
+    py[s] = in ? y : 0.f;
+    pz[s] = in ? z : 0.f;
+    md[s] = in ? __builtin_inff() : 0.f;  // padding: never changes, never wins
   }
   __syncthreads();  // order[] is dead: the scratch becomes the position table
-  for (int i = t; i < n; i += THREADS) table[i] = make_float4(P[3 * i], P[3 * i + 1], P[3 * i + 2], 0.f);
+  // every point sits in exactly one slot (order is a permutation of 0..n-1, PTS * THREADS >= n):
+  // the table is written from the registers instead of read from memory again
+#pragma unroll
+  for (int s = 0; s < PTS; ++s)
+    if (oi[s] != 0xffffffffu) table[oi[s]] = make_float4(px[s], py[s], pz[s], 0.f);
   if (t < 2) slots[t] = 0ull;
 
   // 4. bucket records: box in lane s (bucket of slot s); max min-distance bits, lowest index
