@@ -379,26 +379,46 @@ __global__ __launch_bounds__(kRgFrontThreads) void rg_front(RgWs w, const float*
   bool bad = false;
   uint32_t nv = 0;
   uint32_t kmin[3] = {0xffffffffu, 0xffffffffu, 0xffffffffu}, kmax[3] = {0u, 0u, 0u};
+  // every point's mask, batch entry and position requested at once, at positions clamped into
+  // the cloud (ppc >= 1 here), and used for il < ppc only: loads under the per-point conditions
+  // had become a chain of branches, one wait per load
+  // (a missing mask or batch vector is read from x instead, whose 12 N bytes hold byte i and
+  // 8-byte word i for every i < N, and the value is discarded: a load behind a pointer test
+  // became a branch whose join waited for it)
+  const uint8_t* mp = mask ? mask : reinterpret_cast<const uint8_t*>(x);
+  const int64_t* bp = batch ? batch : reinterpret_cast<const int64_t*>(x);
+  uint8_t mv[kRgFrontPer];
+  int64_t bv[kRgFrontPer];
 #pragma unroll
   for (int k = 0; k < kRgFrontPer; ++k) {
     const int il = tid + k * kRgFrontThreads;
-    ok[k] = false;
-    px[k] = py[k] = pz[k] = 0.f;
-    if (il < ppc) {
-      const int64_t i = lo + il;
-      bool v = !mask || mask[i];
-      if (batch && batch[i] != b) {
-        bad = true;
-        v = false;
-      }
-      if (v) {
-        px[k] = x[3 * i]; py[k] = x[3 * i + 1]; pz[k] = x[3 * i + 2];
-        const uint32_t kk[3] = {float_order_key(px[k]), float_order_key(py[k]), float_order_key(pz[k])};
+    const int64_t i = lo + (il < ppc ? il : ppc - 1);
+    mv[k] = mp[i];
+    bv[k] = bp[i];
+    px[k] = x[3 * i]; py[k] = x[3 * i + 1]; pz[k] = x[3 * i + 2];
+  }
 #pragma unroll
-        for (int a = 0; a < 3; ++a) { kmin[a] = min(kmin[a], kk[a]); kmax[a] = max(kmax[a], kk[a]); }
-        ok[k] = true;
-        ++nv;
-      }
+  for (int k = 0; k < kRgFrontPer; ++k) {
+    mv[k] = mask ? mv[k] : static_cast<uint8_t>(1);
+    bv[k] = batch ? bv[k] : static_cast<int64_t>(b);
+  }
+#pragma unroll
+  for (int k = 0; k < kRgFrontPer; ++k) {
+    const int il = tid + k * kRgFrontThreads;
+    bool v = il < ppc && mv[k] != 0;
+    if (il < ppc && bv[k] != b) {
+      bad = true;
+      v = false;
+    }
+    ok[k] = v;
+    px[k] = v ? px[k] : 0.f;
+    py[k] = v ? py[k] : 0.f;
+    pz[k] = v ? pz[k] : 0.f;
+    if (v) {
+      const uint32_t kk[3] = {float_order_key(px[k]), float_order_key(py[k]), float_order_key(pz[k])};
+#pragma unroll
+      for (int a = 0; a < 3; ++a) { kmin[a] = min(kmin[a], kk[a]); kmax[a] = max(kmax[a], kk[a]); }
+      ++nv;
     }
   }
   // bounding box, valid count and layout check over the workgroup
